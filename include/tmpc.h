@@ -1,0 +1,180 @@
+/*
+ * libtmpc_hip — MI355X (gfx950) batched MPC solver kernels behind a C ABI.
+ *
+ * Every entry point is asynchronous on the caller's HIP stream, takes
+ * caller-owned device buffers, allocates nothing and keeps no global state:
+ * scratch memory is a caller-provided workspace whose size the matching
+ * *_workspace_bytes() query returns.  Return values are tmpc_status codes;
+ * nothing aborts.
+ *
+ * Array layout (all device pointers, row-major, leading problem axis B) is the
+ * reference's batched FFI layout (turbompc/solvers/admm/admm_cudss_ffi_backend.py:131-169):
+ *   D (B,T,n,n)  E (B,N,n,n)  q (B,T,n)  A0 (B,n0,n)  A_minus, A_plus (B,N,nx,n)
+ *   G (B,T,m,n)  l, u (B,T,m)  c0 (B,n0)  c (B,N,nx)
+ *   state: x (B,T,n)  z_g, y_g, xi_g (B,T,m)  y_f0 (B,n0)  y_f (B,N,nx)  rho (B)
+ * with T = N + 1 stages and n = nx + nu.  *_f32 entry points take float
+ * buffers, *_f64 double buffers.  Shapes need 1 <= n <= 64, 0 <= m <= 64,
+ * 1 <= nx <= n, 1 <= n0 <= n and T >= 2.
+ */
+#ifndef TMPC_H
+#define TMPC_H
+
+#include <stddef.h>
+#include <stdint.h>
+#include <hip/hip_runtime_api.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef enum tmpc_status {
+  TMPC_OK = 0,
+  TMPC_EBADSHAPE = 1,  /* dimensions outside the supported range          */
+  TMPC_EBADARG = 2,    /* null pointer or invalid configuration value     */
+  TMPC_EWORKSPACE = 3, /* workspace smaller than *_workspace_bytes()      */
+  TMPC_ELAUNCH = 4     /* a HIP launch or copy failed                     */
+} tmpc_status;
+
+typedef struct tmpc_dims {
+  int32_t B, T, n, nx, n0, m;
+} tmpc_dims;
+
+typedef struct tmpc_qp {
+  const void *D, *E, *q, *A0, *A_minus, *A_plus, *G, *l, *u, *c0, *c;
+  const void* slack_weight; /* (B,) slack penalty per problem, or NULL (0)   */
+} tmpc_qp;
+
+typedef struct tmpc_state {
+  void *x, *z_g, *y_g, *y_f0, *y_f, *xi_g, *rho;
+} tmpc_state;
+
+/* Structure the caller vouches for: A_plus_t == [-I 0] and E_t == 0 for all t
+ * (explicit integrators without a control-rate cost).  Lets the solve skip
+ * reading A_plus and E. */
+#define TMPC_FLAG_STD_DYNAMICS 1u
+
+typedef struct tmpc_admm_cfg {
+  int32_t max_iter, check_every, adapt_rho_every, pcg_max_iter, use_slack;
+  uint32_t flags;
+  double sigma, eps_abs, eps_rel, rho_min, rho_max, adaptive_rho_tolerance,
+      rho_f_factor, alpha, pcg_eps;
+} tmpc_admm_cfg;
+
+const char* tmpc_status_string(int status);
+int tmpc_version(void);
+
+/* ---- ADMM with the exact block-tridiagonal Schur solve ---------------------
+ * Replaces the `admm_cudss_cuda[_f64]` FFI target: AdmmCudssCudaImpl
+ * (turbompc/solvers/admm/csrc/admm_cudss_ffi.cc:13-140) / launchADMMCudss
+ * (turbompc/solvers/admm/csrc/admm_cudss.cu:853-1199), with the semantics of
+ * the reference's pure-JAX loop (turbompc/solvers/admm/admm.py:795-1049).
+ * `in` is the warm start; `out` receives the final state (in == out allowed).
+ * iters_out (B,) uint32 receives the ADMM iteration count per problem. */
+size_t tmpc_admm_direct_workspace_bytes(int elem_bytes, const tmpc_dims* dims);
+int tmpc_admm_direct_f32(hipStream_t stream, const tmpc_dims* dims, const tmpc_qp* qp,
+                         const tmpc_state* in, tmpc_state* out, uint32_t* iters_out,
+                         const tmpc_admm_cfg* cfg, void* workspace, size_t workspace_bytes);
+int tmpc_admm_direct_f64(hipStream_t stream, const tmpc_dims* dims, const tmpc_qp* qp,
+                         const tmpc_state* in, tmpc_state* out, uint32_t* iters_out,
+                         const tmpc_admm_cfg* cfg, void* workspace, size_t workspace_bytes);
+
+/* ---- ADMM with the PCG Schur solve -----------------------------------------
+ * Replaces the `admm_fused_cuda[_f64]` FFI target: AdmmFusedCudaImpl
+ * (turbompc/solvers/admm/csrc/admm_ffi.cc:13-148) / LaunchADMMFusedF32/F64
+ * (turbompc/solvers/admm/csrc/admm_fused.cuh:25-120), with the semantics of the
+ * reference's JAX loop over PCGPrimalOptimalControl
+ * (turbompc/solvers/linear_systems_solvers/pcg_primal.py:70-175): S and the
+ * block preconditioner Phiinv are built on the device (compute_S_Phiinv), PCG
+ * is warm-started at the previous x, cfg->pcg_eps / cfg->pcg_max_iter control
+ * it.  pcg_iters_out (B, max_iter) uint32 may be NULL; otherwise it receives
+ * the PCG iteration count of every ADMM iteration (zero past the last). */
+size_t tmpc_admm_pcg_workspace_bytes(int elem_bytes, const tmpc_dims* dims);
+int tmpc_admm_pcg_f32(hipStream_t stream, const tmpc_dims* dims, const tmpc_qp* qp,
+                      const tmpc_state* in, tmpc_state* out, uint32_t* iters_out,
+                      uint32_t* pcg_iters_out, const tmpc_admm_cfg* cfg, void* workspace,
+                      size_t workspace_bytes);
+int tmpc_admm_pcg_f64(hipStream_t stream, const tmpc_dims* dims, const tmpc_qp* qp,
+                      const tmpc_state* in, tmpc_state* out, uint32_t* iters_out,
+                      uint32_t* pcg_iters_out, const tmpc_admm_cfg* cfg, void* workspace,
+                      size_t workspace_bytes);
+
+/* ---- Schur matrix and block preconditioner ---------------------------------
+ * Replaces compute_S_Phiinv (turbompc/solvers/admm/admm.py:71-154), which the
+ * reference evaluates in XLA before every fused solve: rho (B,) per problem,
+ * rho_f = rho * rho_f_factor.  S, Phiinv (B,T,n,3n). */
+int tmpc_schur_build_f32(hipStream_t stream, const tmpc_dims* dims, const tmpc_qp* qp,
+                         const float* rho, double sigma, double rho_f_factor, float* S,
+                         float* Phiinv);
+int tmpc_schur_build_f64(hipStream_t stream, const tmpc_dims* dims, const tmpc_qp* qp,
+                         const double* rho, double sigma, double rho_f_factor, double* S,
+                         double* Phiinv);
+
+/* ---- Schur-level PCG ---------------------------------------------------------
+ * Replaces `pcg_blktridi_cuda[_f64]` (LaunchPcgBlkTridiF32/F64,
+ * turbompc/solvers/linear_systems_solvers/csrc/pcg_blktridi.cuh:7-33):
+ * S, Phiinv (B,T,n,3n), rhs, x0 (B,T,n) -> x (B,T,n) (x != x0), iters (B,). */
+size_t tmpc_schur_pcg_workspace_bytes(int elem_bytes, int32_t B, int32_t T, int32_t n);
+int tmpc_schur_pcg_f32(hipStream_t stream, int32_t B, int32_t T, int32_t n, const float* S,
+                       const float* Phiinv, const float* rhs, const float* x0, float* x,
+                       uint32_t* iters, double eps, int32_t max_iter, void* workspace,
+                       size_t workspace_bytes);
+int tmpc_schur_pcg_f64(hipStream_t stream, int32_t B, int32_t T, int32_t n, const double* S,
+                       const double* Phiinv, const double* rhs, const double* x0, double* x,
+                       uint32_t* iters, double eps, int32_t max_iter, void* workspace,
+                       size_t workspace_bytes);
+
+/* ---- Schur-level direct solve ----------------------------------------------
+ * Replaces `cudss_blktridi_cuda[_f64]` (CudssBlkTridiSolveF32/F64,
+ * turbompc/solvers/linear_systems_solvers/csrc/cudss_blktridi.cuh:5-21):
+ * S (B,T,n,3n) block rows [prev | diag | next] of an SPD block-tridiagonal
+ * matrix, rhs (B,T,n) -> x (B,T,n).  The factor (workspace) can be reused by
+ * further tmpc_blktri_solve_* calls with the same S. */
+size_t tmpc_blktri_workspace_bytes(int elem_bytes, int32_t B, int32_t T, int32_t n);
+int tmpc_blktri_factor_f32(hipStream_t stream, int32_t B, int32_t T, int32_t n, const float* S,
+                           void* workspace, size_t workspace_bytes);
+int tmpc_blktri_factor_f64(hipStream_t stream, int32_t B, int32_t T, int32_t n, const double* S,
+                           void* workspace, size_t workspace_bytes);
+int tmpc_blktri_solve_f32(hipStream_t stream, int32_t B, int32_t T, int32_t n, const float* S,
+                          const float* rhs, float* x, const void* workspace, size_t workspace_bytes);
+int tmpc_blktri_solve_f64(hipStream_t stream, int32_t B, int32_t T, int32_t n, const double* S,
+                          const double* rhs, double* x, const void* workspace,
+                          size_t workspace_bytes);
+
+/* ---- Adjoint (backward) KKT solve ------------------------------------------
+ * Replaces `cudss_sparse_kkt_f32/f64` (solve_sparse_kkt_f32/f64,
+ * turbompc/solvers/backward/csrc/cudss_sparse_kkt.cuh:21-41) as used by
+ * solve_backward_kkt_cudss_ffi (turbompc/solvers/backward/backward_kkt_cudss_ffi.py:232-277):
+ * solves [[P, C^T, G_act^T], [C, 0, 0], [G_act, 0, 0]] [dz; y_eq; y_ineq] = [-q; 0; 0]
+ * in block form, no CSR.  qp->G holds G_act (inactive rows zero), qp->q the
+ * adjoint linear term; l, u, c0, c are ignored (the constraints are
+ * homogeneous).  dz (B,T,n); mult (B, n0 + N*nx + T*m) laid out
+ * [y_f0 | y_f_dyn | y_ineq] (turbompc/solvers/turbompc_solver.py:727-763).
+ * Method: multipliers on the factorization kernel of S_rho = P + rho C^T C +
+ * rho G_act^T G_act (iterative refinement of the augmented Lagrangian; the
+ * stationarity row is exact at every step).  rho <= 0 selects a default scaled
+ * to max|D|; iters is the refinement count (<= 0: default). */
+size_t tmpc_adjoint_kkt_workspace_bytes(int elem_bytes, const tmpc_dims* dims);
+int tmpc_adjoint_kkt_f32(hipStream_t stream, const tmpc_dims* dims, const tmpc_qp* qp, float* dz,
+                         float* mult, double rho, int32_t iters, uint32_t flags, void* workspace,
+                         size_t workspace_bytes);
+int tmpc_adjoint_kkt_f64(hipStream_t stream, const tmpc_dims* dims, const tmpc_qp* qp, double* dz,
+                         double* mult, double rho, int32_t iters, uint32_t flags, void* workspace,
+                         size_t workspace_bytes);
+
+/* ---- SQP linearization: rotor-thrust quadrotor, RK4 ------------------------
+ * Replaces, for this model, the host JAX linearization
+ * get_dynamics_linearized_matrices (turbompc/problems/optimal_control_problem.py:1176-1332,
+ * explicit branch :1217-1272): states (B,N+1,13), controls (B,N+1,4) ->
+ * A_minus (B,N,13,17) = [df/dx, df/du], c (B,N,13) = -f + A x + B u.
+ * params (host, 7 doubles): mass, Jxx, Jyy, Jzz, arm, yaw coefficient, g. */
+int tmpc_quadrotor_linearize_f32(hipStream_t stream, int32_t B, int32_t N, const float* states,
+                                 const float* controls, double dt, const double* params,
+                                 float* A_minus, float* c);
+int tmpc_quadrotor_linearize_f64(hipStream_t stream, int32_t B, int32_t N, const double* states,
+                                 const double* controls, double dt, const double* params,
+                                 double* A_minus, double* c);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* TMPC_H */

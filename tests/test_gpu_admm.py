@@ -1,0 +1,173 @@
+"""GPU parity of the fused ADMM (direct and PCG Schur solves), the adjoint KKT
+and the quadrotor linearization against the CPU oracle, through the C ABI.
+
+fp64 cases must match the oracle to 1e-9 (normwise relative); fp32 cases to
+1e-4, or -- where the fp32 oracle itself sits further than that from the fp64
+oracle because of the conditioning of S -- to within 4x the fp32 oracle's own
+distance from the fp64 result.
+"""
+import numpy as np
+import pytest
+import torch
+
+import oracle
+from helpers import TOL, random_qp, rel_err, zero_state
+from turbompc_amd.problems import configs
+from turbompc_amd.problems.quadrotor import QUAD_PARAMS, make_quadrotor_config
+from turbompc_amd.solvers.admm.admm import ADMMSolver, ADMMState
+from turbompc_amd.solvers.backward.backward_kkt_hip import solve_backward_kkt_hip
+from turbompc_amd.solvers.linear_systems_solvers.backends import AdmmBackend
+from turbompc_amd.solvers.qp_utils import ZShape
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda"
+FIELDS = ("x_blocks", "z_g", "y_g", "y_f_0", "y_f_dyn", "xi_g", "rho_bar")
+
+
+def _solver(qp, cfg, backend=AdmmBackend.HIP_DIRECT, **kw):
+    B, T, n, nx, n0, m = qp.dims
+    return ADMMSolver(
+        ZShape(T - 1, nx, n - nx),
+        {"max_iter": cfg.pcg_max_iter, "tol_epsilon": cfg.pcg_eps},
+        sigma=cfg.sigma, max_iter=cfg.max_iter, eps_abs=cfg.eps_abs, eps_rel=cfg.eps_rel, rho_min=cfg.rho_min,
+        rho_max=cfg.rho_max, check_termination_every=cfg.check_every, adapt_rho_every=cfg.adapt_rho_every,
+        adaptive_rho_tolerance=cfg.adaptive_rho_tolerance, rho_f_factor=cfg.rho_f_factor, admm_backend=backend,
+        **kw,
+    )
+
+
+def _state_to_dev(st, dtype):
+    return ADMMState(**{k: torch.as_tensor(np.asarray(getattr(st, k)), dtype=dtype, device=DEV) for k in FIELDS})
+
+
+def _run_pair(qp, cfg, dtype, backend=AdmmBackend.HIP_DIRECT, rho0=0.1, schur="direct"):
+    st0 = zero_state(qp, rho0)
+    ref, it_ref, pcg_ref = oracle.admm_solve(qp, st0, cfg, schur=schur, dtype=np.float64)
+    qpd = qp.to(DEV, dtype)
+    solver = _solver(qp, cfg, backend)
+    (_, _), stats, out = solver.solve(qpd, _state_to_dev(st0, dtype), alpha=cfg.alpha)
+    torch.cuda.synchronize()
+    return ref, it_ref, pcg_ref, out, stats
+
+
+def _assert_state_close(out, ref, tol):
+    for k in FIELDS:
+        a, b = getattr(out, k), getattr(ref, k)
+        if np.asarray(b).size:
+            assert rel_err(a, b) < tol, (k, rel_err(a, b))
+
+
+@pytest.mark.parametrize("std", [True, False])
+@pytest.mark.parametrize("shape", [(9, 21, 6, 4, 2), (7, 11, 17, 13, 4), (5, 13, 9, 6, 11), (4, 8, 5, 3, 2), (3, 6, 4, 2, 0)])
+def test_admm_direct_fp64_fixed_iterations(std, shape):
+    B, T, n, nx, m = shape
+    qp = random_qp(B, T, n, nx, m, seed=41, std=std)
+    cfg = oracle.OracleCfg(max_iter=30, check_every=25, adapt_rho_every=25, sigma=1e-6, eps_abs=1e-9,
+                           eps_rel=1e-9, rho_f_factor=1000.0, alpha=1.0)
+    ref, it_ref, _, out, stats = _run_pair(qp, cfg, torch.float64)
+    np.testing.assert_array_equal(stats.num_iter.cpu().numpy(), it_ref)
+    _assert_state_close(out, ref, 1e-9)
+
+
+@pytest.mark.parametrize("alpha", [1.0, 1.6])
+def test_admm_direct_fp64_adaptive_rho_and_termination(alpha):
+    # residual checks every 2 iterations, rho adapted every 4: per-problem
+    # termination and refactorizations inside one call
+    qp = random_qp(11, 9, 6, 4, 3, seed=42, std=False)
+    cfg = oracle.OracleCfg(max_iter=200, check_every=2, adapt_rho_every=4, sigma=1e-6, eps_abs=1e-6, eps_rel=1e-6,
+                           rho_f_factor=50.0, alpha=alpha, adaptive_rho_tolerance=1.5)
+    ref, it_ref, _, out, stats = _run_pair(qp, cfg, torch.float64)
+    np.testing.assert_array_equal(stats.num_iter.cpu().numpy(), it_ref)
+    assert len(set(it_ref.tolist())) > 1  # problems stop at different iterations
+    _assert_state_close(out, ref, 1e-8)
+
+
+def test_admm_direct_config1_fp32():
+    prob = configs.config1(B=64, seed=0)
+    qp = prob.build_qp(*prob.initial_guess())
+    cfg = oracle.OracleCfg(max_iter=50, check_every=25, adapt_rho_every=25, sigma=1e-6, eps_abs=1e-9, eps_rel=1e-9,
+                           rho_f_factor=1000.0, alpha=1.0)
+    ref, it_ref, _, out, stats = _run_pair(qp, cfg, torch.float32)
+    ref32, _, _ = oracle.admm_solve(qp, zero_state(qp, 0.1), cfg, dtype=np.float32)
+    for k in ("x_blocks", "y_f_dyn", "y_g"):
+        e = rel_err(getattr(out, k), getattr(ref, k))
+        e_or = rel_err(getattr(ref32, k), getattr(ref, k))
+        assert e < max(TOL[torch.float32], 4 * e_or), (k, e, e_or)
+
+
+def test_admm_direct_quadrotor_qp_fp32_and_fp64():
+    prob = make_quadrotor_config(B=8, seed=0, dtype=torch.float64, device=DEV)
+    qp = prob.build_qp(*prob.initial_guess()).to("cpu")
+    cfg = oracle.OracleCfg(max_iter=20, check_every=25, adapt_rho_every=25, sigma=1e-6, eps_abs=1e-9, eps_rel=1e-9,
+                           rho_f_factor=1000.0, alpha=1.0)
+    ref, it_ref, _, out64, _ = _run_pair(qp, cfg, torch.float64)
+    _assert_state_close(out64, ref, 1e-9)
+    _, _, _, out32, _ = _run_pair(qp, cfg, torch.float32)
+    ref32, _, _ = oracle.admm_solve(qp, zero_state(qp, 0.1), cfg, dtype=np.float32)
+    e = rel_err(out32.x_blocks, ref.x_blocks)
+    e_or = rel_err(ref32.x_blocks, ref.x_blocks)
+    assert e < max(TOL[torch.float32], 4 * e_or), (e, e_or)
+
+
+def test_admm_direct_warm_start_and_in_place_state():
+    qp = random_qp(6, 10, 6, 4, 3, seed=43, std=True)
+    cfg = oracle.OracleCfg(max_iter=15, check_every=5, adapt_rho_every=5, sigma=1e-6, eps_abs=1e-12, eps_rel=1e-12,
+                           rho_f_factor=100.0, alpha=1.6, adaptive_rho_tolerance=1.2)
+    st0 = zero_state(qp, 0.1)
+    mid, _, _ = oracle.admm_solve(qp, st0, cfg)
+    ref, it_ref, _ = oracle.admm_solve(qp, mid, cfg)
+    solver = _solver(qp, cfg)
+    qpd = qp.to(DEV, torch.float64)
+    _, _, s1 = solver.solve(qpd, _state_to_dev(st0, torch.float64), alpha=1.6)
+    _, stats, s2 = solver.solve(qpd, s1, alpha=1.6)
+    np.testing.assert_array_equal(stats.num_iter.cpu().numpy(), it_ref)
+    _assert_state_close(s2, ref, 1e-8)
+
+
+def test_admm_pcg_config2_fp64():
+    prob = configs.config2(B=6, seed=0)
+    qp = prob.build_qp(*prob.initial_guess())
+    cfg = oracle.OracleCfg(max_iter=12, check_every=25, adapt_rho_every=25, sigma=1e-6, eps_abs=1e-9, eps_rel=1e-9,
+                           rho_f_factor=1000.0, alpha=1.0, pcg_eps=1e-6, pcg_max_iter=50)
+    ref, it_ref, pcg_ref, out, stats = _run_pair(qp, cfg, torch.float64, backend=AdmmBackend.HIP_PCG, schur="pcg")
+    np.testing.assert_array_equal(stats.num_iter.cpu().numpy(), it_ref)
+    assert np.all(stats.num_pcg_iters.sum(1).cpu().numpy() == pcg_ref)
+    _assert_state_close(out, ref, 1e-8)
+
+
+def test_admm_pcg_matches_direct_when_tight():
+    qp = random_qp(4, 12, 6, 4, 3, seed=44, std=True)
+    cfg = oracle.OracleCfg(max_iter=10, check_every=25, adapt_rho_every=25, sigma=1e-6, eps_abs=1e-9, eps_rel=1e-9,
+                           rho_f_factor=100.0, alpha=1.0, pcg_eps=1e-26, pcg_max_iter=400)
+    ref, _, _ = oracle.admm_solve(qp, zero_state(qp, 0.1), cfg, schur="direct")
+    _, _, _, out, _ = _run_pair(qp, cfg, torch.float64, backend=AdmmBackend.HIP_PCG, schur="pcg")
+    assert rel_err(out.x_blocks, ref.x_blocks) < 1e-7
+
+
+def test_adjoint_kkt_matches_dense_oracle_fp64():
+    prob = configs.config5(B=3, seed=0)
+    qp = prob.build_qp(*prob.initial_guess())
+    rng = np.random.default_rng(5)
+    sign = rng.choice([-1.0, 0.0, 1.0], size=tuple(qp.ineq.l.shape), p=[0.2, 0.6, 0.2])
+    G = qp.ineq.G * torch.tensor(sign).unsqueeze(-1)
+    qb = qp.replace_ineq(G=G).replace_cost(q=torch.tensor(rng.standard_normal(tuple(qp.cost.q.shape))))
+    dz_ref, mult_ref = oracle.adjoint_kkt(qb)
+    dz, mult = solve_backward_kkt_hip(qb.to(DEV, torch.float64))
+    assert rel_err(dz, dz_ref) < 1e-9
+    assert rel_err(mult, mult_ref) < 1e-9
+
+
+@pytest.mark.parametrize("dtype", [torch.float64, torch.float32])
+def test_quadrotor_linearization_matches_complex_step(dtype):
+    prob = make_quadrotor_config(B=16, seed=1, dtype=dtype, device=DEV)
+    g = torch.Generator().manual_seed(3)
+    st = (prob.initial_guess()[0].cpu().double() + 0.2 * torch.randn(prob.initial_guess()[0].shape, generator=g))
+    ct = torch.rand((16, 41, 4), generator=g, dtype=torch.float64) * 4.0
+    Am, c = prob.dynamics_blocks(st.to(DEV, dtype), ct.to(DEV, dtype))
+    xu = torch.cat([st[:, :-1], ct[:, :-1]], dim=-1).numpy().reshape(-1, 17)
+    f, J = oracle.quadrotor_rk4_jac(xu, prob.dt, QUAD_PARAMS)
+    Jr = J.reshape(16, 40, 13, 17)
+    cr = (-f + np.einsum("kij,kj->ki", J, xu)).reshape(16, 40, 13)
+    tol = 1e-12 if dtype == torch.float64 else 1e-5
+    assert rel_err(Am, Jr) < tol
+    assert rel_err(c, cr) < (1e-11 if dtype == torch.float64 else 1e-5)

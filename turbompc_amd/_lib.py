@@ -1,0 +1,179 @@
+"""ctypes binding of libtmpc_hip.so (the C ABI declared in include/tmpc.h).
+
+Device memory and streams come from PyTorch-ROCm: every array argument is a
+contiguous `torch.Tensor` on a HIP device and every call is enqueued on
+`torch.cuda.current_stream()`.  The library allocates nothing; workspaces are
+torch byte tensors sized by the *_workspace_bytes() queries.
+
+The library location mirrors the reference's `_find_lib`
+(turbompc/solvers/admm/admm_ffi_backend.py:15-38): the in-tree build
+`turbompc_amd/lib/libtmpc_hip.so`, overridable with the `TMPC_HIP_LIB`
+environment variable.  A missing library raises FileNotFoundError, as the
+reference does; there is no CPU fallback.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+from pathlib import Path
+from typing import Optional
+
+import torch
+
+_PKG = Path(__file__).resolve().parent
+DEFAULT_LIB = _PKG / "lib" / "libtmpc_hip.so"
+
+FLAG_STD_DYNAMICS = 1
+
+_STATUS = {
+    0: "ok",
+    1: "unsupported dimensions",
+    2: "invalid argument",
+    3: "workspace too small",
+    4: "HIP launch failed",
+}
+
+
+class TmpcError(RuntimeError):
+    """Non-zero tmpc_status returned by the library."""
+
+    def __init__(self, fn: str, status: int):
+        super().__init__(f"{fn} failed: {_STATUS.get(status, status)} (status {status})")
+        self.status = status
+
+
+class Dims(ctypes.Structure):
+    _fields_ = [(k, ctypes.c_int32) for k in ("B", "T", "n", "nx", "n0", "m")]
+
+
+class QP(ctypes.Structure):
+    _fields_ = [
+        (k, ctypes.c_void_p)
+        for k in ("D", "E", "q", "A0", "A_minus", "A_plus", "G", "l", "u", "c0", "c", "slack_weight")
+    ]
+
+
+class State(ctypes.Structure):
+    _fields_ = [(k, ctypes.c_void_p) for k in ("x", "z_g", "y_g", "y_f0", "y_f", "xi_g", "rho")]
+
+
+class AdmmCfg(ctypes.Structure):
+    _fields_ = [
+        ("max_iter", ctypes.c_int32),
+        ("check_every", ctypes.c_int32),
+        ("adapt_rho_every", ctypes.c_int32),
+        ("pcg_max_iter", ctypes.c_int32),
+        ("use_slack", ctypes.c_int32),
+        ("flags", ctypes.c_uint32),
+    ] + [
+        (k, ctypes.c_double)
+        for k in (
+            "sigma",
+            "eps_abs",
+            "eps_rel",
+            "rho_min",
+            "rho_max",
+            "adaptive_rho_tolerance",
+            "rho_f_factor",
+            "alpha",
+            "pcg_eps",
+        )
+    ]
+
+
+# name -> argtypes (restype is int unless listed in _SIZE_FNS)
+_VP, _I32, _U32, _F64, _SZ = ctypes.c_void_p, ctypes.c_int32, ctypes.c_uint32, ctypes.c_double, ctypes.c_size_t
+_PD, _PQ, _PS, _PC = (ctypes.POINTER(t) for t in (Dims, QP, State, AdmmCfg))
+SIGNATURES = {
+    "tmpc_version": [],
+    "tmpc_status_string": [ctypes.c_int],
+    "tmpc_admm_direct_workspace_bytes": [ctypes.c_int, _PD],
+    "tmpc_admm_direct_f32": [_VP, _PD, _PQ, _PS, _PS, _VP, _PC, _VP, _SZ],
+    "tmpc_admm_direct_f64": [_VP, _PD, _PQ, _PS, _PS, _VP, _PC, _VP, _SZ],
+    "tmpc_admm_pcg_workspace_bytes": [ctypes.c_int, _PD],
+    "tmpc_admm_pcg_f32": [_VP, _PD, _PQ, _PS, _PS, _VP, _VP, _PC, _VP, _SZ],
+    "tmpc_admm_pcg_f64": [_VP, _PD, _PQ, _PS, _PS, _VP, _VP, _PC, _VP, _SZ],
+    "tmpc_schur_build_f32": [_VP, _PD, _PQ, _VP, _F64, _F64, _VP, _VP],
+    "tmpc_schur_build_f64": [_VP, _PD, _PQ, _VP, _F64, _F64, _VP, _VP],
+    "tmpc_schur_pcg_workspace_bytes": [ctypes.c_int, _I32, _I32, _I32],
+    "tmpc_schur_pcg_f32": [_VP, _I32, _I32, _I32, _VP, _VP, _VP, _VP, _VP, _VP, _F64, _I32, _VP, _SZ],
+    "tmpc_schur_pcg_f64": [_VP, _I32, _I32, _I32, _VP, _VP, _VP, _VP, _VP, _VP, _F64, _I32, _VP, _SZ],
+    "tmpc_blktri_workspace_bytes": [ctypes.c_int, _I32, _I32, _I32],
+    "tmpc_blktri_factor_f32": [_VP, _I32, _I32, _I32, _VP, _VP, _SZ],
+    "tmpc_blktri_factor_f64": [_VP, _I32, _I32, _I32, _VP, _VP, _SZ],
+    "tmpc_blktri_solve_f32": [_VP, _I32, _I32, _I32, _VP, _VP, _VP, _VP, _SZ],
+    "tmpc_blktri_solve_f64": [_VP, _I32, _I32, _I32, _VP, _VP, _VP, _VP, _SZ],
+    "tmpc_adjoint_kkt_workspace_bytes": [ctypes.c_int, _PD],
+    "tmpc_adjoint_kkt_f32": [_VP, _PD, _PQ, _VP, _VP, _F64, _I32, _U32, _VP, _SZ],
+    "tmpc_adjoint_kkt_f64": [_VP, _PD, _PQ, _VP, _VP, _F64, _I32, _U32, _VP, _SZ],
+    "tmpc_quadrotor_linearize_f32": [_VP, _I32, _I32, _VP, _VP, _F64, _VP, _VP, _VP],
+    "tmpc_quadrotor_linearize_f64": [_VP, _I32, _I32, _VP, _VP, _F64, _VP, _VP, _VP],
+}
+_SIZE_FNS = {
+    "tmpc_admm_direct_workspace_bytes",
+    "tmpc_admm_pcg_workspace_bytes",
+    "tmpc_blktri_workspace_bytes",
+    "tmpc_schur_pcg_workspace_bytes",
+    "tmpc_adjoint_kkt_workspace_bytes",
+}
+
+_LIB: Optional[ctypes.CDLL] = None
+
+
+def lib_path() -> Path:
+    env = os.environ.get("TMPC_HIP_LIB")
+    return Path(env) if env else DEFAULT_LIB
+
+
+def load() -> ctypes.CDLL:
+    """Load libtmpc_hip.so; FileNotFoundError if it has not been built."""
+    global _LIB
+    if _LIB is not None:
+        return _LIB
+    p = lib_path()
+    if not p.exists():
+        raise FileNotFoundError(
+            f"Could not find {p}. Build it first:\n"
+            "  python -c 'import __graft_entry__ as g; g.build()'"
+        )
+    lib = ctypes.CDLL(str(p))
+    for name, argtypes in SIGNATURES.items():
+        fn = getattr(lib, name)
+        fn.argtypes = argtypes
+        if name in _SIZE_FNS:
+            fn.restype = ctypes.c_size_t
+        elif name == "tmpc_status_string":
+            fn.restype = ctypes.c_char_p
+        else:
+            fn.restype = ctypes.c_int
+    _LIB = lib
+    return lib
+
+
+def check(fn: str, status: int) -> None:
+    if status != 0:
+        raise TmpcError(fn, status)
+
+
+def ptr(t: Optional[torch.Tensor]) -> Optional[int]:
+    if t is None:
+        return None
+    if not t.is_contiguous():
+        raise ValueError("tensor must be contiguous")
+    return t.data_ptr() if t.numel() else None
+
+
+def stream_handle(device: torch.device) -> int:
+    return torch.cuda.current_stream(device).cuda_stream
+
+
+def suffix(dtype: torch.dtype) -> str:
+    if dtype == torch.float32:
+        return "f32"
+    if dtype == torch.float64:
+        return "f64"
+    raise TypeError(f"unsupported dtype {dtype}; use float32 or float64")
+
+
+def workspace(nbytes: int, device: torch.device) -> torch.Tensor:
+    return torch.empty(max(int(nbytes), 1), dtype=torch.uint8, device=device)

@@ -1,0 +1,677 @@
+// C ABI of libtmpc_hip (declared in include/tmpc.h): argument validation,
+// workspace carving and the asynchronous launch schedules.  Nothing here
+// allocates device memory or synchronises the host with the stream.
+#include "../../include/tmpc.h"
+
+#include <algorithm>
+#include <vector>
+
+#include "admm_direct.hpp"
+#include "common.hpp"
+#include "factor.hpp"
+#include "pcg.hpp"
+#include "quadrotor.hpp"
+
+namespace tmpc {
+namespace {
+
+constexpr size_t kAlign = 256;
+inline size_t align_up(size_t x) { return (x + kAlign - 1) / kAlign * kAlign; }
+
+struct Carver {
+  char* base;
+  size_t off = 0;
+  template <typename U>
+  U* take(size_t count) {
+    U* p = reinterpret_cast<U*>(base + off);
+    off += align_up(count * sizeof(U));
+    return p;
+  }
+};
+
+bool dims_ok(const tmpc_dims* d) {
+  return d && d->B >= 1 && d->T >= 2 && d->n >= 1 && d->n <= 64 && d->m >= 0 && d->m <= 64 &&
+         d->nx >= 1 && d->nx <= d->n && d->n0 >= 1 && d->n0 <= d->n;
+}
+
+Dims to_dims(const tmpc_dims* d) {
+  return Dims{d->B, d->T, d->T - 1, d->n, d->nx, d->n0, d->m};
+}
+
+template <typename R>
+size_t direct_ws_bytes(const Dims& d) {
+  const size_t B = d.B, T = d.T, n = d.n;
+  return align_up(T * B * packed_size(d.n) * sizeof(R)) + 2 * align_up(T * B * n * sizeof(R)) +
+         align_up(B * 4 * sizeof(int32_t)) + align_up(B * 8 * sizeof(R));
+}
+
+template <typename R>
+struct DirectWs {
+  R *thinv, *w, *gam, *res;
+  int32_t* ctl;
+};
+
+template <typename R>
+DirectWs<R> carve_direct(void* ws, const Dims& d) {
+  Carver c{static_cast<char*>(ws)};
+  DirectWs<R> w;
+  const size_t B = d.B, T = d.T, n = d.n;
+  w.thinv = c.take<R>(T * B * packed_size(d.n));
+  w.w = c.take<R>(T * B * n);
+  w.gam = c.take<R>(T * B * n);
+  w.ctl = c.take<int32_t>(B * 4);
+  w.res = c.take<R>(B * 8);
+  return w;
+}
+
+template <typename R>
+QPDev<R> to_qp(const tmpc_qp* q) {
+  return QPDev<R>{static_cast<const R*>(q->D),  static_cast<const R*>(q->E),
+                  static_cast<const R*>(q->q),  static_cast<const R*>(q->A0),
+                  static_cast<const R*>(q->A_minus), static_cast<const R*>(q->A_plus),
+                  static_cast<const R*>(q->G),  static_cast<const R*>(q->l),
+                  static_cast<const R*>(q->u),  static_cast<const R*>(q->c0),
+                  static_cast<const R*>(q->c),  static_cast<const R*>(q->slack_weight)};
+}
+
+template <typename R>
+StateDev<R> to_state(const tmpc_state* s) {
+  return StateDev<R>{static_cast<R*>(s->x),  static_cast<R*>(s->z_g), static_cast<R*>(s->y_g),
+                     static_cast<R*>(s->y_f0), static_cast<R*>(s->y_f), static_cast<R*>(s->xi_g),
+                     static_cast<R*>(s->rho)};
+}
+
+bool qp_ok(const tmpc_qp* q, int m) {
+  if (!q || !q->D || !q->E || !q->q || !q->A0 || !q->A_minus || !q->A_plus || !q->c0 || !q->c)
+    return false;
+  if (m > 0 && (!q->G || !q->l || !q->u)) return false;
+  return true;
+}
+
+bool state_ok(const tmpc_state* s, int m) {
+  if (!s || !s->x || !s->y_f0 || !s->y_f || !s->rho) return false;
+  if (m > 0 && (!s->z_g || !s->y_g || !s->xi_g)) return false;
+  return true;
+}
+
+int launch_status() {
+  return hipGetLastError() == hipSuccess ? TMPC_OK : TMPC_ELAUNCH;
+}
+
+// copies the warm start into the working/output state (skipped when aliased)
+template <typename R>
+int copy_state(hipStream_t s, const Dims& d, const tmpc_state* in, const tmpc_state* out) {
+  const size_t B = d.B, T = d.T, N = d.N;
+  const void* src[7] = {in->x, in->z_g, in->y_g, in->y_f0, in->y_f, in->xi_g, in->rho};
+  void* dst[7] = {out->x, out->z_g, out->y_g, out->y_f0, out->y_f, out->xi_g, out->rho};
+  const size_t cnt[7] = {B * T * d.n, B * T * d.m, B * T * d.m, B * d.n0, B * N * d.nx, B * T * d.m, B};
+  for (int k = 0; k < 7; ++k) {
+    if (cnt[k] == 0 || src[k] == dst[k]) continue;
+    if (!src[k] || !dst[k]) return TMPC_EBADARG;
+    if (hipMemcpyAsync(dst[k], src[k], cnt[k] * sizeof(R), hipMemcpyDeviceToDevice, s) != hipSuccess)
+      return TMPC_ELAUNCH;
+  }
+  return TMPC_OK;
+}
+
+template <typename R>
+int launch_factor_qp(hipStream_t s, const Dims& d, const QPDev<R>& q, const R* rho, R sigma,
+                     R rho_f_factor, int32_t* ctl, R* thinv) {
+  const size_t smem = factor_smem_bytes<R>(d);
+  hipLaunchKernelGGL((factor_kernel<R, SRC_QP>), dim3(d.B), dim3(kWave), smem, s, d, q,
+                     (const R*)nullptr, rho, sigma, rho_f_factor, ctl, thinv);
+  return launch_status();
+}
+
+template <typename R, int NC, bool STD>
+void launch_chunk_nc(hipStream_t s, const AdmmArgs<R>& a) {
+  const int grid = (a.d.B + a.P - 1) / a.P;
+  hipLaunchKernelGGL((admm_chunk_kernel<R, NC, STD>), dim3(grid), dim3(kWave), 0, s, a);
+}
+
+template <typename R, bool STD>
+void launch_chunk(hipStream_t s, const AdmmArgs<R>& a) {
+  switch (a.d.n) {
+    case 6: launch_chunk_nc<R, 6, STD>(s, a); break;
+    case 9: launch_chunk_nc<R, 9, STD>(s, a); break;
+    case 16: launch_chunk_nc<R, 16, STD>(s, a); break;
+    case 17: launch_chunk_nc<R, 17, STD>(s, a); break;
+    default: launch_chunk_nc<R, 0, STD>(s, a); break;
+  }
+}
+
+// Iterations after which a rho change (and so a refactorization) can happen:
+// it >= 2, it % adapt_every == 0 and it % check_every == 0 (admm.py:504-508).
+std::vector<int> chunk_bounds(int max_iter, int check_every, int adapt_every) {
+  const int last = std::max(max_iter, 1);  // cond_fun always runs iteration 0
+  std::vector<int> b{0};
+  if (adapt_every > 0)
+    for (int it = 2; it < last; ++it) {
+      const bool ck = check_every > 0 ? (it % check_every == 0) : (it == 0);
+      if (it % adapt_every == 0 && ck) b.push_back(it + 1);
+    }
+  if (b.back() != last) b.push_back(last);
+  return b;
+}
+
+template <typename R>
+int admm_direct_impl(hipStream_t s, const tmpc_dims* dims, const tmpc_qp* qp,
+                     const tmpc_state* in, tmpc_state* out, uint32_t* iters,
+                     const tmpc_admm_cfg* cfg, void* ws, size_t wsb) {
+  if (!dims_ok(dims)) return TMPC_EBADSHAPE;
+  if (!cfg || !iters || !qp_ok(qp, dims->m) || !state_ok(in, dims->m) || !state_ok(out, dims->m))
+    return TMPC_EBADARG;
+  if (cfg->use_slack && dims->m > 0 && !qp->slack_weight) return TMPC_EBADARG;
+  const Dims d = to_dims(dims);
+  if (!ws || wsb < direct_ws_bytes<R>(d)) return TMPC_EWORKSPACE;
+  int st = copy_state<R>(s, d, in, out);
+  if (st) return st;
+  const DirectWs<R> w = carve_direct<R>(ws, d);
+  AdmmArgs<R> a;
+  a.d = d;
+  a.qp = to_qp<R>(qp);
+  a.st = to_state<R>(out);
+  a.thinv = w.thinv;
+  a.w = w.w;
+  a.gam = w.gam;
+  a.ctl = w.ctl;
+  a.res = w.res;
+  a.iters_out = iters;
+  a.sigma = (R)cfg->sigma;
+  a.alpha = (R)cfg->alpha;
+  a.rho_f_factor = (R)cfg->rho_f_factor;
+  a.eps_abs = (R)cfg->eps_abs;
+  a.eps_rel = (R)cfg->eps_rel;
+  a.rho_min = (R)cfg->rho_min;
+  a.rho_max = (R)cfg->rho_max;
+  a.rho_tol = (R)cfg->adaptive_rho_tolerance;
+  a.max_iter = cfg->max_iter;
+  a.check_every = cfg->check_every;
+  a.adapt_every = cfg->adapt_rho_every;
+  a.use_slack = cfg->use_slack ? 1 : 0;
+  a.g = std::max(d.n, d.m);
+  a.P = kWave / a.g;
+  const bool std_dyn = (cfg->flags & TMPC_FLAG_STD_DYNAMICS) != 0;
+  st = launch_factor_qp<R>(s, d, a.qp, a.st.rho, a.sigma, a.rho_f_factor, nullptr, w.thinv);
+  if (st) return st;
+  const std::vector<int> bounds = chunk_bounds(cfg->max_iter, cfg->check_every, cfg->adapt_rho_every);
+  for (size_t c = 0; c + 1 < bounds.size(); ++c) {
+    if (c > 0) {
+      st = launch_factor_qp<R>(s, d, a.qp, a.st.rho, a.sigma, a.rho_f_factor, w.ctl, w.thinv);
+      if (st) return st;
+    }
+    a.it_lo = bounds[c];
+    a.it_hi = bounds[c + 1];
+    a.first_chunk = c == 0 ? 1 : 0;
+    if (std_dyn)
+      launch_chunk<R, true>(s, a);
+    else
+      launch_chunk<R, false>(s, a);
+    st = launch_status();
+    if (st) return st;
+  }
+  return TMPC_OK;
+}
+
+// ---------------------------------------------------------------- blktri ----
+template <typename R>
+int blktri_factor_impl(hipStream_t s, int B, int T, int n, const R* S, void* ws, size_t wsb) {
+  tmpc_dims td{B, T, n, 1, 1, 0};
+  if (!dims_ok(&td)) return TMPC_EBADSHAPE;
+  if (!S) return TMPC_EBADARG;
+  const Dims d = to_dims(&td);
+  if (!ws || wsb < align_up((size_t)T * B * packed_size(n) * sizeof(R))) return TMPC_EWORKSPACE;
+  QPDev<R> q{};
+  const size_t smem = factor_smem_bytes<R>(d);
+  hipLaunchKernelGGL((factor_kernel<R, SRC_S>), dim3(B), dim3(kWave), smem, s, d, q, S,
+                     (const R*)nullptr, R(0), R(0), (int32_t*)nullptr, static_cast<R*>(ws));
+  return launch_status();
+}
+
+template <typename R, int NC>
+void launch_blktri_solve_nc(hipStream_t s, const Dims& d, int g, int P, const R* S, const R* th,
+                            const R* rhs, R* x) {
+  hipLaunchKernelGGL((blktri_solve_kernel<R, NC>), dim3((d.B + P - 1) / P), dim3(kWave), 0, s, d, g,
+                     P, S, th, rhs, x);
+}
+
+template <typename R>
+int blktri_solve_impl(hipStream_t s, int B, int T, int n, const R* S, const R* rhs, R* x,
+                      const void* ws, size_t wsb) {
+  tmpc_dims td{B, T, n, 1, 1, 0};
+  if (!dims_ok(&td)) return TMPC_EBADSHAPE;
+  if (!S || !rhs || !x) return TMPC_EBADARG;
+  const Dims d = to_dims(&td);
+  if (!ws || wsb < align_up((size_t)T * B * packed_size(n) * sizeof(R))) return TMPC_EWORKSPACE;
+  const R* th = static_cast<const R*>(ws);
+  const int g = n, P = kWave / n;
+  switch (n) {
+    case 6: launch_blktri_solve_nc<R, 6>(s, d, g, P, S, th, rhs, x); break;
+    case 9: launch_blktri_solve_nc<R, 9>(s, d, g, P, S, th, rhs, x); break;
+    case 16: launch_blktri_solve_nc<R, 16>(s, d, g, P, S, th, rhs, x); break;
+    case 17: launch_blktri_solve_nc<R, 17>(s, d, g, P, S, th, rhs, x); break;
+    default: launch_blktri_solve_nc<R, 0>(s, d, g, P, S, th, rhs, x); break;
+  }
+  return launch_status();
+}
+
+// --------------------------------------------------------------- adjoint ----
+template <typename R>
+size_t adjoint_ws_bytes(const Dims& d) {
+  const size_t B = d.B, T = d.T, N = d.N;
+  return direct_ws_bytes<R>(d) + align_up(B * T * d.n * sizeof(R)) +
+         4 * align_up(B * T * std::max(d.m, 1) * sizeof(R)) + 2 * align_up(B * d.n0 * sizeof(R)) +
+         2 * align_up(B * N * d.nx * sizeof(R)) + align_up(B * sizeof(R)) +
+         align_up(B * sizeof(uint32_t));
+}
+
+template <typename R>
+__global__ void adjoint_init_kernel(Dims d, const R* __restrict__ D, R rho_rel, R* x, R* z, R* yg,
+                                    R* xi, R* lu, R* y0, R* c0, R* yf, R* c, R* rho) {
+  const int b = blockIdx.x;
+  const int tid = threadIdx.x;
+  const size_t T = d.T, N = d.N;
+  for (size_t e = tid; e < T * d.n; e += blockDim.x) x[b * T * d.n + e] = R(0);
+  for (size_t e = tid; e < T * d.m; e += blockDim.x) {
+    z[b * T * d.m + e] = R(0);
+    yg[b * T * d.m + e] = R(0);
+    xi[b * T * d.m + e] = R(0);
+    lu[b * T * d.m + e] = R(0);
+  }
+  for (int e = tid; e < d.n0; e += blockDim.x) {
+    y0[(size_t)b * d.n0 + e] = R(0);
+    c0[(size_t)b * d.n0 + e] = R(0);
+  }
+  for (size_t e = tid; e < N * d.nx; e += blockDim.x) {
+    yf[b * N * d.nx + e] = R(0);
+    c[b * N * d.nx + e] = R(0);
+  }
+  // penalty scaled to the cost curvature of this problem
+  __shared__ R red[256];
+  R mx = R(0);
+  for (size_t e = tid; e < T * d.n * d.n; e += blockDim.x) mx = rmax(mx, rabs(D[b * T * d.n * d.n + e]));
+  red[tid] = mx;
+  __syncthreads();
+  if (tid == 0) {
+    R v = R(0);
+    for (unsigned k = 0; k < blockDim.x; ++k) v = rmax(v, red[k]);
+    rho[b] = rho_rel * rmax(v, R(1e-30));
+  }
+}
+
+template <typename R>
+__global__ void adjoint_pack_kernel(Dims d, const R* y0, const R* yf, const R* yg, R* mult) {
+  const int b = blockIdx.x;
+  const size_t N = d.N, T = d.T;
+  const size_t L = d.n0 + N * d.nx + T * d.m;
+  R* o = mult + b * L;
+  for (size_t e = threadIdx.x; e < L; e += blockDim.x) {
+    R v;
+    if (e < (size_t)d.n0)
+      v = y0[(size_t)b * d.n0 + e];
+    else if (e < d.n0 + N * d.nx)
+      v = yf[b * N * d.nx + (e - d.n0)];
+    else
+      v = yg[b * T * d.m + (e - d.n0 - N * d.nx)];
+    o[e] = v;
+  }
+}
+
+template <typename R>
+int adjoint_impl(hipStream_t s, const tmpc_dims* dims, const tmpc_qp* qp, R* dz, R* mult, double rho,
+                 int32_t iters, uint32_t flags, void* ws, size_t wsb) {
+  if (!dims_ok(dims)) return TMPC_EBADSHAPE;
+  if (!qp || !qp->D || !qp->E || !qp->q || !qp->A0 || !qp->A_minus || !qp->A_plus || !dz || !mult)
+    return TMPC_EBADARG;
+  if (dims->m > 0 && !qp->G) return TMPC_EBADARG;
+  const Dims d = to_dims(dims);
+  if (!ws || wsb < adjoint_ws_bytes<R>(d)) return TMPC_EWORKSPACE;
+  const bool f64 = sizeof(R) == 8;
+  const R rho_rel = rho > 0 ? (R)rho : (f64 ? R(1e5) : R(1e2));
+  const int K = iters > 0 ? iters : (f64 ? 12 : 20);
+  // workspace: [direct solve | state | homogeneous l,u,c0,c | iters]
+  Carver c{static_cast<char*>(ws)};
+  c.off = direct_ws_bytes<R>(d);
+  const size_t B = d.B, T = d.T, N = d.N, mm = std::max(d.m, 1);
+  R* x = c.take<R>(B * T * d.n);
+  R* z = c.take<R>(B * T * mm);
+  R* yg = c.take<R>(B * T * mm);
+  R* xi = c.take<R>(B * T * mm);
+  R* lu = c.take<R>(B * T * mm);
+  R* y0 = c.take<R>(B * d.n0);
+  R* c0 = c.take<R>(B * d.n0);
+  R* yf = c.take<R>(B * N * d.nx);
+  R* cz = c.take<R>(B * N * d.nx);
+  R* rh = c.take<R>(B);
+  uint32_t* it = c.take<uint32_t>(B);
+  hipLaunchKernelGGL((adjoint_init_kernel<R>), dim3(d.B), dim3(256), 0, s, d,
+                     static_cast<const R*>(qp->D), rho_rel, x, z, yg, xi, lu, y0, c0, yf, cz, rh);
+  int st = launch_status();
+  if (st) return st;
+  tmpc_qp hq = *qp;
+  hq.l = lu;
+  hq.u = lu;
+  hq.c0 = c0;
+  hq.c = cz;
+  hq.slack_weight = nullptr;
+  if (d.m == 0) hq.G = hq.l;  // unused
+  tmpc_state sv{x, z, yg, y0, yf, xi, rh};
+  tmpc_admm_cfg cfg{};
+  cfg.max_iter = K;
+  cfg.check_every = 0;
+  cfg.adapt_rho_every = 0;
+  cfg.use_slack = 0;
+  cfg.flags = flags;
+  cfg.sigma = 0.0;
+  cfg.eps_abs = 0.0;
+  cfg.eps_rel = 0.0;
+  cfg.rho_min = 0.0;
+  cfg.rho_max = 1e300;
+  cfg.adaptive_rho_tolerance = 5.0;
+  cfg.rho_f_factor = 1.0;
+  cfg.alpha = 1.0;
+  st = admm_direct_impl<R>(s, dims, &hq, &sv, &sv, it, &cfg, ws, direct_ws_bytes<R>(d));
+  if (st) return st;
+  if (hipMemcpyAsync(dz, x, B * T * d.n * sizeof(R), hipMemcpyDeviceToDevice, s) != hipSuccess)
+    return TMPC_ELAUNCH;
+  hipLaunchKernelGGL((adjoint_pack_kernel<R>), dim3(d.B), dim3(256), 0, s, d, y0, yf, yg, mult);
+  return launch_status();
+}
+
+
+// ----------------------------------------------------------- PCG family ----
+template <typename R>
+size_t pcg_vec_bytes(const Dims& d) { return 5 * align_up((size_t)d.B * d.T * d.n * sizeof(R)); }
+
+template <typename R>
+size_t admm_pcg_ws_bytes(const Dims& d) {
+  const size_t B = d.B, T = d.T, n = d.n;
+  return 2 * align_up(B * T * n * 3 * n * sizeof(R)) + 2 * align_up(T * B * n * sizeof(R)) +
+         align_up(B * 4 * sizeof(int32_t)) + align_up(B * 8 * sizeof(R)) + pcg_vec_bytes<R>(d);
+}
+
+template <typename R>
+PcgVecs<R> carve_vecs(Carver& c, const Dims& d, R* x) {
+  const size_t L = (size_t)d.B * d.T * d.n;
+  PcgVecs<R> v;
+  v.x = c.take<R>(L);
+  if (x) v.x = x;
+  v.r = c.take<R>(L);
+  v.p = c.take<R>(L);
+  v.q = c.take<R>(L);
+  v.rt = c.take<R>(L);
+  return v;
+}
+
+template <typename R>
+int launch_schur_build(hipStream_t s, const Dims& d, const QPDev<R>& q, const R* rho, R sigma, R rfac,
+                       int32_t* ctl, R* S, R* Phi) {
+  const size_t smem = factor_smem_bytes<R>(d);
+  hipLaunchKernelGGL((schur_build_kernel<R>), dim3(d.B), dim3(kWave), smem, s, d, q, rho, sigma, rfac, ctl,
+                     S, Phi);
+  return launch_status();
+}
+
+template <typename R>
+int schur_build_impl(hipStream_t s, const tmpc_dims* dims, const tmpc_qp* qp, const R* rho, double sigma,
+                     double rfac, R* S, R* Phi) {
+  if (!dims_ok(dims)) return TMPC_EBADSHAPE;
+  if (!qp_ok(qp, dims->m) || !rho || !S || !Phi) return TMPC_EBADARG;
+  const Dims d = to_dims(dims);
+  return launch_schur_build<R>(s, d, to_qp<R>(qp), rho, (R)sigma, (R)rfac, nullptr, S, Phi);
+}
+
+template <typename R, int NC>
+void launch_pcg_nc(hipStream_t s, const Dims& d, int g, int P, const R* S, const R* Phi, const R* rhs,
+                   const R* x0, const PcgVecs<R>& v, uint32_t* iters, R eps, int max_iter) {
+  hipLaunchKernelGGL((pcg_kernel<R, NC>), dim3((d.B + P - 1) / P), dim3(kWave), 0, s, d, g, P, S, Phi, rhs,
+                     x0, v, iters, eps, max_iter);
+}
+
+template <typename R>
+int schur_pcg_impl(hipStream_t s, int B, int T, int n, const R* S, const R* Phi, const R* rhs, const R* x0,
+                   R* x, uint32_t* iters, double eps, int max_iter, void* ws, size_t wsb) {
+  tmpc_dims td{B, T, n, 1, 1, 0};
+  if (!dims_ok(&td)) return TMPC_EBADSHAPE;
+  if (!S || !Phi || !rhs || !x0 || !x || !iters) return TMPC_EBADARG;
+  if (x == x0) return TMPC_EBADARG;
+  const Dims d = to_dims(&td);
+  if (!ws || wsb < pcg_vec_bytes<R>(d)) return TMPC_EWORKSPACE;
+  Carver c{static_cast<char*>(ws)};
+  const PcgVecs<R> v = carve_vecs<R>(c, d, x);
+  const int g = n, P = kWave / n;
+  switch (n) {
+    case 6: launch_pcg_nc<R, 6>(s, d, g, P, S, Phi, rhs, x0, v, iters, (R)eps, max_iter); break;
+    case 9: launch_pcg_nc<R, 9>(s, d, g, P, S, Phi, rhs, x0, v, iters, (R)eps, max_iter); break;
+    case 16: launch_pcg_nc<R, 16>(s, d, g, P, S, Phi, rhs, x0, v, iters, (R)eps, max_iter); break;
+    case 17: launch_pcg_nc<R, 17>(s, d, g, P, S, Phi, rhs, x0, v, iters, (R)eps, max_iter); break;
+    default: launch_pcg_nc<R, 0>(s, d, g, P, S, Phi, rhs, x0, v, iters, (R)eps, max_iter); break;
+  }
+  return launch_status();
+}
+
+template <typename R, int NC>
+void launch_admm_pcg_nc(hipStream_t s, const AdmmPcgArgs<R>& pa) {
+  const int grid = (pa.a.d.B + pa.a.P - 1) / pa.a.P;
+  hipLaunchKernelGGL((admm_pcg_chunk_kernel<R, NC>), dim3(grid), dim3(kWave), 0, s, pa);
+}
+
+template <typename R>
+int admm_pcg_impl(hipStream_t s, const tmpc_dims* dims, const tmpc_qp* qp, const tmpc_state* in,
+                  tmpc_state* out, uint32_t* iters, uint32_t* pcg_iters, const tmpc_admm_cfg* cfg, void* ws,
+                  size_t wsb) {
+  if (!dims_ok(dims)) return TMPC_EBADSHAPE;
+  if (!cfg || !iters || !qp_ok(qp, dims->m) || !state_ok(in, dims->m) || !state_ok(out, dims->m))
+    return TMPC_EBADARG;
+  if (cfg->use_slack && dims->m > 0 && !qp->slack_weight) return TMPC_EBADARG;
+  const Dims d = to_dims(dims);
+  if (!ws || wsb < admm_pcg_ws_bytes<R>(d)) return TMPC_EWORKSPACE;
+  int st = copy_state<R>(s, d, in, out);
+  if (st) return st;
+  if (pcg_iters && cfg->max_iter > 0 &&
+      hipMemsetAsync(pcg_iters, 0, (size_t)d.B * cfg->max_iter * sizeof(uint32_t), s) != hipSuccess)
+    return TMPC_ELAUNCH;
+  const size_t B = d.B, T = d.T, n = d.n;
+  Carver c{static_cast<char*>(ws)};
+  R* S = c.take<R>(B * T * n * 3 * n);
+  R* Phi = c.take<R>(B * T * n * 3 * n);
+  AdmmPcgArgs<R> pa;
+  AdmmArgs<R>& a = pa.a;
+  a.w = c.take<R>(T * B * n);
+  a.gam = c.take<R>(T * B * n);
+  a.ctl = c.take<int32_t>(B * 4);
+  a.res = c.take<R>(B * 8);
+  pa.v = carve_vecs<R>(c, d, nullptr);
+  a.d = d;
+  a.qp = to_qp<R>(qp);
+  a.st = to_state<R>(out);
+  a.thinv = nullptr;
+  a.iters_out = iters;
+  a.sigma = (R)cfg->sigma;
+  a.alpha = (R)cfg->alpha;
+  a.rho_f_factor = (R)cfg->rho_f_factor;
+  a.eps_abs = (R)cfg->eps_abs;
+  a.eps_rel = (R)cfg->eps_rel;
+  a.rho_min = (R)cfg->rho_min;
+  a.rho_max = (R)cfg->rho_max;
+  a.rho_tol = (R)cfg->adaptive_rho_tolerance;
+  a.max_iter = cfg->max_iter;
+  a.check_every = cfg->check_every;
+  a.adapt_every = cfg->adapt_rho_every;
+  a.use_slack = cfg->use_slack ? 1 : 0;
+  a.g = std::max(d.n, d.m);
+  a.P = kWave / a.g;
+  pa.S = S;
+  pa.Phi = Phi;
+  pa.pcg_iters = pcg_iters;
+  pa.pcg_eps = (R)cfg->pcg_eps;
+  pa.pcg_max_iter = cfg->pcg_max_iter;
+  st = launch_schur_build<R>(s, d, a.qp, a.st.rho, a.sigma, a.rho_f_factor, nullptr, S, Phi);
+  if (st) return st;
+  const std::vector<int> bounds = chunk_bounds(cfg->max_iter, cfg->check_every, cfg->adapt_rho_every);
+  for (size_t k = 0; k + 1 < bounds.size(); ++k) {
+    if (k > 0) {
+      st = launch_schur_build<R>(s, d, a.qp, a.st.rho, a.sigma, a.rho_f_factor, a.ctl, S, Phi);
+      if (st) return st;
+    }
+    a.it_lo = bounds[k];
+    a.it_hi = bounds[k + 1];
+    a.first_chunk = k == 0 ? 1 : 0;
+    switch (d.n) {
+      case 6: launch_admm_pcg_nc<R, 6>(s, pa); break;
+      case 9: launch_admm_pcg_nc<R, 9>(s, pa); break;
+      case 16: launch_admm_pcg_nc<R, 16>(s, pa); break;
+      case 17: launch_admm_pcg_nc<R, 17>(s, pa); break;
+      default: launch_admm_pcg_nc<R, 0>(s, pa); break;
+    }
+    st = launch_status();
+    if (st) return st;
+  }
+  return TMPC_OK;
+}
+
+// ------------------------------------------------------------ quadrotor ----
+template <typename R>
+int quad_impl(hipStream_t s, int B, int N, const R* states, const R* controls, double dt,
+              const double* params, R* Am, R* c) {
+  if (B < 1 || N < 1) return TMPC_EBADSHAPE;
+  if (!states || !controls || !params || !Am || !c) return TMPC_EBADARG;
+  QuadParams<R> P{(R)params[0], (R)params[1], (R)params[2], (R)params[3],
+                  (R)params[4], (R)params[5], (R)params[6]};
+  const long long total = (long long)B * N * 18;
+  const int blk = 256;
+  const long long grid = (total + blk - 1) / blk;
+  hipLaunchKernelGGL((quad_linearize_kernel<R>), dim3((unsigned)grid), dim3(blk), 0, s, B, N, states, controls,
+                     (R)dt, P, Am, c);
+  return launch_status();
+}
+
+}  // namespace
+}  // namespace tmpc
+
+using namespace tmpc;
+
+extern "C" {
+
+const char* tmpc_status_string(int status) {
+  switch (status) {
+    case TMPC_OK: return "ok";
+    case TMPC_EBADSHAPE: return "unsupported dimensions";
+    case TMPC_EBADARG: return "invalid argument";
+    case TMPC_EWORKSPACE: return "workspace too small";
+    case TMPC_ELAUNCH: return "HIP launch failed";
+    default: return "unknown status";
+  }
+}
+
+int tmpc_version(void) { return 100; }
+
+size_t tmpc_admm_direct_workspace_bytes(int elem_bytes, const tmpc_dims* dims) {
+  if (!dims_ok(dims)) return 0;
+  const Dims d = to_dims(dims);
+  return elem_bytes == 8 ? direct_ws_bytes<double>(d) : direct_ws_bytes<float>(d);
+}
+
+int tmpc_admm_direct_f32(hipStream_t s, const tmpc_dims* dims, const tmpc_qp* qp, const tmpc_state* in,
+                         tmpc_state* out, uint32_t* iters, const tmpc_admm_cfg* cfg, void* ws,
+                         size_t wsb) {
+  return admm_direct_impl<float>(s, dims, qp, in, out, iters, cfg, ws, wsb);
+}
+int tmpc_admm_direct_f64(hipStream_t s, const tmpc_dims* dims, const tmpc_qp* qp, const tmpc_state* in,
+                         tmpc_state* out, uint32_t* iters, const tmpc_admm_cfg* cfg, void* ws,
+                         size_t wsb) {
+  return admm_direct_impl<double>(s, dims, qp, in, out, iters, cfg, ws, wsb);
+}
+
+size_t tmpc_blktri_workspace_bytes(int elem_bytes, int32_t B, int32_t T, int32_t n) {
+  tmpc_dims td{B, T, n, 1, 1, 0};
+  if (!dims_ok(&td)) return 0;
+  return align_up((size_t)T * B * packed_size(n) * (elem_bytes == 8 ? 8 : 4));
+}
+int tmpc_blktri_factor_f32(hipStream_t s, int32_t B, int32_t T, int32_t n, const float* S, void* ws,
+                           size_t wsb) {
+  return blktri_factor_impl<float>(s, B, T, n, S, ws, wsb);
+}
+int tmpc_blktri_factor_f64(hipStream_t s, int32_t B, int32_t T, int32_t n, const double* S, void* ws,
+                           size_t wsb) {
+  return blktri_factor_impl<double>(s, B, T, n, S, ws, wsb);
+}
+int tmpc_blktri_solve_f32(hipStream_t s, int32_t B, int32_t T, int32_t n, const float* S,
+                          const float* rhs, float* x, const void* ws, size_t wsb) {
+  return blktri_solve_impl<float>(s, B, T, n, S, rhs, x, ws, wsb);
+}
+int tmpc_blktri_solve_f64(hipStream_t s, int32_t B, int32_t T, int32_t n, const double* S,
+                          const double* rhs, double* x, const void* ws, size_t wsb) {
+  return blktri_solve_impl<double>(s, B, T, n, S, rhs, x, ws, wsb);
+}
+
+size_t tmpc_adjoint_kkt_workspace_bytes(int elem_bytes, const tmpc_dims* dims) {
+  if (!dims_ok(dims)) return 0;
+  const Dims d = to_dims(dims);
+  return elem_bytes == 8 ? adjoint_ws_bytes<double>(d) : adjoint_ws_bytes<float>(d);
+}
+int tmpc_adjoint_kkt_f32(hipStream_t s, const tmpc_dims* dims, const tmpc_qp* qp, float* dz,
+                         float* mult, double rho, int32_t iters, uint32_t flags, void* ws,
+                         size_t wsb) {
+  return adjoint_impl<float>(s, dims, qp, dz, mult, rho, iters, flags, ws, wsb);
+}
+int tmpc_adjoint_kkt_f64(hipStream_t s, const tmpc_dims* dims, const tmpc_qp* qp, double* dz,
+                         double* mult, double rho, int32_t iters, uint32_t flags, void* ws,
+                         size_t wsb) {
+  return adjoint_impl<double>(s, dims, qp, dz, mult, rho, iters, flags, ws, wsb);
+}
+
+size_t tmpc_admm_pcg_workspace_bytes(int elem_bytes, const tmpc_dims* dims) {
+  if (!dims_ok(dims)) return 0;
+  const Dims d = to_dims(dims);
+  return elem_bytes == 8 ? admm_pcg_ws_bytes<double>(d) : admm_pcg_ws_bytes<float>(d);
+}
+int tmpc_admm_pcg_f32(hipStream_t s, const tmpc_dims* dims, const tmpc_qp* qp, const tmpc_state* in,
+                      tmpc_state* out, uint32_t* iters, uint32_t* pcg_iters, const tmpc_admm_cfg* cfg,
+                      void* ws, size_t wsb) {
+  return admm_pcg_impl<float>(s, dims, qp, in, out, iters, pcg_iters, cfg, ws, wsb);
+}
+int tmpc_admm_pcg_f64(hipStream_t s, const tmpc_dims* dims, const tmpc_qp* qp, const tmpc_state* in,
+                      tmpc_state* out, uint32_t* iters, uint32_t* pcg_iters, const tmpc_admm_cfg* cfg,
+                      void* ws, size_t wsb) {
+  return admm_pcg_impl<double>(s, dims, qp, in, out, iters, pcg_iters, cfg, ws, wsb);
+}
+
+int tmpc_schur_build_f32(hipStream_t s, const tmpc_dims* dims, const tmpc_qp* qp, const float* rho,
+                         double sigma, double rho_f_factor, float* S, float* Phiinv) {
+  return schur_build_impl<float>(s, dims, qp, rho, sigma, rho_f_factor, S, Phiinv);
+}
+int tmpc_schur_build_f64(hipStream_t s, const tmpc_dims* dims, const tmpc_qp* qp, const double* rho,
+                         double sigma, double rho_f_factor, double* S, double* Phiinv) {
+  return schur_build_impl<double>(s, dims, qp, rho, sigma, rho_f_factor, S, Phiinv);
+}
+
+size_t tmpc_schur_pcg_workspace_bytes(int elem_bytes, int32_t B, int32_t T, int32_t n) {
+  tmpc_dims td{B, T, n, 1, 1, 0};
+  if (!dims_ok(&td)) return 0;
+  const Dims d = to_dims(&td);
+  return elem_bytes == 8 ? pcg_vec_bytes<double>(d) : pcg_vec_bytes<float>(d);
+}
+int tmpc_schur_pcg_f32(hipStream_t s, int32_t B, int32_t T, int32_t n, const float* S, const float* Phiinv,
+                       const float* rhs, const float* x0, float* x, uint32_t* iters, double eps,
+                       int32_t max_iter, void* ws, size_t wsb) {
+  return schur_pcg_impl<float>(s, B, T, n, S, Phiinv, rhs, x0, x, iters, eps, max_iter, ws, wsb);
+}
+int tmpc_schur_pcg_f64(hipStream_t s, int32_t B, int32_t T, int32_t n, const double* S,
+                       const double* Phiinv, const double* rhs, const double* x0, double* x,
+                       uint32_t* iters, double eps, int32_t max_iter, void* ws, size_t wsb) {
+  return schur_pcg_impl<double>(s, B, T, n, S, Phiinv, rhs, x0, x, iters, eps, max_iter, ws, wsb);
+}
+
+int tmpc_quadrotor_linearize_f32(hipStream_t s, int32_t B, int32_t N, const float* states,
+                                 const float* controls, double dt, const double* params, float* A_minus,
+                                 float* c) {
+  return quad_impl<float>(s, B, N, states, controls, dt, params, A_minus, c);
+}
+int tmpc_quadrotor_linearize_f64(hipStream_t s, int32_t B, int32_t N, const double* states,
+                                 const double* controls, double dt, const double* params, double* A_minus,
+                                 double* c) {
+  return quad_impl<double>(s, B, N, states, controls, dt, params, A_minus, c);
+}
+
+}  // extern "C"

@@ -1,0 +1,97 @@
+// Shared device-side types and helpers for the gfx950 MPC kernels.
+//
+// Data at the boundary keeps the reference's batched layout: a leading problem
+// axis and row-major blocks per problem (turbompc/solvers/qp_data.py:11-100 as
+// seen by the FFI under vmap "broadcast_all",
+// turbompc/solvers/admm/admm_cudss_ffi_backend.py:131-155).  Internal
+// workspaces are stage-major ([t][b][...]) so the problems that share a
+// wavefront read one contiguous run of HBM per stage.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace tmpc {
+
+constexpr int kWave = 64;
+
+struct Dims {
+  int B, T, N, n, nx, n0, m;
+};
+
+template <typename R>
+struct QPDev {
+  const R *D, *E, *q, *A0, *Am, *Ap, *G, *l, *u, *c0, *c;
+  const R* slack_w;  // (B,) or null (= 0)
+};
+
+template <typename R>
+struct StateDev {
+  R *x, *z, *y_g, *y_f0, *y_f, *xi, *rho;
+};
+
+// packed symmetric (lower) index of element (i, k)
+__device__ __forceinline__ int pidx(int i, int k) {
+  return i >= k ? ((i * (i + 1)) >> 1) + k : ((k * (k + 1)) >> 1) + i;
+}
+__host__ __device__ __forceinline__ int packed_size(int n) { return (n * (n + 1)) / 2; }
+
+// `it % k == 0` with XLA's integer remainder convention (x % 0 == x), which is
+// what the reference's jnp expressions evaluate to when k == 0.
+__device__ __forceinline__ bool mod_zero(int it, int k) {
+  return k > 0 ? (it % k) == 0 : it == 0;
+}
+
+template <typename R>
+__device__ __forceinline__ R rmax(R a, R b) {
+  return a > b ? a : b;
+}
+template <typename R>
+__device__ __forceinline__ R rmin(R a, R b) {
+  return a < b ? a : b;
+}
+template <typename R>
+__device__ __forceinline__ R rabs(R a) {
+  return a < R(0) ? -a : a;
+}
+__device__ __forceinline__ float rsqrt_(float a) { return sqrtf(a); }
+__device__ __forceinline__ double rsqrt_(double a) { return sqrt(a); }
+
+template <typename R>
+__device__ __forceinline__ R rinf() {
+  return __builtin_huge_val();
+}
+
+// One workgroup is one wavefront; LDS traffic between lanes of the wave is
+// ordered by this barrier (a single-wave s_barrier is cheap on CDNA).
+__device__ __forceinline__ void wsync() { __syncthreads(); }
+
+// A wavefront is split into P = 64 / g groups of g lanes; group p owns one
+// problem and lane i of the group owns row i of every stage block.
+// Reads always use `prob` (clamped into [0, B) so a partially filled last
+// wave never reads past the arrays); writes are predicated on `live`.  The idle
+// tail lanes get lane >= g, so every row-bounded access skips them.
+struct Group {
+  int lane;   // lane within group, 0..g-1 (>= g for the idle tail lanes)
+  int gid;    // group within wave
+  int prob;   // problem index, clamped to B-1
+  bool live;  // owns a real row of a real problem
+  bool real;  // the group maps to a real problem (any lane, including lane >= g)
+};
+
+__device__ __forceinline__ Group make_group(int g, int P, int B) {
+  Group G;
+  const int tid = threadIdx.x;
+  G.gid = tid / g;
+  G.lane = tid - G.gid * g;
+  if (G.gid >= P) {  // idle tail lanes of the wave
+    G.gid = P - 1;
+    G.lane = g + (tid - P * g);
+  }
+  const int raw = blockIdx.x * P + G.gid;
+  G.prob = raw < B ? raw : B - 1;
+  G.live = (G.lane < g) && (tid < P * g) && (raw < B);
+  G.real = (tid < P * g) && (raw < B);
+  return G;
+}
+
+}  // namespace tmpc

@@ -1,0 +1,183 @@
+"""Batched quadratic-tracking optimal control problems (host side, torch tensors).
+
+Follows OptimalControlProblem (turbompc/problems/optimal_control_problem.py:123-1480)
+for explicit integrators and diagonal tracking weights, where the QP blocks
+have closed forms:
+  * cost (get_cost_linearized_blocks, :1068-1174, stage cost :982-1009, terminal
+    cost :1011-1032):  D_t = 2 diag(w_x, w_u) for t < N, D_N = 2 diag(w_x + w_f, w_u),
+    E = 0, q_t = -2 diag(w) z_ref_t (control reference only when
+    penalize_control_reference, else 0);
+  * initial condition (:914-980): A0 = [I 0], c0 = x0;
+  * dynamics (explicit branch, :1217-1272): A_minus_t = [df/dx, df/du],
+    A_plus_t = [-I 0], c_t = -f(xbar, ubar) + A xbar + B ubar;
+  * box bounds (:413-471): one G row per state/control coordinate with a finite
+    bound (|b| < 1e6 on either side), l/u the bounds.
+Every tensor has a leading batch axis B.  Subclasses provide the dynamics.
+"""
+from __future__ import annotations
+
+from typing import Dict, Optional, Tuple
+
+import torch
+
+from ..solvers.qp_data import QPCostBlocks, QPData, QPEqualityBlocks, QPInequalityBlocks
+
+BOUND_INF = 1.0e6
+
+
+class QuadraticTrackingOCP:
+    """Base class: tracking cost, initial-state equality, box bounds."""
+
+    def __init__(
+        self,
+        *,
+        horizon: int,
+        num_states: int,
+        num_controls: int,
+        initial_state: torch.Tensor,  # (B, nx)
+        weights_state: torch.Tensor,  # (B, nx)
+        weights_control: torch.Tensor,  # (B, nu)
+        weights_final: torch.Tensor,  # (B, nx)
+        reference_state: Optional[torch.Tensor] = None,  # (B, T, nx)
+        reference_control: Optional[torch.Tensor] = None,  # (B, T, nu)
+        penalize_control_reference: bool = False,
+        state_bounds: Optional[Tuple[torch.Tensor, torch.Tensor]] = None,  # (nx,), (nx,)
+        control_bounds: Optional[Tuple[torch.Tensor, torch.Tensor]] = None,  # (nu,), (nu,)
+        initial_guess_final_state: Optional[torch.Tensor] = None,  # (B, nx)
+        dtype: torch.dtype = torch.float64,
+        device="cpu",
+    ):
+        self.horizon = int(horizon)
+        self.num_state_variables = int(num_states)
+        self.num_control_variables = int(num_controls)
+        self.dtype, self.device = dtype, torch.device(device)
+        cv = lambda t: torch.as_tensor(t).to(device=self.device, dtype=dtype).contiguous()  # noqa: E731
+        self.x0 = cv(initial_state)
+        self.B = int(self.x0.shape[0])
+        T, nx, nu = self.horizon + 1, num_states, num_controls
+        self.wx, self.wu, self.wf = cv(weights_state), cv(weights_control), cv(weights_final)
+        self.x_ref = cv(reference_state) if reference_state is not None else torch.zeros(
+            (self.B, T, nx), dtype=dtype, device=self.device)
+        self.u_ref = cv(reference_control) if reference_control is not None else torch.zeros(
+            (self.B, T, nu), dtype=dtype, device=self.device)
+        self.penalize_control_reference = bool(penalize_control_reference)
+        inf = torch.full((nx,), BOUND_INF, dtype=dtype)
+        infu = torch.full((nu,), BOUND_INF, dtype=dtype)
+        xl, xu = (cv(b) for b in state_bounds) if state_bounds is not None else (-inf.to(self.device), inf.to(self.device))
+        ul, uu = (cv(b) for b in control_bounds) if control_bounds is not None else (-infu.to(self.device), infu.to(self.device))
+        self.x_bounds, self.u_bounds = (xl, xu), (ul, uu)
+        # active rows: a finite bound on either side (optimal_control_problem.py:191-199)
+        self.state_mask = (xl > -BOUND_INF) | (xu < BOUND_INF)
+        self.control_mask = (ul > -BOUND_INF) | (uu < BOUND_INF)
+        self.num_inequality_constraints = int(self.state_mask.sum() + self.control_mask.sum())
+        self.x_final_guess = cv(initial_guess_final_state) if initial_guess_final_state is not None else self.x0
+        self.std_dynamics = True  # explicit integrators: A_plus = [-I 0], E = 0
+        self._static = None
+
+    # ------------------------------------------------------------ blocks ----
+    def cost_blocks(self):
+        B, N, nx, nu = self.B, self.horizon, self.num_state_variables, self.num_control_variables
+        T, n = N + 1, nx + nu
+        w = torch.cat([self.wx, self.wu], dim=-1)  # (B, n)
+        wN = torch.cat([self.wx + self.wf, self.wu], dim=-1)
+        wt = w.unsqueeze(1).expand(B, T, n).clone()
+        wt[:, N] = wN
+        D = torch.diag_embed(2.0 * wt)
+        E = torch.zeros((B, N, n, n), dtype=self.dtype, device=self.device)
+        uref = self.u_ref if self.penalize_control_reference else torch.zeros_like(self.u_ref)
+        zref = torch.cat([self.x_ref, uref], dim=-1)
+        q = -2.0 * wt * zref
+        return D.contiguous(), E, q.contiguous()
+
+    def initial_equality(self):
+        nx, nu = self.num_state_variables, self.num_control_variables
+        A0 = torch.zeros((self.B, nx, nx + nu), dtype=self.dtype, device=self.device)
+        A0[:, :, :nx] = torch.eye(nx, dtype=self.dtype, device=self.device)
+        return A0, self.x0.clone()
+
+    def a_plus(self):
+        nx, nu = self.num_state_variables, self.num_control_variables
+        Ap = torch.zeros((self.B, self.horizon, nx, nx + nu), dtype=self.dtype, device=self.device)
+        Ap[..., :nx] = -torch.eye(nx, dtype=self.dtype, device=self.device)
+        return Ap
+
+    def inequality_blocks(self):
+        nx, nu = self.num_state_variables, self.num_control_variables
+        T, n, m = self.horizon + 1, nx + nu, self.num_inequality_constraints
+        rows = [i for i in range(nx) if bool(self.state_mask[i])] + [nx + j for j in range(nu) if bool(self.control_mask[j])]
+        G1 = torch.zeros((m, n), dtype=self.dtype, device=self.device)
+        for r, col in enumerate(rows):
+            G1[r, col] = 1.0
+        lo = torch.cat([self.x_bounds[0][self.state_mask], self.u_bounds[0][self.control_mask]])
+        hi = torch.cat([self.x_bounds[1][self.state_mask], self.u_bounds[1][self.control_mask]])
+        G = G1.expand(self.B, T, m, n).contiguous()
+        return G, lo.expand(self.B, T, m).contiguous(), hi.expand(self.B, T, m).contiguous()
+
+    def dynamics_blocks(self, states: torch.Tensor, controls: torch.Tensor):
+        """A_minus (B,N,nx,n), c (B,N,nx) linearized at (states, controls)."""
+        raise NotImplementedError
+
+    def build_qp(self, states: torch.Tensor, controls: torch.Tensor) -> QPData:
+        """QP of one SQP iteration (TurboMPCSolver._build_qp_data, turbompc_solver.py:1098-1156)."""
+        if self._static is None:
+            D, E, q = self.cost_blocks()
+            A0, c0 = self.initial_equality()
+            G, l, u = self.inequality_blocks()
+            self._static = (D, E, q, A0, c0, self.a_plus(), G, l, u)
+        D, E, q, A0, c0, Ap, G, l, u = self._static
+        Am, c = self.dynamics_blocks(states, controls)
+        return QPData(
+            cost=QPCostBlocks(D, E, q),
+            eq=QPEqualityBlocks(A0, Am, Ap, c0, c),
+            ineq=QPInequalityBlocks(G, l, u, torch.zeros((), dtype=self.dtype), False),
+        )
+
+    def initial_guess(self) -> Tuple[torch.Tensor, torch.Tensor]:
+        """Straight line from x0 to the final guess, +1e-6; controls 1e-6
+        (optimal_control_problem.py:819-839)."""
+        N = self.horizon
+        t = torch.arange(N + 1, dtype=self.dtype, device=self.device).view(1, N + 1, 1)
+        a1, a2 = (N - t) / N, t / N
+        states = self.x0.unsqueeze(1) * a1 + self.x_final_guess.unsqueeze(1) * a2 + 1e-6
+        controls = torch.zeros((self.B, N + 1, self.num_control_variables), dtype=self.dtype, device=self.device) + 1e-6
+        return states.contiguous(), controls.contiguous()
+
+    def to(self, device=None, dtype=None):
+        """Copy of the problem with every tensor moved/cast."""
+        import copy
+
+        other = copy.copy(self)
+        dtype = dtype or self.dtype
+        device = torch.device(device) if device is not None else self.device
+        for k, v in list(vars(self).items()):
+            if torch.is_tensor(v):
+                setattr(other, k, v.to(device=device, dtype=dtype if v.is_floating_point() else v.dtype))
+            elif isinstance(v, tuple) and v and torch.is_tensor(v[0]):
+                setattr(other, k, tuple(t.to(device=device, dtype=dtype) for t in v))
+        other.dtype, other.device, other._static = dtype, device, None
+        return other
+
+    def weights_dict(self) -> Dict[str, torch.Tensor]:
+        return {
+            "weights_penalization_reference_state_trajectory": self.wx,
+            "weights_penalization_control_squared": self.wu,
+            "weights_penalization_final_state": self.wf,
+        }
+
+
+class LinearOCP(QuadraticTrackingOCP):
+    """x_{t+1} = A x_t + B u_t (+ b): constant dynamics blocks, c_t = -b."""
+
+    def __init__(self, *, A: torch.Tensor, Bm: torch.Tensor, b: Optional[torch.Tensor] = None, **kw):
+        super().__init__(**kw)
+        self.A = torch.as_tensor(A).to(self.device, self.dtype)
+        self.Bm = torch.as_tensor(Bm).to(self.device, self.dtype)
+        self.b = (torch.as_tensor(b).to(self.device, self.dtype) if b is not None
+                  else torch.zeros((self.B, self.num_state_variables), dtype=self.dtype, device=self.device))
+
+    def dynamics_blocks(self, states, controls):
+        N = self.horizon
+        AB = torch.cat([self.A, self.Bm], dim=-1)  # (B, nx, n)
+        Am = AB.unsqueeze(1).expand(self.B, N, *AB.shape[1:]).contiguous()
+        c = (-self.b).unsqueeze(1).expand(self.B, N, self.num_state_variables).contiguous()
+        return Am, c

@@ -1,0 +1,136 @@
+"""ctypes marshalling of the fused ADMM entry points (tmpc_admm_direct_*, tmpc_admm_pcg_*).
+
+Counterparts of the reference's FFI wrappers
+  admm_cudss_ffi_solve  (turbompc/solvers/admm/admm_cudss_ffi_backend.py:62-258)
+  admm_ffi_solve        (turbompc/solvers/admm/admm_ffi_backend.py:55-268)
+with the same inputs (QP blocks, warm-start state, solver attributes) and
+outputs (final state, iteration counts).  The Schur matrix is factorized (or S
+and Phiinv are built) on the device, so no precomputed `schur` argument is
+needed.
+"""
+from __future__ import annotations
+
+import ctypes
+from typing import Optional, Tuple
+
+import torch
+
+from ... import _lib
+from ..qp_data import QPData
+
+_WS_CACHE = {}
+
+
+def _ws(kind: str, nbytes: int, device: torch.device) -> torch.Tensor:
+    key = (kind, device)
+    t = _WS_CACHE.get(key)
+    if t is None or t.numel() < nbytes:
+        t = _lib.workspace(nbytes, device)
+        _WS_CACHE[key] = t
+    return t
+
+
+def qp_struct(qp: QPData, slack_weight: Optional[torch.Tensor]):
+    B, T, n, nx, n0, m = qp.dims
+    keep = []
+
+    def p(t):
+        if t is None:
+            return None
+        t = t.contiguous()
+        keep.append(t)
+        return _lib.ptr(t)
+
+    s = _lib.QP(
+        p(qp.cost.D), p(qp.cost.E), p(qp.cost.q), p(qp.eq.A0), p(qp.eq.A_minus), p(qp.eq.A_plus),
+        p(qp.ineq.G) if m else None, p(qp.ineq.l) if m else None, p(qp.ineq.u) if m else None,
+        p(qp.eq.c0), p(qp.eq.c), p(slack_weight),
+    )
+    return s, keep
+
+
+def state_struct(x, z_g, y_g, y_f0, y_f, xi_g, rho):
+    return _lib.State(*[_lib.ptr(t) for t in (x, z_g, y_g, y_f0, y_f, xi_g, rho)])
+
+
+def cfg_struct(*, max_iter, check_every, adapt_rho_every, pcg_max_iter, use_slack, flags, sigma, eps_abs, eps_rel,
+               rho_min, rho_max, adaptive_rho_tolerance, rho_f_factor, alpha, pcg_eps) -> _lib.AdmmCfg:
+    return _lib.AdmmCfg(
+        int(max_iter), int(check_every), int(adapt_rho_every), int(pcg_max_iter), int(bool(use_slack)), int(flags),
+        float(sigma), float(eps_abs), float(eps_rel), float(rho_min), float(rho_max),
+        float(adaptive_rho_tolerance), float(rho_f_factor), float(alpha), float(pcg_eps),
+    )
+
+
+def admm_hip_solve(qp: QPData, state0, *, schur: str, cfg: _lib.AdmmCfg,
+                   slack_weight: Optional[torch.Tensor] = None, want_pcg_iters: bool = False):
+    """Run the fused ADMM on the device.  `state0` is an ADMMState of batched
+    tensors; returns (state fields tuple, iters (B,), pcg_iters or None)."""
+    lib = _lib.load()
+    B, T, n, nx, n0, m = qp.dims
+    dev, dt = qp.device, qp.dtype
+    sfx = _lib.suffix(dt)
+    dims = _lib.Dims(B, T, n, nx, n0, m)
+    if slack_weight is not None:
+        slack_weight = torch.as_tensor(slack_weight, dtype=dt, device=dev).expand(B).contiguous()
+    cq, keep = qp_struct(qp, slack_weight)
+
+    def prep(t, shape):
+        t = torch.as_tensor(t, dtype=dt, device=dev)
+        return t.expand(shape).contiguous().clone() if t.shape != shape else t.contiguous().clone()
+
+    outs = [
+        prep(state0.x_blocks, (B, T, n)),
+        prep(state0.z_g, (B, T, m)),
+        prep(state0.y_g, (B, T, m)),
+        prep(state0.y_f_0, (B, n0)),
+        prep(state0.y_f_dyn, (B, T - 1, nx)),
+        prep(state0.xi_g, (B, T, m)),
+        prep(state0.rho_bar, (B,)),
+    ]
+    sv = state_struct(*outs)
+    iters = torch.zeros(B, dtype=torch.int32, device=dev)
+    stream = _lib.stream_handle(dev)
+    if schur == "direct":
+        nbytes = lib.tmpc_admm_direct_workspace_bytes(ctypes.sizeof(ctypes.c_double) if dt == torch.float64 else 4,
+                                                      ctypes.byref(dims))
+        ws = _ws("admm_direct", nbytes, dev)
+        st = getattr(lib, f"tmpc_admm_direct_{sfx}")(
+            stream, ctypes.byref(dims), ctypes.byref(cq), ctypes.byref(sv), ctypes.byref(sv),
+            _lib.ptr(iters), ctypes.byref(cfg), _lib.ptr(ws), nbytes,
+        )
+        _lib.check(f"tmpc_admm_direct_{sfx}", st)
+        pcg_iters = None
+    elif schur == "pcg":
+        nbytes = lib.tmpc_admm_pcg_workspace_bytes(8 if dt == torch.float64 else 4, ctypes.byref(dims))
+        ws = _ws("admm_pcg", nbytes, dev)
+        pcg_iters = (torch.zeros((B, max(cfg.max_iter, 1)), dtype=torch.int32, device=dev)
+                     if want_pcg_iters and cfg.max_iter > 0 else None)
+        st = getattr(lib, f"tmpc_admm_pcg_{sfx}")(
+            stream, ctypes.byref(dims), ctypes.byref(cq), ctypes.byref(sv), ctypes.byref(sv),
+            _lib.ptr(iters), _lib.ptr(pcg_iters), ctypes.byref(cfg), _lib.ptr(ws), nbytes,
+        )
+        _lib.check(f"tmpc_admm_pcg_{sfx}", st)
+    else:
+        raise ValueError(f"unknown schur mode {schur!r}")
+    del keep
+    return outs, iters, pcg_iters
+
+
+def schur_build(qp: QPData, rho: torch.Tensor, sigma: float, rho_f_factor: float) -> Tuple[torch.Tensor, torch.Tensor]:
+    """compute_S_Phiinv on the device for every problem (rho (B,))."""
+    lib = _lib.load()
+    B, T, n, nx, n0, m = qp.dims
+    dims = _lib.Dims(B, T, n, nx, n0, m)
+    cq, keep = qp_struct(qp, None)
+    rho = torch.as_tensor(rho, dtype=qp.dtype, device=qp.device).expand(B).contiguous()
+    S = torch.empty((B, T, n, 3 * n), dtype=qp.dtype, device=qp.device)
+    P = torch.empty_like(S)
+    sfx = _lib.suffix(qp.dtype)
+    st = getattr(lib, f"tmpc_schur_build_{sfx}")(
+        _lib.stream_handle(qp.device), ctypes.byref(dims), ctypes.byref(cq), _lib.ptr(rho), float(sigma),
+        float(rho_f_factor), _lib.ptr(S), _lib.ptr(P),
+    )
+    _lib.check(f"tmpc_schur_build_{sfx}", st)
+    del keep
+    return S, P
