@@ -149,16 +149,18 @@ int tmpc_blktri_solve_f64(hipStream_t stream, int32_t B, int32_t T, int32_t n, c
  * adjoint linear term; l, u, c0, c are ignored (the constraints are
  * homogeneous).  dz (B,T,n); mult (B, n0 + N*nx + T*m) laid out
  * [y_f0 | y_f_dyn | y_ineq] (turbompc/solvers/turbompc_solver.py:727-763).
- * Method: multipliers on the factorization kernel of S_rho = P + rho C^T C +
- * rho G_act^T G_act (iterative refinement of the augmented Lagrangian; the
- * stationarity row is exact at every step).  rho <= 0 selects a default scaled
- * to max|D|; iters is the refinement count (<= 0: default). */
+ * Method: the KKT regrouped by stage is block tridiagonal with blocks of size
+ * nb = n + max(n0, nx) + m (nb <= 64); it is factorized by the same block
+ * LDL^T kernel as the ADMM Schur matrix after a quasi-definite shift
+ * reg * max|D| (reg <= 0: 1e-12), and refine_steps rounds of iterative
+ * refinement against the unshifted matrix remove the shift (< 0: 2 in fp64,
+ * 3 in fp32).  Inactive rows get zero multipliers, as in the reference. */
 size_t tmpc_adjoint_kkt_workspace_bytes(int elem_bytes, const tmpc_dims* dims);
 int tmpc_adjoint_kkt_f32(hipStream_t stream, const tmpc_dims* dims, const tmpc_qp* qp, float* dz,
-                         float* mult, double rho, int32_t iters, uint32_t flags, void* workspace,
+                         float* mult, double reg, int32_t refine_steps, uint32_t flags, void* workspace,
                          size_t workspace_bytes);
 int tmpc_adjoint_kkt_f64(hipStream_t stream, const tmpc_dims* dims, const tmpc_qp* qp, double* dz,
-                         double* mult, double rho, int32_t iters, uint32_t flags, void* workspace,
+                         double* mult, double reg, int32_t refine_steps, uint32_t flags, void* workspace,
                          size_t workspace_bytes);
 
 /* ---- SQP linearization: rotor-thrust quadrotor, RK4 ------------------------

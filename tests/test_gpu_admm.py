@@ -1,10 +1,17 @@
 """GPU parity of the fused ADMM (direct and PCG Schur solves), the adjoint KKT
 and the quadrotor linearization against the CPU oracle, through the C ABI.
 
-fp64 cases must match the oracle to 1e-9 (normwise relative); fp32 cases to
+Parity protocol (fixed iteration counts, adapt_rho_every = 0): fp64 must match
+the fp64 oracle to 1e-9 (normwise relative); fp32 must match the fp64 oracle to
 1e-4, or -- where the fp32 oracle itself sits further than that from the fp64
-oracle because of the conditioning of S -- to within 4x the fp32 oracle's own
-distance from the fp64 result.
+result because of the conditioning of S -- to within 4x the fp32 oracle's own
+distance.
+
+Adaptive rho is tested separately with a looser bar: the rho candidate
+rho * sqrt(r_p / r_d) is a ratio of residual norms that cancel, so two correct
+implementations summing in different orders move rho by ~1e-9 relative and the
+iterates after the change by up to ~1e-6 (measured: oracle vs GPU rho differ by
+2e-9, states by 4e-7 one iteration later).
 """
 import numpy as np
 import pytest
@@ -62,7 +69,7 @@ def _assert_state_close(out, ref, tol):
 def test_admm_direct_fp64_fixed_iterations(std, shape):
     B, T, n, nx, m = shape
     qp = random_qp(B, T, n, nx, m, seed=41, std=std)
-    cfg = oracle.OracleCfg(max_iter=30, check_every=25, adapt_rho_every=25, sigma=1e-6, eps_abs=1e-9,
+    cfg = oracle.OracleCfg(max_iter=30, check_every=25, adapt_rho_every=0, sigma=1e-6, eps_abs=1e-9,
                            eps_rel=1e-9, rho_f_factor=1000.0, alpha=1.0)
     ref, it_ref, _, out, stats = _run_pair(qp, cfg, torch.float64)
     np.testing.assert_array_equal(stats.num_iter.cpu().numpy(), it_ref)
@@ -79,13 +86,15 @@ def test_admm_direct_fp64_adaptive_rho_and_termination(alpha):
     ref, it_ref, _, out, stats = _run_pair(qp, cfg, torch.float64)
     np.testing.assert_array_equal(stats.num_iter.cpu().numpy(), it_ref)
     assert len(set(it_ref.tolist())) > 1  # problems stop at different iterations
-    _assert_state_close(out, ref, 1e-8)
+    assert rel_err(out.rho_bar, ref.rho_bar) < 1e-7
+    assert np.any(ref.rho_bar != 0.1)  # rho did adapt
+    _assert_state_close(out, ref, 1e-5)
 
 
 def test_admm_direct_config1_fp32():
     prob = configs.config1(B=64, seed=0)
     qp = prob.build_qp(*prob.initial_guess())
-    cfg = oracle.OracleCfg(max_iter=50, check_every=25, adapt_rho_every=25, sigma=1e-6, eps_abs=1e-9, eps_rel=1e-9,
+    cfg = oracle.OracleCfg(max_iter=50, check_every=25, adapt_rho_every=0, sigma=1e-6, eps_abs=1e-9, eps_rel=1e-9,
                            rho_f_factor=1000.0, alpha=1.0)
     ref, it_ref, _, out, stats = _run_pair(qp, cfg, torch.float32)
     ref32, _, _ = oracle.admm_solve(qp, zero_state(qp, 0.1), cfg, dtype=np.float32)
@@ -98,7 +107,7 @@ def test_admm_direct_config1_fp32():
 def test_admm_direct_quadrotor_qp_fp32_and_fp64():
     prob = make_quadrotor_config(B=8, seed=0, dtype=torch.float64, device=DEV)
     qp = prob.build_qp(*prob.initial_guess()).to("cpu")
-    cfg = oracle.OracleCfg(max_iter=20, check_every=25, adapt_rho_every=25, sigma=1e-6, eps_abs=1e-9, eps_rel=1e-9,
+    cfg = oracle.OracleCfg(max_iter=20, check_every=25, adapt_rho_every=0, sigma=1e-6, eps_abs=1e-9, eps_rel=1e-9,
                            rho_f_factor=1000.0, alpha=1.0)
     ref, it_ref, _, out64, _ = _run_pair(qp, cfg, torch.float64)
     _assert_state_close(out64, ref, 1e-9)
@@ -111,8 +120,8 @@ def test_admm_direct_quadrotor_qp_fp32_and_fp64():
 
 def test_admm_direct_warm_start_and_in_place_state():
     qp = random_qp(6, 10, 6, 4, 3, seed=43, std=True)
-    cfg = oracle.OracleCfg(max_iter=15, check_every=5, adapt_rho_every=5, sigma=1e-6, eps_abs=1e-12, eps_rel=1e-12,
-                           rho_f_factor=100.0, alpha=1.6, adaptive_rho_tolerance=1.2)
+    cfg = oracle.OracleCfg(max_iter=15, check_every=5, adapt_rho_every=0, sigma=1e-6, eps_abs=1e-12, eps_rel=1e-12,
+                           rho_f_factor=100.0, alpha=1.6)
     st0 = zero_state(qp, 0.1)
     mid, _, _ = oracle.admm_solve(qp, st0, cfg)
     ref, it_ref, _ = oracle.admm_solve(qp, mid, cfg)
@@ -121,27 +130,40 @@ def test_admm_direct_warm_start_and_in_place_state():
     _, _, s1 = solver.solve(qpd, _state_to_dev(st0, torch.float64), alpha=1.6)
     _, stats, s2 = solver.solve(qpd, s1, alpha=1.6)
     np.testing.assert_array_equal(stats.num_iter.cpu().numpy(), it_ref)
-    _assert_state_close(s2, ref, 1e-8)
+    _assert_state_close(s2, ref, 1e-9)
 
 
 def test_admm_pcg_config2_fp64():
     prob = configs.config2(B=6, seed=0)
     qp = prob.build_qp(*prob.initial_guess())
-    cfg = oracle.OracleCfg(max_iter=12, check_every=25, adapt_rho_every=25, sigma=1e-6, eps_abs=1e-9, eps_rel=1e-9,
+    cfg = oracle.OracleCfg(max_iter=12, check_every=25, adapt_rho_every=0, sigma=1e-6, eps_abs=1e-9, eps_rel=1e-9,
                            rho_f_factor=1000.0, alpha=1.0, pcg_eps=1e-6, pcg_max_iter=50)
     ref, it_ref, pcg_ref, out, stats = _run_pair(qp, cfg, torch.float64, backend=AdmmBackend.HIP_PCG, schur="pcg")
     np.testing.assert_array_equal(stats.num_iter.cpu().numpy(), it_ref)
-    assert np.all(stats.num_pcg_iters.sum(1).cpu().numpy() == pcg_ref)
-    _assert_state_close(out, ref, 1e-8)
+    # the tolerance stop can flip by one iteration between two summation orders
+    assert np.all(np.abs(stats.num_pcg_iters.sum(1).cpu().numpy() - pcg_ref) <= 2)
+    _assert_state_close(out, ref, 1e-6)
+
+
+def test_admm_pcg_fixed_pcg_iterations_fp64():
+    # pcg_eps = 0 runs exactly pcg_max_iter PCG iterations per ADMM iteration
+    prob = configs.config2(B=5, seed=1)
+    qp = prob.build_qp(*prob.initial_guess())
+    cfg = oracle.OracleCfg(max_iter=6, check_every=25, adapt_rho_every=0, sigma=1e-6, eps_abs=1e-9, eps_rel=1e-9,
+                           rho_f_factor=1000.0, alpha=1.0, pcg_eps=0.0, pcg_max_iter=6)
+    ref, it_ref, pcg_ref, out, stats = _run_pair(qp, cfg, torch.float64, backend=AdmmBackend.HIP_PCG, schur="pcg")
+    np.testing.assert_array_equal(stats.num_pcg_iters.sum(1).cpu().numpy(), pcg_ref)
+    _assert_state_close(out, ref, 1e-9)
 
 
 def test_admm_pcg_matches_direct_when_tight():
     qp = random_qp(4, 12, 6, 4, 3, seed=44, std=True)
-    cfg = oracle.OracleCfg(max_iter=10, check_every=25, adapt_rho_every=25, sigma=1e-6, eps_abs=1e-9, eps_rel=1e-9,
+    cfg = oracle.OracleCfg(max_iter=10, check_every=25, adapt_rho_every=0, sigma=1e-6, eps_abs=1e-9, eps_rel=1e-9,
                            rho_f_factor=100.0, alpha=1.0, pcg_eps=1e-26, pcg_max_iter=400)
     ref, _, _ = oracle.admm_solve(qp, zero_state(qp, 0.1), cfg, schur="direct")
     _, _, _, out, _ = _run_pair(qp, cfg, torch.float64, backend=AdmmBackend.HIP_PCG, schur="pcg")
-    assert rel_err(out.x_blocks, ref.x_blocks) < 1e-7
+    # PCG stops once |eta| < 1e-12 (absolute floor of pcg_primal.py:113)
+    assert rel_err(out.x_blocks, ref.x_blocks) < 1e-6
 
 
 def test_adjoint_kkt_matches_dense_oracle_fp64():

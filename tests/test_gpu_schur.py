@@ -65,6 +65,13 @@ def test_schur_pcg_matches_oracle(shape):
     xo, ito = oracle.pcg(S, P, rhs, x0, eps=1e-8, max_iter=40)
     t = lambda a: torch.tensor(a, device=DEV)  # noqa: E731
     x, it = hip_pcg_solve(t(S), t(P), t(rhs), t(x0), eps=1e-8, max_iters=40)
+    # stopped by tolerance: counts may differ by one between summation orders,
+    # iterates agree to the stopping tolerance
+    assert np.all(np.abs(it.cpu().numpy() - ito) <= 1)
+    assert rel_err(x, xo) < 1e-6
+    # fixed iteration count (eps = 0): parity at 1e-9
+    xo, ito = oracle.pcg(S, P, rhs, x0, eps=0.0, max_iter=5)
+    x, it = hip_pcg_solve(t(S), t(P), t(rhs), t(x0), eps=0.0, max_iters=5)
     np.testing.assert_array_equal(it.cpu().numpy(), ito)
     assert rel_err(x, xo) < 1e-9
 

@@ -258,6 +258,7 @@ __global__ __launch_bounds__(kWave) void admm_chunk_kernel(AdmmArgs<R> a) {
     done = false;
     res[0] = res[1] = res[4] = res[5] = rinf<R>();
     res[2] = res[3] = R(1);
+    if (G.live && i == 0) a.ctl[b * 4 + 2] = 0;
   } else {
     it = a.ctl[b * 4 + 0];
     done = a.ctl[b * 4 + 1] != 0;

@@ -11,6 +11,7 @@
 #include "factor.hpp"
 #include "pcg.hpp"
 #include "quadrotor.hpp"
+#include "adjoint.hpp"
 
 namespace tmpc {
 namespace {
@@ -98,6 +99,14 @@ int launch_status() {
   return hipGetLastError() == hipSuccess ? TMPC_OK : TMPC_ELAUNCH;
 }
 
+// Dynamic LDS above the 64 KiB default needs an explicit opt-in per kernel.
+template <typename K>
+void lds_optin(K kernel, size_t bytes) {
+  if (bytes > 65536)
+    (void)hipFuncSetAttribute(reinterpret_cast<const void*>(kernel), hipFuncAttributeMaxDynamicSharedMemorySize,
+                              (int)bytes);
+}
+
 // copies the warm start into the working/output state (skipped when aliased)
 template <typename R>
 int copy_state(hipStream_t s, const Dims& d, const tmpc_state* in, const tmpc_state* out) {
@@ -117,7 +126,8 @@ int copy_state(hipStream_t s, const Dims& d, const tmpc_state* in, const tmpc_st
 template <typename R>
 int launch_factor_qp(hipStream_t s, const Dims& d, const QPDev<R>& q, const R* rho, R sigma,
                      R rho_f_factor, int32_t* ctl, R* thinv) {
-  const size_t smem = factor_smem_bytes<R>(d);
+  const size_t smem = factor_smem_bytes(d);
+  lds_optin(factor_kernel<R, SRC_QP>, smem);
   hipLaunchKernelGGL((factor_kernel<R, SRC_QP>), dim3(d.B), dim3(kWave), smem, s, d, q,
                      (const R*)nullptr, rho, sigma, rho_f_factor, ctl, thinv);
   return launch_status();
@@ -222,7 +232,8 @@ int blktri_factor_impl(hipStream_t s, int B, int T, int n, const R* S, void* ws,
   const Dims d = to_dims(&td);
   if (!ws || wsb < align_up((size_t)T * B * packed_size(n) * sizeof(R))) return TMPC_EWORKSPACE;
   QPDev<R> q{};
-  const size_t smem = factor_smem_bytes<R>(d);
+  const size_t smem = factor_smem_bytes(d);
+  lds_optin(factor_kernel<R, SRC_S>, smem);
   hipLaunchKernelGGL((factor_kernel<R, SRC_S>), dim3(B), dim3(kWave), smem, s, d, q, S,
                      (const R*)nullptr, R(0), R(0), (int32_t*)nullptr, static_cast<R*>(ws));
   return launch_status();
@@ -256,128 +267,77 @@ int blktri_solve_impl(hipStream_t s, int B, int T, int n, const R* S, const R* r
 }
 
 // --------------------------------------------------------------- adjoint ----
+KktDims kkt_dims(const Dims& d) {
+  KktDims k;
+  k.B = d.B;
+  k.T = d.T;
+  k.N = d.N;
+  k.n = d.n;
+  k.nx = d.nx;
+  k.n0 = d.n0;
+  k.m = d.m;
+  k.p = std::max(d.n0, d.nx);
+  k.nb = d.n + k.p + d.m;
+  return k;
+}
+
 template <typename R>
 size_t adjoint_ws_bytes(const Dims& d) {
-  const size_t B = d.B, T = d.T, N = d.N;
-  return direct_ws_bytes<R>(d) + align_up(B * T * d.n * sizeof(R)) +
-         4 * align_up(B * T * std::max(d.m, 1) * sizeof(R)) + 2 * align_up(B * d.n0 * sizeof(R)) +
-         2 * align_up(B * N * d.nx * sizeof(R)) + align_up(B * sizeof(R)) +
-         align_up(B * sizeof(uint32_t));
+  const KktDims k = kkt_dims(d);
+  const size_t B = d.B, T = d.T, nb = k.nb;
+  return align_up(B * T * nb * 3 * nb * sizeof(R)) + align_up(T * B * packed_size(k.nb) * sizeof(R)) +
+         5 * align_up(B * T * nb * sizeof(R)) + align_up(B * sizeof(R));
 }
 
 template <typename R>
-__global__ void adjoint_init_kernel(Dims d, const R* __restrict__ D, R rho_rel, R* x, R* z, R* yg,
-                                    R* xi, R* lu, R* y0, R* c0, R* yf, R* c, R* rho) {
-  const int b = blockIdx.x;
-  const int tid = threadIdx.x;
-  const size_t T = d.T, N = d.N;
-  for (size_t e = tid; e < T * d.n; e += blockDim.x) x[b * T * d.n + e] = R(0);
-  for (size_t e = tid; e < T * d.m; e += blockDim.x) {
-    z[b * T * d.m + e] = R(0);
-    yg[b * T * d.m + e] = R(0);
-    xi[b * T * d.m + e] = R(0);
-    lu[b * T * d.m + e] = R(0);
-  }
-  for (int e = tid; e < d.n0; e += blockDim.x) {
-    y0[(size_t)b * d.n0 + e] = R(0);
-    c0[(size_t)b * d.n0 + e] = R(0);
-  }
-  for (size_t e = tid; e < N * d.nx; e += blockDim.x) {
-    yf[b * N * d.nx + e] = R(0);
-    c[b * N * d.nx + e] = R(0);
-  }
-  // penalty scaled to the cost curvature of this problem
-  __shared__ R red[256];
-  R mx = R(0);
-  for (size_t e = tid; e < T * d.n * d.n; e += blockDim.x) mx = rmax(mx, rabs(D[b * T * d.n * d.n + e]));
-  red[tid] = mx;
-  __syncthreads();
-  if (tid == 0) {
-    R v = R(0);
-    for (unsigned k = 0; k < blockDim.x; ++k) v = rmax(v, red[k]);
-    rho[b] = rho_rel * rmax(v, R(1e-30));
-  }
-}
-
-template <typename R>
-__global__ void adjoint_pack_kernel(Dims d, const R* y0, const R* yf, const R* yg, R* mult) {
-  const int b = blockIdx.x;
-  const size_t N = d.N, T = d.T;
-  const size_t L = d.n0 + N * d.nx + T * d.m;
-  R* o = mult + b * L;
-  for (size_t e = threadIdx.x; e < L; e += blockDim.x) {
-    R v;
-    if (e < (size_t)d.n0)
-      v = y0[(size_t)b * d.n0 + e];
-    else if (e < d.n0 + N * d.nx)
-      v = yf[b * N * d.nx + (e - d.n0)];
-    else
-      v = yg[b * T * d.m + (e - d.n0 - N * d.nx)];
-    o[e] = v;
-  }
-}
-
-template <typename R>
-int adjoint_impl(hipStream_t s, const tmpc_dims* dims, const tmpc_qp* qp, R* dz, R* mult, double rho,
-                 int32_t iters, uint32_t flags, void* ws, size_t wsb) {
+int adjoint_impl(hipStream_t s, const tmpc_dims* dims, const tmpc_qp* qp, R* dz, R* mult, double reg,
+                 int32_t refine, uint32_t flags, void* ws, size_t wsb) {
+  (void)flags;
   if (!dims_ok(dims)) return TMPC_EBADSHAPE;
   if (!qp || !qp->D || !qp->E || !qp->q || !qp->A0 || !qp->A_minus || !qp->A_plus || !dz || !mult)
     return TMPC_EBADARG;
   if (dims->m > 0 && !qp->G) return TMPC_EBADARG;
   const Dims d = to_dims(dims);
+  const KktDims k = kkt_dims(d);
+  if (k.nb > kWave) return TMPC_EBADSHAPE;
   if (!ws || wsb < adjoint_ws_bytes<R>(d)) return TMPC_EWORKSPACE;
   const bool f64 = sizeof(R) == 8;
-  const R rho_rel = rho > 0 ? (R)rho : (f64 ? R(1e5) : R(1e2));
-  const int K = iters > 0 ? iters : (f64 ? 12 : 20);
-  // workspace: [direct solve | state | homogeneous l,u,c0,c | iters]
+  const R eps = reg > 0 ? (R)reg : R(1e-12);
+  const int steps = refine >= 0 ? refine : (f64 ? 2 : 3);
+  const size_t B = d.B, T = d.T, nb = k.nb, L = B * T * nb;
   Carver c{static_cast<char*>(ws)};
-  c.off = direct_ws_bytes<R>(d);
-  const size_t B = d.B, T = d.T, N = d.N, mm = std::max(d.m, 1);
-  R* x = c.take<R>(B * T * d.n);
-  R* z = c.take<R>(B * T * mm);
-  R* yg = c.take<R>(B * T * mm);
-  R* xi = c.take<R>(B * T * mm);
-  R* lu = c.take<R>(B * T * mm);
-  R* y0 = c.take<R>(B * d.n0);
-  R* c0 = c.take<R>(B * d.n0);
-  R* yf = c.take<R>(B * N * d.nx);
-  R* cz = c.take<R>(B * N * d.nx);
-  R* rh = c.take<R>(B);
-  uint32_t* it = c.take<uint32_t>(B);
-  hipLaunchKernelGGL((adjoint_init_kernel<R>), dim3(d.B), dim3(256), 0, s, d,
-                     static_cast<const R*>(qp->D), rho_rel, x, z, yg, xi, lu, y0, c0, yf, cz, rh);
+  R* K = c.take<R>(B * T * nb * 3 * nb);
+  R* th = c.take<R>(T * B * packed_size(k.nb));
+  R* dreg = c.take<R>(L);
+  R* rhs = c.take<R>(L);
+  R* x = c.take<R>(L);
+  R* r = c.take<R>(L);
+  R* dx = c.take<R>(L);
+  R* shift = c.take<R>(B);
+  const QPDev<R> q = to_qp<R>(qp);
+  hipLaunchKernelGGL((kkt_scale_kernel<R>), dim3(d.B), dim3(256), 0, s, k, q.D, eps, shift);
+  hipLaunchKernelGGL((kkt_assemble_kernel<R>), dim3(d.B * d.T), dim3(256), 0, s, k, q, shift, K, dreg, rhs);
   int st = launch_status();
   if (st) return st;
-  tmpc_qp hq = *qp;
-  hq.l = lu;
-  hq.u = lu;
-  hq.c0 = c0;
-  hq.c = cz;
-  hq.slack_weight = nullptr;
-  if (d.m == 0) hq.G = hq.l;  // unused
-  tmpc_state sv{x, z, yg, y0, yf, xi, rh};
-  tmpc_admm_cfg cfg{};
-  cfg.max_iter = K;
-  cfg.check_every = 0;
-  cfg.adapt_rho_every = 0;
-  cfg.use_slack = 0;
-  cfg.flags = flags;
-  cfg.sigma = 0.0;
-  cfg.eps_abs = 0.0;
-  cfg.eps_rel = 0.0;
-  cfg.rho_min = 0.0;
-  cfg.rho_max = 1e300;
-  cfg.adaptive_rho_tolerance = 5.0;
-  cfg.rho_f_factor = 1.0;
-  cfg.alpha = 1.0;
-  st = admm_direct_impl<R>(s, dims, &hq, &sv, &sv, it, &cfg, ws, direct_ws_bytes<R>(d));
+  // block-tridiagonal factorization of the stage-block KKT (factor.hpp, SRC_S)
+  Dims kd{d.B, d.T, d.N, k.nb, 1, 1, 0};
+  const size_t smem = factor_smem_bytes(kd);
+  lds_optin(factor_kernel<R, SRC_S>, smem);
+  hipLaunchKernelGGL((factor_kernel<R, SRC_S>), dim3(d.B), dim3(kWave), smem, s, kd, QPDev<R>{}, (const R*)K,
+                     (const R*)nullptr, R(0), R(0), (int32_t*)nullptr, th);
+  st = launch_status();
   if (st) return st;
-  if (hipMemcpyAsync(dz, x, B * T * d.n * sizeof(R), hipMemcpyDeviceToDevice, s) != hipSuccess)
-    return TMPC_ELAUNCH;
-  hipLaunchKernelGGL((adjoint_pack_kernel<R>), dim3(d.B), dim3(256), 0, s, d, y0, yf, yg, mult);
+  const int P = kWave / k.nb;
+  launch_blktri_solve_nc<R, 0>(s, kd, k.nb, P, K, th, rhs, x);
+  for (int it = 0; it < steps; ++it) {
+    hipLaunchKernelGGL((kkt_residual_kernel<R>), dim3((d.B + P - 1) / P), dim3(kWave), 0, s, k, P, (const R*)K,
+                       (const R*)dreg, (const R*)rhs, (const R*)x, r);
+    launch_blktri_solve_nc<R, 0>(s, kd, k.nb, P, K, th, r, dx);
+    hipLaunchKernelGGL((axpy_kernel<R>), dim3((unsigned)((L + 255) / 256)), dim3(256), 0, s, L, (const R*)dx, x);
+  }
+  hipLaunchKernelGGL((kkt_unpack_kernel<R>), dim3(d.B), dim3(256), 0, s, k, (const R*)x, dz, mult);
   return launch_status();
 }
-
 
 // ----------------------------------------------------------- PCG family ----
 template <typename R>
@@ -406,7 +366,8 @@ PcgVecs<R> carve_vecs(Carver& c, const Dims& d, R* x) {
 template <typename R>
 int launch_schur_build(hipStream_t s, const Dims& d, const QPDev<R>& q, const R* rho, R sigma, R rfac,
                        int32_t* ctl, R* S, R* Phi) {
-  const size_t smem = factor_smem_bytes<R>(d);
+  const size_t smem = factor_smem_bytes(d);
+  lds_optin(schur_build_kernel<R>, smem);
   hipLaunchKernelGGL((schur_build_kernel<R>), dim3(d.B), dim3(kWave), smem, s, d, q, rho, sigma, rfac, ctl,
                      S, Phi);
   return launch_status();
@@ -611,14 +572,14 @@ size_t tmpc_adjoint_kkt_workspace_bytes(int elem_bytes, const tmpc_dims* dims) {
   return elem_bytes == 8 ? adjoint_ws_bytes<double>(d) : adjoint_ws_bytes<float>(d);
 }
 int tmpc_adjoint_kkt_f32(hipStream_t s, const tmpc_dims* dims, const tmpc_qp* qp, float* dz,
-                         float* mult, double rho, int32_t iters, uint32_t flags, void* ws,
+                         float* mult, double reg, int32_t refine_steps, uint32_t flags, void* ws,
                          size_t wsb) {
-  return adjoint_impl<float>(s, dims, qp, dz, mult, rho, iters, flags, ws, wsb);
+  return adjoint_impl<float>(s, dims, qp, dz, mult, reg, refine_steps, flags, ws, wsb);
 }
 int tmpc_adjoint_kkt_f64(hipStream_t s, const tmpc_dims* dims, const tmpc_qp* qp, double* dz,
-                         double* mult, double rho, int32_t iters, uint32_t flags, void* ws,
+                         double* mult, double reg, int32_t refine_steps, uint32_t flags, void* ws,
                          size_t wsb) {
-  return adjoint_impl<double>(s, dims, qp, dz, mult, rho, iters, flags, ws, wsb);
+  return adjoint_impl<double>(s, dims, qp, dz, mult, reg, refine_steps, flags, ws, wsb);
 }
 
 size_t tmpc_admm_pcg_workspace_bytes(int elem_bytes, const tmpc_dims* dims) {

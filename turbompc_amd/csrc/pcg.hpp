@@ -34,83 +34,85 @@ __global__ __launch_bounds__(kWave) void schur_build_kernel(Dims d, QPDev<R> qp,
   const int T = d.T, N = d.N, n = d.n, nx = d.nx, n0 = d.n0, m = d.m;
   const int nn = n * n, w3 = 3 * n;
   extern __shared__ unsigned char smem_raw[];
-  R* sm = reinterpret_cast<R*>(smem_raw);
-  R* A = sm;          // theta_t -> theta_t^{-1}
-  R* Ainv = A + nn;   // theta_{t-1}^{-1}
-  R* ph = Ainv + nn;  // phi_{t-1}
-  R* tmp = ph + nn;
-  R* rowk = tmp + nn;
-  R* colk = rowk + n;
-  R* sG = colk + n;
-  R* sAm = sG + m * n;
-  R* sAp = sAm + nx * n;
-  R* sApp = sAp + nx * n;
-  R* sA0 = sApp + nx * n;
-  const R rho_i = rho[b];
-  const R rho_f = rho_i * rho_f_factor;
-  for (int e = tid; e < n0 * n; e += kWave) sA0[e] = qp.A0[(size_t)b * n0 * n + e];
+  // computed in double like factor_kernel; S and Phiinv are rounded on store
+  Cmp* sm = reinterpret_cast<Cmp*>(smem_raw);
+  Cmp* A = sm;          // theta_t -> theta_t^{-1}
+  Cmp* Ainv = A + nn;   // theta_{t-1}^{-1}
+  Cmp* ph = Ainv + nn;  // phi_{t-1}
+  Cmp* tmp = ph + nn;
+  Cmp* rowk = tmp + nn;
+  Cmp* colk = rowk + n;
+  Cmp* sG = colk + n;
+  Cmp* sAm = sG + m * n;
+  Cmp* sAp = sAm + nx * n;
+  Cmp* sApp = sAp + nx * n;
+  Cmp* sA0 = sApp + nx * n;
+  const Cmp rho_i = (Cmp)rho[b];
+  const Cmp rho_f = rho_i * (Cmp)rho_f_factor;
+  const Cmp sig = (Cmp)sigma;
+  for (int e = tid; e < n0 * n; e += kWave) sA0[e] = (Cmp)qp.A0[(size_t)b * n0 * n + e];
   R* Sb = S + (size_t)b * T * n * w3;
   R* Pb = Phiinv + (size_t)b * T * n * w3;
   for (int t = 0; t < T; ++t) {
-    for (int e = tid; e < m * n; e += kWave) sG[e] = qp.G[((size_t)b * T + t) * m * n + e];
+    for (int e = tid; e < m * n; e += kWave) sG[e] = (Cmp)qp.G[((size_t)b * T + t) * m * n + e];
     if (t < N)
       for (int e = tid; e < nx * n; e += kWave) {
-        sAm[e] = qp.Am[((size_t)b * N + t) * nx * n + e];
-        sAp[e] = qp.Ap[((size_t)b * N + t) * nx * n + e];
+        sAm[e] = (Cmp)qp.Am[((size_t)b * N + t) * nx * n + e];
+        sAp[e] = (Cmp)qp.Ap[((size_t)b * N + t) * nx * n + e];
       }
     wsync();
     for (int e = tid; e < nn; e += kWave) {
       const int i = e / n, j = e - (e / n) * n;
-      R v = qp.D[((size_t)b * T + t) * nn + e] + (i == j ? sigma : R(0));
-      R gg = R(0);
+      Cmp v = (Cmp)qp.D[((size_t)b * T + t) * nn + e] + (i == j ? sig : Cmp(0));
+      Cmp gg = 0;
       for (int r = 0; r < m; ++r) gg += sG[r * n + i] * sG[r * n + j];
-      R cc = R(0);
+      Cmp cc = 0;
       if (t == 0)
         for (int r = 0; r < n0; ++r) cc += sA0[r * n + i] * sA0[r * n + j];
       if (t < N)
         for (int r = 0; r < nx; ++r) cc += sAm[r * n + i] * sAm[r * n + j];
       if (t > 0)
         for (int r = 0; r < nx; ++r) cc += sApp[r * n + i] * sApp[r * n + j];
-      const R th = v + rho_i * gg + rho_f * cc;
+      const Cmp th = v + rho_i * gg + rho_f * cc;
       A[e] = th;
-      Sb[((size_t)t * n + i) * w3 + n + j] = th;                        // theta_t
-      Sb[((size_t)t * n + i) * w3 + j] = t > 0 ? ph[e] : R(0);          // phi_{t-1}
+      Sb[((size_t)t * n + i) * w3 + n + j] = (R)th;                        // theta_t
+      Sb[((size_t)t * n + i) * w3 + j] = t > 0 ? (R)ph[e] : R(0);          // phi_{t-1}
     }
     wsync();
     gj_invert_spd(A, rowk, colk, n);  // theta_t^{-1} (theta_t is SPD)
     for (int e = tid; e < nn; e += kWave) {
       const int i = e / n, j = e - (e / n) * n;
-      Pb[((size_t)t * n + i) * w3 + n + j] = -A[e];
+      Pb[((size_t)t * n + i) * w3 + n + j] = (R)(-A[e]);
     }
     if (t > 0) {
       // tmp = phi_{t-1} theta_{t-1}^{-1};  prev_t = theta_t^{-1} tmp
       for (int e = tid; e < nn; e += kWave) {
         const int i = e / n, j = e - (e / n) * n;
-        R s = R(0);
+        Cmp s = 0;
         for (int l = 0; l < n; ++l) s += ph[i * n + l] * Ainv[l * n + j];
         tmp[e] = s;
       }
       wsync();
       for (int e = tid; e < nn; e += kWave) {
         const int i = e / n, j = e - (e / n) * n;
-        R s = R(0);
+        Cmp s = 0;
         for (int l = 0; l < n; ++l) s += A[i * n + l] * tmp[l * n + j];
-        Pb[((size_t)t * n + i) * w3 + j] = s;
+        Pb[((size_t)t * n + i) * w3 + j] = (R)s;
       }
       wsync();
       // next_{t-1} = theta_{t-1}^{-1} phi_{t-1}^T theta_t^{-1}; tmp = phi_{t-1}^T theta_t^{-1}
       for (int e = tid; e < nn; e += kWave) {
         const int i = e / n, j = e - (e / n) * n;
-        R s = R(0);
+        Cmp s = 0;
         for (int l = 0; l < n; ++l) s += ph[l * n + i] * A[l * n + j];
         tmp[e] = s;
       }
       wsync();
       for (int e = tid; e < nn; e += kWave) {
         const int i = e / n, j = e - (e / n) * n;
-        R s = R(0);
+        Cmp s = 0;
         for (int l = 0; l < n; ++l) s += Ainv[i * n + l] * tmp[l * n + j];
-        Pb[((size_t)(t - 1) * n + i) * w3 + 2 * n + j] = s;
+        Pb[((size_t)(t - 1) * n + i) * w3 + 2 * n + j] = (R)s;
       }
       wsync();
     } else {
@@ -124,15 +126,15 @@ __global__ __launch_bounds__(kWave) void schur_build_kernel(Dims d, QPDev<R> qp,
       const int i = e / n, j = e - (e / n) * n;
       Ainv[e] = A[e];
       if (t < N) {
-        R s = R(0);
+        Cmp s = 0;
         for (int r = 0; r < nx; ++r) s += sAp[r * n + i] * sAm[r * n + j];
-        ph[e] = qp.E[((size_t)b * N + t) * nn + e] + rho_f * s;
+        ph[e] = (Cmp)qp.E[((size_t)b * N + t) * nn + e] + rho_f * s;
       }
     }
     wsync();
     for (int e = tid; e < nn; e += kWave) {
       const int i = e / n, j = e - (e / n) * n;
-      Sb[((size_t)t * n + i) * w3 + 2 * n + j] = t < N ? ph[j * n + i] : R(0);
+      Sb[((size_t)t * n + i) * w3 + 2 * n + j] = t < N ? (R)ph[j * n + i] : R(0);
       if (t == N) Pb[((size_t)t * n + i) * w3 + 2 * n + j] = R(0);
     }
     if (t < N)
@@ -395,6 +397,7 @@ __global__ __launch_bounds__(kWave) void admm_pcg_chunk_kernel(AdmmPcgArgs<R> pa
     done = false;
     res[0] = res[1] = res[4] = res[5] = rinf<R>();
     res[2] = res[3] = R(1);
+    if (G.live && i == 0) a.ctl[b * 4 + 2] = 0;
   } else {
     it = a.ctl[b * 4 + 0];
     done = a.ctl[b * 4 + 1] != 0;
