@@ -1,0 +1,85 @@
+"""GPU SQP (TurboMPCSolver, admm_hip_direct) against the CPU SQP restatement
+(oracle/sqp_cpu.py) on the quadrotor workload of the benchmark (config 3
+shapes, small batch): 5 SQP iterations x 20 ADMM iterations, fixed counts.
+"""
+import copy
+
+import numpy as np
+import pytest
+import torch
+
+import oracle
+from helpers import TOL, rel_err
+from oracle.sqp_cpu import quadrotor_sqp
+from turbompc_amd.problems.quadrotor import make_quadrotor_config
+from turbompc_amd.solvers.turbompc_solver import DEFAULT_SOLVER_PARAMS, TurboMPCSolver
+
+pytestmark = pytest.mark.gpu
+
+
+def _params(n_sqp, admm_iters):
+    p = copy.deepcopy(DEFAULT_SOLVER_PARAMS)
+    p["num_sqp_iteration_max"] = n_sqp
+    p["tol_convergence"] = 0.0
+    p["admm"]["max_iter"] = admm_iters
+    p["admm"]["adapt_rho_every"] = 0
+    p["admm"]["relaxation_parameter"] = 1.0
+    return p
+
+
+def _cpu_sqp(B, seed, n_sqp, admm_iters, dtype):
+    prob = make_quadrotor_config(B=B, seed=seed, dtype=torch.float64, device="cpu")
+    D, E, q = (t.numpy() for t in prob.cost_blocks())
+    A0, c0 = (t.numpy() for t in prob.initial_equality())
+    G, l, u = (t.numpy() for t in prob.inequality_blocks())
+    static = dict(D=D, E=E, q=q, A0=A0, c0=c0, A_plus=prob.a_plus().numpy(), G=G, l=l, u=u)
+    xg, ug = (t.numpy() for t in prob.initial_guess())
+    cfg = oracle.OracleCfg(max_iter=admm_iters, check_every=25, adapt_rho_every=0, sigma=1e-6, eps_abs=1e-9,
+                           eps_rel=1e-9, rho_f_factor=1000.0, alpha=1.0)
+    return quadrotor_sqp(static, xg, ug, dt=prob.dt, params=prob.params, cfg=cfg, rho0=0.1, n_sqp=n_sqp, dtype=dtype)
+
+
+@pytest.mark.parametrize("n_sqp", [1, 5])
+def test_quadrotor_sqp_fp64_matches_cpu(n_sqp):
+    B = 8
+    xs, us, st = _cpu_sqp(B, 0, n_sqp, 20, np.float64)
+    prob = make_quadrotor_config(B=B, seed=0, dtype=torch.float64, device="cuda")
+    solver = TurboMPCSolver(prob, _params(n_sqp, 20))
+    sol = solver.solve(solver.initial_guess())
+    torch.cuda.synchronize()
+    assert rel_err(sol.states, xs) < TOL[torch.float64]
+    assert rel_err(sol.controls, us) < TOL[torch.float64]
+    assert rel_err(sol.admm_state.y_f_dyn, st.y_f_dyn) < 1e-8
+    assert torch.all(sol.num_iter == n_sqp)
+    assert torch.all(sol.admm_iters[:, :n_sqp] == 20)
+
+
+def test_quadrotor_sqp_fp32_matches_cpu():
+    B = 16
+    xs, us, _ = _cpu_sqp(B, 1, 5, 20, np.float64)
+    xs32, us32, _ = _cpu_sqp(B, 1, 5, 20, np.float32)
+    prob = make_quadrotor_config(B=B, seed=1, dtype=torch.float32, device="cuda")
+    solver = TurboMPCSolver(prob, _params(5, 20))
+    sol = solver.solve(solver.initial_guess())
+    torch.cuda.synchronize()
+    for got, ref, ref32 in ((sol.states, xs, xs32), (sol.controls, us, us32)):
+        e, e_or = rel_err(got, ref), rel_err(ref32, ref)
+        assert e < max(TOL[torch.float32], 4 * e_or), (e, e_or)
+
+
+def test_sqp_stops_per_problem_on_tolerance():
+    # with a finite tolerance each problem stops on its own first-order error
+    B = 6
+    prob = make_quadrotor_config(B=B, seed=2, dtype=torch.float64, device="cuda")
+    p = _params(8, 20)
+    p["tol_convergence"] = 5e-2
+    solver = TurboMPCSolver(prob, p)
+    sol = solver.solve(solver.initial_guess())
+    it = sol.num_iter.cpu().numpy()
+    conv = sol.convergence_error.cpu().numpy()
+    assert np.all(it >= 1) and np.all(it <= 8)
+    # stopped problems satisfy the tolerance; problems at the cap may not
+    assert np.all((conv <= 5e-2) | (it == 8))
+    hist = sol.solver_stats.convergence_errors.cpu().numpy()
+    for b in range(B):
+        assert hist[b, it[b] - 1] == pytest.approx(conv[b])

@@ -1,0 +1,364 @@
+"""TurboMPC SQP solver with the gfx950 HIP backends.
+
+Mirrors turbompc/solvers/turbompc_solver.py: backend enums and name maps
+(:56-191, with the new members ADMM_HIP_DIRECT / ADMM_HIP_PCG /
+DIRECT_HIP_KKT), `TurboMPCSolution` (:225-237), `TurboMPCSolver(program,
+params, forward_backend=, backward_backend=)` (:303-438), `initial_guess`
+(:476-509), the SQP loop `_solve_impl` (:1519-1760) with the first-order
+convergence check (:1158-1225) and KKT state (:1387-1439), and the backward
+pass (`_build_backward_qp` :544-618, `_solve_backward_qp_direct` :706-779,
+weight and initial-state gradients :781-1018).
+
+Differences of form, not of semantics: every tensor has a leading batch axis
+(the reference vmaps one problem), problems stop independently exactly as a
+vmapped `lax.while_loop` does, and differentiation is exposed through
+`solve_vjp` / `DifferentiableSolve` instead of `jax.custom_vjp`.
+"""
+from __future__ import annotations
+
+import copy
+import enum
+from pathlib import Path
+from typing import Any, Dict, NamedTuple, Optional, Tuple, Union
+
+import torch
+import yaml
+
+from .admm.admm import ADMMSolver, ADMMState
+from .linear_systems_solvers.backends import AdmmBackend, SchurSolverBackend
+from .qp_data import QPData
+from .qp_ops import apply_C_parts, apply_Ct, apply_G, apply_Gt, apply_P, inf_norm
+from .qp_utils import ZShape, pack_x, pack_z
+
+_PARAMS_DIR = Path(__file__).resolve().parent / "params"
+
+
+def load_solver_params(name: str = "turbompc.yaml") -> Dict[str, Any]:
+    with open(_PARAMS_DIR / name) as f:
+        return yaml.safe_load(f)
+
+
+DEFAULT_SOLVER_PARAMS = load_solver_params("turbompc.yaml")
+
+
+class ForwardBackend(enum.IntEnum):
+    ADMM_JAX_LOOP_PCG = 0
+    ADMM_JAX_LOOP_PCG_FFI = 1
+    ADMM_JAX_LOOP_CUDSS_FFI = 2
+    ADMM_JAX_LOOP_JAX_DENSE = 3
+    ADMM_FUSED_PCG = 4
+    ADMM_FUSED_CUDSS = 5
+    ADMM_HIP_DIRECT = 6  # fused ADMM + block-tridiagonal factorize/solve (gfx950)
+    ADMM_HIP_PCG = 7  # fused ADMM + Schur PCG (gfx950)
+
+
+class BackwardBackend(enum.IntEnum):
+    ADMM_JAX_LOOP_PCG = 0
+    ADMM_JAX_LOOP_PCG_FFI = 1
+    ADMM_JAX_LOOP_CUDSS_FFI = 2
+    ADMM_JAX_LOOP_JAX_DENSE = 3
+    ADMM_FUSED_PCG = 4
+    ADMM_FUSED_CUDSS = 5
+    DIRECT_JAX_DENSE = 6
+    DIRECT_CUDSS_FFI = 7
+    DIRECT_HIP_KKT = 8  # stage-block adjoint KKT factorize/solve (gfx950)
+
+
+_FORWARD_BACKEND_COMPONENTS = {
+    ForwardBackend.ADMM_HIP_DIRECT: (AdmmBackend.HIP_DIRECT, SchurSolverBackend.IGNORED),
+    ForwardBackend.ADMM_HIP_PCG: (AdmmBackend.HIP_PCG, SchurSolverBackend.IGNORED),
+}
+
+_NAME_TO_FORWARD_BACKEND = {
+    "admm_jax_loop_pcg": ForwardBackend.ADMM_JAX_LOOP_PCG,
+    "admm_jax_loop_pcg_ffi": ForwardBackend.ADMM_JAX_LOOP_PCG_FFI,
+    "admm_jax_loop_cudss_ffi": ForwardBackend.ADMM_JAX_LOOP_CUDSS_FFI,
+    "admm_jax_loop_jax_dense": ForwardBackend.ADMM_JAX_LOOP_JAX_DENSE,
+    "admm_fused_pcg": ForwardBackend.ADMM_FUSED_PCG,
+    "admm_fused_cudss": ForwardBackend.ADMM_FUSED_CUDSS,
+    "admm_hip_direct": ForwardBackend.ADMM_HIP_DIRECT,
+    "admm_hip_pcg": ForwardBackend.ADMM_HIP_PCG,
+}
+_NAME_TO_BACKWARD_BACKEND = {
+    "admm_jax_loop_pcg": BackwardBackend.ADMM_JAX_LOOP_PCG,
+    "admm_jax_loop_pcg_ffi": BackwardBackend.ADMM_JAX_LOOP_PCG_FFI,
+    "admm_jax_loop_cudss_ffi": BackwardBackend.ADMM_JAX_LOOP_CUDSS_FFI,
+    "admm_jax_loop_jax_dense": BackwardBackend.ADMM_JAX_LOOP_JAX_DENSE,
+    "admm_fused_pcg": BackwardBackend.ADMM_FUSED_PCG,
+    "admm_fused_cudss": BackwardBackend.ADMM_FUSED_CUDSS,
+    "direct_jax_dense": BackwardBackend.DIRECT_JAX_DENSE,
+    "direct_cudss_ffi": BackwardBackend.DIRECT_CUDSS_FFI,
+    "direct_hip_kkt": BackwardBackend.DIRECT_HIP_KKT,
+}
+FORWARD_BACKEND_CHOICES = tuple(sorted(_NAME_TO_FORWARD_BACKEND))
+BACKWARD_BACKEND_CHOICES = tuple(sorted(_NAME_TO_BACKWARD_BACKEND))
+CONVERGENCE_CRITERION_CHOICES = ("first_order", "step")
+
+
+def parse_forward_backend(value: Union[str, ForwardBackend]) -> ForwardBackend:
+    if isinstance(value, ForwardBackend):
+        return value
+    if not isinstance(value, str):
+        raise TypeError(f"Expected str or ForwardBackend, got {type(value)}")
+    try:
+        return _NAME_TO_FORWARD_BACKEND[value.lower()]
+    except KeyError as exc:
+        raise ValueError(f"Unknown forward backend: {value!r}. Options: {sorted(_NAME_TO_FORWARD_BACKEND)}") from exc
+
+
+def parse_backward_backend(value: Union[str, BackwardBackend]) -> BackwardBackend:
+    if isinstance(value, BackwardBackend):
+        return value
+    if not isinstance(value, str):
+        raise TypeError(f"Expected str or BackwardBackend, got {type(value)}")
+    try:
+        return _NAME_TO_BACKWARD_BACKEND[value.lower()]
+    except KeyError as exc:
+        raise ValueError(f"Unknown backward backend: {value!r}. Options: {sorted(_NAME_TO_BACKWARD_BACKEND)}") from exc
+
+
+def parse_convergence_criterion(value: str) -> str:
+    if not isinstance(value, str):
+        raise TypeError(f"Expected str convergence criterion, got {type(value)}")
+    if value.lower() not in CONVERGENCE_CRITERION_CHOICES:
+        raise ValueError(f"Unknown convergence criterion: {value!r}. Options: {CONVERGENCE_CRITERION_CHOICES}")
+    return value.lower()
+
+
+class KKTState(NamedTuple):
+    states: torch.Tensor
+    controls: torch.Tensor
+    slack: torch.Tensor
+    y_f: torch.Tensor  # (B, T, nx)
+    y_ineq: torch.Tensor
+    ineq_active_lower_idx: torch.Tensor
+    ineq_active_upper_idx: torch.Tensor
+
+
+class SolverStats(NamedTuple):
+    admm_num_iters: torch.Tensor  # (B, max_iter)
+    eq_constraints_violations: torch.Tensor
+    ineq_constraints_violations: torch.Tensor
+    convergence_errors: torch.Tensor
+
+
+class TurboMPCSolution(NamedTuple):
+    states: torch.Tensor
+    controls: torch.Tensor
+    slack: torch.Tensor
+    status: int
+    num_iter: torch.Tensor  # (B,)
+    convergence_error: torch.Tensor  # (B,)
+    admm_iters: torch.Tensor  # (B, max_iter)
+    linesearch_alphas: Optional[torch.Tensor] = None
+    admm_state: Optional[ADMMState] = None
+    solver_stats: Optional[SolverStats] = None
+    dual_backward_guess: Optional[torch.Tensor] = None
+    kkt_state: Optional[KKTState] = None
+
+
+def identify_active_inequalities(g, l, u, eps_abs: float, eps_rel: float):
+    """min(g - l, u - g) <= eps_abs + eps_rel |bound| (turbompc_solver.py:269-292)."""
+    dl, du = g - l, u - g
+    use_upper = du < dl
+    tol = eps_abs + eps_rel * torch.where(use_upper, u.abs(), l.abs())
+    active = torch.minimum(dl, du) <= tol
+    return active & ~use_upper, active & use_upper
+
+
+def _where(mask: torch.Tensor, a: torch.Tensor, b: torch.Tensor) -> torch.Tensor:
+    return torch.where(mask.view(-1, *([1] * (a.dim() - 1))), a, b)
+
+
+class TurboMPCSolver:
+    """SQP solver that uses ADMM (on the GPU) for the QP subproblems."""
+
+    STATUS_SUCCESS = 0
+    STATUS_FAILED = -1
+
+    def __init__(
+        self,
+        program,
+        params: Optional[Dict[str, Any]] = None,
+        name: str = "TurboMPCSolver",
+        *,
+        forward_backend: Union[str, ForwardBackend] = ForwardBackend.ADMM_HIP_DIRECT,
+        backward_backend: Union[str, BackwardBackend] = BackwardBackend.DIRECT_HIP_KKT,
+        use_full_hessian: bool = True,
+    ):
+        self._program = program
+        self._name = name
+        self._params = copy.deepcopy(DEFAULT_SOLVER_PARAMS if params is None else params)
+        self._use_full_hessian = use_full_hessian
+        self._forward_backend = parse_forward_backend(forward_backend)
+        self._backward_backend = parse_backward_backend(backward_backend)
+        self._convergence_criterion = parse_convergence_criterion(
+            self._params.get("convergence_criterion", "first_order"))
+        if self._forward_backend not in _FORWARD_BACKEND_COMPONENTS:
+            raise ValueError(
+                f"forward backend {self._forward_backend.name} needs the reference's JAX/CUDA stack; "
+                "use 'admm_hip_direct' or 'admm_hip_pcg'")
+        if self._backward_backend != BackwardBackend.DIRECT_HIP_KKT:
+            raise ValueError(
+                f"backward backend {self._backward_backend.name} needs the reference's JAX/CUDA stack; "
+                "use 'direct_hip_kkt'")
+        if self._params.get("linesearch", False):
+            raise NotImplementedError("the merit line search (turbompc/solvers/linesearch.py) is not provided")
+        self._forward_admm_backend, self._forward_schur_backend = _FORWARD_BACKEND_COMPONENTS[self._forward_backend]
+        self._zshape = ZShape(program.horizon, program.num_state_variables, program.num_control_variables)
+        ap = self._params["admm"]
+        self._admm_solver_fwd = ADMMSolver(
+            zshape=self._zshape,
+            pcg_params=ap["pcg"],
+            sigma=ap["sigma"],
+            max_iter=ap["max_iter"],
+            eps_abs=ap.get("eps_abs", 1.0e-4),
+            eps_rel=ap.get("eps_rel", 1.0e-3),
+            rho_min=ap.get("rho_min", 1.0e-6),
+            rho_max=ap.get("rho_max", 1.0e6),
+            check_termination_every=ap.get("check_termination_every", 1),
+            adapt_rho_every=ap.get("adapt_rho_every", 5),
+            adaptive_rho_tolerance=ap.get("adaptive_rho_tolerance", 5.0),
+            rho_f_factor=ap.get("rho_f_factor", ap.get("active_constraint_rho_factor", 1000.0)),
+            admm_backend=self._forward_admm_backend,
+            use_slack=False,
+            std_dynamics=getattr(program, "std_dynamics", None),
+        )
+
+    program = property(lambda self: self._program)
+    params = property(lambda self: self._params)
+    name = property(lambda self: self._name)
+    forward_backend = property(lambda self: self._forward_backend)
+    backward_backend = property(lambda self: self._backward_backend)
+    forward_admm_backend = property(lambda self: self._forward_admm_backend)
+    forward_schur_backend = property(lambda self: self._forward_schur_backend)
+
+    # ------------------------------------------------------------------ API ----
+    def initial_guess(self, params=None) -> TurboMPCSolution:
+        """SQP-ADMM initial guess (turbompc_solver.py:476-509)."""
+        states, controls = self._program.initial_guess()
+        B, max_iter = states.shape[0], self._params["num_sqp_iteration_max"]
+        m = self._program.num_inequality_constraints
+        z = lambda *s: torch.zeros(s, dtype=states.dtype, device=states.device)  # noqa: E731
+        zi = lambda *s: torch.zeros(s, dtype=torch.int32, device=states.device)  # noqa: E731
+        return TurboMPCSolution(
+            states=states, controls=controls, slack=z(B, states.shape[1], m), status=self.STATUS_SUCCESS,
+            num_iter=zi(B), convergence_error=z(B), admm_iters=zi(B, max_iter), linesearch_alphas=None,
+            admm_state=None,
+            solver_stats=SolverStats(zi(B, max_iter), z(B, max_iter), z(B, max_iter), z(B, max_iter)),
+            dual_backward_guess=None, kkt_state=None,
+        )
+
+    def solve(self, initial_guess: TurboMPCSolution, problem_params=None, weights=None) -> TurboMPCSolution:
+        program = self._program if weights is None else self._program.with_weights(weights)
+        return self._solve_impl(program, initial_guess.states, initial_guess.controls, initial_guess.admm_state)
+
+    # ------------------------------------------------------------ internals ----
+    def _first_order_check(self, qp: QPData, states, controls, slacks, admm_state: ADMMState):
+        """_compute_first_order_convergence_error (turbompc_solver.py:1158-1225)."""
+        x = pack_x(states, controls)
+        stat = apply_P(qp, x) + qp.cost.q + apply_Ct(qp, admm_state.y_f_0, admm_state.y_f_dyn)
+        m = qp.dims[5]
+        if m:
+            stat = stat + apply_Gt(qp, admm_state.y_g)
+        stat_err = inf_norm(stat)
+        c0x, cx = apply_C_parts(qp, x)
+        eq_err = torch.maximum(inf_norm(c0x - qp.eq.c0), inf_norm(cx - qp.eq.c))
+        g = apply_G(qp, x) if m else torch.zeros_like(qp.ineq.l)
+        if qp.ineq.use_slack_variables:
+            g = g + slacks
+        if m:
+            viol = torch.maximum(torch.clamp(qp.ineq.l - g, min=0.0), torch.clamp(g - qp.ineq.u, min=0.0))
+            ineq_err = inf_norm(viol)
+        else:
+            ineq_err = torch.zeros_like(stat_err)
+        conv = torch.maximum(stat_err, torch.maximum(eq_err, ineq_err))
+        return conv, eq_err, ineq_err, g
+
+    def _build_kkt_state(self, states, controls, admm_state: ADMMState, g, l, u) -> KKTState:
+        """Active sets from proximity, disambiguated by the dual sign (turbompc_solver.py:1387-1439)."""
+        ap = self._params["admm"]
+        y_f = torch.cat([admm_state.y_f_0[:, None, : self._zshape.num_states], admm_state.y_f_dyn], dim=1)
+        y_ineq = admm_state.y_g
+        lo, up = identify_active_inequalities(g, l, u, ap["eps_abs"], ap["eps_rel"])
+        if y_ineq.shape[-1] > 0:
+            tol = ap["eps_abs"]
+            dl, du = y_ineq < -tol, y_ineq > tol
+            und = ~(dl | du)
+            lo, up = dl | (und & lo), du | (und & up)
+        return KKTState(states, controls, admm_state.xi_g, y_f, y_ineq, lo, up)
+
+    def _solve_impl(self, program, states, controls, admm_state0: Optional[ADMMState] = None) -> TurboMPCSolution:
+        """The SQP loop of turbompc_solver.py:1519-1760, batched with per-problem termination."""
+        P, ap = self._params, self._params["admm"]
+        max_iter, tol = int(P["num_sqp_iteration_max"]), float(P["tol_convergence"])
+        alpha = float(ap.get("relaxation_parameter", 1.0))
+        admm = self._admm_solver_fwd
+        B, dev, dt = states.shape[0], states.device, states.dtype
+        qp = program.build_qp(states, controls)
+        if admm_state0 is None:
+            admm_state0 = admm.initial_state(qp, rho_bar=ap["rho"], states0=torch.zeros_like(states),
+                                             controls0=torch.zeros_like(controls))
+        admm_state = admm_state0
+        slacks = admm_state0.xi_g
+        z_prev = pack_z(states, controls)
+        conv = torch.full((B,), float("inf"), dtype=dt, device=dev)
+        admm_iters = torch.zeros((B, max_iter), dtype=torch.int32, device=dev)
+        eq_v = torch.zeros((B, max_iter), dtype=dt, device=dev)
+        in_v = torch.zeros_like(eq_v)
+        conv_h = torch.zeros_like(eq_v)
+        num_iter = torch.zeros(B, dtype=torch.int32, device=dev)
+        active = torch.ones(B, dtype=torch.bool, device=dev)
+        kkt = None
+        for it in range(max_iter):
+            if it >= 1:
+                active = active & (conv > tol)
+                if tol > 0 and not bool(active.any()):
+                    break
+            (s_new, c_new), stats, adm_new = admm.solve(qp, admm_state, rho_bar=ap["rho"], alpha=alpha)
+            sl_new = adm_new.xi_g
+            z_new = pack_z(s_new, c_new)
+            step = (z_new - z_prev).abs().amax(dim=1)
+            if sl_new.shape[-1] > 0:
+                step = step + (sl_new - slacks).abs().flatten(1).amax(dim=1)
+            if self._convergence_criterion == "first_order" and it + 1 < max_iter:
+                qp_next = program.build_qp(s_new, c_new)
+                c_new_err, e_err, i_err, g = self._first_order_check(qp_next, s_new, c_new, sl_new, adm_new)
+            else:
+                rebuild = self._convergence_criterion == "step" and it + 1 < max_iter
+                qp_next = program.build_qp(s_new, c_new) if rebuild else qp
+                c_new_err = step if (it == 0 or self._convergence_criterion == "step") else conv
+                e_err = torch.zeros_like(step)
+                i_err = torch.zeros_like(step)
+                g = apply_G(qp_next, pack_x(s_new, c_new))
+            kkt_new = self._build_kkt_state(s_new, c_new, adm_new, g, qp_next.ineq.l, qp_next.ineq.u)
+            # commit where active (vmapped while_loop semantics)
+            sel = lambda a, b: _where(active, a, b)  # noqa: E731
+            states, controls, slacks, z_prev = sel(s_new, states), sel(c_new, controls), sel(sl_new, slacks), sel(z_new, z_prev)
+            admm_state = ADMMState(*[sel(a, b) for a, b in zip(adm_new, admm_state)])
+            qp = _select_qp(active, qp_next, qp)
+            kkt = kkt_new if kkt is None else KKTState(*[sel(a, b) for a, b in zip(kkt_new, kkt)])
+            conv = sel(c_new_err, conv)
+            admm_iters[:, it] = torch.where(active, stats.num_iter, admm_iters[:, it])
+            eq_v[:, it] = torch.where(active, e_err, eq_v[:, it])
+            in_v[:, it] = torch.where(active, i_err, in_v[:, it])
+            conv_h[:, it] = torch.where(active, c_new_err, conv_h[:, it])
+            num_iter = num_iter + active.to(torch.int32)
+        return TurboMPCSolution(
+            states=states, controls=controls, slack=admm_state.xi_g, status=self.STATUS_SUCCESS, num_iter=num_iter,
+            convergence_error=conv, admm_iters=admm_iters, linesearch_alphas=None, admm_state=admm_state,
+            solver_stats=SolverStats(admm_iters, eq_v, in_v, conv_h), kkt_state=kkt,
+        )
+
+
+def _select_qp(mask: torch.Tensor, a: QPData, b: QPData) -> QPData:
+    if a is b:
+        return a
+    pick = lambda x, y: x if x is y else _where(mask, x, y)  # noqa: E731
+    return QPData(
+        cost=type(a.cost)(pick(a.cost.D, b.cost.D), pick(a.cost.E, b.cost.E), pick(a.cost.q, b.cost.q)),
+        eq=type(a.eq)(pick(a.eq.A0, b.eq.A0), pick(a.eq.A_minus, b.eq.A_minus), pick(a.eq.A_plus, b.eq.A_plus),
+                      pick(a.eq.c0, b.eq.c0), pick(a.eq.c, b.eq.c)),
+        ineq=type(a.ineq)(pick(a.ineq.G, b.ineq.G), pick(a.ineq.l, b.ineq.l), pick(a.ineq.u, b.ineq.u),
+                          a.ineq.slack_penalization_weight, a.ineq.use_slack_variables),
+    )
