@@ -83,3 +83,18 @@ def test_sqp_stops_per_problem_on_tolerance():
     hist = sol.solver_stats.convergence_errors.cpu().numpy()
     for b in range(B):
         assert hist[b, it[b] - 1] == pytest.approx(conv[b])
+
+
+@pytest.mark.parametrize("dtype", [torch.float64, torch.float32])
+def test_first_order_check_kernel_matches_torch(dtype):
+    B = 12
+    prob = make_quadrotor_config(B=B, seed=3, dtype=dtype, device="cuda")
+    solver = TurboMPCSolver(prob, _params(2, 10))
+    sol = solver.solve(solver.initial_guess())
+    qp = prob.build_qp(sol.states, sol.controls)
+    args = (qp, sol.states, sol.controls, sol.slack, sol.admm_state)
+    ck, ek, ik, gk = solver._first_order_check(*args)
+    ct, et, it_, gt = solver._first_order_check_torch(*args)
+    tol = 1e-12 if dtype == torch.float64 else 1e-5
+    for a, b in ((ck, ct), (ek, et), (ik, it_), (gk, gt)):
+        assert rel_err(a, b) < tol

@@ -1,0 +1,39 @@
+"""Device-side SQP helpers (tmpc_sqp_first_order_*).
+
+first_order_check: _compute_first_order_convergence_error
+(turbompc/solvers/turbompc_solver.py:1158-1225) for the whole batch in one
+kernel, returning (conv, eq_err, ineq_err, g) with g = G x (+ slack).
+"""
+from __future__ import annotations
+
+import ctypes
+from typing import Optional
+
+import torch
+
+from .. import _lib
+from .admm.admm_hip_backend import qp_struct
+from .qp_data import QPData
+
+
+def first_order_check(qp: QPData, x: torch.Tensor, y_f0: torch.Tensor, y_f: torch.Tensor, y_g: torch.Tensor,
+                      slack: Optional[torch.Tensor] = None, slack_weight: float = 0.0):
+    lib = _lib.load()
+    B, T, n, nx, n0, m = qp.dims
+    dt, dev = qp.dtype, qp.device
+    dims = _lib.Dims(B, T, n, nx, n0, m)
+    cq, keep = qp_struct(qp, None)
+    x, y_f0, y_f, y_g = (t.to(dt).contiguous() for t in (x, y_f0, y_f, y_g))
+    slack = slack.to(dt).contiguous() if slack is not None else None
+    conv = torch.empty(B, dtype=dt, device=dev)
+    eq = torch.empty(B, dtype=dt, device=dev)
+    iq = torch.empty(B, dtype=dt, device=dev)
+    g = torch.empty((B, T, m), dtype=dt, device=dev)
+    sfx = _lib.suffix(dt)
+    st = getattr(lib, f"tmpc_sqp_first_order_{sfx}")(
+        _lib.stream_handle(dev), ctypes.byref(dims), ctypes.byref(cq), _lib.ptr(x), _lib.ptr(y_f0), _lib.ptr(y_f),
+        _lib.ptr(y_g), _lib.ptr(slack), float(slack_weight), _lib.ptr(conv), _lib.ptr(eq), _lib.ptr(iq), _lib.ptr(g),
+    )
+    _lib.check(f"tmpc_sqp_first_order_{sfx}", st)
+    del keep
+    return conv, eq, iq, g

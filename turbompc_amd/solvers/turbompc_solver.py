@@ -29,6 +29,7 @@ from .linear_systems_solvers.backends import AdmmBackend, SchurSolverBackend
 from .qp_data import QPData
 from .qp_ops import apply_C_parts, apply_Ct, apply_G, apply_Gt, apply_P, inf_norm
 from .qp_utils import ZShape, pack_x, pack_z
+from .sqp_hip import first_order_check
 
 _PARAMS_DIR = Path(__file__).resolve().parent / "params"
 
@@ -255,7 +256,14 @@ class TurboMPCSolver:
 
     # ------------------------------------------------------------ internals ----
     def _first_order_check(self, qp: QPData, states, controls, slacks, admm_state: ADMMState):
-        """_compute_first_order_convergence_error (turbompc_solver.py:1158-1225)."""
+        """_compute_first_order_convergence_error (turbompc_solver.py:1158-1225), one HIP kernel."""
+        x = pack_x(states, controls)
+        use_slack = bool(qp.ineq.use_slack_variables) and qp.dims[5] > 0
+        return first_order_check(qp, x, admm_state.y_f_0, admm_state.y_f_dyn, admm_state.y_g,
+                                 slacks if use_slack else None, float(qp.ineq.slack_penalization_weight))
+
+    def _first_order_check_torch(self, qp: QPData, states, controls, slacks, admm_state: ADMMState):
+        """Same check with torch operators; kept for validating the kernel."""
         x = pack_x(states, controls)
         stat = apply_P(qp, x) + qp.cost.q + apply_Ct(qp, admm_state.y_f_0, admm_state.y_f_dyn)
         m = qp.dims[5]
