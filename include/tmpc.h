@@ -52,6 +52,14 @@ typedef struct tmpc_state {
  * (explicit integrators without a control-rate cost).  Lets the solve skip
  * reading A_plus and E. */
 #define TMPC_FLAG_STD_DYNAMICS 1u
+/* With TMPC_FLAG_STD_DYNAMICS the direct solve streams stage records through
+ * a batched kernel when the shape allows it (n in {6, 9, 16, 17}, nx < n,
+ * m <= min(n, 8)).  TMPC_FLAG_GENERIC_KERNEL selects the generic per-stage
+ * kernel instead (same iteration; for cross-checks).  Bits 8-9 force the
+ * number of problems per wavefront of the streaming kernel (1-3; 0 = chosen
+ * from B). */
+#define TMPC_FLAG_GENERIC_KERNEL 2u
+#define TMPC_FLAG_STREAM_P(p) (((uint32_t)(p) & 3u) << 8)
 
 typedef struct tmpc_admm_cfg {
   int32_t max_iter, check_every, adapt_rho_every, pcg_max_iter, use_slack;

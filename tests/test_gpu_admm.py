@@ -19,6 +19,7 @@ import torch
 
 import oracle
 from helpers import TOL, random_qp, rel_err, zero_state
+from turbompc_amd import _lib
 from turbompc_amd.problems import configs
 from turbompc_amd.problems.quadrotor import QUAD_PARAMS, make_quadrotor_config
 from turbompc_amd.solvers.admm.admm import ADMMSolver, ADMMState
@@ -47,11 +48,11 @@ def _state_to_dev(st, dtype):
     return ADMMState(**{k: torch.as_tensor(np.asarray(getattr(st, k)), dtype=dtype, device=DEV) for k in FIELDS})
 
 
-def _run_pair(qp, cfg, dtype, backend=AdmmBackend.HIP_DIRECT, rho0=0.1, schur="direct"):
+def _run_pair(qp, cfg, dtype, backend=AdmmBackend.HIP_DIRECT, rho0=0.1, schur="direct", **kw):
     st0 = zero_state(qp, rho0)
     ref, it_ref, pcg_ref = oracle.admm_solve(qp, st0, cfg, schur=schur, dtype=np.float64)
     qpd = qp.to(DEV, dtype)
-    solver = _solver(qp, cfg, backend)
+    solver = _solver(qp, cfg, backend, **kw)
     (_, _), stats, out = solver.solve(qpd, _state_to_dev(st0, dtype), alpha=cfg.alpha)
     torch.cuda.synchronize()
     return ref, it_ref, pcg_ref, out, stats
@@ -193,3 +194,54 @@ def test_quadrotor_linearization_matches_complex_step(dtype):
     tol = 1e-12 if dtype == torch.float64 else 1e-5
     assert rel_err(Am, Jr) < tol
     assert rel_err(c, cr) < (1e-11 if dtype == torch.float64 else 1e-5)
+
+
+# ---- streaming kernel (explicit-integrator structure, stage records) ---------
+# B is chosen so that the last wavefront is partially filled for P = 2 and 3.
+
+@pytest.mark.parametrize("P", [1, 2, 3])
+@pytest.mark.parametrize("shape", [(13, 21, 6, 4, 2), (8, 11, 17, 13, 4), (7, 13, 9, 6, 5), (5, 9, 16, 12, 0)])
+def test_admm_stream_kernel_fp64_matches_oracle(P, shape):
+    B, T, n, nx, m = shape
+    qp = random_qp(B, T, n, nx, m, seed=51, std=True)
+    # residual pass every 3 iterations (no adaptation): exercises the
+    # residual sweep without changing the fixed-iteration trajectory
+    cfg = oracle.OracleCfg(max_iter=20, check_every=3, adapt_rho_every=0, sigma=1e-6, eps_abs=1e-12,
+                           eps_rel=1e-12, rho_f_factor=1000.0, alpha=1.6)
+    ref, it_ref, _, out, stats = _run_pair(qp, cfg, torch.float64, kernel_flags=_lib.flag_stream_p(P))
+    np.testing.assert_array_equal(stats.num_iter.cpu().numpy(), it_ref)
+    _assert_state_close(out, ref, 1e-9)
+
+
+@pytest.mark.parametrize("alpha", [1.0, 1.6])
+def test_admm_stream_kernel_adaptive_rho_and_termination(alpha):
+    qp = random_qp(11, 9, 6, 4, 3, seed=42, std=True)
+    cfg = oracle.OracleCfg(max_iter=200, check_every=2, adapt_rho_every=4, sigma=1e-6, eps_abs=1e-6, eps_rel=1e-6,
+                           rho_f_factor=50.0, alpha=alpha, adaptive_rho_tolerance=1.5)
+    ref, it_ref, _, out, stats = _run_pair(qp, cfg, torch.float64, kernel_flags=_lib.flag_stream_p(2))
+    np.testing.assert_array_equal(stats.num_iter.cpu().numpy(), it_ref)
+    assert len(set(it_ref.tolist())) > 1
+    assert np.any(ref.rho_bar != 0.1)
+    assert rel_err(out.rho_bar, ref.rho_bar) < 1e-7
+    _assert_state_close(out, ref, 1e-5)
+
+
+def test_admm_stream_kernel_matches_generic_on_bench_batch():
+    # the benchmark's shapes at a batch that selects P = 2 with a partial last
+    # wavefront: streaming and generic kernels run the same fp32 iteration
+    B = 4099
+    prob = make_quadrotor_config(B=B, seed=5, dtype=torch.float32, device=DEV)
+    qp = prob.build_qp(*prob.initial_guess())
+    cfg = oracle.OracleCfg(max_iter=20, check_every=25, adapt_rho_every=0, sigma=1e-6, eps_abs=1e-9, eps_rel=1e-9,
+                           rho_f_factor=1000.0, alpha=1.0)
+    outs = []
+    for flags in (0, _lib.FLAG_GENERIC_KERNEL):
+        solver = _solver(qp, cfg, kernel_flags=flags)
+        st0 = solver.initial_state(qp, rho_bar=0.1)
+        _, stats, out = solver.solve(qp, st0)
+        outs.append((stats, out))
+    torch.cuda.synchronize()
+    (s_a, o_a), (s_b, o_b) = outs
+    assert torch.equal(s_a.num_iter, s_b.num_iter)
+    for k in ("x_blocks", "y_f_dyn", "y_g", "z_g", "y_f_0"):
+        assert rel_err(getattr(o_a, k), getattr(o_b, k)) < TOL[torch.float32], k

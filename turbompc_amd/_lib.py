@@ -24,6 +24,12 @@ _PKG = Path(__file__).resolve().parent
 DEFAULT_LIB = _PKG / "lib" / "libtmpc_hip.so"
 
 FLAG_STD_DYNAMICS = 1
+FLAG_GENERIC_KERNEL = 2
+
+
+def flag_stream_p(p: int) -> int:
+    """Forces the problems per wavefront of the streaming kernel (1-3)."""
+    return (int(p) & 3) << 8
 
 _STATUS = {
     0: "ok",

@@ -242,7 +242,7 @@ __global__ __launch_bounds__(kWave) void admm_chunk_kernel(AdmmArgs<R> a) {
   const Dims d = a.d;
   const int n = NC > 0 ? NC : d.n;
   const int T = d.T, N = d.N, nx = d.nx, n0 = d.n0, m = d.m, B = d.B;
-  const int pk = packed_size(n);
+  const int pk = th_pitch(n);
   const Group G = make_group(a.g, a.P, B);
   const int b = G.prob, i = G.lane, base = G.gid * a.g;
   const R alpha = a.alpha, one_m_alpha = R(1) - a.alpha;
@@ -475,7 +475,7 @@ __global__ __launch_bounds__(kWave) void blktri_solve_kernel(Dims d, int g, int 
                                                              const R* __restrict__ rhs, R* __restrict__ x) {
   __shared__ R sv[3][kWave];
   const int n = NC > 0 ? NC : d.n;
-  const int T = d.T, B = d.B, pk = packed_size(n), w3 = 3 * n;
+  const int T = d.T, B = d.B, pk = th_pitch(n), w3 = 3 * n;
   const Group G = make_group(g, P, B);
   const int b = G.prob, i = G.lane, base = G.gid * g;
   R* sw = sv[0] + base;

@@ -7,6 +7,7 @@
 #include <vector>
 
 #include "admm_direct.hpp"
+#include "admm_stream.hpp"
 #include "common.hpp"
 #include "factor.hpp"
 #include "pcg.hpp"
@@ -40,29 +41,43 @@ Dims to_dims(const tmpc_dims* d) {
   return Dims{d->B, d->T, d->T - 1, d->n, d->nx, d->n0, d->m};
 }
 
+// Stage records of the streaming path (admm_stream.hpp).
+template <typename R>
+size_t stream_ws_bytes(const Dims& d) {
+  const RecGeom g = rec_geom(d);
+  const size_t B = d.B, T = d.T, N = d.N;
+  return align_up(N * B * g.amp * sizeof(R)) + align_up(T * B * g.rvp * sizeof(R)) +
+         align_up(T * B * th_pitch(d.n) * sizeof(R));
+}
+
 template <typename R>
 size_t direct_ws_bytes(const Dims& d) {
   const size_t B = d.B, T = d.T, n = d.n;
-  return align_up(T * B * packed_size(d.n) * sizeof(R)) + 2 * align_up(T * B * n * sizeof(R)) +
-         align_up(B * 4 * sizeof(int32_t)) + align_up(B * 8 * sizeof(R));
+  return align_up(T * B * th_pitch(d.n) * sizeof(R)) + 2 * align_up(T * B * n * sizeof(R)) +
+         align_up(B * 4 * sizeof(int32_t)) + align_up(B * 8 * sizeof(R)) + stream_ws_bytes<R>(d);
 }
 
 template <typename R>
 struct DirectWs {
   R *thinv, *w, *gam, *res;
   int32_t* ctl;
+  R *am, *rv, *dm;  // stage records of the streaming path
 };
 
 template <typename R>
 DirectWs<R> carve_direct(void* ws, const Dims& d) {
   Carver c{static_cast<char*>(ws)};
   DirectWs<R> w;
-  const size_t B = d.B, T = d.T, n = d.n;
-  w.thinv = c.take<R>(T * B * packed_size(d.n));
+  const size_t B = d.B, T = d.T, N = d.N, n = d.n;
+  const RecGeom g = rec_geom(d);
+  w.thinv = c.take<R>(T * B * th_pitch(d.n));
   w.w = c.take<R>(T * B * n);
   w.gam = c.take<R>(T * B * n);
   w.ctl = c.take<int32_t>(B * 4);
   w.res = c.take<R>(B * 8);
+  w.am = c.take<R>(N * B * g.amp);
+  w.rv = c.take<R>(T * B * g.rvp);
+  w.dm = c.take<R>(T * B * th_pitch(d.n));
   return w;
 }
 
@@ -151,6 +166,87 @@ void launch_chunk(hipStream_t s, const AdmmArgs<R>& a) {
   }
 }
 
+// Streaming kernel (explicit-integrator structure, n in {6, 9, 16, 17},
+// nx <= n - 1, m <= min(n, 8)).  P problems per wavefront: as many as keep
+// about two wavefronts per SIMD busy on a 256-CU device, at most 3.
+constexpr int kStreamDepth = 2;
+constexpr size_t kMaxLds = 160 * 1024;
+
+inline int stream_problems_per_wave(int B, uint32_t flags) {
+  const int forced = (int)((flags >> 8) & 3u);
+  return forced ? forced : std::max(1, std::min(3, B / 2048));
+}
+
+template <typename R>
+bool stream_ok(const Dims& d, int P) {
+  if (!(d.n == 6 || d.n == 9 || d.n == 16 || d.n == 17)) return false;
+  if (d.nx > d.n - 1 || d.m > d.n || d.m > kMaxStreamM) return false;
+  const StreamLayout L = stream_layout(d, P, kStreamDepth);
+  return (size_t)L.total * sizeof(R) <= kMaxLds;
+}
+
+template <typename R, int NC, int P>
+void launch_stream_p(hipStream_t s, const StreamArgs<R>& a) {
+  const StreamLayout L = stream_layout(a.d, P, kStreamDepth);
+  const size_t smem = (size_t)L.total * sizeof(R);
+  lds_optin(admm_stream_kernel<R, NC, P, kStreamDepth>, smem);
+  const int grid = (a.d.B + P - 1) / P;
+  hipLaunchKernelGGL((admm_stream_kernel<R, NC, P, kStreamDepth>), dim3(grid), dim3(kWave), smem, s, a);
+}
+
+template <typename R, int NC>
+void launch_stream_nc(hipStream_t s, const StreamArgs<R>& a, int P) {
+  switch (P) {
+    case 1: launch_stream_p<R, NC, 1>(s, a); break;
+    case 2: launch_stream_p<R, NC, 2>(s, a); break;
+    default: launch_stream_p<R, NC, 3>(s, a); break;
+  }
+}
+
+template <typename R>
+void launch_stream(hipStream_t s, const StreamArgs<R>& a, int P) {
+  switch (a.d.n) {
+    case 6: launch_stream_nc<R, 6>(s, a, P); break;
+    case 9: launch_stream_nc<R, 9>(s, a, P); break;
+    case 16: launch_stream_nc<R, 16>(s, a, P); break;
+    default: launch_stream_nc<R, 17>(s, a, P); break;
+  }
+}
+
+template <typename R>
+StreamArgs<R> stream_args(const AdmmArgs<R>& a, const DirectWs<R>& w) {
+  StreamArgs<R> s;
+  s.d = a.d;
+  s.th = w.thinv;
+  s.dm = w.dm;
+  s.am = w.am;
+  s.rv = w.rv;
+  s.A0 = a.qp.A0;
+  s.c0 = a.qp.c0;
+  s.slack_w = a.qp.slack_w;
+  s.y_f0 = a.st.y_f0;
+  s.rho = a.st.rho;
+  s.ctl = a.ctl;
+  s.res = a.res;
+  s.iters_out = a.iters_out;
+  s.sigma = a.sigma;
+  s.alpha = a.alpha;
+  s.rho_f_factor = a.rho_f_factor;
+  s.eps_abs = a.eps_abs;
+  s.eps_rel = a.eps_rel;
+  s.rho_min = a.rho_min;
+  s.rho_max = a.rho_max;
+  s.rho_tol = a.rho_tol;
+  s.max_iter = a.max_iter;
+  s.check_every = a.check_every;
+  s.adapt_every = a.adapt_every;
+  s.use_slack = a.use_slack;
+  s.it_lo = a.it_lo;
+  s.it_hi = a.it_hi;
+  s.first_chunk = a.first_chunk;
+  return s;
+}
+
 // Iterations after which a rho change (and so a refactorization) can happen:
 // it >= 2, it % adapt_every == 0 and it % check_every == 0 (admm.py:504-508).
 std::vector<int> chunk_bounds(int max_iter, int check_every, int adapt_every) {
@@ -203,8 +299,15 @@ int admm_direct_impl(hipStream_t s, const tmpc_dims* dims, const tmpc_qp* qp,
   a.g = std::max(d.n, d.m);
   a.P = kWave / a.g;
   const bool std_dyn = (cfg->flags & TMPC_FLAG_STD_DYNAMICS) != 0;
+  const int sp = stream_problems_per_wave(d.B, cfg->flags);
+  const bool stream = std_dyn && (cfg->flags & TMPC_FLAG_GENERIC_KERNEL) == 0 && stream_ok<R>(d, sp);
   st = launch_factor_qp<R>(s, d, a.qp, a.st.rho, a.sigma, a.rho_f_factor, nullptr, w.thinv);
   if (st) return st;
+  if (stream) {
+    hipLaunchKernelGGL((stage_pack_kernel<R>), dim3(d.B, d.T), dim3(kWave), 0, s, d, a.qp, a.st, w.am, w.rv, w.dm);
+    st = launch_status();
+    if (st) return st;
+  }
   const std::vector<int> bounds = chunk_bounds(cfg->max_iter, cfg->check_every, cfg->adapt_rho_every);
   for (size_t c = 0; c + 1 < bounds.size(); ++c) {
     if (c > 0) {
@@ -214,10 +317,17 @@ int admm_direct_impl(hipStream_t s, const tmpc_dims* dims, const tmpc_qp* qp,
     a.it_lo = bounds[c];
     a.it_hi = bounds[c + 1];
     a.first_chunk = c == 0 ? 1 : 0;
-    if (std_dyn)
+    if (stream)
+      launch_stream<R>(s, stream_args<R>(a, w), sp);
+    else if (std_dyn)
       launch_chunk<R, true>(s, a);
     else
       launch_chunk<R, false>(s, a);
+    st = launch_status();
+    if (st) return st;
+  }
+  if (stream) {
+    hipLaunchKernelGGL((stage_unpack_kernel<R>), dim3(d.B, d.T), dim3(kWave), 0, s, d, (const R*)w.rv, a.st);
     st = launch_status();
     if (st) return st;
   }
@@ -231,7 +341,7 @@ int blktri_factor_impl(hipStream_t s, int B, int T, int n, const R* S, void* ws,
   if (!dims_ok(&td)) return TMPC_EBADSHAPE;
   if (!S) return TMPC_EBADARG;
   const Dims d = to_dims(&td);
-  if (!ws || wsb < align_up((size_t)T * B * packed_size(n) * sizeof(R))) return TMPC_EWORKSPACE;
+  if (!ws || wsb < align_up((size_t)T * B * th_pitch(n) * sizeof(R))) return TMPC_EWORKSPACE;
   QPDev<R> q{};
   const size_t smem = factor_smem_bytes(d);
   lds_optin(factor_kernel<R, SRC_S>, smem);
@@ -254,7 +364,7 @@ int blktri_solve_impl(hipStream_t s, int B, int T, int n, const R* S, const R* r
   if (!dims_ok(&td)) return TMPC_EBADSHAPE;
   if (!S || !rhs || !x) return TMPC_EBADARG;
   const Dims d = to_dims(&td);
-  if (!ws || wsb < align_up((size_t)T * B * packed_size(n) * sizeof(R))) return TMPC_EWORKSPACE;
+  if (!ws || wsb < align_up((size_t)T * B * th_pitch(n) * sizeof(R))) return TMPC_EWORKSPACE;
   const R* th = static_cast<const R*>(ws);
   const int g = n, P = kWave / n;
   switch (n) {
@@ -286,7 +396,7 @@ template <typename R>
 size_t adjoint_ws_bytes(const Dims& d) {
   const KktDims k = kkt_dims(d);
   const size_t B = d.B, T = d.T, nb = k.nb;
-  return align_up(B * T * nb * 3 * nb * sizeof(R)) + align_up(T * B * packed_size(k.nb) * sizeof(R)) +
+  return align_up(B * T * nb * 3 * nb * sizeof(R)) + align_up(T * B * th_pitch(k.nb) * sizeof(R)) +
          5 * align_up(B * T * nb * sizeof(R)) + align_up(B * sizeof(R));
 }
 
@@ -308,7 +418,7 @@ int adjoint_impl(hipStream_t s, const tmpc_dims* dims, const tmpc_qp* qp, R* dz,
   const size_t B = d.B, T = d.T, nb = k.nb, L = B * T * nb;
   Carver c{static_cast<char*>(ws)};
   R* K = c.take<R>(B * T * nb * 3 * nb);
-  R* th = c.take<R>(T * B * packed_size(k.nb));
+  R* th = c.take<R>(T * B * th_pitch(k.nb));
   R* dreg = c.take<R>(L);
   R* rhs = c.take<R>(L);
   R* x = c.take<R>(L);
@@ -575,7 +685,7 @@ int tmpc_admm_direct_f64(hipStream_t s, const tmpc_dims* dims, const tmpc_qp* qp
 size_t tmpc_blktri_workspace_bytes(int elem_bytes, int32_t B, int32_t T, int32_t n) {
   tmpc_dims td{B, T, n, 1, 1, 0};
   if (!dims_ok(&td)) return 0;
-  return align_up((size_t)T * B * packed_size(n) * (elem_bytes == 8 ? 8 : 4));
+  return align_up((size_t)T * B * th_pitch(n) * (elem_bytes == 8 ? 8 : 4));
 }
 int tmpc_blktri_factor_f32(hipStream_t s, int32_t B, int32_t T, int32_t n, const float* S, void* ws,
                            size_t wsb) {

@@ -33,7 +33,11 @@ struct StateDev {
 __device__ __forceinline__ int pidx(int i, int k) {
   return i >= k ? ((i * (i + 1)) >> 1) + k : ((k * (k + 1)) >> 1) + i;
 }
-__host__ __device__ __forceinline__ int packed_size(int n) { return (n * (n + 1)) / 2; }
+__host__ __device__ __forceinline__ constexpr int packed_size(int n) { return (n * (n + 1)) / 2; }
+// Stored pitch of one packed Theta^{-1} block: padded to a multiple of four
+// elements so that every block starts on a 16-byte boundary and the blocks of
+// consecutive problems load as one run of 128-bit accesses.
+__host__ __device__ __forceinline__ constexpr int th_pitch(int n) { return (packed_size(n) + 3) & ~3; }
 
 // `it % k == 0` with XLA's integer remainder convention (x % 0 == x), which is
 // what the reference's jnp expressions evaluate to when k == 0.

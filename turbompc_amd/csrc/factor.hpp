@@ -78,7 +78,7 @@ __global__ __launch_bounds__(kWave) void factor_kernel(Dims d, QPDev<R> qp,
   if (ctl != nullptr && ctl[b * 4 + 2] == 0) return;  // refactor only when flagged
   const int tid = threadIdx.x;
   const int T = d.T, N = d.N, n = d.n, nx = d.nx, n0 = d.n0, m = d.m;
-  const int nn = n * n, pk = packed_size(n);
+  const int nn = n * n, pk = th_pitch(n);
   extern __shared__ unsigned char smem_raw[];
   Cmp* sm = reinterpret_cast<Cmp*>(smem_raw);
   Cmp* A = sm;              // Theta_t, inverted in place

@@ -93,6 +93,7 @@ class ADMMSolver:
         admm_backend: AdmmBackend = AdmmBackend.HIP_DIRECT,
         use_slack: bool = False,
         std_dynamics: Optional[bool] = None,
+        kernel_flags: int = 0,
     ):
         admm_backend = AdmmBackend(admm_backend)
         if admm_backend not in (AdmmBackend.HIP_DIRECT, AdmmBackend.HIP_PCG):
@@ -115,6 +116,7 @@ class ADMMSolver:
         self._use_slack = bool(use_slack)
         self._zshape = zshape
         self._std_dynamics = std_dynamics
+        self._kernel_flags = int(kernel_flags)  # _lib.FLAG_GENERIC_KERNEL / flag_stream_p (cross-checks)
 
     # properties of the reference solver
     schur_solver = property(lambda self: self._schur_solver)
@@ -162,7 +164,7 @@ class ADMMSolver:
             raise ValueError("ADMMSolver (HIP backends) needs device tensors; there is no CPU path")
         state0 = self.initial_state(qp_data, rho_bar=rho_bar) if admm_state0 is None else admm_state0
         std = self._std_dynamics if self._std_dynamics is not None else is_std_dynamics(qp_data)
-        cfg = self._cfg(alpha, _lib.FLAG_STD_DYNAMICS if std else 0)
+        cfg = self._cfg(alpha, (_lib.FLAG_STD_DYNAMICS if std else 0) | self._kernel_flags)
         sw = slack_weight if self._use_slack else None
         outs, iters, pcg_iters = hip.admm_hip_solve(
             qp_data,
