@@ -685,4 +685,156 @@ __global__ __launch_bounds__(kWave, StreamOcc<R>::waves) void admm_stream_kernel
   }
 }
 
+// ---- factorization of S for the explicit-integrator structure ---------------
+//
+// factor_kernel's recursion (factor.hpp) specialised to A_plus_t = [-I 0],
+// E_t = 0, where phi_{t-1} = -rho_f [A_minus_{t-1}; 0]:
+//   theta_t = D_t + sigma I + rho G_t^T G_t
+//             + rho_f (A_minus_t^T A_minus_t [t < N] + diag(I_nx, 0) [t > 0] + A0^T A0 [t = 0])
+//   Theta_t = theta_t - rho_f^2 [A_minus_{t-1} Theta_{t-1}^{-1} A_minus_{t-1}^T, 0; 0, 0]
+// so the Schur update touches the leading nx x nx block only.  fp64 throughout.
+//
+// A wavefront holds P problems; lane i of a group keeps row i of Theta_t in
+// registers and the rows it needs from the other lanes come through LDS:
+// A_minus blocks (double-buffered across stages), Theta_{t-1}^{-1} (full), the
+// Gauss-Jordan pivot row.  Reads the stage records of stage_pack_kernel.
+
+__host__ __device__ inline int factor_std_per(const Dims& d) {
+  const int n = d.n;
+  return 2 * d.nx * n + n * n + n + d.m * n + th_pitch(n) + d.n0 * n;
+}
+
+template <typename R, int NC, int P>
+__global__ __launch_bounds__(kWave) void factor_std_kernel(Dims d, const R* __restrict__ am, const R* __restrict__ rv,
+                                                          const R* __restrict__ dm, const R* __restrict__ A0,
+                                                          const R* __restrict__ rho, R sigma, R rho_f_factor,
+                                                          int32_t* __restrict__ ctl, R* __restrict__ thinv) {
+  using C = double;
+  constexpr int n = NC, PITCH = th_pitch(NC);
+  extern __shared__ __align__(16) unsigned char smem_raw[];
+  C* lds = reinterpret_cast<C*>(smem_raw);
+  const int T = d.T, N = d.N, nx = d.nx, n0 = d.n0, m = d.m, B = d.B;
+  const RecGeom rg = rec_geom(d);
+  const Group G = make_group(n, P, B);
+  const int b = G.prob, i = G.lane, p = G.gid, tid = threadIdx.x;
+  const int b0 = blockIdx.x * P, nprob = min(P, B - b0);
+  if (ctl != nullptr && __ballot(G.real && ctl[b * 4 + 2] != 0) == 0) return;  // nothing flagged here
+  const int nxn = nx * n, mn = m * n, n0n = n0 * n;
+  const int per = factor_std_per(d);
+  const int o_th = 2 * nxn, o_piv = o_th + n * n, o_gm = o_piv + n, o_dm = o_gm + mn, o_a0 = o_dm + PITCH;
+  C* mine = lds + p * per;
+  C* th = mine + o_th;
+  C* piv = mine + o_piv;
+  const C* gm = mine + o_gm;
+  const C* dmt = mine + o_dm;
+  const C* a0 = mine + o_a0;
+  // copies `cnt` elements of each problem's block (block pp at src + pp * stride) to LDS offset `off`
+  auto fetch = [&](const R* src, int stride, int cnt, int off) {
+    for (int pp = 0; pp < nprob; ++pp)
+      for (int e = tid; e < cnt; e += kWave) lds[pp * per + off + e] = (C)src[(size_t)pp * stride + e];
+  };
+  fetch(A0 + (size_t)b0 * n0n, n0n, n0n, o_a0);
+  const C rho_i = (C)rho[b];
+  const C rho_f = rho_i * (C)rho_f_factor;
+  const C sig = (C)sigma;
+
+  C a[NC];  // row i of Theta_t, then of Theta_t^{-1}
+  for (int t = 0; t < T; ++t) {
+    const int cur = (t & 1) * nxn, prv = ((t & 1) ^ 1) * nxn;
+    if (t < N) fetch(am + ((size_t)t * B + b0) * rg.amp, rg.amp, nxn, cur);
+    if (m) fetch(rv + ((size_t)t * B + b0) * rg.rvp + rg.g, rg.rvp, mn, o_gm);
+    fetch(dm + ((size_t)t * B + b0) * PITCH, PITCH, packed_size(n), o_dm);
+    wsync();
+    const C* amc = mine + cur;
+    const C* amq = mine + prv;
+    if (i < n) {
+      // theta_t row i
+      C c[NC], g[NC];
+#pragma unroll
+      for (int k = 0; k < NC; ++k) {
+        a[k] = dmt[pidx(i, k)] + (k == i ? sig : C(0));
+        c[k] = C(0);
+        g[k] = C(0);
+      }
+      if (t == 0)
+        for (int r = 0; r < n0; ++r) {
+          const C ar = a0[r * n + i];
+#pragma unroll
+          for (int k = 0; k < NC; ++k) c[k] += ar * a0[r * n + k];
+        }
+      if (t < N)
+        for (int r = 0; r < nx; ++r) {
+          const C ar = amc[r * n + i];
+#pragma unroll
+          for (int k = 0; k < NC; ++k) c[k] += ar * amc[r * n + k];
+        }
+      for (int r = 0; r < m; ++r) {
+        const C gr = gm[r * n + i];
+#pragma unroll
+        for (int k = 0; k < NC; ++k) g[k] += gr * gm[r * n + k];
+      }
+#pragma unroll
+      for (int k = 0; k < NC; ++k) {
+        if (t > 0 && k == i && i < nx) c[k] += C(1);  // A_plus_{t-1}^T A_plus_{t-1} = diag(I_nx, 0)
+        a[k] += rho_i * g[k] + rho_f * c[k];
+      }
+      // Schur update of the leading nx x nx block
+      if (t > 0 && i < nx) {
+        C mr[NC];
+#pragma unroll
+        for (int j = 0; j < NC; ++j) mr[j] = C(0);
+#pragma unroll
+        for (int k = 0; k < NC; ++k) {
+          const C ak = amq[i * n + k];
+#pragma unroll
+          for (int j = 0; j < NC; ++j) mr[j] += ak * th[k * n + j];
+        }
+        const C f2 = rho_f * rho_f;
+#pragma unroll
+        for (int s = 0; s < NC; ++s) {
+          if (s < nx) {
+            C sv = C(0);
+#pragma unroll
+            for (int k = 0; k < NC; ++k) sv += mr[k] * amq[s * n + k];
+            a[s] -= f2 * sv;
+          }
+        }
+      }
+    }
+    // Gauss-Jordan inversion without pivoting, rows in lanes
+#pragma unroll
+    for (int k = 0; k < NC; ++k) {
+      wsync();
+      if (i == k)
+#pragma unroll
+        for (int j = 0; j < NC; ++j) piv[j] = a[j];
+      wsync();
+      if (i < n) {
+        const C ip = C(1) / piv[k];
+        if (i == k) {
+#pragma unroll
+          for (int j = 0; j < NC; ++j) a[j] = (j == k) ? ip : a[j] * ip;
+        } else {
+          const C f = a[k];
+#pragma unroll
+          for (int j = 0; j < NC; ++j) a[j] = (j == k) ? -f * ip : a[j] - f * piv[j] * ip;
+        }
+      }
+    }
+    wsync();
+    if (i < n) {
+#pragma unroll
+      for (int j = 0; j < NC; ++j) th[i * n + j] = a[j];
+      if (G.live) {
+        R* out = thinv + ((size_t)t * B + b) * PITCH + ((i * (i + 1)) >> 1);
+#pragma unroll
+        for (int k = 0; k < NC; ++k)
+          if (k <= i) out[k] = (R)a[k];
+      }
+    }
+    wsync();
+  }
+  if (ctl != nullptr && G.live && i == 0) ctl[b * 4 + 2] = 0;
+}
+
 }  // namespace tmpc

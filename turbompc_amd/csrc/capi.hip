@@ -213,6 +213,39 @@ void launch_stream(hipStream_t s, const StreamArgs<R>& a, int P) {
   }
 }
 
+template <typename R, int NC, int P>
+void launch_factor_std_p(hipStream_t s, const Dims& d, const DirectWs<R>& w, const QPDev<R>& q, const R* rho,
+                         R sigma, R rho_f_factor, int32_t* ctl) {
+  const size_t smem = (size_t)P * factor_std_per(d) * sizeof(double);
+  lds_optin(factor_std_kernel<R, NC, P>, smem);
+  const int grid = (d.B + P - 1) / P;
+  hipLaunchKernelGGL((factor_std_kernel<R, NC, P>), dim3(grid), dim3(kWave), smem, s, d, (const R*)w.am,
+                     (const R*)w.rv, (const R*)w.dm, q.A0, rho, sigma, rho_f_factor, ctl, w.thinv);
+}
+
+template <typename R, int NC>
+void launch_factor_std_nc(hipStream_t s, const Dims& d, const DirectWs<R>& w, const QPDev<R>& q, const R* rho,
+                          R sigma, R rho_f_factor, int32_t* ctl, int P) {
+  switch (P) {
+    case 1: launch_factor_std_p<R, NC, 1>(s, d, w, q, rho, sigma, rho_f_factor, ctl); break;
+    case 2: launch_factor_std_p<R, NC, 2>(s, d, w, q, rho, sigma, rho_f_factor, ctl); break;
+    default: launch_factor_std_p<R, NC, 3>(s, d, w, q, rho, sigma, rho_f_factor, ctl); break;
+  }
+}
+
+// fp64 factorization from the stage records (explicit-integrator structure)
+template <typename R>
+int launch_factor_std(hipStream_t s, const Dims& d, const DirectWs<R>& w, const QPDev<R>& q, const R* rho,
+                      R sigma, R rho_f_factor, int32_t* ctl, int P) {
+  switch (d.n) {
+    case 6: launch_factor_std_nc<R, 6>(s, d, w, q, rho, sigma, rho_f_factor, ctl, P); break;
+    case 9: launch_factor_std_nc<R, 9>(s, d, w, q, rho, sigma, rho_f_factor, ctl, P); break;
+    case 16: launch_factor_std_nc<R, 16>(s, d, w, q, rho, sigma, rho_f_factor, ctl, P); break;
+    default: launch_factor_std_nc<R, 17>(s, d, w, q, rho, sigma, rho_f_factor, ctl, P); break;
+  }
+  return launch_status();
+}
+
 template <typename R>
 StreamArgs<R> stream_args(const AdmmArgs<R>& a, const DirectWs<R>& w) {
   StreamArgs<R> s;
@@ -301,17 +334,20 @@ int admm_direct_impl(hipStream_t s, const tmpc_dims* dims, const tmpc_qp* qp,
   const bool std_dyn = (cfg->flags & TMPC_FLAG_STD_DYNAMICS) != 0;
   const int sp = stream_problems_per_wave(d.B, cfg->flags);
   const bool stream = std_dyn && (cfg->flags & TMPC_FLAG_GENERIC_KERNEL) == 0 && stream_ok<R>(d, sp);
-  st = launch_factor_qp<R>(s, d, a.qp, a.st.rho, a.sigma, a.rho_f_factor, nullptr, w.thinv);
-  if (st) return st;
   if (stream) {
     hipLaunchKernelGGL((stage_pack_kernel<R>), dim3(d.B, d.T), dim3(kWave), 0, s, d, a.qp, a.st, w.am, w.rv, w.dm);
     st = launch_status();
     if (st) return st;
+    st = launch_factor_std<R>(s, d, w, a.qp, a.st.rho, a.sigma, a.rho_f_factor, nullptr, sp);
+  } else {
+    st = launch_factor_qp<R>(s, d, a.qp, a.st.rho, a.sigma, a.rho_f_factor, nullptr, w.thinv);
   }
+  if (st) return st;
   const std::vector<int> bounds = chunk_bounds(cfg->max_iter, cfg->check_every, cfg->adapt_rho_every);
   for (size_t c = 0; c + 1 < bounds.size(); ++c) {
     if (c > 0) {
-      st = launch_factor_qp<R>(s, d, a.qp, a.st.rho, a.sigma, a.rho_f_factor, w.ctl, w.thinv);
+      st = stream ? launch_factor_std<R>(s, d, w, a.qp, a.st.rho, a.sigma, a.rho_f_factor, w.ctl, sp)
+                  : launch_factor_qp<R>(s, d, a.qp, a.st.rho, a.sigma, a.rho_f_factor, w.ctl, w.thinv);
       if (st) return st;
     }
     a.it_lo = bounds[c];

@@ -199,7 +199,7 @@ class ADMMSolver:
         if m == 0:
             z0 = torch.zeros((B, T, 0), dtype=dt, device=dev)
         else:
-            gx = torch.matmul(qp_data.ineq.G, x0.unsqueeze(-1)).squeeze(-1)
+            gx = (qp_data.ineq.G * x0.unsqueeze(-2)).sum(-1)
             z0 = torch.minimum(torch.maximum(gx, qp_data.ineq.l), qp_data.ineq.u)
         return ADMMState(
             x_blocks=x0,

@@ -13,12 +13,15 @@ import torch
 from .qp_data import QPData
 
 
+# Block products as broadcast-multiply-reduce: the blocks are tiny (at most
+# 64 x 64) and batched over B x T, which a batched GEMM library call handles
+# far worse than one elementwise pass over the blocks.
 def _mv(A: torch.Tensor, x: torch.Tensor) -> torch.Tensor:
-    return torch.matmul(A, x.unsqueeze(-1)).squeeze(-1)
+    return (A * x.unsqueeze(-2)).sum(-1)
 
 
 def _mtv(A: torch.Tensor, y: torch.Tensor) -> torch.Tensor:
-    return torch.matmul(y.unsqueeze(-2), A).squeeze(-2)
+    return (A * y.unsqueeze(-1)).sum(-2)
 
 
 def apply_P(qp: QPData, x: torch.Tensor) -> torch.Tensor:
