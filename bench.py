@@ -6,10 +6,11 @@ linearization + ADMM (block-tridiagonal factorization + 20 fused iterations)
 + the first-order convergence check, from the same initial guess every step.
 Inputs are resident on the GPU before timing starts.
 
-Prints one JSON line with the metric, a roofline entry for the ADMM solve
-(factor_kernel + admm_chunk_kernel, timed live with HIP events on the solve
-stream) and the CPU baseline (the liboracle restatement of the reference CPU
-path on a bounded sample of the same workload).
+Prints one JSON line with the metric, a roofline entry for the dominant kernel
+(admm_stream_kernel: 20 ADMM iterations of the batch per launch, timed live
+with HIP events the library records around it on the solve stream; the whole QP
+solve is reported beside it) and the CPU baseline (the liboracle restatement of
+the reference CPU path on a bounded sample of the same workload).
 """
 from __future__ import annotations
 
@@ -90,6 +91,21 @@ def cpu_baseline(B_gpu, n_sqp, admm_iters, seed, budget_s):
     }
 
 
+TRAFFIC_FILE = ROOT / "profiles" / "admm_stream_kernel_config3_pmc.txt"
+
+
+def measured_traffic():
+    """HBM bytes per launch of the iteration kernel from the committed
+    rocprofv3 --pmc summary (FETCH_SIZE + WRITE_SIZE, copy-calibrated), or None."""
+    try:
+        for line in TRAFFIC_FILE.read_text().splitlines():
+            if line.startswith("traffic_bytes_per_launch"):
+                return float(line.split("=")[1])
+    except (OSError, ValueError, IndexError):
+        pass
+    return None
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -101,6 +117,8 @@ def main():
     ap.add_argument("--admm-iters", type=int, default=20)
     ap.add_argument("--cpu-baseline", type=int, default=1)
     ap.add_argument("--cpu-budget", type=float, default=15.0, help="seconds of CPU work for the baseline sample")
+    ap.add_argument("--copy-calibration", type=int, default=0,
+                    help="after timing, copy this many MiB device-to-device (counter calibration under rocprofv3)")
     args = ap.parse_args()
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
@@ -110,6 +128,7 @@ def main():
 
     import torch
 
+    from turbompc_amd import _lib
     from turbompc_amd.problems.quadrotor import make_quadrotor_config
     from turbompc_amd.solvers.admm import admm as admm_mod
 
@@ -120,38 +139,53 @@ def main():
     solver = make_solver(prob, args.sqp, args.admm_iters)
     guess = solver.initial_guess()
 
-    # time every ADMM solve (factor_kernel + admm_chunk_kernel) with events on
-    # the stream the library launches on
-    events = []
+    # every ADMM solve is timed twice with HIP events on the stream the library
+    # launches on: the whole QP solve (pack + factorization + iterations +
+    # unpack) and, through the library's hook, the iteration phase alone (the
+    # single admm_stream_kernel launch of a fixed-iteration solve)
+    solve_events = []
+    iter_timer = _lib.IterationTimer()
     orig = admm_mod.ADMMSolver.solve
 
     def timed_solve(self, *a, **kw):
         s = torch.cuda.current_stream(dev)
         e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
         e0.record(s)
-        out = orig(self, *a, **kw)
+        with iter_timer:
+            out = orig(self, *a, **kw)
         e1.record(s)
-        events.append((e0, e1))
+        solve_events.append((e0, e1))
         return out
 
     admm_mod.ADMMSolver.solve = timed_solve
     for _ in range(args.warmup):
         solver.solve(guess)
     torch.cuda.synchronize()
-    events.clear()
+    solve_events.clear()
+    iter_timer.clear()
     t0 = time.perf_counter()
     for _ in range(args.steps):
         sol = solver.solve(guess)
     torch.cuda.synchronize()
     elapsed = time.perf_counter() - t0
     admm_mod.ADMMSolver.solve = orig
-    admm_ms = [a.elapsed_time(b) for a, b in events]
-    admm_avg_s = sum(admm_ms) / len(admm_ms) / 1e3
+    solve_ms = [a.elapsed_time(b) for a, b in solve_events]
+    iter_ms = iter_timer.results()
+    solve_avg_s = sum(solve_ms) / len(solve_ms) / 1e3
+    iter_avg_s = sum(iter_ms) / len(iter_ms) / 1e3
+    if args.copy_calibration:
+        x = torch.ones(args.copy_calibration * (1 << 18), dtype=torch.float32, device=dev)
+        y = torch.empty_like(x)
+        y.copy_(x)
+        torch.cuda.synchronize()
 
     T, n, nx, n0, m = prob.horizon + 1, 17, 13, 13, 4
     per_qp, F, It = bytes_per_qp(T, n, nx, n0, m, args.admm_iters, 4)
-    achieved = per_qp * B / admm_avg_s / 1e9
+    iter_bytes = B * args.admm_iters * It  # algorithmic bytes of one iteration-kernel launch
+    achieved = iter_bytes / iter_avg_s / 1e9
+    qp_achieved = per_qp * B / solve_avg_s / 1e9
     finite = bool(torch.isfinite(sol.states).all() and torch.isfinite(sol.controls).all())
+    traffic = measured_traffic()
 
     value = B * args.steps / elapsed
     line = {
@@ -176,6 +210,7 @@ def main():
             "admm_iterations": args.admm_iters,
             "parallelism": "single GPU, batch-parallel",
             "solution_finite": finite,
+            "kernel_only_solves_per_s": B / (args.sqp * solve_avg_s),
         },
         "roofline": {
             "bound": "hbm",
@@ -183,10 +218,17 @@ def main():
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
             "frac": achieved / HBM_PEAK_GBS,
-            "traffic": None,
-            "kernel": "ADMM solve = factor_kernel + admm_chunk_kernel (per SQP iteration)",
-            "bytes_per_qp": per_qp,
-            "avg_solve_ms": admm_avg_s * 1e3,
+            "traffic": traffic,
+            "kernel": "admm_stream_kernel (one launch = 20 ADMM iterations of the batch)",
+            "algorithmic_bytes_per_launch": iter_bytes,
+            "avg_launch_ms": iter_avg_s * 1e3,
+            "qp_solve": {
+                "kernels": "stage_pack + factor_std + admm_stream + stage_unpack",
+                "algorithmic_bytes": per_qp * B,
+                "avg_ms": solve_avg_s * 1e3,
+                "achieved": qp_achieved,
+                "frac": qp_achieved / HBM_PEAK_GBS,
+            },
         },
     }
     if args.cpu_baseline:

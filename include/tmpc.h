@@ -71,6 +71,15 @@ typedef struct tmpc_admm_cfg {
 const char* tmpc_status_string(int status);
 int tmpc_version(void);
 
+/* Measurement hook (no counterpart in the reference): while set, every
+ * tmpc_admm_direct_* call records `before` on its stream right before its
+ * ADMM-iteration phase (the iteration kernels and any refactorizations
+ * between chunks) and `after` right after it, so the caller can time that
+ * phase alone with hipEventElapsedTime.  NULL, NULL switches it off.  The
+ * setting is process-wide and not synchronised: set it from the thread that
+ * launches the solves. */
+void tmpc_set_timing_events(hipEvent_t before, hipEvent_t after);
+
 /* ---- ADMM with the exact block-tridiagonal Schur solve ---------------------
  * Replaces the `admm_cudss_cuda[_f64]` FFI target: AdmmCudssCudaImpl
  * (turbompc/solvers/admm/csrc/admm_cudss_ffi.cc:13-140) / launchADMMCudss

@@ -92,6 +92,7 @@ _VP, _I32, _U32, _F64, _SZ = ctypes.c_void_p, ctypes.c_int32, ctypes.c_uint32, c
 _PD, _PQ, _PS, _PC = (ctypes.POINTER(t) for t in (Dims, QP, State, AdmmCfg))
 SIGNATURES = {
     "tmpc_version": [],
+    "tmpc_set_timing_events": [_VP, _VP],
     "tmpc_status_string": [ctypes.c_int],
     "tmpc_admm_direct_workspace_bytes": [ctypes.c_int, _PD],
     "tmpc_admm_direct_f32": [_VP, _PD, _PQ, _PS, _PS, _VP, _PC, _VP, _SZ],
@@ -152,6 +153,8 @@ def load() -> ctypes.CDLL:
             fn.restype = ctypes.c_size_t
         elif name == "tmpc_status_string":
             fn.restype = ctypes.c_char_p
+        elif name == "tmpc_set_timing_events":
+            fn.restype = None
         else:
             fn.restype = ctypes.c_int
     _LIB = lib
@@ -185,3 +188,34 @@ def suffix(dtype: torch.dtype) -> str:
 
 def workspace(nbytes: int, device: torch.device) -> torch.Tensor:
     return torch.empty(max(int(nbytes), 1), dtype=torch.uint8, device=device)
+
+
+class IterationTimer:
+    """Times the ADMM-iteration phase of tmpc_admm_direct_* calls with HIP
+    events recorded by the library (tmpc_set_timing_events).  Use as a context
+    manager around each solve; read the millisecond durations with results()
+    after synchronising the device."""
+
+    def __init__(self):
+        self._pairs = []
+        self._lib = load()
+
+    def __enter__(self):
+        import torch
+
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()  # materialise the underlying HIP events
+        e1.record()
+        self._lib.tmpc_set_timing_events(ctypes.c_void_p(e0.cuda_event), ctypes.c_void_p(e1.cuda_event))
+        self._pairs.append((e0, e1))
+        return self
+
+    def __exit__(self, *exc):
+        self._lib.tmpc_set_timing_events(None, None)
+        return False
+
+    def clear(self):
+        self._pairs.clear()
+
+    def results(self):
+        return [a.elapsed_time(b) for a, b in self._pairs]

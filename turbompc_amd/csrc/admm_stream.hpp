@@ -309,8 +309,8 @@ __global__ __launch_bounds__(kWave, StreamOcc<R>::waves) void admm_stream_kernel
   const RecGeom rg = rec_geom(d);
   const int amp = rg.amp, rvp = rg.rvp;
   const StreamLayout L = stream_layout(d, P, DPF);
-  const Group G = make_group(n, P, B);
-  const int b = G.prob, i = G.lane, p = G.gid, base = p * n, tid = threadIdx.x;
+  const Group G = make_group_strided(n, P, B);
+  const int b = G.prob, i = G.lane, p = G.gid, base = p * (kWave / P), tid = threadIdx.x;
   const int b0 = blockIdx.x * P;
   const int nprob = min(P, B - b0);
   const int nch_th = nprob * PITCH / W, nch_am = nprob * amp / W, nch_rv = nprob * rvp / W;
@@ -715,7 +715,7 @@ __global__ __launch_bounds__(kWave) void factor_std_kernel(Dims d, const R* __re
   C* lds = reinterpret_cast<C*>(smem_raw);
   const int T = d.T, N = d.N, nx = d.nx, n0 = d.n0, m = d.m, B = d.B;
   const RecGeom rg = rec_geom(d);
-  const Group G = make_group(n, P, B);
+  const Group G = make_group_strided(n, P, B);
   const int b = G.prob, i = G.lane, p = G.gid, tid = threadIdx.x;
   const int b0 = blockIdx.x * P, nprob = min(P, B - b0);
   if (ctl != nullptr && __ballot(G.real && ctl[b * 4 + 2] != 0) == 0) return;  // nothing flagged here

@@ -19,6 +19,9 @@ namespace tmpc {
 namespace {
 
 constexpr size_t kAlign = 256;
+
+// events of tmpc_set_timing_events (process-wide)
+hipEvent_t g_iter_events[2] = {nullptr, nullptr};
 inline size_t align_up(size_t x) { return (x + kAlign - 1) / kAlign * kAlign; }
 
 struct Carver {
@@ -344,6 +347,7 @@ int admm_direct_impl(hipStream_t s, const tmpc_dims* dims, const tmpc_qp* qp,
   }
   if (st) return st;
   const std::vector<int> bounds = chunk_bounds(cfg->max_iter, cfg->check_every, cfg->adapt_rho_every);
+  if (g_iter_events[0] && hipEventRecord(g_iter_events[0], s) != hipSuccess) return TMPC_ELAUNCH;
   for (size_t c = 0; c + 1 < bounds.size(); ++c) {
     if (c > 0) {
       st = stream ? launch_factor_std<R>(s, d, w, a.qp, a.st.rho, a.sigma, a.rho_f_factor, w.ctl, sp)
@@ -362,6 +366,7 @@ int admm_direct_impl(hipStream_t s, const tmpc_dims* dims, const tmpc_qp* qp,
     st = launch_status();
     if (st) return st;
   }
+  if (g_iter_events[1] && hipEventRecord(g_iter_events[1], s) != hipSuccess) return TMPC_ELAUNCH;
   if (stream) {
     hipLaunchKernelGGL((stage_unpack_kernel<R>), dim3(d.B, d.T), dim3(kWave), 0, s, d, (const R*)w.rv, a.st);
     st = launch_status();
@@ -700,6 +705,11 @@ const char* tmpc_status_string(int status) {
 }
 
 int tmpc_version(void) { return 100; }
+
+void tmpc_set_timing_events(hipEvent_t before, hipEvent_t after) {
+  g_iter_events[0] = before;
+  g_iter_events[1] = after;
+}
 
 size_t tmpc_admm_direct_workspace_bytes(int elem_bytes, const tmpc_dims* dims) {
   if (!dims_ok(dims)) return 0;

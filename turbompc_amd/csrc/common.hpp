@@ -98,4 +98,20 @@ __device__ __forceinline__ Group make_group(int g, int P, int B) {
   return G;
 }
 
+// Groups at lane offsets 0, S, 2S, ... with S = 64 / P.  For P = 2 each group
+// sits in its own half-wave, so the LDS accesses of different groups never
+// share an LDS pass and cannot conflict on a bank.  Every lane belongs to a
+// group; lanes at offset >= g inside a group are idle (lane >= g).
+__device__ __forceinline__ Group make_group_strided(int g, int P, int B) {
+  Group G;
+  const int tid = threadIdx.x, S = kWave / P;
+  G.gid = min(tid / S, P - 1);
+  G.lane = tid - G.gid * S;
+  const int raw = blockIdx.x * P + G.gid;
+  G.prob = raw < B ? raw : B - 1;
+  G.live = G.lane < g && raw < B;
+  G.real = raw < B;
+  return G;
+}
+
 }  // namespace tmpc
