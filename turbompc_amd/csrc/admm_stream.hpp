@@ -699,9 +699,32 @@ __global__ __launch_bounds__(kWave, StreamOcc<R>::waves) void admm_stream_kernel
 // A_minus blocks (double-buffered across stages), Theta_{t-1}^{-1} (full), the
 // Gauss-Jordan pivot row.  Reads the stage records of stage_pack_kernel.
 
-__host__ __device__ inline int factor_std_per(const Dims& d) {
+// LDS of factor_std_kernel, in bytes: fp64 work area [P][n n] Theta_{t-1}^{-1}
+// and [P][n] pivot row, then the staged stage runs in the storage type R:
+// A_minus double-buffered [2][P][amp], the rv records [P][rvp] (G at offset
+// 0), D_t [P][pitch], A0 [P][n0 n].
+struct FactorLayout {
+  int th, piv;          // fp64 offsets (elements)
+  int am, rv, dm, a0;   // R offsets (elements, from the start of the R region)
+  size_t r_base;        // byte offset of the R region
+  size_t bytes;
+};
+
+template <typename R>
+__host__ __device__ inline FactorLayout factor_layout(const Dims& d, int P) {
+  const RecGeom g = rec_geom(d);
+  FactorLayout L;
   const int n = d.n;
-  return 2 * d.nx * n + n * n + n + d.m * n + th_pitch(n) + d.n0 * n;
+  L.th = 0;
+  L.piv = P * n * n;
+  const int c_elems = L.piv + P * n;
+  L.r_base = ((size_t)c_elems * sizeof(double) + 15) / 16 * 16;
+  L.am = 0;
+  L.rv = 2 * P * g.amp;
+  L.dm = L.rv + P * g.rvp;
+  L.a0 = L.dm + P * th_pitch(n);
+  L.bytes = L.r_base + (size_t)(L.a0 + P * d.n0 * n) * sizeof(R);
+  return L;
 }
 
 template <typename R, int NC, int P>
@@ -710,43 +733,57 @@ __global__ __launch_bounds__(kWave) void factor_std_kernel(Dims d, const R* __re
                                                           const R* __restrict__ rho, R sigma, R rho_f_factor,
                                                           int32_t* __restrict__ ctl, R* __restrict__ thinv) {
   using C = double;
-  constexpr int n = NC, PITCH = th_pitch(NC);
+  using V = typename Vec16<R>::T;
+  using K = StreamShape<R, NC, P>;
+  constexpr int n = NC, PITCH = K::PITCH, W = K::W;
+  constexpr int CH_TH = K::CH_TH, CH_AM = K::CH_AM, CH_RV = K::CH_RV;
   extern __shared__ __align__(16) unsigned char smem_raw[];
+  const Dims dd = d;
+  const int T = dd.T, N = dd.N, nx = dd.nx, n0 = dd.n0, m = dd.m, B = dd.B;
+  const RecGeom rg = rec_geom(dd);
+  const FactorLayout FL = factor_layout<R>(dd, P);
   C* lds = reinterpret_cast<C*>(smem_raw);
-  const int T = d.T, N = d.N, nx = d.nx, n0 = d.n0, m = d.m, B = d.B;
-  const RecGeom rg = rec_geom(d);
+  R* ldr = reinterpret_cast<R*>(smem_raw + FL.r_base);
   const Group G = make_group_strided(n, P, B);
   const int b = G.prob, i = G.lane, p = G.gid, tid = threadIdx.x;
   const int b0 = blockIdx.x * P, nprob = min(P, B - b0);
   if (ctl != nullptr && __ballot(G.real && ctl[b * 4 + 2] != 0) == 0) return;  // nothing flagged here
-  const int nxn = nx * n, mn = m * n, n0n = n0 * n;
-  const int per = factor_std_per(d);
-  const int o_th = 2 * nxn, o_piv = o_th + n * n, o_gm = o_piv + n, o_dm = o_gm + mn, o_a0 = o_dm + PITCH;
-  C* mine = lds + p * per;
-  C* th = mine + o_th;
-  C* piv = mine + o_piv;
-  const C* gm = mine + o_gm;
-  const C* dmt = mine + o_dm;
-  const C* a0 = mine + o_a0;
-  // copies `cnt` elements of each problem's block (block pp at src + pp * stride) to LDS offset `off`
-  auto fetch = [&](const R* src, int stride, int cnt, int off) {
-    for (int pp = 0; pp < nprob; ++pp)
-      for (int e = tid; e < cnt; e += kWave) lds[pp * per + off + e] = (C)src[(size_t)pp * stride + e];
+  const int n0n = n0 * n;
+  const int nch_am = nprob * rg.amp / W, nch_rv = nprob * rg.rvp / W, nch_dm = nprob * PITCH / W;
+  C* th = lds + FL.th + p * n * n;
+  C* piv = lds + FL.piv + p * n;
+  const R* gm = ldr + FL.rv + p * rg.rvp + rg.g;
+  const R* dmt = ldr + FL.dm + p * PITCH;
+  const R* a0 = ldr + FL.a0 + p * n0n;
+  for (int e = tid; e < nprob * n0n; e += kWave) ldr[FL.a0 + e] = A0[(size_t)b0 * n0n + e];
+  // stage runs of the next stage are loaded into registers while the current
+  // stage computes (as in admm_stream_kernel)
+  auto run = [&](const R* arr, int pitch, int t) {
+    return reinterpret_cast<const V*>(arr + ((size_t)t * B + b0) * pitch);
   };
-  fetch(A0 + (size_t)b0 * n0n, n0n, n0n, o_a0);
+  struct Regs {
+    V am[CH_AM], rv[CH_RV], dm[CH_TH];
+  } nxt;
+  auto load = [&](int t) {
+    if (t < N) load_run<V, CH_AM>(nxt.am, run(am, rg.amp, t), nch_am);
+    load_run<V, CH_RV>(nxt.rv, run(rv, rg.rvp, t), nch_rv);
+    load_run<V, CH_TH>(nxt.dm, run(dm, PITCH, t), nch_dm);
+  };
+  load(0);
   const C rho_i = (C)rho[b];
   const C rho_f = rho_i * (C)rho_f_factor;
   const C sig = (C)sigma;
 
   C a[NC];  // row i of Theta_t, then of Theta_t^{-1}
   for (int t = 0; t < T; ++t) {
-    const int cur = (t & 1) * nxn, prv = ((t & 1) ^ 1) * nxn;
-    if (t < N) fetch(am + ((size_t)t * B + b0) * rg.amp, rg.amp, nxn, cur);
-    if (m) fetch(rv + ((size_t)t * B + b0) * rg.rvp + rg.g, rg.rvp, mn, o_gm);
-    fetch(dm + ((size_t)t * B + b0) * PITCH, PITCH, packed_size(n), o_dm);
+    const int cur = (t & 1) * (P * rg.amp), prv = ((t & 1) ^ 1) * (P * rg.amp);
+    if (t < N) store_run<V, CH_AM>(nxt.am, reinterpret_cast<V*>(ldr + FL.am + cur), nch_am);
+    store_run<V, CH_RV>(nxt.rv, reinterpret_cast<V*>(ldr + FL.rv), nch_rv);
+    store_run<V, CH_TH>(nxt.dm, reinterpret_cast<V*>(ldr + FL.dm), nch_dm);
     wsync();
-    const C* amc = mine + cur;
-    const C* amq = mine + prv;
+    if (t + 1 < T) load(t + 1);
+    const R* amc = ldr + FL.am + cur + p * rg.amp;
+    const R* amq = ldr + FL.am + prv + p * rg.amp;
     if (i < n) {
       // theta_t row i
       C c[NC], g[NC];

@@ -219,7 +219,7 @@ void launch_stream(hipStream_t s, const StreamArgs<R>& a, int P) {
 template <typename R, int NC, int P>
 void launch_factor_std_p(hipStream_t s, const Dims& d, const DirectWs<R>& w, const QPDev<R>& q, const R* rho,
                          R sigma, R rho_f_factor, int32_t* ctl) {
-  const size_t smem = (size_t)P * factor_std_per(d) * sizeof(double);
+  const size_t smem = factor_layout<R>(d, P).bytes;
   lds_optin(factor_std_kernel<R, NC, P>, smem);
   const int grid = (d.B + P - 1) / P;
   hipLaunchKernelGGL((factor_std_kernel<R, NC, P>), dim3(grid), dim3(kWave), smem, s, d, (const R*)w.am,
