@@ -238,32 +238,55 @@ __device__ __forceinline__ void store_run(const V (&r)[CH], V* dst, int nch) {
 }
 
 // Row i of a (rows x NC) row-major block times v; column i times v (rows entries).
+// The dot products first issue all their LDS reads, then (after a scheduling
+// barrier) the FMAs: left alone, the compiler interleaves one read pair with
+// one FMA pair and waits for every pair.
 template <typename R, int NC>
 __device__ __forceinline__ R lrow(const R* A, int i, const R* v) {
-  R acc = R(0);
+  R ak[NC], vk[NC];
   const R* a = A + i * NC;
 #pragma unroll
-  for (int k = 0; k < NC; ++k) acc += a[k] * v[k];
-  return acc;
-}
-template <typename R, int NC>
-__device__ __forceinline__ R lcol(const R* A, int rows, int i, const R* v) {
+  for (int k = 0; k < NC; ++k) {
+    ak[k] = a[k];
+    vk[k] = v[k];
+  }
+  __builtin_amdgcn_sched_barrier(0);
   R acc = R(0);
 #pragma unroll
-  for (int r = 0; r < NC; ++r)
-    if (r < rows) acc += A[r * NC + i] * v[r];
+  for (int k = 0; k < NC; ++k) acc += ak[k] * vk[k];
+  return acc;
+}
+// Rows past `rows` are read (they stay inside the LDS allocation) but their
+// values are replaced by zero before any arithmetic.
+template <typename R, int NC>
+__device__ __forceinline__ R lcol(const R* A, int rows, int i, const R* v) {
+  R ak[NC], vk[NC];
+#pragma unroll
+  for (int r = 0; r < NC; ++r) {
+    ak[r] = A[r * NC + i];
+    vk[r] = v[r];
+  }
+  __builtin_amdgcn_sched_barrier(0);
+  R acc = R(0);
+#pragma unroll
+  for (int r = 0; r < NC; ++r) acc += (r < rows ? ak[r] : R(0)) * (r < rows ? vk[r] : R(0));
   return acc;
 }
 // Row i of a packed symmetric (lower) block times v.
 template <typename R, int NC>
 __device__ __forceinline__ R lsym(const R* Th, int i, const R* v) {
-  R acc = R(0);
+  R ak[NC], vk[NC];
   const int ri = (i * (i + 1)) >> 1;
 #pragma unroll
   for (int k = 0; k < NC; ++k) {
     const int idx = k <= i ? ri + k : ((k * (k + 1)) >> 1) + i;
-    acc += Th[idx] * v[k];
+    ak[k] = Th[idx];
+    vk[k] = v[k];
   }
+  __builtin_amdgcn_sched_barrier(0);
+  R acc = R(0);
+#pragma unroll
+  for (int k = 0; k < NC; ++k) acc += ak[k] * vk[k];
   return acc;
 }
 

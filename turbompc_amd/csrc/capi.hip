@@ -172,7 +172,7 @@ void launch_chunk(hipStream_t s, const AdmmArgs<R>& a) {
 // Streaming kernel (explicit-integrator structure, n in {6, 9, 16, 17},
 // nx <= n - 1, m <= min(n, 8)).  P problems per wavefront: as many as keep
 // about two wavefronts per SIMD busy on a 256-CU device, at most 3.
-constexpr int kStreamDepth = 2;
+constexpr int kStreamDepth = 1;
 constexpr size_t kMaxLds = 160 * 1024;
 
 inline int stream_problems_per_wave(int B, uint32_t flags) {
