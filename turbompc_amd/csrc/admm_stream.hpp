@@ -808,31 +808,43 @@ __global__ __launch_bounds__(kWave) void factor_std_kernel(Dims d, const R* __re
     const R* amc = ldr + FL.am + cur + p * rg.amp;
     const R* amq = ldr + FL.am + prv + p * rg.amp;
     if (i < n) {
-      // theta_t row i
+      // theta_t row i.  Every loop body below issues its LDS reads, then a
+      // scheduling barrier, then its FMAs, so the reads of a body share one
+      // round trip.
       C c[NC], g[NC];
+      {
+        R dk[NC];
 #pragma unroll
-      for (int k = 0; k < NC; ++k) {
-        a[k] = dmt[pidx(i, k)] + (k == i ? sig : C(0));
-        c[k] = C(0);
-        g[k] = C(0);
-      }
-      if (t == 0)
-        for (int r = 0; r < n0; ++r) {
-          const C ar = a0[r * n + i];
+        for (int k = 0; k < NC; ++k) dk[k] = dmt[pidx(i, k)];
+        __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-          for (int k = 0; k < NC; ++k) c[k] += ar * a0[r * n + k];
+        for (int k = 0; k < NC; ++k) {
+          a[k] = (C)dk[k] + (k == i ? sig : C(0));
+          c[k] = C(0);
+          g[k] = C(0);
         }
-      if (t < N)
-        for (int r = 0; r < nx; ++r) {
-          const C ar = amc[r * n + i];
-#pragma unroll
-          for (int k = 0; k < NC; ++k) c[k] += ar * amc[r * n + k];
-        }
-      for (int r = 0; r < m; ++r) {
-        const C gr = gm[r * n + i];
-#pragma unroll
-        for (int k = 0; k < NC; ++k) g[k] += gr * gm[r * n + k];
       }
+      // c += sum_r M[r][i] M[r][:] over the rows of an (rows x n) block, two rows per round trip
+      auto gram = [&](const R* M, int rows, C* acc) {
+        for (int r = 0; r < rows; r += 2) {
+          const bool two = r + 1 < rows;
+          R m0[NC], m1[NC];
+          const R a0v = M[r * n + i];
+          const R a1v = M[(two ? r + 1 : r) * n + i];
+#pragma unroll
+          for (int k = 0; k < NC; ++k) {
+            m0[k] = M[r * n + k];
+            m1[k] = M[(two ? r + 1 : r) * n + k];
+          }
+          __builtin_amdgcn_sched_barrier(0);
+          const C s0 = (C)a0v, s1 = two ? (C)a1v : C(0);
+#pragma unroll
+          for (int k = 0; k < NC; ++k) acc[k] += s0 * (C)m0[k] + s1 * (C)m1[k];
+        }
+      };
+      if (t == 0) gram(a0, n0, c);
+      if (t < N) gram(amc, nx, c);
+      if (m) gram(gm, m, g);
 #pragma unroll
       for (int k = 0; k < NC; ++k) {
         if (t > 0 && k == i && i < nx) c[k] += C(1);  // A_plus_{t-1}^T A_plus_{t-1} = diag(I_nx, 0)
@@ -841,21 +853,32 @@ __global__ __launch_bounds__(kWave) void factor_std_kernel(Dims d, const R* __re
       // Schur update of the leading nx x nx block
       if (t > 0 && i < nx) {
         C mr[NC];
+        R aq[NC];
+#pragma unroll
+        for (int k = 0; k < NC; ++k) aq[k] = amq[i * n + k];
 #pragma unroll
         for (int j = 0; j < NC; ++j) mr[j] = C(0);
 #pragma unroll
         for (int k = 0; k < NC; ++k) {
-          const C ak = amq[i * n + k];
+          C tk[NC];
 #pragma unroll
-          for (int j = 0; j < NC; ++j) mr[j] += ak * th[k * n + j];
+          for (int j = 0; j < NC; ++j) tk[j] = th[k * n + j];
+          __builtin_amdgcn_sched_barrier(0);
+          const C ak = (C)aq[k];
+#pragma unroll
+          for (int j = 0; j < NC; ++j) mr[j] += ak * tk[j];
         }
         const C f2 = rho_f * rho_f;
 #pragma unroll
         for (int s = 0; s < NC; ++s) {
           if (s < nx) {
+            R qs[NC];
+#pragma unroll
+            for (int k = 0; k < NC; ++k) qs[k] = amq[s * n + k];
+            __builtin_amdgcn_sched_barrier(0);
             C sv = C(0);
 #pragma unroll
-            for (int k = 0; k < NC; ++k) sv += mr[k] * amq[s * n + k];
+            for (int k = 0; k < NC; ++k) sv += mr[k] * (C)qs[k];
             a[s] -= f2 * sv;
           }
         }
@@ -870,14 +893,18 @@ __global__ __launch_bounds__(kWave) void factor_std_kernel(Dims d, const R* __re
         for (int j = 0; j < NC; ++j) piv[j] = a[j];
       wsync();
       if (i < n) {
-        const C ip = C(1) / piv[k];
+        C pv[NC];
+#pragma unroll
+        for (int j = 0; j < NC; ++j) pv[j] = piv[j];
+        __builtin_amdgcn_sched_barrier(0);
+        const C ip = C(1) / pv[k];
         if (i == k) {
 #pragma unroll
           for (int j = 0; j < NC; ++j) a[j] = (j == k) ? ip : a[j] * ip;
         } else {
           const C f = a[k];
 #pragma unroll
-          for (int j = 0; j < NC; ++j) a[j] = (j == k) ? -f * ip : a[j] - f * piv[j] * ip;
+          for (int j = 0; j < NC; ++j) a[j] = (j == k) ? -f * ip : a[j] - f * pv[j] * ip;
         }
       }
     }
