@@ -200,13 +200,14 @@ int tmpc_quadrotor_linearize_f64(hipStream_t stream, int32_t B, int32_t N, const
  * y_f (B,N,nx), y_g (B,T,m); slack (B,T,m) or NULL when slack variables are off.
  * conv (B,) = max(stationarity, equality, inequality-violation, slack
  * stationarity) inf-norms; eq_err, ineq_err (B,) and g_out (B,T,m) = G x (+ slack)
- * may be NULL. */
+ * may be NULL.  flags: TMPC_FLAG_STD_DYNAMICS asserts A_plus_t = [-I 0] and
+ * E_t = 0, which are then not read. */
 int tmpc_sqp_first_order_f32(hipStream_t stream, const tmpc_dims* dims, const tmpc_qp* qp, const float* x,
                              const float* y_f0, const float* y_f, const float* y_g, const float* slack,
-                             double slack_weight, float* conv, float* eq_err, float* ineq_err, float* g_out);
+                             double slack_weight, uint32_t flags, float* conv, float* eq_err, float* ineq_err, float* g_out);
 int tmpc_sqp_first_order_f64(hipStream_t stream, const tmpc_dims* dims, const tmpc_qp* qp, const double* x,
                              const double* y_f0, const double* y_f, const double* y_g, const double* slack,
-                             double slack_weight, double* conv, double* eq_err, double* ineq_err, double* g_out);
+                             double slack_weight, uint32_t flags, double* conv, double* eq_err, double* ineq_err, double* g_out);
 
 #ifdef __cplusplus
 }

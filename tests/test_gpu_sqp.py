@@ -98,3 +98,40 @@ def test_first_order_check_kernel_matches_torch(dtype):
     tol = 1e-12 if dtype == torch.float64 else 1e-5
     for a, b in ((ck, ct), (ek, et), (ik, it_), (gk, gt)):
         assert rel_err(a, b) < tol
+
+
+@pytest.mark.parametrize("std", [False, True])
+@pytest.mark.parametrize("dtype", [torch.float64, torch.float32])
+@pytest.mark.parametrize("use_slack", [False, True])
+def test_first_order_check_kernel_matches_dense_assembly(std, dtype, use_slack):
+    """The check on random QPs (general E / A_plus, or the explicit-integrator
+    structure read with std_dynamics=True) against dense P, C, G products."""
+    from helpers import dense_C, dense_G, dense_P, np_qp, random_qp
+    from turbompc_amd.solvers.sqp_hip import first_order_check
+
+    B, T, n, nx, m = 5, 7, 9, 6, 11
+    qp = random_qp(B, T, n, nx, m, seed=11 + std, std=std)
+    rng = np.random.default_rng(4)
+    x, yg = rng.standard_normal((B, T, n)), rng.standard_normal((B, T, m))
+    y0, yf = rng.standard_normal((B, nx)), rng.standard_normal((B, T - 1, nx))
+    sl = rng.standard_normal((B, T, m)) * 0.3 if use_slack else None
+    w = 2.5
+    dev = lambda a: torch.tensor(a, dtype=dtype, device="cuda")  # noqa: E731
+    conv, eq, iq, g = first_order_check(qp.to("cuda", dtype), dev(x), dev(y0), dev(yf), dev(yg),
+                                        dev(sl) if use_slack else None, w, std_dynamics=std)
+    a = np_qp(qp)
+    for b in range(B):
+        P, C, Gd = dense_P(a["D"][b], a["E"][b]), dense_C(a["A0"][b], a["Am"][b], a["Ap"][b]), dense_G(a["G"][b])
+        xv = x[b].ravel()
+        y = np.concatenate([y0[b], yf[b].ravel()])
+        stat = np.abs(P @ xv + a["q"][b].ravel() + C.T @ y + Gd.T @ yg[b].ravel()).max()
+        e = np.abs(C @ xv - np.concatenate([a["c0"][b], a["c"][b].ravel()])).max()
+        gv = Gd @ xv + (sl[b].ravel() if use_slack else 0.0)
+        i = max(np.maximum(a["l"][b].ravel() - gv, 0).max(), np.maximum(gv - a["u"][b].ravel(), 0).max())
+        s = np.abs(w * sl[b].ravel() + yg[b].ravel()).max() if use_slack else 0.0
+        tol = 1e-12 if dtype == torch.float64 else 1e-5
+        scale = max(stat, e, i, 1.0)
+        assert abs(float(conv[b]) - max(stat, e, i, s)) <= tol * scale
+        assert abs(float(eq[b]) - e) <= tol * scale
+        assert abs(float(iq[b]) - i) <= tol * scale
+        assert rel_err(g[b].reshape(-1), gv) < tol * 10

@@ -113,8 +113,8 @@ SIGNATURES = {
     "tmpc_adjoint_kkt_workspace_bytes": [ctypes.c_int, _PD],
     "tmpc_adjoint_kkt_f32": [_VP, _PD, _PQ, _VP, _VP, _F64, _I32, _U32, _VP, _SZ],
     "tmpc_adjoint_kkt_f64": [_VP, _PD, _PQ, _VP, _VP, _F64, _I32, _U32, _VP, _SZ],
-    "tmpc_sqp_first_order_f32": [_VP, _PD, _PQ, _VP, _VP, _VP, _VP, _VP, _F64, _VP, _VP, _VP, _VP],
-    "tmpc_sqp_first_order_f64": [_VP, _PD, _PQ, _VP, _VP, _VP, _VP, _VP, _F64, _VP, _VP, _VP, _VP],
+    "tmpc_sqp_first_order_f32": [_VP, _PD, _PQ, _VP, _VP, _VP, _VP, _VP, _F64, _U32, _VP, _VP, _VP, _VP],
+    "tmpc_sqp_first_order_f64": [_VP, _PD, _PQ, _VP, _VP, _VP, _VP, _VP, _F64, _U32, _VP, _VP, _VP, _VP],
     "tmpc_quadrotor_linearize_f32": [_VP, _I32, _I32, _VP, _VP, _F64, _VP, _VP, _VP],
     "tmpc_quadrotor_linearize_f64": [_VP, _I32, _I32, _VP, _VP, _F64, _VP, _VP, _VP],
 }

@@ -662,26 +662,36 @@ int quad_impl(hipStream_t s, int B, int N, const R* states, const R* controls, d
 
 // ------------------------------------------------------------- SQP check ----
 template <typename R, int NC>
-void launch_sqp_nc(hipStream_t s, const Dims& d, int g, int P, const QPDev<R>& q, const R* x, const R* y0,
+void launch_sqp_nc(hipStream_t s, const Dims& d, bool std_dyn, const QPDev<R>& q, const R* x, const R* y0,
                    const R* yf, const R* yg, const R* sl, R sw, R* conv, R* eq, R* iq, R* gout) {
-  hipLaunchKernelGGL((sqp_check_kernel<R, NC>), dim3((d.B + P - 1) / P), dim3(kWave), 0, s, d, g, P, q, x, y0, yf,
-                     yg, sl, sw, conv, eq, iq, gout);
+  const dim3 grid(d.B * d.T);
+  const size_t smem = check_smem_bytes<R>(d.n, d.nx, d.m);
+  lds_optin(sqp_check_stage_kernel<R, NC, true>, smem);
+  lds_optin(sqp_check_stage_kernel<R, NC, false>, smem);
+  if (std_dyn)
+    hipLaunchKernelGGL((sqp_check_stage_kernel<R, NC, true>), grid, dim3(kWave), smem, s, d, q, x, y0, yf, yg, sl, sw,
+                       conv, eq, iq, gout);
+  else
+    hipLaunchKernelGGL((sqp_check_stage_kernel<R, NC, false>), grid, dim3(kWave), smem, s, d, q, x, y0, yf, yg, sl, sw,
+                       conv, eq, iq, gout);
 }
 
 template <typename R>
 int sqp_check_impl(hipStream_t s, const tmpc_dims* dims, const tmpc_qp* qp, const R* x, const R* y0, const R* yf,
-                   const R* yg, const R* slack, double slack_w, R* conv, R* eq, R* iq, R* gout) {
+                   const R* yg, const R* slack, double slack_w, uint32_t flags, R* conv, R* eq, R* iq, R* gout) {
   if (!dims_ok(dims)) return TMPC_EBADSHAPE;
   if (!qp_ok(qp, dims->m) || !x || !y0 || !yf || !conv || (dims->m > 0 && !yg)) return TMPC_EBADARG;
   const Dims d = to_dims(dims);
+  if ((long long)d.B * d.T > INT32_MAX) return TMPC_EBADSHAPE;
   const QPDev<R> q = to_qp<R>(qp);
-  const int g = std::max(d.n, d.m), P = kWave / g;
+  hipLaunchKernelGGL((sqp_check_init_kernel<R>), dim3((d.B + 255) / 256), dim3(256), 0, s, d.B, conv, eq, iq);
+  const bool std_dyn = flags & TMPC_FLAG_STD_DYNAMICS;
   switch (d.n) {
-    case 6: launch_sqp_nc<R, 6>(s, d, g, P, q, x, y0, yf, yg, slack, (R)slack_w, conv, eq, iq, gout); break;
-    case 9: launch_sqp_nc<R, 9>(s, d, g, P, q, x, y0, yf, yg, slack, (R)slack_w, conv, eq, iq, gout); break;
-    case 16: launch_sqp_nc<R, 16>(s, d, g, P, q, x, y0, yf, yg, slack, (R)slack_w, conv, eq, iq, gout); break;
-    case 17: launch_sqp_nc<R, 17>(s, d, g, P, q, x, y0, yf, yg, slack, (R)slack_w, conv, eq, iq, gout); break;
-    default: launch_sqp_nc<R, 0>(s, d, g, P, q, x, y0, yf, yg, slack, (R)slack_w, conv, eq, iq, gout); break;
+    case 6: launch_sqp_nc<R, 6>(s, d, std_dyn, q, x, y0, yf, yg, slack, (R)slack_w, conv, eq, iq, gout); break;
+    case 9: launch_sqp_nc<R, 9>(s, d, std_dyn, q, x, y0, yf, yg, slack, (R)slack_w, conv, eq, iq, gout); break;
+    case 16: launch_sqp_nc<R, 16>(s, d, std_dyn, q, x, y0, yf, yg, slack, (R)slack_w, conv, eq, iq, gout); break;
+    case 17: launch_sqp_nc<R, 17>(s, d, std_dyn, q, x, y0, yf, yg, slack, (R)slack_w, conv, eq, iq, gout); break;
+    default: launch_sqp_nc<R, 0>(s, d, std_dyn, q, x, y0, yf, yg, slack, (R)slack_w, conv, eq, iq, gout); break;
   }
   return launch_status();
 }
@@ -821,13 +831,15 @@ int tmpc_quadrotor_linearize_f64(hipStream_t s, int32_t B, int32_t N, const doub
 
 int tmpc_sqp_first_order_f32(hipStream_t s, const tmpc_dims* dims, const tmpc_qp* qp, const float* x,
                              const float* y_f0, const float* y_f, const float* y_g, const float* slack,
-                             double slack_weight, float* conv, float* eq_err, float* ineq_err, float* g_out) {
-  return sqp_check_impl<float>(s, dims, qp, x, y_f0, y_f, y_g, slack, slack_weight, conv, eq_err, ineq_err, g_out);
+                             double slack_weight, uint32_t flags, float* conv, float* eq_err, float* ineq_err,
+                             float* g_out) {
+  return sqp_check_impl<float>(s, dims, qp, x, y_f0, y_f, y_g, slack, slack_weight, flags, conv, eq_err, ineq_err, g_out);
 }
 int tmpc_sqp_first_order_f64(hipStream_t s, const tmpc_dims* dims, const tmpc_qp* qp, const double* x,
                              const double* y_f0, const double* y_f, const double* y_g, const double* slack,
-                             double slack_weight, double* conv, double* eq_err, double* ineq_err, double* g_out) {
-  return sqp_check_impl<double>(s, dims, qp, x, y_f0, y_f, y_g, slack, slack_weight, conv, eq_err, ineq_err, g_out);
+                             double slack_weight, uint32_t flags, double* conv, double* eq_err, double* ineq_err,
+                             double* g_out) {
+  return sqp_check_impl<double>(s, dims, qp, x, y_f0, y_f, y_g, slack, slack_weight, flags, conv, eq_err, ineq_err, g_out);
 }
 
 }  // extern "C"

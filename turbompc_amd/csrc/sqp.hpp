@@ -7,100 +7,248 @@
 //   ineq_err      = || max(l - g, 0), max(g - u, 0) ||_inf,  g = G x (+ slack)
 //   conv          = max(stationarity, eq_err, ineq_err, slack stationarity)
 // and g itself (the inequality values the KKT-state active sets are built
-// from, :1387-1439).  One group of g = max(n, m) lanes per problem walks the
-// stages with a three-stage window of x in LDS, like the ADMM residual pass.
+// from, :1387-1439).
+//
+// Every (problem, stage) pair is independent here, so one 64-lane block per
+// pair evaluates its stage's rows (lane i = row i, read straight from the QP
+// blocks) and folds its maxima into the per-problem outputs with atomicMax
+// on the IEEE bit pattern (non-negative values order like unsigned integers).
+// sqp_check_init_kernel zeroes the outputs first.
 #pragma once
-#include "admm_direct.hpp"
 #include "common.hpp"
 
 namespace tmpc {
 
+template <typename R>
+struct Bits;
+template <>
+struct Bits<float> {
+  using U = unsigned int;
+  __device__ static U of(float v) { return __float_as_uint(v) & 0x7fffffffu; }
+};
+template <>
+struct Bits<double> {
+  using U = unsigned long long;
+  __device__ static U of(double v) { return (U)__double_as_longlong(v) & 0x7fffffffffffffffull; }
+};
+
+template <typename R>
+__device__ __forceinline__ void atomic_max_abs(R* p, R v) {
+  using U = typename Bits<R>::U;
+  atomicMax(reinterpret_cast<U*>(p), Bits<R>::of(v));
+}
+
+template <typename R>
+__device__ __forceinline__ R wave_max(R v) {
+#pragma unroll
+  for (int off = kWave / 2; off > 0; off >>= 1) v = rmax(v, __shfl_xor(v, off));
+  return v;
+}
+
+template <typename R>
+__global__ void sqp_check_init_kernel(int B, R* __restrict__ conv, R* __restrict__ eq, R* __restrict__ iq) {
+  const int b = blockIdx.x * blockDim.x + threadIdx.x;
+  if (b >= B) return;
+  conv[b] = R(0);
+  if (eq) eq[b] = R(0);
+  if (iq) iq[b] = R(0);
+}
+
+// Broadcast lane `k` of v to the whole wave (v_readlane: the value lands in a
+// scalar register, so the dot products below read no LDS for vector operands).
+__device__ __forceinline__ float lane_bcast(float v, int k) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), k));
+}
+__device__ __forceinline__ double lane_bcast(double v, int k) {
+  const long long u = __builtin_bit_cast(long long, v);
+  const int lo = __builtin_amdgcn_readlane((int)u, k), hi = __builtin_amdgcn_readlane((int)(u >> 32), k);
+  return __builtin_bit_cast(double, ((long long)hi << 32) | (unsigned)lo);
+}
+
+// Row stride of a staged block in LDS: odd, so lane i reading row i hits
+// distinct banks.
+__host__ __device__ constexpr int check_ld(int n) { return n | 1; }
+
+// A stage block of len (<= K * 64) contiguous elements, loaded into
+// registers (K elements per lane) so every load of a stage is in flight
+// before the first LDS store; put() writes it as rows of stride ld (n
+// columns).  K = 0 (n known only at run time) copies in a plain loop.
+template <typename R, int K>
+struct StageBlock {
+  R r[K > 0 ? K : 1];
+  const R* src = nullptr;
+  int len = 0;
+  __device__ __forceinline__ void get(const R* __restrict__ s, int l) {
+    src = s;
+    len = l;
+    if constexpr (K > 0) {
+#pragma unroll
+      for (int j = 0; j < K; ++j) {
+        const int e = threadIdx.x + j * kWave;
+        r[j] = e < l ? s[e] : R(0);
+      }
+    }
+  }
+  __device__ __forceinline__ void put(R* __restrict__ dst, int n, int ld) const {
+    if constexpr (K > 0) {
+#pragma unroll
+      for (int j = 0; j < K; ++j) {
+        const int e = threadIdx.x + j * kWave;
+        if (e < len) dst[(e / n) * ld + e % n] = r[j];
+      }
+    } else {
+      for (int e = threadIdx.x; e < len; e += kWave) dst[(e / n) * ld + e % n] = src[e];
+    }
+  }
+};
+
+// sum_k A[i*ld + k] * bcast(v, k), k < n (A in LDS).
 template <typename R, int NC>
-__global__ __launch_bounds__(kWave) void sqp_check_kernel(Dims d, int g, int P, QPDev<R> qp, const R* __restrict__ x,
-                                                          const R* __restrict__ y0, const R* __restrict__ yf,
-                                                          const R* __restrict__ yg, const R* __restrict__ slack,
-                                                          R slack_w, R* __restrict__ conv, R* __restrict__ eq_err,
-                                                          R* __restrict__ ineq_err, R* __restrict__ gout) {
-  __shared__ R sv[7][kWave];
-  __shared__ R red[4][kWave];
-  const int n = NC > 0 ? NC : d.n;
-  const int T = d.T, N = d.N, nx = d.nx, n0 = d.n0, m = d.m;
-  const Group G = make_group(g, P, d.B);
-  const int b = G.prob, i = G.lane, base = G.gid * g;
-  R* xp = sv[0] + base;
-  R* xc = sv[1] + base;
-  R* xn = sv[2] + base;
-  R* yp = sv[3] + base;
-  R* yc = sv[4] + base;
-  R* yy = sv[5] + base;
-  R* y00 = sv[6] + base;
-  const R* X = x + (size_t)b * T * n;
-  R st = 0, eq = 0, iq = 0, sl = 0;
-  if (i < n) {
-    xp[i] = R(0);
-    xc[i] = X[i];
-    xn[i] = X[n + i];
+__device__ __forceinline__ R row_bdot(const R* A, int i, int ld, int n, R v) {
+  if constexpr (NC > 0) {
+    R a[NC];
+#pragma unroll
+    for (int k = 0; k < NC; ++k) a[k] = A[i * ld + k];
+    __builtin_amdgcn_sched_barrier(0);
+    R acc = R(0);
+#pragma unroll
+    for (int k = 0; k < NC; ++k) acc += a[k] * lane_bcast(v, k);
+    return acc;
+  } else {
+    R acc = R(0);
+    for (int k = 0; k < n; ++k) acc += A[i * ld + k] * lane_bcast(v, k);
+    return acc;
   }
-  if (i < n0) y00[i] = y0[(size_t)b * n0 + i];
-  for (int t = 0; t < T; ++t) {
-    if (t < N && i < nx) yc[i] = yf[((size_t)b * N + t) * nx + i];
-    if (i < m) yy[i] = yg[((size_t)b * T + t) * m + i];
-    wsync();
-    if (i < n) {
-      R px = row_dot<R, NC>(qp.D + ((size_t)b * T + t) * n * n, i, n, xc);
-      if (t > 0) px += row_dot<R, NC>(qp.E + ((size_t)b * N + t - 1) * n * n, i, n, xp);
-      if (t < N) {
-        const R* Et = qp.E + ((size_t)b * N + t) * n * n;
-        R s = 0;
-        for (int k = 0; k < n; ++k) s += Et[k * n + i] * xn[k];
-        px += s;
-      }
-      R aty = R(0);
-      if (t == 0) aty += col_dot(qp.A0 + (size_t)b * n0 * n, n0, n, i, y00);
-      if (t < N) aty += col_dot(qp.Am + ((size_t)b * N + t) * nx * n, nx, n, i, yc);
-      if (t > 0) aty += col_dot(qp.Ap + ((size_t)b * N + t - 1) * nx * n, nx, n, i, yp);
-      if (m) aty += col_dot(qp.G + ((size_t)b * T + t) * m * n, m, n, i, yy);
-      st = rmax(st, rabs(px + qp.q[((size_t)b * T + t) * n + i] + aty));
-    }
-    if (t < N && i < nx) {
-      const R cx = row_dot<R, NC>(qp.Am + ((size_t)b * N + t) * nx * n, i, n, xc) +
-                   row_dot<R, NC>(qp.Ap + ((size_t)b * N + t) * nx * n, i, n, xn);
-      eq = rmax(eq, rabs(cx - qp.c[((size_t)b * N + t) * nx + i]));
-    }
-    if (t == 0 && i < n0) eq = rmax(eq, rabs(row_dot<R, NC>(qp.A0 + (size_t)b * n0 * n, i, n, xc) - qp.c0[(size_t)b * n0 + i]));
-    if (i < m) {
-      const size_t o = ((size_t)b * T + t) * m + i;
-      R gv = row_dot<R, NC>(qp.G + ((size_t)b * T + t) * m * n, i, n, xc);
-      if (slack) {
-        gv += slack[o];
-        sl = rmax(sl, rabs(slack_w * slack[o] + yy[i]));
-      }
-      iq = rmax(iq, rmax(rmax(qp.l[o] - gv, R(0)), rmax(gv - qp.u[o], R(0))));
-      if (G.live && gout) gout[o] = gv;
-    }
-    wsync();
-    if (i < n) {
-      xp[i] = xc[i];
-      xc[i] = xn[i];
-    }
-    if (t < N && i < nx) yp[i] = yc[i];
-    wsync();
-    if (i < n) xn[i] = (t + 2 < T) ? X[(size_t)(t + 2) * n + i] : R(0);
+}
+
+// sum_r A[r*ld + i] * bcast(v, r), r < rows (LDS reads batched four at a time).
+template <typename R>
+__device__ __forceinline__ R col_bdot(const R* A, int i, int ld, int rows, R v) {
+  R acc = R(0);
+  int r = 0;
+  for (; r + 4 <= rows; r += 4) {
+    R a[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) a[j] = A[(r + j) * ld + i];
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) acc += a[j] * lane_bcast(v, r + j);
   }
-  const int tid = threadIdx.x;
-  red[0][tid] = i < g ? st : R(0);
-  red[1][tid] = i < g ? eq : R(0);
-  red[2][tid] = i < g ? iq : R(0);
-  red[3][tid] = i < g ? sl : R(0);
+  for (; r < rows; ++r) acc += A[r * ld + i] * lane_bcast(v, r);
+  return acc;
+}
+
+// One wave per (problem, stage).  D_t, A_minus_t and G_t are staged through
+// LDS; the vectors stay in registers (lane k holds element k) and reach the
+// other lanes by broadcast.  STD: A_plus_t = [-I 0] and E_t = 0 (neither is
+// read); otherwise E and A_plus are read from global memory directly.
+template <typename R, int NC, bool STD>
+__global__ __launch_bounds__(kWave) void sqp_check_stage_kernel(Dims d, QPDev<R> qp, const R* __restrict__ x,
+                                                              const R* __restrict__ y0, const R* __restrict__ yf,
+                                                              const R* __restrict__ yg, const R* __restrict__ slack,
+                                                              R slack_w, R* __restrict__ conv, R* __restrict__ eq_err,
+                                                              R* __restrict__ ineq_err, R* __restrict__ gout) {
+  extern __shared__ __align__(16) unsigned char check_smem[];
+  R* sD = reinterpret_cast<R*>(check_smem);
+  const int T = d.T, b = blockIdx.x / T, t = blockIdx.x - b * T, i = threadIdx.x;
+  const int N = d.N, n = NC > 0 ? NC : d.n, nx = d.nx, n0 = d.n0, m = d.m;
+  const int ld = check_ld(n);
+  R* sAm = sD + n * ld;
+  R* sG = sAm + nx * ld;
+  const size_t bt = (size_t)b * T + t, bn = (size_t)b * N;
+  const bool has_next = t < N, has_prev = t > 0;
+  constexpr int KB = NC > 0 ? (NC * NC + kWave - 1) / kWave : 0;
+  constexpr int KG = NC > 0 ? NC : 0;  // m <= 64 rows of NC
+
+  // Every load of the stage is issued before the first use.
+  const R xt = i < n ? x[bt * n + i] : R(0);
+  const R xn = has_next && i < n ? x[(bt + 1) * n + i] : R(0);
+  const R xp = !STD && has_prev && i < n ? x[(bt - 1) * n + i] : R(0);
+  const R yc = has_next && i < nx ? yf[(bn + t) * nx + i] : R(0);
+  const R yp = has_prev && i < nx ? yf[(bn + t - 1) * nx + i] : R(0);
+  const R y0v = t == 0 && i < n0 ? y0[(size_t)b * n0 + i] : R(0);
+  const R ygv = i < m ? yg[bt * m + i] : R(0);
+  const R qv = i < n ? qp.q[bt * n + i] : R(0);
+  const R cv = has_next && i < nx ? qp.c[(bn + t) * nx + i] : R(0);
+  const R c0v = t == 0 && i < n0 ? qp.c0[(size_t)b * n0 + i] : R(0);
+  const R lv = i < m ? qp.l[bt * m + i] : R(0);
+  const R uv = i < m ? qp.u[bt * m + i] : R(0);
+  const R slv = slack && i < m ? slack[bt * m + i] : R(0);
+  StageBlock<R, KB> bD, bA;
+  StageBlock<R, KG> bG;
+  bD.get(qp.D + bt * n * n, n * n);
+  bA.get(qp.Am + (bn + (has_next ? t : 0)) * nx * n, has_next ? nx * n : 0);
+  bG.get(qp.G + bt * m * n, m * n);
+  __builtin_amdgcn_sched_barrier(0);
+  bD.put(sD, n, ld);
+  bA.put(sAm, n, ld);
+  bG.put(sG, n, ld);
   wsync();
-  if (G.live && i == 0) {
-    R r[4] = {0, 0, 0, 0};
-    for (int k = 0; k < 4; ++k)
-      for (int l = 0; l < g; ++l) r[k] = rmax(r[k], red[k][base + l]);
-    conv[b] = rmax(r[0], rmax(r[1], rmax(r[2], r[3])));
-    if (eq_err) eq_err[b] = r[1];
-    if (ineq_err) ineq_err[b] = r[2];
+
+  // Branches below depend on the stage only (uniform); rows past the block's
+  // height are computed on row 0 and dropped, so every lane reaches every
+  // broadcast.
+  const int in = i < n ? i : 0, ix = i < nx ? i : 0, im = i < m ? i : 0, i0 = i < n0 ? i : 0;
+  R px = row_bdot<R, NC>(sD, in, ld, n, xt);
+  R aty = m ? col_bdot(sG, in, ld, m, ygv) : R(0);
+  if (has_next) aty += col_bdot(sAm, in, ld, nx, yc);
+  if (STD) {
+    if (has_prev && i < nx) aty -= yp;
+  } else {
+    if (has_prev) {
+      const R* Ep = qp.E + (bn + t - 1) * n * n + (size_t)in * n;
+      const R* Ap = qp.Ap + (bn + t - 1) * nx * n;
+      for (int k = 0; k < n; ++k) px += Ep[k] * lane_bcast(xp, k);
+      for (int r = 0; r < nx; ++r) aty += Ap[(size_t)r * n + in] * lane_bcast(yp, r);
+    }
+    if (has_next) {
+      const R* En = qp.E + (bn + t) * n * n;
+      for (int k = 0; k < n; ++k) px += En[(size_t)k * n + in] * lane_bcast(xn, k);
+    }
   }
+  if (t == 0) {
+    const R* A0 = qp.A0 + (size_t)b * n0 * n;
+    for (int r = 0; r < n0; ++r) aty += A0[(size_t)r * n + in] * lane_bcast(y0v, r);
+  }
+  R st = i < n ? rabs(px + qv + aty) : R(0);
+  R eq = 0, iq = 0, sl = 0;
+  if (has_next) {
+    R cx = row_bdot<R, NC>(sAm, ix, ld, n, xt);
+    if (STD) {
+      cx -= xn;
+    } else {
+      const R* Ap = qp.Ap + (bn + t) * nx * n + (size_t)ix * n;
+      for (int k = 0; k < n; ++k) cx += Ap[k] * lane_bcast(xn, k);
+    }
+    if (i < nx) eq = rabs(cx - cv);
+  }
+  if (t == 0) {
+    const R* A0 = qp.A0 + ((size_t)b * n0 + i0) * n;
+    R cx = 0;
+    for (int k = 0; k < n; ++k) cx += A0[k] * lane_bcast(xt, k);
+    if (i < n0) eq = rmax(eq, rabs(cx - c0v));
+  }
+  if (m) {
+    const R gv = row_bdot<R, NC>(sG, im, ld, n, xt) + slv;
+    if (i < m) {
+      if (slack) sl = rabs(slack_w * slv + ygv);
+      iq = rmax(rmax(lv - gv, R(0)), rmax(gv - uv, R(0)));
+      if (gout) gout[bt * m + i] = gv;
+    }
+  }
+  const R all = wave_max(rmax(rmax(st, eq), rmax(iq, sl)));
+  if (eq_err) eq = wave_max(eq);
+  if (ineq_err) iq = wave_max(iq);
+  if (i == 0) {
+    atomic_max_abs(conv + b, all);
+    if (eq_err) atomic_max_abs(eq_err + b, eq);
+    if (ineq_err) atomic_max_abs(ineq_err + b, iq);
+  }
+}
+
+template <typename R>
+constexpr size_t check_smem_bytes(int n, int nx, int m) {
+  return (size_t)(n + nx + m) * check_ld(n) * sizeof(R);
 }
 
 }  // namespace tmpc

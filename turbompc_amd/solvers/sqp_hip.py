@@ -2,7 +2,10 @@
 
 first_order_check: _compute_first_order_convergence_error
 (turbompc/solvers/turbompc_solver.py:1158-1225) for the whole batch in one
-kernel, returning (conv, eq_err, ineq_err, g) with g = G x (+ slack).
+kernel launch over every (problem, stage) pair, returning
+(conv, eq_err, ineq_err, g) with g = G x (+ slack).  std_dynamics=True asserts
+A_plus_t = [-I 0] and E_t = 0 (explicit integrators), which the kernel then
+does not read; None or False evaluates the general blocks.
 """
 from __future__ import annotations
 
@@ -17,7 +20,8 @@ from .qp_data import QPData
 
 
 def first_order_check(qp: QPData, x: torch.Tensor, y_f0: torch.Tensor, y_f: torch.Tensor, y_g: torch.Tensor,
-                      slack: Optional[torch.Tensor] = None, slack_weight: float = 0.0):
+                      slack: Optional[torch.Tensor] = None, slack_weight: float = 0.0,
+                      std_dynamics: Optional[bool] = None):
     lib = _lib.load()
     B, T, n, nx, n0, m = qp.dims
     dt, dev = qp.dtype, qp.device
@@ -32,7 +36,8 @@ def first_order_check(qp: QPData, x: torch.Tensor, y_f0: torch.Tensor, y_f: torc
     sfx = _lib.suffix(dt)
     st = getattr(lib, f"tmpc_sqp_first_order_{sfx}")(
         _lib.stream_handle(dev), ctypes.byref(dims), ctypes.byref(cq), _lib.ptr(x), _lib.ptr(y_f0), _lib.ptr(y_f),
-        _lib.ptr(y_g), _lib.ptr(slack), float(slack_weight), _lib.ptr(conv), _lib.ptr(eq), _lib.ptr(iq), _lib.ptr(g),
+        _lib.ptr(y_g), _lib.ptr(slack), float(slack_weight),
+        _lib.FLAG_STD_DYNAMICS if std_dynamics else 0, _lib.ptr(conv), _lib.ptr(eq), _lib.ptr(iq), _lib.ptr(g),
     )
     _lib.check(f"tmpc_sqp_first_order_{sfx}", st)
     del keep
