@@ -9,10 +9,14 @@
 // Stage records.  Before the first iteration, stage_pack_kernel copies the QP
 // and the warm start into stage-major workspace arrays, so that for a stage t
 // the P problems of one wavefront (b0 .. b0+P-1) sit in one contiguous run:
-//   th [T][B][pitch]  Theta_t^{-1} (packed, written by factor_kernel)
-//   am [N][B][amp]    A_minus_t
-//   rv [T][B][rvp]    G_t | x q z y_g xi l u (stage t) | y_f c (dynamics row t)
-//   dm [T][B][pitch]  D_t (packed; residual pass only)
+//   th [T][B][pitch]  Theta_t^{-1} (packed, written by factor_std_kernel)
+//   am [T][B][amp]    M_t = [A_minus_t; G_t], (nx + m) x n (A_minus_N = 0)
+//   rv [T][B][rvp]    x q (stage t) | y = [y_f; y_g] | cz = [c; z] | xi l u
+//   dm [T][B][pitch]  D_t (packed; iterations that evaluate the residuals)
+// The constraint rows of a stage are stacked: row r < nx is dynamics row t,
+// row nx + j is inequality j, so lane r of a problem's group owns both the
+// row of M_t and the matching entries of y and cz, and one dot product with
+// M_t serves both kinds of constraint.
 // and stage_unpack_kernel writes the state back after the last iteration.
 //
 // Sweeps.  Every sweep over the stages runs in batches of DPF stages: the
@@ -25,8 +29,9 @@
 // overwrites w_{t+1} with the next iteration's gamma_{t+1}.  y_f0 and c0 stay
 // in registers; A0 stays in LDS.
 //
-// HBM traffic per iteration and problem: Theta^{-1} and A_minus twice (forward
-// and backward sweep), the rv record once, the written state once.
+// HBM traffic per iteration and problem: Theta^{-1} and M twice (forward and
+// backward sweep), the rv record once (D_t too when the residuals are due),
+// the written state once.
 #pragma once
 #include "admm_direct.hpp"
 
@@ -54,45 +59,48 @@ __host__ __device__ inline constexpr int up4(int x) { return (x + 3) & ~3; }
 
 // Stage-record geometry (elements of R).
 struct RecGeom {
-  int amp;                              // A_minus_t block pitch
-  int rvp;                              // rv record pitch
-  int g, x, q, z, yg, xi, l, u, yf, c;  // offsets inside an rv record
+  int amp;                      // M_t = [A_minus_t; G_t] block pitch
+  int rvp;                      // rv record pitch
+  int x, q, y, cz, xi, l, u;    // offsets inside an rv record
+  int yf, yg, c, z;             // y = [y_f; y_g], cz = [c; z]
 };
 
 __host__ __device__ inline RecGeom rec_geom(const Dims& d) {
   RecGeom r;
   const int n = d.n, m = d.m, nx = d.nx;
-  r.amp = up4(nx * n);
-  r.g = 0;
-  r.x = up4(m * n);
-  r.q = r.x + n;
-  r.z = r.q + n;
-  r.yg = r.z + m;
-  r.xi = r.yg + m;
+  r.amp = up4((nx + m) * n);
+  r.x = 0;
+  r.q = n;
+  r.y = 2 * n;
+  r.cz = r.y + nx + m;
+  r.xi = r.cz + nx + m;
   r.l = r.xi + m;
   r.u = r.l + m;
-  r.yf = r.u + m;
-  r.c = r.yf + nx;
-  r.rvp = up4(r.c + nx);
+  r.rvp = up4(r.u + m);
+  r.yf = r.y;
+  r.yg = r.y + nx;
+  r.c = r.cz;
+  r.z = r.cz + nx;
   return r;
 }
 
 // Compile-time caps of the streaming kernel (host checks, else the generic
-// kernel runs): nx <= n - 1, m <= kMaxStreamM.
+// kernel runs): nx <= n - 1, m <= kMaxStreamM, nx + m <= n (the stacked
+// constraint rows of a stage fit the problem's n lanes).
 constexpr int kMaxStreamM = 8;
 
 template <typename R, int NC, int P>
 struct StreamShape {
   static constexpr int W = Vec16<R>::W;
   static constexpr int PITCH = th_pitch(NC);
-  static constexpr int AMP_MAX = up4(NC * (NC - 1));
-  static constexpr int RVP_MAX = up4(kMaxStreamM * NC) + up4(2 * NC + 5 * kMaxStreamM + 2 * (NC - 1));
+  static constexpr int AMP_MAX = up4(NC * NC);
+  static constexpr int RVP_MAX = up4(4 * NC + 3 * kMaxStreamM);
   static constexpr int CH_TH = (P * PITCH / W + kWave - 1) / kWave;  // 16-byte chunks per lane
   static constexpr int CH_AM = (P * AMP_MAX / W + kWave - 1) / kWave;
   static constexpr int CH_RV = (P * RVP_MAX / W + kWave - 1) / kWave;
 };
 
-constexpr int kNV = 6;  // per-lane broadcast vectors in LDS
+constexpr int kNV = 8;  // per-lane broadcast vectors in LDS
 
 // LDS layout in elements of R (host and device agree).  The DPF Theta^{-1}
 // slots come first at a compile-time stride (P x pitch), so one set of
@@ -100,9 +108,10 @@ constexpr int kNV = 6;  // per-lane broadcast vectors in LDS
 // the LDS instructions.
 struct StreamLayout {
   int wg;   // [P][T][n]          w_t / gamma_t trajectory
-  int th;   // [DPF][P][pitch]    Theta_t^{-1} (D_t in the residual pass)
+  int th;   // [DPF][P][pitch]    Theta_t^{-1}
   int am;   // [DPF][P][amp]
   int rv;   // [DPF][P][rvp]
+  int dm;   // [DPF][P][pitch]    D_t (iterations that evaluate the residuals)
   int a0;   // [P][n0 n]
   int vec;  // [kNV][64]
   int total;
@@ -115,7 +124,8 @@ __host__ __device__ inline StreamLayout stream_layout(const Dims& d, int P, int 
   L.th = up4(P * d.T * d.n);
   L.am = L.th + DPF * P * th_pitch(d.n);
   L.rv = L.am + DPF * P * g.amp;
-  int end = L.rv + DPF * P * g.rvp;
+  L.dm = L.rv + DPF * P * g.rvp;
+  int end = L.dm + DPF * P * th_pitch(d.n);
   if (end < L.th + 12 * kWave) end = L.th + 12 * kWave;  // the residual reduction reuses the slots
   L.a0 = end;
   L.vec = up4(L.a0 + P * d.n0 * d.n);
@@ -150,18 +160,25 @@ __global__ __launch_bounds__(kWave) void stage_pack_kernel(Dims d, QPDev<R> qp, 
   const int B = d.B, T = d.T, N = d.N, n = d.n, nx = d.nx, m = d.m;
   const RecGeom g = rec_geom(d);
   const int pitch = th_pitch(n);
-  if (t < N) {
+  const size_t bt = (size_t)b * T + t;
+  {
     R* o = am + ((size_t)t * B + b) * g.amp;
-    const R* s = qp.Am + ((size_t)b * N + t) * nx * n;
-    for (int e = tid; e < g.amp; e += kWave) o[e] = e < nx * n ? s[e] : R(0);
+    const R* sa = qp.Am + ((size_t)b * N + t) * nx * n;
+    const R* sg = qp.G + bt * m * n;
+    for (int e = tid; e < g.amp; e += kWave) {
+      R v = R(0);
+      if (e < nx * n) {
+        if (t < N) v = sa[e];
+      } else if (e < (nx + m) * n) {
+        v = sg[e - nx * n];
+      }
+      o[e] = v;
+    }
   }
   R* o = rv + ((size_t)t * B + b) * g.rvp;
-  const size_t bt = (size_t)b * T + t;
   for (int e = tid; e < g.rvp; e += kWave) {
     R v = R(0);
-    if (e < m * n) {
-      v = qp.G[bt * m * n + e];
-    } else if (e >= g.x && e < g.x + n) {
+    if (e >= g.x && e < g.x + n) {
       v = st.x[bt * n + e - g.x];
     } else if (e >= g.q && e < g.q + n) {
       v = qp.q[bt * n + e - g.q];
@@ -348,11 +365,17 @@ __global__ __launch_bounds__(kWave, StreamOcc<R>::waves) void admm_stream_kernel
   R* sx = vec + 3 * kWave + base;
   R* sc = vec + 4 * kWave + base;
   R* sc0 = vec + 5 * kWave + base;
-  R* sz = sr;  // the inequality part of the next gamma (m <= n; sr is free then)
+  R* sy = vec + 6 * kWave + base;   // new stacked duals [y_f; y_g] (residuals)
+  R* sy0 = vec + 7 * kWave + base;  // new y_f0 (residuals)
+  R* sxn = su;  // the relaxed iterate for the residuals (su is free then)
+  const int nr = nx + m;            // stacked constraint rows of a stage
+  const bool dyn = i < nx, ineq = i >= nx && i < nr;
+  const int ji = ineq ? i - nx : 0;  // inequality index of an inequality row
   const R* a0p = lds + L.a0 + p * n0 * n;
   auto thS = [&](int j) { return lds + L.th + j * (P * PITCH); };
   auto amS = [&](int j) { return lds + L.am + j * (P * amp); };
   auto rvS = [&](int j) { return lds + L.rv + j * (P * rvp); };
+  auto dmS = [&](int j) { return lds + L.dm + j * (P * PITCH); };
   auto th_run = [&](int t) { return reinterpret_cast<const V*>(a.th + ((size_t)t * B + b0) * PITCH); };
   auto dm_run = [&](int t) { return reinterpret_cast<const V*>(a.dm + ((size_t)t * B + b0) * PITCH); };
   auto am_run = [&](int t) { return reinterpret_cast<const V*>(a.am + ((size_t)t * B + b0) * amp); };
@@ -396,7 +419,7 @@ __global__ __launch_bounds__(kWave, StreamOcc<R>::waves) void admm_stream_kernel
     run_sweep<1, GRegs>(
         T, true,
         [&](GRegs& r, int t) {
-          if (t < N) load_run<V, CH_AM>(r.am, am_run(t), nch_am);
+          load_run<V, CH_AM>(r.am, am_run(t), nch_am);
           load_run<V, CH_RV>(r.rv, rv_run(t), nch_rv);
         },
         [&](GRegs& r, int j) {
@@ -404,20 +427,17 @@ __global__ __launch_bounds__(kWave, StreamOcc<R>::waves) void admm_stream_kernel
           store_run<V, CH_RV>(r.rv, reinterpret_cast<V*>(rvS(j)), nch_rv);
         },
         [&](int j, int t) {
-          const R* am = amS(j) + p * amp;
+          const R* mt = amS(j) + p * amp;
           const R* rv = rvS(j) + p * rvp;
+          // stacked [rho_f c - y_f; rho z - y_g] (dynamics rows vanish at t = N)
           R sct = R(0);
-          if (t < N && i < nx) {
-            sct = rho_f * rv[rg.c + i] - rv[rg.yf + i];
-            sc[i] = sct;
-          }
-          if (i < m) sz[i] = rho * rv[rg.z + i] - rv[rg.yg + i];
+          if ((dyn && t < N) || ineq) sct = (dyn ? rho_f : rho) * rv[rg.cz + i] - rv[rg.y + i];
+          if (i < nr) sc[i] = sct;
           wsync();
           if (i < n) {
             R gv = sigma * rv[rg.x + i] - rv[rg.q + i];
-            if (t < N) gv += lcol<R, NC>(am, nx, i, sc);
+            gv += lcol<R, NC>(mt, nr, i, sc);
             if (t > 0 && i < nx) gv -= scp;  // A_plus_{t-1}^T = [-I; 0]
-            if (m) gv += lcol<R, NC>(rv + rg.g, m, i, sz);
             if (t == 0) gv += lcol<R, NC>(a0p, n0, i, sc0);
             wgp[t * n + i] = gv;
           }
@@ -467,61 +487,70 @@ __global__ __launch_bounds__(kWave, StreamOcc<R>::waves) void admm_stream_kernel
           });
     }
 
-    // ---- backward sweep fused with the ADMM updates and the next gamma -------
+    // ---- backward sweep fused with the ADMM updates, the next gamma and (on
+    // checking iterations) the residuals of the new iterate (admm.py:392-556)
+    const bool chk = mod_zero(iter, a.check_every);
+    R rp = 0, nCx = 0, nc = 0, nGx = 0, nz = 0, rd = 0, nPx = 0, nAty = 0, nq = 0, nxi = 0, nyg = 0;
     {
       struct BRegs {
-        V th[CH_TH], am[CH_AM], rv[CH_RV];
+        V th[CH_TH], am[CH_AM], rv[CH_RV], dm[CH_TH];
       };
-      R xn = R(0);  // xt_{t+1}[i]
-      R gp = R(0);  // gamma_{t+1}[i] awaiting its A_plus_t^T term
+      R xn = R(0);   // xt_{t+1}[i]
+      R xnn = R(0);  // relaxed x_{t+1}[i]
+      R gp = R(0);   // gamma_{t+1}[i] awaiting its A_plus_t^T term
+      // dual residual row t+1 awaiting its A_plus_t^T y_f_t term (i < nx):
+      // P x + q and the rest of C^T y + G^T y_g
+      R pq_p = R(0), aty_p = R(0);
       run_sweep<DPF, BRegs>(
           T, false,
           [&](BRegs& r, int t) {
             load_run<V, CH_TH>(r.th, th_run(t), nch_th);
-            if (t < N) load_run<V, CH_AM>(r.am, am_run(t), nch_am);
+            load_run<V, CH_AM>(r.am, am_run(t), nch_am);
             load_run<V, CH_RV>(r.rv, rv_run(t), nch_rv);
+            if (chk) load_run<V, CH_TH>(r.dm, dm_run(t), nch_th);
           },
           [&](BRegs& r, int j) {
             store_run<V, CH_TH>(r.th, reinterpret_cast<V*>(thS(j)), nch_th);
             store_run<V, CH_AM>(r.am, reinterpret_cast<V*>(amS(j)), nch_am);
             store_run<V, CH_RV>(r.rv, reinterpret_cast<V*>(rvS(j)), nch_rv);
+            if (chk) store_run<V, CH_TH>(r.dm, reinterpret_cast<V*>(dmS(j)), nch_th);
           },
           [&](int j, int t) {
             const R* th = thS(j) + p * PITCH;
-            const R* am = amS(j) + p * amp;
+            const R* mt = amS(j) + p * amp;  // [A_minus_t; G_t]
             const R* rv = rvS(j) + p * rvp;
-            const R* gm = rv + rg.g;
             R* rvg = a.rv + ((size_t)t * B + b0) * rvp + rv_lane;  // this problem's record in HBM
+            const bool drow = dyn && t < N;  // a live dynamics row
             const R wv = i < n ? wgp[t * n + i] : R(0);
             R xt = wv;
             R u = R(0);  // (A_plus_t xt_{t+1})[i] = -xt_{t+1}[i], i < nx
             if (t < N) {
-              u = i < nx ? -xn : R(0);
-              if (i < nx) su[i] = u;
+              u = dyn ? -xn : R(0);
+              if (dyn) su[i] = u;
               wsync();
-              if (i < n) ss[i] = rho_f * lcol<R, NC>(am, nx, i, su);
+              if (i < n) ss[i] = rho_f * lcol<R, NC>(mt, nx, i, su);
               wsync();
               if (i < n) xt = wv - lsym<R, NC>(th, i, ss);
             }
             if (i < n) sx[i] = xt;
             wsync();
-            // C and G products of the pre-relaxation iterate
-            R cx = R(0), cx0 = R(0), gx = R(0);
-            if (t < N && i < nx) cx = lrow<R, NC>(am, i, sx) + u;
+            // stacked C and G products of the pre-relaxation iterate
+            R mx = R(0), cx0 = R(0);
+            if (i < nr) mx = lrow<R, NC>(mt, i, sx);
             if (t == 0 && i < n0) cx0 = lrow<R, NC>(a0p, i, sx);
-            if (i < m) gx = lrow<R, NC>(gm, i, sx);
             // over-relaxation
             R xnew = R(0);
             if (i < n) {
               xnew = alpha * xt + one_m_alpha * rv[rg.x + i];
               if (commit) rvg[rg.x + i] = xnew;
             }
-            // box projection / slack and the inequality dual
-            R zeta = R(0);
-            if (i < m) {
-              const R zo = rv[rg.z + i], ygo = rv[rg.yg + i];
-              const R zt = alpha * gx + one_m_alpha * zo + ygo / rho;
-              const R proj = rmin(rmax(zt, rv[rg.l + i]), rv[rg.u + i]);
+            // constraint row i: the dual, the next gamma's entry, and (inequality
+            // rows) the box projection / slack
+            R tgt = R(0), y_r = R(0), z_r = R(0), xi_r = R(0);
+            if (ineq) {
+              const R zo = rv[rg.cz + i], ygo = rv[rg.y + i];
+              const R zt = alpha * mx + one_m_alpha * zo + ygo / rho;
+              const R proj = rmin(rmax(zt, rv[rg.l + ji]), rv[rg.u + ji]);
               R zn, xin;
               if (a.use_slack) {
                 const R frac = gs / (gs + rho);
@@ -531,22 +560,26 @@ __global__ __launch_bounds__(kWave, StreamOcc<R>::waves) void admm_stream_kernel
                 zn = proj;
                 xin = R(0);
               }
-              const R ygn = ygo + rho * (alpha * gx + one_m_alpha * zo - zn);
+              const R ygn = ygo + rho * (alpha * mx + one_m_alpha * zo - zn);
               if (commit) {
-                rvg[rg.z + i] = zn;
-                rvg[rg.xi + i] = xin;
-                rvg[rg.yg + i] = ygn;
+                rvg[rg.cz + i] = zn;
+                rvg[rg.xi + ji] = xin;
+                rvg[rg.y + i] = ygn;
               }
-              zeta = rho * zn - ygn;
+              tgt = rho * zn - ygn;
+              y_r = ygn;
+              z_r = zn;
+              xi_r = xin;
             }
-            // equality duals
-            R ct = R(0), ct0 = R(0);
-            if (t < N && i < nx) {
-              const R cv = rv[rg.c + i];
-              const R yf = rv[rg.yf + i] + rho_f * (alpha * cx + one_m_alpha * cv - cv);
-              if (commit) rvg[rg.yf + i] = yf;
-              ct = rho_f * cv - yf;
+            if (drow) {
+              const R cx = mx + u;
+              const R cv = rv[rg.cz + i];
+              const R yf = rv[rg.y + i] + rho_f * (alpha * cx + one_m_alpha * cv - cv);
+              if (commit) rvg[rg.y + i] = yf;
+              tgt = rho_f * cv - yf;
+              y_r = yf;
             }
+            R ct0 = R(0), yf0_r = R(0);
             if (t == 0 && i < n0) {
               const R yf = yf0v + rho_f * (alpha * cx0 + one_m_alpha * c0v - c0v);
               if (commit) {
@@ -554,102 +587,88 @@ __global__ __launch_bounds__(kWave, StreamOcc<R>::waves) void admm_stream_kernel
                 yf0v = yf;
               }
               ct0 = rho_f * c0v - yf;
+              yf0_r = yf;
             }
             // next iteration's gamma (valid while rho is unchanged)
-            if (i < nx) sc[i] = ct;
-            if (i < m) sz[i] = zeta;
+            if (i < nr) sc[i] = tgt;
             if (i < n0) sc0[i] = ct0;
+            if (chk) {
+              if (i < n) sxn[i] = xnew;
+              if (i < nr) sy[i] = y_r;
+              if (i < n0) sy0[i] = yf0_r;
+            }
             wsync();
             if (t < N) {
-              if (i < nx) gp -= ct;  // A_plus_t^T = [-I; 0]
+              if (dyn) gp -= tgt;  // A_plus_t^T = [-I; 0]
               if (i < n) wgp[(t + 1) * n + i] = gp;
             }
             if (i < n) {
               R gv = sigma * xnew - rv[rg.q + i];
-              if (t < N) gv += lcol<R, NC>(am, nx, i, sc);
-              if (m) gv += lcol<R, NC>(gm, m, i, sz);
+              gv += lcol<R, NC>(mt, nr, i, sc);
               if (t == 0) gv += lcol<R, NC>(a0p, n0, i, sc0);
               gp = gv;
             }
+            if (chk) {
+              // dual residual row t+1 is complete with -[y_f_t; 0]
+              if (drow) {
+                const R aty = aty_p - y_r;
+                rd = rmax(rd, rabs(pq_p + aty));
+                nAty = rmax(nAty, rabs(aty));
+              }
+              // stacked primal rows of the relaxed iterate
+              if (i < nr) {
+                const R m1 = lrow<R, NC>(mt, i, sxn);
+                if (drow) {  // A_minus_t x_t - x_{t+1} - c_t
+                  const R cx1 = m1 - xnn;
+                  const R cv = rv[rg.cz + i];
+                  rp = rmax(rp, rabs(cx1 - cv));
+                  nCx = rmax(nCx, rabs(cx1));
+                  nc = rmax(nc, rabs(cv));
+                }
+                if (ineq) {
+                  rp = rmax(rp, rabs(m1 - z_r));
+                  nGx = rmax(nGx, rabs(m1));
+                  nz = rmax(nz, rabs(z_r));
+                  if (slack) {
+                    rd = rmax(rd, rabs(gs * xi_r + y_r));
+                    nxi = rmax(nxi, rabs(xi_r));
+                    nyg = rmax(nyg, rabs(y_r));
+                  }
+                }
+              }
+              if (t == 0 && i < n0) {
+                const R cx1 = lrow<R, NC>(a0p, i, sxn);
+                rp = rmax(rp, rabs(cx1 - c0v));
+                nCx = rmax(nCx, rabs(cx1));
+                nc = rmax(nc, rabs(c0v));
+              }
+              if (i < n) {
+                const R px = lsym<R, NC>(dmS(j) + p * PITCH, i, sxn);
+                R aty = R(0);
+                if (t == 0) aty += lcol<R, NC>(a0p, n0, i, sy0);
+                aty += lcol<R, NC>(mt, nr, i, sy);  // A_minus_t^T y_f_t + G_t^T y_g_t
+                const R qv = rv[rg.q + i];
+                if (t > 0 && dyn) {  // awaits -y_f_{t-1}[i]
+                  pq_p = px + qv;
+                  aty_p = aty;
+                } else {
+                  rd = rmax(rd, rabs(px + qv + aty));
+                  nAty = rmax(nAty, rabs(aty));
+                }
+                nPx = rmax(nPx, rabs(px));
+                nq = rmax(nq, rabs(qv));
+              }
+            }
             xn = xt;
+            xnn = xnew;
             wsync();
           });
       if (i < n) wgp[i] = gp;
       wsync();
     }
 
-    // ---- residuals and adaptive rho (admm.py:392-556) ------------------------
-    if (mod_zero(iter, a.check_every)) {
-      struct RRegs {
-        V dm[CH_TH], am[CH_AM], rv[CH_RV];
-      };
-      R rp = 0, nCx = 0, nc = 0, nGx = 0, nz = 0, rd = 0, nPx = 0, nAty = 0, nq = 0, nxi = 0, nyg = 0;
-      R yprev = R(0);  // y_f_{t-1}[i]
-      R cxp = R(0);    // (A_minus_{t-1} x_{t-1})[i], awaiting A_plus_{t-1} x_t
-      R cvp = R(0);    // c_{t-1}[i]
-      if (i < n0) sc0[i] = yf0v;
-      run_sweep<1, RRegs>(
-          T, true,
-          [&](RRegs& r, int t) {
-            load_run<V, CH_TH>(r.dm, dm_run(t), nch_th);
-            if (t < N) load_run<V, CH_AM>(r.am, am_run(t), nch_am);
-            load_run<V, CH_RV>(r.rv, rv_run(t), nch_rv);
-          },
-          [&](RRegs& r, int j) {
-            store_run<V, CH_TH>(r.dm, reinterpret_cast<V*>(thS(j)), nch_th);
-            store_run<V, CH_AM>(r.am, reinterpret_cast<V*>(amS(j)), nch_am);
-            store_run<V, CH_RV>(r.rv, reinterpret_cast<V*>(rvS(j)), nch_rv);
-          },
-          [&](int j, int t) {
-            const R* dmt = thS(j) + p * PITCH;
-            const R* am = amS(j) + p * amp;
-            const R* rv = rvS(j) + p * rvp;
-            const R* xv = rv + rg.x;
-            if (t > 0 && i < nx) {  // dynamics row t-1: A_minus x_{t-1} - x_t - c_{t-1}
-              const R cx = cxp - xv[i];
-              rp = rmax(rp, rabs(cx - cvp));
-              nCx = rmax(nCx, rabs(cx));
-              nc = rmax(nc, rabs(cvp));
-            }
-            if (i < n) {
-              const R px = lsym<R, NC>(dmt, i, xv);
-              R aty = R(0);
-              if (t == 0) aty += lcol<R, NC>(a0p, n0, i, sc0);
-              if (t < N) aty += lcol<R, NC>(am, nx, i, rv + rg.yf);
-              if (t > 0 && i < nx) aty -= yprev;  // A_plus_{t-1}^T y_f_{t-1}
-              if (m) aty += lcol<R, NC>(rv + rg.g, m, i, rv + rg.yg);
-              const R qv = rv[rg.q + i];
-              rd = rmax(rd, rabs(px + qv + aty));
-              nPx = rmax(nPx, rabs(px));
-              nAty = rmax(nAty, rabs(aty));
-              nq = rmax(nq, rabs(qv));
-            }
-            if (t < N && i < nx) {
-              cxp = lrow<R, NC>(am, i, xv);
-              cvp = rv[rg.c + i];
-              yprev = rv[rg.yf + i];
-            }
-            if (t == 0 && i < n0) {
-              const R cx = lrow<R, NC>(a0p, i, xv);
-              rp = rmax(rp, rabs(cx - c0v));
-              nCx = rmax(nCx, rabs(cx));
-              nc = rmax(nc, rabs(c0v));
-            }
-            if (i < m) {
-              const R gx = lrow<R, NC>(rv + rg.g, i, xv);
-              const R zv = rv[rg.z + i], ygv = rv[rg.yg + i];
-              rp = rmax(rp, rabs(gx - zv));
-              nGx = rmax(nGx, rabs(gx));
-              nz = rmax(nz, rabs(zv));
-              if (slack) {
-                const R xiv = rv[rg.xi + i];
-                rd = rmax(rd, rabs(gs * xiv + ygv));
-                nxi = rmax(nxi, rabs(xiv));
-                nyg = rmax(nyg, rabs(ygv));
-              }
-            }
-            wsync();
-          });
+    // ---- residual reductions and adaptive rho (admm.py:392-556) --------------
+    if (chk) {
       // group max-reductions (the slot region is free now)
       R* red = lds + L.th;
       const R vals[11] = {rp, nCx, nc, nGx, nz, rd, nPx, nAty, nq, nxi, nyg};
@@ -724,11 +743,11 @@ __global__ __launch_bounds__(kWave, StreamOcc<R>::waves) void admm_stream_kernel
 
 // LDS of factor_std_kernel, in bytes: fp64 work area [P][n n] Theta_{t-1}^{-1}
 // and [P][n] pivot row, then the staged stage runs in the storage type R:
-// A_minus double-buffered [2][P][amp], the rv records [P][rvp] (G at offset
-// 0), D_t [P][pitch], A0 [P][n0 n].
+// M_t = [A_minus_t; G_t] double-buffered [2][P][amp], D_t [P][pitch],
+// A0 [P][n0 n].
 struct FactorLayout {
   int th, piv;          // fp64 offsets (elements)
-  int am, rv, dm, a0;   // R offsets (elements, from the start of the R region)
+  int am, dm, a0;       // R offsets (elements, from the start of the R region)
   size_t r_base;        // byte offset of the R region
   size_t bytes;
 };
@@ -743,23 +762,21 @@ __host__ __device__ inline FactorLayout factor_layout(const Dims& d, int P) {
   const int c_elems = L.piv + P * n;
   L.r_base = ((size_t)c_elems * sizeof(double) + 15) / 16 * 16;
   L.am = 0;
-  L.rv = 2 * P * g.amp;
-  L.dm = L.rv + P * g.rvp;
+  L.dm = 2 * P * g.amp;
   L.a0 = L.dm + P * th_pitch(n);
   L.bytes = L.r_base + (size_t)(L.a0 + P * d.n0 * n) * sizeof(R);
   return L;
 }
 
 template <typename R, int NC, int P>
-__global__ __launch_bounds__(kWave) void factor_std_kernel(Dims d, const R* __restrict__ am, const R* __restrict__ rv,
-                                                          const R* __restrict__ dm, const R* __restrict__ A0,
+__global__ __launch_bounds__(kWave) void factor_std_kernel(Dims d, const R* __restrict__ am, const R* __restrict__ dm, const R* __restrict__ A0,
                                                           const R* __restrict__ rho, R sigma, R rho_f_factor,
                                                           int32_t* __restrict__ ctl, R* __restrict__ thinv) {
   using C = double;
   using V = typename Vec16<R>::T;
   using K = StreamShape<R, NC, P>;
   constexpr int n = NC, PITCH = K::PITCH, W = K::W;
-  constexpr int CH_TH = K::CH_TH, CH_AM = K::CH_AM, CH_RV = K::CH_RV;
+  constexpr int CH_TH = K::CH_TH, CH_AM = K::CH_AM;
   extern __shared__ __align__(16) unsigned char smem_raw[];
   const Dims dd = d;
   const int T = dd.T, N = dd.N, nx = dd.nx, n0 = dd.n0, m = dd.m, B = dd.B;
@@ -772,10 +789,9 @@ __global__ __launch_bounds__(kWave) void factor_std_kernel(Dims d, const R* __re
   const int b0 = blockIdx.x * P, nprob = min(P, B - b0);
   if (ctl != nullptr && __ballot(G.real && ctl[b * 4 + 2] != 0) == 0) return;  // nothing flagged here
   const int n0n = n0 * n;
-  const int nch_am = nprob * rg.amp / W, nch_rv = nprob * rg.rvp / W, nch_dm = nprob * PITCH / W;
+  const int nch_am = nprob * rg.amp / W, nch_dm = nprob * PITCH / W;
   C* th = lds + FL.th + p * n * n;
   C* piv = lds + FL.piv + p * n;
-  const R* gm = ldr + FL.rv + p * rg.rvp + rg.g;
   const R* dmt = ldr + FL.dm + p * PITCH;
   const R* a0 = ldr + FL.a0 + p * n0n;
   for (int e = tid; e < nprob * n0n; e += kWave) ldr[FL.a0 + e] = A0[(size_t)b0 * n0n + e];
@@ -785,11 +801,10 @@ __global__ __launch_bounds__(kWave) void factor_std_kernel(Dims d, const R* __re
     return reinterpret_cast<const V*>(arr + ((size_t)t * B + b0) * pitch);
   };
   struct Regs {
-    V am[CH_AM], rv[CH_RV], dm[CH_TH];
+    V am[CH_AM], dm[CH_TH];
   } nxt;
   auto load = [&](int t) {
-    if (t < N) load_run<V, CH_AM>(nxt.am, run(am, rg.amp, t), nch_am);
-    load_run<V, CH_RV>(nxt.rv, run(rv, rg.rvp, t), nch_rv);
+    load_run<V, CH_AM>(nxt.am, run(am, rg.amp, t), nch_am);
     load_run<V, CH_TH>(nxt.dm, run(dm, PITCH, t), nch_dm);
   };
   load(0);
@@ -800,8 +815,7 @@ __global__ __launch_bounds__(kWave) void factor_std_kernel(Dims d, const R* __re
   C a[NC];  // row i of Theta_t, then of Theta_t^{-1}
   for (int t = 0; t < T; ++t) {
     const int cur = (t & 1) * (P * rg.amp), prv = ((t & 1) ^ 1) * (P * rg.amp);
-    if (t < N) store_run<V, CH_AM>(nxt.am, reinterpret_cast<V*>(ldr + FL.am + cur), nch_am);
-    store_run<V, CH_RV>(nxt.rv, reinterpret_cast<V*>(ldr + FL.rv), nch_rv);
+    store_run<V, CH_AM>(nxt.am, reinterpret_cast<V*>(ldr + FL.am + cur), nch_am);
     store_run<V, CH_TH>(nxt.dm, reinterpret_cast<V*>(ldr + FL.dm), nch_dm);
     wsync();
     if (t + 1 < T) load(t + 1);
@@ -811,7 +825,7 @@ __global__ __launch_bounds__(kWave) void factor_std_kernel(Dims d, const R* __re
       // theta_t row i.  Every loop body below issues its LDS reads, then a
       // scheduling barrier, then its FMAs, so the reads of a body share one
       // round trip.
-      C c[NC], g[NC];
+      C c[NC];
       {
         R dk[NC];
 #pragma unroll
@@ -821,13 +835,13 @@ __global__ __launch_bounds__(kWave) void factor_std_kernel(Dims d, const R* __re
         for (int k = 0; k < NC; ++k) {
           a[k] = (C)dk[k] + (k == i ? sig : C(0));
           c[k] = C(0);
-          g[k] = C(0);
         }
       }
-      // c += sum_r M[r][i] M[r][:] over the rows of an (rows x n) block, two rows per round trip
-      auto gram = [&](const R* M, int rows, C* acc) {
-        for (int r = 0; r < rows; r += 2) {
-          const bool two = r + 1 < rows;
+      // c += sum_r w_r M[r][i] M[r][:] over rows r0..r1-1 of an (rows x n)
+      // block, two rows per round trip; w_r = rho_f below row wsplit, rho from it
+      auto gram = [&](const R* M, int r0, int r1, int wsplit) {
+        for (int r = r0; r < r1; r += 2) {
+          const bool two = r + 1 < r1;
           R m0[NC], m1[NC];
           const R a0v = M[r * n + i];
           const R a1v = M[(two ? r + 1 : r) * n + i];
@@ -837,18 +851,18 @@ __global__ __launch_bounds__(kWave) void factor_std_kernel(Dims d, const R* __re
             m1[k] = M[(two ? r + 1 : r) * n + k];
           }
           __builtin_amdgcn_sched_barrier(0);
-          const C s0 = (C)a0v, s1 = two ? (C)a1v : C(0);
+          const C s0 = (C)a0v * (r < wsplit ? rho_f : rho_i);
+          const C s1 = two ? (C)a1v * (r + 1 < wsplit ? rho_f : rho_i) : C(0);
 #pragma unroll
-          for (int k = 0; k < NC; ++k) acc[k] += s0 * (C)m0[k] + s1 * (C)m1[k];
+          for (int k = 0; k < NC; ++k) c[k] += s0 * (C)m0[k] + s1 * (C)m1[k];
         }
       };
-      if (t == 0) gram(a0, n0, c);
-      if (t < N) gram(amc, nx, c);
-      if (m) gram(gm, m, g);
+      if (t == 0) gram(a0, 0, n0, n0);
+      gram(amc, t < N ? 0 : nx, nx + m, nx);  // [A_minus_t; G_t]
 #pragma unroll
       for (int k = 0; k < NC; ++k) {
-        if (t > 0 && k == i && i < nx) c[k] += C(1);  // A_plus_{t-1}^T A_plus_{t-1} = diag(I_nx, 0)
-        a[k] += rho_i * g[k] + rho_f * c[k];
+        if (t > 0 && k == i && i < nx) c[k] += rho_f;  // rho_f A_plus_{t-1}^T A_plus_{t-1} = rho_f diag(I_nx, 0)
+        a[k] += c[k];
       }
       // Schur update of the leading nx x nx block
       if (t > 0 && i < nx) {

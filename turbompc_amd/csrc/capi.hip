@@ -49,7 +49,7 @@ template <typename R>
 size_t stream_ws_bytes(const Dims& d) {
   const RecGeom g = rec_geom(d);
   const size_t B = d.B, T = d.T, N = d.N;
-  return align_up(N * B * g.amp * sizeof(R)) + align_up(T * B * g.rvp * sizeof(R)) +
+  return align_up(T * B * g.amp * sizeof(R)) + align_up(T * B * g.rvp * sizeof(R)) +
          align_up(T * B * th_pitch(d.n) * sizeof(R));
 }
 
@@ -78,7 +78,7 @@ DirectWs<R> carve_direct(void* ws, const Dims& d) {
   w.gam = c.take<R>(T * B * n);
   w.ctl = c.take<int32_t>(B * 4);
   w.res = c.take<R>(B * 8);
-  w.am = c.take<R>(N * B * g.amp);
+  w.am = c.take<R>(T * B * g.amp);
   w.rv = c.take<R>(T * B * g.rvp);
   w.dm = c.take<R>(T * B * th_pitch(d.n));
   return w;
@@ -183,7 +183,7 @@ inline int stream_problems_per_wave(int B, uint32_t flags) {
 template <typename R>
 bool stream_ok(const Dims& d, int P) {
   if (!(d.n == 6 || d.n == 9 || d.n == 16 || d.n == 17)) return false;
-  if (d.nx > d.n - 1 || d.m > d.n || d.m > kMaxStreamM) return false;
+  if (d.nx > d.n - 1 || d.nx + d.m > d.n || d.m > kMaxStreamM) return false;
   const StreamLayout L = stream_layout(d, P, kStreamDepth);
   return (size_t)L.total * sizeof(R) <= kMaxLds;
 }
@@ -223,7 +223,7 @@ void launch_factor_std_p(hipStream_t s, const Dims& d, const DirectWs<R>& w, con
   lds_optin(factor_std_kernel<R, NC, P>, smem);
   const int grid = (d.B + P - 1) / P;
   hipLaunchKernelGGL((factor_std_kernel<R, NC, P>), dim3(grid), dim3(kWave), smem, s, d, (const R*)w.am,
-                     (const R*)w.rv, (const R*)w.dm, q.A0, rho, sigma, rho_f_factor, ctl, w.thinv);
+                     (const R*)w.dm, q.A0, rho, sigma, rho_f_factor, ctl, w.thinv);
 }
 
 template <typename R, int NC>
