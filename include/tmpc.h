@@ -60,6 +60,11 @@ typedef struct tmpc_state {
  * from B). */
 #define TMPC_FLAG_GENERIC_KERNEL 2u
 #define TMPC_FLAG_STREAM_P(p) (((uint32_t)(p) & 3u) << 8)
+/* Every D_t is diagonal (quadratic costs with per-variable weights), vouched
+ * for by the caller.  The streaming kernel then keeps diag(D_t) in its stage
+ * records and forms the D_t x terms from it: the same products term by term
+ * (ignored by the other paths). */
+#define TMPC_FLAG_DIAG_COST 4u
 
 typedef struct tmpc_admm_cfg {
   int32_t max_iter, check_every, adapt_rho_every, pcg_max_iter, use_slack;

@@ -70,9 +70,9 @@ def blocks_to_dense(S):
     return A
 
 
-def random_qp(B, T, n, nx, m, *, seed=0, std=False, dtype=torch.float64, n0=None):
-    """Random well-posed QP batch: SPD-ish D, small E, random dynamics rows,
-    random G, boxes around zero."""
+def random_qp(B, T, n, nx, m, *, seed=0, std=False, dtype=torch.float64, n0=None, diag=False):
+    """Random well-posed QP batch: SPD-ish D (diagonal with diag=True), small
+    E, random dynamics rows, random G, boxes around zero."""
     from turbompc_amd.solvers.qp_data import QPCostBlocks, QPData, QPEqualityBlocks, QPInequalityBlocks
 
     rng = np.random.default_rng(seed)
@@ -94,6 +94,8 @@ def random_qp(B, T, n, nx, m, *, seed=0, std=False, dtype=torch.float64, n0=None
     zf = rng.standard_normal((B, T, n))
     c0 = np.einsum("bij,bj->bi", A0, zf[:, 0])
     c = np.einsum("btij,btj->bti", Am, zf[:, :-1]) + np.einsum("btij,btj->bti", Ap, zf[:, 1:])
+    if diag:
+        D = np.einsum("btij,ij->btij", D, np.eye(n))
     G = rng.standard_normal((B, T, m, n))
     gz = np.einsum("btij,btj->bti", G, zf)
     l = gz - rng.uniform(0.2, 1.0, size=(B, T, m))

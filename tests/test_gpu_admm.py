@@ -245,3 +245,52 @@ def test_admm_stream_kernel_matches_generic_on_bench_batch():
     assert torch.equal(s_a.num_iter, s_b.num_iter)
     for k in ("x_blocks", "y_f_dyn", "y_g", "z_g", "y_f_0"):
         assert rel_err(getattr(o_a, k), getattr(o_b, k)) < TOL[torch.float32], k
+
+
+@pytest.mark.parametrize("P", [1, 2, 3])
+@pytest.mark.parametrize("shape", [(13, 21, 6, 4, 2), (8, 11, 17, 13, 4), (7, 13, 9, 6, 3)])
+def test_admm_stream_kernel_structured_records_fp64_matches_oracle(P, shape):
+    # diagonal D_t declared to the kernel: it then streams diag(D_t)
+    B, T, n, nx, m = shape
+    qp = random_qp(B, T, n, nx, m, seed=61, std=True, diag=True)
+    cfg = oracle.OracleCfg(max_iter=20, check_every=3, adapt_rho_every=0, sigma=1e-6, eps_abs=1e-12,
+                           eps_rel=1e-12, rho_f_factor=1000.0, alpha=1.6)
+    ref, it_ref, _, out, stats = _run_pair(qp, cfg, torch.float64, kernel_flags=_lib.flag_stream_p(P),
+                                           diag_cost=True)
+    np.testing.assert_array_equal(stats.num_iter.cpu().numpy(), it_ref)
+    _assert_state_close(out, ref, 1e-9)
+
+
+@pytest.mark.parametrize("alpha", [1.0, 1.6])
+def test_admm_stream_kernel_structured_records_adaptive_rho(alpha):
+    # termination and rho adaptation read the residuals of the structured path
+    qp = random_qp(11, 9, 6, 4, 3, seed=42, std=True, diag=True)
+    cfg = oracle.OracleCfg(max_iter=200, check_every=2, adapt_rho_every=4, sigma=1e-6, eps_abs=1e-6, eps_rel=1e-6,
+                           rho_f_factor=50.0, alpha=alpha, adaptive_rho_tolerance=1.5)
+    ref, it_ref, _, out, stats = _run_pair(qp, cfg, torch.float64, kernel_flags=_lib.flag_stream_p(2),
+                                           diag_cost=True)
+    np.testing.assert_array_equal(stats.num_iter.cpu().numpy(), it_ref)
+    assert len(set(it_ref.tolist())) > 1
+    assert rel_err(out.rho_bar, ref.rho_bar) < 1e-7
+    _assert_state_close(out, ref, 1e-5)
+
+
+def test_admm_stream_kernel_structured_records_match_dense_on_bench_batch():
+    # the benchmark QP (quadrotor: diagonal weights) solved with the structure
+    # declared and with dense D_t records
+    B = 4099
+    prob = make_quadrotor_config(B=B, seed=7, dtype=torch.float32, device=DEV)
+    qp = prob.build_qp(*prob.initial_guess())
+    cfg = oracle.OracleCfg(max_iter=20, check_every=1, adapt_rho_every=0, sigma=1e-6, eps_abs=1e-9, eps_rel=1e-9,
+                           rho_f_factor=1000.0, alpha=1.6)
+    outs = []
+    for kw in ({}, {"diag_cost": True}):
+        solver = _solver(qp, cfg, **kw)
+        st0 = solver.initial_state(qp, rho_bar=0.1)
+        _, stats, out = solver.solve(qp, st0, alpha=cfg.alpha)
+        outs.append((stats, out))
+    torch.cuda.synchronize()
+    (s_a, o_a), (s_b, o_b) = outs
+    assert torch.equal(s_a.num_iter, s_b.num_iter)
+    for k in ("x_blocks", "y_f_dyn", "y_g", "z_g", "y_f_0"):
+        assert rel_err(getattr(o_a, k), getattr(o_b, k)) < 1e-5, k

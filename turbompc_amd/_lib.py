@@ -25,6 +25,7 @@ DEFAULT_LIB = _PKG / "lib" / "libtmpc_hip.so"
 
 FLAG_STD_DYNAMICS = 1
 FLAG_GENERIC_KERNEL = 2
+FLAG_DIAG_COST = 4  # every D_t diagonal
 
 
 def flag_stream_p(p: int) -> int:

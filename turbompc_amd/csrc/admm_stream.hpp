@@ -12,7 +12,8 @@
 //   th [T][B][pitch]  Theta_t^{-1} (packed, written by factor_std_kernel)
 //   am [T][B][amp]    M_t = [A_minus_t; G_t], (nx + m) x n (A_minus_N = 0)
 //   rv [T][B][rvp]    x q (stage t) | y = [y_f; y_g] | cz = [c; z] | xi l u
-//   dm [T][B][pitch]  D_t (packed; iterations that evaluate the residuals)
+//   dm [T][B][dmp]    D_t (packed, or its diagonal when the caller vouches that
+//                     every D_t is diagonal; iterations that evaluate the residuals)
 // The constraint rows of a stage are stacked: row r < nx is dynamics row t,
 // row nx + j is inequality j, so lane r of a problem's group owns both the
 // row of M_t and the matching entries of y and cz, and one dot product with
@@ -61,14 +62,19 @@ __host__ __device__ inline constexpr int up4(int x) { return (x + 3) & ~3; }
 struct RecGeom {
   int amp;                      // M_t = [A_minus_t; G_t] block pitch
   int rvp;                      // rv record pitch
+  int dmp;                      // D_t record pitch
+  bool diag;                    // D_t records hold the diagonal only
   int x, q, y, cz, xi, l, u;    // offsets inside an rv record
   int yf, yg, c, z;             // y = [y_f; y_g], cz = [c; z]
 };
 
-__host__ __device__ inline RecGeom rec_geom(const Dims& d) {
+// Without the flag: the larger (packed) D_t record, for workspace sizing.
+__host__ __device__ inline RecGeom rec_geom(const Dims& d, bool diag = false) {
   RecGeom r;
   const int n = d.n, m = d.m, nx = d.nx;
   r.amp = up4((nx + m) * n);
+  r.diag = diag;
+  r.dmp = diag ? up4(n) : th_pitch(n);
   r.x = 0;
   r.q = n;
   r.y = 2 * n;
@@ -117,15 +123,15 @@ struct StreamLayout {
   int total;
 };
 
-__host__ __device__ inline StreamLayout stream_layout(const Dims& d, int P, int DPF) {
-  const RecGeom g = rec_geom(d);
+__host__ __device__ inline StreamLayout stream_layout(const Dims& d, int P, int DPF, bool diag) {
+  const RecGeom g = rec_geom(d, diag);
   StreamLayout L;
   L.wg = 0;
   L.th = up4(P * d.T * d.n);
   L.am = L.th + DPF * P * th_pitch(d.n);
   L.rv = L.am + DPF * P * g.amp;
   L.dm = L.rv + DPF * P * g.rvp;
-  int end = L.dm + DPF * P * th_pitch(d.n);
+  int end = L.dm + DPF * P * g.dmp;
   if (end < L.th + 12 * kWave) end = L.th + 12 * kWave;  // the residual reduction reuses the slots
   L.a0 = end;
   L.vec = up4(L.a0 + P * d.n0 * d.n);
@@ -137,7 +143,7 @@ template <typename R>
 struct StreamArgs {
   Dims d;
   const R* th;  // [T][B][pitch]
-  const R* dm;  // [T][B][pitch]
+  const R* dm;  // [T][B][dmp]
   const R* am;  // [N][B][amp]
   R* rv;        // [T][B][rvp]
   const R *A0, *c0, *slack_w;
@@ -147,6 +153,7 @@ struct StreamArgs {
   uint32_t* iters_out;
   R sigma, alpha, rho_f_factor, eps_abs, eps_rel, rho_min, rho_max, rho_tol;
   int max_iter, check_every, adapt_every, use_slack;
+  int diag;  // D_t records hold the diagonal (RecGeom)
   int it_lo, it_hi, first_chunk;
 };
 
@@ -155,11 +162,10 @@ struct StreamArgs {
 // One 64-lane block per (problem, stage).
 template <typename R>
 __global__ __launch_bounds__(kWave) void stage_pack_kernel(Dims d, QPDev<R> qp, StateDev<R> st, R* __restrict__ am,
-                                                           R* __restrict__ rv, R* __restrict__ dm) {
+                                                           R* __restrict__ rv, R* __restrict__ dm, int diag) {
   const int b = blockIdx.x, t = blockIdx.y, tid = threadIdx.x;
   const int B = d.B, T = d.T, N = d.N, n = d.n, nx = d.nx, m = d.m;
-  const RecGeom g = rec_geom(d);
-  const int pitch = th_pitch(n);
+  const RecGeom g = rec_geom(d, diag != 0);
   const size_t bt = (size_t)b * T + t;
   {
     R* o = am + ((size_t)t * B + b) * g.amp;
@@ -199,12 +205,14 @@ __global__ __launch_bounds__(kWave) void stage_pack_kernel(Dims d, QPDev<R> qp, 
     }
     o[e] = v;
   }
-  // D_t packed lower (D is symmetric: the diagonal blocks of the QP Hessian)
-  R* od = dm + ((size_t)t * B + b) * pitch;
+  // D_t: the diagonal, or packed lower (D is symmetric)
+  R* od = dm + ((size_t)t * B + b) * g.dmp;
   const R* Dt = qp.D + bt * n * n;
-  for (int e = tid; e < pitch; e += kWave) {
+  for (int e = tid; e < g.dmp; e += kWave) {
     R v = R(0);
-    if (e < packed_size(n)) {
+    if (diag) {
+      if (e < n) v = Dt[e * n + e];
+    } else if (e < packed_size(n)) {
       int i = (int)((sqrtf(8.0f * e + 1.0f) - 1.0f) * 0.5f);
       while ((i + 1) * (i + 2) / 2 <= e) ++i;
       while (i * (i + 1) / 2 > e) --i;
@@ -346,14 +354,16 @@ __global__ __launch_bounds__(kWave, StreamOcc<R>::waves) void admm_stream_kernel
   R* lds = reinterpret_cast<R*>(smem_raw);
   const Dims d = a.d;
   const int T = d.T, N = d.N, nx = d.nx, n0 = d.n0, m = d.m, B = d.B;
-  const RecGeom rg = rec_geom(d);
-  const int amp = rg.amp, rvp = rg.rvp;
-  const StreamLayout L = stream_layout(d, P, DPF);
+  const bool diagD = a.diag != 0;
+  const RecGeom rg = rec_geom(d, diagD);
+  const int amp = rg.amp, rvp = rg.rvp, dmp = rg.dmp;
+  const StreamLayout L = stream_layout(d, P, DPF, diagD);
   const Group G = make_group_strided(n, P, B);
   const int b = G.prob, i = G.lane, p = G.gid, base = p * (kWave / P), tid = threadIdx.x;
   const int b0 = blockIdx.x * P;
   const int nprob = min(P, B - b0);
   const int nch_th = nprob * PITCH / W, nch_am = nprob * amp / W, nch_rv = nprob * rvp / W;
+  const int nch_dm = nprob * dmp / W;
   const unsigned pl = (unsigned)min(p, nprob - 1);
   const R alpha = a.alpha, one_m_alpha = R(1) - a.alpha, sigma = a.sigma;
 
@@ -375,9 +385,9 @@ __global__ __launch_bounds__(kWave, StreamOcc<R>::waves) void admm_stream_kernel
   auto thS = [&](int j) { return lds + L.th + j * (P * PITCH); };
   auto amS = [&](int j) { return lds + L.am + j * (P * amp); };
   auto rvS = [&](int j) { return lds + L.rv + j * (P * rvp); };
-  auto dmS = [&](int j) { return lds + L.dm + j * (P * PITCH); };
+  auto dmS = [&](int j) { return lds + L.dm + j * (P * dmp); };
   auto th_run = [&](int t) { return reinterpret_cast<const V*>(a.th + ((size_t)t * B + b0) * PITCH); };
-  auto dm_run = [&](int t) { return reinterpret_cast<const V*>(a.dm + ((size_t)t * B + b0) * PITCH); };
+  auto dm_run = [&](int t) { return reinterpret_cast<const V*>(a.dm + ((size_t)t * B + b0) * dmp); };
   auto am_run = [&](int t) { return reinterpret_cast<const V*>(a.am + ((size_t)t * B + b0) * amp); };
   auto rv_run = [&](int t) { return reinterpret_cast<const V*>(a.rv + ((size_t)t * B + b0) * rvp); };
   const unsigned rv_lane = pl * rvp;  // this lane's problem inside a stage run
@@ -507,13 +517,13 @@ __global__ __launch_bounds__(kWave, StreamOcc<R>::waves) void admm_stream_kernel
             load_run<V, CH_TH>(r.th, th_run(t), nch_th);
             load_run<V, CH_AM>(r.am, am_run(t), nch_am);
             load_run<V, CH_RV>(r.rv, rv_run(t), nch_rv);
-            if (chk) load_run<V, CH_TH>(r.dm, dm_run(t), nch_th);
+            if (chk) load_run<V, CH_TH>(r.dm, dm_run(t), nch_dm);
           },
           [&](BRegs& r, int j) {
             store_run<V, CH_TH>(r.th, reinterpret_cast<V*>(thS(j)), nch_th);
             store_run<V, CH_AM>(r.am, reinterpret_cast<V*>(amS(j)), nch_am);
             store_run<V, CH_RV>(r.rv, reinterpret_cast<V*>(rvS(j)), nch_rv);
-            if (chk) store_run<V, CH_TH>(r.dm, reinterpret_cast<V*>(dmS(j)), nch_th);
+            if (chk) store_run<V, CH_TH>(r.dm, reinterpret_cast<V*>(dmS(j)), nch_dm);
           },
           [&](int j, int t) {
             const R* th = thS(j) + p * PITCH;
@@ -643,7 +653,8 @@ __global__ __launch_bounds__(kWave, StreamOcc<R>::waves) void admm_stream_kernel
                 nc = rmax(nc, rabs(c0v));
               }
               if (i < n) {
-                const R px = lsym<R, NC>(dmS(j) + p * PITCH, i, sxn);
+                const R* dmt = dmS(j) + p * dmp;
+                const R px = diagD ? dmt[i] * xnew : lsym<R, NC>(dmt, i, sxn);
                 R aty = R(0);
                 if (t == 0) aty += lcol<R, NC>(a0p, n0, i, sy0);
                 aty += lcol<R, NC>(mt, nr, i, sy);  // A_minus_t^T y_f_t + G_t^T y_g_t
@@ -753,8 +764,8 @@ struct FactorLayout {
 };
 
 template <typename R>
-__host__ __device__ inline FactorLayout factor_layout(const Dims& d, int P) {
-  const RecGeom g = rec_geom(d);
+__host__ __device__ inline FactorLayout factor_layout(const Dims& d, int P, bool diag) {
+  const RecGeom g = rec_geom(d, diag);
   FactorLayout L;
   const int n = d.n;
   L.th = 0;
@@ -763,7 +774,7 @@ __host__ __device__ inline FactorLayout factor_layout(const Dims& d, int P) {
   L.r_base = ((size_t)c_elems * sizeof(double) + 15) / 16 * 16;
   L.am = 0;
   L.dm = 2 * P * g.amp;
-  L.a0 = L.dm + P * th_pitch(n);
+  L.a0 = L.dm + P * g.dmp;
   L.bytes = L.r_base + (size_t)(L.a0 + P * d.n0 * n) * sizeof(R);
   return L;
 }
@@ -771,7 +782,8 @@ __host__ __device__ inline FactorLayout factor_layout(const Dims& d, int P) {
 template <typename R, int NC, int P>
 __global__ __launch_bounds__(kWave) void factor_std_kernel(Dims d, const R* __restrict__ am, const R* __restrict__ dm, const R* __restrict__ A0,
                                                           const R* __restrict__ rho, R sigma, R rho_f_factor,
-                                                          int32_t* __restrict__ ctl, R* __restrict__ thinv) {
+                                                          int32_t* __restrict__ ctl, R* __restrict__ thinv,
+                                                          int diag) {
   using C = double;
   using V = typename Vec16<R>::T;
   using K = StreamShape<R, NC, P>;
@@ -780,8 +792,8 @@ __global__ __launch_bounds__(kWave) void factor_std_kernel(Dims d, const R* __re
   extern __shared__ __align__(16) unsigned char smem_raw[];
   const Dims dd = d;
   const int T = dd.T, N = dd.N, nx = dd.nx, n0 = dd.n0, m = dd.m, B = dd.B;
-  const RecGeom rg = rec_geom(dd);
-  const FactorLayout FL = factor_layout<R>(dd, P);
+  const RecGeom rg = rec_geom(dd, diag != 0);
+  const FactorLayout FL = factor_layout<R>(dd, P, diag != 0);
   C* lds = reinterpret_cast<C*>(smem_raw);
   R* ldr = reinterpret_cast<R*>(smem_raw + FL.r_base);
   const Group G = make_group_strided(n, P, B);
@@ -789,10 +801,10 @@ __global__ __launch_bounds__(kWave) void factor_std_kernel(Dims d, const R* __re
   const int b0 = blockIdx.x * P, nprob = min(P, B - b0);
   if (ctl != nullptr && __ballot(G.real && ctl[b * 4 + 2] != 0) == 0) return;  // nothing flagged here
   const int n0n = n0 * n;
-  const int nch_am = nprob * rg.amp / W, nch_dm = nprob * PITCH / W;
+  const int nch_am = nprob * rg.amp / W, nch_dm = nprob * rg.dmp / W;
   C* th = lds + FL.th + p * n * n;
   C* piv = lds + FL.piv + p * n;
-  const R* dmt = ldr + FL.dm + p * PITCH;
+  const R* dmt = ldr + FL.dm + p * rg.dmp;
   const R* a0 = ldr + FL.a0 + p * n0n;
   for (int e = tid; e < nprob * n0n; e += kWave) ldr[FL.a0 + e] = A0[(size_t)b0 * n0n + e];
   // stage runs of the next stage are loaded into registers while the current
@@ -805,7 +817,7 @@ __global__ __launch_bounds__(kWave) void factor_std_kernel(Dims d, const R* __re
   } nxt;
   auto load = [&](int t) {
     load_run<V, CH_AM>(nxt.am, run(am, rg.amp, t), nch_am);
-    load_run<V, CH_TH>(nxt.dm, run(dm, PITCH, t), nch_dm);
+    load_run<V, CH_TH>(nxt.dm, run(dm, rg.dmp, t), nch_dm);
   };
   load(0);
   const C rho_i = (C)rho[b];
@@ -828,8 +840,13 @@ __global__ __launch_bounds__(kWave) void factor_std_kernel(Dims d, const R* __re
       C c[NC];
       {
         R dk[NC];
+        if (diag) {
 #pragma unroll
-        for (int k = 0; k < NC; ++k) dk[k] = dmt[pidx(i, k)];
+          for (int k = 0; k < NC; ++k) dk[k] = k == i ? dmt[i] : R(0);
+        } else {
+#pragma unroll
+          for (int k = 0; k < NC; ++k) dk[k] = dmt[pidx(i, k)];
+        }
         __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
         for (int k = 0; k < NC; ++k) {

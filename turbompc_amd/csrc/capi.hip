@@ -181,16 +181,16 @@ inline int stream_problems_per_wave(int B, uint32_t flags) {
 }
 
 template <typename R>
-bool stream_ok(const Dims& d, int P) {
+bool stream_ok(const Dims& d, int P, bool diag) {
   if (!(d.n == 6 || d.n == 9 || d.n == 16 || d.n == 17)) return false;
   if (d.nx > d.n - 1 || d.nx + d.m > d.n || d.m > kMaxStreamM) return false;
-  const StreamLayout L = stream_layout(d, P, kStreamDepth);
+  const StreamLayout L = stream_layout(d, P, kStreamDepth, diag);
   return (size_t)L.total * sizeof(R) <= kMaxLds;
 }
 
 template <typename R, int NC, int P>
 void launch_stream_p(hipStream_t s, const StreamArgs<R>& a) {
-  const StreamLayout L = stream_layout(a.d, P, kStreamDepth);
+  const StreamLayout L = stream_layout(a.d, P, kStreamDepth, a.diag != 0);
   const size_t smem = (size_t)L.total * sizeof(R);
   lds_optin(admm_stream_kernel<R, NC, P, kStreamDepth>, smem);
   const int grid = (a.d.B + P - 1) / P;
@@ -218,41 +218,42 @@ void launch_stream(hipStream_t s, const StreamArgs<R>& a, int P) {
 
 template <typename R, int NC, int P>
 void launch_factor_std_p(hipStream_t s, const Dims& d, const DirectWs<R>& w, const QPDev<R>& q, const R* rho,
-                         R sigma, R rho_f_factor, int32_t* ctl) {
-  const size_t smem = factor_layout<R>(d, P).bytes;
+                         R sigma, R rho_f_factor, int32_t* ctl, bool diag) {
+  const size_t smem = factor_layout<R>(d, P, diag).bytes;
   lds_optin(factor_std_kernel<R, NC, P>, smem);
   const int grid = (d.B + P - 1) / P;
   hipLaunchKernelGGL((factor_std_kernel<R, NC, P>), dim3(grid), dim3(kWave), smem, s, d, (const R*)w.am,
-                     (const R*)w.dm, q.A0, rho, sigma, rho_f_factor, ctl, w.thinv);
+                     (const R*)w.dm, q.A0, rho, sigma, rho_f_factor, ctl, w.thinv, diag ? 1 : 0);
 }
 
 template <typename R, int NC>
 void launch_factor_std_nc(hipStream_t s, const Dims& d, const DirectWs<R>& w, const QPDev<R>& q, const R* rho,
-                          R sigma, R rho_f_factor, int32_t* ctl, int P) {
+                          R sigma, R rho_f_factor, int32_t* ctl, int P, bool diag) {
   switch (P) {
-    case 1: launch_factor_std_p<R, NC, 1>(s, d, w, q, rho, sigma, rho_f_factor, ctl); break;
-    case 2: launch_factor_std_p<R, NC, 2>(s, d, w, q, rho, sigma, rho_f_factor, ctl); break;
-    default: launch_factor_std_p<R, NC, 3>(s, d, w, q, rho, sigma, rho_f_factor, ctl); break;
+    case 1: launch_factor_std_p<R, NC, 1>(s, d, w, q, rho, sigma, rho_f_factor, ctl, diag); break;
+    case 2: launch_factor_std_p<R, NC, 2>(s, d, w, q, rho, sigma, rho_f_factor, ctl, diag); break;
+    default: launch_factor_std_p<R, NC, 3>(s, d, w, q, rho, sigma, rho_f_factor, ctl, diag); break;
   }
 }
 
 // fp64 factorization from the stage records (explicit-integrator structure)
 template <typename R>
 int launch_factor_std(hipStream_t s, const Dims& d, const DirectWs<R>& w, const QPDev<R>& q, const R* rho,
-                      R sigma, R rho_f_factor, int32_t* ctl, int P) {
+                      R sigma, R rho_f_factor, int32_t* ctl, int P, bool diag) {
   switch (d.n) {
-    case 6: launch_factor_std_nc<R, 6>(s, d, w, q, rho, sigma, rho_f_factor, ctl, P); break;
-    case 9: launch_factor_std_nc<R, 9>(s, d, w, q, rho, sigma, rho_f_factor, ctl, P); break;
-    case 16: launch_factor_std_nc<R, 16>(s, d, w, q, rho, sigma, rho_f_factor, ctl, P); break;
-    default: launch_factor_std_nc<R, 17>(s, d, w, q, rho, sigma, rho_f_factor, ctl, P); break;
+    case 6: launch_factor_std_nc<R, 6>(s, d, w, q, rho, sigma, rho_f_factor, ctl, P, diag); break;
+    case 9: launch_factor_std_nc<R, 9>(s, d, w, q, rho, sigma, rho_f_factor, ctl, P, diag); break;
+    case 16: launch_factor_std_nc<R, 16>(s, d, w, q, rho, sigma, rho_f_factor, ctl, P, diag); break;
+    default: launch_factor_std_nc<R, 17>(s, d, w, q, rho, sigma, rho_f_factor, ctl, P, diag); break;
   }
   return launch_status();
 }
 
 template <typename R>
-StreamArgs<R> stream_args(const AdmmArgs<R>& a, const DirectWs<R>& w) {
+StreamArgs<R> stream_args(const AdmmArgs<R>& a, const DirectWs<R>& w, bool diag) {
   StreamArgs<R> s;
   s.d = a.d;
+  s.diag = diag ? 1 : 0;
   s.th = w.thinv;
   s.dm = w.dm;
   s.am = w.am;
@@ -336,12 +337,14 @@ int admm_direct_impl(hipStream_t s, const tmpc_dims* dims, const tmpc_qp* qp,
   a.P = kWave / a.g;
   const bool std_dyn = (cfg->flags & TMPC_FLAG_STD_DYNAMICS) != 0;
   const int sp = stream_problems_per_wave(d.B, cfg->flags);
-  const bool stream = std_dyn && (cfg->flags & TMPC_FLAG_GENERIC_KERNEL) == 0 && stream_ok<R>(d, sp);
+  const bool diag = (cfg->flags & TMPC_FLAG_DIAG_COST) != 0;
+  const bool stream = std_dyn && (cfg->flags & TMPC_FLAG_GENERIC_KERNEL) == 0 && stream_ok<R>(d, sp, diag);
   if (stream) {
-    hipLaunchKernelGGL((stage_pack_kernel<R>), dim3(d.B, d.T), dim3(kWave), 0, s, d, a.qp, a.st, w.am, w.rv, w.dm);
+    hipLaunchKernelGGL((stage_pack_kernel<R>), dim3(d.B, d.T), dim3(kWave), 0, s, d, a.qp, a.st, w.am, w.rv, w.dm,
+                       diag ? 1 : 0);
     st = launch_status();
     if (st) return st;
-    st = launch_factor_std<R>(s, d, w, a.qp, a.st.rho, a.sigma, a.rho_f_factor, nullptr, sp);
+    st = launch_factor_std<R>(s, d, w, a.qp, a.st.rho, a.sigma, a.rho_f_factor, nullptr, sp, diag);
   } else {
     st = launch_factor_qp<R>(s, d, a.qp, a.st.rho, a.sigma, a.rho_f_factor, nullptr, w.thinv);
   }
@@ -350,7 +353,7 @@ int admm_direct_impl(hipStream_t s, const tmpc_dims* dims, const tmpc_qp* qp,
   if (g_iter_events[0] && hipEventRecord(g_iter_events[0], s) != hipSuccess) return TMPC_ELAUNCH;
   for (size_t c = 0; c + 1 < bounds.size(); ++c) {
     if (c > 0) {
-      st = stream ? launch_factor_std<R>(s, d, w, a.qp, a.st.rho, a.sigma, a.rho_f_factor, w.ctl, sp)
+      st = stream ? launch_factor_std<R>(s, d, w, a.qp, a.st.rho, a.sigma, a.rho_f_factor, w.ctl, sp, diag)
                   : launch_factor_qp<R>(s, d, a.qp, a.st.rho, a.sigma, a.rho_f_factor, w.ctl, w.thinv);
       if (st) return st;
     }
@@ -358,7 +361,7 @@ int admm_direct_impl(hipStream_t s, const tmpc_dims* dims, const tmpc_qp* qp,
     a.it_hi = bounds[c + 1];
     a.first_chunk = c == 0 ? 1 : 0;
     if (stream)
-      launch_stream<R>(s, stream_args<R>(a, w), sp);
+      launch_stream<R>(s, stream_args<R>(a, w, diag), sp);
     else if (std_dyn)
       launch_chunk<R, true>(s, a);
     else

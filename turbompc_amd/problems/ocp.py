@@ -72,6 +72,7 @@ class QuadraticTrackingOCP:
         self.num_inequality_constraints = int(self.state_mask.sum() + self.control_mask.sum())
         self.x_final_guess = cv(initial_guess_final_state) if initial_guess_final_state is not None else self.x0
         self.std_dynamics = True  # explicit integrators: A_plus = [-I 0], E = 0
+        self.diag_cost = True  # D_t = diag(2 w): per-variable tracking weights (cost_blocks)
         self._static = None
 
     # ------------------------------------------------------------ blocks ----

@@ -94,6 +94,7 @@ class ADMMSolver:
         use_slack: bool = False,
         std_dynamics: Optional[bool] = None,
         kernel_flags: int = 0,
+        diag_cost: bool = False,
     ):
         admm_backend = AdmmBackend(admm_backend)
         if admm_backend not in (AdmmBackend.HIP_DIRECT, AdmmBackend.HIP_PCG):
@@ -117,6 +118,8 @@ class ADMMSolver:
         self._zshape = zshape
         self._std_dynamics = std_dynamics
         self._kernel_flags = int(kernel_flags)  # _lib.FLAG_GENERIC_KERNEL / flag_stream_p (cross-checks)
+        if diag_cost:  # the caller vouches that every D_t is diagonal
+            self._kernel_flags |= _lib.FLAG_DIAG_COST
 
     # properties of the reference solver
     schur_solver = property(lambda self: self._schur_solver)

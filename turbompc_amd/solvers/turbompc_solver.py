@@ -224,6 +224,7 @@ class TurboMPCSolver:
             admm_backend=self._forward_admm_backend,
             use_slack=False,
             std_dynamics=getattr(program, "std_dynamics", None),
+            diag_cost=bool(getattr(program, "diag_cost", False)),
         )
 
     program = property(lambda self: self._program)
