@@ -115,9 +115,9 @@ constexpr int kNV = 8;  // per-lane broadcast vectors in LDS
 struct StreamLayout {
   int wg;   // [P][T][n]          w_t / gamma_t trajectory
   int th;   // [DPF][P][pitch]    Theta_t^{-1}
-  int am;   // [DPF][P][amp]
   int rv;   // [DPF][P][rvp]
-  int dm;   // [DPF][P][pitch]    D_t (iterations that evaluate the residuals)
+  int dm;   // [DPF][P][dmp]      D_t (iterations that evaluate the residuals)
+  int am;   // [DPF][P][amp]      (then n x n zeros)
   int a0;   // [P][n0 n]
   int vec;  // [kNV][64]
   int total;
@@ -128,12 +128,15 @@ __host__ __device__ inline StreamLayout stream_layout(const Dims& d, int P, int 
   StreamLayout L;
   L.wg = 0;
   L.th = up4(P * d.T * d.n);
-  L.am = L.th + DPF * P * th_pitch(d.n);
-  L.rv = L.am + DPF * P * g.amp;
+  L.rv = L.th + DPF * P * th_pitch(d.n);
   L.dm = L.rv + DPF * P * g.rvp;
-  int end = L.dm + DPF * P * g.dmp;
+  L.am = L.dm + DPF * P * g.dmp;
+  int end = L.am + DPF * P * g.amp;
   if (end < L.th + 12 * kWave) end = L.th + 12 * kWave;  // the residual reduction reuses the slots
-  L.a0 = end;
+  // n x n zeros: column products read all NC rows of a block, so the rows past
+  // the last stacked block land here (rows past other blocks land on the
+  // next block's data); every such row meets a zero vector entry
+  L.a0 = up4(end + d.n * d.n);
   L.vec = up4(L.a0 + P * d.n0 * d.n);
   L.total = L.vec + kNV * kWave;
   return L;
@@ -281,10 +284,12 @@ __device__ __forceinline__ R lrow(const R* A, int i, const R* v) {
   for (int k = 0; k < NC; ++k) acc += ak[k] * vk[k];
   return acc;
 }
-// Rows past `rows` are read (they stay inside the LDS allocation) but their
-// values are replaced by zero before any arithmetic.
+// All NC rows are read: the caller keeps v[r] = 0 for r >= rows and every
+// row read finite (LDS is zeroed at kernel start; rows past a block land on
+// finite data), so the rows past `rows` add exact zeros.
 template <typename R, int NC>
 __device__ __forceinline__ R lcol(const R* A, int rows, int i, const R* v) {
+  (void)rows;
   R ak[NC], vk[NC];
 #pragma unroll
   for (int r = 0; r < NC; ++r) {
@@ -294,7 +299,7 @@ __device__ __forceinline__ R lcol(const R* A, int rows, int i, const R* v) {
   __builtin_amdgcn_sched_barrier(0);
   R acc = R(0);
 #pragma unroll
-  for (int r = 0; r < NC; ++r) acc += (r < rows ? ak[r] : R(0)) * (r < rows ? vk[r] : R(0));
+  for (int r = 0; r < NC; ++r) acc += ak[r] * vk[r];
   return acc;
 }
 // Row i of a packed symmetric (lower) block times v.
@@ -392,7 +397,10 @@ __global__ __launch_bounds__(kWave, StreamOcc<R>::waves) void admm_stream_kernel
   auto rv_run = [&](int t) { return reinterpret_cast<const V*>(a.rv + ((size_t)t * B + b0) * rvp); };
   const unsigned rv_lane = pl * rvp;  // this lane's problem inside a stage run
 
-  // ---- resident data: A0 in LDS, c0 / y_f0 in registers ---------------------
+  // ---- LDS starts zeroed (the column products rely on finite data past the
+  // blocks); resident data: A0 in LDS, c0 / y_f0 in registers ---------------
+  for (int e = tid; e < L.total / W; e += kWave) reinterpret_cast<V*>(lds)[e] = V{};
+  wsync();
   for (int e = tid; e < nprob * n0 * n; e += kWave) lds[L.a0 + e] = a.A0[(size_t)b0 * n0 * n + e];
   const R c0v = (i < n0) ? a.c0[(size_t)b * n0 + i] : R(0);
   R yf0v = (i < n0) ? a.y_f0[(size_t)b * n0 + i] : R(0);
@@ -425,7 +433,7 @@ __global__ __launch_bounds__(kWave, StreamOcc<R>::waves) void admm_stream_kernel
     };
     const R rho_f = rho * a.rho_f_factor;
     R scp = R(0);
-    if (i < n0) sc0[i] = rho_f * c0v - yf0v;
+    if (i < NC) sc0[i] = rho_f * c0v - yf0v;  // 0 past n0
     run_sweep<1, GRegs>(
         T, true,
         [&](GRegs& r, int t) {
@@ -442,7 +450,7 @@ __global__ __launch_bounds__(kWave, StreamOcc<R>::waves) void admm_stream_kernel
           // stacked [rho_f c - y_f; rho z - y_g] (dynamics rows vanish at t = N)
           R sct = R(0);
           if ((dyn && t < N) || ineq) sct = (dyn ? rho_f : rho) * rv[rg.cz + i] - rv[rg.y + i];
-          if (i < nr) sc[i] = sct;
+          if (i < NC) sc[i] = sct;  // 0 past nr
           wsync();
           if (i < n) {
             R gv = sigma * rv[rg.x + i] - rv[rg.q + i];
@@ -536,7 +544,7 @@ __global__ __launch_bounds__(kWave, StreamOcc<R>::waves) void admm_stream_kernel
             R u = R(0);  // (A_plus_t xt_{t+1})[i] = -xt_{t+1}[i], i < nx
             if (t < N) {
               u = dyn ? -xn : R(0);
-              if (dyn) su[i] = u;
+              if (i < NC) su[i] = u;  // 0 past nx
               wsync();
               if (i < n) ss[i] = rho_f * lcol<R, NC>(mt, nx, i, su);
               wsync();
@@ -600,12 +608,12 @@ __global__ __launch_bounds__(kWave, StreamOcc<R>::waves) void admm_stream_kernel
               yf0_r = yf;
             }
             // next iteration's gamma (valid while rho is unchanged)
-            if (i < nr) sc[i] = tgt;
-            if (i < n0) sc0[i] = ct0;
+            if (i < NC) sc[i] = tgt;   // 0 past nr
+            if (i < NC) sc0[i] = ct0;  // 0 past n0
             if (chk) {
               if (i < n) sxn[i] = xnew;
-              if (i < nr) sy[i] = y_r;
-              if (i < n0) sy0[i] = yf0_r;
+              if (i < NC) sy[i] = y_r;     // 0 past nr
+              if (i < NC) sy0[i] = yf0_r;  // 0 past n0
             }
             wsync();
             if (t < N) {
