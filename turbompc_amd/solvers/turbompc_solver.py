@@ -311,7 +311,10 @@ class TurboMPCSolver:
                                              controls0=torch.zeros_like(controls))
         admm_state = admm_state0
         slacks = admm_state0.xi_g
-        z_prev = pack_z(states, controls)
+        # the SQP step is read only by the "step" criterion (and by a single
+        # iteration's convergence error)
+        need_step = self._convergence_criterion == "step" or max_iter == 1
+        z_prev = pack_z(states, controls) if need_step else None
         conv = torch.full((B,), float("inf"), dtype=dt, device=dev)
         admm_iters = torch.zeros((B, max_iter), dtype=torch.int32, device=dev)
         eq_v = torch.zeros((B, max_iter), dtype=dt, device=dev)
@@ -319,18 +322,22 @@ class TurboMPCSolver:
         conv_h = torch.zeros_like(eq_v)
         num_iter = torch.zeros(B, dtype=torch.int32, device=dev)
         active = torch.ones(B, dtype=torch.bool, device=dev)
-        kkt = None
+        g_c = None  # G x (+ slack) at each problem's last committed iterate
         for it in range(max_iter):
             if it >= 1:
                 active = active & (conv > tol)
                 if tol > 0 and not bool(active.any()):
                     break
+            # while no problem has stopped, committing is plain assignment (one
+            # host sync per SQP iteration instead of a masked select per tensor)
+            all_active = it == 0 or bool(active.all())
             (s_new, c_new), stats, adm_new = admm.solve(qp, admm_state, rho_bar=ap["rho"], alpha=alpha)
             sl_new = adm_new.xi_g
-            z_new = pack_z(s_new, c_new)
-            step = (z_new - z_prev).abs().amax(dim=1)
-            if sl_new.shape[-1] > 0:
-                step = step + (sl_new - slacks).abs().flatten(1).amax(dim=1)
+            if need_step:
+                z_new = pack_z(s_new, c_new)
+                step = (z_new - z_prev).abs().amax(dim=1)
+                if sl_new.shape[-1] > 0:
+                    step = step + (sl_new - slacks).abs().flatten(1).amax(dim=1)
             if self._convergence_criterion == "first_order" and it + 1 < max_iter:
                 qp_next = program.build_qp(s_new, c_new)
                 c_new_err, e_err, i_err, g = self._first_order_check(qp_next, s_new, c_new, sl_new, adm_new)
@@ -338,22 +345,39 @@ class TurboMPCSolver:
                 rebuild = self._convergence_criterion == "step" and it + 1 < max_iter
                 qp_next = program.build_qp(s_new, c_new) if rebuild else qp
                 c_new_err = step if (it == 0 or self._convergence_criterion == "step") else conv
-                e_err = torch.zeros_like(step)
-                i_err = torch.zeros_like(step)
+                e_err = torch.zeros_like(c_new_err)
+                i_err = torch.zeros_like(c_new_err)
                 g = apply_G(qp_next, pack_x(s_new, c_new))
-            kkt_new = self._build_kkt_state(s_new, c_new, adm_new, g, qp_next.ineq.l, qp_next.ineq.u)
             # commit where active (vmapped while_loop semantics)
-            sel = lambda a, b: _where(active, a, b)  # noqa: E731
-            states, controls, slacks, z_prev = sel(s_new, states), sel(c_new, controls), sel(sl_new, slacks), sel(z_new, z_prev)
+            if all_active:
+                sel = lambda a, b: a  # noqa: E731
+                qp = qp_next
+            else:
+                sel = lambda a, b: _where(active, a, b)  # noqa: E731
+                qp = _select_qp(active, qp_next, qp)
+            states, controls, slacks = sel(s_new, states), sel(c_new, controls), sel(sl_new, slacks)
+            if need_step:
+                z_prev = sel(z_new, z_prev)
             admm_state = ADMMState(*[sel(a, b) for a, b in zip(adm_new, admm_state)])
-            qp = _select_qp(active, qp_next, qp)
-            kkt = kkt_new if kkt is None else KKTState(*[sel(a, b) for a, b in zip(kkt_new, kkt)])
+            g_c = g if g_c is None else sel(g, g_c)
             conv = sel(c_new_err, conv)
-            admm_iters[:, it] = torch.where(active, stats.num_iter, admm_iters[:, it])
-            eq_v[:, it] = torch.where(active, e_err, eq_v[:, it])
-            in_v[:, it] = torch.where(active, i_err, in_v[:, it])
-            conv_h[:, it] = torch.where(active, c_new_err, conv_h[:, it])
-            num_iter = num_iter + active.to(torch.int32)
+            if all_active:
+                admm_iters[:, it] = stats.num_iter
+                eq_v[:, it] = e_err
+                in_v[:, it] = i_err
+                conv_h[:, it] = c_new_err
+                num_iter = num_iter + 1
+            else:
+                admm_iters[:, it] = torch.where(active, stats.num_iter, admm_iters[:, it])
+                eq_v[:, it] = torch.where(active, e_err, eq_v[:, it])
+                in_v[:, it] = torch.where(active, i_err, in_v[:, it])
+                conv_h[:, it] = torch.where(active, c_new_err, conv_h[:, it])
+                num_iter = num_iter + active.to(torch.int32)
+        # the KKT state of each problem's last committed iterate (a per-problem
+        # function of committed values, so it is formed once, after the loop)
+        kkt = None
+        if g_c is not None:
+            kkt = self._build_kkt_state(states, controls, admm_state, g_c, qp.ineq.l, qp.ineq.u)
         return TurboMPCSolution(
             states=states, controls=controls, slack=admm_state.xi_g, status=self.STATUS_SUCCESS, num_iter=num_iter,
             convergence_error=conv, admm_iters=admm_iters, linesearch_alphas=None, admm_state=admm_state,
