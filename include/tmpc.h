@@ -62,8 +62,9 @@ typedef struct tmpc_state {
 #define TMPC_FLAG_STREAM_P(p) (((uint32_t)(p) & 3u) << 8)
 /* Every D_t is diagonal (quadratic costs with per-variable weights), vouched
  * for by the caller.  The streaming kernel then keeps diag(D_t) in its stage
- * records and forms the D_t x terms from it: the same products term by term
- * (ignored by the other paths). */
+ * records and forms the D_t x terms from it, and the first-order check reads
+ * only the diagonal: the same products term by term (ignored by the other
+ * paths). */
 #define TMPC_FLAG_DIAG_COST 4u
 
 typedef struct tmpc_admm_cfg {
@@ -206,7 +207,8 @@ int tmpc_quadrotor_linearize_f64(hipStream_t stream, int32_t B, int32_t N, const
  * conv (B,) = max(stationarity, equality, inequality-violation, slack
  * stationarity) inf-norms; eq_err, ineq_err (B,) and g_out (B,T,m) = G x (+ slack)
  * may be NULL.  flags: TMPC_FLAG_STD_DYNAMICS asserts A_plus_t = [-I 0] and
- * E_t = 0, which are then not read. */
+ * E_t = 0, which are then not read; TMPC_FLAG_DIAG_COST asserts diagonal D_t
+ * (only the diagonal is read). */
 int tmpc_sqp_first_order_f32(hipStream_t stream, const tmpc_dims* dims, const tmpc_qp* qp, const float* x,
                              const float* y_f0, const float* y_f, const float* y_g, const float* slack,
                              double slack_weight, uint32_t flags, float* conv, float* eq_err, float* ineq_err, float* g_out);

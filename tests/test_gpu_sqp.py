@@ -103,14 +103,15 @@ def test_first_order_check_kernel_matches_torch(dtype):
 @pytest.mark.parametrize("std", [False, True])
 @pytest.mark.parametrize("dtype", [torch.float64, torch.float32])
 @pytest.mark.parametrize("use_slack", [False, True])
-def test_first_order_check_kernel_matches_dense_assembly(std, dtype, use_slack):
+@pytest.mark.parametrize("diag", [False, True])
+def test_first_order_check_kernel_matches_dense_assembly(std, dtype, use_slack, diag):
     """The check on random QPs (general E / A_plus, or the explicit-integrator
     structure read with std_dynamics=True) against dense P, C, G products."""
     from helpers import dense_C, dense_G, dense_P, np_qp, random_qp
     from turbompc_amd.solvers.sqp_hip import first_order_check
 
     B, T, n, nx, m = 5, 7, 9, 6, 11
-    qp = random_qp(B, T, n, nx, m, seed=11 + std, std=std)
+    qp = random_qp(B, T, n, nx, m, seed=11 + std, std=std, diag=diag)
     rng = np.random.default_rng(4)
     x, yg = rng.standard_normal((B, T, n)), rng.standard_normal((B, T, m))
     y0, yf = rng.standard_normal((B, nx)), rng.standard_normal((B, T - 1, nx))
@@ -118,7 +119,7 @@ def test_first_order_check_kernel_matches_dense_assembly(std, dtype, use_slack):
     w = 2.5
     dev = lambda a: torch.tensor(a, dtype=dtype, device="cuda")  # noqa: E731
     conv, eq, iq, g = first_order_check(qp.to("cuda", dtype), dev(x), dev(y0), dev(yf), dev(yg),
-                                        dev(sl) if use_slack else None, w, std_dynamics=std)
+                                        dev(sl) if use_slack else None, w, std_dynamics=std, diag_cost=diag)
     a = np_qp(qp)
     for b in range(B):
         P, C, Gd = dense_P(a["D"][b], a["E"][b]), dense_C(a["A0"][b], a["Am"][b], a["Ap"][b]), dense_G(a["G"][b])

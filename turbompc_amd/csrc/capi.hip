@@ -665,18 +665,18 @@ int quad_impl(hipStream_t s, int B, int N, const R* states, const R* controls, d
 
 // ------------------------------------------------------------- SQP check ----
 template <typename R, int NC>
-void launch_sqp_nc(hipStream_t s, const Dims& d, bool std_dyn, const QPDev<R>& q, const R* x, const R* y0,
-                   const R* yf, const R* yg, const R* sl, R sw, R* conv, R* eq, R* iq, R* gout) {
+void launch_sqp_nc(hipStream_t s, const Dims& d, bool std_dyn, int diag, const QPDev<R>& q, const R* x,
+                   const R* y0, const R* yf, const R* yg, const R* sl, R sw, R* conv, R* eq, R* iq, R* gout) {
   const dim3 grid(d.B * d.T);
   const size_t smem = check_smem_bytes<R>(d.n, d.nx, d.m);
   lds_optin(sqp_check_stage_kernel<R, NC, true>, smem);
   lds_optin(sqp_check_stage_kernel<R, NC, false>, smem);
   if (std_dyn)
     hipLaunchKernelGGL((sqp_check_stage_kernel<R, NC, true>), grid, dim3(kWave), smem, s, d, q, x, y0, yf, yg, sl, sw,
-                       conv, eq, iq, gout);
+                       conv, eq, iq, gout, diag);
   else
     hipLaunchKernelGGL((sqp_check_stage_kernel<R, NC, false>), grid, dim3(kWave), smem, s, d, q, x, y0, yf, yg, sl, sw,
-                       conv, eq, iq, gout);
+                       conv, eq, iq, gout, diag);
 }
 
 template <typename R>
@@ -689,12 +689,13 @@ int sqp_check_impl(hipStream_t s, const tmpc_dims* dims, const tmpc_qp* qp, cons
   const QPDev<R> q = to_qp<R>(qp);
   hipLaunchKernelGGL((sqp_check_init_kernel<R>), dim3((d.B + 255) / 256), dim3(256), 0, s, d.B, conv, eq, iq);
   const bool std_dyn = flags & TMPC_FLAG_STD_DYNAMICS;
+  const int diag = (flags & TMPC_FLAG_DIAG_COST) ? 1 : 0;
   switch (d.n) {
-    case 6: launch_sqp_nc<R, 6>(s, d, std_dyn, q, x, y0, yf, yg, slack, (R)slack_w, conv, eq, iq, gout); break;
-    case 9: launch_sqp_nc<R, 9>(s, d, std_dyn, q, x, y0, yf, yg, slack, (R)slack_w, conv, eq, iq, gout); break;
-    case 16: launch_sqp_nc<R, 16>(s, d, std_dyn, q, x, y0, yf, yg, slack, (R)slack_w, conv, eq, iq, gout); break;
-    case 17: launch_sqp_nc<R, 17>(s, d, std_dyn, q, x, y0, yf, yg, slack, (R)slack_w, conv, eq, iq, gout); break;
-    default: launch_sqp_nc<R, 0>(s, d, std_dyn, q, x, y0, yf, yg, slack, (R)slack_w, conv, eq, iq, gout); break;
+    case 6: launch_sqp_nc<R, 6>(s, d, std_dyn, diag, q, x, y0, yf, yg, slack, (R)slack_w, conv, eq, iq, gout); break;
+    case 9: launch_sqp_nc<R, 9>(s, d, std_dyn, diag, q, x, y0, yf, yg, slack, (R)slack_w, conv, eq, iq, gout); break;
+    case 16: launch_sqp_nc<R, 16>(s, d, std_dyn, diag, q, x, y0, yf, yg, slack, (R)slack_w, conv, eq, iq, gout); break;
+    case 17: launch_sqp_nc<R, 17>(s, d, std_dyn, diag, q, x, y0, yf, yg, slack, (R)slack_w, conv, eq, iq, gout); break;
+    default: launch_sqp_nc<R, 0>(s, d, std_dyn, diag, q, x, y0, yf, yg, slack, (R)slack_w, conv, eq, iq, gout); break;
   }
   return launch_status();
 }

@@ -147,7 +147,8 @@ __global__ __launch_bounds__(kWave) void sqp_check_stage_kernel(Dims d, QPDev<R>
                                                               const R* __restrict__ y0, const R* __restrict__ yf,
                                                               const R* __restrict__ yg, const R* __restrict__ slack,
                                                               R slack_w, R* __restrict__ conv, R* __restrict__ eq_err,
-                                                              R* __restrict__ ineq_err, R* __restrict__ gout) {
+                                                              R* __restrict__ ineq_err, R* __restrict__ gout,
+                                                              int diag) {
   extern __shared__ __align__(16) unsigned char check_smem[];
   R* sD = reinterpret_cast<R*>(check_smem);
   const int T = d.T, b = blockIdx.x / T, t = blockIdx.x - b * T, i = threadIdx.x;
@@ -174,9 +175,10 @@ __global__ __launch_bounds__(kWave) void sqp_check_stage_kernel(Dims d, QPDev<R>
   const R lv = i < m ? qp.l[bt * m + i] : R(0);
   const R uv = i < m ? qp.u[bt * m + i] : R(0);
   const R slv = slack && i < m ? slack[bt * m + i] : R(0);
+  const R dii = diag && i < n ? qp.D[bt * n * n + (size_t)i * (n + 1)] : R(0);  // diagonal D_t
   StageBlock<R, KB> bD, bA;
   StageBlock<R, KG> bG;
-  bD.get(qp.D + bt * n * n, n * n);
+  bD.get(qp.D + bt * n * n, diag ? 0 : n * n);
   bA.get(qp.Am + (bn + (has_next ? t : 0)) * nx * n, has_next ? nx * n : 0);
   bG.get(qp.G + bt * m * n, m * n);
   __builtin_amdgcn_sched_barrier(0);
@@ -189,7 +191,7 @@ __global__ __launch_bounds__(kWave) void sqp_check_stage_kernel(Dims d, QPDev<R>
   // height are computed on row 0 and dropped, so every lane reaches every
   // broadcast.
   const int in = i < n ? i : 0, ix = i < nx ? i : 0, im = i < m ? i : 0, i0 = i < n0 ? i : 0;
-  R px = row_bdot<R, NC>(sD, in, ld, n, xt);
+  R px = diag ? dii * xt : row_bdot<R, NC>(sD, in, ld, n, xt);
   R aty = m ? col_bdot(sG, in, ld, m, ygv) : R(0);
   if (has_next) aty += col_bdot(sAm, in, ld, nx, yc);
   if (STD) {

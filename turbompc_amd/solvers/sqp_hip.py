@@ -5,7 +5,8 @@ first_order_check: _compute_first_order_convergence_error
 kernel launch over every (problem, stage) pair, returning
 (conv, eq_err, ineq_err, g) with g = G x (+ slack).  std_dynamics=True asserts
 A_plus_t = [-I 0] and E_t = 0 (explicit integrators), which the kernel then
-does not read; None or False evaluates the general blocks.
+does not read; None or False evaluates the general blocks.  diag_cost=True
+asserts diagonal D_t (only the diagonal is read).
 """
 from __future__ import annotations
 
@@ -21,7 +22,7 @@ from .qp_data import QPData
 
 def first_order_check(qp: QPData, x: torch.Tensor, y_f0: torch.Tensor, y_f: torch.Tensor, y_g: torch.Tensor,
                       slack: Optional[torch.Tensor] = None, slack_weight: float = 0.0,
-                      std_dynamics: Optional[bool] = None):
+                      std_dynamics: Optional[bool] = None, diag_cost: bool = False):
     lib = _lib.load()
     B, T, n, nx, n0, m = qp.dims
     dt, dev = qp.dtype, qp.device
@@ -37,7 +38,7 @@ def first_order_check(qp: QPData, x: torch.Tensor, y_f0: torch.Tensor, y_f: torc
     st = getattr(lib, f"tmpc_sqp_first_order_{sfx}")(
         _lib.stream_handle(dev), ctypes.byref(dims), ctypes.byref(cq), _lib.ptr(x), _lib.ptr(y_f0), _lib.ptr(y_f),
         _lib.ptr(y_g), _lib.ptr(slack), float(slack_weight),
-        _lib.FLAG_STD_DYNAMICS if std_dynamics else 0, _lib.ptr(conv), _lib.ptr(eq), _lib.ptr(iq), _lib.ptr(g),
+        (_lib.FLAG_STD_DYNAMICS if std_dynamics else 0) | (_lib.FLAG_DIAG_COST if diag_cost else 0), _lib.ptr(conv), _lib.ptr(eq), _lib.ptr(iq), _lib.ptr(g),
     )
     _lib.check(f"tmpc_sqp_first_order_{sfx}", st)
     del keep

@@ -262,7 +262,8 @@ class TurboMPCSolver:
         use_slack = bool(qp.ineq.use_slack_variables) and qp.dims[5] > 0
         return first_order_check(qp, x, admm_state.y_f_0, admm_state.y_f_dyn, admm_state.y_g,
                                  slacks if use_slack else None, float(qp.ineq.slack_penalization_weight),
-                                 std_dynamics=getattr(self._program, "std_dynamics", None))
+                                 std_dynamics=getattr(self._program, "std_dynamics", None),
+                                 diag_cost=bool(getattr(self._program, "diag_cost", False)))
 
     def _first_order_check_torch(self, qp: QPData, states, controls, slacks, admm_state: ADMMState):
         """Same check with torch operators; kept for validating the kernel."""
