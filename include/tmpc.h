@@ -199,6 +199,19 @@ int tmpc_quadrotor_linearize_f64(hipStream_t stream, int32_t B, int32_t N, const
                                  const double* controls, double dt, const double* params,
                                  double* A_minus, double* c);
 
+/* Lagrangian Hessian of the same dynamics rows for the exact-Hessian backward
+ * pass: replaces get_dynamics_lagrangian_hessian for explicit schemes
+ * (turbompc/problems/optimal_control_problem.py:1334-1441), called from
+ * _augment_D_with_dynamics_hessian (turbompc/solvers/turbompc_solver.py:1323-1349).
+ * lambdas (B,N,13) are the dynamics multipliers y_f_dyn; H (B,N+1,17,17) gets
+ * H_t = d^2/dz_t^2 [lambda_t . f(z_t)] for t < N and zeros at t = N. */
+int tmpc_quadrotor_lagrangian_hessian_f32(hipStream_t stream, int32_t B, int32_t N, const float* states,
+                                          const float* controls, double dt, const double* params,
+                                          const float* lambdas, float* H);
+int tmpc_quadrotor_lagrangian_hessian_f64(hipStream_t stream, int32_t B, int32_t N, const double* states,
+                                          const double* controls, double dt, const double* params,
+                                          const double* lambdas, double* H);
+
 /* ---- SQP first-order convergence check ------------------------------------
  * Replaces _compute_first_order_convergence_error
  * (turbompc/solvers/turbompc_solver.py:1158-1225), evaluated in XLA by the

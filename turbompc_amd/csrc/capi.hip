@@ -662,6 +662,22 @@ int quad_impl(hipStream_t s, int B, int N, const R* states, const R* controls, d
   return launch_status();
 }
 
+template <typename R>
+int quad_hess_impl(hipStream_t s, int B, int N, const R* states, const R* controls, double dt,
+                   const double* params, const R* lambdas, R* H) {
+  if (B < 1 || N < 1) return TMPC_EBADSHAPE;
+  if (!states || !controls || !params || !lambdas || !H) return TMPC_EBADARG;
+  QuadParams<R> P{(R)params[0], (R)params[1], (R)params[2], (R)params[3],
+                  (R)params[4], (R)params[5], (R)params[6]};
+  const long long total = (long long)B * (N + 1) * (17 * 18 / 2);
+  const int blk = 256;
+  const long long grid = (total + blk - 1) / blk;
+  if (grid > INT32_MAX) return TMPC_EBADSHAPE;
+  hipLaunchKernelGGL((quad_lag_hessian_kernel<R>), dim3((unsigned)grid), dim3(blk), 0, s, B, N, states, controls,
+                     (R)dt, P, lambdas, H);
+  return launch_status();
+}
+
 
 // ------------------------------------------------------------- SQP check ----
 template <typename R, int NC>
@@ -831,6 +847,17 @@ int tmpc_quadrotor_linearize_f64(hipStream_t s, int32_t B, int32_t N, const doub
                                  const double* controls, double dt, const double* params, double* A_minus,
                                  double* c) {
   return quad_impl<double>(s, B, N, states, controls, dt, params, A_minus, c);
+}
+
+int tmpc_quadrotor_lagrangian_hessian_f32(hipStream_t s, int32_t B, int32_t N, const float* states,
+                                          const float* controls, double dt, const double* params,
+                                          const float* lambdas, float* H) {
+  return quad_hess_impl<float>(s, B, N, states, controls, dt, params, lambdas, H);
+}
+int tmpc_quadrotor_lagrangian_hessian_f64(hipStream_t s, int32_t B, int32_t N, const double* states,
+                                          const double* controls, double dt, const double* params,
+                                          const double* lambdas, double* H) {
+  return quad_hess_impl<double>(s, B, N, states, controls, dt, params, lambdas, H);
 }
 
 int tmpc_sqp_first_order_f32(hipStream_t s, const tmpc_dims* dims, const tmpc_qp* qp, const float* x,

@@ -118,6 +118,71 @@ class QuadraticTrackingOCP:
         """A_minus (B,N,nx,n), c (B,N,nx) linearized at (states, controls)."""
         raise NotImplementedError
 
+    def dynamics_lagrangian_hessian(self, states: torch.Tensor, controls: torch.Tensor, lambdas: torch.Tensor):
+        """(B,T,n,n) blocks d^2/dz_t^2 [lambda_t . f(z_t)] (zero at t = N), or None
+        when the dynamics are linear (get_dynamics_lagrangian_hessian,
+        optimal_control_problem.py:1334-1441)."""
+        raise NotImplementedError
+
+    # -------------------------------------------------------- parameters ----
+    WEIGHT_KEYS = (
+        "weights_penalization_reference_state_trajectory",
+        "weights_penalization_control_squared",
+        "weights_penalization_final_state",
+    )
+
+    def with_weights(self, weights: Optional[Dict[str, torch.Tensor]]) -> "QuadraticTrackingOCP":
+        """Copy with the tracking weights of `weights` (keys of weights_dict; missing
+        keys keep their value), as make_params_with_weights does for the
+        reference's solve(..., weights)."""
+        import copy
+
+        if not weights:
+            return self
+        unknown = set(weights) - set(self.WEIGHT_KEYS)
+        if unknown:
+            raise KeyError(f"unknown weight keys {sorted(unknown)}; expected {self.WEIGHT_KEYS}")
+        other = copy.copy(self)
+        cv = lambda t, ref: torch.as_tensor(t).to(device=self.device, dtype=self.dtype).expand_as(ref).contiguous()  # noqa: E731
+        k = self.WEIGHT_KEYS
+        if k[0] in weights:
+            other.wx = cv(weights[k[0]], self.wx)
+        if k[1] in weights:
+            other.wu = cv(weights[k[1]], self.wu)
+        if k[2] in weights:
+            other.wf = cv(weights[k[2]], self.wf)
+        other._static = None
+        return other
+
+    def with_params(self, problem_params: Optional[Dict[str, torch.Tensor]]) -> "QuadraticTrackingOCP":
+        """Copy with the entries of problem_params that this problem carries
+        ("initial_state": (B, nx)); others are ignored."""
+        import copy
+
+        if not problem_params or "initial_state" not in problem_params:
+            return self
+        other = copy.copy(self)
+        other.x0 = torch.as_tensor(problem_params["initial_state"]).to(
+            device=self.device, dtype=self.dtype).expand_as(self.x0).contiguous()
+        other._static = None
+        return other
+
+    def weight_gradient(self, states, controls, dx_states, dx_controls) -> Dict[str, torch.Tensor]:
+        """dL/dtheta for the tracking weights given the adjoint step dz
+        (_assemble_parameter_gradient, turbompc_solver.py:930-966): the cost
+        gradient sum_t 2 w (z_t - zref_t) gives d/dw grad = 2 (z_t - zref_t) per
+        variable, and neither the dynamics nor the bounds depend on the
+        weights, so dL/dw = -sum_t 2 (z_t - zref_t) dz_t (the final-state weight
+        only at t = N)."""
+        uref = self.u_ref if self.penalize_control_reference else torch.zeros_like(self.u_ref)
+        ex = states - self.x_ref
+        eu = controls - uref
+        return {
+            self.WEIGHT_KEYS[0]: -2.0 * (ex * dx_states).sum(dim=1),
+            self.WEIGHT_KEYS[1]: -2.0 * (eu * dx_controls).sum(dim=1),
+            self.WEIGHT_KEYS[2]: -2.0 * ex[:, -1] * dx_states[:, -1],
+        }
+
     def build_qp(self, states: torch.Tensor, controls: torch.Tensor) -> QPData:
         """QP of one SQP iteration (TurboMPCSolver._build_qp_data, turbompc_solver.py:1098-1156)."""
         if self._static is None:
@@ -175,6 +240,9 @@ class LinearOCP(QuadraticTrackingOCP):
         self.Bm = torch.as_tensor(Bm).to(self.device, self.dtype)
         self.b = (torch.as_tensor(b).to(self.device, self.dtype) if b is not None
                   else torch.zeros((self.B, self.num_state_variables), dtype=self.dtype, device=self.device))
+
+    def dynamics_lagrangian_hessian(self, states, controls, lambdas):
+        return None  # linear dynamics
 
     def dynamics_blocks(self, states, controls):
         N = self.horizon

@@ -54,6 +54,25 @@ class QuadrotorOCP(QuadraticTrackingOCP):
         _lib.check(f"tmpc_quadrotor_linearize_{sfx}", st)
         return Am, c
 
+    def dynamics_lagrangian_hessian(self, states, controls, lambdas):
+        """(B, N+1, 17, 17): d^2/dz_t^2 [lambda_t . f(z_t)] for t < N, zero at N
+        (tmpc_quadrotor_lagrangian_hessian_*, hyper-dual numbers on the device)."""
+        if not states.is_cuda:
+            raise ValueError("QuadrotorOCP Hessians run on the GPU; pass device tensors")
+        lib = _lib.load()
+        B, N = self.B, self.horizon
+        states = states.to(self.dtype).contiguous()
+        controls = controls.to(self.dtype).contiguous()
+        lambdas = lambdas.to(self.dtype).contiguous()
+        H = torch.empty((B, N + 1, 17, 17), dtype=self.dtype, device=states.device)
+        sfx = _lib.suffix(self.dtype)
+        st = getattr(lib, f"tmpc_quadrotor_lagrangian_hessian_{sfx}")(
+            _lib.stream_handle(states.device), B, N, _lib.ptr(states), _lib.ptr(controls), self.dt,
+            self._cparams, _lib.ptr(lambdas), _lib.ptr(H),
+        )
+        _lib.check(f"tmpc_quadrotor_lagrangian_hessian_{sfx}", st)
+        return H
+
 
 def quaternion_from_rotvec(r: torch.Tensor) -> torch.Tensor:
     """(..., 3) rotation vectors -> (..., 4) unit quaternions (w, x, y, z)."""

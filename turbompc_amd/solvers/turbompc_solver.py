@@ -29,6 +29,8 @@ from .linear_systems_solvers.backends import AdmmBackend, SchurSolverBackend
 from .qp_data import QPData
 from .qp_ops import apply_C_parts, apply_Ct, apply_G, apply_Gt, apply_P, inf_norm
 from .qp_utils import ZShape, pack_x, pack_z
+from .backward.backward_kkt_hip import solve_backward_kkt_hip
+from .qp_data import QPCostBlocks, QPEqualityBlocks, QPInequalityBlocks
 from .sqp_hip import first_order_check
 
 _PARAMS_DIR = Path(__file__).resolve().parent / "params"
@@ -252,8 +254,108 @@ class TurboMPCSolver:
         )
 
     def solve(self, initial_guess: TurboMPCSolution, problem_params=None, weights=None) -> TurboMPCSolution:
-        program = self._program if weights is None else self._program.with_weights(weights)
+        program = self._program_for(problem_params, weights)
         return self._solve_impl(program, initial_guess.states, initial_guess.controls, initial_guess.admm_state)
+
+    def solve_vjp(self, solution: TurboMPCSolution, dl_dstates: torch.Tensor, dl_dcontrols: torch.Tensor,
+                  dl_dslack: Optional[torch.Tensor] = None, problem_params=None, weights=None):
+        """Backward pass of the differentiable solve (`_solve_bwd` of
+        get_differentiable_solve_function, turbompc_solver.py:1052-1084): returns
+        (problem_params cotangent {"initial_state": dL/dx0 (B, nx)}, dL/dweights
+        {key: (B, ...)}) for the cotangents of the solution's states and controls."""
+        program = self._program_for(problem_params, weights)
+        if solution.kkt_state is None:
+            raise ValueError("the solution carries no KKT state (no SQP iteration ran)")
+        if dl_dslack is None:
+            dl_dslack = torch.zeros_like(solution.kkt_state.slack)
+        ctx = self._build_backward_qp(program, solution, dl_dstates, dl_dcontrols, dl_dslack)
+        res = self._solve_backward_qp_direct(program, ctx, solution, dl_dslack)
+        kkt = solution.kkt_state
+        dL_dw = program.weight_gradient(kkt.states, kkt.controls, res.dx_states, res.dx_controls)
+        cot = {"initial_state": res.dL_dx_init}
+        return cot, dL_dw
+
+    def get_differentiable_solve_function(self):
+        """A solve(initial_guess, problem_params=None, weights=None) whose states
+        and controls carry torch autograd with respect to
+        problem_params["initial_state"] and the weight tensors (the custom_vjp
+        of turbompc_solver.py:1020-1090)."""
+        return DifferentiableSolve(self)
+
+    def _program_for(self, problem_params, weights):
+        program = self._program
+        if weights:
+            program = program.with_weights(weights)
+        if problem_params:
+            program = program.with_params(problem_params)
+        return program
+
+    # ---------------------------------------------------------- backward ----
+    def _build_backward_qp(self, program, solution: TurboMPCSolution, dl_dstates, dl_dcontrols, dl_dslack):
+        """The adjoint QP (`_build_backward_qp`, turbompc_solver.py:544-618): the QP
+        at the solution with c0 = c = 0, q = -dL/dz, the active rows of G signed
+        (+1 lower, -1 upper, 0 inactive) and, with use_full_hessian, the
+        dynamics Lagrangian Hessian added to D (:1323-1349)."""
+        kkt = solution.kkt_state
+        qp = program.build_qp(kkt.states, kkt.controls)
+        D = qp.cost.D
+        if self._use_full_hessian:
+            lambdas = solution.admm_state.y_f_dyn if solution.admm_state is not None else kkt.y_f[:, 1:]
+            H = program.dynamics_lagrangian_hessian(kkt.states, kkt.controls, lambdas)
+            if H is not None:
+                D = D + H
+            # the inequality rows are linear in z here (bounds): no Hessian term
+        base = QPData(cost=QPCostBlocks(D, qp.cost.E, qp.cost.q), eq=qp.eq, ineq=qp.ineq)
+        eq = QPEqualityBlocks(qp.eq.A0, qp.eq.A_minus, qp.eq.A_plus, torch.zeros_like(qp.eq.c0),
+                              torch.zeros_like(qp.eq.c))
+        G = qp.ineq.G
+        if G.shape[2] == 0:
+            G_active = G
+        else:
+            sign = kkt.ineq_active_lower_idx.to(G.dtype) - kkt.ineq_active_upper_idx.to(G.dtype)
+            G_active = G * sign.unsqueeze(-1)
+        dl = pack_x(dl_dstates.to(D.dtype), dl_dcontrols.to(D.dtype))
+        if qp.ineq.use_slack_variables and G.shape[2] > 0:
+            gamma = qp.ineq.slack_penalization_weight
+            Gt = G_active.transpose(-1, -2)
+            D2 = D + gamma * torch.matmul(Gt, G_active)
+            shift = torch.matmul(Gt, dl_dslack.to(D.dtype).unsqueeze(-1)).squeeze(-1)
+            cost = QPCostBlocks(D2, qp.cost.E, -(dl - shift))
+            empty = torch.zeros(G.shape[:2] + (0,), dtype=G.dtype, device=G.device)
+            ineq = QPInequalityBlocks(torch.zeros(G.shape[:2] + (0, G.shape[-1]), dtype=G.dtype, device=G.device),
+                                      empty, empty, gamma, False)
+        else:
+            cost = QPCostBlocks(D, qp.cost.E, -dl)
+            ineq = QPInequalityBlocks(G_active, torch.zeros_like(qp.ineq.l), torch.zeros_like(qp.ineq.u),
+                                      qp.ineq.slack_penalization_weight, qp.ineq.use_slack_variables)
+        return _BackwardQPContext(base, QPData(cost=cost, eq=eq, ineq=ineq), G_active)
+
+    def _solve_backward_qp_direct(self, program, ctx: "_BackwardQPContext", solution: TurboMPCSolution,
+                                  dl_dslack) -> "_BackwardSolveResult":
+        """`_solve_backward_qp_direct` (turbompc_solver.py:706-779): one batched
+        adjoint KKT solve (tmpc_adjoint_kkt_*) and the multiplier unpacking."""
+        (dxs, dus), mult = solve_backward_kkt_hip(ctx.solve_qp, self._zshape,
+                                                  std_dynamics=getattr(program, "std_dynamics", None))
+        B, T, n, nx, n0, m = ctx.solve_qp.dims
+        m_eq = n0 + (T - 1) * nx
+        y_f0 = mult[:, :n0]
+        y_eq_lin = mult[:, :m_eq]
+        kkt = solution.kkt_state
+        dL_dgamma = torch.zeros((), dtype=mult.dtype, device=mult.device)
+        base = ctx.base_qp
+        if base.ineq.use_slack_variables and base.ineq.G.shape[2] > 0:
+            # _recover_slack_active_ineq_gradient (:620-643)
+            active = (kkt.ineq_active_lower_idx | kkt.ineq_active_upper_idx).to(mult.dtype)
+            dls = dl_dslack.to(mult.dtype) * active
+            dz = pack_x(dxs, dus)
+            g_dz = torch.matmul(ctx.G_active, dz.unsqueeze(-1)).squeeze(-1)
+            gamma = base.ineq.slack_penalization_weight
+            y_ineq_lin = (dls + gamma * g_dz).flatten(1)
+            sign = kkt.ineq_active_lower_idx.to(mult.dtype) - kkt.ineq_active_upper_idx.to(mult.dtype)
+            dL_dgamma = (sign * kkt.slack * active * g_dz).flatten(1).sum(dim=1)
+        else:
+            y_ineq_lin = mult[:, m_eq:]
+        return _BackwardSolveResult(dxs, dus, y_eq_lin, y_ineq_lin, dL_dgamma, y_f0[:, :nx], None)
 
     # ------------------------------------------------------------ internals ----
     def _first_order_check(self, qp: QPData, states, controls, slacks, admm_state: ADMMState):
@@ -384,6 +486,62 @@ class TurboMPCSolver:
             convergence_error=conv, admm_iters=admm_iters, linesearch_alphas=None, admm_state=admm_state,
             solver_stats=SolverStats(admm_iters, eq_v, in_v, conv_h), kkt_state=kkt,
         )
+
+
+class _BackwardQPContext(NamedTuple):
+    base_qp: QPData
+    solve_qp: QPData
+    G_active: torch.Tensor
+
+
+class _BackwardSolveResult(NamedTuple):
+    dx_states: torch.Tensor
+    dx_controls: torch.Tensor
+    y_eq_lin: torch.Tensor
+    y_ineq_lin: torch.Tensor
+    dL_dgamma: torch.Tensor
+    dL_dx_init: torch.Tensor
+    dL_du_init: Optional[torch.Tensor]
+
+
+class _AttachSolution(torch.autograd.Function):
+    """Attaches a computed solution's states and controls to the autograd graph
+    of (x0, weights...); the backward pass is TurboMPCSolver.solve_vjp."""
+
+    @staticmethod
+    def forward(ctx, solver, sol, params, weights, keys, has_x0, *inputs):
+        ctx.solver, ctx.sol, ctx.params, ctx.weights, ctx.keys, ctx.has_x0 = solver, sol, params, weights, keys, has_x0
+        ctx.shapes = [t.shape for t in inputs]
+        return sol.states.clone(), sol.controls.clone()
+
+    @staticmethod
+    def backward(ctx, g_states, g_controls):
+        cot, dw = ctx.solver.solve_vjp(ctx.sol, g_states, g_controls, None, ctx.params, ctx.weights)
+        grads = ([cot["initial_state"]] if ctx.has_x0 else []) + [dw[k] for k in ctx.keys]
+        # inputs shared across the batch get the batch sum of their per-problem gradients
+        grads = [g.sum_to_size(shape) for g, shape in zip(grads, ctx.shapes)]
+        return (None, None, None, None, None, None, *grads)
+
+
+class DifferentiableSolve:
+    """Callable returned by TurboMPCSolver.get_differentiable_solve_function."""
+
+    def __init__(self, solver: "TurboMPCSolver"):
+        self._solver = solver
+
+    def __call__(self, initial_guess: TurboMPCSolution, problem_params=None, weights=None) -> TurboMPCSolution:
+        keys = tuple(weights.keys()) if weights else ()
+        x0 = problem_params.get("initial_state") if problem_params else None
+        inputs = ([torch.as_tensor(x0)] if x0 is not None else []) + [torch.as_tensor(weights[k]) for k in keys]
+        det = lambda d: {k: (v.detach() if torch.is_tensor(v) else v) for k, v in d.items()} if d else d  # noqa: E731
+        params_d, weights_d = det(problem_params), det(weights)
+        with torch.no_grad():
+            sol = self._solver.solve(initial_guess, params_d, weights_d)
+        if not any(t.requires_grad for t in inputs):
+            return sol
+        states, controls = _AttachSolution.apply(self._solver, sol, params_d, weights_d, keys, x0 is not None,
+                                                 *inputs)
+        return sol._replace(states=states, controls=controls)
 
 
 def _select_qp(mask: torch.Tensor, a: QPData, b: QPData) -> QPData:
