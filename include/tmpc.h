@@ -212,6 +212,37 @@ int tmpc_quadrotor_lagrangian_hessian_f64(hipStream_t stream, int32_t B, int32_t
                                           const double* controls, double dt, const double* params,
                                           const double* lambdas, double* H);
 
+/* ---- spherical obstacle constraints ----------------------------------------
+ * Linearized obstacle rows g_k = 1 - |p - c_k| / (r_k + 0.001) <= 0, p = the
+ * first dim state coordinates: replaces the vmapped jacfwd of
+ * get_inequalities_linearized_matrices (turbompc/problems/optimal_control_problem.py:580-626)
+ * over OptimalControlProblemObstacle.step_inequality_constraints
+ * (turbompc/problems/obstacle_avoidance.py:16-52).  states (B,N+1,nx),
+ * centers (B,K,dim), radii (B,K).  Writes rows row0..row0+K-1 of G (B,N+1,m,n),
+ * l and u (B,N+1,m): the gradient row, l = -1e9 - offset, u = -offset with
+ * offset = g(xbar) - dg/dx xbar.  Other rows are left untouched. */
+int tmpc_obstacle_linearize_f32(hipStream_t stream, int32_t B, int32_t N, int32_t nx, int32_t nu, int32_t dim,
+                                int32_t K, const float* states, const float* centers, const float* radii, int32_t m,
+                                int32_t row0, float* G, float* l, float* u);
+int tmpc_obstacle_linearize_f64(hipStream_t stream, int32_t B, int32_t N, int32_t nx, int32_t nu, int32_t dim,
+                                int32_t K, const double* states, const double* centers, const double* radii,
+                                int32_t m, int32_t row0, double* G, double* l, double* u);
+
+/* Inequality Lagrangian Hessian of the obstacle rows for the exact-Hessian
+ * backward pass: replaces get_inequality_lagrangian_hessian
+ * (turbompc/problems/optimal_control_problem.py:1443-1480), called from
+ * _augment_D_with_inequality_hessian (turbompc/solvers/turbompc_solver.py:1357-1385).
+ * mus (B,N+1,m) are the multipliers of all m rows (active mask times y_g; the
+ * box rows are linear and contribute nothing).  H (B,N+1,n,n) is overwritten
+ * with sum_k mus[row0+k] d^2 g_k / dz^2. */
+int tmpc_obstacle_lagrangian_hessian_f32(hipStream_t stream, int32_t B, int32_t N, int32_t nx, int32_t nu, int32_t dim,
+                                         int32_t K, const float* states, const float* centers, const float* radii,
+                                         int32_t m, int32_t row0, const float* mus, float* H);
+int tmpc_obstacle_lagrangian_hessian_f64(hipStream_t stream, int32_t B, int32_t N, int32_t nx, int32_t nu, int32_t dim,
+                                         int32_t K, const double* states, const double* centers,
+                                         const double* radii, int32_t m, int32_t row0, const double* mus,
+                                         double* H);
+
 /* ---- SQP first-order convergence check ------------------------------------
  * Replaces _compute_first_order_convergence_error
  * (turbompc/solvers/turbompc_solver.py:1158-1225), evaluated in XLA by the

@@ -117,3 +117,15 @@ def zero_state(qp, rho):
     z0 = np.clip(np.zeros((B, T, m)), np.asarray(qp.ineq.l, dtype=np.float64), np.asarray(qp.ineq.u, dtype=np.float64))
     return St(np.zeros((B, T, n)), np.zeros((B, T, m)), np.zeros((B, n0)), np.zeros((B, T - 1, nx)), z0,
               np.zeros((B, T, m)), np.full((B,), float(rho)))
+
+
+def soften(qp, gamma, shrink=1.0):
+    """The QP with soft inequality rows (slack weight gamma), each box shrunk
+    about its midpoint by `shrink` so that some rows end up violated."""
+    from turbompc_amd.solvers.qp_data import QPData, QPInequalityBlocks
+
+    l, u = qp.ineq.l, qp.ineq.u
+    mid, half = 0.5 * (l + u), 0.5 * shrink * (u - l)
+    return QPData(cost=qp.cost, eq=qp.eq,
+                  ineq=QPInequalityBlocks(qp.ineq.G, mid - half, mid + half,
+                                          torch.tensor(float(gamma), dtype=l.dtype), True))

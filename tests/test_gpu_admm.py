@@ -18,7 +18,7 @@ import pytest
 import torch
 
 import oracle
-from helpers import TOL, random_qp, rel_err, zero_state
+from helpers import TOL, random_qp, rel_err, soften, zero_state
 from turbompc_amd import _lib
 from turbompc_amd.problems import configs
 from turbompc_amd.problems.quadrotor import QUAD_PARAMS, make_quadrotor_config
@@ -53,7 +53,8 @@ def _run_pair(qp, cfg, dtype, backend=AdmmBackend.HIP_DIRECT, rho0=0.1, schur="d
     ref, it_ref, pcg_ref = oracle.admm_solve(qp, st0, cfg, schur=schur, dtype=np.float64)
     qpd = qp.to(DEV, dtype)
     solver = _solver(qp, cfg, backend, **kw)
-    (_, _), stats, out = solver.solve(qpd, _state_to_dev(st0, dtype), alpha=cfg.alpha)
+    (_, _), stats, out = solver.solve(qpd, _state_to_dev(st0, dtype), alpha=cfg.alpha,
+                                      slack_weight=qpd.ineq.slack_penalization_weight)
     torch.cuda.synchronize()
     return ref, it_ref, pcg_ref, out, stats
 
@@ -75,6 +76,36 @@ def test_admm_direct_fp64_fixed_iterations(std, shape):
     ref, it_ref, _, out, stats = _run_pair(qp, cfg, torch.float64)
     np.testing.assert_array_equal(stats.num_iter.cpu().numpy(), it_ref)
     _assert_state_close(out, ref, 1e-9)
+
+
+# soft constraints (slack variables): generic kernel with general and
+# explicit-integrator structure, streaming kernel with 1 and 2 problems per
+# wavefront; the residual sweep (with its slack terms) runs every 4 iterations
+@pytest.mark.parametrize("kernel", ["generic", "generic-std", "stream-1", "stream-2"])
+def test_admm_slack_fp64_fixed_iterations(kernel):
+    if kernel.startswith("stream"):
+        shape, flags, std = (13, 21, 6, 4, 2), _lib.flag_stream_p(int(kernel[-1])), True
+    else:
+        shape, flags, std = (5, 13, 9, 6, 11), _lib.FLAG_GENERIC_KERNEL, kernel.endswith("std")
+    B, T, n, nx, m = shape
+    qp = soften(random_qp(B, T, n, nx, m, seed=61, std=std), 20.0, shrink=0.3)
+    cfg = oracle.OracleCfg(max_iter=30, check_every=4, adapt_rho_every=0, sigma=1e-6, eps_abs=1e-12,
+                           eps_rel=1e-12, rho_f_factor=1000.0, alpha=1.6)
+    ref, it_ref, _, out, stats = _run_pair(qp, cfg, torch.float64, use_slack=True, kernel_flags=flags)
+    np.testing.assert_array_equal(stats.num_iter.cpu().numpy(), it_ref)
+    assert float(np.max(np.abs(ref.xi_g))) > 1e-3  # rows are softened
+    _assert_state_close(out, ref, 1e-9)
+
+
+def test_admm_slack_converges_with_termination_and_adaptive_rho():
+    qp = soften(random_qp(9, 9, 6, 4, 3, seed=62, std=True), 5.0, shrink=0.3)
+    cfg = oracle.OracleCfg(max_iter=300, check_every=2, adapt_rho_every=4, sigma=1e-6, eps_abs=1e-6, eps_rel=1e-6,
+                           rho_f_factor=50.0, alpha=1.0, adaptive_rho_tolerance=1.5)
+    ref, it_ref, _, out, stats = _run_pair(qp, cfg, torch.float64, use_slack=True)
+    np.testing.assert_array_equal(stats.num_iter.cpu().numpy(), it_ref)
+    assert np.all(it_ref < cfg.max_iter)
+    assert rel_err(out.rho_bar, ref.rho_bar) < 1e-7
+    _assert_state_close(out, ref, 1e-5)
 
 
 @pytest.mark.parametrize("alpha", [1.0, 1.6])

@@ -18,13 +18,13 @@ pytestmark = pytest.mark.gpu
 DEV = "cuda"
 
 
-def _tight_params(n_sqp, admm_iters):
+def _tight_params(n_sqp, admm_iters, tol=0.0, eps=1e-13):
     p = copy.deepcopy(DEFAULT_SOLVER_PARAMS)
     p["num_sqp_iteration_max"] = n_sqp
-    p["tol_convergence"] = 0.0
+    p["tol_convergence"] = tol
     p["admm"]["max_iter"] = admm_iters
-    p["admm"]["eps_abs"] = 1e-13
-    p["admm"]["eps_rel"] = 1e-13
+    p["admm"]["eps_abs"] = eps
+    p["admm"]["eps_rel"] = eps
     return p
 
 
@@ -56,7 +56,10 @@ def test_quadrotor_lagrangian_hessian_matches_jacobian_differences():
     assert rel_err(H[:, :N], Hfd) < 1e-6
 
 
-def _check_gradients(solver, prob, n_checks, h, rtol, seed, floor=1e-2):
+def _check_gradients(solver, prob, n_checks, h, rtol, seed, floor=1e-2, warm=False):
+    """warm: the finite-difference solves start from the solution (states,
+    controls and ADMM state), which a converged SQP reaches again in a few
+    iterations."""
     guess = solver.initial_guess()
     g = torch.Generator().manual_seed(seed)
     B, T, nx = guess.states.shape
@@ -68,6 +71,8 @@ def _check_gradients(solver, prob, n_checks, h, rtol, seed, floor=1e-2):
     sol = fsolve(guess, {"initial_state": x0}, w)
     L = (cs * sol.states).sum() + (cu * sol.controls).sum()
     L.backward()
+    if warm:
+        guess = sol._replace(states=sol.states.detach(), controls=sol.controls.detach())
 
     def loss(x0v, wv):
         s = solver.solve(guess, {"initial_state": x0v}, wv)
@@ -92,6 +97,7 @@ def _check_gradients(solver, prob, n_checks, h, rtol, seed, floor=1e-2):
             wm[name][b, i] -= h
             fd = (loss(x0.detach(), wp) - loss(x0.detach(), wm)) / (2 * h)
             got = float(w[name].grad[b, i])
+        print(f"  {name}[{b},{i}]: adjoint {got:.9g}  central difference {fd:.9g}", flush=True)
         assert abs(got - fd) <= rtol * max(abs(fd), floor), (name, b, i, got, fd)
 
 
@@ -114,3 +120,77 @@ def test_quadrotor_gradients_match_finite_differences():
     # gradients here span 5e-3 .. 2e2: the floor keeps the tiny ones to an
     # absolute 1e-4 (finite differences of a solve converged to ~1e-9)
     _check_gradients(solver, prob, n_checks=1, h=1e-5, rtol=1e-4, seed=2, floor=1.0)
+
+
+def test_obstacle_lagrangian_hessian_matches_gradient_differences():
+    B = 3
+    prob = configs.config4(B=B, seed=6).to(DEV, torch.float64)
+    xs, us = prob.initial_guess()
+    g = torch.Generator().manual_seed(4)
+    xs = xs + 0.3 * torch.randn(xs.shape, generator=g, dtype=torch.float64).to(DEV)
+    m, mb = prob.num_inequality_constraints, prob.num_box_constraints
+    mus = torch.randn((B, prob.horizon + 1, m), generator=g, dtype=torch.float64).to(DEV)
+    H = prob.inequality_lagrangian_hessian(xs, us, mus)
+    h = 1e-6
+    cols = []
+    for j in range(9):
+        dx = torch.zeros_like(xs)
+        if j < 6:
+            dx[..., j] = h
+        Gp, _, _ = prob.inequality_blocks_at(xs + dx, us)
+        Gm, _, _ = prob.inequality_blocks_at(xs - dx, us)
+        cols.append(torch.einsum("bti,btik->btk", mus[..., mb:], (Gp - Gm)[:, :, mb:] / (2 * h)))
+    Hfd = torch.stack(cols, dim=-1)
+    assert rel_err(H, Hfd) < 1e-7
+
+
+def test_obstacle_gradients_match_finite_differences():
+    # nonlinear inequality rows: the adjoint QP carries their Lagrangian Hessian
+    prob = configs.config4(B=2, seed=7).to(DEV, torch.float64)
+    solver = TurboMPCSolver(prob, _tight_params(40, 4000, tol=1e-10, eps=1e-12))
+    sol = solver.solve(solver.initial_guess())
+    print(f"  SQP iterations {sol.num_iter.tolist()}, first-order error {sol.convergence_error.tolist()}", flush=True)
+    assert float(sol.convergence_error.max()) < 1e-8
+    # every problem has an active obstacle row, so the Hessian term is in play
+    mb = prob.num_box_constraints
+    assert bool((sol.admm_state.y_g[..., mb:].abs().flatten(1).amax(dim=1) > 1.0).all())
+    _check_gradients(solver, prob, n_checks=2, h=1e-5, rtol=1e-4, seed=3, floor=1.0, warm=True)
+
+
+def test_slack_weight_gradient_matches_finite_differences():
+    # soft obstacle rows: dL/dgamma from the active slacks
+    # (_recover_slack_active_ineq_gradient, turbompc_solver.py:620-643)
+    gamma = 20.0
+    prob = configs.config4(B=2, seed=7, use_slack_variables=True,
+                           slack_penalization_weight=gamma).to(DEV, torch.float64)
+    solver = TurboMPCSolver(prob, _tight_params(40, 4000, tol=1e-10, eps=1e-12))
+    gam = torch.tensor(gamma, dtype=torch.float64, requires_grad=True)
+    x0 = prob.x0.clone().requires_grad_(True)
+    out = solver.get_differentiable_solve_function()(solver.initial_guess(), {"initial_state": x0},
+                                                     {"slack_penalization_weight": gam})
+    print(f"  SQP iterations {out.num_iter.tolist()}, first-order error {out.convergence_error.tolist()}", flush=True)
+    assert float(out.convergence_error.max()) < 1e-8
+    assert float(out.slack.abs().max()) > 1e-4
+    mb = prob.num_box_constraints
+    assert float(out.slack[..., mb:].abs().max()) > 1e-4  # a softened obstacle row
+    g = torch.Generator().manual_seed(5)
+    cs = torch.randn(out.states.shape, generator=g, dtype=torch.float64).to(DEV)
+    cu = torch.randn(out.controls.shape, generator=g, dtype=torch.float64).to(DEV)
+    ((cs * out.states).sum() + (cu * out.controls).sum()).backward()
+    guess = out._replace(states=out.states.detach(), controls=out.controls.detach())  # warm start
+
+    def loss(gv, x0v):
+        s = solver.solve(guess, {"initial_state": x0v}, {"slack_penalization_weight": gv})
+        return float((cs * s.states).sum() + (cu * s.controls).sum())
+
+    h = 1e-4
+    fd = (loss(gamma + h, prob.x0) - loss(gamma - h, prob.x0)) / (2 * h)
+    print(f"  gamma: adjoint {float(gam.grad):.9g}  central difference {fd:.9g}", flush=True)
+    assert abs(float(gam.grad) - fd) <= 1e-4 * max(abs(fd), 1e-2), (float(gam.grad), fd)
+    for b, i in ((0, 1), (1, 4)):
+        xp, xm = prob.x0.clone(), prob.x0.clone()
+        xp[b, i] += 1e-5
+        xm[b, i] -= 1e-5
+        fd = (loss(gamma, xp) - loss(gamma, xm)) / 2e-5
+        print(f"  x0[{b},{i}]: adjoint {float(x0.grad[b, i]):.9g}  central difference {fd:.9g}", flush=True)
+        assert abs(float(x0.grad[b, i]) - fd) <= 1e-4 * max(abs(fd), 1.0), (b, i, float(x0.grad[b, i]), fd)

@@ -1,0 +1,127 @@
+"""Obstacle-avoidance workload (config 4 shapes) on the GPU against the CPU
+restatement: the linearized obstacle rows and their Lagrangian Hessian
+(tmpc_obstacle_*), and the SQP at fixed iteration counts (8 SQP x 30 ADMM,
+ADMM state carried across SQP iterations), with hard and with soft
+(slack-variable) constraints."""
+import copy
+
+import numpy as np
+import pytest
+import torch
+
+import oracle
+from helpers import TOL, rel_err
+from oracle.sqp_cpu import linearize_obstacles, obstacle_hessian, obstacle_sqp
+from turbompc_amd.problems import configs
+from turbompc_amd.problems.ocp import LinearOCP
+from turbompc_amd.solvers.turbompc_solver import DEFAULT_SOLVER_PARAMS, TurboMPCSolver
+
+pytestmark = pytest.mark.gpu
+
+
+def _params(n_sqp, admm_iters):
+    p = copy.deepcopy(DEFAULT_SOLVER_PARAMS)
+    p["num_sqp_iteration_max"] = n_sqp
+    p["tol_convergence"] = 0.0
+    p["admm"]["max_iter"] = admm_iters
+    p["admm"]["adapt_rho_every"] = 0
+    p["admm"]["relaxation_parameter"] = 1.0
+    return p
+
+
+def _states(B, T, seed):
+    rng = np.random.default_rng(seed)
+    s = rng.uniform(-4, 4, (B, T, 6))
+    s[..., 3:] *= 0.25
+    return s, rng.uniform(-3, 3, (B, T, 3))
+
+
+@pytest.mark.parametrize("dtype", [torch.float64, torch.float32])
+def test_obstacle_rows_match_cpu(dtype):
+    B = 7
+    prob = configs.config4(B=B, seed=3)
+    s, u = _states(B, prob.horizon + 1, 4)
+    dev = prob.to("cuda", dtype)
+    G, l, up = dev.inequality_blocks_at(torch.tensor(s, dtype=dtype, device="cuda"),
+                                        torch.tensor(u, dtype=dtype, device="cuda"))
+    torch.cuda.synchronize()
+    G, l, up = (t.double().cpu().numpy() for t in (G, l, up))
+    Gb, lb, ub = (t.numpy() for t in LinearOCP.inequality_blocks(prob))
+    mb = prob.num_box_constraints
+    np.testing.assert_array_equal(G[:, :, :mb], Gb)
+    np.testing.assert_array_equal(l[:, :, :mb], lb)
+    np.testing.assert_array_equal(up[:, :, :mb], ub)
+    s_in = torch.tensor(s, dtype=dtype).double().numpy()
+    grad, lo_ref, up_ref = linearize_obstacles(s_in, prob.centers.to(dtype).double().numpy(),
+                                               prob.radii.to(dtype).double().numpy(), 3)
+    tol = 1e-12 if dtype == torch.float64 else 2e-6
+    assert rel_err(G[:, :, mb:, :3], grad) < tol
+    assert np.all(G[:, :, mb:, 3:] == 0)
+    assert rel_err(up[:, :, mb:], up_ref) < (tol if dtype == torch.float64 else 1e-5)
+    assert rel_err(l[:, :, mb:], lo_ref) < tol
+
+
+@pytest.mark.parametrize("dtype", [torch.float64, torch.float32])
+def test_obstacle_hessian_matches_cpu(dtype):
+    B = 5
+    prob = configs.config4(B=B, seed=5)
+    T, m, n = prob.horizon + 1, prob.num_inequality_constraints, 9
+    s, u = _states(B, T, 6)
+    mus = np.random.default_rng(7).standard_normal((B, T, m))
+    dev = prob.to("cuda", dtype)
+    H = dev.inequality_lagrangian_hessian(torch.tensor(s, dtype=dtype, device="cuda"),
+                                          torch.tensor(u, dtype=dtype, device="cuda"),
+                                          torch.tensor(mus, dtype=dtype, device="cuda"))
+    torch.cuda.synchronize()
+    c = lambda a: torch.tensor(a, dtype=dtype).double().numpy()  # noqa: E731
+    ref = obstacle_hessian(c(s), prob.centers.to(dtype).double().numpy(), prob.radii.to(dtype).double().numpy(), 3,
+                           c(mus)[..., prob.num_box_constraints:], n)
+    assert rel_err(H, ref) < (1e-12 if dtype == torch.float64 else 1e-5)
+
+
+def _cpu_sqp(prob, n_sqp, admm_iters, dtype, *, use_slack=False, gamma=0.0):
+    D, E, q = (t.numpy() for t in prob.cost_blocks())
+    A0, c0 = (t.numpy() for t in prob.initial_equality())
+    G, l, u = (t.numpy() for t in LinearOCP.inequality_blocks(prob))
+    static = dict(D=D, E=E, q=q, A0=A0, c0=c0, A_plus=prob.a_plus().numpy(), G=G, l=l, u=u)
+    xg, ug = (t.numpy() for t in prob.initial_guess())
+    Am, c = (t.numpy() for t in prob.dynamics_blocks(*prob.initial_guess()))
+    cfg = oracle.OracleCfg(max_iter=admm_iters, check_every=50, adapt_rho_every=0, sigma=1e-6, eps_abs=1e-9,
+                           eps_rel=1e-9, rho_f_factor=1000.0, alpha=1.0)
+    return obstacle_sqp(static, xg, ug, A_minus=Am, c=c, centers=prob.centers.numpy(), radii=prob.radii.numpy(),
+                        dim=3, cfg=cfg, rho0=0.1, n_sqp=n_sqp, slack_weight=gamma, use_slack=use_slack, dtype=dtype)
+
+
+@pytest.mark.parametrize("use_slack", [False, True])
+def test_config4_sqp_fp64_matches_cpu(use_slack):
+    B = 6
+    prob = configs.config4(B=B, seed=0, use_slack_variables=use_slack, slack_penalization_weight=50.0)
+    xs, us, st = _cpu_sqp(prob, 8, 30, np.float64, use_slack=use_slack, gamma=50.0)
+    solver = TurboMPCSolver(prob.to("cuda"), _params(8, 30))
+    sol = solver.solve(solver.initial_guess())
+    torch.cuda.synchronize()
+    assert rel_err(sol.states, xs) < TOL[torch.float64]
+    assert rel_err(sol.controls, us) < TOL[torch.float64]
+    assert rel_err(sol.admm_state.y_g, st.y_g) < 1e-8
+    if use_slack:
+        assert rel_err(sol.slack, st.xi_g) < 1e-8
+        assert float(np.max(np.abs(st.xi_g))) > 1e-6  # the soft rows are in play
+    else:
+        assert np.all(sol.slack.cpu().numpy() == 0)
+    assert torch.all(sol.num_iter == 8)
+    # some obstacle row is active or violated at the linearization, so the
+    # obstacle rows shape the solution
+    assert float(np.max(np.abs(st.y_g[..., prob.num_box_constraints:]))) > 1e-6
+
+
+def test_config4_sqp_fp32_matches_cpu():
+    B = 16
+    prob = configs.config4(B=B, seed=1)
+    xs, us, _ = _cpu_sqp(prob, 8, 30, np.float64)
+    xs32, us32, _ = _cpu_sqp(prob, 8, 30, np.float32)
+    solver = TurboMPCSolver(prob.to("cuda", torch.float32), _params(8, 30))
+    sol = solver.solve(solver.initial_guess())
+    torch.cuda.synchronize()
+    for got, ref, ref32 in ((sol.states, xs, xs32), (sol.controls, us, us32)):
+        e, e_or = rel_err(got, ref), rel_err(ref32, ref)
+        assert e < max(TOL[torch.float32], 4 * e_or), (e, e_or)

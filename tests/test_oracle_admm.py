@@ -16,7 +16,7 @@ import numpy as np
 import pytest
 
 import oracle
-from helpers import dense_C, dense_G, dense_P, np_qp, random_qp, zero_state
+from helpers import soften, dense_C, dense_G, dense_P, np_qp, random_qp, zero_state
 
 
 def dense_admm(a, b, x, z, yg, y0, yf, xi, rho, cfg, iters):
@@ -151,6 +151,49 @@ def test_oracle_admm_matches_bruteforce_active_set():
                            eps_rel=1e-12, rho_f_factor=100.0, alpha=1.6)
     out, iters, _ = oracle.admm_solve(qp, zero_state(qp, 0.1), cfg)
     np.testing.assert_allclose(out.x_blocks[0].reshape(-1), best, atol=1e-7)
+
+
+def test_oracle_slack_admm_matches_bruteforce_soft_constraints():
+    # soft rows l <= G x + xi <= u with cost gamma/2 |xi|^2 (admm.py:895-919):
+    # the x-part minimizes 1/2 x'Px + q'x + gamma/2 dist(Gx, [l, u])^2 s.t. Cx = c,
+    # a piecewise quadratic; enumerate below / inside / above for each row
+    gamma = 3.0
+    qp = soften(random_qp(1, 3, 2, 1, 1, seed=17, std=True), gamma, shrink=0.1)
+    a = np_qp(qp)
+    C = dense_C(a["A0"][0], a["Am"][0], a["Ap"][0])
+    G = dense_G(a["G"][0])
+    P = dense_P(a["D"][0], a["E"][0])
+    q = a["q"][0].reshape(-1)
+    cst = np.concatenate([a["c0"][0], a["c"][0].reshape(-1)])
+    l, u = a["l"][0].reshape(-1), a["u"][0].reshape(-1)
+    nz, nc = P.shape[0], C.shape[0]
+    best, n_out = None, 0
+    for pat in itertools.product((0, -1, 1), repeat=len(l)):  # inside / below l / above u
+        H, rhs = P.copy(), -q.copy()
+        for i, p in enumerate(pat):
+            if p:
+                b = l[i] if p < 0 else u[i]
+                H += gamma * np.outer(G[i], G[i])
+                rhs += gamma * G[i] * b
+        K = np.block([[H, C.T], [C, np.zeros((nc, nc))]])
+        x = np.linalg.solve(K, np.concatenate([rhs, cst]))[:nz]
+        Gx = G @ x
+        ok = all((p == 0 and l[i] - 1e-9 <= Gx[i] <= u[i] + 1e-9) or (p < 0 and Gx[i] <= l[i] + 1e-9)
+                 or (p > 0 and Gx[i] >= u[i] - 1e-9) for i, p in enumerate(pat))
+        if ok:
+            best, n_out = x, sum(1 for p in pat if p)
+            break
+    assert best is not None and n_out > 0  # some row is softened at the optimum
+    cfg = oracle.OracleCfg(max_iter=20000, check_every=10, adapt_rho_every=50, sigma=1e-9, eps_abs=1e-12,
+                           eps_rel=1e-12, rho_f_factor=100.0, alpha=1.6)
+    out, iters, _ = oracle.admm_solve(qp, zero_state(qp, 0.1), cfg)
+    np.testing.assert_allclose(out.x_blocks[0].reshape(-1), best, atol=1e-7)
+    # slack stationarity gamma xi + y_g = 0, and G x + xi inside the box
+    xi, yg = out.xi_g[0].reshape(-1), out.y_g[0].reshape(-1)
+    np.testing.assert_allclose(gamma * xi + yg, 0.0, atol=1e-7)
+    s = G @ out.x_blocks[0].reshape(-1) + xi
+    assert np.all(s >= l - 1e-7) and np.all(s <= u + 1e-7)
+    assert np.max(np.abs(xi)) > 1e-3
 
 
 def test_oracle_iteration_count_oracle():

@@ -120,6 +120,10 @@ SIGNATURES = {
     "tmpc_quadrotor_linearize_f64": [_VP, _I32, _I32, _VP, _VP, _F64, _VP, _VP, _VP],
     "tmpc_quadrotor_lagrangian_hessian_f32": [_VP, _I32, _I32, _VP, _VP, _F64, _VP, _VP, _VP],
     "tmpc_quadrotor_lagrangian_hessian_f64": [_VP, _I32, _I32, _VP, _VP, _F64, _VP, _VP, _VP],
+    "tmpc_obstacle_linearize_f32": [_VP] + [_I32] * 6 + [_VP] * 3 + [_I32, _I32] + [_VP] * 3,
+    "tmpc_obstacle_linearize_f64": [_VP] + [_I32] * 6 + [_VP] * 3 + [_I32, _I32] + [_VP] * 3,
+    "tmpc_obstacle_lagrangian_hessian_f32": [_VP] + [_I32] * 6 + [_VP] * 3 + [_I32, _I32] + [_VP] * 2,
+    "tmpc_obstacle_lagrangian_hessian_f64": [_VP] + [_I32] * 6 + [_VP] * 3 + [_I32, _I32] + [_VP] * 2,
 }
 _SIZE_FNS = {
     "tmpc_admm_direct_workspace_bytes",

@@ -11,6 +11,7 @@
 #include "common.hpp"
 #include "factor.hpp"
 #include "pcg.hpp"
+#include "obstacle.hpp"
 #include "quadrotor.hpp"
 #include "adjoint.hpp"
 #include "sqp.hpp"
@@ -679,6 +680,46 @@ int quad_hess_impl(hipStream_t s, int B, int N, const R* states, const R* contro
 }
 
 
+// ------------------------------------------------------------- obstacles ----
+inline int obstacle_check(int B, int N, int nx, int nu, int dim, int K, int m, int row0) {
+  if (B < 1 || N < 1 || nx < 1 || nu < 0 || dim < 1 || dim > nx || K < 0 || row0 < 0 || row0 + K > m)
+    return TMPC_EBADSHAPE;
+  return TMPC_OK;
+}
+
+template <typename R>
+int obstacle_lin_impl(hipStream_t s, int B, int N, int nx, int nu, int dim, int K, const R* states,
+                      const R* centers, const R* radii, int m, int row0, R* G, R* l, R* u) {
+  int st = obstacle_check(B, N, nx, nu, dim, K, m, row0);
+  if (st) return st;
+  if (K == 0) return TMPC_OK;
+  if (!states || !centers || !radii || !G || !l || !u) return TMPC_EBADARG;
+  const int T = N + 1, n = nx + nu;
+  const long long total = (long long)B * T * K * n;
+  const int blk = 256;
+  const long long grid = (total + blk - 1) / blk;
+  if (grid > INT32_MAX) return TMPC_EBADSHAPE;
+  hipLaunchKernelGGL((obstacle_linearize_kernel<R>), dim3((unsigned)grid), dim3(blk), 0, s, B, T, nx, n, dim, K,
+                     states, centers, radii, m, row0, G, l, u);
+  return launch_status();
+}
+
+template <typename R>
+int obstacle_hess_impl(hipStream_t s, int B, int N, int nx, int nu, int dim, int K, const R* states,
+                       const R* centers, const R* radii, int m, int row0, const R* mus, R* H) {
+  int st = obstacle_check(B, N, nx, nu, dim, K, m, row0);
+  if (st) return st;
+  if (!states || !H || !mus || (K > 0 && (!centers || !radii))) return TMPC_EBADARG;
+  const int T = N + 1, n = nx + nu;
+  const long long total = (long long)B * T * n * n;
+  const int blk = 256;
+  const long long grid = (total + blk - 1) / blk;
+  if (grid > INT32_MAX) return TMPC_EBADSHAPE;
+  hipLaunchKernelGGL((obstacle_hessian_kernel<R>), dim3((unsigned)grid), dim3(blk), 0, s, B, T, nx, n, dim, K,
+                     states, centers, radii, m, row0, mus, H);
+  return launch_status();
+}
+
 // ------------------------------------------------------------- SQP check ----
 template <typename R, int NC>
 void launch_sqp_nc(hipStream_t s, const Dims& d, bool std_dyn, int diag, const QPDev<R>& q, const R* x,
@@ -858,6 +899,28 @@ int tmpc_quadrotor_lagrangian_hessian_f64(hipStream_t s, int32_t B, int32_t N, c
                                           const double* controls, double dt, const double* params,
                                           const double* lambdas, double* H) {
   return quad_hess_impl<double>(s, B, N, states, controls, dt, params, lambdas, H);
+}
+
+int tmpc_obstacle_linearize_f32(hipStream_t s, int32_t B, int32_t N, int32_t nx, int32_t nu, int32_t dim,
+                                int32_t K, const float* states, const float* centers, const float* radii, int32_t m,
+                                int32_t row0, float* G, float* l, float* u) {
+  return obstacle_lin_impl<float>(s, B, N, nx, nu, dim, K, states, centers, radii, m, row0, G, l, u);
+}
+int tmpc_obstacle_linearize_f64(hipStream_t s, int32_t B, int32_t N, int32_t nx, int32_t nu, int32_t dim,
+                                int32_t K, const double* states, const double* centers, const double* radii,
+                                int32_t m, int32_t row0, double* G, double* l, double* u) {
+  return obstacle_lin_impl<double>(s, B, N, nx, nu, dim, K, states, centers, radii, m, row0, G, l, u);
+}
+int tmpc_obstacle_lagrangian_hessian_f32(hipStream_t s, int32_t B, int32_t N, int32_t nx, int32_t nu, int32_t dim,
+                                         int32_t K, const float* states, const float* centers, const float* radii,
+                                         int32_t m, int32_t row0, const float* mus, float* H) {
+  return obstacle_hess_impl<float>(s, B, N, nx, nu, dim, K, states, centers, radii, m, row0, mus, H);
+}
+int tmpc_obstacle_lagrangian_hessian_f64(hipStream_t s, int32_t B, int32_t N, int32_t nx, int32_t nu, int32_t dim,
+                                         int32_t K, const double* states, const double* centers,
+                                         const double* radii, int32_t m, int32_t row0, const double* mus,
+                                         double* H) {
+  return obstacle_hess_impl<double>(s, B, N, nx, nu, dim, K, states, centers, radii, m, row0, mus, H);
 }
 
 int tmpc_sqp_first_order_f32(hipStream_t s, const tmpc_dims* dims, const tmpc_qp* qp, const float* x,

@@ -1,0 +1,105 @@
+"""Linear-dynamics tracking OCP with spherical obstacle-avoidance constraints.
+
+Follows OptimalControlProblemObstacle (turbompc/problems/obstacle_avoidance.py:13-52)
+and its slack variant OptimalControlProblemObstacleSlack (:55, through
+make_slack_problem, optimal_control_problem.py:1539-1544): every stage carries
+the box rows of the base problem followed by one row per obstacle,
+    g_k(x) = 1 - |p - c_k| / (r_k + 0.001) <= 0      (l = -1e9, u = 0),
+with p the first `obstacles_dimension` state coordinates.  The obstacle rows
+are linearized at each SQP iterate on the device (tmpc_obstacle_linearize_*);
+the backward pass adds their Lagrangian Hessian (tmpc_obstacle_lagrangian_hessian_*).
+"""
+from __future__ import annotations
+
+import torch
+
+from .. import _lib
+from ..solvers.qp_data import QPCostBlocks, QPData, QPEqualityBlocks, QPInequalityBlocks
+from .ocp import LinearOCP, as_tensor
+
+
+class ObstacleOCP(LinearOCP):
+    def __init__(self, *, obstacles_centers: torch.Tensor, obstacles_radii: torch.Tensor,
+                 obstacles_dimension: int = 3, **kw):
+        """obstacles_centers (B, K, dim) or (K, dim); obstacles_radii (B, K) or (K,)."""
+        super().__init__(**kw)
+        c = as_tensor(obstacles_centers, self.dtype, self.device)
+        r = as_tensor(obstacles_radii, self.dtype, self.device)
+        self.obstacles_dimension = int(obstacles_dimension)
+        if c.dim() == 2:
+            c = c.unsqueeze(0).expand(self.B, *c.shape)
+        if r.dim() == 1:
+            r = r.unsqueeze(0).expand(self.B, r.shape[0])
+        if c.shape[0] != self.B or c.shape[-1] != self.obstacles_dimension or r.shape != c.shape[:2]:
+            raise ValueError(f"obstacle shapes {tuple(c.shape)}, {tuple(r.shape)} do not match B={self.B}, "
+                             f"dim={self.obstacles_dimension}")
+        if not 1 <= self.obstacles_dimension <= self.num_state_variables:
+            raise ValueError("obstacles_dimension must lie in [1, nx]")
+        self.centers, self.radii = c.contiguous(), r.contiguous()
+        self.num_obstacles = int(c.shape[1])
+        self.num_box_constraints = self.num_inequality_constraints
+        self.num_inequality_constraints = self.num_box_constraints + self.num_obstacles
+
+    def _call(self, name: str, states: torch.Tensor, *tensors: torch.Tensor):
+        if not states.is_cuda:
+            raise ValueError("ObstacleOCP linearization runs on the GPU; pass device tensors")
+        lib = _lib.load()
+        sfx = _lib.suffix(self.dtype)
+        fn = f"{name}_{sfx}"
+        st = getattr(lib, fn)(
+            _lib.stream_handle(states.device), self.B, self.horizon, self.num_state_variables,
+            self.num_control_variables, self.obstacles_dimension, self.num_obstacles, _lib.ptr(states),
+            _lib.ptr(self.centers), _lib.ptr(self.radii), self.num_inequality_constraints, self.num_box_constraints,
+            *[_lib.ptr(t) for t in tensors],
+        )
+        _lib.check(fn, st)
+
+    def inequality_blocks_at(self, states: torch.Tensor, controls: torch.Tensor, box=None):
+        """G (B,T,m,n), l, u (B,T,m): the box rows, then the obstacle rows
+        linearized at (states, controls)."""
+        nx, nu = self.num_state_variables, self.num_control_variables
+        T, n, m, mb = self.horizon + 1, nx + nu, self.num_inequality_constraints, self.num_box_constraints
+        if box is None:
+            box = super().inequality_blocks()
+        Gb, lb, ub = box
+        states = states.to(self.dtype).contiguous()
+        G = torch.empty((self.B, T, m, n), dtype=self.dtype, device=states.device)
+        l = torch.empty((self.B, T, m), dtype=self.dtype, device=states.device)
+        u = torch.empty_like(l)
+        if mb:
+            G[:, :, :mb] = Gb
+            l[:, :, :mb] = lb
+            u[:, :, :mb] = ub
+        self._call("tmpc_obstacle_linearize", states, G, l, u)
+        return G, l, u
+
+    def inequality_blocks(self):
+        raise NotImplementedError("obstacle rows depend on the iterate; use inequality_blocks_at(states, controls)")
+
+    def inequality_lagrangian_hessian(self, states, controls, mus):
+        """(B, T, n, n): sum_k mu_k d^2 g_k/dz^2 of the obstacle rows (box rows are linear)."""
+        states = states.to(self.dtype).contiguous()
+        mus = mus.to(self.dtype).contiguous()
+        n = self.num_state_variables + self.num_control_variables
+        H = torch.empty((self.B, self.horizon + 1, n, n), dtype=self.dtype, device=states.device)
+        self._call("tmpc_obstacle_lagrangian_hessian", states, mus, H)
+        return H
+
+    def build_qp(self, states: torch.Tensor, controls: torch.Tensor) -> QPData:
+        if self._static is None:
+            D, E, q = self.cost_blocks()
+            A0, c0 = self.initial_equality()
+            box = super().inequality_blocks()
+            self._static = (D, E, q, A0, c0, self.a_plus(), box)
+        D, E, q, A0, c0, Ap, box = self._static
+        Am, c = self.dynamics_blocks(states, controls)
+        G, l, u = self.inequality_blocks_at(states, controls, box)
+        return QPData(
+            cost=QPCostBlocks(D, E, q),
+            eq=QPEqualityBlocks(A0, Am, Ap, c0, c),
+            ineq=QPInequalityBlocks(G, l, u, torch.tensor(self.slack_penalization_weight, dtype=self.dtype),
+                                    self.use_slack_variables),
+        )
+
+
+__all__ = ["ObstacleOCP"]

@@ -11,7 +11,10 @@ have closed forms:
   * dynamics (explicit branch, :1217-1272): A_minus_t = [df/dx, df/du],
     A_plus_t = [-I 0], c_t = -f(xbar, ubar) + A xbar + B ubar;
   * box bounds (:413-471): one G row per state/control coordinate with a finite
-    bound (|b| < 1e6 on either side), l/u the bounds.
+    bound (|b| < 1e6 on either side), l/u the bounds;
+  * soft constraints (SlackProblemAdapter, :1483-1544): with
+    use_slack_variables the QP carries the slack weight gamma, and the
+    inequality rows are softened to l <= G z + xi <= u with cost gamma/2 |xi|^2.
 Every tensor has a leading batch axis B.  Subclasses provide the dynamics.
 """
 from __future__ import annotations
@@ -23,6 +26,14 @@ import torch
 from ..solvers.qp_data import QPCostBlocks, QPData, QPEqualityBlocks, QPInequalityBlocks
 
 BOUND_INF = 1.0e6
+
+
+def as_tensor(t, dtype, device) -> torch.Tensor:
+    """t as a `dtype` tensor on `device`; Python and numpy numbers are converted
+    straight to `dtype` (no detour through torch's default float32)."""
+    if torch.is_tensor(t):
+        return t.to(device=device, dtype=dtype)
+    return torch.as_tensor(t, dtype=dtype, device=device)
 
 
 class QuadraticTrackingOCP:
@@ -44,6 +55,8 @@ class QuadraticTrackingOCP:
         state_bounds: Optional[Tuple[torch.Tensor, torch.Tensor]] = None,  # (nx,), (nx,)
         control_bounds: Optional[Tuple[torch.Tensor, torch.Tensor]] = None,  # (nu,), (nu,)
         initial_guess_final_state: Optional[torch.Tensor] = None,  # (B, nx)
+        use_slack_variables: bool = False,
+        slack_penalization_weight: float = 0.0,
         dtype: torch.dtype = torch.float64,
         device="cpu",
     ):
@@ -51,7 +64,7 @@ class QuadraticTrackingOCP:
         self.num_state_variables = int(num_states)
         self.num_control_variables = int(num_controls)
         self.dtype, self.device = dtype, torch.device(device)
-        cv = lambda t: torch.as_tensor(t).to(device=self.device, dtype=dtype).contiguous()  # noqa: E731
+        cv = lambda t: as_tensor(t, dtype, self.device).contiguous()  # noqa: E731
         self.x0 = cv(initial_state)
         self.B = int(self.x0.shape[0])
         T, nx, nu = self.horizon + 1, num_states, num_controls
@@ -71,6 +84,10 @@ class QuadraticTrackingOCP:
         self.control_mask = (ul > -BOUND_INF) | (uu < BOUND_INF)
         self.num_inequality_constraints = int(self.state_mask.sum() + self.control_mask.sum())
         self.x_final_guess = cv(initial_guess_final_state) if initial_guess_final_state is not None else self.x0
+        self.use_slack_variables = bool(use_slack_variables)
+        self.slack_penalization_weight = float(slack_penalization_weight)
+        if self.use_slack_variables and not self.slack_penalization_weight > 0.0:
+            raise ValueError("use_slack_variables needs a positive slack_penalization_weight")
         self.std_dynamics = True  # explicit integrators: A_plus = [-I 0], E = 0
         self.diag_cost = True  # D_t = diag(2 w): per-variable tracking weights (cost_blocks)
         self._static = None
@@ -104,8 +121,8 @@ class QuadraticTrackingOCP:
 
     def inequality_blocks(self):
         nx, nu = self.num_state_variables, self.num_control_variables
-        T, n, m = self.horizon + 1, nx + nu, self.num_inequality_constraints
         rows = [i for i in range(nx) if bool(self.state_mask[i])] + [nx + j for j in range(nu) if bool(self.control_mask[j])]
+        T, n, m = self.horizon + 1, nx + nu, len(rows)
         G1 = torch.zeros((m, n), dtype=self.dtype, device=self.device)
         for r, col in enumerate(rows):
             G1[r, col] = 1.0
@@ -124,6 +141,12 @@ class QuadraticTrackingOCP:
         optimal_control_problem.py:1334-1441)."""
         raise NotImplementedError
 
+    def inequality_lagrangian_hessian(self, states: torch.Tensor, controls: torch.Tensor, mus: torch.Tensor):
+        """(B,T,n,n) blocks sum_i mu_i d^2 g_i/dz_t^2, or None when every
+        inequality row is linear, as the box rows are
+        (get_inequality_lagrangian_hessian, optimal_control_problem.py:1443-1480)."""
+        return None
+
     # -------------------------------------------------------- parameters ----
     WEIGHT_KEYS = (
         "weights_penalization_reference_state_trajectory",
@@ -139,11 +162,16 @@ class QuadraticTrackingOCP:
 
         if not weights:
             return self
-        unknown = set(weights) - set(self.WEIGHT_KEYS)
+        unknown = set(weights) - set(self.WEIGHT_KEYS) - {"slack_penalization_weight"}
         if unknown:
             raise KeyError(f"unknown weight keys {sorted(unknown)}; expected {self.WEIGHT_KEYS}")
         other = copy.copy(self)
-        cv = lambda t, ref: torch.as_tensor(t).to(device=self.device, dtype=self.dtype).expand_as(ref).contiguous()  # noqa: E731
+        if "slack_penalization_weight" in weights:
+            gamma = weights["slack_penalization_weight"]
+            if torch.is_tensor(gamma) and gamma.numel() != 1:
+                raise ValueError("slack_penalization_weight is one scalar shared by the batch")
+            other.slack_penalization_weight = float(gamma)
+        cv = lambda t, ref: as_tensor(t, self.dtype, self.device).expand_as(ref).contiguous()  # noqa: E731
         k = self.WEIGHT_KEYS
         if k[0] in weights:
             other.wx = cv(weights[k[0]], self.wx)
@@ -162,8 +190,7 @@ class QuadraticTrackingOCP:
         if not problem_params or "initial_state" not in problem_params:
             return self
         other = copy.copy(self)
-        other.x0 = torch.as_tensor(problem_params["initial_state"]).to(
-            device=self.device, dtype=self.dtype).expand_as(self.x0).contiguous()
+        other.x0 = as_tensor(problem_params["initial_state"], self.dtype, self.device).expand_as(self.x0).contiguous()
         other._static = None
         return other
 
@@ -195,7 +222,8 @@ class QuadraticTrackingOCP:
         return QPData(
             cost=QPCostBlocks(D, E, q),
             eq=QPEqualityBlocks(A0, Am, Ap, c0, c),
-            ineq=QPInequalityBlocks(G, l, u, torch.zeros((), dtype=self.dtype), False),
+            ineq=QPInequalityBlocks(G, l, u, torch.tensor(self.slack_penalization_weight, dtype=self.dtype),
+                                    self.use_slack_variables),
         )
 
     def initial_guess(self) -> Tuple[torch.Tensor, torch.Tensor]:
@@ -236,9 +264,9 @@ class LinearOCP(QuadraticTrackingOCP):
 
     def __init__(self, *, A: torch.Tensor, Bm: torch.Tensor, b: Optional[torch.Tensor] = None, **kw):
         super().__init__(**kw)
-        self.A = torch.as_tensor(A).to(self.device, self.dtype)
-        self.Bm = torch.as_tensor(Bm).to(self.device, self.dtype)
-        self.b = (torch.as_tensor(b).to(self.device, self.dtype) if b is not None
+        self.A = as_tensor(A, self.dtype, self.device)
+        self.Bm = as_tensor(Bm, self.dtype, self.device)
+        self.b = (as_tensor(b, self.dtype, self.device) if b is not None
                   else torch.zeros((self.B, self.num_state_variables), dtype=self.dtype, device=self.device))
 
     def dynamics_lagrangian_hessian(self, states, controls, lambdas):

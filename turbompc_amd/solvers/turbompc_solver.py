@@ -224,7 +224,7 @@ class TurboMPCSolver:
             adaptive_rho_tolerance=ap.get("adaptive_rho_tolerance", 5.0),
             rho_f_factor=ap.get("rho_f_factor", ap.get("active_constraint_rho_factor", 1000.0)),
             admm_backend=self._forward_admm_backend,
-            use_slack=False,
+            use_slack=bool(getattr(program, "use_slack_variables", False)),
             std_dynamics=getattr(program, "std_dynamics", None),
             diag_cost=bool(getattr(program, "diag_cost", False)),
         )
@@ -272,6 +272,8 @@ class TurboMPCSolver:
         res = self._solve_backward_qp_direct(program, ctx, solution, dl_dslack)
         kkt = solution.kkt_state
         dL_dw = program.weight_gradient(kkt.states, kkt.controls, res.dx_states, res.dx_controls)
+        if weights and "slack_penalization_weight" in weights:
+            dL_dw["slack_penalization_weight"] = res.dL_dgamma
         cot = {"initial_state": res.dL_dx_init}
         return cot, dL_dw
 
@@ -295,7 +297,7 @@ class TurboMPCSolver:
         """The adjoint QP (`_build_backward_qp`, turbompc_solver.py:544-618): the QP
         at the solution with c0 = c = 0, q = -dL/dz, the active rows of G signed
         (+1 lower, -1 upper, 0 inactive) and, with use_full_hessian, the
-        dynamics Lagrangian Hessian added to D (:1323-1349)."""
+        dynamics and inequality Lagrangian Hessians added to D (:1323-1385)."""
         kkt = solution.kkt_state
         qp = program.build_qp(kkt.states, kkt.controls)
         D = qp.cost.D
@@ -304,7 +306,12 @@ class TurboMPCSolver:
             H = program.dynamics_lagrangian_hessian(kkt.states, kkt.controls, lambdas)
             if H is not None:
                 D = D + H
-            # the inequality rows are linear in z here (bounds): no Hessian term
+            # mu = active * y_g (:1357-1385); None when every row is linear (bounds)
+            y_g = solution.admm_state.y_g if solution.admm_state is not None else kkt.y_ineq
+            active = (kkt.ineq_active_lower_idx | kkt.ineq_active_upper_idx).to(y_g.dtype)
+            Hg = program.inequality_lagrangian_hessian(kkt.states, kkt.controls, active * y_g)
+            if Hg is not None:
+                D = D + Hg
         base = QPData(cost=QPCostBlocks(D, qp.cost.E, qp.cost.q), eq=qp.eq, ineq=qp.ineq)
         eq = QPEqualityBlocks(qp.eq.A0, qp.eq.A_minus, qp.eq.A_plus, torch.zeros_like(qp.eq.c0),
                               torch.zeros_like(qp.eq.c))
@@ -393,6 +400,10 @@ class TurboMPCSolver:
         ap = self._params["admm"]
         y_f = torch.cat([admm_state.y_f_0[:, None, : self._zshape.num_states], admm_state.y_f_dyn], dim=1)
         y_ineq = admm_state.y_g
+        if getattr(self._program, "use_slack_variables", False):
+            # soft constraints: the slack's sign marks the active side (:1413-1415)
+            slack = admm_state.xi_g
+            return KKTState(states, controls, slack, y_f, y_ineq, slack > 1.0e-12, slack < -1.0e-12)
         lo, up = identify_active_inequalities(g, l, u, ap["eps_abs"], ap["eps_rel"])
         if y_ineq.shape[-1] > 0:
             tol = ap["eps_abs"]
@@ -434,7 +445,8 @@ class TurboMPCSolver:
             # while no problem has stopped, committing is plain assignment (one
             # host sync per SQP iteration instead of a masked select per tensor)
             all_active = it == 0 or bool(active.all())
-            (s_new, c_new), stats, adm_new = admm.solve(qp, admm_state, rho_bar=ap["rho"], alpha=alpha)
+            (s_new, c_new), stats, adm_new = admm.solve(qp, admm_state, rho_bar=ap["rho"], alpha=alpha,
+                                                        slack_weight=qp.ineq.slack_penalization_weight)
             sl_new = adm_new.xi_g
             if need_step:
                 z_new = pack_z(s_new, c_new)
@@ -511,7 +523,7 @@ class _AttachSolution(torch.autograd.Function):
     @staticmethod
     def forward(ctx, solver, sol, params, weights, keys, has_x0, *inputs):
         ctx.solver, ctx.sol, ctx.params, ctx.weights, ctx.keys, ctx.has_x0 = solver, sol, params, weights, keys, has_x0
-        ctx.shapes = [t.shape for t in inputs]
+        ctx.metas = [(t.shape, t.device, t.dtype) for t in inputs]
         return sol.states.clone(), sol.controls.clone()
 
     @staticmethod
@@ -519,7 +531,7 @@ class _AttachSolution(torch.autograd.Function):
         cot, dw = ctx.solver.solve_vjp(ctx.sol, g_states, g_controls, None, ctx.params, ctx.weights)
         grads = ([cot["initial_state"]] if ctx.has_x0 else []) + [dw[k] for k in ctx.keys]
         # inputs shared across the batch get the batch sum of their per-problem gradients
-        grads = [g.sum_to_size(shape) for g, shape in zip(grads, ctx.shapes)]
+        grads = [g.sum_to_size(shape).to(device=dev, dtype=dt) for g, (shape, dev, dt) in zip(grads, ctx.metas)]
         return (None, None, None, None, None, None, *grads)
 
 
