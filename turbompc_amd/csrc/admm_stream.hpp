@@ -923,7 +923,12 @@ __global__ __launch_bounds__(kWave) void factor_std_kernel(Dims d, const R* __re
         }
       }
     }
-    // Gauss-Jordan inversion without pivoting, rows in lanes
+    // Gauss-Jordan inversion without pivoting, rows in lanes.  The pivot row k
+    // is not normalized at its step: it keeps the scale p_k (its diagonal entry
+    // holds 1 instead of 1/p_k), which the later row operations carry along,
+    // and is multiplied by 1/p_k after the last step.  So every step runs the
+    // same instructions in every lane (no divergent pivot-row branch).
+    C myip = C(0);
 #pragma unroll
     for (int k = 0; k < NC; ++k) {
       wsync();
@@ -937,17 +942,17 @@ __global__ __launch_bounds__(kWave) void factor_std_kernel(Dims d, const R* __re
         for (int j = 0; j < NC; ++j) pv[j] = piv[j];
         __builtin_amdgcn_sched_barrier(0);
         const C ip = C(1) / pv[k];
-        if (i == k) {
+        const bool me = i == k;
+        myip = me ? ip : myip;
+        const C g = me ? C(0) : a[k] * ip;
 #pragma unroll
-          for (int j = 0; j < NC; ++j) a[j] = (j == k) ? ip : a[j] * ip;
-        } else {
-          const C f = a[k];
-#pragma unroll
-          for (int j = 0; j < NC; ++j) a[j] = (j == k) ? -f * ip : a[j] - f * pv[j] * ip;
-        }
+        for (int j = 0; j < NC; ++j) a[j] = (j == k) ? (me ? C(1) : -g) : a[j] - g * pv[j];
       }
     }
     wsync();
+    if (i < n)
+#pragma unroll
+      for (int j = 0; j < NC; ++j) a[j] *= myip;
     if (i < n) {
 #pragma unroll
       for (int j = 0; j < NC; ++j) th[i * n + j] = a[j];

@@ -181,6 +181,14 @@ inline int stream_problems_per_wave(int B, uint32_t flags) {
   return forced ? forced : std::max(1, std::min(3, B / 2048));
 }
 
+// The factorization is bound by instruction issue rather than latency, so it
+// packs more problems per wavefront (fewer instructions per problem) as soon
+// as that still leaves about one wavefront per SIMD.
+inline int factor_problems_per_wave(int B, uint32_t flags) {
+  const int forced = (int)((flags >> 8) & 3u);
+  return forced ? forced : std::max(1, std::min(3, B / 1024));
+}
+
 template <typename R>
 bool stream_ok(const Dims& d, int P, bool diag) {
   if (!(d.n == 6 || d.n == 9 || d.n == 16 || d.n == 17)) return false;
@@ -338,6 +346,7 @@ int admm_direct_impl(hipStream_t s, const tmpc_dims* dims, const tmpc_qp* qp,
   a.P = kWave / a.g;
   const bool std_dyn = (cfg->flags & TMPC_FLAG_STD_DYNAMICS) != 0;
   const int sp = stream_problems_per_wave(d.B, cfg->flags);
+  const int fp = factor_problems_per_wave(d.B, cfg->flags);
   const bool diag = (cfg->flags & TMPC_FLAG_DIAG_COST) != 0;
   const bool stream = std_dyn && (cfg->flags & TMPC_FLAG_GENERIC_KERNEL) == 0 && stream_ok<R>(d, sp, diag);
   if (stream) {
@@ -345,7 +354,7 @@ int admm_direct_impl(hipStream_t s, const tmpc_dims* dims, const tmpc_qp* qp,
                        diag ? 1 : 0);
     st = launch_status();
     if (st) return st;
-    st = launch_factor_std<R>(s, d, w, a.qp, a.st.rho, a.sigma, a.rho_f_factor, nullptr, sp, diag);
+    st = launch_factor_std<R>(s, d, w, a.qp, a.st.rho, a.sigma, a.rho_f_factor, nullptr, fp, diag);
   } else {
     st = launch_factor_qp<R>(s, d, a.qp, a.st.rho, a.sigma, a.rho_f_factor, nullptr, w.thinv);
   }
@@ -354,7 +363,7 @@ int admm_direct_impl(hipStream_t s, const tmpc_dims* dims, const tmpc_qp* qp,
   if (g_iter_events[0] && hipEventRecord(g_iter_events[0], s) != hipSuccess) return TMPC_ELAUNCH;
   for (size_t c = 0; c + 1 < bounds.size(); ++c) {
     if (c > 0) {
-      st = stream ? launch_factor_std<R>(s, d, w, a.qp, a.st.rho, a.sigma, a.rho_f_factor, w.ctl, sp, diag)
+      st = stream ? launch_factor_std<R>(s, d, w, a.qp, a.st.rho, a.sigma, a.rho_f_factor, w.ctl, fp, diag)
                   : launch_factor_qp<R>(s, d, a.qp, a.st.rho, a.sigma, a.rho_f_factor, w.ctl, w.thinv);
       if (st) return st;
     }
