@@ -117,9 +117,10 @@ struct StreamLayout {
   int th;   // [DPF][P][pitch]    Theta_t^{-1}
   int rv;   // [DPF][P][rvp]
   int dm;   // [DPF][P][dmp]      D_t (iterations that evaluate the residuals)
-  int am;   // [DPF][P][amp]      (then n x n zeros)
+  int am;   // [max(DPF, 2)][P][amp] (then n x n zeros)
   int a0;   // [P][n0 n]
   int vec;  // [kNV][64]
+  int spill;  // 16-byte dump for the stores of lanes past a run
   int total;
 };
 
@@ -131,14 +132,16 @@ __host__ __device__ inline StreamLayout stream_layout(const Dims& d, int P, int 
   L.rv = L.th + DPF * P * th_pitch(d.n);
   L.dm = L.rv + DPF * P * g.rvp;
   L.am = L.dm + DPF * P * g.dmp;
-  int end = L.am + DPF * P * g.amp;
+  // at least two M slots: the backward sweep holds the blocks of stages t and t-1
+  int end = L.am + (DPF > 2 ? DPF : 2) * P * g.amp;
   if (end < L.th + 12 * kWave) end = L.th + 12 * kWave;  // the residual reduction reuses the slots
   // n x n zeros: column products read all NC rows of a block, so the rows past
   // the last stacked block land here (rows past other blocks land on the
   // next block's data); every such row meets a zero vector entry
   L.a0 = up4(end + d.n * d.n);
   L.vec = up4(L.a0 + P * d.n0 * d.n);
-  L.total = L.vec + kNV * kWave;
+  L.spill = L.vec + kNV * kWave;
+  L.total = L.spill + 4;
   return L;
 }
 
@@ -245,13 +248,32 @@ __global__ __launch_bounds__(kWave) void stage_unpack_kernel(Dims d, const R* __
 
 // ---- wavefront helpers ---------------------------------------------------------
 
+// A run of nch 16-byte chunks, chunk c * 64 + lane in register r[c].  No
+// branches: the loads go through a buffer resource whose range is the run
+// (lanes past it read zeros), and lanes past the run store to `spill`, a
+// 16-byte LDS dump, so every chunk costs the same instructions in every lane
+// instead of an exec-mask branch.  `src` is wavefront-uniform.
+constexpr int kBufferFlags = 0x00020000;  // dword 3 of a raw buffer resource (gfx9 family)
+
 template <typename V, int CH>
 __device__ __forceinline__ void load_run(V (&r)[CH], const V* __restrict__ src, int nch) {
+  const __amdgpu_buffer_rsrc_t rs =
+      __builtin_amdgcn_make_buffer_rsrc(const_cast<V*>(src), (short)0, nch * 16, kBufferFlags);
+  const unsigned tid = threadIdx.x;
+#pragma unroll
+  for (int c = 0; c < CH; ++c) {
+    const int off = (int)((c * kWave + tid) * 16u);
+    r[c] = __builtin_bit_cast(V, __builtin_amdgcn_raw_buffer_load_b128(rs, off, 0, 0));
+  }
+}
+
+template <typename V, int CH>
+__device__ __forceinline__ void store_run(const V (&r)[CH], V* dst, int nch, V* spill) {
   const unsigned tid = threadIdx.x;
 #pragma unroll
   for (int c = 0; c < CH; ++c) {
     const unsigned e = c * kWave + tid;
-    if (e < (unsigned)nch) r[c] = src[e];
+    *(e < (unsigned)nch ? dst + e : spill) = r[c];
   }
 }
 
@@ -284,22 +306,22 @@ __device__ __forceinline__ R lrow(const R* A, int i, const R* v) {
   for (int k = 0; k < NC; ++k) acc += ak[k] * vk[k];
   return acc;
 }
-// All NC rows are read: the caller keeps v[r] = 0 for r >= rows and every
+// All NR rows are read: the caller keeps v[r] = 0 for r >= rows and every
 // row read finite (LDS is zeroed at kernel start; rows past a block land on
 // finite data), so the rows past `rows` add exact zeros.
-template <typename R, int NC>
+template <typename R, int NC, int NR = NC>
 __device__ __forceinline__ R lcol(const R* A, int rows, int i, const R* v) {
   (void)rows;
-  R ak[NC], vk[NC];
+  R ak[NR], vk[NR];
 #pragma unroll
-  for (int r = 0; r < NC; ++r) {
+  for (int r = 0; r < NR; ++r) {
     ak[r] = A[r * NC + i];
     vk[r] = v[r];
   }
   __builtin_amdgcn_sched_barrier(0);
   R acc = R(0);
 #pragma unroll
-  for (int r = 0; r < NC; ++r) acc += ak[r] * vk[r];
+  for (int r = 0; r < NR; ++r) acc += ak[r] * vk[r];
   return acc;
 }
 // Row i of a packed symmetric (lower) block times v.
@@ -354,6 +376,7 @@ __global__ __launch_bounds__(kWave, StreamOcc<R>::waves) void admm_stream_kernel
   using V = typename Vec16<R>::T;
   using K = StreamShape<R, NC, P>;
   constexpr int n = NC, PITCH = K::PITCH, W = K::W;
+  constexpr int NL = NC;  // lanes of a problem's group that own a row
   constexpr int CH_TH = K::CH_TH, CH_AM = K::CH_AM, CH_RV = K::CH_RV;
   extern __shared__ __align__(16) unsigned char smem_raw[];
   R* lds = reinterpret_cast<R*>(smem_raw);
@@ -373,6 +396,7 @@ __global__ __launch_bounds__(kWave, StreamOcc<R>::waves) void admm_stream_kernel
   const R alpha = a.alpha, one_m_alpha = R(1) - a.alpha, sigma = a.sigma;
 
   R* wgp = lds + L.wg + p * T * n;
+  V* spl = reinterpret_cast<V*>(lds + L.spill);
   R* vec = lds + L.vec;
   R* sr = vec + 0 * kWave + base;
   R* su = vec + 1 * kWave + base;
@@ -382,7 +406,7 @@ __global__ __launch_bounds__(kWave, StreamOcc<R>::waves) void admm_stream_kernel
   R* sc0 = vec + 5 * kWave + base;
   R* sy = vec + 6 * kWave + base;   // new stacked duals [y_f; y_g] (residuals)
   R* sy0 = vec + 7 * kWave + base;  // new y_f0 (residuals)
-  R* sxn = su;  // the relaxed iterate for the residuals (su is free then)
+  R* sxn = sr;  // the relaxed iterate for the residuals (sr is free in the backward sweep)
   const int nr = nx + m;            // stacked constraint rows of a stage
   const bool dyn = i < nx, ineq = i >= nx && i < nr;
   const int ji = ineq ? i - nx : 0;  // inequality index of an inequality row
@@ -441,8 +465,8 @@ __global__ __launch_bounds__(kWave, StreamOcc<R>::waves) void admm_stream_kernel
           load_run<V, CH_RV>(r.rv, rv_run(t), nch_rv);
         },
         [&](GRegs& r, int j) {
-          store_run<V, CH_AM>(r.am, reinterpret_cast<V*>(amS(j)), nch_am);
-          store_run<V, CH_RV>(r.rv, reinterpret_cast<V*>(rvS(j)), nch_rv);
+          store_run<V, CH_AM>(r.am, reinterpret_cast<V*>(amS(j)), nch_am, spl);
+          store_run<V, CH_RV>(r.rv, reinterpret_cast<V*>(rvS(j)), nch_rv, spl);
         },
         [&](int j, int t) {
           const R* mt = amS(j) + p * amp;
@@ -491,8 +515,8 @@ __global__ __launch_bounds__(kWave, StreamOcc<R>::waves) void admm_stream_kernel
             if (t < N) load_run<V, CH_AM>(r.am, am_run(t), nch_am);
           },
           [&](FRegs& r, int j) {
-            store_run<V, CH_TH>(r.th, reinterpret_cast<V*>(thS(j)), nch_th);
-            store_run<V, CH_AM>(r.am, reinterpret_cast<V*>(amS(j)), nch_am);
+            store_run<V, CH_TH>(r.th, reinterpret_cast<V*>(thS(j)), nch_th, spl);
+            store_run<V, CH_AM>(r.am, reinterpret_cast<V*>(amS(j)), nch_am, spl);
           },
           [&](int j, int t) {
             R rr = i < n ? wgp[t * n + i] : R(0);
@@ -506,182 +530,203 @@ __global__ __launch_bounds__(kWave, StreamOcc<R>::waves) void admm_stream_kernel
     }
 
     // ---- backward sweep fused with the ADMM updates, the next gamma and (on
-    // checking iterations) the residuals of the new iterate (admm.py:392-556)
+    // checking iterations) the residuals of the new iterate (admm.py:392-556).
+    //
+    // Software-pipelined over two stages: step t runs the recursion part of
+    // stage t-1 (A: xt_{t-1} = w_{t-1} - Theta_{t-1}^{-1} rho_f A_minus_{t-1}^T
+    // (-xt_t), the only dependence between stages) together with the rest of
+    // stage t (B: constraint products, relaxation, projection, duals, the next
+    // gamma_t, residual terms), which needs xt_t only.  A and B share each of
+    // the three barrier-separated regions of a step, so their LDS round trips
+    // overlap.  LDS slots: Theta^{-1} of stage t-1; M of stages t and t-1 (by
+    // stage parity); rv and D of stage t.  Registers prefetch the next step's
+    // runs (Theta^{-1}, M of t-2; rv, D of t-1).
     const bool chk = mod_zero(iter, a.check_every);
     R rp = 0, nCx = 0, nc = 0, nGx = 0, nz = 0, rd = 0, nPx = 0, nAty = 0, nq = 0, nxi = 0, nyg = 0;
     {
-      struct BRegs {
-        V th[CH_TH], am[CH_AM], rv[CH_RV], dm[CH_TH];
-      };
+      V pth[CH_TH], pam[CH_AM], prv[CH_RV], pdm[CH_TH];
+      auto amP = [&](int t) { return lds + L.am + (t & 1) * (P * amp); };
+      R* th_slot = thS(0);
+      R* rv_slot = rvS(0);
+      R* dm_slot = dmS(0);
+      // prologue: M_{T-1} into its slot; registers <- Theta^{-1}, M of T-2 and rv, D of T-1
+      load_run<V, CH_AM>(pam, am_run(T - 1), nch_am);
+      store_run<V, CH_AM>(pam, reinterpret_cast<V*>(amP(T - 1)), nch_am, spl);
+      if (T >= 2) {
+        load_run<V, CH_TH>(pth, th_run(T - 2), nch_th);
+        load_run<V, CH_AM>(pam, am_run(T - 2), nch_am);
+      }
+      load_run<V, CH_RV>(prv, rv_run(T - 1), nch_rv);
+      if (chk) load_run<V, CH_TH>(pdm, dm_run(T - 1), nch_dm);
+      R xa = i < n ? wgp[N * n + i] : R(0);  // xt_t for the coming step (xt_N = w_N)
       R xn = R(0);   // xt_{t+1}[i]
       R xnn = R(0);  // relaxed x_{t+1}[i]
       R gp = R(0);   // gamma_{t+1}[i] awaiting its A_plus_t^T term
       // dual residual row t+1 awaiting its A_plus_t^T y_f_t term (i < nx):
       // P x + q and the rest of C^T y + G^T y_g
       R pq_p = R(0), aty_p = R(0);
-      run_sweep<DPF, BRegs>(
-          T, false,
-          [&](BRegs& r, int t) {
-            load_run<V, CH_TH>(r.th, th_run(t), nch_th);
-            load_run<V, CH_AM>(r.am, am_run(t), nch_am);
-            load_run<V, CH_RV>(r.rv, rv_run(t), nch_rv);
-            if (chk) load_run<V, CH_TH>(r.dm, dm_run(t), nch_dm);
-          },
-          [&](BRegs& r, int j) {
-            store_run<V, CH_TH>(r.th, reinterpret_cast<V*>(thS(j)), nch_th);
-            store_run<V, CH_AM>(r.am, reinterpret_cast<V*>(amS(j)), nch_am);
-            store_run<V, CH_RV>(r.rv, reinterpret_cast<V*>(rvS(j)), nch_rv);
-            if (chk) store_run<V, CH_TH>(r.dm, reinterpret_cast<V*>(dmS(j)), nch_dm);
-          },
-          [&](int j, int t) {
-            const R* th = thS(j) + p * PITCH;
-            const R* mt = amS(j) + p * amp;  // [A_minus_t; G_t]
-            const R* rv = rvS(j) + p * rvp;
-            R* rvg = a.rv + ((size_t)t * B + b0) * rvp + rv_lane;  // this problem's record in HBM
-            const bool drow = dyn && t < N;  // a live dynamics row
-            const R wv = i < n ? wgp[t * n + i] : R(0);
-            R xt = wv;
-            R u = R(0);  // (A_plus_t xt_{t+1})[i] = -xt_{t+1}[i], i < nx
-            if (t < N) {
-              u = dyn ? -xn : R(0);
-              if (i < NC) su[i] = u;  // 0 past nx
-              wsync();
-              if (i < n) ss[i] = rho_f * lcol<R, NC>(mt, nx, i, su);
-              wsync();
-              if (i < n) xt = wv - lsym<R, NC>(th, i, ss);
-            }
-            if (i < n) sx[i] = xt;
-            wsync();
-            // stacked C and G products of the pre-relaxation iterate
-            R mx = R(0), cx0 = R(0);
-            if (i < nr) mx = lrow<R, NC>(mt, i, sx);
-            if (t == 0 && i < n0) cx0 = lrow<R, NC>(a0p, i, sx);
-            // over-relaxation
-            R xnew = R(0);
-            if (i < n) {
-              xnew = alpha * xt + one_m_alpha * rv[rg.x + i];
-              if (commit) rvg[rg.x + i] = xnew;
-            }
-            // constraint row i: the dual, the next gamma's entry, and (inequality
-            // rows) the box projection / slack
-            R tgt = R(0), y_r = R(0), z_r = R(0), xi_r = R(0);
-            if (ineq) {
-              const R zo = rv[rg.cz + i], ygo = rv[rg.y + i];
-              const R zt = alpha * mx + one_m_alpha * zo + ygo / rho;
-              const R proj = rmin(rmax(zt, rv[rg.l + ji]), rv[rg.u + ji]);
-              R zn, xin;
-              if (a.use_slack) {
-                const R frac = gs / (gs + rho);
-                zn = (R(1) - frac) * zt + frac * proj;
-                xin = (rho / (gs + rho)) * (proj - zt);
-              } else {
-                zn = proj;
-                xin = R(0);
-              }
-              const R ygn = ygo + rho * (alpha * mx + one_m_alpha * zo - zn);
-              if (commit) {
-                rvg[rg.cz + i] = zn;
-                rvg[rg.xi + ji] = xin;
-                rvg[rg.y + i] = ygn;
-              }
-              tgt = rho * zn - ygn;
-              y_r = ygn;
-              z_r = zn;
-              xi_r = xin;
-            }
-            if (drow) {
-              const R cx = mx + u;
+      for (int t = T - 1; t >= 0; --t) {
+        const bool hasA = t >= 1;  // the recursion part of stage t-1 runs in this step
+        // ---- region 1: stage the runs; su for A, sx for B
+        if (hasA) {
+          store_run<V, CH_TH>(pth, reinterpret_cast<V*>(th_slot), nch_th, spl);
+          store_run<V, CH_AM>(pam, reinterpret_cast<V*>(amP(t - 1)), nch_am, spl);
+        }
+        store_run<V, CH_RV>(prv, reinterpret_cast<V*>(rv_slot), nch_rv, spl);
+        if (chk) store_run<V, CH_TH>(pdm, reinterpret_cast<V*>(dm_slot), nch_dm, spl);
+        if (i < NL) su[i] = dyn ? -xa : R(0);  // A_plus_{t-1} xt_t, 0 past nx
+        if (i < n) sx[i] = xa;
+        wsync();
+        if (t >= 2) {
+          load_run<V, CH_TH>(pth, th_run(t - 2), nch_th);
+          load_run<V, CH_AM>(pam, am_run(t - 2), nch_am);
+        }
+        if (t >= 1) {
+          load_run<V, CH_RV>(prv, rv_run(t - 1), nch_rv);
+          if (chk) load_run<V, CH_TH>(pdm, dm_run(t - 1), nch_dm);
+        }
+        // ---- region 2
+        const R* mA = amP(t - 1) + p * amp;  // M_{t-1} (A)
+        const R* mt = amP(t) + p * amp;      // M_t = [A_minus_t; G_t] (B)
+        const R* rv = rv_slot + p * rvp;
+        R* rvg = a.rv + ((size_t)t * B + b0) * rvp + rv_lane;  // this problem's record in HBM
+        if (hasA && i < n) ss[i] = rho_f * lcol<R, NC, NL>(mA, nx, i, su);
+        const bool drow = dyn && t < N;  // a live dynamics row of stage t
+        const R u = (dyn && t < N) ? -xn : R(0);  // (A_plus_t xt_{t+1})[i]
+        // stacked C and G products of the pre-relaxation iterate
+        R mx = R(0), cx0 = R(0);
+        if (i < nr) mx = lrow<R, NC>(mt, i, sx);
+        if (t == 0 && i < n0) cx0 = lrow<R, NC>(a0p, i, sx);
+        // over-relaxation
+        R xnew = R(0);
+        if (i < n) {
+          xnew = alpha * xa + one_m_alpha * rv[rg.x + i];
+          if (commit) rvg[rg.x + i] = xnew;
+        }
+        // constraint row i: the dual, the next gamma's entry, and (inequality
+        // rows) the box projection / slack
+        R tgt = R(0), y_r = R(0), z_r = R(0), xi_r = R(0);
+        if (ineq) {
+          const R zo = rv[rg.cz + i], ygo = rv[rg.y + i];
+          const R zt = alpha * mx + one_m_alpha * zo + ygo / rho;
+          const R proj = rmin(rmax(zt, rv[rg.l + ji]), rv[rg.u + ji]);
+          R zn, xin;
+          if (a.use_slack) {
+            const R frac = gs / (gs + rho);
+            zn = (R(1) - frac) * zt + frac * proj;
+            xin = (rho / (gs + rho)) * (proj - zt);
+          } else {
+            zn = proj;
+            xin = R(0);
+          }
+          const R ygn = ygo + rho * (alpha * mx + one_m_alpha * zo - zn);
+          if (commit) {
+            rvg[rg.cz + i] = zn;
+            rvg[rg.xi + ji] = xin;
+            rvg[rg.y + i] = ygn;
+          }
+          tgt = rho * zn - ygn;
+          y_r = ygn;
+          z_r = zn;
+          xi_r = xin;
+        }
+        if (drow) {
+          const R cx = mx + u;
+          const R cv = rv[rg.cz + i];
+          const R yf = rv[rg.y + i] + rho_f * (alpha * cx + one_m_alpha * cv - cv);
+          if (commit) rvg[rg.y + i] = yf;
+          tgt = rho_f * cv - yf;
+          y_r = yf;
+        }
+        R ct0 = R(0), yf0_r = R(0);
+        if (t == 0 && i < n0) {
+          const R yf = yf0v + rho_f * (alpha * cx0 + one_m_alpha * c0v - c0v);
+          if (commit) {
+            a.y_f0[(size_t)b * n0 + i] = yf;
+            yf0v = yf;
+          }
+          ct0 = rho_f * c0v - yf;
+          yf0_r = yf;
+        }
+        // next iteration's gamma (valid while rho is unchanged)
+        if (i < NL) sc[i] = tgt;   // 0 past nr
+        if (i < NL) sc0[i] = ct0;  // 0 past n0
+        if (chk) {
+          if (i < n) sxn[i] = xnew;
+          if (i < NL) sy[i] = y_r;     // 0 past nr
+          if (i < NL) sy0[i] = yf0_r;  // 0 past n0
+        }
+        wsync();
+        // ---- region 3
+        R xa_next = R(0);
+        if (hasA && i < n) xa_next = wgp[(t - 1) * n + i] - lsym<R, NC>(th_slot + p * PITCH, i, ss);
+        if (t < N) {
+          if (dyn) gp -= tgt;  // A_plus_t^T = [-I; 0]
+          if (i < n) wgp[(t + 1) * n + i] = gp;
+        }
+        if (i < n) {
+          R gv = sigma * xnew - rv[rg.q + i];
+          gv += lcol<R, NC, NL>(mt, nr, i, sc);
+          if (t == 0) gv += lcol<R, NC, NC>(a0p, n0, i, sc0);
+          gp = gv;
+        }
+        if (chk) {
+          // dual residual row t+1 is complete with -[y_f_t; 0]
+          if (drow) {
+            const R aty = aty_p - y_r;
+            rd = rmax(rd, rabs(pq_p + aty));
+            nAty = rmax(nAty, rabs(aty));
+          }
+          // stacked primal rows of the relaxed iterate
+          if (i < nr) {
+            const R m1 = lrow<R, NC>(mt, i, sxn);
+            if (drow) {  // A_minus_t x_t - x_{t+1} - c_t
+              const R cx1 = m1 - xnn;
               const R cv = rv[rg.cz + i];
-              const R yf = rv[rg.y + i] + rho_f * (alpha * cx + one_m_alpha * cv - cv);
-              if (commit) rvg[rg.y + i] = yf;
-              tgt = rho_f * cv - yf;
-              y_r = yf;
+              rp = rmax(rp, rabs(cx1 - cv));
+              nCx = rmax(nCx, rabs(cx1));
+              nc = rmax(nc, rabs(cv));
             }
-            R ct0 = R(0), yf0_r = R(0);
-            if (t == 0 && i < n0) {
-              const R yf = yf0v + rho_f * (alpha * cx0 + one_m_alpha * c0v - c0v);
-              if (commit) {
-                a.y_f0[(size_t)b * n0 + i] = yf;
-                yf0v = yf;
-              }
-              ct0 = rho_f * c0v - yf;
-              yf0_r = yf;
-            }
-            // next iteration's gamma (valid while rho is unchanged)
-            if (i < NC) sc[i] = tgt;   // 0 past nr
-            if (i < NC) sc0[i] = ct0;  // 0 past n0
-            if (chk) {
-              if (i < n) sxn[i] = xnew;
-              if (i < NC) sy[i] = y_r;     // 0 past nr
-              if (i < NC) sy0[i] = yf0_r;  // 0 past n0
-            }
-            wsync();
-            if (t < N) {
-              if (dyn) gp -= tgt;  // A_plus_t^T = [-I; 0]
-              if (i < n) wgp[(t + 1) * n + i] = gp;
-            }
-            if (i < n) {
-              R gv = sigma * xnew - rv[rg.q + i];
-              gv += lcol<R, NC>(mt, nr, i, sc);
-              if (t == 0) gv += lcol<R, NC>(a0p, n0, i, sc0);
-              gp = gv;
-            }
-            if (chk) {
-              // dual residual row t+1 is complete with -[y_f_t; 0]
-              if (drow) {
-                const R aty = aty_p - y_r;
-                rd = rmax(rd, rabs(pq_p + aty));
-                nAty = rmax(nAty, rabs(aty));
-              }
-              // stacked primal rows of the relaxed iterate
-              if (i < nr) {
-                const R m1 = lrow<R, NC>(mt, i, sxn);
-                if (drow) {  // A_minus_t x_t - x_{t+1} - c_t
-                  const R cx1 = m1 - xnn;
-                  const R cv = rv[rg.cz + i];
-                  rp = rmax(rp, rabs(cx1 - cv));
-                  nCx = rmax(nCx, rabs(cx1));
-                  nc = rmax(nc, rabs(cv));
-                }
-                if (ineq) {
-                  rp = rmax(rp, rabs(m1 - z_r));
-                  nGx = rmax(nGx, rabs(m1));
-                  nz = rmax(nz, rabs(z_r));
-                  if (slack) {
-                    rd = rmax(rd, rabs(gs * xi_r + y_r));
-                    nxi = rmax(nxi, rabs(xi_r));
-                    nyg = rmax(nyg, rabs(y_r));
-                  }
-                }
-              }
-              if (t == 0 && i < n0) {
-                const R cx1 = lrow<R, NC>(a0p, i, sxn);
-                rp = rmax(rp, rabs(cx1 - c0v));
-                nCx = rmax(nCx, rabs(cx1));
-                nc = rmax(nc, rabs(c0v));
-              }
-              if (i < n) {
-                const R* dmt = dmS(j) + p * dmp;
-                const R px = diagD ? dmt[i] * xnew : lsym<R, NC>(dmt, i, sxn);
-                R aty = R(0);
-                if (t == 0) aty += lcol<R, NC>(a0p, n0, i, sy0);
-                aty += lcol<R, NC>(mt, nr, i, sy);  // A_minus_t^T y_f_t + G_t^T y_g_t
-                const R qv = rv[rg.q + i];
-                if (t > 0 && dyn) {  // awaits -y_f_{t-1}[i]
-                  pq_p = px + qv;
-                  aty_p = aty;
-                } else {
-                  rd = rmax(rd, rabs(px + qv + aty));
-                  nAty = rmax(nAty, rabs(aty));
-                }
-                nPx = rmax(nPx, rabs(px));
-                nq = rmax(nq, rabs(qv));
+            if (ineq) {
+              rp = rmax(rp, rabs(m1 - z_r));
+              nGx = rmax(nGx, rabs(m1));
+              nz = rmax(nz, rabs(z_r));
+              if (slack) {
+                rd = rmax(rd, rabs(gs * xi_r + y_r));
+                nxi = rmax(nxi, rabs(xi_r));
+                nyg = rmax(nyg, rabs(y_r));
               }
             }
-            xn = xt;
-            xnn = xnew;
-            wsync();
-          });
+          }
+          if (t == 0 && i < n0) {
+            const R cx1 = lrow<R, NC>(a0p, i, sxn);
+            rp = rmax(rp, rabs(cx1 - c0v));
+            nCx = rmax(nCx, rabs(cx1));
+            nc = rmax(nc, rabs(c0v));
+          }
+          if (i < n) {
+            const R* dmt = dm_slot + p * dmp;
+            const R px = diagD ? dmt[i] * xnew : lsym<R, NC>(dmt, i, sxn);
+            R aty = R(0);
+            if (t == 0) aty += lcol<R, NC, NC>(a0p, n0, i, sy0);
+            aty += lcol<R, NC, NL>(mt, nr, i, sy);  // A_minus_t^T y_f_t + G_t^T y_g_t
+            const R qv = rv[rg.q + i];
+            if (t > 0 && dyn) {  // awaits -y_f_{t-1}[i]
+              pq_p = px + qv;
+              aty_p = aty;
+            } else {
+              rd = rmax(rd, rabs(px + qv + aty));
+              nAty = rmax(nAty, rabs(aty));
+            }
+            nPx = rmax(nPx, rabs(px));
+            nq = rmax(nq, rabs(qv));
+          }
+        }
+        xn = xa;
+        xnn = xnew;
+        xa = xa_next;
+        wsync();
+      }
       if (i < n) wgp[i] = gp;
       wsync();
     }
