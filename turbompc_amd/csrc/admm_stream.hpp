@@ -108,6 +108,10 @@ struct StreamShape {
 
 constexpr int kNV = 8;  // per-lane broadcast vectors in LDS
 
+// One broadcast vector holds P group slots of up4(64 / P) entries, so that
+// every group's slot starts on a 16-byte boundary (16-byte vector reads).
+__host__ __device__ inline constexpr int vec_stride(int P) { return P * up4(kWave / P); }
+
 // LDS layout in elements of R (host and device agree).  The DPF Theta^{-1}
 // slots come first at a compile-time stride (P x pitch), so one set of
 // per-lane row addresses serves every slot through the immediate offset of
@@ -119,7 +123,7 @@ struct StreamLayout {
   int dm;   // [DPF][P][dmp]      D_t (iterations that evaluate the residuals)
   int am;   // [max(DPF, 2)][P][amp] (then n x n zeros)
   int a0;   // [P][n0 n]
-  int vec;  // [kNV][64]
+  int vec;  // [kNV][vec_stride(P)]
   int spill;  // 16-byte dump for the stores of lanes past a run
   int total;
 };
@@ -140,7 +144,7 @@ __host__ __device__ inline StreamLayout stream_layout(const Dims& d, int P, int 
   // next block's data); every such row meets a zero vector entry
   L.a0 = up4(end + d.n * d.n);
   L.vec = up4(L.a0 + P * d.n0 * d.n);
-  L.spill = L.vec + kNV * kWave;
+  L.spill = L.vec + kNV * vec_stride(P);
   L.total = L.spill + 4;
   return L;
 }
@@ -267,6 +271,18 @@ __device__ __forceinline__ void load_run(V (&r)[CH], const V* __restrict__ src, 
   }
 }
 
+// Stores element `elem` of a buffer when `on`; otherwise the offset lies past
+// any range and the hardware drops the store (no exec-mask branch).
+__device__ __forceinline__ void buf_store(float v, __amdgpu_buffer_rsrc_t rs, bool on, unsigned elem) {
+  const int off = on ? (int)(elem * 4u) : (int)0x80000000u;
+  __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(int, v), rs, off, 0, 0);
+}
+__device__ __forceinline__ void buf_store(double v, __amdgpu_buffer_rsrc_t rs, bool on, unsigned elem) {
+  typedef int i32x2 __attribute__((ext_vector_type(2)));
+  const int off = on ? (int)(elem * 8u) : (int)0x80000000u;
+  __builtin_amdgcn_raw_buffer_store_b64(__builtin_bit_cast(i32x2, v), rs, off, 0, 0);
+}
+
 template <typename V, int CH>
 __device__ __forceinline__ void store_run(const V (&r)[CH], V* dst, int nch, V* spill) {
   const unsigned tid = threadIdx.x;
@@ -291,15 +307,36 @@ __device__ __forceinline__ void store_run(const V (&r)[CH], V* dst, int nch) {
 // The dot products first issue all their LDS reads, then (after a scheduling
 // barrier) the FMAs: left alone, the compiler interleaves one read pair with
 // one FMA pair and waits for every pair.
-template <typename R, int NC>
+// The vector operand of the dot products is the same for all lanes of a
+// group; it is read with 16-byte loads (4 floats or 2 doubles per LDS
+// instruction) when it is 16-byte aligned (VA).
+template <typename R, int N, bool VA>
+__device__ __forceinline__ void lds_vec(const R* v, R (&out)[N]) {
+  if constexpr (VA) {
+    using V = typename Vec16<R>::T;
+    constexpr int W = Vec16<R>::W;
+    const V* v4 = reinterpret_cast<const V*>(v);
+#pragma unroll
+    for (int q = 0; q < N / W; ++q) {
+      const V c = v4[q];
+#pragma unroll
+      for (int w = 0; w < W; ++w) out[q * W + w] = c[w];
+    }
+#pragma unroll
+    for (int k = (N / W) * W; k < N; ++k) out[k] = v[k];
+  } else {
+#pragma unroll
+    for (int k = 0; k < N; ++k) out[k] = v[k];
+  }
+}
+
+template <typename R, int NC, bool VA = true>
 __device__ __forceinline__ R lrow(const R* A, int i, const R* v) {
   R ak[NC], vk[NC];
   const R* a = A + i * NC;
 #pragma unroll
-  for (int k = 0; k < NC; ++k) {
-    ak[k] = a[k];
-    vk[k] = v[k];
-  }
+  for (int k = 0; k < NC; ++k) ak[k] = a[k];
+  lds_vec<R, NC, VA>(v, vk);
   __builtin_amdgcn_sched_barrier(0);
   R acc = R(0);
 #pragma unroll
@@ -314,10 +351,8 @@ __device__ __forceinline__ R lcol(const R* A, int rows, int i, const R* v) {
   (void)rows;
   R ak[NR], vk[NR];
 #pragma unroll
-  for (int r = 0; r < NR; ++r) {
-    ak[r] = A[r * NC + i];
-    vk[r] = v[r];
-  }
+  for (int r = 0; r < NR; ++r) ak[r] = A[r * NC + i];
+  lds_vec<R, NR, true>(v, vk);
   __builtin_amdgcn_sched_barrier(0);
   R acc = R(0);
 #pragma unroll
@@ -333,8 +368,8 @@ __device__ __forceinline__ R lsym(const R* Th, int i, const R* v) {
   for (int k = 0; k < NC; ++k) {
     const int idx = k <= i ? ri + k : ((k * (k + 1)) >> 1) + i;
     ak[k] = Th[idx];
-    vk[k] = v[k];
   }
+  lds_vec<R, NC, true>(v, vk);
   __builtin_amdgcn_sched_barrier(0);
   R acc = R(0);
 #pragma unroll
@@ -397,17 +432,21 @@ __global__ __launch_bounds__(kWave, StreamOcc<R>::waves) void admm_stream_kernel
 
   R* wgp = lds + L.wg + p * T * n;
   V* spl = reinterpret_cast<V*>(lds + L.spill);
-  R* vec = lds + L.vec;
-  R* sr = vec + 0 * kWave + base;
-  R* su = vec + 1 * kWave + base;
-  R* ss = vec + 2 * kWave + base;
-  R* sx = vec + 3 * kWave + base;
-  R* sc = vec + 4 * kWave + base;
-  R* sc0 = vec + 5 * kWave + base;
-  R* sy = vec + 6 * kWave + base;   // new stacked duals [y_f; y_g] (residuals)
-  R* sy0 = vec + 7 * kWave + base;  // new y_f0 (residuals)
+  constexpr int VW = vec_stride(P);
+  R* vec = lds + L.vec + p * up4(kWave / P);
+  R* sr = vec + 0 * VW;
+  R* su = vec + 1 * VW;
+  R* ss = vec + 2 * VW;
+  R* sx = vec + 3 * VW;
+  R* sc = vec + 4 * VW;
+  R* sc0 = vec + 5 * VW;
+  R* sy = vec + 6 * VW;   // new stacked duals [y_f; y_g] (residuals)
+  R* sy0 = vec + 7 * VW;  // new y_f0 (residuals)
   R* sxn = sr;  // the relaxed iterate for the residuals (sr is free in the backward sweep)
   const int nr = nx + m;            // stacked constraint rows of a stage
+  // lane index clamped into the blocks, for lanes that compute values they
+  // discard (so that their LDS reads stay inside the blocks and the pad)
+  const int icn = min(i, NC - 1), icr = min(i, NL - 1);
   const bool dyn = i < nx, ineq = i >= nx && i < nr;
   const int ji = ineq ? i - nx : 0;  // inequality index of an inequality row
   const R* a0p = lds + L.a0 + p * n0 * n;
@@ -415,10 +454,17 @@ __global__ __launch_bounds__(kWave, StreamOcc<R>::waves) void admm_stream_kernel
   auto amS = [&](int j) { return lds + L.am + j * (P * amp); };
   auto rvS = [&](int j) { return lds + L.rv + j * (P * rvp); };
   auto dmS = [&](int j) { return lds + L.dm + j * (P * dmp); };
-  auto th_run = [&](int t) { return reinterpret_cast<const V*>(a.th + ((size_t)t * B + b0) * PITCH); };
-  auto dm_run = [&](int t) { return reinterpret_cast<const V*>(a.dm + ((size_t)t * B + b0) * dmp); };
-  auto am_run = [&](int t) { return reinterpret_cast<const V*>(a.am + ((size_t)t * B + b0) * amp); };
-  auto rv_run = [&](int t) { return reinterpret_cast<const V*>(a.rv + ((size_t)t * B + b0) * rvp); };
+  // stage runs: base of this wavefront's problems plus t times the stage
+  // stride, in 32-bit element offsets (the host keeps T B pitch below 2^31)
+  const R* th0 = a.th + (size_t)b0 * PITCH;
+  const R* dm0 = a.dm + (size_t)b0 * dmp;
+  const R* am0 = a.am + (size_t)b0 * amp;
+  R* rv0 = a.rv + (size_t)b0 * rvp;
+  const unsigned sth = (unsigned)B * PITCH, sdm = (unsigned)B * dmp, sam = (unsigned)B * amp, srv = (unsigned)B * rvp;
+  auto th_run = [&](int t) { return reinterpret_cast<const V*>(th0 + (unsigned)t * sth); };
+  auto dm_run = [&](int t) { return reinterpret_cast<const V*>(dm0 + (unsigned)t * sdm); };
+  auto am_run = [&](int t) { return reinterpret_cast<const V*>(am0 + (unsigned)t * sam); };
+  auto rv_run = [&](int t) { return reinterpret_cast<const V*>(rv0 + (unsigned)t * srv); };
   const unsigned rv_lane = pl * rvp;  // this lane's problem inside a stage run
 
   // ---- LDS starts zeroed (the column products rely on finite data past the
@@ -519,13 +565,16 @@ __global__ __launch_bounds__(kWave, StreamOcc<R>::waves) void admm_stream_kernel
             store_run<V, CH_AM>(r.am, reinterpret_cast<V*>(amS(j)), nch_am, spl);
           },
           [&](int j, int t) {
+            // lanes past n compute throwaway values in their own vector slots
             R rr = i < n ? wgp[t * n + i] : R(0);
-            if (t > 0 && i < nx) rr += rho_f * v;
-            if (i < n) sr[i] = rr;
+            if (t > 0) rr += (i < nx) ? rho_f * v : R(0);
+            sr[i] = rr;
             wsync();
-            if (i < n) wgp[t * n + i] = lsym<R, NC>(thS(j) + p * PITCH, i, sr);
+            const R wv = lsym<R, NC>(thS(j) + p * PITCH, icn, sr);
+            if (i < n) wgp[t * n + i] = wv;
+            sx[i] = wv;
             wsync();
-            if (t < N && i < nx) v = lrow<R, NC>(amS(j) + p * amp, i, wgp + t * n);
+            if (t < N) v = lrow<R, NC>(amS(j) + p * amp, icr, sx);
           });
     }
 
@@ -543,6 +592,9 @@ __global__ __launch_bounds__(kWave, StreamOcc<R>::waves) void admm_stream_kernel
     // runs (Theta^{-1}, M of t-2; rv, D of t-1).
     const bool chk = mod_zero(iter, a.check_every);
     R rp = 0, nCx = 0, nc = 0, nGx = 0, nz = 0, rd = 0, nPx = 0, nAty = 0, nq = 0, nxi = 0, nyg = 0;
+    // per-iteration constants of the projection: y / rho as y * (1 / rho)
+    const R inv_rho = R(1) / rho;
+    const R frac = slack ? gs / (gs + rho) : R(0), xi_f = slack ? rho / (gs + rho) : R(0);
     {
       V pth[CH_TH], pam[CH_AM], prv[CH_RV], pdm[CH_TH];
       auto amP = [&](int t) { return lds + L.am + (t & 1) * (P * amp); };
@@ -567,15 +619,17 @@ __global__ __launch_bounds__(kWave, StreamOcc<R>::waves) void admm_stream_kernel
       R pq_p = R(0), aty_p = R(0);
       for (int t = T - 1; t >= 0; --t) {
         const bool hasA = t >= 1;  // the recursion part of stage t-1 runs in this step
-        // ---- region 1: stage the runs; su for A, sx for B
+        // ---- region 1: stage the runs; su for A, sx for B.  Lanes past a
+        // vector's length write zeros or throwaway values into their own
+        // group's slot (never read as part of the vector).
         if (hasA) {
           store_run<V, CH_TH>(pth, reinterpret_cast<V*>(th_slot), nch_th, spl);
           store_run<V, CH_AM>(pam, reinterpret_cast<V*>(amP(t - 1)), nch_am, spl);
         }
         store_run<V, CH_RV>(prv, reinterpret_cast<V*>(rv_slot), nch_rv, spl);
         if (chk) store_run<V, CH_TH>(pdm, reinterpret_cast<V*>(dm_slot), nch_dm, spl);
-        if (i < NL) su[i] = dyn ? -xa : R(0);  // A_plus_{t-1} xt_t, 0 past nx
-        if (i < n) sx[i] = xa;
+        su[i] = dyn ? -xa : R(0);  // A_plus_{t-1} xt_t, 0 past nx
+        sx[i] = xa;
         wsync();
         if (t >= 2) {
           load_run<V, CH_TH>(pth, th_run(t - 2), nch_th);
@@ -589,113 +643,95 @@ __global__ __launch_bounds__(kWave, StreamOcc<R>::waves) void admm_stream_kernel
         const R* mA = amP(t - 1) + p * amp;  // M_{t-1} (A)
         const R* mt = amP(t) + p * amp;      // M_t = [A_minus_t; G_t] (B)
         const R* rv = rv_slot + p * rvp;
-        R* rvg = a.rv + ((size_t)t * B + b0) * rvp + rv_lane;  // this problem's record in HBM
-        if (hasA && i < n) ss[i] = rho_f * lcol<R, NC, NL>(mA, nx, i, su);
+        // this wavefront's rv records of stage t in HBM; stores outside the
+        // masks go past the range and are dropped
+        const __amdgpu_buffer_rsrc_t rsg = __builtin_amdgcn_make_buffer_rsrc(
+            rv0 + (unsigned)t * srv, (short)0, (int)(nprob * rvp * sizeof(R)), kBufferFlags);
+        if (hasA) ss[i] = rho_f * lcol<R, NC, NL>(mA, nx, icn, su);
         const bool drow = dyn && t < N;  // a live dynamics row of stage t
-        const R u = (dyn && t < N) ? -xn : R(0);  // (A_plus_t xt_{t+1})[i]
+        const R u = drow ? -xn : R(0);   // (A_plus_t xt_{t+1})[i]
         // stacked C and G products of the pre-relaxation iterate
-        R mx = R(0), cx0 = R(0);
-        if (i < nr) mx = lrow<R, NC>(mt, i, sx);
+        const R mx = lrow<R, NC>(mt, icr, sx);
+        R cx0 = R(0);
         if (t == 0 && i < n0) cx0 = lrow<R, NC>(a0p, i, sx);
         // over-relaxation
-        R xnew = R(0);
-        if (i < n) {
-          xnew = alpha * xa + one_m_alpha * rv[rg.x + i];
-          if (commit) rvg[rg.x + i] = xnew;
-        }
+        const R xnew = alpha * xa + one_m_alpha * rv[rg.x + icn];
+        buf_store(xnew, rsg, commit && i < n, rv_lane + rg.x + i);
         // constraint row i: the dual, the next gamma's entry, and (inequality
         // rows) the box projection / slack
-        R tgt = R(0), y_r = R(0), z_r = R(0), xi_r = R(0);
-        if (ineq) {
-          const R zo = rv[rg.cz + i], ygo = rv[rg.y + i];
-          const R zt = alpha * mx + one_m_alpha * zo + ygo / rho;
-          const R proj = rmin(rmax(zt, rv[rg.l + ji]), rv[rg.u + ji]);
-          R zn, xin;
-          if (a.use_slack) {
-            const R frac = gs / (gs + rho);
-            zn = (R(1) - frac) * zt + frac * proj;
-            xin = (rho / (gs + rho)) * (proj - zt);
-          } else {
-            zn = proj;
-            xin = R(0);
-          }
-          const R ygn = ygo + rho * (alpha * mx + one_m_alpha * zo - zn);
-          if (commit) {
-            rvg[rg.cz + i] = zn;
-            rvg[rg.xi + ji] = xin;
-            rvg[rg.y + i] = ygn;
-          }
-          tgt = rho * zn - ygn;
-          y_r = ygn;
-          z_r = zn;
-          xi_r = xin;
+        const R zo = rv[rg.cz + icr], yo = rv[rg.y + icr];
+        const R zt = alpha * mx + one_m_alpha * zo + yo * inv_rho;
+        const R proj = rmin(rmax(zt, rv[rg.l + ji]), rv[rg.u + ji]);
+        R zn = proj, xin = R(0);
+        if (slack) {
+          zn = (R(1) - frac) * zt + frac * proj;
+          xin = xi_f * (proj - zt);
         }
-        if (drow) {
-          const R cx = mx + u;
-          const R cv = rv[rg.cz + i];
-          const R yf = rv[rg.y + i] + rho_f * (alpha * cx + one_m_alpha * cv - cv);
-          if (commit) rvg[rg.y + i] = yf;
-          tgt = rho_f * cv - yf;
-          y_r = yf;
-        }
+        const R ygn = yo + rho * (alpha * mx + one_m_alpha * zo - zn);
+        const R cv = zo;  // c_t[i] on a dynamics row
+        const R yf = yo + rho_f * (alpha * (mx + u) + one_m_alpha * cv - cv);
+        const R y_r = ineq ? ygn : (drow ? yf : R(0));
+        const R tgt = ineq ? rho * zn - ygn : (drow ? rho_f * cv - yf : R(0));
+        const R z_r = zn, xi_r = xin;
+        buf_store(y_r, rsg, commit && (ineq || drow), rv_lane + rg.y + i);
+        buf_store(zn, rsg, commit && ineq, rv_lane + rg.cz + i);
+        buf_store(xin, rsg, commit && ineq, rv_lane + rg.xi + ji);
         R ct0 = R(0), yf0_r = R(0);
         if (t == 0 && i < n0) {
-          const R yf = yf0v + rho_f * (alpha * cx0 + one_m_alpha * c0v - c0v);
+          const R yf0 = yf0v + rho_f * (alpha * cx0 + one_m_alpha * c0v - c0v);
           if (commit) {
-            a.y_f0[(size_t)b * n0 + i] = yf;
-            yf0v = yf;
+            a.y_f0[(size_t)b * n0 + i] = yf0;
+            yf0v = yf0;
           }
-          ct0 = rho_f * c0v - yf;
-          yf0_r = yf;
+          ct0 = rho_f * c0v - yf0;
+          yf0_r = yf0;
         }
         // next iteration's gamma (valid while rho is unchanged)
-        if (i < NL) sc[i] = tgt;   // 0 past nr
-        if (i < NL) sc0[i] = ct0;  // 0 past n0
+        sc[i] = tgt;    // 0 past nr
+        sc0[i] = ct0;   // 0 past n0
         if (chk) {
-          if (i < n) sxn[i] = xnew;
-          if (i < NL) sy[i] = y_r;     // 0 past nr
-          if (i < NL) sy0[i] = yf0_r;  // 0 past n0
+          sxn[i] = xnew;
+          sy[i] = y_r;     // 0 past nr
+          sy0[i] = yf0_r;  // 0 past n0
         }
         wsync();
         // ---- region 3
         R xa_next = R(0);
-        if (hasA && i < n) xa_next = wgp[(t - 1) * n + i] - lsym<R, NC>(th_slot + p * PITCH, i, ss);
+        if (hasA) {
+          const R xv = wgp[(t - 1) * n + icn] - lsym<R, NC>(th_slot + p * PITCH, icn, ss);
+          xa_next = i < n ? xv : R(0);
+        }
         if (t < N) {
-          if (dyn) gp -= tgt;  // A_plus_t^T = [-I; 0]
+          gp -= dyn ? tgt : R(0);  // A_plus_t^T = [-I; 0]
           if (i < n) wgp[(t + 1) * n + i] = gp;
         }
-        if (i < n) {
-          R gv = sigma * xnew - rv[rg.q + i];
-          gv += lcol<R, NC, NL>(mt, nr, i, sc);
-          if (t == 0) gv += lcol<R, NC, NC>(a0p, n0, i, sc0);
+        {
+          R gv = sigma * xnew - rv[rg.q + icn];
+          gv += lcol<R, NC, NL>(mt, nr, icn, sc);
+          if (t == 0) gv += lcol<R, NC, NC>(a0p, n0, icn, sc0);
           gp = gv;
         }
         if (chk) {
+          const bool cl = i < n;  // a lane of an n-vector
           // dual residual row t+1 is complete with -[y_f_t; 0]
-          if (drow) {
+          {
             const R aty = aty_p - y_r;
-            rd = rmax(rd, rabs(pq_p + aty));
-            nAty = rmax(nAty, rabs(aty));
+            rd = rmax(rd, drow ? rabs(pq_p + aty) : R(0));
+            nAty = rmax(nAty, drow ? rabs(aty) : R(0));
           }
           // stacked primal rows of the relaxed iterate
-          if (i < nr) {
-            const R m1 = lrow<R, NC>(mt, i, sxn);
-            if (drow) {  // A_minus_t x_t - x_{t+1} - c_t
-              const R cx1 = m1 - xnn;
-              const R cv = rv[rg.cz + i];
-              rp = rmax(rp, rabs(cx1 - cv));
-              nCx = rmax(nCx, rabs(cx1));
-              nc = rmax(nc, rabs(cv));
-            }
-            if (ineq) {
-              rp = rmax(rp, rabs(m1 - z_r));
-              nGx = rmax(nGx, rabs(m1));
-              nz = rmax(nz, rabs(z_r));
-              if (slack) {
-                rd = rmax(rd, rabs(gs * xi_r + y_r));
-                nxi = rmax(nxi, rabs(xi_r));
-                nyg = rmax(nyg, rabs(y_r));
-              }
+          const R m1 = lrow<R, NC>(mt, icr, sxn);
+          {
+            const R cx1 = m1 - xnn;  // A_minus_t x_t - x_{t+1}, dynamics rows
+            rp = rmax(rp, drow ? rabs(cx1 - cv) : (ineq ? rabs(m1 - z_r) : R(0)));
+            nCx = rmax(nCx, drow ? rabs(cx1) : R(0));
+            nc = rmax(nc, drow ? rabs(cv) : R(0));
+            nGx = rmax(nGx, ineq ? rabs(m1) : R(0));
+            nz = rmax(nz, ineq ? rabs(z_r) : R(0));
+            if (slack) {
+              rd = rmax(rd, ineq ? rabs(gs * xi_r + y_r) : R(0));
+              nxi = rmax(nxi, ineq ? rabs(xi_r) : R(0));
+              nyg = rmax(nyg, ineq ? rabs(y_r) : R(0));
             }
           }
           if (t == 0 && i < n0) {
@@ -704,22 +740,20 @@ __global__ __launch_bounds__(kWave, StreamOcc<R>::waves) void admm_stream_kernel
             nCx = rmax(nCx, rabs(cx1));
             nc = rmax(nc, rabs(c0v));
           }
-          if (i < n) {
+          {
             const R* dmt = dm_slot + p * dmp;
-            const R px = diagD ? dmt[i] * xnew : lsym<R, NC>(dmt, i, sxn);
+            const R px = diagD ? dmt[icn] * xnew : lsym<R, NC>(dmt, icn, sxn);
             R aty = R(0);
-            if (t == 0) aty += lcol<R, NC, NC>(a0p, n0, i, sy0);
-            aty += lcol<R, NC, NL>(mt, nr, i, sy);  // A_minus_t^T y_f_t + G_t^T y_g_t
-            const R qv = rv[rg.q + i];
-            if (t > 0 && dyn) {  // awaits -y_f_{t-1}[i]
-              pq_p = px + qv;
-              aty_p = aty;
-            } else {
-              rd = rmax(rd, rabs(px + qv + aty));
-              nAty = rmax(nAty, rabs(aty));
-            }
-            nPx = rmax(nPx, rabs(px));
-            nq = rmax(nq, rabs(qv));
+            if (t == 0) aty += lcol<R, NC, NC>(a0p, n0, icn, sy0);
+            aty += lcol<R, NC, NL>(mt, nr, icn, sy);  // A_minus_t^T y_f_t + G_t^T y_g_t
+            const R qv = rv[rg.q + icn];
+            const bool wait = t > 0 && dyn;  // awaits -y_f_{t-1}[i]
+            pq_p = px + qv;
+            aty_p = aty;
+            rd = rmax(rd, (cl && !wait) ? rabs(px + qv + aty) : R(0));
+            nAty = rmax(nAty, (cl && !wait) ? rabs(aty) : R(0));
+            nPx = rmax(nPx, cl ? rabs(px) : R(0));
+            nq = rmax(nq, cl ? rabs(qv) : R(0));
           }
         }
         xn = xa;

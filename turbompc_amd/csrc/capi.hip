@@ -194,6 +194,10 @@ bool stream_ok(const Dims& d, int P, bool diag) {
   if (!(d.n == 6 || d.n == 9 || d.n == 16 || d.n == 17)) return false;
   if (d.nx > d.n - 1 || d.nx + d.m > d.n || d.m > kMaxStreamM) return false;
   const StreamLayout L = stream_layout(d, P, kStreamDepth, diag);
+  // stage-run offsets are 32-bit element offsets
+  const RecGeom g = rec_geom(d, diag);
+  const int widest = std::max(std::max(g.amp, g.rvp), std::max(th_pitch(d.n), g.dmp));
+  if ((long long)d.T * d.B * widest >= (1LL << 31)) return false;
   return (size_t)L.total * sizeof(R) <= kMaxLds;
 }
 

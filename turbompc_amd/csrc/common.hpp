@@ -45,18 +45,15 @@ __device__ __forceinline__ bool mod_zero(int it, int k) {
   return k > 0 ? (it % k) == 0 : it == 0;
 }
 
-template <typename R>
-__device__ __forceinline__ R rmax(R a, R b) {
-  return a > b ? a : b;
-}
-template <typename R>
-__device__ __forceinline__ R rmin(R a, R b) {
-  return a < b ? a : b;
-}
-template <typename R>
-__device__ __forceinline__ R rabs(R a) {
-  return a < R(0) ? -a : a;
-}
+// max / min / abs as single instructions (v_max, v_min, and the |x| source
+// modifier).  On finite operands they equal the reference's jnp.maximum /
+// jnp.minimum / jnp.abs; a NaN operand yields the other operand.
+__device__ __forceinline__ float rmax(float a, float b) { return __builtin_fmaxf(a, b); }
+__device__ __forceinline__ double rmax(double a, double b) { return __builtin_fmax(a, b); }
+__device__ __forceinline__ float rmin(float a, float b) { return __builtin_fminf(a, b); }
+__device__ __forceinline__ double rmin(double a, double b) { return __builtin_fmin(a, b); }
+__device__ __forceinline__ float rabs(float a) { return __builtin_fabsf(a); }
+__device__ __forceinline__ double rabs(double a) { return __builtin_fabs(a); }
 __device__ __forceinline__ float rsqrt_(float a) { return sqrtf(a); }
 __device__ __forceinline__ double rsqrt_(double a) { return sqrt(a); }
 
