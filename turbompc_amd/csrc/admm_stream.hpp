@@ -466,6 +466,19 @@ __global__ __launch_bounds__(kWave, StreamOcc<R>::waves) void admm_stream_kernel
   auto am_run = [&](int t) { return reinterpret_cast<const V*>(am0 + (unsigned)t * sam); };
   auto rv_run = [&](int t) { return reinterpret_cast<const V*>(rv0 + (unsigned)t * srv); };
   const unsigned rv_lane = pl * rvp;  // this lane's problem inside a stage run
+  // byte offsets of this lane's 16-byte chunks of the A_minus rows of the M
+  // runs (the forward sweep reads no G rows): chunk e of the wavefront maps to
+  // problem e / ca, chunk e % ca of its block; -1 marks lanes past the last
+  // chunk (their loads go out of range and read zeros)
+  int fa_off[CH_AM];
+  {
+    const int ca = (nx * n + W - 1) / W;
+#pragma unroll
+    for (int c = 0; c < CH_AM; ++c) {
+      const int e = c * kWave + tid, pe = e / ca;
+      fa_off[c] = pe < nprob ? (pe * amp + (e - pe * ca) * W) * (int)sizeof(R) : -1;
+    }
+  }
 
   // ---- LDS starts zeroed (the column products rely on finite data past the
   // blocks); resident data: A0 in LDS, c0 / y_f0 in registers ---------------
@@ -558,11 +571,20 @@ __global__ __launch_bounds__(kWave, StreamOcc<R>::waves) void admm_stream_kernel
           T, true,
           [&](FRegs& r, int t) {
             load_run<V, CH_TH>(r.th, th_run(t), nch_th);
-            if (t < N) load_run<V, CH_AM>(r.am, am_run(t), nch_am);
+            if (t < N) {  // the A_minus rows of M_t only
+              const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
+                  const_cast<V*>(am_run(t)), (short)0, nch_am * 16, kBufferFlags);
+#pragma unroll
+              for (int c = 0; c < CH_AM; ++c)
+                r.am[c] = __builtin_bit_cast(V, __builtin_amdgcn_raw_buffer_load_b128(rs, fa_off[c], 0, 0));
+            }
           },
           [&](FRegs& r, int j) {
             store_run<V, CH_TH>(r.th, reinterpret_cast<V*>(thS(j)), nch_th, spl);
-            store_run<V, CH_AM>(r.am, reinterpret_cast<V*>(amS(j)), nch_am, spl);
+            V* dst = reinterpret_cast<V*>(amS(j));
+#pragma unroll
+            for (int c = 0; c < CH_AM; ++c)
+              *(fa_off[c] >= 0 ? dst + (fa_off[c] >> 4) : spl) = r.am[c];
           },
           [&](int j, int t) {
             // lanes past n compute throwaway values in their own vector slots
