@@ -101,6 +101,36 @@ int tmpc_admm_direct_f64(hipStream_t stream, const tmpc_dims* dims, const tmpc_q
                          const tmpc_state* in, tmpc_state* out, uint32_t* iters_out,
                          const tmpc_admm_cfg* cfg, void* workspace, size_t workspace_bytes);
 
+/* ---- one SQP step on the device --------------------------------------------
+ * The body of the reference's SQP while_loop (turbompc/solvers/turbompc_solver.py:1570-1711)
+ * evaluates _compute_first_order_convergence_error (:1158-1225) on the new
+ * iterate and its relinearized QP; the next test of cond_fun (conv >
+ * tol_convergence per problem under vmap, :1713-1718) is followed by
+ * ADMMSolver.solve of that same QP from that same iterate (:1575-1581).
+ * This entry point does the three in one call: the check of `in` against
+ * `qp` (fused into the first sweep of the ADMM kernel on the explicit-
+ * integrator path), the activity test, and the ADMM solve of the problems
+ * that pass it.  A problem that fails it runs no iteration: `out` keeps `in`
+ * and iters_out is 0, so the caller needs no masked commit.  The workspace is
+ * the one of tmpc_admm_direct_*. */
+typedef struct {
+  const uint8_t* active_in; /* (B,) 1 = still iterating, or NULL = all */
+  uint8_t* active_out;      /* (B,) active_in && conv > tol (may alias active_in) */
+  double tol;               /* tol_convergence */
+  void* conv;               /* (B,) first-order error of `in` */
+  void* eq_err;             /* (B,) equality violation, or NULL */
+  void* ineq_err;           /* (B,) inequality violation, or NULL */
+  void* g_out;              /* (B,T,m) G x (+ slack) of `in`, or NULL */
+} tmpc_sqp_step;
+int tmpc_sqp_admm_step_f32(hipStream_t stream, const tmpc_dims* dims, const tmpc_qp* qp,
+                           const tmpc_state* in, tmpc_state* out, uint32_t* iters_out,
+                           const tmpc_admm_cfg* cfg, const tmpc_sqp_step* sqp, void* workspace,
+                           size_t workspace_bytes);
+int tmpc_sqp_admm_step_f64(hipStream_t stream, const tmpc_dims* dims, const tmpc_qp* qp,
+                           const tmpc_state* in, tmpc_state* out, uint32_t* iters_out,
+                           const tmpc_admm_cfg* cfg, const tmpc_sqp_step* sqp, void* workspace,
+                           size_t workspace_bytes);
+
 /* ---- ADMM with the PCG Schur solve -----------------------------------------
  * Replaces the `admm_fused_cuda[_f64]` FFI target: AdmmFusedCudaImpl
  * (turbompc/solvers/admm/csrc/admm_ffi.cc:13-148) / LaunchADMMFusedF32/F64

@@ -136,3 +136,74 @@ def test_first_order_check_kernel_matches_dense_assembly(std, dtype, use_slack, 
         assert abs(float(eq[b]) - e) <= tol * scale
         assert abs(float(iq[b]) - i) <= tol * scale
         assert rel_err(g[b].reshape(-1), gv) < tol * 10
+
+
+def _random_state(qp, rng, dtype, use_slack):
+    from turbompc_amd.solvers.admm.admm import ADMMState
+
+    B, T, n, nx, n0, m = qp.dims
+    dev = lambda a: torch.tensor(a, dtype=dtype, device="cuda")  # noqa: E731
+    l, u = qp.ineq.l.numpy(), qp.ineq.u.numpy()
+    return ADMMState(
+        x_blocks=dev(rng.standard_normal((B, T, n))), y_g=dev(rng.standard_normal((B, T, m))),
+        y_f_0=dev(rng.standard_normal((B, n0))), y_f_dyn=dev(rng.standard_normal((B, T - 1, nx))),
+        z_g=dev(np.clip(rng.standard_normal((B, T, m)), l, u)),
+        xi_g=dev(rng.standard_normal((B, T, m)) * 0.3 if use_slack else np.zeros((B, T, m))),
+        rho_bar=dev(np.full(B, 0.1)))
+
+
+# kernel: the check fused into the streaming kernel (explicit-integrator
+# structure, P problems per wavefront) or the generic path (check kernel, then
+# the activity test, then the generic ADMM kernel)
+@pytest.mark.parametrize("kernel", ["stream-1", "stream-2", "stream-3", "generic-std", "generic"])
+@pytest.mark.parametrize("use_slack", [False, True])
+@pytest.mark.parametrize("dtype", [torch.float64, torch.float32])
+def test_sqp_step_check_and_activity(kernel, use_slack, dtype):
+    """tmpc_sqp_admm_step: the first-order check of the input iterate matches
+    tmpc_sqp_first_order_*, the activity test is active & (conv > tol), stopped
+    problems keep their state with zero iterations, and the others match a
+    plain ADMM solve from the same state."""
+    from helpers import random_qp, soften
+    from turbompc_amd import _lib
+    from turbompc_amd.solvers.admm.admm import ADMMSolver
+    from turbompc_amd.solvers.linear_systems_solvers.backends import AdmmBackend
+    from turbompc_amd.solvers.qp_utils import ZShape
+    from turbompc_amd.solvers.sqp_hip import first_order_check
+
+    std = kernel != "generic"
+    B, T, n, nx, m = (13, 21, 6, 4, 2) if kernel.startswith("stream") else (7, 9, 9, 6, 11)
+    if kernel == "stream-2":
+        B, T, n, nx, m = 9, 11, 17, 13, 4
+    qp = random_qp(B, T, n, nx, m, seed=71, std=std, diag=std)
+    if use_slack:
+        qp = soften(qp, 3.0, shrink=0.5)
+    rng = np.random.default_rng(9)
+    st = _random_state(qp, rng, dtype, use_slack)
+    qpd = qp.to("cuda", dtype)
+    flags = _lib.flag_stream_p(int(kernel[-1])) if kernel.startswith("stream") else _lib.FLAG_GENERIC_KERNEL
+    solver = ADMMSolver(ZShape(T - 1, nx, n - nx), {"max_iter": 50, "tol_epsilon": 1e-8}, sigma=1e-6, max_iter=15,
+                        eps_abs=1e-12, eps_rel=1e-12, check_termination_every=25, adapt_rho_every=0,
+                        rho_f_factor=1000.0, admm_backend=AdmmBackend.HIP_DIRECT, use_slack=use_slack,
+                        std_dynamics=std, kernel_flags=flags, diag_cost=std)
+    sw = qpd.ineq.slack_penalization_weight
+    x = st.x_blocks
+    ref = first_order_check(qpd, x, st.y_f_0, st.y_f_dyn, st.y_g, st.xi_g if use_slack else None, float(sw),
+                            std_dynamics=std, diag_cost=std)
+    tol = float(ref[0].median())
+    active = torch.tensor(rng.random(B) < 0.7, device="cuda")
+    (_, _), stats, out, (cv, e, i, g), act = solver.sqp_step(qpd, st, active, tol, slack_weight=sw)
+    (_, _), stats_p, out_p = solver.solve(qpd, st, slack_weight=sw)
+    torch.cuda.synchronize()
+    bar = 1e-12 if dtype == torch.float64 else 1e-5
+    for got, want in zip((cv, e, i, g), ref):
+        assert rel_err(got, want) < bar, rel_err(got, want)
+    want_act = active & (ref[0] > tol)
+    assert torch.equal(act, want_act)
+    assert 0 < int(want_act.sum()) < B
+    on = want_act.cpu().numpy()
+    assert np.all(stats.num_iter.cpu().numpy()[~on] == 0)
+    assert np.all(stats.num_iter.cpu().numpy()[on] == stats_p.num_iter.cpu().numpy()[on])
+    for k in ("x_blocks", "z_g", "y_g", "y_f_0", "y_f_dyn", "xi_g", "rho_bar"):
+        a, b0, p = getattr(out, k).cpu().numpy(), getattr(st, k).cpu().numpy(), getattr(out_p, k).cpu().numpy()
+        np.testing.assert_array_equal(a[~on], b0[~on])
+        np.testing.assert_array_equal(a[on], p[on])

@@ -88,9 +88,21 @@ class AdmmCfg(ctypes.Structure):
     ]
 
 
+class SqpStep(ctypes.Structure):
+    _fields_ = [
+        ("active_in", ctypes.c_void_p),
+        ("active_out", ctypes.c_void_p),
+        ("tol", ctypes.c_double),
+        ("conv", ctypes.c_void_p),
+        ("eq_err", ctypes.c_void_p),
+        ("ineq_err", ctypes.c_void_p),
+        ("g_out", ctypes.c_void_p),
+    ]
+
+
 # name -> argtypes (restype is int unless listed in _SIZE_FNS)
 _VP, _I32, _U32, _F64, _SZ = ctypes.c_void_p, ctypes.c_int32, ctypes.c_uint32, ctypes.c_double, ctypes.c_size_t
-_PD, _PQ, _PS, _PC = (ctypes.POINTER(t) for t in (Dims, QP, State, AdmmCfg))
+_PD, _PQ, _PS, _PC, _PSQ = (ctypes.POINTER(t) for t in (Dims, QP, State, AdmmCfg, SqpStep))
 SIGNATURES = {
     "tmpc_version": [],
     "tmpc_set_timing_events": [_VP, _VP],
@@ -98,6 +110,8 @@ SIGNATURES = {
     "tmpc_admm_direct_workspace_bytes": [ctypes.c_int, _PD],
     "tmpc_admm_direct_f32": [_VP, _PD, _PQ, _PS, _PS, _VP, _PC, _VP, _SZ],
     "tmpc_admm_direct_f64": [_VP, _PD, _PQ, _PS, _PS, _VP, _PC, _VP, _SZ],
+    "tmpc_sqp_admm_step_f32": [_VP, _PD, _PQ, _PS, _PS, _VP, _PC, _PSQ, _VP, _SZ],
+    "tmpc_sqp_admm_step_f64": [_VP, _PD, _PQ, _PS, _PS, _VP, _PC, _PSQ, _VP, _SZ],
     "tmpc_admm_pcg_workspace_bytes": [ctypes.c_int, _PD],
     "tmpc_admm_pcg_f32": [_VP, _PD, _PQ, _PS, _PS, _VP, _VP, _PC, _VP, _SZ],
     "tmpc_admm_pcg_f64": [_VP, _PD, _PQ, _PS, _PS, _VP, _VP, _PC, _VP, _SZ],

@@ -47,6 +47,7 @@ struct AdmmArgs {
   int max_iter, check_every, adapt_every, use_slack;
   int it_lo, it_hi, first_chunk;
   int g, P;
+  const uint8_t* act;  // (B,) or null: problems with act[b] == 0 run no iteration
 };
 
 enum { SB_W, SB_R, SB_U, SB_S, SB_X, SB_C, SB_Z, SB_C0, SB_XP, SB_XN, SB_YP, SB_Y, SB_YG, SB_CP, SB_COUNT };
@@ -255,7 +256,7 @@ __global__ __launch_bounds__(kWave) void admm_chunk_kernel(AdmmArgs<R> a) {
     // init_residuals of the reference loop (admm.py:998-1005): infinite
     // residuals and unit norm terms; res[] = {rp, rd, np, nd, pn, dn}
     it = 0;
-    done = false;
+    done = a.act ? a.act[b] == 0 : false;
     res[0] = res[1] = res[4] = res[5] = rinf<R>();
     res[2] = res[3] = R(1);
     if (G.live && i == 0) a.ctl[b * 4 + 2] = 0;

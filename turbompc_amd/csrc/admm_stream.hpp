@@ -165,6 +165,13 @@ struct StreamArgs {
   int max_iter, check_every, adapt_every, use_slack;
   int diag;  // D_t records hold the diagonal (RecGeom)
   int it_lo, it_hi, first_chunk;
+  // SQP step (optional, first chunk): first-order check of the input iterate
+  // and the activity test act_out = act_in && conv > chk_tol; a problem that
+  // fails it runs no iteration
+  R *chk_conv, *chk_eq, *chk_iq, *chk_g;
+  const uint8_t* act_in;
+  uint8_t* act_out;
+  R chk_tol;
 };
 
 // ---- pack / unpack -----------------------------------------------------------
@@ -509,42 +516,105 @@ __global__ __launch_bounds__(kWave, StreamOcc<R>::waves) void admm_stream_kernel
   const R gs = (slack && a.slack_w) ? a.slack_w[b] : R(0);
   wsync();
 
-  // ---- gamma_t for the current state and rho (compute_gamma, admm.py:157-174)
+  // ---- gamma_t for the current state and rho (compute_gamma, admm.py:157-174),
+  // and, in the first chunk of an SQP step, the first-order check of the input
+  // iterate against this QP (_compute_first_order_convergence_error,
+  // turbompc_solver.py:1158-1225) from the same stage records:
+  //   stationarity P x + q + C^T y_f + G^T y_g, equality C x - c, inequality
+  //   violation of g = G x (+ slack), slack stationarity gamma_s xi + y_g.
+  const bool fochk = a.first_chunk && a.chk_conv != nullptr;
   {
     struct GRegs {
-      V am[CH_AM], rv[CH_RV];
+      V am[CH_AM], rv[CH_RV], dm[CH_TH];
     };
     const R rho_f = rho * a.rho_f_factor;
     R scp = R(0);
-    if (i < NC) sc0[i] = rho_f * c0v - yf0v;  // 0 past n0
+    R c_st = R(0), c_eq = R(0), c_iq = R(0), c_sl = R(0);  // this lane's maxima
+    R pend = R(0);  // (A_minus_{t-1} x_{t-1} - c_{t-1})[i], awaiting -x_t
+    R yfp = R(0);   // y_f_{t-1}[i]
+    sc0[i] = rho_f * c0v - yf0v;  // 0 past n0
+    if (fochk) sy0[i] = yf0v;     // 0 past n0
     run_sweep<1, GRegs>(
         T, true,
         [&](GRegs& r, int t) {
           load_run<V, CH_AM>(r.am, am_run(t), nch_am);
           load_run<V, CH_RV>(r.rv, rv_run(t), nch_rv);
+          if (fochk) load_run<V, CH_TH>(r.dm, dm_run(t), nch_dm);
         },
         [&](GRegs& r, int j) {
           store_run<V, CH_AM>(r.am, reinterpret_cast<V*>(amS(j)), nch_am, spl);
           store_run<V, CH_RV>(r.rv, reinterpret_cast<V*>(rvS(j)), nch_rv, spl);
+          if (fochk) store_run<V, CH_TH>(r.dm, reinterpret_cast<V*>(dmS(j)), nch_dm, spl);
         },
         [&](int j, int t) {
           const R* mt = amS(j) + p * amp;
           const R* rv = rvS(j) + p * rvp;
+          const bool crow = (dyn && t < N) || ineq;  // a live stacked constraint row
           // stacked [rho_f c - y_f; rho z - y_g] (dynamics rows vanish at t = N)
-          R sct = R(0);
-          if ((dyn && t < N) || ineq) sct = (dyn ? rho_f : rho) * rv[rg.cz + i] - rv[rg.y + i];
-          if (i < NC) sc[i] = sct;  // 0 past nr
+          const R czv = rv[rg.cz + icr], yv = crow ? rv[rg.y + icr] : R(0);
+          const R sct = crow ? (dyn ? rho_f : rho) * czv - yv : R(0);
+          const R xv = rv[rg.x + icn];
+          sc[i] = sct;  // 0 past nr
+          if (fochk) {
+            sx[i] = xv;
+            sy[i] = yv;  // [y_f_t; y_g], 0 past nr
+          }
           wsync();
-          if (i < n) {
-            R gv = sigma * rv[rg.x + i] - rv[rg.q + i];
-            gv += lcol<R, NC>(mt, nr, i, sc);
-            if (t > 0 && i < nx) gv -= scp;  // A_plus_{t-1}^T = [-I; 0]
-            if (t == 0) gv += lcol<R, NC>(a0p, n0, i, sc0);
-            wgp[t * n + i] = gv;
+          {
+            R gv = sigma * xv - rv[rg.q + icn];
+            gv += lcol<R, NC, NL>(mt, nr, icn, sc);
+            if (t > 0) gv -= (i < nx) ? scp : R(0);  // A_plus_{t-1}^T = [-I; 0]
+            if (t == 0) gv += lcol<R, NC, NC>(a0p, n0, icn, sc0);
+            if (i < n) wgp[t * n + i] = gv;
+          }
+          if (fochk) {
+            const R* dmt = dmS(j) + p * dmp;
+            const R px = diagD ? dmt[icn] * xv : lsym<R, NC>(dmt, icn, sx);
+            R aty = lcol<R, NC, NL>(mt, nr, icn, sy);  // A_minus_t^T y_f_t + G_t^T y_g
+            if (t == 0) aty += lcol<R, NC, NC>(a0p, n0, icn, sy0);
+            if (t > 0) aty -= dyn ? yfp : R(0);  // A_plus_{t-1}^T y_f_{t-1}
+            c_st = rmax(c_st, i < n ? rabs(px + rv[rg.q + icn] + aty) : R(0));
+            const R mxv = lrow<R, NC>(mt, icr, sx);
+            // dynamics row t-1 is complete with -x_t
+            if (t > 0) c_eq = rmax(c_eq, dyn ? rabs(pend - xv) : R(0));
+            pend = (dyn && t < N) ? mxv - czv : R(0);
+            if (t == 0 && i < n0) c_eq = rmax(c_eq, rabs(lrow<R, NC>(a0p, i, sx) - c0v));
+            const R xiv = rv[rg.xi + ji];
+            const R g = mxv + (slack ? xiv : R(0));
+            const R viol = rmax(rmax(rv[rg.l + ji] - g, g - rv[rg.u + ji]), R(0));
+            c_iq = rmax(c_iq, ineq ? viol : R(0));
+            if (slack) c_sl = rmax(c_sl, ineq ? rabs(gs * xiv + yv) : R(0));
+            if (a.chk_g && ineq && G.live) a.chk_g[((size_t)b * T + t) * m + ji] = g;
+            yfp = (dyn && t < N) ? yv : R(0);
           }
           scp = sct;
           wsync();
         });
+    if (fochk) {
+      // group maxima (every lane of a group reduces its group: the result
+      // decides whether the problem iterates), then the activity of the step
+      R* red = lds + L.th;
+      red[0 * kWave + tid] = c_st;
+      red[1 * kWave + tid] = c_eq;
+      red[2 * kWave + tid] = c_iq;
+      red[3 * kWave + tid] = c_sl;
+      wsync();
+      R mxs[4] = {R(0), R(0), R(0), R(0)};
+#pragma unroll
+      for (int k = 0; k < 4; ++k)
+#pragma unroll
+        for (int l = 0; l < NL; ++l) mxs[k] = rmax(mxs[k], red[k * kWave + base + l]);
+      wsync();
+      const R conv = rmax(rmax(mxs[0], mxs[1]), rmax(mxs[2], mxs[3]));
+      const bool act = (a.act_in ? a.act_in[b] != 0 : true) && conv > a.chk_tol;
+      if (G.live && i == 0) {
+        a.chk_conv[b] = conv;
+        if (a.chk_eq) a.chk_eq[b] = mxs[1];
+        if (a.chk_iq) a.chk_iq[b] = mxs[2];
+        if (a.act_out) a.act_out[b] = act ? 1 : 0;
+      }
+      done = !act;  // a stopped problem keeps its input iterate (zero iterations)
+    }
   }
 
   for (int iter = a.it_lo; iter < a.it_hi; ++iter) {

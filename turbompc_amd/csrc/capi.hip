@@ -263,8 +263,15 @@ int launch_factor_std(hipStream_t s, const Dims& d, const DirectWs<R>& w, const 
 }
 
 template <typename R>
-StreamArgs<R> stream_args(const AdmmArgs<R>& a, const DirectWs<R>& w, bool diag) {
+StreamArgs<R> stream_args(const AdmmArgs<R>& a, const DirectWs<R>& w, bool diag, const tmpc_sqp_step* sq) {
   StreamArgs<R> s;
+  s.chk_conv = sq ? static_cast<R*>(sq->conv) : nullptr;
+  s.chk_eq = sq ? static_cast<R*>(sq->eq_err) : nullptr;
+  s.chk_iq = sq ? static_cast<R*>(sq->ineq_err) : nullptr;
+  s.chk_g = sq ? static_cast<R*>(sq->g_out) : nullptr;
+  s.act_in = sq ? sq->active_in : nullptr;
+  s.act_out = sq ? sq->active_out : nullptr;
+  s.chk_tol = sq ? (R)sq->tol : R(0);
   s.d = a.d;
   s.diag = diag ? 1 : 0;
   s.th = w.thinv;
@@ -312,12 +319,20 @@ std::vector<int> chunk_bounds(int max_iter, int check_every, int adapt_every) {
 }
 
 template <typename R>
+int sqp_check_impl(hipStream_t s, const tmpc_dims* dims, const tmpc_qp* qp, const R* x, const R* y0, const R* yf,
+                   const R* yg, const R* slack, double slack_w, uint32_t flags, R* conv, R* eq, R* iq, R* gout,
+                   const R* slack_wp = nullptr);
+
+// sq != nullptr: one SQP step -- the first-order check of the input iterate,
+// the activity test, and the ADMM solve of the problems that pass it.
+template <typename R>
 int admm_direct_impl(hipStream_t s, const tmpc_dims* dims, const tmpc_qp* qp,
                      const tmpc_state* in, tmpc_state* out, uint32_t* iters,
-                     const tmpc_admm_cfg* cfg, void* ws, size_t wsb) {
+                     const tmpc_admm_cfg* cfg, void* ws, size_t wsb, const tmpc_sqp_step* sq = nullptr) {
   if (!dims_ok(dims)) return TMPC_EBADSHAPE;
   if (!cfg || !iters || !qp_ok(qp, dims->m) || !state_ok(in, dims->m) || !state_ok(out, dims->m))
     return TMPC_EBADARG;
+  if (sq && (!sq->conv || !sq->active_out)) return TMPC_EBADARG;
   if (cfg->use_slack && dims->m > 0 && !qp->slack_weight) return TMPC_EBADARG;
   const Dims d = to_dims(dims);
   if (!ws || wsb < direct_ws_bytes<R>(d)) return TMPC_EWORKSPACE;
@@ -348,11 +363,27 @@ int admm_direct_impl(hipStream_t s, const tmpc_dims* dims, const tmpc_qp* qp,
   a.use_slack = cfg->use_slack ? 1 : 0;
   a.g = std::max(d.n, d.m);
   a.P = kWave / a.g;
+  a.act = nullptr;
   const bool std_dyn = (cfg->flags & TMPC_FLAG_STD_DYNAMICS) != 0;
   const int sp = stream_problems_per_wave(d.B, cfg->flags);
   const int fp = factor_problems_per_wave(d.B, cfg->flags);
   const bool diag = (cfg->flags & TMPC_FLAG_DIAG_COST) != 0;
   const bool stream = std_dyn && (cfg->flags & TMPC_FLAG_GENERIC_KERNEL) == 0 && stream_ok<R>(d, sp, diag);
+  if (sq && !stream) {
+    // generic path: the check kernel on the input iterate, then the activity
+    // test, which the ADMM kernel reads as its per-problem start state
+    const bool slack = cfg->use_slack && d.m > 0;
+    st = sqp_check_impl<R>(s, dims, qp, a.st.x, a.st.y_f0, a.st.y_f, a.st.y_g, slack ? a.st.xi : nullptr, 0.0,
+                           cfg->flags, static_cast<R*>(sq->conv), static_cast<R*>(sq->eq_err),
+                           static_cast<R*>(sq->ineq_err), static_cast<R*>(sq->g_out),
+                           slack ? static_cast<const R*>(qp->slack_weight) : nullptr);
+    if (st) return st;
+    hipLaunchKernelGGL((sqp_activity_kernel<R>), dim3((d.B + 255) / 256), dim3(256), 0, s, d.B,
+                       (const R*)sq->conv, (R)sq->tol, sq->active_in, sq->active_out);
+    st = launch_status();
+    if (st) return st;
+    a.act = sq->active_out;
+  }
   if (stream) {
     hipLaunchKernelGGL((stage_pack_kernel<R>), dim3(d.B, d.T), dim3(kWave), 0, s, d, a.qp, a.st, w.am, w.rv, w.dm,
                        diag ? 1 : 0);
@@ -375,7 +406,7 @@ int admm_direct_impl(hipStream_t s, const tmpc_dims* dims, const tmpc_qp* qp,
     a.it_hi = bounds[c + 1];
     a.first_chunk = c == 0 ? 1 : 0;
     if (stream)
-      launch_stream<R>(s, stream_args<R>(a, w, diag), sp);
+      launch_stream<R>(s, stream_args<R>(a, w, diag, sq), sp);
     else if (std_dyn)
       launch_chunk<R, true>(s, a);
     else
@@ -736,22 +767,24 @@ int obstacle_hess_impl(hipStream_t s, int B, int N, int nx, int nu, int dim, int
 // ------------------------------------------------------------- SQP check ----
 template <typename R, int NC>
 void launch_sqp_nc(hipStream_t s, const Dims& d, bool std_dyn, int diag, const QPDev<R>& q, const R* x,
-                   const R* y0, const R* yf, const R* yg, const R* sl, R sw, R* conv, R* eq, R* iq, R* gout) {
+                   const R* y0, const R* yf, const R* yg, const R* sl, R sw, R* conv, R* eq, R* iq, R* gout,
+                   const R* swp) {
   const dim3 grid(d.B * d.T);
   const size_t smem = check_smem_bytes<R>(d.n, d.nx, d.m);
   lds_optin(sqp_check_stage_kernel<R, NC, true>, smem);
   lds_optin(sqp_check_stage_kernel<R, NC, false>, smem);
   if (std_dyn)
     hipLaunchKernelGGL((sqp_check_stage_kernel<R, NC, true>), grid, dim3(kWave), smem, s, d, q, x, y0, yf, yg, sl, sw,
-                       conv, eq, iq, gout, diag);
+                       swp, conv, eq, iq, gout, diag);
   else
     hipLaunchKernelGGL((sqp_check_stage_kernel<R, NC, false>), grid, dim3(kWave), smem, s, d, q, x, y0, yf, yg, sl, sw,
-                       conv, eq, iq, gout, diag);
+                       swp, conv, eq, iq, gout, diag);
 }
 
 template <typename R>
 int sqp_check_impl(hipStream_t s, const tmpc_dims* dims, const tmpc_qp* qp, const R* x, const R* y0, const R* yf,
-                   const R* yg, const R* slack, double slack_w, uint32_t flags, R* conv, R* eq, R* iq, R* gout) {
+                   const R* yg, const R* slack, double slack_w, uint32_t flags, R* conv, R* eq, R* iq, R* gout,
+                   const R* slack_wp) {
   if (!dims_ok(dims)) return TMPC_EBADSHAPE;
   if (!qp_ok(qp, dims->m) || !x || !y0 || !yf || !conv || (dims->m > 0 && !yg)) return TMPC_EBADARG;
   const Dims d = to_dims(dims);
@@ -761,11 +794,11 @@ int sqp_check_impl(hipStream_t s, const tmpc_dims* dims, const tmpc_qp* qp, cons
   const bool std_dyn = flags & TMPC_FLAG_STD_DYNAMICS;
   const int diag = (flags & TMPC_FLAG_DIAG_COST) ? 1 : 0;
   switch (d.n) {
-    case 6: launch_sqp_nc<R, 6>(s, d, std_dyn, diag, q, x, y0, yf, yg, slack, (R)slack_w, conv, eq, iq, gout); break;
-    case 9: launch_sqp_nc<R, 9>(s, d, std_dyn, diag, q, x, y0, yf, yg, slack, (R)slack_w, conv, eq, iq, gout); break;
-    case 16: launch_sqp_nc<R, 16>(s, d, std_dyn, diag, q, x, y0, yf, yg, slack, (R)slack_w, conv, eq, iq, gout); break;
-    case 17: launch_sqp_nc<R, 17>(s, d, std_dyn, diag, q, x, y0, yf, yg, slack, (R)slack_w, conv, eq, iq, gout); break;
-    default: launch_sqp_nc<R, 0>(s, d, std_dyn, diag, q, x, y0, yf, yg, slack, (R)slack_w, conv, eq, iq, gout); break;
+    case 6: launch_sqp_nc<R, 6>(s, d, std_dyn, diag, q, x, y0, yf, yg, slack, (R)slack_w, conv, eq, iq, gout, slack_wp); break;
+    case 9: launch_sqp_nc<R, 9>(s, d, std_dyn, diag, q, x, y0, yf, yg, slack, (R)slack_w, conv, eq, iq, gout, slack_wp); break;
+    case 16: launch_sqp_nc<R, 16>(s, d, std_dyn, diag, q, x, y0, yf, yg, slack, (R)slack_w, conv, eq, iq, gout, slack_wp); break;
+    case 17: launch_sqp_nc<R, 17>(s, d, std_dyn, diag, q, x, y0, yf, yg, slack, (R)slack_w, conv, eq, iq, gout, slack_wp); break;
+    default: launch_sqp_nc<R, 0>(s, d, std_dyn, diag, q, x, y0, yf, yg, slack, (R)slack_w, conv, eq, iq, gout, slack_wp); break;
   }
   return launch_status();
 }
@@ -810,6 +843,19 @@ int tmpc_admm_direct_f64(hipStream_t s, const tmpc_dims* dims, const tmpc_qp* qp
                          tmpc_state* out, uint32_t* iters, const tmpc_admm_cfg* cfg, void* ws,
                          size_t wsb) {
   return admm_direct_impl<double>(s, dims, qp, in, out, iters, cfg, ws, wsb);
+}
+
+int tmpc_sqp_admm_step_f32(hipStream_t s, const tmpc_dims* dims, const tmpc_qp* qp, const tmpc_state* in,
+                           tmpc_state* out, uint32_t* iters, const tmpc_admm_cfg* cfg, const tmpc_sqp_step* sqp,
+                           void* ws, size_t wsb) {
+  if (!sqp) return TMPC_EBADARG;
+  return admm_direct_impl<float>(s, dims, qp, in, out, iters, cfg, ws, wsb, sqp);
+}
+int tmpc_sqp_admm_step_f64(hipStream_t s, const tmpc_dims* dims, const tmpc_qp* qp, const tmpc_state* in,
+                           tmpc_state* out, uint32_t* iters, const tmpc_admm_cfg* cfg, const tmpc_sqp_step* sqp,
+                           void* ws, size_t wsb) {
+  if (!sqp) return TMPC_EBADARG;
+  return admm_direct_impl<double>(s, dims, qp, in, out, iters, cfg, ws, wsb, sqp);
 }
 
 size_t tmpc_blktri_workspace_bytes(int elem_bytes, int32_t B, int32_t T, int32_t n) {

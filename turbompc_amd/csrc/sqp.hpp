@@ -141,12 +141,14 @@ __device__ __forceinline__ R col_bdot(const R* A, int i, int ld, int rows, R v) 
 // One wave per (problem, stage).  D_t, A_minus_t and G_t are staged through
 // LDS; the vectors stay in registers (lane k holds element k) and reach the
 // other lanes by broadcast.  STD: A_plus_t = [-I 0] and E_t = 0 (neither is
-// read); otherwise E and A_plus are read from global memory directly.
+// read); otherwise E and A_plus are read from global memory directly.  The
+// slack weight is slack_wp[b] when slack_wp is given, else slack_w.
 template <typename R, int NC, bool STD>
 __global__ __launch_bounds__(kWave) void sqp_check_stage_kernel(Dims d, QPDev<R> qp, const R* __restrict__ x,
                                                               const R* __restrict__ y0, const R* __restrict__ yf,
                                                               const R* __restrict__ yg, const R* __restrict__ slack,
-                                                              R slack_w, R* __restrict__ conv, R* __restrict__ eq_err,
+                                                              R slack_w, const R* __restrict__ slack_wp,
+                                                              R* __restrict__ conv, R* __restrict__ eq_err,
                                                               R* __restrict__ ineq_err, R* __restrict__ gout,
                                                               int diag) {
   extern __shared__ __align__(16) unsigned char check_smem[];
@@ -233,7 +235,7 @@ __global__ __launch_bounds__(kWave) void sqp_check_stage_kernel(Dims d, QPDev<R>
   if (m) {
     const R gv = row_bdot<R, NC>(sG, im, ld, n, xt) + slv;
     if (i < m) {
-      if (slack) sl = rabs(slack_w * slv + ygv);
+      if (slack) sl = rabs((slack_wp ? slack_wp[b] : slack_w) * slv + ygv);
       iq = rmax(rmax(lv - gv, R(0)), rmax(gv - uv, R(0)));
       if (gout) gout[bt * m + i] = gv;
     }
@@ -246,6 +248,16 @@ __global__ __launch_bounds__(kWave) void sqp_check_stage_kernel(Dims d, QPDev<R>
     if (eq_err) atomic_max_abs(eq_err + b, eq);
     if (ineq_err) atomic_max_abs(ineq_err + b, iq);
   }
+}
+
+// The SQP activity test of one step: act_out = act_in && conv > tol (a NaN
+// error stops the problem, as the reference's `conv > tol` does).
+template <typename R>
+__global__ void sqp_activity_kernel(int B, const R* __restrict__ conv, R tol, const uint8_t* __restrict__ act_in,
+                                    uint8_t* __restrict__ act_out) {
+  const int b = blockIdx.x * blockDim.x + threadIdx.x;
+  if (b >= B) return;
+  act_out[b] = ((act_in ? act_in[b] != 0 : true) && conv[b] > tol) ? 1 : 0;
 }
 
 template <typename R>

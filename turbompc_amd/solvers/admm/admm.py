@@ -182,6 +182,25 @@ class ADMMSolver:
         states, controls = unpack_x(x, self._zshape)
         return (states, controls), ADMMStats(num_iter=iters, num_pcg_iters=pcg_iters), state
 
+    def sqp_step(self, qp_data: QPData, admm_state0: ADMMState, active: torch.Tensor, tol: float,
+                 rho_bar: float = 1.0, alpha: float = 1.0, *, slack_weight=0.0):
+        """One device SQP step (tmpc_sqp_admm_step_*): the first-order check of
+        admm_state0's iterate against qp_data, the activity test
+        active & (conv > tol), and the solve of the problems that pass it (the
+        others keep their state and report 0 iterations).  Returns
+        ((states, controls), stats, state, (conv, eq_err, ineq_err, g), active_out)."""
+        if self._admm_backend != AdmmBackend.HIP_DIRECT:
+            raise ValueError("sqp_step needs the direct Schur solve (HIP_DIRECT)")
+        std = self._std_dynamics if self._std_dynamics is not None else is_std_dynamics(qp_data)
+        cfg = self._cfg(alpha, (_lib.FLAG_STD_DYNAMICS if std else 0) | self._kernel_flags)
+        sw = slack_weight if self._use_slack else None
+        outs, iters, _, (conv, eq, iq, g, act) = hip.admm_hip_solve(
+            qp_data, admm_state0, schur="direct", cfg=cfg, slack_weight=sw, sqp=(active, tol))
+        x, z, yg, y0, yf, xi, rho = outs
+        state = ADMMState(x_blocks=x, y_g=yg, y_f_0=y0, y_f_dyn=yf, z_g=z, xi_g=xi, rho_bar=rho)
+        states, controls = unpack_x(x, self._zshape)
+        return (states, controls), ADMMStats(num_iter=iters, num_pcg_iters=None), state, (conv, eq, iq, g), act
+
     def initial_state(
         self,
         qp_data: QPData,

@@ -63,9 +63,17 @@ def cfg_struct(*, max_iter, check_every, adapt_rho_every, pcg_max_iter, use_slac
 
 
 def admm_hip_solve(qp: QPData, state0, *, schur: str, cfg: _lib.AdmmCfg,
-                   slack_weight: Optional[torch.Tensor] = None, want_pcg_iters: bool = False):
+                   slack_weight: Optional[torch.Tensor] = None, want_pcg_iters: bool = False, sqp=None):
     """Run the fused ADMM on the device.  `state0` is an ADMMState of batched
-    tensors; returns (state fields tuple, iters (B,), pcg_iters or None)."""
+    tensors; returns (state fields tuple, iters (B,), pcg_iters or None).
+
+    sqp = (active (B,) bool, tol) makes the call one SQP step
+    (tmpc_sqp_admm_step_*, direct Schur solve only): the first-order check of
+    state0 against qp, the activity test active & (conv > tol), and the solve of
+    the problems that pass it; the call then also returns (conv, eq_err,
+    ineq_err, g, active_out)."""
+    if sqp is not None and schur != "direct":
+        raise ValueError("an SQP step (sqp=...) needs the direct Schur solve")
     lib = _lib.load()
     B, T, n, nx, n0, m = qp.dims
     dev, dt = qp.device, qp.dtype
@@ -95,6 +103,23 @@ def admm_hip_solve(qp: QPData, state0, *, schur: str, cfg: _lib.AdmmCfg,
         nbytes = lib.tmpc_admm_direct_workspace_bytes(ctypes.sizeof(ctypes.c_double) if dt == torch.float64 else 4,
                                                       ctypes.byref(dims))
         ws = _ws("admm_direct", nbytes, dev)
+        if sqp is not None:
+            active, tol = sqp
+            act_in = active.to(device=dev, dtype=torch.uint8).contiguous()
+            act_out = torch.empty(B, dtype=torch.uint8, device=dev)
+            conv = torch.empty(B, dtype=dt, device=dev)
+            eq = torch.empty(B, dtype=dt, device=dev)
+            iq = torch.empty(B, dtype=dt, device=dev)
+            g = torch.empty((B, T, m), dtype=dt, device=dev)
+            sq = _lib.SqpStep(_lib.ptr(act_in), _lib.ptr(act_out), float(tol), _lib.ptr(conv), _lib.ptr(eq),
+                              _lib.ptr(iq), _lib.ptr(g))
+            st = getattr(lib, f"tmpc_sqp_admm_step_{sfx}")(
+                stream, ctypes.byref(dims), ctypes.byref(cq), ctypes.byref(sv), ctypes.byref(sv),
+                _lib.ptr(iters), ctypes.byref(cfg), ctypes.byref(sq), _lib.ptr(ws), nbytes,
+            )
+            _lib.check(f"tmpc_sqp_admm_step_{sfx}", st)
+            del keep
+            return outs, iters, None, (conv, eq, iq, g, act_out.bool())
         st = getattr(lib, f"tmpc_admm_direct_{sfx}")(
             stream, ctypes.byref(dims), ctypes.byref(cq), ctypes.byref(sv), ctypes.byref(sv),
             _lib.ptr(iters), ctypes.byref(cfg), _lib.ptr(ws), nbytes,

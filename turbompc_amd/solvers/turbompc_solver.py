@@ -414,6 +414,78 @@ class TurboMPCSolver:
 
     def _solve_impl(self, program, states, controls, admm_state0: Optional[ADMMState] = None) -> TurboMPCSolution:
         """The SQP loop of turbompc_solver.py:1519-1760, batched with per-problem termination."""
+        if (self._convergence_criterion == "first_order" and int(self._params["num_sqp_iteration_max"]) > 1
+                and self._forward_admm_backend == AdmmBackend.HIP_DIRECT):
+            return self._solve_impl_device(program, states, controls, admm_state0)
+        return self._solve_impl_masked(program, states, controls, admm_state0)
+
+    def _solve_impl_device(self, program, states, controls, admm_state0: Optional[ADMMState] = None) -> TurboMPCSolution:
+        """The SQP loop with the per-problem bookkeeping on the device: from the
+        second iteration on, each step is one tmpc_sqp_admm_step call that
+        evaluates the first-order check of the committed iterate (the check
+        the reference runs at the end of the previous iteration), applies the
+        activity test conv > tol_convergence and solves the QP of the problems
+        that pass it.  Stopped problems keep their iterate (zero ADMM
+        iterations), so no masked commit and no host synchronisation is needed
+        (one per iteration only when tol_convergence > 0, to stop early)."""
+        P, ap = self._params, self._params["admm"]
+        max_iter, tol = int(P["num_sqp_iteration_max"]), float(P["tol_convergence"])
+        alpha = float(ap.get("relaxation_parameter", 1.0))
+        admm = self._admm_solver_fwd
+        B, dev, dt = states.shape[0], states.device, states.dtype
+        qp = program.build_qp(states, controls)
+        if admm_state0 is None:
+            admm_state0 = admm.initial_state(qp, rho_bar=ap["rho"], states0=torch.zeros_like(states),
+                                             controls0=torch.zeros_like(controls))
+        admm_state = admm_state0
+        conv = torch.full((B,), float("inf"), dtype=dt, device=dev)
+        admm_iters = torch.zeros((B, max_iter), dtype=torch.int32, device=dev)
+        eq_v = torch.zeros((B, max_iter), dtype=dt, device=dev)
+        in_v = torch.zeros_like(eq_v)
+        conv_h = torch.zeros_like(eq_v)
+        num_iter = torch.zeros(B, dtype=torch.int32, device=dev)
+        active = torch.ones(B, dtype=torch.bool, device=dev)
+        g_c = None
+        last = 0
+        for it in range(max_iter):
+            sw = qp.ineq.slack_penalization_weight
+            if it == 0:  # cond_fun runs the first iteration unconditionally
+                (states, controls), stats, admm_state = admm.solve(qp, admm_state, rho_bar=ap["rho"], alpha=alpha,
+                                                                    slack_weight=sw)
+            else:
+                (states, controls), stats, admm_state, (cv, e, i, g), act = admm.sqp_step(
+                    qp, admm_state, active, tol, rho_bar=ap["rho"], alpha=alpha, slack_weight=sw)
+                # the check belongs to the iterate committed at it - 1
+                conv = torch.where(active, cv, conv)
+                eq_v[:, it - 1] = torch.where(active, e, eq_v[:, it - 1])
+                in_v[:, it - 1] = torch.where(active, i, in_v[:, it - 1])
+                conv_h[:, it - 1] = torch.where(active, cv, conv_h[:, it - 1])
+                g_c = g if g_c is None else torch.where(active[:, None, None], g, g_c)
+                active = act
+                if tol > 0 and not bool(active.any()):
+                    break  # no problem iterated in this step
+            admm_iters[:, it] = stats.num_iter
+            num_iter = num_iter + active.to(torch.int32)
+            last = it
+            if it + 1 < max_iter:
+                qp = program.build_qp(states, controls)
+        # the last committed iterate is not checked (the reference evaluates no
+        # check after its final iteration): its record keeps the previous error
+        # and G x at the QP it was solved on
+        conv_h[:, last] = torch.where(active, conv, conv_h[:, last])
+        g_last = apply_G(qp, pack_x(states, controls))
+        g_c = g_last if g_c is None else torch.where(active[:, None, None], g_last, g_c)
+        kkt = self._build_kkt_state(states, controls, admm_state, g_c, qp.ineq.l, qp.ineq.u)
+        return TurboMPCSolution(
+            states=states, controls=controls, slack=admm_state.xi_g, status=self.STATUS_SUCCESS, num_iter=num_iter,
+            convergence_error=conv, admm_iters=admm_iters, linesearch_alphas=None, admm_state=admm_state,
+            solver_stats=SolverStats(admm_iters, eq_v, in_v, conv_h), kkt_state=kkt,
+        )
+
+    def _solve_impl_masked(self, program, states, controls, admm_state0: Optional[ADMMState] = None) -> TurboMPCSolution:
+        """The SQP loop with host-side commits (masked selects once a problem
+        has stopped); used for the `step` criterion, single iterations and the
+        PCG backend."""
         P, ap = self._params, self._params["admm"]
         max_iter, tol = int(P["num_sqp_iteration_max"]), float(P["tol_convergence"])
         alpha = float(ap.get("relaxation_parameter", 1.0))
