@@ -66,6 +66,14 @@ typedef struct tmpc_state {
  * only the diagonal: the same products term by term (ignored by the other
  * paths). */
 #define TMPC_FLAG_DIAG_COST 4u
+/* Warm stage records (streaming path of tmpc_admm_direct_* and
+ * tmpc_sqp_admm_step_*): the workspace holds the stage records of the previous
+ * call, whose output state is this call's input state, and this QP differs from
+ * that call's only in A_minus and c (an SQP iteration relinearizing explicit
+ * dynamics: D, E, q, G, l, u, A0, c0 and the slack weight are unchanged).  Only
+ * the A_minus and c records are rewritten.  Vouched for by the caller; the
+ * other paths ignore it. */
+#define TMPC_FLAG_WARM_RECORDS 8u
 
 typedef struct tmpc_admm_cfg {
   int32_t max_iter, check_every, adapt_rho_every, pcg_max_iter, use_slack;

@@ -207,3 +207,25 @@ def test_sqp_step_check_and_activity(kernel, use_slack, dtype):
         a, b0, p = getattr(out, k).cpu().numpy(), getattr(st, k).cpu().numpy(), getattr(out_p, k).cpu().numpy()
         np.testing.assert_array_equal(a[~on], b0[~on])
         np.testing.assert_array_equal(a[on], p[on])
+
+
+def test_sqp_warm_records_match_repacking():
+    """FLAG_WARM_RECORDS: an SQP solve whose steps rewrite only the A_minus and
+    c records gives the same iterates, bit for bit, as one that repacks every
+    record at every step."""
+    import turbompc_amd.solvers.turbompc_solver as ts
+
+    B = 24
+    prob = make_quadrotor_config(B=B, seed=6, dtype=torch.float32, device="cuda")
+    solver = TurboMPCSolver(prob, _params(4, 12))
+    warm = solver.solve(solver.initial_guess())
+    orig = ts._same_static_blocks
+    try:
+        ts._same_static_blocks = lambda qp, prev: False
+        cold = solver.solve(solver.initial_guess())
+    finally:
+        ts._same_static_blocks = orig
+    torch.cuda.synchronize()
+    assert torch.equal(warm.states, cold.states) and torch.equal(warm.controls, cold.controls)
+    assert torch.equal(warm.admm_state.y_f_dyn, cold.admm_state.y_f_dyn)
+    assert torch.equal(warm.convergence_error, cold.convergence_error)

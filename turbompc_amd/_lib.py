@@ -26,6 +26,7 @@ DEFAULT_LIB = _PKG / "lib" / "libtmpc_hip.so"
 FLAG_STD_DYNAMICS = 1
 FLAG_GENERIC_KERNEL = 2
 FLAG_DIAG_COST = 4  # every D_t diagonal
+FLAG_WARM_RECORDS = 8  # the workspace's stage records are the previous SQP step's
 
 
 def flag_stream_p(p: int) -> int:

@@ -240,6 +240,27 @@ __global__ __launch_bounds__(kWave) void stage_pack_kernel(Dims d, QPDev<R> qp, 
   }
 }
 
+// Warm records: the stage records already hold the previous solve's output
+// state and this QP's blocks that do not change between SQP iterations (D, q,
+// G, l, u); only the relinearized dynamics rows (A_minus_t into M_t, c_t into
+// cz) are written.  One thread per element of a stage's nx (n + 1) values.
+template <typename R>
+__global__ void stage_repack_dynamics_kernel(Dims d, const R* __restrict__ Am, const R* __restrict__ c,
+                                             R* __restrict__ am, R* __restrict__ rv, int diag) {
+  const int per = d.nx * (d.n + 1);
+  const long long e = (long long)blockIdx.x * blockDim.x + threadIdx.x;
+  if (e >= (long long)d.B * d.N * per) return;
+  const RecGeom g = rec_geom(d, diag != 0);
+  const int k = (int)(e % per);
+  const long long bt = e / per;  // b * N + t
+  const int t = (int)(bt % d.N), b = (int)(bt / d.N);
+  const size_t rec = (size_t)t * d.B + b;
+  if (k < d.nx * d.n)
+    am[rec * g.amp + k] = Am[bt * d.nx * d.n + k];
+  else
+    rv[rec * g.rvp + g.c + (k - d.nx * d.n)] = c[bt * d.nx + (k - d.nx * d.n)];
+}
+
 template <typename R>
 __global__ __launch_bounds__(kWave) void stage_unpack_kernel(Dims d, const R* __restrict__ rv, StateDev<R> st) {
   const int b = blockIdx.x, t = blockIdx.y, tid = threadIdx.x;

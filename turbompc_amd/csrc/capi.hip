@@ -384,7 +384,14 @@ int admm_direct_impl(hipStream_t s, const tmpc_dims* dims, const tmpc_qp* qp,
     if (st) return st;
     a.act = sq->active_out;
   }
-  if (stream) {
+  if (stream && (cfg->flags & TMPC_FLAG_WARM_RECORDS)) {
+    const long long total = (long long)d.B * d.N * d.nx * (d.n + 1);
+    hipLaunchKernelGGL((stage_repack_dynamics_kernel<R>), dim3((unsigned)((total + 255) / 256)), dim3(256), 0, s, d,
+                       a.qp.Am, a.qp.c, w.am, w.rv, diag ? 1 : 0);
+    st = launch_status();
+    if (st) return st;
+    st = launch_factor_std<R>(s, d, w, a.qp, a.st.rho, a.sigma, a.rho_f_factor, nullptr, fp, diag);
+  } else if (stream) {
     hipLaunchKernelGGL((stage_pack_kernel<R>), dim3(d.B, d.T), dim3(kWave), 0, s, d, a.qp, a.st, w.am, w.rv, w.dm,
                        diag ? 1 : 0);
     st = launch_status();

@@ -162,7 +162,10 @@ class ADMMSolver:
         alpha: float = 1.0,
         *,
         slack_weight=0.0,
+        workspace: Optional[torch.Tensor] = None,
     ) -> Tuple[Tuple[torch.Tensor, torch.Tensor], ADMMStats, ADMMState]:
+        """`workspace` (direct backend): a caller-owned workspace instead of the
+        shared cached one (an SQP loop passes its own, see sqp_step)."""
         if not qp_data.cost.D.is_cuda:
             raise ValueError("ADMMSolver (HIP backends) needs device tensors; there is no CPU path")
         state0 = self.initial_state(qp_data, rho_bar=rho_bar) if admm_state0 is None else admm_state0
@@ -176,6 +179,7 @@ class ADMMSolver:
             cfg=cfg,
             slack_weight=sw,
             want_pcg_iters=self._admm_backend == AdmmBackend.HIP_PCG,
+            workspace=workspace,
         )
         x, z, yg, y0, yf, xi, rho = outs
         state = ADMMState(x_blocks=x, y_g=yg, y_f_0=y0, y_f_dyn=yf, z_g=z, xi_g=xi, rho_bar=rho)
@@ -183,19 +187,28 @@ class ADMMSolver:
         return (states, controls), ADMMStats(num_iter=iters, num_pcg_iters=pcg_iters), state
 
     def sqp_step(self, qp_data: QPData, admm_state0: ADMMState, active: torch.Tensor, tol: float,
-                 rho_bar: float = 1.0, alpha: float = 1.0, *, slack_weight=0.0):
+                 rho_bar: float = 1.0, alpha: float = 1.0, *, slack_weight=0.0,
+                 workspace: Optional[torch.Tensor] = None, warm_records: bool = False):
         """One device SQP step (tmpc_sqp_admm_step_*): the first-order check of
         admm_state0's iterate against qp_data, the activity test
         active & (conv > tol), and the solve of the problems that pass it (the
-        others keep their state and report 0 iterations).  Returns
+        others keep their state and report 0 iterations).  warm_records: the
+        caller vouches that `workspace` holds the records of the previous call
+        on it, whose output is admm_state0, and that qp_data differs from that
+        call's QP only in A_minus and c (FLAG_WARM_RECORDS).  Returns
         ((states, controls), stats, state, (conv, eq_err, ineq_err, g), active_out)."""
         if self._admm_backend != AdmmBackend.HIP_DIRECT:
             raise ValueError("sqp_step needs the direct Schur solve (HIP_DIRECT)")
+        if warm_records and workspace is None:
+            raise ValueError("warm_records needs the caller's workspace")
         std = self._std_dynamics if self._std_dynamics is not None else is_std_dynamics(qp_data)
-        cfg = self._cfg(alpha, (_lib.FLAG_STD_DYNAMICS if std else 0) | self._kernel_flags)
+        flags = (_lib.FLAG_STD_DYNAMICS if std else 0) | self._kernel_flags
+        if warm_records:
+            flags |= _lib.FLAG_WARM_RECORDS
+        cfg = self._cfg(alpha, flags)
         sw = slack_weight if self._use_slack else None
         outs, iters, _, (conv, eq, iq, g, act) = hip.admm_hip_solve(
-            qp_data, admm_state0, schur="direct", cfg=cfg, slack_weight=sw, sqp=(active, tol))
+            qp_data, admm_state0, schur="direct", cfg=cfg, slack_weight=sw, sqp=(active, tol), workspace=workspace)
         x, z, yg, y0, yf, xi, rho = outs
         state = ADMMState(x_blocks=x, y_g=yg, y_f_0=y0, y_f_dyn=yf, z_g=z, xi_g=xi, rho_bar=rho)
         states, controls = unpack_x(x, self._zshape)

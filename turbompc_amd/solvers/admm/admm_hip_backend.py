@@ -62,8 +62,20 @@ def cfg_struct(*, max_iter, check_every, adapt_rho_every, pcg_max_iter, use_slac
     )
 
 
+def direct_workspace(qp: QPData) -> torch.Tensor:
+    """A workspace of its own for tmpc_admm_direct_* / tmpc_sqp_admm_step_* (an
+    SQP loop keeps one per solve so that its stage records stay valid between
+    steps, see FLAG_WARM_RECORDS)."""
+    lib = _lib.load()
+    B, T, n, nx, n0, m = qp.dims
+    nbytes = lib.tmpc_admm_direct_workspace_bytes(8 if qp.dtype == torch.float64 else 4,
+                                                  ctypes.byref(_lib.Dims(B, T, n, nx, n0, m)))
+    return _lib.workspace(nbytes, qp.device)
+
+
 def admm_hip_solve(qp: QPData, state0, *, schur: str, cfg: _lib.AdmmCfg,
-                   slack_weight: Optional[torch.Tensor] = None, want_pcg_iters: bool = False, sqp=None):
+                   slack_weight: Optional[torch.Tensor] = None, want_pcg_iters: bool = False, sqp=None,
+                   workspace: Optional[torch.Tensor] = None):
     """Run the fused ADMM on the device.  `state0` is an ADMMState of batched
     tensors; returns (state fields tuple, iters (B,), pcg_iters or None).
 
@@ -102,7 +114,9 @@ def admm_hip_solve(qp: QPData, state0, *, schur: str, cfg: _lib.AdmmCfg,
     if schur == "direct":
         nbytes = lib.tmpc_admm_direct_workspace_bytes(ctypes.sizeof(ctypes.c_double) if dt == torch.float64 else 4,
                                                       ctypes.byref(dims))
-        ws = _ws("admm_direct", nbytes, dev)
+        ws = _ws("admm_direct", nbytes, dev) if workspace is None else workspace
+        if ws.numel() < nbytes:
+            raise ValueError(f"workspace of {ws.numel()} bytes, {nbytes} needed")
         if sqp is not None:
             active, tol = sqp
             act_in = active.to(device=dev, dtype=torch.uint8).contiguous()

@@ -25,6 +25,7 @@ import torch
 import yaml
 
 from .admm.admm import ADMMSolver, ADMMState
+from .admm.admm_hip_backend import direct_workspace as admm_direct_workspace
 from .linear_systems_solvers.backends import AdmmBackend, SchurSolverBackend
 from .qp_data import QPData
 from .qp_ops import apply_C_parts, apply_Ct, apply_G, apply_Gt, apply_P, inf_norm
@@ -447,14 +448,20 @@ class TurboMPCSolver:
         active = torch.ones(B, dtype=torch.bool, device=dev)
         g_c = None
         last = 0
+        # a workspace of the solve's own: its stage records stay valid between
+        # steps, so a step whose QP differs from the previous one only in the
+        # relinearized dynamics (A_minus, c) rewrites just those records
+        ws = admm_direct_workspace(qp)
+        prev = None
         for it in range(max_iter):
             sw = qp.ineq.slack_penalization_weight
             if it == 0:  # cond_fun runs the first iteration unconditionally
                 (states, controls), stats, admm_state = admm.solve(qp, admm_state, rho_bar=ap["rho"], alpha=alpha,
-                                                                    slack_weight=sw)
+                                                                    slack_weight=sw, workspace=ws)
             else:
                 (states, controls), stats, admm_state, (cv, e, i, g), act = admm.sqp_step(
-                    qp, admm_state, active, tol, rho_bar=ap["rho"], alpha=alpha, slack_weight=sw)
+                    qp, admm_state, active, tol, rho_bar=ap["rho"], alpha=alpha, slack_weight=sw, workspace=ws,
+                    warm_records=_same_static_blocks(qp, prev))
                 # the check belongs to the iterate committed at it - 1
                 conv = torch.where(active, cv, conv)
                 eq_v[:, it - 1] = torch.where(active, e, eq_v[:, it - 1])
@@ -467,6 +474,7 @@ class TurboMPCSolver:
             admm_iters[:, it] = stats.num_iter
             num_iter = num_iter + active.to(torch.int32)
             last = it
+            prev = qp
             if it + 1 < max_iter:
                 qp = program.build_qp(states, controls)
         # the last committed iterate is not checked (the reference evaluates no
@@ -626,6 +634,20 @@ class DifferentiableSolve:
         states, controls = _AttachSolution.apply(self._solver, sol, params_d, weights_d, keys, x0 is not None,
                                                  *inputs)
         return sol._replace(states=states, controls=controls)
+
+
+def _same_static_blocks(qp: QPData, prev: Optional[QPData]) -> bool:
+    """Whether qp differs from prev at most in A_minus and c: the blocks that
+    do not depend on the linearization point are the same tensors (the OCP
+    classes build them once per problem) and the slack weight is unchanged."""
+    if prev is None:
+        return False
+    same = lambda a, b: a is b  # noqa: E731
+    return (same(qp.cost.D, prev.cost.D) and same(qp.cost.E, prev.cost.E) and same(qp.cost.q, prev.cost.q)
+            and same(qp.eq.A0, prev.eq.A0) and same(qp.eq.c0, prev.eq.c0) and same(qp.eq.A_plus, prev.eq.A_plus)
+            and same(qp.ineq.G, prev.ineq.G) and same(qp.ineq.l, prev.ineq.l) and same(qp.ineq.u, prev.ineq.u)
+            and qp.ineq.use_slack_variables == prev.ineq.use_slack_variables
+            and float(qp.ineq.slack_penalization_weight) == float(prev.ineq.slack_penalization_weight))
 
 
 def _select_qp(mask: torch.Tensor, a: QPData, b: QPData) -> QPData:
