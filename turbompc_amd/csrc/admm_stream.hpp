@@ -243,39 +243,77 @@ __global__ __launch_bounds__(kWave) void stage_pack_kernel(Dims d, QPDev<R> qp, 
 // Warm records: the stage records already hold the previous solve's output
 // state and this QP's blocks that do not change between SQP iterations (D, q,
 // G, l, u); only the relinearized dynamics rows (A_minus_t into M_t, c_t into
-// cz) are written.  One thread per element of a stage's nx (n + 1) values.
-template <typename R>
-__global__ void stage_repack_dynamics_kernel(Dims d, const R* __restrict__ Am, const R* __restrict__ c,
-                                             R* __restrict__ am, R* __restrict__ rv, int diag) {
-  const int per = d.nx * (d.n + 1);
-  const long long e = (long long)blockIdx.x * blockDim.x + threadIdx.x;
-  if (e >= (long long)d.B * d.N * per) return;
-  const RecGeom g = rec_geom(d, diag != 0);
-  const int k = (int)(e % per);
-  const long long bt = e / per;  // b * N + t
-  const int t = (int)(bt % d.N), b = (int)(bt / d.N);
-  const size_t rec = (size_t)t * d.B + b;
-  if (k < d.nx * d.n)
-    am[rec * g.amp + k] = Am[bt * d.nx * d.n + k];
-  else
-    rv[rec * g.rvp + g.c + (k - d.nx * d.n)] = c[bt * d.nx + (k - d.nx * d.n)];
-}
+// cz) are written.  A block handles stage t of kRepackProblems consecutive
+// problems (adjacent records), one thread per value and problem, so that each
+// thread keeps several independent copies in flight.
+constexpr int kRepackProblems = 8;
 
 template <typename R>
-__global__ __launch_bounds__(kWave) void stage_unpack_kernel(Dims d, const R* __restrict__ rv, StateDev<R> st) {
-  const int b = blockIdx.x, t = blockIdx.y, tid = threadIdx.x;
+__global__ __launch_bounds__(256) void stage_repack_dynamics_kernel(Dims d, const R* __restrict__ Am,
+                                                                    const R* __restrict__ c, R* __restrict__ am,
+                                                                    R* __restrict__ rv, int diag) {
+  const int t = blockIdx.y, b0 = blockIdx.x * kRepackProblems;
+  const RecGeom g = rec_geom(d, diag != 0);
+  const int na = d.nx * d.n, per = na + d.nx;
+  for (int k = threadIdx.x; k < per; k += blockDim.x) {
+    R v[kRepackProblems];
+#pragma unroll
+    for (int j = 0; j < kRepackProblems; ++j) {
+      const int b = min(b0 + j, d.B - 1);
+      const size_t bt = (size_t)b * d.N + t;
+      v[j] = k < na ? Am[bt * na + k] : c[bt * d.nx + (k - na)];
+    }
+#pragma unroll
+    for (int j = 0; j < kRepackProblems; ++j) {
+      if (b0 + j >= d.B) break;
+      const size_t rec = (size_t)t * d.B + b0 + j;
+      if (k < na)
+        am[rec * g.amp + k] = v[j];
+      else
+        rv[rec * g.rvp + g.c + (k - na)] = v[j];
+    }
+  }
+}
+
+// The state back from the rv records: a block handles stage t of
+// kRepackProblems consecutive problems, one thread per state value of a stage
+// (x, z, y_g, xi, then y_f for t < N) across those problems.
+template <typename R>
+__global__ __launch_bounds__(256) void stage_unpack_kernel(Dims d, const R* __restrict__ rv, StateDev<R> st) {
+  const int t = blockIdx.y, b0 = blockIdx.x * kRepackProblems;
   const int B = d.B, T = d.T, N = d.N, n = d.n, nx = d.nx, m = d.m;
   const RecGeom g = rec_geom(d);
-  const R* s = rv + ((size_t)t * B + b) * g.rvp;
-  const size_t bt = (size_t)b * T + t;
-  for (int e = tid; e < n; e += kWave) st.x[bt * n + e] = s[g.x + e];
-  for (int e = tid; e < m; e += kWave) {
-    st.z[bt * m + e] = s[g.z + e];
-    st.y_g[bt * m + e] = s[g.yg + e];
-    st.xi[bt * m + e] = s[g.xi + e];
+  const int per = n + 3 * m + (t < N ? nx : 0);
+  for (int k = threadIdx.x; k < per; k += blockDim.x) {
+    // source offset in the record, destination array and its per-problem pitch
+    int src, e, pitch;
+    R* dst;
+    if (k < n) {
+      src = g.x + k; dst = st.x; e = k; pitch = n;
+    } else if (k < n + m) {
+      src = g.z + (k - n); dst = st.z; e = k - n; pitch = m;
+    } else if (k < n + 2 * m) {
+      src = g.yg + (k - n - m); dst = st.y_g; e = k - n - m; pitch = m;
+    } else if (k < n + 3 * m) {
+      src = g.xi + (k - n - 2 * m); dst = st.xi; e = k - n - 2 * m; pitch = m;
+    } else {
+      src = g.yf + (k - n - 3 * m); dst = st.y_f; e = k - n - 3 * m; pitch = nx;
+    }
+    const bool dyn = k >= n + 3 * m;  // y_f: (B, N, nx); the others (B, T, .)
+    R v[kRepackProblems];
+#pragma unroll
+    for (int j = 0; j < kRepackProblems; ++j) {
+      const int b = min(b0 + j, B - 1);
+      v[j] = rv[((size_t)t * B + b) * g.rvp + src];
+    }
+#pragma unroll
+    for (int j = 0; j < kRepackProblems; ++j) {
+      const int b = b0 + j;
+      if (b >= B) break;
+      const size_t row = dyn ? (size_t)b * N + t : (size_t)b * T + t;
+      dst[row * pitch + e] = v[j];
+    }
   }
-  if (t < N)
-    for (int e = tid; e < nx; e += kWave) st.y_f[((size_t)b * N + t) * nx + e] = s[g.yf + e];
 }
 
 // ---- wavefront helpers ---------------------------------------------------------

@@ -385,9 +385,9 @@ int admm_direct_impl(hipStream_t s, const tmpc_dims* dims, const tmpc_qp* qp,
     a.act = sq->active_out;
   }
   if (stream && (cfg->flags & TMPC_FLAG_WARM_RECORDS)) {
-    const long long total = (long long)d.B * d.N * d.nx * (d.n + 1);
-    hipLaunchKernelGGL((stage_repack_dynamics_kernel<R>), dim3((unsigned)((total + 255) / 256)), dim3(256), 0, s, d,
-                       a.qp.Am, a.qp.c, w.am, w.rv, diag ? 1 : 0);
+    hipLaunchKernelGGL((stage_repack_dynamics_kernel<R>),
+                       dim3((unsigned)((d.B + kRepackProblems - 1) / kRepackProblems), (unsigned)d.N), dim3(256), 0, s,
+                       d, a.qp.Am, a.qp.c, w.am, w.rv, diag ? 1 : 0);
     st = launch_status();
     if (st) return st;
     st = launch_factor_std<R>(s, d, w, a.qp, a.st.rho, a.sigma, a.rho_f_factor, nullptr, fp, diag);
@@ -423,7 +423,9 @@ int admm_direct_impl(hipStream_t s, const tmpc_dims* dims, const tmpc_qp* qp,
   }
   if (g_iter_events[1] && hipEventRecord(g_iter_events[1], s) != hipSuccess) return TMPC_ELAUNCH;
   if (stream) {
-    hipLaunchKernelGGL((stage_unpack_kernel<R>), dim3(d.B, d.T), dim3(kWave), 0, s, d, (const R*)w.rv, a.st);
+    hipLaunchKernelGGL((stage_unpack_kernel<R>),
+                       dim3((unsigned)((d.B + kRepackProblems - 1) / kRepackProblems), (unsigned)d.T), dim3(256), 0, s,
+                       d, (const R*)w.rv, a.st);
     st = launch_status();
     if (st) return st;
   }
