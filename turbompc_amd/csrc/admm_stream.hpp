@@ -991,7 +991,7 @@ __global__ __launch_bounds__(kWave, StreamOcc<R>::waves) void admm_stream_kernel
 // Gauss-Jordan pivot row.  Reads the stage records of stage_pack_kernel.
 
 // LDS of factor_std_kernel, in bytes: fp64 work area [P][n n] Theta_{t-1}^{-1}
-// and [P][n] pivot row, then the staged stage runs in the storage type R:
+// and [P][2 n] pivot rows, then the staged stage runs in the storage type R:
 // M_t = [A_minus_t; G_t] double-buffered [2][P][amp], D_t [P][pitch],
 // A0 [P][n0 n].
 struct FactorLayout {
@@ -1008,7 +1008,7 @@ __host__ __device__ inline FactorLayout factor_layout(const Dims& d, int P, bool
   const int n = d.n;
   L.th = 0;
   L.piv = P * n * n;
-  const int c_elems = L.piv + P * n;
+  const int c_elems = L.piv + 2 * P * n;
   L.r_base = ((size_t)c_elems * sizeof(double) + 15) / 16 * 16;
   L.am = 0;
   L.dm = 2 * P * g.amp;
@@ -1018,7 +1018,7 @@ __host__ __device__ inline FactorLayout factor_layout(const Dims& d, int P, bool
 }
 
 template <typename R, int NC, int P>
-__global__ __launch_bounds__(kWave) void factor_std_kernel(Dims d, const R* __restrict__ am, const R* __restrict__ dm, const R* __restrict__ A0,
+__global__ __launch_bounds__(kWave, 2) void factor_std_kernel(Dims d, const R* __restrict__ am, const R* __restrict__ dm, const R* __restrict__ A0,
                                                           const R* __restrict__ rho, R sigma, R rho_f_factor,
                                                           int32_t* __restrict__ ctl, R* __restrict__ thinv,
                                                           int diag) {
@@ -1041,7 +1041,7 @@ __global__ __launch_bounds__(kWave) void factor_std_kernel(Dims d, const R* __re
   const int n0n = n0 * n;
   const int nch_am = nprob * rg.amp / W, nch_dm = nprob * rg.dmp / W;
   C* th = lds + FL.th + p * n * n;
-  C* piv = lds + FL.piv + p * n;
+  C* piv = lds + FL.piv + p * 2 * n;  // two pivot rows
   const R* dmt = ldr + FL.dm + p * rg.dmp;
   const R* a0 = ldr + FL.a0 + p * n0n;
   for (int e = tid; e < nprob * n0n; e += kWave) ldr[FL.a0 + e] = A0[(size_t)b0 * n0n + e];
@@ -1153,30 +1153,57 @@ __global__ __launch_bounds__(kWave) void factor_std_kernel(Dims d, const R* __re
         }
       }
     }
-    // Gauss-Jordan inversion without pivoting, rows in lanes.  The pivot row k
-    // is not normalized at its step: it keeps the scale p_k (its diagonal entry
-    // holds 1 instead of 1/p_k), which the later row operations carry along,
-    // and is multiplied by 1/p_k after the last step.  So every step runs the
-    // same instructions in every lane (no divergent pivot-row branch).
-    C myip = C(0);
+    // Gauss-Jordan inversion without pivoting, rows in lanes, in 2x2 pivot
+    // blocks (half the pivot-row round trips; the pivot blocks of an SPD
+    // matrix are SPD).  For a block K = {k, k+1} with inverse Q of its 2x2
+    // pivot block, row i outside K takes a_i -= G_i [row_k; row_k+1] with
+    // G_i = (a_ik, a_ik+1) Q and a_iK = -G_i; the rows of K become Q times the
+    // pair.  Both are written as a_i -= g0 row_k + g1 row_k+1 with per-lane
+    // (g0, g1), so every lane runs the same instructions.  An odd n ends with
+    // a single step whose pivot row is normalized after the step (as in the
+    // 2x2 case, no divergent pivot-row branch).
+    C myip = C(1);
 #pragma unroll
-    for (int k = 0; k < NC; ++k) {
+    for (int k = 0; k < NC; k += 2) {
+      const bool pair = k + 1 < NC;
       wsync();
-      if (i == k)
+      if (i == k || (pair && i == k + 1))
 #pragma unroll
-        for (int j = 0; j < NC; ++j) piv[j] = a[j];
+        for (int j = 0; j < NC; ++j) piv[(i - k) * NC + j] = a[j];
       wsync();
       if (i < n) {
-        C pv[NC];
+        C p1[NC], p2[NC];
 #pragma unroll
-        for (int j = 0; j < NC; ++j) pv[j] = piv[j];
+        for (int j = 0; j < NC; ++j) {
+          p1[j] = piv[j];
+          p2[j] = pair ? piv[NC + j] : C(0);
+        }
         __builtin_amdgcn_sched_barrier(0);
-        const C ip = C(1) / pv[k];
-        const bool me = i == k;
-        myip = me ? ip : myip;
-        const C g = me ? C(0) : a[k] * ip;
+        const bool m0 = i == k, m1 = pair && i == k + 1;
+        if (pair) {
+          const C q00 = p1[k], q01 = p1[k + 1], q10 = p2[k], q11 = p2[k + 1];
+          const C idet = C(1) / (q00 * q11 - q01 * q10);
+          const C Q00 = q11 * idet, Q01 = -q01 * idet, Q10 = -q10 * idet, Q11 = q00 * idet;
+          const C f0 = a[k], f1 = a[k + 1];
+          C g0 = f0 * Q00 + f1 * Q10, g1 = f0 * Q01 + f1 * Q11;
+          g0 = m0 ? C(1) - Q00 : (m1 ? -Q10 : g0);
+          g1 = m0 ? -Q01 : (m1 ? C(1) - Q11 : g1);
 #pragma unroll
-        for (int j = 0; j < NC; ++j) a[j] = (j == k) ? (me ? C(1) : -g) : a[j] - g * pv[j];
+          for (int j = 0; j < NC; ++j) {
+            if (j == k)
+              a[j] = m0 ? Q00 : (m1 ? Q10 : -g0);
+            else if (j == k + 1)
+              a[j] = m0 ? Q01 : (m1 ? Q11 : -g1);
+            else
+              a[j] = a[j] - g0 * p1[j] - g1 * p2[j];
+          }
+        } else {
+          const C ip = C(1) / p1[k];
+          myip = m0 ? ip : myip;
+          const C g = m0 ? C(0) : a[k] * ip;
+#pragma unroll
+          for (int j = 0; j < NC; ++j) a[j] = (j == k) ? (m0 ? C(1) : -g) : a[j] - g * p1[j];
+        }
       }
     }
     wsync();
