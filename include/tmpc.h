@@ -237,6 +237,15 @@ int tmpc_quadrotor_linearize_f64(hipStream_t stream, int32_t B, int32_t N, const
                                  const double* controls, double dt, const double* params,
                                  double* A_minus, double* c);
 
+/* The RK4 step of the same dynamics: next (B,N,13) = predict_next_state(x_t, u_t)
+ * for t < N, the dynamics part of equality_constraints
+ * (turbompc/problems/optimal_control_problem.py:841-912), which the merit line
+ * search evaluates at trial points (turbompc/solvers/linesearch.py:14-52). */
+int tmpc_quadrotor_dynamics_f32(hipStream_t stream, int32_t B, int32_t N, const float* states,
+                                const float* controls, double dt, const double* params, float* next);
+int tmpc_quadrotor_dynamics_f64(hipStream_t stream, int32_t B, int32_t N, const double* states,
+                                const double* controls, double dt, const double* params, double* next);
+
 /* Lagrangian Hessian of the same dynamics rows for the exact-Hessian backward
  * pass: replaces get_dynamics_lagrangian_hessian for explicit schemes
  * (turbompc/problems/optimal_control_problem.py:1334-1441), called from

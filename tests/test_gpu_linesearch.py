@@ -1,0 +1,106 @@
+"""SQP with the merit line search (linesearch=True, turbompc/solvers/linesearch.py:54-178)
+on the GPU against the CPU restatement (oracle/sqp_cpu.py merit_linesearch) at
+fixed iteration counts: the quadrotor (config 3 shapes) and the obstacle
+workload (config 4 shapes) with hard and soft constraints.  The step chosen
+for every problem and SQP iteration must be the same; the iterates agree to
+the fp64 tolerance.  Also the quadrotor's RK4 step kernel
+(tmpc_quadrotor_dynamics_*), which the equality residuals of the merit use,
+against the CPU RK4."""
+import copy
+
+import numpy as np
+import pytest
+import torch
+
+import oracle
+from helpers import TOL, rel_err
+from oracle.sqp_cpu import obstacle_sqp, quadrotor_sqp
+from turbompc_amd.problems import configs
+from turbompc_amd.problems.ocp import LinearOCP
+from turbompc_amd.problems.quadrotor import make_quadrotor_config
+from turbompc_amd.solvers.turbompc_solver import DEFAULT_SOLVER_PARAMS, TurboMPCSolver
+
+pytestmark = pytest.mark.gpu
+
+
+def _params(n_sqp, admm_iters):
+    p = copy.deepcopy(DEFAULT_SOLVER_PARAMS)
+    p["num_sqp_iteration_max"] = n_sqp
+    p["tol_convergence"] = 0.0
+    p["admm"]["max_iter"] = admm_iters
+    p["admm"]["adapt_rho_every"] = 0
+    p["admm"]["relaxation_parameter"] = 1.0
+    p["linesearch"] = True
+    return p
+
+
+@pytest.mark.parametrize("dtype", [torch.float64, torch.float32])
+def test_quadrotor_dynamics_kernel_matches_cpu(dtype):
+    B = 9
+    prob = make_quadrotor_config(B=B, seed=2, dtype=torch.float64, device="cpu")
+    rng = np.random.default_rng(3)
+    T = prob.horizon + 1
+    s = rng.standard_normal((B, T, 13))
+    s[..., 3:7] /= np.linalg.norm(s[..., 3:7], axis=-1, keepdims=True)
+    u = rng.uniform(0.0, 4.0, (B, T, 4))
+    dev = make_quadrotor_config(B=B, seed=2, dtype=dtype, device="cuda")
+    got = dev.next_states(torch.tensor(s, dtype=dtype, device="cuda"), torch.tensor(u, dtype=dtype, device="cuda"))
+    torch.cuda.synchronize()
+    c = lambda a: torch.tensor(a, dtype=dtype).double().numpy()  # noqa: E731
+    xu = np.concatenate([c(s)[:, :-1], c(u)[:, :-1]], axis=-1).reshape(-1, 17)
+    f, _ = oracle.quadrotor_rk4_jac(xu, float(prob.dt), prob.params)
+    assert got.shape == (B, T - 1, 13)
+    assert rel_err(got, f.reshape(B, T - 1, 13)) < (1e-13 if dtype == torch.float64 else 2e-6)
+
+
+def test_quadrotor_sqp_linesearch_fp64_matches_cpu():
+    B, n_sqp, admm_iters = 8, 6, 20
+    cpu = make_quadrotor_config(B=B, seed=0, dtype=torch.float64, device="cpu")
+    D, E, q = (t.numpy() for t in cpu.cost_blocks())
+    A0, c0 = (t.numpy() for t in cpu.initial_equality())
+    G, l, u = (t.numpy() for t in cpu.inequality_blocks())
+    static = dict(D=D, E=E, q=q, A0=A0, c0=c0, A_plus=cpu.a_plus().numpy(), G=G, l=l, u=u)
+    xg, ug = (t.numpy() for t in cpu.initial_guess())
+    cfg = oracle.OracleCfg(max_iter=admm_iters, check_every=25, adapt_rho_every=0, sigma=1e-6, eps_abs=1e-9,
+                           eps_rel=1e-9, rho_f_factor=1000.0, alpha=1.0)
+    xs, us, st, _, alphas = quadrotor_sqp(static, xg, ug, dt=cpu.dt, params=cpu.params, cfg=cfg, rho0=0.1,
+                                          n_sqp=n_sqp, linesearch={})
+    print(f"  CPU steps {alphas.tolist()}", flush=True)
+    prob = make_quadrotor_config(B=B, seed=0, dtype=torch.float64, device="cuda")
+    solver = TurboMPCSolver(prob, _params(n_sqp, admm_iters))
+    sol = solver.solve(solver.initial_guess())
+    torch.cuda.synchronize()
+    np.testing.assert_array_equal(sol.linesearch_alphas.cpu().numpy(), alphas)
+    assert rel_err(sol.states, xs) < TOL[torch.float64]
+    assert rel_err(sol.controls, us) < TOL[torch.float64]
+    assert rel_err(sol.admm_state.y_f_dyn, st.y_f_dyn) < 1e-8
+    assert torch.all(sol.num_iter == n_sqp)
+    assert len(set(alphas.ravel().tolist())) >= 2
+
+
+@pytest.mark.parametrize("use_slack", [False, True])
+def test_config4_sqp_linesearch_fp64_matches_cpu(use_slack):
+    B, n_sqp, admm_iters, gamma = 6, 8, 30, 50.0
+    prob = configs.config4(B=B, seed=0, use_slack_variables=use_slack, slack_penalization_weight=gamma)
+    D, E, q = (t.numpy() for t in prob.cost_blocks())
+    A0, c0 = (t.numpy() for t in prob.initial_equality())
+    G, l, u = (t.numpy() for t in LinearOCP.inequality_blocks(prob))
+    static = dict(D=D, E=E, q=q, A0=A0, c0=c0, A_plus=prob.a_plus().numpy(), G=G, l=l, u=u)
+    xg, ug = (t.numpy() for t in prob.initial_guess())
+    Am, c = (t.numpy() for t in prob.dynamics_blocks(*prob.initial_guess()))
+    cfg = oracle.OracleCfg(max_iter=admm_iters, check_every=50, adapt_rho_every=0, sigma=1e-6, eps_abs=1e-9,
+                           eps_rel=1e-9, rho_f_factor=1000.0, alpha=1.0)
+    xs, us, st, sl, alphas = obstacle_sqp(static, xg, ug, A_minus=Am, c=c, centers=prob.centers.numpy(),
+                                          radii=prob.radii.numpy(), dim=3, cfg=cfg, rho0=0.1, n_sqp=n_sqp,
+                                          slack_weight=gamma, use_slack=use_slack, linesearch={})
+    print(f"  CPU steps {alphas.tolist()}", flush=True)
+    solver = TurboMPCSolver(prob.to("cuda"), _params(n_sqp, admm_iters))
+    sol = solver.solve(solver.initial_guess())
+    torch.cuda.synchronize()
+    np.testing.assert_array_equal(sol.linesearch_alphas.cpu().numpy(), alphas)
+    assert rel_err(sol.states, xs) < TOL[torch.float64]
+    assert rel_err(sol.controls, us) < TOL[torch.float64]
+    assert rel_err(sol.admm_state.y_g, st.y_g) < 1e-8
+    # the returned slack is the ADMM state's (turbompc_solver.py:1747-1751)
+    assert rel_err(sol.slack, st.xi_g) < 1e-8
+    assert len(set(alphas.ravel().tolist())) >= 3

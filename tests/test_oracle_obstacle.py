@@ -4,7 +4,7 @@ on and beyond the sphere, exactness of the linearization at its own point, and
 the Hessian against differences of the gradient and its null direction d."""
 import numpy as np
 
-from oracle.sqp_cpu import OBSTACLE_LOWER, linearize_obstacles, obstacle_hessian
+from oracle.sqp_cpu import OBSTACLE_LOWER, linearize_obstacles, obstacle_hessian, obstacle_values
 
 
 def _g(states, centers, radii, dim):
@@ -40,6 +40,11 @@ def test_known_answers_on_the_sphere():
     grad, lo, up = linearize_obstacles(s, c, r, 3)
     g = _g(s, c, r, 3)
     np.testing.assert_allclose(g[0, :, 0], [0.0, -1.0], atol=1e-12)
+    np.testing.assert_allclose(obstacle_values(s, c, r, 3)[0, :, 0], [0.0, -1.0], atol=1e-12)
+    # the centre: g = 1
+    s0 = np.zeros((1, 1, 6))
+    s0[0, 0, :3] = c[0, 0]
+    np.testing.assert_allclose(obstacle_values(s0, c, r, 3), 1.0, rtol=0, atol=0)
     np.testing.assert_allclose(grad[0, 0, 0], [0.0, -1.0 / 0.401, 0.0], atol=1e-12)
     np.testing.assert_allclose(grad[0, 1, 0], [0.0, 0.0, 1.0 / 0.401], atol=1e-12)
 

@@ -717,6 +717,21 @@ int quad_impl(hipStream_t s, int B, int N, const R* states, const R* controls, d
 }
 
 template <typename R>
+int quad_step_impl(hipStream_t s, int B, int N, const R* states, const R* controls, double dt, const double* params,
+                   R* next) {
+  if (B < 1 || N < 1) return TMPC_EBADSHAPE;
+  if (!states || !controls || !params || !next) return TMPC_EBADARG;
+  QuadParams<R> P{(R)params[0], (R)params[1], (R)params[2], (R)params[3],
+                  (R)params[4], (R)params[5], (R)params[6]};
+  const long long total = (long long)B * N;
+  const long long grid = (total + 255) / 256;
+  if (grid > INT32_MAX) return TMPC_EBADSHAPE;
+  hipLaunchKernelGGL((quad_step_kernel<R>), dim3((unsigned)grid), dim3(256), 0, s, B, N, states, controls, (R)dt, P,
+                     next);
+  return launch_status();
+}
+
+template <typename R>
 int quad_hess_impl(hipStream_t s, int B, int N, const R* states, const R* controls, double dt,
                    const double* params, const R* lambdas, R* H) {
   if (B < 1 || N < 1) return TMPC_EBADSHAPE;
@@ -956,6 +971,15 @@ int tmpc_quadrotor_linearize_f64(hipStream_t s, int32_t B, int32_t N, const doub
                                  const double* controls, double dt, const double* params, double* A_minus,
                                  double* c) {
   return quad_impl<double>(s, B, N, states, controls, dt, params, A_minus, c);
+}
+
+int tmpc_quadrotor_dynamics_f32(hipStream_t s, int32_t B, int32_t N, const float* states, const float* controls,
+                                double dt, const double* params, float* next) {
+  return quad_step_impl<float>(s, B, N, states, controls, dt, params, next);
+}
+int tmpc_quadrotor_dynamics_f64(hipStream_t s, int32_t B, int32_t N, const double* states, const double* controls,
+                                double dt, const double* params, double* next) {
+  return quad_step_impl<double>(s, B, N, states, controls, dt, params, next);
 }
 
 int tmpc_quadrotor_lagrangian_hessian_f32(hipStream_t s, int32_t B, int32_t N, const float* states,

@@ -131,6 +131,39 @@ __global__ __launch_bounds__(256) void quad_linearize_kernel(int B, int N, const
   }
 }
 
+// The RK4 step itself (predict_next_state for the explicit scheme, as used by
+// equality_constraints, turbompc/problems/optimal_control_problem.py:841-912):
+// next[b][t] = x_t + dt/6 (k1 + 2 k2 + 2 k3 + k4), one thread per (b, t < N).
+template <typename R>
+__global__ __launch_bounds__(256) void quad_step_kernel(int B, int N, const R* __restrict__ states,
+                                                        const R* __restrict__ controls, R dt, QuadParams<R> P,
+                                                        R* __restrict__ next) {
+  const long long pr = (long long)blockIdx.x * blockDim.x + threadIdx.x;
+  if (pr >= (long long)B * N) return;
+  const int b = (int)(pr / N), t = (int)(pr - (long long)b * N);
+  const int T = N + 1;
+  const R* xs = states + ((size_t)b * T + t) * 13;
+  const R* us = controls + ((size_t)b * T + t) * 4;
+  R x[13], u[4], k1[13], k2[13], k3[13], k4[13], tmp[13];
+#pragma unroll
+  for (int k = 0; k < 13; ++k) x[k] = xs[k];
+#pragma unroll
+  for (int k = 0; k < 4; ++k) u[k] = us[k];
+  quad_xdot(x, u, P, k1);
+#pragma unroll
+  for (int k = 0; k < 13; ++k) tmp[k] = x[k] + (R(0.5) * dt) * k1[k];
+  quad_xdot(tmp, u, P, k2);
+#pragma unroll
+  for (int k = 0; k < 13; ++k) tmp[k] = x[k] + (R(0.5) * dt) * k2[k];
+  quad_xdot(tmp, u, P, k3);
+#pragma unroll
+  for (int k = 0; k < 13; ++k) tmp[k] = x[k] + dt * k3[k];
+  quad_xdot(tmp, u, P, k4);
+  R* o = next + (size_t)pr * 13;
+#pragma unroll
+  for (int k = 0; k < 13; ++k) o[k] = x[k] + (R(1) / R(6)) * ((k1[k] + R(2) * k2[k] + R(2) * k3[k] + k4[k]) * dt);
+}
+
 // Lagrangian Hessian of the dynamics rows, get_dynamics_lagrangian_hessian for
 // explicit schemes (turbompc/problems/optimal_control_problem.py:1334-1441):
 //   H_t = d^2 / dz_t^2 [lambda_t . f(z_t)],  t < N;   H_N = 0,

@@ -76,6 +76,15 @@ class ObstacleOCP(LinearOCP):
     def inequality_blocks(self):
         raise NotImplementedError("obstacle rows depend on the iterate; use inequality_blocks_at(states, controls)")
 
+    def inequality_values(self, states, controls):
+        """(g, l, u): the box rows, then g_k = 1 - |p - c_k| / (r_k + 0.001) with
+        bounds (-1e9, 0) (obstacle_avoidance.py:16-52)."""
+        g, lo, hi = super().inequality_values(states, controls)
+        d = states[..., None, : self.obstacles_dimension] - self.centers[:, None]
+        go = 1.0 - torch.linalg.norm(d, dim=-1) / (self.radii[:, None] + 0.001)
+        return (torch.cat([g, go], dim=-1), torch.cat([lo, torch.full_like(go, -1.0e9)], dim=-1),
+                torch.cat([hi, torch.zeros_like(go)], dim=-1))
+
     def inequality_lagrangian_hessian(self, states, controls, mus):
         """(B, T, n, n): sum_k mu_k d^2 g_k/dz^2 of the obstacle rows (box rows are linear)."""
         states = states.to(self.dtype).contiguous()

@@ -147,6 +147,60 @@ class QuadraticTrackingOCP:
         (get_inequality_lagrangian_hessian, optimal_control_problem.py:1443-1480)."""
         return None
 
+    # ------------------------------------------------ merit-function terms ----
+    def tracking_weights(self):
+        """(w, zref), each (B, T, n): the per-stage weights of the tracking
+        cost (w_x + w_f on the final state) and the reference (the control
+        reference only with penalize_control_reference)."""
+        B, N = self.B, self.horizon
+        T, n = N + 1, self.num_state_variables + self.num_control_variables
+        w = torch.cat([self.wx, self.wu], dim=-1).unsqueeze(1).expand(B, T, n).clone()
+        w[:, N, : self.num_state_variables] += self.wf
+        uref = self.u_ref if self.penalize_control_reference else torch.zeros_like(self.u_ref)
+        return w, torch.cat([self.x_ref, uref], dim=-1)
+
+    def cost(self, states, controls, slacks=None):
+        """(B,) cost of each problem (cost, optimal_control_problem.py:982-1066:
+        sum_t w (z_t - zref_t)^2 with the final-state weight w_x + w_f), plus
+        gamma/2 |slack|^2 for soft constraints (cost_with_slack, :1504-1515)."""
+        w, zref = self.tracking_weights()
+        e = torch.cat([states, controls], dim=-1) - zref
+        c = (w * e * e).flatten(1).sum(dim=1)
+        if self.use_slack_variables and slacks is not None and slacks.numel():
+            c = c + 0.5 * self.slack_penalization_weight * (slacks * slacks).flatten(1).sum(dim=1)
+        return c
+
+    def cost_directional_derivative(self, states, controls, slacks, dstates, dcontrols, dslacks):
+        """(B,) gradient of `cost` along the direction (dstates, dcontrols, dslacks)."""
+        w, zref = self.tracking_weights()
+        z = torch.cat([states, controls], dim=-1)
+        d = (2.0 * w * (z - zref) * torch.cat([dstates, dcontrols], dim=-1)).flatten(1).sum(dim=1)
+        if self.use_slack_variables and slacks is not None and slacks.numel():
+            d = d + self.slack_penalization_weight * (slacks * dslacks).flatten(1).sum(dim=1)
+        return d
+
+    def next_states(self, states: torch.Tensor, controls: torch.Tensor) -> torch.Tensor:
+        """(B, N, nx): the discrete dynamics x_{t+1} = f(x_t, u_t) for t < N."""
+        raise NotImplementedError
+
+    def equality_residuals(self, states, controls):
+        """(B, T, nx): x_0 - x0, then f(x_t, u_t) - x_{t+1} (equality_constraints,
+        optimal_control_problem.py:841-912)."""
+        x0 = (states[:, 0] - self.x0).unsqueeze(1)
+        return torch.cat([x0, self.next_states(states, controls) - states[:, 1:]], dim=1)
+
+    def inequality_values(self, states, controls):
+        """(g, l, u), each (B, T, m): the inequality rows g(x, u) and their
+        bounds (step_inequality_constraints, :413-471)."""
+        nx = self.num_state_variables
+        rows = [i for i in range(nx) if bool(self.state_mask[i])] + \
+            [nx + j for j in range(self.num_control_variables) if bool(self.control_mask[j])]
+        z = torch.cat([states, controls], dim=-1)
+        g = z[..., rows]
+        lo = torch.cat([self.x_bounds[0][self.state_mask], self.u_bounds[0][self.control_mask]])
+        hi = torch.cat([self.x_bounds[1][self.state_mask], self.u_bounds[1][self.control_mask]])
+        return g, lo.expand_as(g), hi.expand_as(g)
+
     # -------------------------------------------------------- parameters ----
     WEIGHT_KEYS = (
         "weights_penalization_reference_state_trajectory",
@@ -271,6 +325,11 @@ class LinearOCP(QuadraticTrackingOCP):
 
     def dynamics_lagrangian_hessian(self, states, controls, lambdas):
         return None  # linear dynamics
+
+    def next_states(self, states, controls):
+        xn = torch.einsum("bij,btj->bti", self.A, states[:, :-1]) + torch.einsum("bij,btj->bti", self.Bm,
+                                                                                controls[:, :-1])
+        return xn + self.b.unsqueeze(1)
 
     def dynamics_blocks(self, states, controls):
         N = self.horizon

@@ -54,6 +54,22 @@ class QuadrotorOCP(QuadraticTrackingOCP):
         _lib.check(f"tmpc_quadrotor_linearize_{sfx}", st)
         return Am, c
 
+    def next_states(self, states, controls):
+        """(B, N, 13): the RK4 step at every stage (tmpc_quadrotor_dynamics_*)."""
+        if not states.is_cuda:
+            raise ValueError("QuadrotorOCP dynamics run on the GPU; pass device tensors")
+        lib = _lib.load()
+        B, N = self.B, self.horizon
+        states = states.to(self.dtype).contiguous()
+        controls = controls.to(self.dtype).contiguous()
+        nxt = torch.empty((B, N, 13), dtype=self.dtype, device=states.device)
+        sfx = _lib.suffix(self.dtype)
+        st = getattr(lib, f"tmpc_quadrotor_dynamics_{sfx}")(
+            _lib.stream_handle(states.device), B, N, _lib.ptr(states), _lib.ptr(controls), self.dt,
+            self._cparams, _lib.ptr(nxt))
+        _lib.check(f"tmpc_quadrotor_dynamics_{sfx}", st)
+        return nxt
+
     def dynamics_lagrangian_hessian(self, states, controls, lambdas):
         """(B, N+1, 17, 17): d^2/dz_t^2 [lambda_t . f(z_t)] for t < N, zero at N
         (tmpc_quadrotor_lagrangian_hessian_*, hyper-dual numbers on the device)."""

@@ -1,0 +1,73 @@
+"""Backtracking line search on the l1 merit function, batched over problems.
+
+Follows backtracking_linesearch / evaluate_constraints_with_bounds
+(turbompc/solvers/linesearch.py:14-178), which the reference applies per
+problem under vmap:
+  merit(z)  = cost(z) + mu * (|h(z)|_1 + |viol(g(z))|_1)
+  mu        = clip(nan_to_num(dcost / (0.5 max(|c|_1, floor))), mu_min, mu_max)
+  accept the largest alpha of `linesearch_alphas` with
+      merit(z + alpha dz) <= merit(z) + eta alpha (dcost - mu |c|_1)
+  and, when no finite candidate passes, the finite candidate of least merit
+  (the first candidate if none is finite).
+The problem supplies cost, cost_directional_derivative, equality_residuals
+and inequality_values (problems/ocp.py).
+"""
+from __future__ import annotations
+
+from typing import Any, Dict, Tuple
+
+import torch
+
+
+def evaluate_constraints_with_bounds(program, states, controls, slacks):
+    """(|h|_1, |viol|_1) per problem, with g + slack for soft constraints
+    (evaluate_constraints_with_bounds, linesearch.py:14-52)."""
+    eq = program.equality_residuals(states, controls).abs().flatten(1).sum(dim=1)
+    g, lo, hi = program.inequality_values(states, controls)
+    if getattr(program, "use_slack_variables", False) and slacks is not None and slacks.numel():
+        g = g + slacks
+    if g.shape[-1] == 0:
+        return eq, torch.zeros_like(eq)
+    viol = torch.clamp(lo - g, min=0.0) + torch.clamp(g - hi, min=0.0)
+    return eq, viol.flatten(1).sum(dim=1)
+
+
+def backtracking_linesearch(program, solver_params: Dict[str, Any], states, controls, slacks, states_new,
+                            controls_new, slacks_new) -> Tuple[Tuple[torch.Tensor, torch.Tensor, torch.Tensor],
+                                                               torch.Tensor]:
+    """Returns ((states, controls, slacks) at the accepted step, alpha (B,))."""
+    eta = float(solver_params["linesearch_eta"])
+    alphas = [float(a) for a in solver_params["linesearch_alphas"]]
+    mu_min = float(solver_params.get("linesearch_mu_min", 0.1))
+    mu_max = float(solver_params.get("linesearch_mu_max", 1.0e6))
+    floor = float(solver_params.get("linesearch_constraint_floor", 1.0e-8))
+    ds, dc, dsl = states_new - states, controls_new - controls, slacks_new - slacks
+
+    cost = program.cost(states, controls, slacks)
+    dcost = program.cost_directional_derivative(states, controls, slacks, ds, dc, dsl)
+    eq, iq = evaluate_constraints_with_bounds(program, states, controls, slacks)
+    cl1 = eq + iq
+    mu_raw = dcost / (0.5 * torch.clamp(cl1, min=floor))
+    mu = torch.clamp(torch.nan_to_num(mu_raw, nan=mu_min, posinf=mu_max, neginf=mu_min), mu_min, mu_max)
+    merit = cost + mu * cl1
+    merit_deriv = dcost - mu * cl1
+
+    cand, dec = [], []
+    for a in alphas:
+        s_a, c_a, sl_a = states + a * ds, controls + a * dc, slacks + a * dsl
+        e_a, i_a = evaluate_constraints_with_bounds(program, s_a, c_a, sl_a)
+        m_a = program.cost(s_a, c_a, sl_a) + mu * (e_a + i_a)
+        cand.append(m_a)
+        dec.append(m_a - (merit + eta * a * merit_deriv))
+    cand, dec = torch.stack(cand, dim=1), torch.stack(dec, dim=1)  # (B, n_alpha)
+    a_t = torch.tensor(alphas, dtype=cand.dtype, device=cand.device)
+    finite = torch.isfinite(a_t)[None] & torch.isfinite(cand) & torch.isfinite(dec)
+    valid = finite & (dec <= 0)
+    idx = torch.arange(len(alphas), device=cand.device).expand_as(cand)
+    valid_index = torch.where(valid, idx, torch.full_like(idx, -1)).amax(dim=1)
+    best_finite = torch.where(finite, cand, torch.full_like(cand, float("inf"))).argmin(dim=1)
+    fallback = torch.where(finite.any(dim=1), best_finite, torch.zeros_like(best_finite))
+    index = torch.where(valid_index >= 0, valid_index, fallback)
+    alpha = a_t[index]
+    al = alpha.view(-1, 1, 1)
+    return (states + al * ds, controls + al * dc, slacks + al * dsl), alpha

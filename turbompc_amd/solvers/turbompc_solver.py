@@ -27,6 +27,7 @@ import yaml
 from .admm.admm import ADMMSolver, ADMMState
 from .admm.admm_hip_backend import direct_workspace as admm_direct_workspace
 from .linear_systems_solvers.backends import AdmmBackend, SchurSolverBackend
+from .linesearch import backtracking_linesearch
 from .qp_data import QPData
 from .qp_ops import apply_C_parts, apply_Ct, apply_G, apply_Gt, apply_P, inf_norm
 from .qp_utils import ZShape, pack_x, pack_z
@@ -206,8 +207,6 @@ class TurboMPCSolver:
             raise ValueError(
                 f"backward backend {self._backward_backend.name} needs the reference's JAX/CUDA stack; "
                 "use 'direct_hip_kkt'")
-        if self._params.get("linesearch", False):
-            raise NotImplementedError("the merit line search (turbompc/solvers/linesearch.py) is not provided")
         self._forward_admm_backend, self._forward_schur_backend = _FORWARD_BACKEND_COMPONENTS[self._forward_backend]
         self._zshape = ZShape(program.horizon, program.num_state_variables, program.num_control_variables)
         ap = self._params["admm"]
@@ -248,7 +247,8 @@ class TurboMPCSolver:
         zi = lambda *s: torch.zeros(s, dtype=torch.int32, device=states.device)  # noqa: E731
         return TurboMPCSolution(
             states=states, controls=controls, slack=z(B, states.shape[1], m), status=self.STATUS_SUCCESS,
-            num_iter=zi(B), convergence_error=z(B), admm_iters=zi(B, max_iter), linesearch_alphas=None,
+            num_iter=zi(B), convergence_error=z(B), admm_iters=zi(B, max_iter),
+            linesearch_alphas=z(B, max_iter) if self._params.get("linesearch") else None,
             admm_state=None,
             solver_stats=SolverStats(zi(B, max_iter), z(B, max_iter), z(B, max_iter), z(B, max_iter)),
             dual_backward_guess=None, kkt_state=None,
@@ -416,7 +416,7 @@ class TurboMPCSolver:
     def _solve_impl(self, program, states, controls, admm_state0: Optional[ADMMState] = None) -> TurboMPCSolution:
         """The SQP loop of turbompc_solver.py:1519-1760, batched with per-problem termination."""
         if (self._convergence_criterion == "first_order" and int(self._params["num_sqp_iteration_max"]) > 1
-                and self._forward_admm_backend == AdmmBackend.HIP_DIRECT):
+                and self._forward_admm_backend == AdmmBackend.HIP_DIRECT and not self._params.get("linesearch")):
             return self._solve_impl_device(program, states, controls, admm_state0)
         return self._solve_impl_masked(program, states, controls, admm_state0)
 
@@ -492,8 +492,10 @@ class TurboMPCSolver:
 
     def _solve_impl_masked(self, program, states, controls, admm_state0: Optional[ADMMState] = None) -> TurboMPCSolution:
         """The SQP loop with host-side commits (masked selects once a problem
-        has stopped); used for the `step` criterion, single iterations and the
-        PCG backend."""
+        has stopped); used for the `step` criterion, single iterations, the
+        PCG backend and the merit line search, whose iterate (a blend of the
+        previous iterate and the QP solution, linesearch.py:54-178) differs
+        from the ADMM state's primal variable."""
         P, ap = self._params, self._params["admm"]
         max_iter, tol = int(P["num_sqp_iteration_max"]), float(P["tol_convergence"])
         alpha = float(ap.get("relaxation_parameter", 1.0))
@@ -517,6 +519,8 @@ class TurboMPCSolver:
         num_iter = torch.zeros(B, dtype=torch.int32, device=dev)
         active = torch.ones(B, dtype=torch.bool, device=dev)
         g_c = None  # G x (+ slack) at each problem's last committed iterate
+        use_ls = bool(P.get("linesearch", False))
+        ls_alphas = torch.zeros((B, max_iter), dtype=dt, device=dev) if use_ls else None
         for it in range(max_iter):
             if it >= 1:
                 active = active & (conv > tol)
@@ -528,6 +532,12 @@ class TurboMPCSolver:
             (s_new, c_new), stats, adm_new = admm.solve(qp, admm_state, rho_bar=ap["rho"], alpha=alpha,
                                                         slack_weight=qp.ineq.slack_penalization_weight)
             sl_new = adm_new.xi_g
+            if use_ls:
+                # the step (s_new, c_new, sl_new) - (states, controls, slacks) is
+                # scaled per problem; the ADMM state (multipliers, x blocks) is not
+                (s_new, c_new, sl_new), ls_a = backtracking_linesearch(program, P, states, controls, slacks, s_new,
+                                                                     c_new, sl_new)
+                ls_alphas[:, it] = ls_a if all_active else torch.where(active, ls_a, ls_alphas[:, it])
             if need_step:
                 z_new = pack_z(s_new, c_new)
                 step = (z_new - z_prev).abs().amax(dim=1)
@@ -575,7 +585,7 @@ class TurboMPCSolver:
             kkt = self._build_kkt_state(states, controls, admm_state, g_c, qp.ineq.l, qp.ineq.u)
         return TurboMPCSolution(
             states=states, controls=controls, slack=admm_state.xi_g, status=self.STATUS_SUCCESS, num_iter=num_iter,
-            convergence_error=conv, admm_iters=admm_iters, linesearch_alphas=None, admm_state=admm_state,
+            convergence_error=conv, admm_iters=admm_iters, linesearch_alphas=ls_alphas, admm_state=admm_state,
             solver_stats=SolverStats(admm_iters, eq_v, in_v, conv_h), kkt_state=kkt,
         )
 
