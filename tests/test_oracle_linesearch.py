@@ -215,7 +215,7 @@ def test_host_linesearch_matches_oracle(case):
     s_new, c_new = states + scale * r(states), controls + scale * r(controls)
     sl_new = slacks + scale * 0.1 * r(slacks) if use_slack else slacks.clone()
     params = dict(linesearch_eta=0.4, linesearch_alphas=[0.1, 0.3, 0.7, 1.0])
-    (s, u, sl), alpha = backtracking_linesearch(prob, params, states, controls, slacks, s_new, c_new, sl_new)
+    (s, u, sl), alpha = backtracking_linesearch(prob, None, params, states, controls, slacks, s_new, c_new, sl_new)
     merit = _oracle_merit(prob, states, controls, use_slack, 30.0)
     n = lambda t: t.numpy()  # noqa: E731
     (s_o, u_o, sl_o), alpha_o, _ = merit_linesearch(merit, n(states), n(controls), n(slacks), n(s_new), n(c_new),
@@ -226,7 +226,7 @@ def test_host_linesearch_matches_oracle(case):
     np.testing.assert_allclose(u.numpy(), u_o, rtol=0, atol=1e-13)
     np.testing.assert_allclose(sl.numpy(), sl_o, rtol=0, atol=1e-13)
     # the constraint norms of both sides at the start point
-    e, i = evaluate_constraints_with_bounds(prob, states, controls, slacks)
+    e, i, *_ = evaluate_constraints_with_bounds(prob, states, controls, slacks)
     np.testing.assert_allclose((e + i).numpy(), merit.constraint_l1(n(states), n(controls), n(slacks)),
                                rtol=1e-12)
     # the cost differs from the QP-block cost by a constant only

@@ -10,7 +10,8 @@ problem under vmap:
   and, when no finite candidate passes, the finite candidate of least merit
   (the first candidate if none is finite).
 The problem supplies cost, cost_directional_derivative, equality_residuals
-and inequality_values (problems/ocp.py).
+and inequality_values (problems/ocp.py); problem_params, when given, are
+applied with program.with_params as in the solver.
 """
 from __future__ import annotations
 
@@ -19,23 +20,29 @@ from typing import Any, Dict, Tuple
 import torch
 
 
-def evaluate_constraints_with_bounds(program, states, controls, slacks):
-    """(|h|_1, |viol|_1) per problem, with g + slack for soft constraints
-    (evaluate_constraints_with_bounds, linesearch.py:14-52)."""
+def _with_params(program, problem_params):
+    return program.with_params(problem_params) if problem_params else program
+
+
+def evaluate_constraints_with_bounds(program, states, controls, slacks, problem_params=None):
+    """(|h|_1 (B,), |viol|_1 (B,), g, l, u (B, T, m)), with g + slack for soft
+    constraints (evaluate_constraints_with_bounds, linesearch.py:14-52)."""
+    program = _with_params(program, problem_params)
     eq = program.equality_residuals(states, controls).abs().flatten(1).sum(dim=1)
     g, lo, hi = program.inequality_values(states, controls)
     if getattr(program, "use_slack_variables", False) and slacks is not None and slacks.numel():
         g = g + slacks
     if g.shape[-1] == 0:
-        return eq, torch.zeros_like(eq)
+        return eq, torch.zeros_like(eq), g, lo, hi
     viol = torch.clamp(lo - g, min=0.0) + torch.clamp(g - hi, min=0.0)
-    return eq, viol.flatten(1).sum(dim=1)
+    return eq, viol.flatten(1).sum(dim=1), g, lo, hi
 
 
-def backtracking_linesearch(program, solver_params: Dict[str, Any], states, controls, slacks, states_new,
-                            controls_new, slacks_new) -> Tuple[Tuple[torch.Tensor, torch.Tensor, torch.Tensor],
-                                                               torch.Tensor]:
+def backtracking_linesearch(program, problem_params, solver_params: Dict[str, Any], states, controls, slacks,
+                            states_new, controls_new, slacks_new
+                            ) -> Tuple[Tuple[torch.Tensor, torch.Tensor, torch.Tensor], torch.Tensor]:
     """Returns ((states, controls, slacks) at the accepted step, alpha (B,))."""
+    program = _with_params(program, problem_params)
     eta = float(solver_params["linesearch_eta"])
     alphas = [float(a) for a in solver_params["linesearch_alphas"]]
     mu_min = float(solver_params.get("linesearch_mu_min", 0.1))
@@ -45,7 +52,7 @@ def backtracking_linesearch(program, solver_params: Dict[str, Any], states, cont
 
     cost = program.cost(states, controls, slacks)
     dcost = program.cost_directional_derivative(states, controls, slacks, ds, dc, dsl)
-    eq, iq = evaluate_constraints_with_bounds(program, states, controls, slacks)
+    eq, iq, *_ = evaluate_constraints_with_bounds(program, states, controls, slacks)
     cl1 = eq + iq
     mu_raw = dcost / (0.5 * torch.clamp(cl1, min=floor))
     mu = torch.clamp(torch.nan_to_num(mu_raw, nan=mu_min, posinf=mu_max, neginf=mu_min), mu_min, mu_max)
@@ -55,7 +62,7 @@ def backtracking_linesearch(program, solver_params: Dict[str, Any], states, cont
     cand, dec = [], []
     for a in alphas:
         s_a, c_a, sl_a = states + a * ds, controls + a * dc, slacks + a * dsl
-        e_a, i_a = evaluate_constraints_with_bounds(program, s_a, c_a, sl_a)
+        e_a, i_a, *_ = evaluate_constraints_with_bounds(program, s_a, c_a, sl_a)
         m_a = program.cost(s_a, c_a, sl_a) + mu * (e_a + i_a)
         cand.append(m_a)
         dec.append(m_a - (merit + eta * a * merit_deriv))

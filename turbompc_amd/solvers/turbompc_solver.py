@@ -535,8 +535,8 @@ class TurboMPCSolver:
             if use_ls:
                 # the step (s_new, c_new, sl_new) - (states, controls, slacks) is
                 # scaled per problem; the ADMM state (multipliers, x blocks) is not
-                (s_new, c_new, sl_new), ls_a = backtracking_linesearch(program, P, states, controls, slacks, s_new,
-                                                                     c_new, sl_new)
+                (s_new, c_new, sl_new), ls_a = backtracking_linesearch(program, None, P, states, controls, slacks,
+                                                                     s_new, c_new, sl_new)
                 ls_alphas[:, it] = ls_a if all_active else torch.where(active, ls_a, ls_alphas[:, it])
             if need_step:
                 z_new = pack_z(s_new, c_new)
