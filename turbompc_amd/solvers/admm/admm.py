@@ -163,9 +163,12 @@ class ADMMSolver:
         *,
         slack_weight=0.0,
         workspace: Optional[torch.Tensor] = None,
+        donate_state: bool = False,
     ) -> Tuple[Tuple[torch.Tensor, torch.Tensor], ADMMStats, ADMMState]:
         """`workspace` (direct backend): a caller-owned workspace instead of the
-        shared cached one (an SQP loop passes its own, see sqp_step)."""
+        shared cached one (an SQP loop passes its own, see sqp_step).
+        donate_state: admm_state0's buffers may be updated in place (the caller
+        does not read admm_state0 again)."""
         if not qp_data.cost.D.is_cuda:
             raise ValueError("ADMMSolver (HIP backends) needs device tensors; there is no CPU path")
         state0 = self.initial_state(qp_data, rho_bar=rho_bar) if admm_state0 is None else admm_state0
@@ -180,6 +183,7 @@ class ADMMSolver:
             slack_weight=sw,
             want_pcg_iters=self._admm_backend == AdmmBackend.HIP_PCG,
             workspace=workspace,
+            donate=donate_state and admm_state0 is not None,
         )
         x, z, yg, y0, yf, xi, rho = outs
         state = ADMMState(x_blocks=x, y_g=yg, y_f_0=y0, y_f_dyn=yf, z_g=z, xi_g=xi, rho_bar=rho)
@@ -188,14 +192,16 @@ class ADMMSolver:
 
     def sqp_step(self, qp_data: QPData, admm_state0: ADMMState, active: torch.Tensor, tol: float,
                  rho_bar: float = 1.0, alpha: float = 1.0, *, slack_weight=0.0,
-                 workspace: Optional[torch.Tensor] = None, warm_records: bool = False):
+                 workspace: Optional[torch.Tensor] = None, warm_records: bool = False,
+                 donate_state: bool = False):
         """One device SQP step (tmpc_sqp_admm_step_*): the first-order check of
         admm_state0's iterate against qp_data, the activity test
         active & (conv > tol), and the solve of the problems that pass it (the
         others keep their state and report 0 iterations).  warm_records: the
         caller vouches that `workspace` holds the records of the previous call
         on it, whose output is admm_state0, and that qp_data differs from that
-        call's QP only in A_minus and c (FLAG_WARM_RECORDS).  Returns
+        call's QP only in A_minus and c (FLAG_WARM_RECORDS).  donate_state:
+        admm_state0's buffers may be updated in place.  Returns
         ((states, controls), stats, state, (conv, eq_err, ineq_err, g), active_out)."""
         if self._admm_backend != AdmmBackend.HIP_DIRECT:
             raise ValueError("sqp_step needs the direct Schur solve (HIP_DIRECT)")
@@ -208,7 +214,8 @@ class ADMMSolver:
         cfg = self._cfg(alpha, flags)
         sw = slack_weight if self._use_slack else None
         outs, iters, _, (conv, eq, iq, g, act) = hip.admm_hip_solve(
-            qp_data, admm_state0, schur="direct", cfg=cfg, slack_weight=sw, sqp=(active, tol), workspace=workspace)
+            qp_data, admm_state0, schur="direct", cfg=cfg, slack_weight=sw, sqp=(active, tol), workspace=workspace,
+            donate=donate_state)
         x, z, yg, y0, yf, xi, rho = outs
         state = ADMMState(x_blocks=x, y_g=yg, y_f_0=y0, y_f_dyn=yf, z_g=z, xi_g=xi, rho_bar=rho)
         states, controls = unpack_x(x, self._zshape)
@@ -226,6 +233,7 @@ class ADMMSolver:
         B, T, n, nx, n0, m = qp_data.dims
         dt, dev = qp_data.dtype, qp_data.device
         zs = self._zshape
+        x_zero = states0 is None and controls0 is None  # then G x = 0 needs no product
         if states0 is None:
             states0 = torch.zeros((B, T, zs.num_states), dtype=dt, device=dev)
         if controls0 is None:
@@ -233,6 +241,8 @@ class ADMMSolver:
         x0 = pack_x(states0.to(dt), controls0.to(dt)).contiguous()
         if m == 0:
             z0 = torch.zeros((B, T, 0), dtype=dt, device=dev)
+        elif x_zero:
+            z0 = torch.minimum(qp_data.ineq.l.to(dt).clamp(min=0.0), qp_data.ineq.u.to(dt))
         else:
             gx = (qp_data.ineq.G * x0.unsqueeze(-2)).sum(-1)
             z0 = torch.minimum(torch.maximum(gx, qp_data.ineq.l), qp_data.ineq.u)

@@ -75,7 +75,7 @@ def direct_workspace(qp: QPData) -> torch.Tensor:
 
 def admm_hip_solve(qp: QPData, state0, *, schur: str, cfg: _lib.AdmmCfg,
                    slack_weight: Optional[torch.Tensor] = None, want_pcg_iters: bool = False, sqp=None,
-                   workspace: Optional[torch.Tensor] = None):
+                   workspace: Optional[torch.Tensor] = None, donate: bool = False):
     """Run the fused ADMM on the device.  `state0` is an ADMMState of batched
     tensors; returns (state fields tuple, iters (B,), pcg_iters or None).
 
@@ -83,7 +83,11 @@ def admm_hip_solve(qp: QPData, state0, *, schur: str, cfg: _lib.AdmmCfg,
     (tmpc_sqp_admm_step_*, direct Schur solve only): the first-order check of
     state0 against qp, the activity test active & (conv > tol), and the solve of
     the problems that pass it; the call then also returns (conv, eq_err,
-    ineq_err, g, active_out)."""
+    ineq_err, g, active_out).
+
+    donate: the caller gives up state0: fields that already have the output's
+    shape, dtype and layout are updated in place instead of copied (the
+    library reads and writes the same buffers)."""
     if sqp is not None and schur != "direct":
         raise ValueError("an SQP step (sqp=...) needs the direct Schur solve")
     lib = _lib.load()
@@ -96,6 +100,9 @@ def admm_hip_solve(qp: QPData, state0, *, schur: str, cfg: _lib.AdmmCfg,
     cq, keep = qp_struct(qp, slack_weight)
 
     def prep(t, shape):
+        if donate and torch.is_tensor(t) and t.dtype == dt and t.device == dev and t.shape == shape \
+                and t.is_contiguous():
+            return t
         t = torch.as_tensor(t, dtype=dt, device=dev)
         return t.expand(shape).contiguous().clone() if t.shape != shape else t.contiguous().clone()
 

@@ -435,16 +435,16 @@ class TurboMPCSolver:
         admm = self._admm_solver_fwd
         B, dev, dt = states.shape[0], states.device, states.dtype
         qp = program.build_qp(states, controls)
+        own_state = admm_state0 is None  # the loop may update its own state in place
         if admm_state0 is None:
-            admm_state0 = admm.initial_state(qp, rho_bar=ap["rho"], states0=torch.zeros_like(states),
-                                             controls0=torch.zeros_like(controls))
+            admm_state0 = admm.initial_state(qp, rho_bar=ap["rho"])  # x = 0 (turbompc_solver.py:1545-1551)
         admm_state = admm_state0
         conv = torch.full((B,), float("inf"), dtype=dt, device=dev)
-        admm_iters = torch.zeros((B, max_iter), dtype=torch.int32, device=dev)
-        eq_v = torch.zeros((B, max_iter), dtype=dt, device=dev)
-        in_v = torch.zeros_like(eq_v)
-        conv_h = torch.zeros_like(eq_v)
-        num_iter = torch.zeros(B, dtype=torch.int32, device=dev)
+        # per-iteration records, iteration-major so that one iteration's entries
+        # are contiguous: [0] eq violation, [1] ineq violation, [2] convergence error
+        hist = torch.zeros((3, max_iter, B), dtype=dt, device=dev)
+        admm_iters = torch.zeros((max_iter, B), dtype=torch.int32, device=dev)
+        ran = torch.zeros((max_iter, B), dtype=torch.bool, device=dev)
         active = torch.ones(B, dtype=torch.bool, device=dev)
         g_c = None
         last = 0
@@ -457,22 +457,28 @@ class TurboMPCSolver:
             sw = qp.ineq.slack_penalization_weight
             if it == 0:  # cond_fun runs the first iteration unconditionally
                 (states, controls), stats, admm_state = admm.solve(qp, admm_state, rho_bar=ap["rho"], alpha=alpha,
-                                                                    slack_weight=sw, workspace=ws)
+                                                                    slack_weight=sw, workspace=ws,
+                                                                    donate_state=own_state)
             else:
+                # the state is the loop's own from here on: updated in place
                 (states, controls), stats, admm_state, (cv, e, i, g), act = admm.sqp_step(
                     qp, admm_state, active, tol, rho_bar=ap["rho"], alpha=alpha, slack_weight=sw, workspace=ws,
-                    warm_records=_same_static_blocks(qp, prev))
-                # the check belongs to the iterate committed at it - 1
-                conv = torch.where(active, cv, conv)
-                eq_v[:, it - 1] = torch.where(active, e, eq_v[:, it - 1])
-                in_v[:, it - 1] = torch.where(active, i, in_v[:, it - 1])
-                conv_h[:, it - 1] = torch.where(active, cv, conv_h[:, it - 1])
-                g_c = g if g_c is None else torch.where(active[:, None, None], g, g_c)
+                    warm_records=_same_static_blocks(qp, prev), donate_state=True)
+                # the check belongs to the iterate committed at it - 1 (the
+                # records of a stopped problem stay zero, as in the reference)
+                if it == 1:
+                    conv = cv
+                    hist[:, 0] = torch.stack([e, i, cv])
+                    g_c = g
+                else:
+                    conv = torch.where(active, cv, conv)
+                    hist[:, it - 1] = torch.where(active, torch.stack([e, i, cv]), hist[:, it - 1])
+                    g_c = torch.where(active[:, None, None], g, g_c)
                 active = act
                 if tol > 0 and not bool(active.any()):
                     break  # no problem iterated in this step
-            admm_iters[:, it] = stats.num_iter
-            num_iter = num_iter + active.to(torch.int32)
+            admm_iters[it] = stats.num_iter
+            ran[it] = active
             last = it
             prev = qp
             if it + 1 < max_iter:
@@ -480,14 +486,16 @@ class TurboMPCSolver:
         # the last committed iterate is not checked (the reference evaluates no
         # check after its final iteration): its record keeps the previous error
         # and G x at the QP it was solved on
-        conv_h[:, last] = torch.where(active, conv, conv_h[:, last])
+        hist[2, last] = torch.where(active, conv, hist[2, last])
         g_last = apply_G(qp, pack_x(states, controls))
         g_c = g_last if g_c is None else torch.where(active[:, None, None], g_last, g_c)
         kkt = self._build_kkt_state(states, controls, admm_state, g_c, qp.ineq.l, qp.ineq.u)
+        num_iter = ran.sum(dim=0, dtype=torch.int32)
+        admm_iters = admm_iters.t()
         return TurboMPCSolution(
             states=states, controls=controls, slack=admm_state.xi_g, status=self.STATUS_SUCCESS, num_iter=num_iter,
             convergence_error=conv, admm_iters=admm_iters, linesearch_alphas=None, admm_state=admm_state,
-            solver_stats=SolverStats(admm_iters, eq_v, in_v, conv_h), kkt_state=kkt,
+            solver_stats=SolverStats(admm_iters, hist[0].t(), hist[1].t(), hist[2].t()), kkt_state=kkt,
         )
 
     def _solve_impl_masked(self, program, states, controls, admm_state0: Optional[ADMMState] = None) -> TurboMPCSolution:
@@ -503,8 +511,7 @@ class TurboMPCSolver:
         B, dev, dt = states.shape[0], states.device, states.dtype
         qp = program.build_qp(states, controls)
         if admm_state0 is None:
-            admm_state0 = admm.initial_state(qp, rho_bar=ap["rho"], states0=torch.zeros_like(states),
-                                             controls0=torch.zeros_like(controls))
+            admm_state0 = admm.initial_state(qp, rho_bar=ap["rho"])  # x = 0 (turbompc_solver.py:1545-1551)
         admm_state = admm_state0
         slacks = admm_state0.xi_g
         # the SQP step is read only by the "step" criterion (and by a single
