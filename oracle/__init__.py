@@ -18,6 +18,7 @@ tests/test_oracle_*.py.
 """
 from .oracle import (  # noqa: F401
     OracleCfg,
+    OracleState,
     admm_solve,
     adjoint_kkt,
     blktri_solve,
