@@ -292,6 +292,62 @@ def test_admm_stream_kernel_structured_records_fp64_matches_oracle(P, shape):
     _assert_state_close(out, ref, 1e-9)
 
 
+# the wide form: n = 9 with more stacked rows than n (the obstacle workload's
+# 6 + 11 rows), up to 17 row lanes per problem; 11 rows exercise the rows past
+# the block that the column products read
+@pytest.mark.parametrize("P", [1, 2, 3])
+@pytest.mark.parametrize("shape", [(7, 13, 9, 6, 11), (10, 9, 9, 6, 5)])
+@pytest.mark.parametrize("variant", ["dense", "diag", "slack-diag"])
+def test_admm_stream_kernel_wide_rows_fp64_matches_oracle(P, shape, variant):
+    B, T, n, nx, m = shape
+    diag = variant.endswith("diag")
+    qp = random_qp(B, T, n, nx, m, seed=71, std=True, diag=diag)
+    kw = {"diag_cost": True} if diag else {}
+    if variant.startswith("slack"):
+        qp = soften(qp, 20.0, shrink=0.3)
+        kw["use_slack"] = True
+    cfg = oracle.OracleCfg(max_iter=20, check_every=3, adapt_rho_every=0, sigma=1e-6, eps_abs=1e-12,
+                           eps_rel=1e-12, rho_f_factor=1000.0, alpha=1.6)
+    ref, it_ref, _, out, stats = _run_pair(qp, cfg, torch.float64, kernel_flags=_lib.flag_stream_p(P), **kw)
+    np.testing.assert_array_equal(stats.num_iter.cpu().numpy(), it_ref)
+    _assert_state_close(out, ref, 1e-9)
+    if variant.startswith("slack"):
+        assert float(np.max(np.abs(ref.xi_g))) > 1e-6  # the soft rows are in play
+
+
+def test_admm_stream_kernel_wide_rows_adaptive_rho_and_termination():
+    qp = random_qp(11, 9, 9, 6, 11, seed=43, std=True, diag=True)
+    cfg = oracle.OracleCfg(max_iter=200, check_every=2, adapt_rho_every=4, sigma=1e-6, eps_abs=1e-6, eps_rel=1e-6,
+                           rho_f_factor=50.0, alpha=1.6, adaptive_rho_tolerance=1.5)
+    ref, it_ref, _, out, stats = _run_pair(qp, cfg, torch.float64, kernel_flags=_lib.flag_stream_p(3),
+                                           diag_cost=True)
+    np.testing.assert_array_equal(stats.num_iter.cpu().numpy(), it_ref)
+    assert len(set(it_ref.tolist())) > 1
+    assert rel_err(out.rho_bar, ref.rho_bar) < 1e-7
+    _assert_state_close(out, ref, 1e-5)
+
+
+def test_admm_stream_kernel_wide_rows_match_generic_on_config4_batch():
+    # config 4 at a batch that selects P = 2 with a partial last wavefront:
+    # the wide streaming kernel and the generic kernel run the same fp32 iteration
+    prob = configs.config4(B=4099, seed=2).to(DEV, torch.float32)
+    qp = prob.build_qp(*prob.initial_guess())
+    cfg = oracle.OracleCfg(max_iter=30, check_every=25, adapt_rho_every=0, sigma=1e-6, eps_abs=1e-9, eps_rel=1e-9,
+                           rho_f_factor=1000.0, alpha=1.0)
+    outs = []
+    for flags in (0, _lib.FLAG_GENERIC_KERNEL):
+        solver = _solver(qp, cfg, kernel_flags=flags, diag_cost=True)
+        st0 = solver.initial_state(qp, rho_bar=0.1)
+        _, stats, out = solver.solve(qp, st0)
+        outs.append((stats, out))
+    torch.cuda.synchronize()
+    (s_a, o_a), (s_b, o_b) = outs
+    assert torch.equal(s_a.num_iter, s_b.num_iter)
+    for k in ("x_blocks", "y_f_dyn", "y_g", "z_g", "y_f_0"):
+        assert rel_err(getattr(o_a, k), getattr(o_b, k)) < TOL[torch.float32], k
+    assert not torch.equal(o_a.x_blocks, o_b.x_blocks)  # two different kernels ran
+
+
 @pytest.mark.parametrize("alpha", [1.0, 1.6])
 def test_admm_stream_kernel_structured_records_adaptive_rho(alpha):
     # termination and rho adaptation read the residuals of the structured path

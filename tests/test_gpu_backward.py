@@ -147,14 +147,16 @@ def test_obstacle_lagrangian_hessian_matches_gradient_differences():
 def test_obstacle_gradients_match_finite_differences():
     # nonlinear inequality rows: the adjoint QP carries their Lagrangian Hessian
     prob = configs.config4(B=2, seed=7).to(DEV, torch.float64)
-    solver = TurboMPCSolver(prob, _tight_params(40, 4000, tol=1e-10, eps=1e-12))
+    # solves stopped at a first-order error of 1e-11, differences over h = 1e-4:
+    # the difference quotient's error (about tol / h) stays well below the bar
+    solver = TurboMPCSolver(prob, _tight_params(40, 4000, tol=1e-11, eps=1e-12))
     sol = solver.solve(solver.initial_guess())
     print(f"  SQP iterations {sol.num_iter.tolist()}, first-order error {sol.convergence_error.tolist()}", flush=True)
     assert float(sol.convergence_error.max()) < 1e-8
     # every problem has an active obstacle row, so the Hessian term is in play
     mb = prob.num_box_constraints
     assert bool((sol.admm_state.y_g[..., mb:].abs().flatten(1).amax(dim=1) > 1.0).all())
-    _check_gradients(solver, prob, n_checks=2, h=1e-5, rtol=1e-4, seed=3, floor=1.0, warm=True)
+    _check_gradients(solver, prob, n_checks=2, h=1e-4, rtol=1e-4, seed=3, floor=1.0, warm=True)
 
 
 def test_slack_weight_gradient_matches_finite_differences():

@@ -91,16 +91,22 @@ __host__ __device__ inline RecGeom rec_geom(const Dims& d, bool diag = false) {
 }
 
 // Compile-time caps of the streaming kernel (host checks, else the generic
-// kernel runs): nx <= n - 1, m <= kMaxStreamM, nx + m <= n (the stacked
-// constraint rows of a stage fit the problem's n lanes).
+// kernel runs): nx <= n - 1 and either m <= kMaxStreamM, nx + m <= n (the
+// stacked constraint rows of a stage fit the problem's n lanes), or, for
+// n = 9 (the obstacle workload's 6 states and 3 controls), the wide form:
+// m <= kWideMaxM, nx + m <= kWideRows row lanes per problem (NL > NC).
 constexpr int kMaxStreamM = 8;
+constexpr int kWideRows = 17;
+constexpr int kWideMaxM = 12;
 
-template <typename R, int NC, int P>
+// NL: lanes of a problem's group that own a stacked constraint row (NL >= NC);
+// MM: most inequality rows per stage.
+template <typename R, int NC, int P, int NL = NC, int MM = kMaxStreamM>
 struct StreamShape {
   static constexpr int W = Vec16<R>::W;
   static constexpr int PITCH = th_pitch(NC);
-  static constexpr int AMP_MAX = up4(NC * NC);
-  static constexpr int RVP_MAX = up4(4 * NC + 3 * kMaxStreamM);
+  static constexpr int AMP_MAX = up4(NL * NC);
+  static constexpr int RVP_MAX = up4(2 * NC + 2 * NL + 3 * MM);
   static constexpr int CH_TH = (P * PITCH / W + kWave - 1) / kWave;  // 16-byte chunks per lane
   static constexpr int CH_AM = (P * AMP_MAX / W + kWave - 1) / kWave;
   static constexpr int CH_RV = (P * RVP_MAX / W + kWave - 1) / kWave;
@@ -139,9 +145,11 @@ __host__ __device__ inline StreamLayout stream_layout(const Dims& d, int P, int 
   // at least two M slots: the backward sweep holds the blocks of stages t and t-1
   int end = L.am + (DPF > 2 ? DPF : 2) * P * g.amp;
   if (end < L.th + 12 * kWave) end = L.th + 12 * kWave;  // the residual reduction reuses the slots
-  // n x n zeros: column products read all NC rows of a block, so the rows past
+  // n x n zeros: column products read all NL rows of a block, so the rows past
   // the last stacked block land here (rows past other blocks land on the
-  // next block's data); every such row meets a zero vector entry
+  // next block's data); every such row meets a zero vector entry.  NL rows
+  // overshoot a block of nx + m rows by (NL - nx - m) n < n n entries (NL = n,
+  // or the wide form's kWideRows with nx + m > n)
   L.a0 = up4(end + d.n * d.n);
   L.vec = up4(L.a0 + P * d.n0 * d.n);
   L.spill = L.vec + kNV * vec_stride(P);
@@ -472,12 +480,12 @@ struct StreamOcc {
   static constexpr int waves = sizeof(R) == 4 ? 2 : 1;
 };
 
-template <typename R, int NC, int P, int DPF>
+template <typename R, int NC, int P, int DPF, int NL = NC, int MM = kMaxStreamM>
 __global__ __launch_bounds__(kWave, StreamOcc<R>::waves) void admm_stream_kernel(StreamArgs<R> a) {
+  static_assert(NL >= NC && NL <= kWave / P, "row lanes must fit a problem's group");
   using V = typename Vec16<R>::T;
-  using K = StreamShape<R, NC, P>;
+  using K = StreamShape<R, NC, P, NL, MM>;
   constexpr int n = NC, PITCH = K::PITCH, W = K::W;
-  constexpr int NL = NC;  // lanes of a problem's group that own a row
   constexpr int CH_TH = K::CH_TH, CH_AM = K::CH_AM, CH_RV = K::CH_RV;
   extern __shared__ __align__(16) unsigned char smem_raw[];
   R* lds = reinterpret_cast<R*>(smem_raw);
@@ -487,7 +495,9 @@ __global__ __launch_bounds__(kWave, StreamOcc<R>::waves) void admm_stream_kernel
   const RecGeom rg = rec_geom(d, diagD);
   const int amp = rg.amp, rvp = rg.rvp, dmp = rg.dmp;
   const StreamLayout L = stream_layout(d, P, DPF, diagD);
-  const Group G = make_group_strided(n, P, B);
+  // lanes 0..NL-1 of a group are live: the first n hold the n-vectors, the
+  // first nx + m the stacked constraint rows
+  const Group G = make_group_strided(NL, P, B);
   const int b = G.prob, i = G.lane, p = G.gid, base = p * (kWave / P), tid = threadIdx.x;
   const int b0 = blockIdx.x * P;
   const int nprob = min(P, B - b0);
@@ -922,22 +932,23 @@ __global__ __launch_bounds__(kWave, StreamOcc<R>::waves) void admm_stream_kernel
       R* red = lds + L.th;
       const R vals[11] = {rp, nCx, nc, nGx, nz, rd, nPx, nAty, nq, nxi, nyg};
 #pragma unroll
-      for (int k = 0; k < 11; ++k) red[k * kWave + tid] = (i < n) ? vals[k] : R(0);
+      for (int k = 0; k < 11; ++k) red[k * kWave + tid] = (i < NL) ? vals[k] : R(0);
       wsync();
-      // lane i of each group reduces values k = i, i + n, ... over the group's lanes
-      R mx[(11 + NC - 1) / NC];
+      // lane i of each group reduces values k = i, i + NL, ... over the group's
+      // NL lanes (lanes past NL that land on k < 11 repeat a value of lane k - NL)
+      R mx[(11 + NL - 1) / NL];
 #pragma unroll
-      for (int q = 0; q < (11 + NC - 1) / NC; ++q) {
-        const int k = i + q * NC;
+      for (int q = 0; q < (11 + NL - 1) / NL; ++q) {
+        const int k = i + q * NL;
         mx[q] = R(0);
         if (k < 11)
 #pragma unroll
-          for (int l = 0; l < NC; ++l) mx[q] = rmax(mx[q], red[k * kWave + base + l]);
+          for (int l = 0; l < NL; ++l) mx[q] = rmax(mx[q], red[k * kWave + base + l]);
       }
       wsync();
 #pragma unroll
-      for (int q = 0; q < (11 + NC - 1) / NC; ++q)
-        if (i + q * NC < 11) red[(i + q * NC) * kWave + base] = mx[q];
+      for (int q = 0; q < (11 + NL - 1) / NL; ++q)
+        if (i + q * NL < 11) red[(i + q * NL) * kWave + base] = mx[q];
       wsync();
       R r[11];
 #pragma unroll
@@ -1017,14 +1028,14 @@ __host__ __device__ inline FactorLayout factor_layout(const Dims& d, int P, bool
   return L;
 }
 
-template <typename R, int NC, int P>
+template <typename R, int NC, int P, int NL = NC, int MM = kMaxStreamM>
 __global__ __launch_bounds__(kWave, 2) void factor_std_kernel(Dims d, const R* __restrict__ am, const R* __restrict__ dm, const R* __restrict__ A0,
                                                           const R* __restrict__ rho, R sigma, R rho_f_factor,
                                                           int32_t* __restrict__ ctl, R* __restrict__ thinv,
                                                           int diag) {
   using C = double;
   using V = typename Vec16<R>::T;
-  using K = StreamShape<R, NC, P>;
+  using K = StreamShape<R, NC, P, NL, MM>;  // stage-run chunk counts
   constexpr int n = NC, PITCH = K::PITCH, W = K::W;
   constexpr int CH_TH = K::CH_TH, CH_AM = K::CH_AM;
   extern __shared__ __align__(16) unsigned char smem_raw[];

@@ -171,8 +171,9 @@ void launch_chunk(hipStream_t s, const AdmmArgs<R>& a) {
 }
 
 // Streaming kernel (explicit-integrator structure, n in {6, 9, 16, 17},
-// nx <= n - 1, m <= min(n, 8)).  P problems per wavefront: as many as keep
-// about two wavefronts per SIMD busy on a 256-CU device, at most 3.
+// nx <= n - 1, and nx + m <= n with m <= 8, or for n = 9 the wide form with
+// nx + m <= 17 and m <= 12).  P problems per wavefront: as many as keep about
+// two wavefronts per SIMD busy on a 256-CU device, at most 3.
 constexpr int kStreamDepth = 1;
 constexpr size_t kMaxLds = 160 * 1024;
 
@@ -189,10 +190,19 @@ inline int factor_problems_per_wave(int B, uint32_t flags) {
   return forced ? forced : std::max(1, std::min(3, B / 1024));
 }
 
+// The stacked constraint rows of a stage exceed n lanes: the wide form of the
+// streaming kernels (n = 9, kWideRows row lanes per problem).
+inline bool stream_wide(const Dims& d) { return d.nx + d.m > d.n; }
+
 template <typename R>
 bool stream_ok(const Dims& d, int P, bool diag) {
   if (!(d.n == 6 || d.n == 9 || d.n == 16 || d.n == 17)) return false;
-  if (d.nx > d.n - 1 || d.nx + d.m > d.n || d.m > kMaxStreamM) return false;
+  if (d.nx > d.n - 1) return false;
+  if (stream_wide(d)) {
+    if (d.n != 9 || d.nx + d.m > kWideRows || d.m > kWideMaxM || P > kWave / kWideRows) return false;
+  } else if (d.m > kMaxStreamM) {
+    return false;
+  }
   const StreamLayout L = stream_layout(d, P, kStreamDepth, diag);
   // stage-run offsets are 32-bit element offsets
   const RecGeom g = rec_geom(d, diag);
@@ -201,21 +211,21 @@ bool stream_ok(const Dims& d, int P, bool diag) {
   return (size_t)L.total * sizeof(R) <= kMaxLds;
 }
 
-template <typename R, int NC, int P>
+template <typename R, int NC, int P, int NL = NC, int MM = kMaxStreamM>
 void launch_stream_p(hipStream_t s, const StreamArgs<R>& a) {
   const StreamLayout L = stream_layout(a.d, P, kStreamDepth, a.diag != 0);
   const size_t smem = (size_t)L.total * sizeof(R);
-  lds_optin(admm_stream_kernel<R, NC, P, kStreamDepth>, smem);
+  lds_optin(admm_stream_kernel<R, NC, P, kStreamDepth, NL, MM>, smem);
   const int grid = (a.d.B + P - 1) / P;
-  hipLaunchKernelGGL((admm_stream_kernel<R, NC, P, kStreamDepth>), dim3(grid), dim3(kWave), smem, s, a);
+  hipLaunchKernelGGL((admm_stream_kernel<R, NC, P, kStreamDepth, NL, MM>), dim3(grid), dim3(kWave), smem, s, a);
 }
 
-template <typename R, int NC>
+template <typename R, int NC, int NL = NC, int MM = kMaxStreamM>
 void launch_stream_nc(hipStream_t s, const StreamArgs<R>& a, int P) {
   switch (P) {
-    case 1: launch_stream_p<R, NC, 1>(s, a); break;
-    case 2: launch_stream_p<R, NC, 2>(s, a); break;
-    default: launch_stream_p<R, NC, 3>(s, a); break;
+    case 1: launch_stream_p<R, NC, 1, NL, MM>(s, a); break;
+    case 2: launch_stream_p<R, NC, 2, NL, MM>(s, a); break;
+    default: launch_stream_p<R, NC, 3, NL, MM>(s, a); break;
   }
 }
 
@@ -223,29 +233,34 @@ template <typename R>
 void launch_stream(hipStream_t s, const StreamArgs<R>& a, int P) {
   switch (a.d.n) {
     case 6: launch_stream_nc<R, 6>(s, a, P); break;
-    case 9: launch_stream_nc<R, 9>(s, a, P); break;
+    case 9:
+      if (stream_wide(a.d))
+        launch_stream_nc<R, 9, kWideRows, kWideMaxM>(s, a, P);
+      else
+        launch_stream_nc<R, 9>(s, a, P);
+      break;
     case 16: launch_stream_nc<R, 16>(s, a, P); break;
     default: launch_stream_nc<R, 17>(s, a, P); break;
   }
 }
 
-template <typename R, int NC, int P>
+template <typename R, int NC, int P, int NL = NC, int MM = kMaxStreamM>
 void launch_factor_std_p(hipStream_t s, const Dims& d, const DirectWs<R>& w, const QPDev<R>& q, const R* rho,
                          R sigma, R rho_f_factor, int32_t* ctl, bool diag) {
   const size_t smem = factor_layout<R>(d, P, diag).bytes;
-  lds_optin(factor_std_kernel<R, NC, P>, smem);
+  lds_optin(factor_std_kernel<R, NC, P, NL, MM>, smem);
   const int grid = (d.B + P - 1) / P;
-  hipLaunchKernelGGL((factor_std_kernel<R, NC, P>), dim3(grid), dim3(kWave), smem, s, d, (const R*)w.am,
+  hipLaunchKernelGGL((factor_std_kernel<R, NC, P, NL, MM>), dim3(grid), dim3(kWave), smem, s, d, (const R*)w.am,
                      (const R*)w.dm, q.A0, rho, sigma, rho_f_factor, ctl, w.thinv, diag ? 1 : 0);
 }
 
-template <typename R, int NC>
+template <typename R, int NC, int NL = NC, int MM = kMaxStreamM>
 void launch_factor_std_nc(hipStream_t s, const Dims& d, const DirectWs<R>& w, const QPDev<R>& q, const R* rho,
                           R sigma, R rho_f_factor, int32_t* ctl, int P, bool diag) {
   switch (P) {
-    case 1: launch_factor_std_p<R, NC, 1>(s, d, w, q, rho, sigma, rho_f_factor, ctl, diag); break;
-    case 2: launch_factor_std_p<R, NC, 2>(s, d, w, q, rho, sigma, rho_f_factor, ctl, diag); break;
-    default: launch_factor_std_p<R, NC, 3>(s, d, w, q, rho, sigma, rho_f_factor, ctl, diag); break;
+    case 1: launch_factor_std_p<R, NC, 1, NL, MM>(s, d, w, q, rho, sigma, rho_f_factor, ctl, diag); break;
+    case 2: launch_factor_std_p<R, NC, 2, NL, MM>(s, d, w, q, rho, sigma, rho_f_factor, ctl, diag); break;
+    default: launch_factor_std_p<R, NC, 3, NL, MM>(s, d, w, q, rho, sigma, rho_f_factor, ctl, diag); break;
   }
 }
 
@@ -255,7 +270,12 @@ int launch_factor_std(hipStream_t s, const Dims& d, const DirectWs<R>& w, const 
                       R sigma, R rho_f_factor, int32_t* ctl, int P, bool diag) {
   switch (d.n) {
     case 6: launch_factor_std_nc<R, 6>(s, d, w, q, rho, sigma, rho_f_factor, ctl, P, diag); break;
-    case 9: launch_factor_std_nc<R, 9>(s, d, w, q, rho, sigma, rho_f_factor, ctl, P, diag); break;
+    case 9:
+      if (stream_wide(d))
+        launch_factor_std_nc<R, 9, kWideRows, kWideMaxM>(s, d, w, q, rho, sigma, rho_f_factor, ctl, P, diag);
+      else
+        launch_factor_std_nc<R, 9>(s, d, w, q, rho, sigma, rho_f_factor, ctl, P, diag);
+      break;
     case 16: launch_factor_std_nc<R, 16>(s, d, w, q, rho, sigma, rho_f_factor, ctl, P, diag); break;
     default: launch_factor_std_nc<R, 17>(s, d, w, q, rho, sigma, rho_f_factor, ctl, P, diag); break;
   }
