@@ -53,8 +53,8 @@ typedef struct tmpc_state {
  * reading A_plus and E. */
 #define TMPC_FLAG_STD_DYNAMICS 1u
 /* With TMPC_FLAG_STD_DYNAMICS the direct solve streams stage records through
- * a batched kernel when the shape allows it (n in {6, 9, 16, 17}, nx < n,
- * m <= min(n, 8)).  TMPC_FLAG_GENERIC_KERNEL selects the generic per-stage
+ * a batched kernel when the shape allows it (n in {6, 9, 16, 17}, nx < n, and
+ * nx + m <= n with m <= 8, or n = 9 with nx + m <= 17 and m <= 12).  TMPC_FLAG_GENERIC_KERNEL selects the generic per-stage
  * kernel instead (same iteration; for cross-checks).  Bits 8-9 force the
  * number of problems per wavefront of the streaming kernel (1-3; 0 = chosen
  * from B). */
@@ -74,6 +74,11 @@ typedef struct tmpc_state {
  * the A_minus and c records are rewritten.  Vouched for by the caller; the
  * other paths ignore it. */
 #define TMPC_FLAG_WARM_RECORDS 8u
+/* With TMPC_FLAG_WARM_RECORDS: the QP also differs from the previous call's in
+ * G, l and u (inequality rows relinearized at the new iterate, as the obstacle
+ * rows are), whose records are rewritten too; D, E, q, A0, c0 and the slack
+ * weight are still unchanged. */
+#define TMPC_FLAG_WARM_INEQ 16u
 
 typedef struct tmpc_admm_cfg {
   int32_t max_iter, check_every, adapt_rho_every, pcg_max_iter, use_slack;

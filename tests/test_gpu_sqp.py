@@ -209,23 +209,37 @@ def test_sqp_step_check_and_activity(kernel, use_slack, dtype):
         np.testing.assert_array_equal(a[on], p[on])
 
 
-def test_sqp_warm_records_match_repacking():
-    """FLAG_WARM_RECORDS: an SQP solve whose steps rewrite only the A_minus and
-    c records gives the same iterates, bit for bit, as one that repacks every
-    record at every step."""
+@pytest.mark.parametrize("case", ["quadrotor", "config4", "config4-slack"])
+def test_sqp_warm_records_match_repacking(case):
+    """FLAG_WARM_RECORDS: an SQP solve whose steps rewrite only the records
+    that changed (A_minus and c for the quadrotor; with FLAG_WARM_INEQ also the
+    obstacle rows' G, l, u for config 4) gives the same iterates, bit for bit,
+    as one that repacks every record at every step."""
     import turbompc_amd.solvers.turbompc_solver as ts
+    from turbompc_amd.problems import configs
 
     B = 24
-    prob = make_quadrotor_config(B=B, seed=6, dtype=torch.float32, device="cuda")
-    solver = TurboMPCSolver(prob, _params(4, 12))
-    warm = solver.solve(solver.initial_guess())
-    orig = ts._same_static_blocks
+    if case == "quadrotor":
+        prob, level, n_sqp, iters = make_quadrotor_config(B=B, seed=6, dtype=torch.float32, device="cuda"), \
+            "dynamics", 4, 12
+    else:
+        prob = configs.config4(B=B, seed=6, use_slack_variables=case.endswith("slack"),
+                               slack_penalization_weight=50.0).to("cuda", torch.float32)
+        level, n_sqp, iters = "constraints", 5, 15
+    solver = TurboMPCSolver(prob, _params(n_sqp, iters))
+    seen = []
+    orig = ts._warm_level
     try:
-        ts._same_static_blocks = lambda qp, prev: False
+        ts._warm_level = lambda qp, prev: seen.append(orig(qp, prev)) or seen[-1]
+        warm = solver.solve(solver.initial_guess())
+        ts._warm_level = lambda qp, prev: None
         cold = solver.solve(solver.initial_guess())
     finally:
-        ts._same_static_blocks = orig
+        ts._warm_level = orig
     torch.cuda.synchronize()
+    assert seen and all(v == level for v in seen), seen
     assert torch.equal(warm.states, cold.states) and torch.equal(warm.controls, cold.controls)
     assert torch.equal(warm.admm_state.y_f_dyn, cold.admm_state.y_f_dyn)
+    assert torch.equal(warm.admm_state.y_g, cold.admm_state.y_g)
+    assert torch.equal(warm.slack, cold.slack)
     assert torch.equal(warm.convergence_error, cold.convergence_error)

@@ -27,6 +27,7 @@ FLAG_STD_DYNAMICS = 1
 FLAG_GENERIC_KERNEL = 2
 FLAG_DIAG_COST = 4  # every D_t diagonal
 FLAG_WARM_RECORDS = 8  # the workspace's stage records are the previous SQP step's
+FLAG_WARM_INEQ = 16  # with FLAG_WARM_RECORDS: G, l, u changed too
 
 
 def flag_stream_p(p: int) -> int:

@@ -256,20 +256,40 @@ __global__ __launch_bounds__(kWave) void stage_pack_kernel(Dims d, QPDev<R> qp, 
 // thread keeps several independent copies in flight.
 constexpr int kRepackProblems = 8;
 
-template <typename R>
+//
+// With INEQ the G rows of the M records and the l, u entries of the rv
+// records are rewritten as well, at every stage t < T (the grid's y extent;
+// N without INEQ).
+template <typename R, bool INEQ>
 __global__ __launch_bounds__(256) void stage_repack_dynamics_kernel(Dims d, const R* __restrict__ Am,
-                                                                    const R* __restrict__ c, R* __restrict__ am,
+                                                                    const R* __restrict__ c,
+                                                                    const R* __restrict__ G,
+                                                                    const R* __restrict__ l,
+                                                                    const R* __restrict__ u, R* __restrict__ am,
                                                                     R* __restrict__ rv, int diag) {
   const int t = blockIdx.y, b0 = blockIdx.x * kRepackProblems;
   const RecGeom g = rec_geom(d, diag != 0);
-  const int na = d.nx * d.n, per = na + d.nx;
+  const int n = d.n, nx = d.nx, m = d.m;
+  // per stage: [A_minus (nx n) | c (nx)] for t < N, then [G (m n) | l (m) | u (m)]
+  const bool dyn = !INEQ || t < d.N;
+  const int na = dyn ? nx * n : 0, nd = dyn ? na + nx : 0;
+  const int ng = INEQ ? m * n : 0, per = nd + (INEQ ? ng + 2 * m : 0);
   for (int k = threadIdx.x; k < per; k += blockDim.x) {
     R v[kRepackProblems];
 #pragma unroll
     for (int j = 0; j < kRepackProblems; ++j) {
       const int b = min(b0 + j, d.B - 1);
-      const size_t bt = (size_t)b * d.N + t;
-      v[j] = k < na ? Am[bt * na + k] : c[bt * d.nx + (k - na)];
+      const size_t bn = (size_t)b * d.N + t, bt = (size_t)b * d.T + t;
+      if (k < na)
+        v[j] = Am[bn * na + k];
+      else if (k < nd)
+        v[j] = c[bn * nx + (k - na)];
+      else if (k < nd + ng)
+        v[j] = G[bt * ng + (k - nd)];
+      else if (k < nd + ng + m)
+        v[j] = l[bt * m + (k - nd - ng)];
+      else
+        v[j] = u[bt * m + (k - nd - ng - m)];
     }
 #pragma unroll
     for (int j = 0; j < kRepackProblems; ++j) {
@@ -277,8 +297,14 @@ __global__ __launch_bounds__(256) void stage_repack_dynamics_kernel(Dims d, cons
       const size_t rec = (size_t)t * d.B + b0 + j;
       if (k < na)
         am[rec * g.amp + k] = v[j];
-      else
+      else if (k < nd)
         rv[rec * g.rvp + g.c + (k - na)] = v[j];
+      else if (k < nd + ng)
+        am[rec * g.amp + nx * n + (k - nd)] = v[j];  // G rows follow the A_minus rows
+      else if (k < nd + ng + m)
+        rv[rec * g.rvp + g.l + (k - nd - ng)] = v[j];
+      else
+        rv[rec * g.rvp + g.u + (k - nd - ng - m)] = v[j];
     }
   }
 }

@@ -405,9 +405,13 @@ int admm_direct_impl(hipStream_t s, const tmpc_dims* dims, const tmpc_qp* qp,
     a.act = sq->active_out;
   }
   if (stream && (cfg->flags & TMPC_FLAG_WARM_RECORDS)) {
-    hipLaunchKernelGGL((stage_repack_dynamics_kernel<R>),
-                       dim3((unsigned)((d.B + kRepackProblems - 1) / kRepackProblems), (unsigned)d.N), dim3(256), 0, s,
-                       d, a.qp.Am, a.qp.c, w.am, w.rv, diag ? 1 : 0);
+    const unsigned gx = (unsigned)((d.B + kRepackProblems - 1) / kRepackProblems);
+    if ((cfg->flags & TMPC_FLAG_WARM_INEQ) != 0 && d.m > 0)
+      hipLaunchKernelGGL((stage_repack_dynamics_kernel<R, true>), dim3(gx, (unsigned)d.T), dim3(256), 0, s, d,
+                         a.qp.Am, a.qp.c, a.qp.G, a.qp.l, a.qp.u, w.am, w.rv, diag ? 1 : 0);
+    else
+      hipLaunchKernelGGL((stage_repack_dynamics_kernel<R, false>), dim3(gx, (unsigned)d.N), dim3(256), 0, s, d,
+                         a.qp.Am, a.qp.c, a.qp.G, a.qp.l, a.qp.u, w.am, w.rv, diag ? 1 : 0);
     st = launch_status();
     if (st) return st;
     st = launch_factor_std<R>(s, d, w, a.qp, a.st.rho, a.sigma, a.rho_f_factor, nullptr, fp, diag);

@@ -193,14 +193,15 @@ class ADMMSolver:
     def sqp_step(self, qp_data: QPData, admm_state0: ADMMState, active: torch.Tensor, tol: float,
                  rho_bar: float = 1.0, alpha: float = 1.0, *, slack_weight=0.0,
                  workspace: Optional[torch.Tensor] = None, warm_records: bool = False,
-                 donate_state: bool = False):
+                 warm_ineq: bool = False, donate_state: bool = False):
         """One device SQP step (tmpc_sqp_admm_step_*): the first-order check of
         admm_state0's iterate against qp_data, the activity test
         active & (conv > tol), and the solve of the problems that pass it (the
         others keep their state and report 0 iterations).  warm_records: the
         caller vouches that `workspace` holds the records of the previous call
         on it, whose output is admm_state0, and that qp_data differs from that
-        call's QP only in A_minus and c (FLAG_WARM_RECORDS).  donate_state:
+        call's QP only in A_minus and c (FLAG_WARM_RECORDS); with warm_ineq
+        also in G, l and u (FLAG_WARM_INEQ).  donate_state:
         admm_state0's buffers may be updated in place.  Returns
         ((states, controls), stats, state, (conv, eq_err, ineq_err, g), active_out)."""
         if self._admm_backend != AdmmBackend.HIP_DIRECT:
@@ -211,6 +212,8 @@ class ADMMSolver:
         flags = (_lib.FLAG_STD_DYNAMICS if std else 0) | self._kernel_flags
         if warm_records:
             flags |= _lib.FLAG_WARM_RECORDS
+            if warm_ineq:
+                flags |= _lib.FLAG_WARM_INEQ
         cfg = self._cfg(alpha, flags)
         sw = slack_weight if self._use_slack else None
         outs, iters, _, (conv, eq, iq, g, act) = hip.admm_hip_solve(

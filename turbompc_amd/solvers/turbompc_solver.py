@@ -461,9 +461,10 @@ class TurboMPCSolver:
                                                                     donate_state=own_state)
             else:
                 # the state is the loop's own from here on: updated in place
+                warm = _warm_level(qp, prev)
                 (states, controls), stats, admm_state, (cv, e, i, g), act = admm.sqp_step(
                     qp, admm_state, active, tol, rho_bar=ap["rho"], alpha=alpha, slack_weight=sw, workspace=ws,
-                    warm_records=_same_static_blocks(qp, prev), donate_state=True)
+                    warm_records=warm is not None, warm_ineq=warm == "constraints", donate_state=True)
                 # the check belongs to the iterate committed at it - 1 (the
                 # records of a stopped problem stay zero, as in the reference)
                 if it == 1:
@@ -653,18 +654,29 @@ class DifferentiableSolve:
         return sol._replace(states=states, controls=controls)
 
 
-def _same_static_blocks(qp: QPData, prev: Optional[QPData]) -> bool:
-    """Whether qp differs from prev at most in A_minus and c: the blocks that
-    do not depend on the linearization point are the same tensors (the OCP
-    classes build them once per problem) and the slack weight is unchanged."""
+def _warm_level(qp: QPData, prev: Optional[QPData]) -> Optional[str]:
+    """How qp differs from prev, for the warm stage records of an SQP step:
+    "dynamics" (at most in A_minus and c), "constraints" (also in G, l, u) or
+    None (in other blocks too).  The blocks that do not depend on the
+    linearization point are the same tensors (the OCP classes build them once
+    per problem) and the slack weight is unchanged."""
     if prev is None:
-        return False
+        return None
     same = lambda a, b: a is b  # noqa: E731
-    return (same(qp.cost.D, prev.cost.D) and same(qp.cost.E, prev.cost.E) and same(qp.cost.q, prev.cost.q)
-            and same(qp.eq.A0, prev.eq.A0) and same(qp.eq.c0, prev.eq.c0) and same(qp.eq.A_plus, prev.eq.A_plus)
-            and same(qp.ineq.G, prev.ineq.G) and same(qp.ineq.l, prev.ineq.l) and same(qp.ineq.u, prev.ineq.u)
-            and qp.ineq.use_slack_variables == prev.ineq.use_slack_variables
-            and float(qp.ineq.slack_penalization_weight) == float(prev.ineq.slack_penalization_weight))
+    fixed = (same(qp.cost.D, prev.cost.D) and same(qp.cost.E, prev.cost.E) and same(qp.cost.q, prev.cost.q)
+             and same(qp.eq.A0, prev.eq.A0) and same(qp.eq.c0, prev.eq.c0) and same(qp.eq.A_plus, prev.eq.A_plus)
+             and qp.ineq.use_slack_variables == prev.ineq.use_slack_variables
+             and float(qp.ineq.slack_penalization_weight) == float(prev.ineq.slack_penalization_weight))
+    if not fixed:
+        return None
+    if same(qp.ineq.G, prev.ineq.G) and same(qp.ineq.l, prev.ineq.l) and same(qp.ineq.u, prev.ineq.u):
+        return "dynamics"
+    return "constraints"
+
+
+def _same_static_blocks(qp: QPData, prev: Optional[QPData]) -> bool:
+    """Whether qp differs from prev at most in A_minus and c."""
+    return _warm_level(qp, prev) == "dynamics"
 
 
 def _select_qp(mask: torch.Tensor, a: QPData, b: QPData) -> QPData:
