@@ -348,6 +348,26 @@ def test_admm_stream_kernel_wide_rows_match_generic_on_config4_batch():
     assert not torch.equal(o_a.x_blocks, o_b.x_blocks)  # two different kernels ran
 
 
+@pytest.mark.parametrize("seed", [0, 3])
+def test_admm_config5_first_rho_update_matches_oracle(seed):
+    # config 5 (dt = 10, rho_f / sigma = 1e8 at the start): the dual residual
+    # is a cancellation of terms ~1e2 down to ~1e-6, so the first adaptive rho
+    # update (iteration 25) follows the factorization's accuracy; a closed-form
+    # 2x2 block inverse in the Gauss-Jordan steps moved it by 40%
+    prob = configs.config5(B=2, seed=seed)
+    qp = prob.build_qp(*prob.initial_guess())
+    cfg = oracle.OracleCfg(max_iter=26, check_every=25, adapt_rho_every=25, sigma=1e-6, eps_abs=1e-13, eps_rel=1e-13,
+                           rho_f_factor=1000.0, alpha=1.6, adaptive_rho_tolerance=5.0)
+    ref, it_ref, _, out, stats = _run_pair(qp, cfg, torch.float64, diag_cost=True)
+    np.testing.assert_array_equal(stats.num_iter.cpu().numpy(), it_ref)
+    assert np.all(ref.rho_bar > 100.0)  # the update fired
+    # rho is a ratio of cancelled residuals: ~1e-5 apart between two summation orders
+    assert rel_err(out.rho_bar, ref.rho_bar) < 1e-4
+    for k in FIELDS[:-1]:  # the state after one iteration at the new rho
+        if np.asarray(getattr(ref, k)).size:
+            assert rel_err(getattr(out, k), getattr(ref, k)) < 1e-5, k
+
+
 @pytest.mark.parametrize("alpha", [1.0, 1.6])
 def test_admm_stream_kernel_structured_records_adaptive_rho(alpha):
     # termination and rho adaptation read the residuals of the structured path

@@ -1190,15 +1190,15 @@ __global__ __launch_bounds__(kWave, 2) void factor_std_kernel(Dims d, const R* _
         }
       }
     }
-    // Gauss-Jordan inversion without pivoting, rows in lanes, in 2x2 pivot
-    // blocks (half the pivot-row round trips; the pivot blocks of an SPD
-    // matrix are SPD).  For a block K = {k, k+1} with inverse Q of its 2x2
-    // pivot block, row i outside K takes a_i -= G_i [row_k; row_k+1] with
-    // G_i = (a_ik, a_ik+1) Q and a_iK = -G_i; the rows of K become Q times the
-    // pair.  Both are written as a_i -= g0 row_k + g1 row_k+1 with per-lane
-    // (g0, g1), so every lane runs the same instructions.  An odd n ends with
-    // a single step whose pivot row is normalized after the step (as in the
-    // 2x2 case, no divergent pivot-row branch).
+    // Gauss-Jordan inversion without pivoting, rows in lanes (the pivots of an
+    // SPD matrix stay positive), two pivots per LDS round trip: rows k and k+1
+    // are broadcast together and every lane replays the two single-pivot steps
+    // itself, forming row k+1 after step k from the pair, so the arithmetic is
+    // that of one pivot at a time (a closed-form 2x2 block inverse instead
+    // loses digits on strongly coupled pivot pairs).  The pivot row of a step
+    // is not normalized at its step: its lane keeps the pivot as a scale
+    // (myip) and normalizes after the last step, so every lane runs the same
+    // instructions.
     C myip = C(1);
 #pragma unroll
     for (int k = 0; k < NC; k += 2) {
@@ -1217,29 +1217,23 @@ __global__ __launch_bounds__(kWave, 2) void factor_std_kernel(Dims d, const R* _
         }
         __builtin_amdgcn_sched_barrier(0);
         const bool m0 = i == k, m1 = pair && i == k + 1;
+        // step k
+        const C ip = C(1) / p1[k];
+        myip = m0 ? ip : myip;
+        const C g = m0 ? C(0) : a[k] * ip;
+#pragma unroll
+        for (int j = 0; j < NC; ++j) a[j] = (j == k) ? (m0 ? C(1) : -g) : a[j] - g * p1[j];
         if (pair) {
-          const C q00 = p1[k], q01 = p1[k + 1], q10 = p2[k], q11 = p2[k + 1];
-          const C idet = C(1) / (q00 * q11 - q01 * q10);
-          const C Q00 = q11 * idet, Q01 = -q01 * idet, Q10 = -q10 * idet, Q11 = q00 * idet;
-          const C f0 = a[k], f1 = a[k + 1];
-          C g0 = f0 * Q00 + f1 * Q10, g1 = f0 * Q01 + f1 * Q11;
-          g0 = m0 ? C(1) - Q00 : (m1 ? -Q10 : g0);
-          g1 = m0 ? -Q01 : (m1 ? C(1) - Q11 : g1);
+          // row k+1 after step k (what lane k+1 now holds), in place of p2
+          const C gq = p2[k] * ip;
 #pragma unroll
-          for (int j = 0; j < NC; ++j) {
-            if (j == k)
-              a[j] = m0 ? Q00 : (m1 ? Q10 : -g0);
-            else if (j == k + 1)
-              a[j] = m0 ? Q01 : (m1 ? Q11 : -g1);
-            else
-              a[j] = a[j] - g0 * p1[j] - g1 * p2[j];
-          }
-        } else {
-          const C ip = C(1) / p1[k];
-          myip = m0 ? ip : myip;
-          const C g = m0 ? C(0) : a[k] * ip;
+          for (int j = 0; j < NC; ++j) p2[j] = (j == k) ? -gq : p2[j] - gq * p1[j];
+          // step k+1
+          const C ip2 = C(1) / p2[k + 1];
+          myip = m1 ? ip2 : myip;
+          const C g2 = m1 ? C(0) : a[k + 1] * ip2;
 #pragma unroll
-          for (int j = 0; j < NC; ++j) a[j] = (j == k) ? (m0 ? C(1) : -g) : a[j] - g * p1[j];
+          for (int j = 0; j < NC; ++j) a[j] = (j == k + 1) ? (m1 ? C(1) : -g2) : a[j] - g2 * p2[j];
         }
       }
     }
