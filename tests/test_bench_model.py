@@ -1,0 +1,33 @@
+"""bench.py on the CPU: the algorithmic-bytes model behind roofline.achieved
+reproduces the per-problem figures it is quoted from (F = factorization, I =
+one ADMM iteration: config 3 195.6 / 122.4 KiB, config 4 97.8 / 86.0 KiB, fp32),
+and a multi-GPU request exits with a message before touching a device."""
+import subprocess
+import sys
+from pathlib import Path
+
+import pytest
+
+ROOT = Path(__file__).resolve().parent.parent
+sys.path.insert(0, str(ROOT))
+
+import bench  # noqa: E402
+
+
+@pytest.mark.parametrize("args, F_kib, I_kib", [
+    ((41, 17, 13, 13, 4, 20, 4), 195.6, 122.4),          # config 3: box rows only
+    ((61, 9, 6, 6, 11, 30, 4, 8), 97.8, 86.0),           # config 4: 8 data-carrying obstacle rows
+])
+def test_bytes_model_matches_quoted_figures(args, F_kib, I_kib):
+    per_qp, F, I = bench.bytes_per_qp(*args)
+    assert round(F / 1024, 1) == F_kib
+    assert round(I / 1024, 1) == I_kib
+    K = args[5]
+    assert per_qp == F + K * I
+
+
+def test_multi_gpu_request_exits_with_message():
+    r = subprocess.run([sys.executable, str(ROOT / "bench.py"), "--gpus", "2"], capture_output=True, text=True,
+                       timeout=120)
+    assert r.returncode == 2
+    assert "one GPU" in r.stderr
