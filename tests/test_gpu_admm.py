@@ -348,6 +348,26 @@ def test_admm_stream_kernel_wide_rows_match_generic_on_config4_batch():
     assert not torch.equal(o_a.x_blocks, o_b.x_blocks)  # two different kernels ran
 
 
+@pytest.mark.parametrize("kernel", ["stream", "generic"])
+def test_admm_config5_large_rho_stays_with_oracle(kernel):
+    # the reference's default adaptation on config 5 raises rho ~2000x at
+    # iteration 25 (rho_f ~ 2.4e5, cond(Theta) ~ 1e9); the stored stage
+    # inverses must be the symmetric part of the computed inverses: mirroring
+    # one triangle made both kernels diverge (x off by 1e-2 one iteration
+    # later, 1e13 after fifteen)
+    prob = configs.config5(B=2, seed=3)
+    qp = prob.build_qp(*prob.initial_guess())
+    cfg = oracle.OracleCfg(max_iter=60, check_every=25, adapt_rho_every=25, sigma=1e-6, eps_abs=1e-13, eps_rel=1e-13,
+                           rho_f_factor=1000.0, alpha=1.6, adaptive_rho_tolerance=5.0)
+    flags = _lib.FLAG_GENERIC_KERNEL if kernel == "generic" else 0
+    ref, it_ref, _, out, stats = _run_pair(qp, cfg, torch.float64, diag_cost=True, kernel_flags=flags)
+    np.testing.assert_array_equal(stats.num_iter.cpu().numpy(), it_ref)
+    assert np.all(ref.rho_bar > 100.0)
+    assert rel_err(out.rho_bar, ref.rho_bar) < 1e-4
+    assert rel_err(out.x_blocks, ref.x_blocks) < 1e-5
+    assert rel_err(out.y_f_dyn, ref.y_f_dyn) < 1e-4
+
+
 @pytest.mark.parametrize("seed", [0, 3])
 def test_admm_config5_first_rho_update_matches_oracle(seed):
     # config 5 (dt = 10, rho_f / sigma = 1e8 at the start): the dual residual

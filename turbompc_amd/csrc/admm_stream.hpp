@@ -1241,6 +1241,23 @@ __global__ __launch_bounds__(kWave, 2) void factor_std_kernel(Dims d, const R* _
     if (i < n)
 #pragma unroll
       for (int j = 0; j < NC; ++j) a[j] *= myip;
+    // keep the symmetric part of the computed inverse (row i averaged with
+    // column i): mirroring one triangle of the slightly asymmetric result
+    // breaks its small residual at cond(Theta) ~ 1e9 (large rho_f), and the
+    // ADMM iteration then diverges
+    if (i < n)
+#pragma unroll
+      for (int j = 0; j < NC; ++j) th[i * n + j] = a[j];
+    wsync();
+    if (i < n) {
+      C col[NC];
+#pragma unroll
+      for (int k = 0; k < NC; ++k) col[k] = th[k * n + i];
+      __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+      for (int k = 0; k < NC; ++k) a[k] = C(0.5) * (a[k] + col[k]);
+    }
+    wsync();
     if (i < n) {
 #pragma unroll
       for (int j = 0; j < NC; ++j) th[i * n + j] = a[j];

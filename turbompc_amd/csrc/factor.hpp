@@ -151,12 +151,20 @@ __global__ __launch_bounds__(kWave) void factor_kernel(Dims d, QPDev<R> qp,
     }
     // ---- invert and store packed ------------------------------------------
     gj_invert_spd(A, rowk, colk, n);
+    wsync();
+    // the computed inverse is slightly asymmetric; its symmetric part (not one
+    // triangle mirrored, which at cond(Theta) ~ 1e9 breaks the inverse's small
+    // residual and makes the ADMM iteration diverge) is what the solves and
+    // the next Schur complement use
     R* out = thinv + ((size_t)t * d.B + b) * pk;
     for (int e = tid; e < nn; e += kWave) {
       const int i = e / n, j = e - (e / n) * n;
-      if (j <= i) out[((i * (i + 1)) >> 1) + j] = (R)A[e];
-      Ainv[e] = A[e];
+      const Cmp v = Cmp(0.5) * (A[e] + A[j * n + i]);
+      if (j <= i) out[((i * (i + 1)) >> 1) + j] = (R)v;
+      Ainv[e] = v;
     }
+    wsync();
+    for (int e = tid; e < nn; e += kWave) A[e] = Ainv[e];
     // ---- phi_t for the next stage ------------------------------------------
     if (t < N) {
       if (SRC == SRC_QP) {
