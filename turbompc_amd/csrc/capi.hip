@@ -662,9 +662,14 @@ int admm_pcg_impl(hipStream_t s, const tmpc_dims* dims, const tmpc_qp* qp, const
   if (!ws || wsb < admm_pcg_ws_bytes<R>(d)) return TMPC_EWORKSPACE;
   int st = copy_state<R>(s, d, in, out);
   if (st) return st;
-  if (pcg_iters && cfg->max_iter > 0 &&
-      hipMemsetAsync(pcg_iters, 0, (size_t)d.B * cfg->max_iter * sizeof(uint32_t), s) != hipSuccess)
-    return TMPC_ELAUNCH;
+  if (pcg_iters && cfg->max_iter > 0) {
+    const size_t cnt = (size_t)d.B * cfg->max_iter;
+    if ((cnt + 255) / 256 > (size_t)INT32_MAX) return TMPC_EBADSHAPE;
+    hipLaunchKernelGGL((fill_kernel<uint32_t>), dim3((unsigned)((cnt + 255) / 256)), dim3(256), 0, s, pcg_iters,
+                       cnt, 0u);
+    st = launch_status();
+    if (st) return st;
+  }
   const size_t B = d.B, T = d.T, n = d.n;
   Carver c{static_cast<char*>(ws)};
   R* S = c.take<R>(B * T * n * 3 * n);

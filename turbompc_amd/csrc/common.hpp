@@ -62,6 +62,14 @@ __device__ __forceinline__ R rinf() {
   return __builtin_huge_val();
 }
 
+// Fills n words with v.  Used instead of hipMemsetAsync so that a solve
+// captured in a HIP graph holds kernel nodes only.
+template <typename W>
+__global__ void fill_kernel(W* p, size_t n, W v) {
+  const size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < n) p[i] = v;
+}
+
 // One workgroup is one wavefront; LDS traffic between lanes of the wave is
 // ordered by this barrier (a single-wave s_barrier is cheap on CDNA).
 __device__ __forceinline__ void wsync() { __syncthreads(); }
