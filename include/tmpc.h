@@ -32,7 +32,9 @@ typedef enum tmpc_status {
   TMPC_EBADSHAPE = 1,  /* dimensions outside the supported range          */
   TMPC_EBADARG = 2,    /* null pointer or invalid configuration value     */
   TMPC_EWORKSPACE = 3, /* workspace smaller than *_workspace_bytes()      */
-  TMPC_ELAUNCH = 4     /* a HIP launch or copy failed                     */
+  TMPC_ELAUNCH = 4,    /* a HIP launch or copy failed                     */
+  TMPC_ESCRATCH = 5    /* the problem needs more scratch than the
+                          allocation-free entry point holds               */
 } tmpc_status;
 
 typedef struct tmpc_dims {
@@ -113,6 +115,25 @@ int tmpc_admm_direct_f32(hipStream_t stream, const tmpc_dims* dims, const tmpc_q
 int tmpc_admm_direct_f64(hipStream_t stream, const tmpc_dims* dims, const tmpc_qp* qp,
                          const tmpc_state* in, tmpc_state* out, uint32_t* iters_out,
                          const tmpc_admm_cfg* cfg, void* workspace, size_t workspace_bytes);
+
+/* ---- allocation-free variant of tmpc_admm_direct_* -------------------------
+ * No counterpart in the reference.  It is for callers that cannot allocate
+ * device memory or pass a workspace: code under HIP graph capture, tight
+ * serving loops, harnesses that forbid hipMalloc.  Same solve as
+ * tmpc_admm_direct_f32 (elem_bytes 4) / _f64 (elem_bytes 8), with the
+ * workspace taken from a scratch array of TMPC_NOALLOC_SCRATCH_BYTES that the
+ * library holds on each GPU it runs on until the process ends; the call
+ * itself allocates nothing.  A problem batch whose workspace
+ * (tmpc_admm_direct_workspace_bytes) exceeds that size is rejected with
+ * TMPC_ESCRATCH.  Every call on one GPU shares that GPU's array: calls that
+ * overlap on one GPU (different streams or host threads) race, so serialise
+ * them.  TMPC_FLAG_WARM_RECORDS is rejected (TMPC_EBADARG), since the shared
+ * array cannot vouch for the previous call's records.  `stream` must belong
+ * to the current device. */
+#define TMPC_NOALLOC_SCRATCH_BYTES ((size_t)64 << 20)
+int tmpc_admm_direct_noalloc(hipStream_t stream, int elem_bytes, const tmpc_dims* dims, const tmpc_qp* qp,
+                             const tmpc_state* in, tmpc_state* out, uint32_t* iters_out,
+                             const tmpc_admm_cfg* cfg);
 
 /* ---- one SQP step on the device --------------------------------------------
  * The body of the reference's SQP while_loop (turbompc/solvers/turbompc_solver.py:1570-1711)

@@ -39,7 +39,7 @@ def test_every_declared_entry_point_is_exported_and_bound(lib):
 
 def test_version_and_status_strings(lib):
     assert lib.tmpc_version() >= 100
-    for code in range(5):
+    for code in range(6):
         assert lib.tmpc_status_string(code)
     assert lib.tmpc_status_string(99)
 
@@ -69,3 +69,24 @@ def test_shape_and_argument_errors_return_before_any_launch(lib):
     assert st == 2  # TMPC_EBADARG: null QP / state pointers
     assert lib.tmpc_blktri_factor_f32(None, 4, 1, 17, None, None, 0) == 1
     assert lib.tmpc_blktri_factor_f32(None, 4, 10, 17, None, None, 0) == 2
+
+
+def test_noalloc_entry_rejects_on_the_host(lib):
+    """tmpc_admm_direct_noalloc: checks that return before any HIP call."""
+    cfg = _lib.AdmmCfg()
+    ok = _lib.Dims(4, 10, 17, 13, 13, 4)
+    assert lib.tmpc_admm_direct_noalloc(None, 2, ctypes.byref(ok), None, None, None, None, ctypes.byref(cfg)) == 2
+    bad = _lib.Dims(4, 1, 17, 13, 13, 4)
+    assert lib.tmpc_admm_direct_noalloc(None, 4, ctypes.byref(bad), None, None, None, None, ctypes.byref(cfg)) == 1
+    warm = _lib.AdmmCfg()
+    warm.flags = _lib.FLAG_STD_DYNAMICS | _lib.FLAG_WARM_RECORDS
+    assert lib.tmpc_admm_direct_noalloc(None, 4, ctypes.byref(ok), None, None, None, None, ctypes.byref(warm)) == 2
+    # the smallest batch whose workspace exceeds the scratch array
+    B = 1
+    while lib.tmpc_admm_direct_workspace_bytes(4, ctypes.byref(_lib.Dims(B, 41, 17, 13, 13, 4))) \
+            <= _lib.NOALLOC_SCRATCH_BYTES:
+        B *= 2
+    big = _lib.Dims(B, 41, 17, 13, 13, 4)
+    st = lib.tmpc_admm_direct_noalloc(None, 4, ctypes.byref(big), None, None, None, None, ctypes.byref(cfg))
+    assert st == 5  # TMPC_ESCRATCH
+    assert b"scratch" in lib.tmpc_status_string(st)

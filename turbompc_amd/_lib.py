@@ -28,6 +28,7 @@ FLAG_GENERIC_KERNEL = 2
 FLAG_DIAG_COST = 4  # every D_t diagonal
 FLAG_WARM_RECORDS = 8  # the workspace's stage records are the previous SQP step's
 FLAG_WARM_INEQ = 16  # with FLAG_WARM_RECORDS: G, l, u changed too
+NOALLOC_SCRATCH_BYTES = 64 << 20  # TMPC_NOALLOC_SCRATCH_BYTES (scratch of tmpc_admm_direct_noalloc)
 
 
 def flag_stream_p(p: int) -> int:
@@ -40,6 +41,7 @@ _STATUS = {
     2: "invalid argument",
     3: "workspace too small",
     4: "HIP launch failed",
+    5: "problem needs more than the allocation-free scratch",
 }
 
 
@@ -112,6 +114,7 @@ SIGNATURES = {
     "tmpc_admm_direct_workspace_bytes": [ctypes.c_int, _PD],
     "tmpc_admm_direct_f32": [_VP, _PD, _PQ, _PS, _PS, _VP, _PC, _VP, _SZ],
     "tmpc_admm_direct_f64": [_VP, _PD, _PQ, _PS, _PS, _VP, _PC, _VP, _SZ],
+    "tmpc_admm_direct_noalloc": [_VP, ctypes.c_int, _PD, _PQ, _PS, _PS, _VP, _PC],
     "tmpc_sqp_admm_step_f32": [_VP, _PD, _PQ, _PS, _PS, _VP, _PC, _PSQ, _VP, _SZ],
     "tmpc_sqp_admm_step_f64": [_VP, _PD, _PQ, _PS, _PS, _VP, _PC, _PSQ, _VP, _SZ],
     "tmpc_admm_pcg_workspace_bytes": [ctypes.c_int, _PD],

@@ -4,6 +4,7 @@
 #include "../../include/tmpc.h"
 
 #include <algorithm>
+#include <mutex>
 #include <vector>
 
 #include "admm_direct.hpp"
@@ -15,6 +16,12 @@
 #include "quadrotor.hpp"
 #include "adjoint.hpp"
 #include "sqp.hpp"
+
+// Workspace of tmpc_admm_direct_noalloc: one copy per GPU, at its own device
+// address, held until the process ends.  Host code never uses this name as an
+// address: it asks each device for the array's address once
+// (noalloc_scratch() below) and passes that pointer.
+static __device__ __align__(256) unsigned char scratch[TMPC_NOALLOC_SCRATCH_BYTES];
 
 namespace tmpc {
 namespace {
@@ -456,6 +463,48 @@ int admm_direct_impl(hipStream_t s, const tmpc_dims* dims, const tmpc_qp* qp,
   return TMPC_OK;
 }
 
+// ------------------------------------------------------- allocation-free ----
+// Device address of `scratch` on each device, looked up once per device with
+// that device current (each GPU holds its own copy at its own address).
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[kMaxDevices] = {};
+
+int noalloc_scratch(hipStream_t s, void** out) {
+  int dev = -1;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) return TMPC_ELAUNCH;
+  if (s != nullptr) {
+    hipDevice_t sdev = -1;
+    if (hipStreamGetDevice(s, &sdev) != hipSuccess) return TMPC_EBADARG;
+    if ((int)sdev != dev) return TMPC_EBADARG;  // the stream belongs to another device
+  }
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (g_scratch_ptr[dev] == nullptr) {
+    void* p = nullptr;
+    if (hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)) != hipSuccess || p == nullptr) return TMPC_ELAUNCH;
+    g_scratch_ptr[dev] = p;
+  }
+  *out = g_scratch_ptr[dev];
+  return TMPC_OK;
+}
+
+// The kernels of tmpc_admm_direct_* initialise every workspace word they read
+// (per-problem control words and residuals in the first chunk, the factor and
+// stage records before the iterations), so the scratch needs no clearing.
+template <typename R>
+int admm_direct_noalloc_impl(hipStream_t s, const tmpc_dims* dims, const tmpc_qp* qp, const tmpc_state* in,
+                             tmpc_state* out, uint32_t* iters, const tmpc_admm_cfg* cfg) {
+  if (!dims_ok(dims)) return TMPC_EBADSHAPE;
+  if (!cfg) return TMPC_EBADARG;
+  if (cfg->flags & TMPC_FLAG_WARM_RECORDS) return TMPC_EBADARG;
+  const size_t need = direct_ws_bytes<R>(to_dims(dims));
+  if (need > TMPC_NOALLOC_SCRATCH_BYTES) return TMPC_ESCRATCH;
+  void* ws = nullptr;
+  const int st = noalloc_scratch(s, &ws);
+  if (st) return st;
+  return admm_direct_impl<R>(s, dims, qp, in, out, iters, cfg, ws, TMPC_NOALLOC_SCRATCH_BYTES);
+}
+
 // ---------------------------------------------------------------- blktri ----
 template <typename R>
 int blktri_factor_impl(hipStream_t s, int B, int T, int n, const R* S, void* ws, size_t wsb) {
@@ -870,6 +919,7 @@ const char* tmpc_status_string(int status) {
     case TMPC_EBADARG: return "invalid argument";
     case TMPC_EWORKSPACE: return "workspace too small";
     case TMPC_ELAUNCH: return "HIP launch failed";
+    case TMPC_ESCRATCH: return "problem needs more than the allocation-free scratch";
     default: return "unknown status";
   }
 }
@@ -896,6 +946,13 @@ int tmpc_admm_direct_f64(hipStream_t s, const tmpc_dims* dims, const tmpc_qp* qp
                          tmpc_state* out, uint32_t* iters, const tmpc_admm_cfg* cfg, void* ws,
                          size_t wsb) {
   return admm_direct_impl<double>(s, dims, qp, in, out, iters, cfg, ws, wsb);
+}
+
+int tmpc_admm_direct_noalloc(hipStream_t s, int elem_bytes, const tmpc_dims* dims, const tmpc_qp* qp,
+                             const tmpc_state* in, tmpc_state* out, uint32_t* iters, const tmpc_admm_cfg* cfg) {
+  if (elem_bytes == 4) return admm_direct_noalloc_impl<float>(s, dims, qp, in, out, iters, cfg);
+  if (elem_bytes == 8) return admm_direct_noalloc_impl<double>(s, dims, qp, in, out, iters, cfg);
+  return TMPC_EBADARG;
 }
 
 int tmpc_sqp_admm_step_f32(hipStream_t s, const tmpc_dims* dims, const tmpc_qp* qp, const tmpc_state* in,
