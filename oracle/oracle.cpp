@@ -8,8 +8,10 @@
 //   schur_build      closed form S = P + sigma I + rho_f C^T C + rho G^T G and the
 //                    Phiinv block formula, checked against dense numpy assembly.
 //   blktri_solve     dense numpy.linalg.solve on the assembled S.
-//   pcg              converges to the dense solve; iteration count of a
-//                    diagonal system with k distinct eigenvalues is k.
+//   pcg              converges to the dense solve; stops after exactly r + 1
+//                    iterations when M^{-1} S has r + 1 distinct eigenvalues;
+//                    every fixed-count iterate is the Galerkin solution on its
+//                    Krylov space (tests/test_oracle_pcg_pins.py).
 //   admm_solve       (a) one iteration against a hand-assembled dense
 //                    restatement in numpy; (b) at convergence: primal
 //                    feasibility, stationarity, complementarity; (c) brute-force

@@ -8,7 +8,12 @@ with the first_order criterion at a fixed iteration count (tol_convergence = 0):
   -> relinearize at the new iterate, carrying the ADMM state (including rho)
 Used by bench.py's cpu_baseline leg and by the SQP parity tests.
 
-Pins: the quadrotor Jacobians are checked against central differences and
+Pins: the loop itself (tests/test_oracle_sqp.py) -- on linear dynamics n_sqp
+iterations of K ADMM steps equal one solve of n_sqp*K steps from the zero
+state bit for bit (x starts at 0 once, z and the duals carry), and with
+adaptive rho the chain of ADMM calls on the carried state, rho included; the
+converged quadrotor SQP meets the NLP first-order conditions evaluated with an
+independent numpy RK4 and complex-step Jacobians.  The quadrotor Jacobians are checked against central differences and
 torch.func.jacfwd (tests/test_oracle_adjoint_quadrotor.py); the obstacle rows
 against central differences of g, known answers on the sphere and the exactness
 of the linearization at its own point, and their Hessian against differences
