@@ -129,3 +129,40 @@ def soften(qp, gamma, shrink=1.0):
     return QPData(cost=qp.cost, eq=qp.eq,
                   ineq=QPInequalityBlocks(qp.ineq.G, mid - half, mid + half,
                                           torch.tensor(float(gamma), dtype=l.dtype), True))
+
+
+def polish(a, b, lower, upper):
+    """Exact solution of QP problem b (dict of np_qp arrays) on a fixed active
+    set: the equality-constrained KKT [[P, C^T, Ga^T], [C, 0, 0], [Ga, 0, 0]]
+    with the active rows of G held at their bounds, solved densely.  lower /
+    upper (T*m,) mark the rows held at l / u.  Returns (x (T,n), y_f0, y_f
+    (N,nx), y_g (T,m), bound violation of the other rows, sign margin): the
+    active set is the QP's own when the violation is ~0 and the margin
+    positive (y_g >= 0 at upper rows, <= 0 at lower rows, the sign convention
+    P x + q + C^T y_f + G^T y_g = 0)."""
+    T, n, _ = a["D"][b].shape
+    N, nx, _ = a["Am"][b].shape
+    m = a["G"][b].shape[1]
+    n0 = a["A0"][b].shape[0]
+    P = dense_P(a["D"][b], a["E"][b])
+    C = dense_C(a["A0"][b], a["Am"][b], a["Ap"][b])
+    G = dense_G(a["G"][b])
+    l, u = a["l"][b].reshape(-1), a["u"][b].reshape(-1)
+    act = lower | upper
+    Ga, ba = G[act], np.where(lower, l, u)[act]
+    c = np.concatenate([a["c0"][b], a["c"][b].reshape(-1)])
+    nz, ne, na = P.shape[0], C.shape[0], Ga.shape[0]
+    K = np.zeros((nz + ne + na, nz + ne + na))
+    K[:nz, :nz] = P
+    K[:nz, nz:nz + ne] = C.T
+    K[nz:nz + ne, :nz] = C
+    K[:nz, nz + ne:] = Ga.T
+    K[nz + ne:, :nz] = Ga
+    sol = np.linalg.solve(K, np.concatenate([-a["q"][b].reshape(-1), c, ba]))
+    x, y = sol[:nz], sol[nz:nz + ne]
+    yg = np.zeros(T * m)
+    yg[act] = sol[nz + ne:]
+    gx = G @ x
+    viol = float(np.max(np.maximum(l - gx, 0) + np.maximum(gx - u, 0))) if T * m else 0.0
+    margin = min(np.min(yg[upper], initial=np.inf), -np.max(yg[lower], initial=-np.inf))
+    return x.reshape(T, n), y[:n0], y[n0:].reshape(N, nx), yg.reshape(T, m), viol, margin

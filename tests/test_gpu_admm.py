@@ -3,9 +3,9 @@ and the quadrotor linearization against the CPU oracle, through the C ABI.
 
 Parity protocol (fixed iteration counts, adapt_rho_every = 0): fp64 must match
 the fp64 oracle to 1e-9 (normwise relative); fp32 must match the fp64 oracle to
-1e-4, or -- where the fp32 oracle itself sits further than that from the fp64
-result because of the conditioning of S -- to within 4x the fp32 oracle's own
-distance.
+1e-4.  The fp32 kernels factor in fp64, so they sit closer to the fp64 result
+than the fp32 oracle does (quadrotor QP states: 2.5e-5 against the fp32
+oracle's 8.0e-5).
 
 Adaptive rho is tested separately with a looser bar: the rho candidate
 rho * sqrt(r_p / r_d) is a ratio of residual norms that cancel, so two correct
@@ -129,11 +129,10 @@ def test_admm_direct_config1_fp32():
     cfg = oracle.OracleCfg(max_iter=50, check_every=25, adapt_rho_every=0, sigma=1e-6, eps_abs=1e-9, eps_rel=1e-9,
                            rho_f_factor=1000.0, alpha=1.0)
     ref, it_ref, _, out, stats = _run_pair(qp, cfg, torch.float32)
-    ref32, _, _ = oracle.admm_solve(qp, zero_state(qp, 0.1), cfg, dtype=np.float32)
-    for k in ("x_blocks", "y_f_dyn", "y_g"):
+    for k in ("x_blocks", "y_f_dyn", "y_g", "z_g", "y_f_0"):
         e = rel_err(getattr(out, k), getattr(ref, k))
-        e_or = rel_err(getattr(ref32, k), getattr(ref, k))
-        assert e < max(TOL[torch.float32], 4 * e_or), (k, e, e_or)
+        print(f"config1 fp32 {k}: rel err vs fp64 oracle {e:.2e}")
+        assert e < TOL[torch.float32], (k, e)
 
 
 def test_admm_direct_quadrotor_qp_fp32_and_fp64():
@@ -144,10 +143,10 @@ def test_admm_direct_quadrotor_qp_fp32_and_fp64():
     ref, it_ref, _, out64, _ = _run_pair(qp, cfg, torch.float64)
     _assert_state_close(out64, ref, 1e-9)
     _, _, _, out32, _ = _run_pair(qp, cfg, torch.float32)
-    ref32, _, _ = oracle.admm_solve(qp, zero_state(qp, 0.1), cfg, dtype=np.float32)
-    e = rel_err(out32.x_blocks, ref.x_blocks)
-    e_or = rel_err(ref32.x_blocks, ref.x_blocks)
-    assert e < max(TOL[torch.float32], 4 * e_or), (e, e_or)
+    for k in ("x_blocks", "y_f_dyn", "y_g"):
+        e = rel_err(getattr(out32, k), getattr(ref, k))
+        print(f"quadrotor QP fp32 {k}: rel err vs fp64 oracle {e:.2e}")
+        assert e < TOL[torch.float32], (k, e)
 
 
 def test_admm_direct_warm_start_and_in_place_state():
@@ -186,6 +185,36 @@ def test_admm_pcg_fixed_pcg_iterations_fp64():
     ref, it_ref, pcg_ref, out, stats = _run_pair(qp, cfg, torch.float64, backend=AdmmBackend.HIP_PCG, schur="pcg")
     np.testing.assert_array_equal(stats.num_pcg_iters.sum(1).cpu().numpy(), pcg_ref)
     _assert_state_close(out, ref, 1e-9)
+
+
+def test_admm_pcg_config2_fp32():
+    """Config 2 in fp32 on the PCG backend, tolerance-stopped (pcg_eps 1e-6,
+    at most 50 PCG iterations, as the workload specifies) against the fp64
+    oracle."""
+    prob = configs.config2(B=6, seed=0)
+    qp = prob.build_qp(*prob.initial_guess())
+    cfg = oracle.OracleCfg(max_iter=12, check_every=25, adapt_rho_every=0, sigma=1e-6, eps_abs=1e-9, eps_rel=1e-9,
+                           rho_f_factor=1000.0, alpha=1.0, pcg_eps=1e-6, pcg_max_iter=50)
+    ref, it_ref, pcg_ref, out, stats = _run_pair(qp, cfg, torch.float32, backend=AdmmBackend.HIP_PCG, schur="pcg")
+    np.testing.assert_array_equal(stats.num_iter.cpu().numpy(), it_ref)
+    assert np.all(np.abs(stats.num_pcg_iters.sum(1).cpu().numpy() - pcg_ref) <= 2)
+    for k in ("x_blocks", "y_f_dyn", "y_g"):
+        e = rel_err(getattr(out, k), getattr(ref, k))
+        print(f"config2 PCG fp32 {k}: rel err vs fp64 oracle {e:.2e}")
+        assert e < TOL[torch.float32], (k, e)
+
+
+def test_admm_pcg_fixed_pcg_iterations_fp32():
+    prob = configs.config2(B=5, seed=1)
+    qp = prob.build_qp(*prob.initial_guess())
+    cfg = oracle.OracleCfg(max_iter=6, check_every=25, adapt_rho_every=0, sigma=1e-6, eps_abs=1e-9, eps_rel=1e-9,
+                           rho_f_factor=1000.0, alpha=1.0, pcg_eps=0.0, pcg_max_iter=6)
+    ref, it_ref, pcg_ref, out, stats = _run_pair(qp, cfg, torch.float32, backend=AdmmBackend.HIP_PCG, schur="pcg")
+    np.testing.assert_array_equal(stats.num_pcg_iters.sum(1).cpu().numpy(), pcg_ref)
+    for k in ("x_blocks", "y_f_dyn", "y_g"):
+        e = rel_err(getattr(out, k), getattr(ref, k))
+        print(f"config2 PCG fixed-count fp32 {k}: rel err vs fp64 oracle {e:.2e}")
+        assert e < TOL[torch.float32], (k, e)
 
 
 def test_admm_pcg_matches_direct_when_tight():

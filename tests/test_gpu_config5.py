@@ -1,0 +1,217 @@
+"""Config 5 (Clohessy-Wiltshire rendezvous: nx=6, nu=3, N=100, dt=10 s,
+|u| <= 0.01, x0 ~ N(0, diag(100^2 I3, 0.1^2 I3)), fp64) end to end:
+forward ADMM with the reference defaults, then the implicit-differentiation
+backward pass (direct_hip_kkt).
+
+The workload as specified: 200 ADMM iterations (adaptive rho every 25,
+alpha 1.6) and the adjoint of the loss sum ||x_N||^2 with respect to x0, Q
+and R.  The forward iterate is compared with the CPU restatement, the adjoint
+KKT solve at that iterate with the dense oracle.
+
+Gradient check: ADMM converges slowly on this workload (measured with the
+oracle: the 200-iteration iterate sits 59-99 % from the exact QP solution,
+and 40,000 iterations identify the active set of only 2 of 16 problems), so
+the central differences are taken of the exact solution instead: the QP solved
+on its active set (helpers.polish), which is the tightly converged forward
+solve.  The GPU solve is warm-started at that solution (an ADMM fixed point)
+and its gradients are compared with the differences.  At the exact solution
+x_N is ~1e-15 (the optimum holds the spacecraft at the origin long before
+t = N), so sum ||x_N||^2 has vanishing gradients; the check adds a random
+linear functional of the whole trajectory, as the reference's own test does
+with norms of states and controls (tests/cuda/solvers/test_differentiable.py:120-127).
+"""
+import copy
+
+import numpy as np
+import pytest
+import torch
+
+import oracle
+from helpers import np_qp, polish, rel_err, zero_state
+from turbompc_amd.problems import configs
+from turbompc_amd.problems.ocp import LinearOCP
+from turbompc_amd.solvers.admm.admm import ADMMState
+from turbompc_amd.solvers.turbompc_solver import DEFAULT_SOLVER_PARAMS, TurboMPCSolver
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda"
+WX, WU, _ = LinearOCP.WEIGHT_KEYS
+
+
+def _params(K, adapt=25):
+    p = copy.deepcopy(DEFAULT_SOLVER_PARAMS)  # reference defaults (turbompc.yaml)
+    p["num_sqp_iteration_max"] = 1  # linear dynamics: the QP is the problem
+    p["admm"]["max_iter"] = K
+    p["admm"]["adapt_rho_every"] = adapt
+    return p
+
+
+def _select(prob, idx):
+    """The problems idx of a config 5 batch."""
+    lo, hi = prob.u_bounds
+    return LinearOCP(A=prob.A[idx], Bm=prob.Bm[idx], horizon=prob.horizon, num_states=prob.num_state_variables,
+                     num_controls=prob.num_control_variables, initial_state=prob.x0[idx], weights_state=prob.wx[idx],
+                     weights_control=prob.wu[idx], weights_final=prob.wf[idx], control_bounds=(lo, hi))
+
+
+def test_config5_workload_forward_and_adjoint():
+    B = 32
+    prob = configs.config5(B=B, seed=0)
+    qp = prob.build_qp(*prob.initial_guess())
+    cfg = oracle.OracleCfg(max_iter=200, check_every=25, adapt_rho_every=25, sigma=1e-6, eps_abs=1e-9, eps_rel=1e-9,
+                           rho_f_factor=1000.0, alpha=1.6, adaptive_rho_tolerance=5.0)
+    ref, it_ref, _ = oracle.admm_solve(qp, zero_state(qp, 0.1), cfg)
+    solver = TurboMPCSolver(prob.to(DEV), _params(200))
+    x0 = solver.program.x0.clone().requires_grad_(True)
+    w = {k: v.clone().requires_grad_(True) for k, v in solver.program.weights_dict().items()}
+    sol = solver.get_differentiable_solve_function()(solver.initial_guess(), {"initial_state": x0}, w)
+    L = (sol.states[:, -1] ** 2).sum()
+    L.backward()
+    torch.cuda.synchronize()
+    assert torch.all(sol.admm_iters[:, 0].cpu() == torch.as_tensor(it_ref))
+    # adaptive rho: the candidate is a ratio of cancelled residuals, so rho and
+    # the iterates after each update agree to ~1e-5 between summation orders
+    e = rel_err(sol.admm_state.x_blocks, ref.x_blocks)
+    print(f"config 5 forward (200 iterations): rel err vs oracle {e:.2e}, rho err "
+          f"{rel_err(sol.admm_state.rho_bar, ref.rho_bar):.2e}")
+    assert e < 1e-4
+    assert rel_err(sol.admm_state.rho_bar, ref.rho_bar) < 1e-3
+    for g in (x0.grad, w[WX].grad, w[WU].grad):
+        assert g is not None and bool(torch.isfinite(g).all())
+    # the adjoint KKT of this iterate against the dense oracle
+    kkt = sol.kkt_state
+    dl = torch.zeros_like(sol.states)
+    dl[:, -1] = 2 * sol.states[:, -1].detach()
+    ctx = solver._build_backward_qp(solver.program, sol, dl, torch.zeros_like(sol.controls),
+                                    torch.zeros_like(kkt.slack))
+    res = solver._solve_backward_qp_direct(solver.program, ctx, sol, torch.zeros_like(kkt.slack))
+    dz_ref, _ = oracle.adjoint_kkt(ctx.solve_qp.to("cpu"))
+    dz = torch.cat([res.dx_states, res.dx_controls], dim=-1)
+    assert rel_err(dz, dz_ref) < 1e-9
+
+
+def _exact_solution(prob, a, guess):
+    """helpers.polish on each problem with the active set of `guess` (an
+    ADMMState-like with z_g, y_g), asserting that it is the QP's own."""
+    B = prob.B
+    out = []
+    for b in range(B):
+        z, yg = guess.z_g[b].reshape(-1), guess.y_g[b].reshape(-1)
+        l, u = a["l"][b].reshape(-1), a["u"][b].reshape(-1)
+        lower, upper = (z <= l + 1e-9) & (yg < 0), (z >= u - 1e-9) & (yg > 0)
+        x, y0, yf, ygp, viol, margin = polish(a, b, lower, upper)
+        assert viol < 1e-9 and margin > 1e-6, (b, viol, margin)
+        out.append((x, y0, yf, ygp, lower, upper))
+    return out
+
+
+def test_config5_gradients_match_differences_of_the_exact_solution():
+    full = configs.config5(B=16, seed=0)
+    prob = _select(full, [0, 7])  # the two problems whose active set 40k oracle iterations identify
+    B, T, nx, nu = prob.B, prob.horizon + 1, prob.num_state_variables, prob.num_control_variables
+    a = np_qp(prob.build_qp(*prob.initial_guess()))
+    cfg = oracle.OracleCfg(max_iter=40000, check_every=25, adapt_rho_every=25, sigma=1e-6, eps_abs=1e-14,
+                           eps_rel=1e-14, rho_f_factor=1000.0, alpha=1.6, adaptive_rho_tolerance=5.0)
+    qp = prob.build_qp(*prob.initial_guess())
+    long, _, _ = oracle.admm_solve(qp, zero_state(qp, 0.1), cfg)
+    exact = _exact_solution(prob, a, long)
+    act = [(lo, up) for (_, _, _, _, lo, up) in exact]
+
+    g = np.random.default_rng(0)
+    cs, cu = g.standard_normal((B, T, nx)), g.standard_normal((B, T, nu))
+
+    def loss_of(x):  # x (B, T, n) -> per-problem loss
+        s, uu = x[..., :nx], x[..., nx:]
+        return np.sum(cs * s, axis=(1, 2)) + np.sum(cu * uu, axis=(1, 2)) + np.sum(s[:, -1] ** 2, axis=1)
+
+    def exact_loss(p):
+        ap = np_qp(p.build_qp(*p.initial_guess()))
+        xs = []
+        for b in range(B):
+            x, _, _, _, viol, margin = polish(ap, b, *act[b])
+            assert viol < 1e-9 and margin > 0, (b, viol, margin)  # the active set still holds
+            xs.append(x)
+        return loss_of(np.stack(xs))
+
+    # the GPU solve, warm-started at the exact solution (an ADMM fixed point)
+    x_ex = np.stack([e[0] for e in exact])
+    t = lambda v: torch.as_tensor(np.asarray(v), dtype=torch.float64, device=DEV)  # noqa: E731
+    G = np.asarray(a["G"])
+    st0 = ADMMState(x_blocks=t(x_ex), y_g=t(np.stack([e[3] for e in exact])), y_f_0=t(np.stack([e[1] for e in exact])),
+                    y_f_dyn=t(np.stack([e[2] for e in exact])),
+                    z_g=t(np.clip(np.einsum("btij,btj->bti", G, x_ex), a["l"], a["u"])),
+                    xi_g=t(np.zeros((B, T, G.shape[2]))), rho_bar=t(np.full(B, 0.1)))
+    solver = TurboMPCSolver(prob.to(DEV), _params(50, adapt=0))
+    guess = solver.initial_guess()._replace(states=t(x_ex[..., :nx]), controls=t(x_ex[..., nx:]), admm_state=st0)
+    x0 = solver.program.x0.clone().requires_grad_(True)
+    w = {k: v.clone().requires_grad_(True) for k, v in solver.program.weights_dict().items()}
+    sol = solver.get_differentiable_solve_function()(guess, {"initial_state": x0}, w)
+    assert rel_err(sol.states, x_ex[..., :nx]) < 1e-9  # stayed at the fixed point
+    L = (t(cs) * sol.states).sum() + (t(cu) * sol.controls).sum() + (sol.states[:, -1] ** 2).sum()
+    L.backward()
+    torch.cuda.synchronize()
+
+    rng = np.random.default_rng(1)
+    checks = [("x0", b, int(rng.integers(nx))) for b in range(B) for _ in range(2)]
+    checks += [(WX, b, int(rng.integers(nx))) for b in range(B) for _ in range(2)]
+    checks += [(WU, b, int(rng.integers(nu))) for b in range(B) for _ in range(2)]
+    wscale = [max(float(w[WX].grad[b].abs().max()), float(w[WU].grad[b].abs().max())) for b in range(B)]
+
+    def central(fn, h):
+        return (fn(h) - fn(-h)) / (2 * h)
+
+    for name, b, i in checks:
+        if name == "x0":
+            # the solution is affine in x0 on its active set: the difference is exact
+            def f(d):
+                xp = prob.x0.clone()
+                xp[b, i] += d
+                return exact_loss(prob.with_params({"initial_state": xp}))[b]
+            fd, got, floor = central(f, 1e-4), float(x0.grad[b, i]), 1e-6
+        else:
+            base = prob.wx if name == WX else prob.wu
+
+            def f(d):
+                wp = base.clone()
+                wp[b, i] += d
+                return exact_loss(prob.with_weights({name: wp}))[b]
+            # smooth in the weights; Richardson's combination cancels the h^2
+            # term, and h = 1e-3 keeps the rounding of the polished solve
+            # (cond ~1e9-1e11) at ~1e-7 absolute (measured from the spread of
+            # the differences over h = 1e-3 .. 1e-7), which sets the floor
+            fd = (4 * central(f, 1e-3) - central(f, 2e-3)) / 3
+            got, floor = float(w[name].grad[b, i]), max(1e-6 * wscale[b], 3e-7)
+        print(f"  {name}[{b},{i}]: adjoint {got:.9g}  central difference of the exact solution {fd:.9g}", flush=True)
+        assert abs(got - fd) <= 1e-4 * abs(fd) + floor, (name, b, i, got, fd)
+
+
+@pytest.mark.parametrize("rho0", [0.1, 1e3, 1e4])
+def test_config5_large_rho_sweep_fp64(rho0):
+    """64 problems, the reference defaults (100 iterations, rho adapted every
+    25, alpha 1.6) from a default and from high starting rho: every problem
+    stays finite, stops at the oracle's iteration and tracks it.  rho_f = 1000
+    rho reaches ~1e7 here (cond(Theta) ~ 1e13).  The adapted rho is a ratio of
+    residuals that cancel, so after each update the iterates agree only to the
+    accuracy of that ratio (the fixed-rho runs below are the strict check)."""
+    prob = configs.config5(B=64, seed=0)
+    qp = prob.build_qp(*prob.initial_guess())
+    import test_gpu_admm as TA  # the paired oracle/GPU runner
+
+    cfg = oracle.OracleCfg(max_iter=100, check_every=25, adapt_rho_every=25, sigma=1e-6, eps_abs=1e-9, eps_rel=1e-9,
+                           rho_f_factor=1000.0, alpha=1.6, adaptive_rho_tolerance=5.0)
+    ref, it_ref, _, out, stats = TA._run_pair(qp, cfg, torch.float64, rho0=rho0, diag_cost=True)
+    x = out.x_blocks.cpu().numpy()
+    assert np.isfinite(x).all() and np.isfinite(out.y_f_dyn.cpu().numpy()).all()
+    np.testing.assert_array_equal(stats.num_iter.cpu().numpy(), it_ref)
+    worst = max(rel_err(x[b], ref.x_blocks[b]) for b in range(64))
+    print(f"rho0 {rho0:g}: adaptive, worst-problem x rel err {worst:.2e}, rho err {rel_err(out.rho_bar, ref.rho_bar):.2e}")
+    assert worst < {0.1: 1e-4, 1e3: 1e-3, 1e4: 5e-3}[rho0]
+    cfg0 = oracle.OracleCfg(**{**cfg.__dict__, "adapt_rho_every": 0})
+    ref, it_ref, _, out, stats = TA._run_pair(qp, cfg0, torch.float64, rho0=rho0, diag_cost=True)
+    x = out.x_blocks.cpu().numpy()
+    worst = max(rel_err(x[b], ref.x_blocks[b]) for b in range(64))
+    print(f"rho0 {rho0:g}: fixed rho, worst-problem x rel err {worst:.2e}, y_f {rel_err(out.y_f_dyn, ref.y_f_dyn):.2e}")
+    # rho_f / sigma reaches 1e12-1e13 at rho0 = 1e3-1e4: two exact-arithmetic
+    # equivalent factorizations (Gauss-Jordan stage inverses here, Cholesky in
+    # the oracle) agree to about cond * eps (measured 3.6e-6 and 1.2e-4)
+    assert worst < {0.1: 1e-9, 1e3: 2e-5, 1e4: 5e-4}[rho0]

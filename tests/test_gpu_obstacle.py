@@ -118,10 +118,10 @@ def test_config4_sqp_fp32_matches_cpu():
     B = 16
     prob = configs.config4(B=B, seed=1)
     xs, us, _ = _cpu_sqp(prob, 8, 30, np.float64)
-    xs32, us32, _ = _cpu_sqp(prob, 8, 30, np.float32)
     solver = TurboMPCSolver(prob.to("cuda", torch.float32), _params(8, 30))
     sol = solver.solve(solver.initial_guess())
     torch.cuda.synchronize()
-    for got, ref, ref32 in ((sol.states, xs, xs32), (sol.controls, us, us32)):
-        e, e_or = rel_err(got, ref), rel_err(ref32, ref)
-        assert e < max(TOL[torch.float32], 4 * e_or), (e, e_or)
+    for name, got, ref in (("states", sol.states, xs), ("controls", sol.controls, us)):
+        e = rel_err(got, ref)
+        print(f"config4 SQP fp32 {name}: rel err vs fp64 CPU SQP {e:.2e}")
+        assert e < TOL[torch.float32], (name, e)

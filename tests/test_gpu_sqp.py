@@ -57,14 +57,14 @@ def test_quadrotor_sqp_fp64_matches_cpu(n_sqp):
 def test_quadrotor_sqp_fp32_matches_cpu():
     B = 16
     xs, us, _ = _cpu_sqp(B, 1, 5, 20, np.float64)
-    xs32, us32, _ = _cpu_sqp(B, 1, 5, 20, np.float32)
     prob = make_quadrotor_config(B=B, seed=1, dtype=torch.float32, device="cuda")
     solver = TurboMPCSolver(prob, _params(5, 20))
     sol = solver.solve(solver.initial_guess())
     torch.cuda.synchronize()
-    for got, ref, ref32 in ((sol.states, xs, xs32), (sol.controls, us, us32)):
-        e, e_or = rel_err(got, ref), rel_err(ref32, ref)
-        assert e < max(TOL[torch.float32], 4 * e_or), (e, e_or)
+    for name, got, ref in (("states", sol.states, xs), ("controls", sol.controls, us)):
+        e = rel_err(got, ref)
+        print(f"quadrotor SQP fp32 {name}: rel err vs fp64 CPU SQP {e:.2e}")
+        assert e < TOL[torch.float32], (name, e)
 
 
 def test_sqp_stops_per_problem_on_tolerance():
