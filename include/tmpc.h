@@ -33,9 +33,19 @@ typedef enum tmpc_status {
   TMPC_EBADARG = 2,    /* null pointer or invalid configuration value     */
   TMPC_EWORKSPACE = 3, /* workspace smaller than *_workspace_bytes()      */
   TMPC_ELAUNCH = 4,    /* a HIP launch or copy failed                     */
-  TMPC_ESCRATCH = 5    /* the problem needs more scratch than the
+  TMPC_ESCRATCH = 5,   /* the problem needs more scratch than the
                           allocation-free entry point holds               */
+  TMPC_ENONFINITE = 6  /* a solution holds NaN or infinity: never returned
+                          by the asynchronous entry points, which flag it
+                          per problem in iters_out (TMPC_ITERS_NONFINITE);
+                          for host layers that turn the flag into an error */
 } tmpc_status;
+
+/* Bit 31 of iters_out[b] (tmpc_admm_direct_*, tmpc_sqp_admm_step_*,
+ * tmpc_admm_pcg_*, tmpc_admm_direct_noalloc): set when problem b's output
+ * state (x, z_g, y_g, xi_g, y_f0, y_f or rho) holds a NaN or an infinity.
+ * The iteration count is iters_out[b] & 0x7fffffff. */
+#define TMPC_ITERS_NONFINITE 0x80000000u
 
 typedef struct tmpc_dims {
   int32_t B, T, n, nx, n0, m;
@@ -107,7 +117,8 @@ void tmpc_set_timing_events(hipEvent_t before, hipEvent_t after);
  * (turbompc/solvers/admm/csrc/admm_cudss.cu:853-1199), with the semantics of
  * the reference's pure-JAX loop (turbompc/solvers/admm/admm.py:795-1049).
  * `in` is the warm start; `out` receives the final state (in == out allowed).
- * iters_out (B,) uint32 receives the ADMM iteration count per problem. */
+ * iters_out (B,) uint32 receives the ADMM iteration count per problem, with
+ * TMPC_ITERS_NONFINITE set for a problem whose final state is not finite. */
 size_t tmpc_admm_direct_workspace_bytes(int elem_bytes, const tmpc_dims* dims);
 int tmpc_admm_direct_f32(hipStream_t stream, const tmpc_dims* dims, const tmpc_qp* qp,
                          const tmpc_state* in, tmpc_state* out, uint32_t* iters_out,

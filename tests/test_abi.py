@@ -90,3 +90,14 @@ def test_noalloc_entry_rejects_on_the_host(lib):
     st = lib.tmpc_admm_direct_noalloc(None, 4, ctypes.byref(big), None, None, None, None, ctypes.byref(cfg))
     assert st == 5  # TMPC_ESCRATCH
     assert b"scratch" in lib.tmpc_status_string(st)
+
+
+def test_iteration_words_split_into_counts_and_nonfinite_flags():
+    import torch
+
+    from turbompc_amd.solvers.admm.admm import _split_iters
+
+    words = torch.tensor([0, 12, 0x7FFFFFFF, -(2 ** 31) + 12, -(2 ** 31)], dtype=torch.int32)  # bit 31 = flag
+    counts, bad = _split_iters(words)
+    assert counts.tolist() == [0, 12, 0x7FFFFFFF, 12, 0]
+    assert bad.tolist() == [False, False, False, True, True]

@@ -100,6 +100,28 @@ def test_first_order_check_kernel_matches_torch(dtype):
         assert rel_err(a, b) < tol
 
 
+@pytest.mark.parametrize("dtype", [torch.float64, torch.float32])
+def test_first_order_check_kernel_matches_torch_with_slack(dtype):
+    """Soft obstacle rows: the slack-stationarity term |gamma xi + y_g| of the
+    reference (turbompc_solver.py:1207-1212) in both checks.  The slack is
+    shifted off the ADMM fixed point so that this term sets the error."""
+    from turbompc_amd.problems import configs
+
+    prob = configs.config4(B=6, seed=4, use_slack_variables=True, slack_penalization_weight=30.0).to("cuda", dtype)
+    solver = TurboMPCSolver(prob, _params(2, 10))
+    sol = solver.solve(solver.initial_guess())
+    qp = prob.build_qp(sol.states, sol.controls)
+    slack = sol.slack + 0.05
+    args = (qp, sol.states, sol.controls, slack, sol.admm_state)
+    ck, ek, ik, gk = solver._first_order_check(*args)
+    ct, et, it_, gt = solver._first_order_check_torch(*args)
+    tol = 1e-12 if dtype == torch.float64 else 1e-5
+    for a, b in ((ck, ct), (ek, et), (ik, it_), (gk, gt)):
+        assert rel_err(a, b) < tol
+    # the slack term dominates the error here (30 * 0.05 = 1.5 on every row)
+    assert bool(torch.all(ct >= 1.0))
+
+
 @pytest.mark.parametrize("std", [False, True])
 @pytest.mark.parametrize("dtype", [torch.float64, torch.float32])
 @pytest.mark.parametrize("use_slack", [False, True])

@@ -151,6 +151,12 @@ int copy_state(hipStream_t s, const Dims& d, const tmpc_state* in, const tmpc_st
 }
 
 template <typename R>
+int launch_nonfinite_flags(hipStream_t s, const Dims& d, const StateDev<R>& st, uint32_t* iters) {
+  hipLaunchKernelGGL((nonfinite_flag_kernel<R>), dim3(d.B), dim3(kWave), 0, s, d, st, iters);
+  return launch_status();
+}
+
+template <typename R>
 int launch_factor_qp(hipStream_t s, const Dims& d, const QPDev<R>& q, const R* rho, R sigma,
                      R rho_f_factor, int32_t* ctl, R* thinv) {
   const size_t smem = factor_smem_bytes(d);
@@ -460,7 +466,7 @@ int admm_direct_impl(hipStream_t s, const tmpc_dims* dims, const tmpc_qp* qp,
     st = launch_status();
     if (st) return st;
   }
-  return TMPC_OK;
+  return launch_nonfinite_flags<R>(s, d, a.st, iters);
 }
 
 // ------------------------------------------------------- allocation-free ----
@@ -775,7 +781,7 @@ int admm_pcg_impl(hipStream_t s, const tmpc_dims* dims, const tmpc_qp* qp, const
     st = launch_status();
     if (st) return st;
   }
-  return TMPC_OK;
+  return launch_nonfinite_flags<R>(s, d, a.st, iters);
 }
 
 // ------------------------------------------------------------ quadrotor ----
@@ -920,6 +926,7 @@ const char* tmpc_status_string(int status) {
     case TMPC_EWORKSPACE: return "workspace too small";
     case TMPC_ELAUNCH: return "HIP launch failed";
     case TMPC_ESCRATCH: return "problem needs more than the allocation-free scratch";
+    case TMPC_ENONFINITE: return "non-finite values in the solution";
     default: return "unknown status";
   }
 }

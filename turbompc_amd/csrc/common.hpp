@@ -70,6 +70,28 @@ __global__ void fill_kernel(W* p, size_t n, W v) {
   if (i < n) p[i] = v;
 }
 
+// Sets bit 31 of iters[b] (TMPC_ITERS_NONFINITE) when problem b's state
+// holds a NaN or an infinity.  One wavefront per problem reads its arrays
+// (contiguous per problem) once; lane 0 updates the word with a plain store.
+template <typename R>
+__global__ __launch_bounds__(64) void nonfinite_flag_kernel(Dims d, StateDev<R> st, uint32_t* iters) {
+  const int b = blockIdx.x, lane = threadIdx.x;
+  bool bad = false;
+  auto scan = [&](const R* p, int cnt) {
+    if (p == nullptr || cnt == 0) return;
+    const R* q = p + (size_t)b * cnt;
+    for (int k = lane; k < cnt; k += kWave) bad |= !__builtin_isfinite(q[k]);
+  };
+  scan(st.x, d.T * d.n);
+  scan(st.z, d.T * d.m);
+  scan(st.y_g, d.T * d.m);
+  scan(st.xi, d.T * d.m);
+  scan(st.y_f0, d.n0);
+  scan(st.y_f, d.N * d.nx);
+  scan(st.rho, 1);
+  if (__ballot(bad) != 0 && lane == 0) iters[b] |= 0x80000000u;
+}
+
 // One workgroup is one wavefront; LDS traffic between lanes of the wave is
 // ordered by this barrier (a single-wave s_barrier is cheap on CDNA).
 __device__ __forceinline__ void wsync() { __syncthreads(); }

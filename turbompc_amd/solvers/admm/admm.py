@@ -52,6 +52,13 @@ class ADMMStats(NamedTuple):
 
     num_iter: torch.Tensor  # (B,)
     num_pcg_iters: Optional[torch.Tensor]  # (B, max_iter) for the PCG backend
+    nonfinite: Optional[torch.Tensor] = None  # (B,) bool: the output state holds NaN or infinity
+
+
+def _split_iters(iters: torch.Tensor):
+    """iters_out words -> (iteration counts, non-finite flags): bit 31 is
+    TMPC_ITERS_NONFINITE, which makes the int32 view negative."""
+    return iters & 0x7FFFFFFF, iters < 0
 
 
 def compute_S_Phiinv(qp_data: QPData, rho_f, sigma: float, rho_ineq=0.0) -> SchurComplementMatrices:
@@ -188,7 +195,8 @@ class ADMMSolver:
         x, z, yg, y0, yf, xi, rho = outs
         state = ADMMState(x_blocks=x, y_g=yg, y_f_0=y0, y_f_dyn=yf, z_g=z, xi_g=xi, rho_bar=rho)
         states, controls = unpack_x(x, self._zshape)
-        return (states, controls), ADMMStats(num_iter=iters, num_pcg_iters=pcg_iters), state
+        iters, bad = _split_iters(iters)
+        return (states, controls), ADMMStats(num_iter=iters, num_pcg_iters=pcg_iters, nonfinite=bad), state
 
     def sqp_step(self, qp_data: QPData, admm_state0: ADMMState, active: torch.Tensor, tol: float,
                  rho_bar: float = 1.0, alpha: float = 1.0, *, slack_weight=0.0,
@@ -222,7 +230,9 @@ class ADMMSolver:
         x, z, yg, y0, yf, xi, rho = outs
         state = ADMMState(x_blocks=x, y_g=yg, y_f_0=y0, y_f_dyn=yf, z_g=z, xi_g=xi, rho_bar=rho)
         states, controls = unpack_x(x, self._zshape)
-        return (states, controls), ADMMStats(num_iter=iters, num_pcg_iters=None), state, (conv, eq, iq, g), act
+        iters, bad = _split_iters(iters)
+        return ((states, controls), ADMMStats(num_iter=iters, num_pcg_iters=None, nonfinite=bad), state,
+                (conv, eq, iq, g), act)
 
     def initial_state(
         self,

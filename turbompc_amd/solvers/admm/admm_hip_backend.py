@@ -18,25 +18,36 @@ import torch
 from ... import _lib
 from ..qp_data import QPData
 
+# Workspaces of the calls that do not bring their own, one per (kind, device,
+# stream): calls issued on different streams never share one, and the calls of
+# one stream run in order.  A grown workspace replaces the old one only after
+# the stream has finished with it (the caching allocator's stream semantics).
 _WS_CACHE = {}
 
 
 def _ws(kind: str, nbytes: int, device: torch.device) -> torch.Tensor:
-    key = (kind, device)
+    stream = torch.cuda.current_stream(device)
+    key = (kind, device, stream.cuda_stream)
     t = _WS_CACHE.get(key)
     if t is None or t.numel() < nbytes:
-        t = _lib.workspace(nbytes, device)
+        with torch.cuda.stream(stream):
+            t = _lib.workspace(nbytes, device)
         _WS_CACHE[key] = t
     return t
 
 
 def qp_struct(qp: QPData, slack_weight: Optional[torch.Tensor]):
+    """Pointers of the QP blocks for the C ABI.  Every block must carry the
+    solve's dtype: the library reads the buffers as that type."""
     B, T, n, nx, n0, m = qp.dims
     keep = []
+    dt = qp.dtype
 
     def p(t):
         if t is None:
             return None
+        if t.dtype != dt:
+            raise TypeError(f"QP block of dtype {t.dtype} in a {dt} solve; convert the QP with QPData.to()")
         t = t.contiguous()
         keep.append(t)
         return _lib.ptr(t)

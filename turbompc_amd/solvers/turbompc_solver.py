@@ -160,6 +160,18 @@ class TurboMPCSolution(NamedTuple):
     solver_stats: Optional[SolverStats] = None
     dual_backward_guess: Optional[torch.Tensor] = None
     kkt_state: Optional[KKTState] = None
+    nonfinite: Optional[torch.Tensor] = None  # (B,) bool: the returned iterate or ADMM state holds NaN or infinity
+
+
+def _nonfinite(*tensors) -> torch.Tensor:
+    """(B,) True where any of the batched tensors holds a NaN or an infinity."""
+    bad = None
+    for t in tensors:
+        if t is None or t.numel() == 0:
+            continue
+        b = ~torch.isfinite(t).reshape(t.shape[0], -1).all(dim=1)
+        bad = b if bad is None else bad | b
+    return bad
 
 
 def identify_active_inequalities(g, l, u, eps_abs: float, eps_rel: float):
@@ -394,6 +406,10 @@ class TurboMPCSolver:
         else:
             ineq_err = torch.zeros_like(stat_err)
         conv = torch.maximum(stat_err, torch.maximum(eq_err, ineq_err))
+        if qp.ineq.use_slack_variables and m:
+            # slack stationarity |gamma xi + y_g| (turbompc_solver.py:1207-1212)
+            slack_err = inf_norm(qp.ineq.slack_penalization_weight * slacks + admm_state.y_g)
+            conv = torch.maximum(conv, slack_err)
         return conv, eq_err, ineq_err, g
 
     def _build_kkt_state(self, states, controls, admm_state: ADMMState, g, l, u) -> KKTState:
@@ -497,6 +513,8 @@ class TurboMPCSolver:
             states=states, controls=controls, slack=admm_state.xi_g, status=self.STATUS_SUCCESS, num_iter=num_iter,
             convergence_error=conv, admm_iters=admm_iters, linesearch_alphas=None, admm_state=admm_state,
             solver_stats=SolverStats(admm_iters, hist[0].t(), hist[1].t(), hist[2].t()), kkt_state=kkt,
+            # the last step scanned every problem's state (stopped ones keep theirs)
+            nonfinite=stats.nonfinite,
         )
 
     def _solve_impl_masked(self, program, states, controls, admm_state0: Optional[ADMMState] = None) -> TurboMPCSolution:
@@ -595,6 +613,7 @@ class TurboMPCSolver:
             states=states, controls=controls, slack=admm_state.xi_g, status=self.STATUS_SUCCESS, num_iter=num_iter,
             convergence_error=conv, admm_iters=admm_iters, linesearch_alphas=ls_alphas, admm_state=admm_state,
             solver_stats=SolverStats(admm_iters, eq_v, in_v, conv_h), kkt_state=kkt,
+            nonfinite=_nonfinite(states, controls, *admm_state),
         )
 
 
