@@ -7,20 +7,31 @@ linearization + ADMM (block-tridiagonal factorization + 20 fused iterations)
 Inputs are resident on the GPU before timing starts.
 
 Prints one JSON line with the metric, a roofline entry for the dominant kernel
-(admm_stream_kernel: 20 ADMM iterations of the batch per launch, timed live
-with HIP events the library records around every launch on the solve stream;
-the whole QP solve is reported beside it) and the CPU baseline (the liboracle
-restatement of the reference CPU path on a bounded sample of the same workload).
+(timed live with HIP events the library records around every iteration phase
+on the solve stream; the whole QP solve is reported beside it) and the CPU
+baseline (the oracle's restatement of the reference CPU path, compiled with
+-march=native on this host, on a bounded sample of the same workload, on all
+cores and on one).
 
---workload config4 measures the obstacle-avoidance workload instead (B=16384,
-8 SQP x 30 ADMM, fp32), a secondary line; the default is the metric's config 3.
+Secondary workloads (one line each; the default is the metric's config 3):
+  --workload config4  obstacle avoidance, B=16384, 8 SQP x 30 ADMM, fp32
+  --workload config5  spacecraft rendezvous, B=2048, fp64: 200 ADMM iterations
+                      and the implicit-differentiation backward pass (gradients
+                      of sum |x_N|^2 with respect to Q, R and x0)
+  --workload config2  random stable LTI, B=1024, 100 ADMM iterations on the PCG
+                      Schur solve (tolerance 1e-6, at most 50 PCG iterations),
+                      --dtype f32 or f64
+Every workload follows the fixed-iteration protocol: rho is not adapted and
+the convergence tests cannot stop a solve early.
 """
 from __future__ import annotations
 
 import argparse
+import copy
 import json
 import os
 import sys
+import tempfile
 import time
 from pathlib import Path
 
@@ -43,9 +54,24 @@ def bytes_per_qp(T, n, nx, n0, m, K, w, m_g=0):
     return w * (F + K * It), w * F, w * It
 
 
-def make_solver(prob, n_sqp, admm_iters):
-    from turbompc_amd.solvers.turbompc_solver import DEFAULT_SOLVER_PARAMS, TurboMPCSolver
-    import copy
+def bytes_pcg(T, n, nx, n0, m, K, pcg_iters, w, m_g=0):
+    """The PCG variant of the model: F reads D, E and A_minus and writes S and
+    Phiinv (2 (3T - 2) n^2 words); each ADMM iteration moves I of the direct
+    model without its factor read, plus 2 (3T - 2) n^2 + 9 T n words per
+    PCG iteration actually run (S and Phiinv streamed, the CG vectors).
+    Returns (bytes of the solve, bytes of its iteration phase)."""
+    N = T - 1
+    sp = 2 * (3 * T - 2) * n * n
+    F = T * n * n + N * n * n + N * nx * n + T * m_g * n + sp
+    It = N * nx * n + T * m_g * n + T * n + (N * nx + n0) + 2 * T * m \
+        + 2 * (T * n + (N * nx + n0) + T * m + T * m)
+    per_pcg = sp + 9 * T * n
+    phase = K * It + pcg_iters * per_pcg
+    return w * (F + phase), w * phase
+
+
+def sqp_params(n_sqp, admm_iters):
+    from turbompc_amd.solvers.turbompc_solver import DEFAULT_SOLVER_PARAMS
 
     params = copy.deepcopy(DEFAULT_SOLVER_PARAMS)
     params["num_sqp_iteration_max"] = n_sqp
@@ -53,10 +79,21 @@ def make_solver(prob, n_sqp, admm_iters):
     params["admm"]["max_iter"] = admm_iters
     params["admm"]["adapt_rho_every"] = 0  # fixed-iteration protocol
     params["admm"]["relaxation_parameter"] = 1.0
-    return TurboMPCSolver(prob, params, forward_backend="admm_hip_direct", backward_backend="direct_hip_kkt")
+    return params
 
 
-def cpu_baseline(B_gpu, n_sqp, admm_iters, seed, budget_s, workload="config3"):
+def make_solver(prob, n_sqp, admm_iters):
+    from turbompc_amd.solvers.turbompc_solver import TurboMPCSolver
+
+    return TurboMPCSolver(prob, sqp_params(n_sqp, admm_iters), forward_backend="admm_hip_direct",
+                          backward_backend="direct_hip_kkt")
+
+
+# ------------------------------------------------------------ CPU baseline ----
+def cpu_baseline(workload, B_gpu, args):
+    """The oracle (the restated reference CPU path) on a bounded sample of the
+    workload, built with -march=native on this host: all cores (value), then
+    one thread (single_thread)."""
     import numpy as np
     import torch
 
@@ -66,52 +103,115 @@ def cpu_baseline(B_gpu, n_sqp, admm_iters, seed, budget_s, workload="config3"):
     from turbompc_amd.problems.ocp import LinearOCP
     from turbompc_amd.problems.quadrotor import make_quadrotor_config
 
+    build = "g++ -O3 -march=native (oracle/Makefile native, built on this host)"
+    try:
+        oracle.use_native_build(tempfile.mkdtemp(prefix="tmpc_oracle_native_"))
+    except Exception as e:  # keep the portable build
+        build = f"portable x86-64-v2 build (native build failed: {type(e).__name__})"
     cores = len(os.sched_getaffinity(0))
+    n_sqp, K, seed = args.sqp, args.admm_iters, args.seed
 
-    def run_config4(Bs):
-        prob = configs.config4(B=Bs, seed=seed)
+    def cfg(**kw):
+        base = dict(max_iter=K, check_every=K + 1, adapt_rho_every=0, sigma=1e-6, eps_abs=1e-30, eps_rel=1e-30,
+                    rho_f_factor=1000.0, alpha=1.0)
+        base.update(kw)
+        return oracle.OracleCfg(**base)
+
+    def static_of(prob):
         D, E, q = (t.numpy() for t in prob.cost_blocks())
         A0, c0 = (t.numpy() for t in prob.initial_equality())
         G, l, u = (t.numpy() for t in LinearOCP.inequality_blocks(prob))
-        static = dict(D=D, E=E, q=q, A0=A0, c0=c0, A_plus=prob.a_plus().numpy(), G=G, l=l, u=u)
-        xg, ug = (t.numpy() for t in prob.initial_guess())
-        Am, c = (t.numpy() for t in prob.dynamics_blocks(*prob.initial_guess()))
-        cfg = oracle.OracleCfg(max_iter=admm_iters, check_every=50, adapt_rho_every=0, sigma=1e-6, eps_abs=1e-9,
-                               eps_rel=1e-9, rho_f_factor=1000.0, alpha=1.0)
-        t0 = time.perf_counter()
-        obstacle_sqp(static, xg, ug, A_minus=Am, c=c, centers=prob.centers.numpy(), radii=prob.radii.numpy(), dim=3,
-                     cfg=cfg, rho0=0.1, n_sqp=n_sqp, dtype=np.float32, nthreads=cores)
-        return time.perf_counter() - t0
+        return dict(D=D, E=E, q=q, A0=A0, c0=c0, A_plus=prob.a_plus().numpy(), G=G, l=l, u=u)
 
-    def run(Bs):
+    def run(Bs, threads):
         if workload == "config4":
-            return run_config4(Bs)
-        prob = make_quadrotor_config(B=Bs, seed=seed, dtype=torch.float64, device="cpu")
-        D, E, q = (t.numpy() for t in prob.cost_blocks())
-        A0, c0 = (t.numpy() for t in prob.initial_equality())
-        G, l, u = (t.numpy() for t in prob.inequality_blocks())
-        static = dict(D=D, E=E, q=q, A0=A0, c0=c0, A_plus=prob.a_plus().numpy(), G=G, l=l, u=u)
-        xg, ug = (t.numpy() for t in prob.initial_guess())
-        cfg = oracle.OracleCfg(max_iter=admm_iters, check_every=25, adapt_rho_every=0, sigma=1e-6, eps_abs=1e-9,
-                               eps_rel=1e-9, rho_f_factor=1000.0, alpha=1.0)
+            prob = configs.config4(B=Bs, seed=seed)
+            xg, ug = (t.numpy() for t in prob.initial_guess())
+            Am, c = (t.numpy() for t in prob.dynamics_blocks(*prob.initial_guess()))
+            t0 = time.perf_counter()
+            obstacle_sqp(static_of(prob), xg, ug, A_minus=Am, c=c, centers=prob.centers.numpy(),
+                         radii=prob.radii.numpy(), dim=3, cfg=cfg(), rho0=0.1, n_sqp=n_sqp, dtype=np.float32,
+                         nthreads=threads)
+            return time.perf_counter() - t0
+        if workload == "config3":
+            prob = make_quadrotor_config(B=Bs, seed=seed, dtype=torch.float64, device="cpu")
+            xg, ug = (t.numpy() for t in prob.initial_guess())
+            t0 = time.perf_counter()
+            quadrotor_sqp(static_of(prob), xg, ug, dt=prob.dt, params=prob.params, cfg=cfg(), rho0=0.1,
+                          n_sqp=n_sqp, dtype=np.float32, nthreads=threads)
+            return time.perf_counter() - t0
+        if workload == "config2":
+            prob = configs.config2(B=Bs, seed=seed)
+            qp = prob.build_qp(*prob.initial_guess())
+            st0 = _zero_state_np(qp)
+            dt = np.float64 if args.dtype == "f64" else np.float32
+            t0 = time.perf_counter()
+            oracle.admm_solve(qp, st0, cfg(pcg_eps=1e-6, pcg_max_iter=50), schur="pcg", dtype=dt, nthreads=threads)
+            return time.perf_counter() - t0
+        # config5: forward ADMM, then the dense adjoint KKT of the reference's
+        # pure-JAX backward pass (backward_kkt_jax.py:177-198)
+        prob = configs.config5(B=Bs, seed=seed)
+        qp = prob.build_qp(*prob.initial_guess())
         t0 = time.perf_counter()
-        quadrotor_sqp(static, xg, ug, dt=prob.dt, params=prob.params, cfg=cfg, rho0=0.1, n_sqp=n_sqp,
-                      dtype=np.float32, nthreads=cores)
+        st, _, _ = oracle.admm_solve(qp, _zero_state_np(qp), cfg(), nthreads=threads)
+        oracle.adjoint_kkt(_adjoint_qp_np(qp, st, prob.num_state_variables), nthreads=threads)
         return time.perf_counter() - t0
 
-    t_cal = run(64)
-    Bs = int(min(B_gpu, max(64, budget_s / max(t_cal, 1e-6) * 64)))
-    dt = run(Bs) if Bs > 64 else t_cal
-    if workload == "config4":
-        sample = (f"{Bs} obstacle problems (config 4 shapes, seed {seed}), {n_sqp} SQP x {admm_iters} ADMM, "
-                  f"fp32 ADMM (liboracle, OpenMP over the batch) + numpy obstacle rows, {dt:.2f} s wall")
-    else:
-        sample = (f"{Bs} quadrotor problems (config 3 shapes, seed {seed}), {n_sqp} SQP x {admm_iters} ADMM, "
-                  f"fp32 ADMM (liboracle, OpenMP over the batch) + fp64 complex-step RK4 linearization, "
-                  f"{dt:.2f} s wall")
-    return {"value": Bs / dt, "unit": "MPC solves/s", "cores": cores, "kind": "port", "sample": sample}
+    def sample(threads, budget):
+        t_cal = run(8, threads)
+        Bs = int(min(B_gpu, max(8, budget / max(t_cal, 1e-6) * 8)))
+        dt = run(Bs, threads) if Bs > 8 else t_cal
+        return Bs, dt
+
+    Bs, dt = sample(cores, args.cpu_budget)
+    B1, dt1 = sample(1, args.cpu_budget / 3)
+    what = {
+        "config3": f"quadrotor problems (config 3 shapes), {n_sqp} SQP x {K} ADMM, fp32 ADMM + fp64 complex-step "
+                   "RK4 linearization",
+        "config4": f"obstacle problems (config 4 shapes), {n_sqp} SQP x {K} ADMM, fp32 ADMM + numpy obstacle rows",
+        "config2": f"LTI problems (config 2 shapes), {K} ADMM iterations on PCG (tol 1e-6, <= 50), {args.dtype}",
+        "config5": f"spacecraft problems (config 5 shapes), {K} ADMM iterations + dense adjoint KKT, fp64",
+    }[workload]
+    return {
+        "value": Bs / dt, "unit": "MPC solves/s", "cores": cores, "kind": "port",
+        "sample": f"{Bs} {what} (seed {seed}), OpenMP over the batch on {cores} threads, {dt:.2f} s wall; {build}",
+        "single_thread": {"value": B1 / dt1, "sample": f"{B1} problems on 1 thread, {dt1:.2f} s wall"},
+    }
 
 
+def _zero_state_np(qp):
+    import numpy as np
+
+    import oracle
+
+    B, T, n, nx, n0, m = qp.dims
+    f = lambda t: np.asarray(t, dtype=np.float64)  # noqa: E731
+    z = np.clip(np.zeros((B, T, m)), f(qp.ineq.l), f(qp.ineq.u))
+    return oracle.OracleState(np.zeros((B, T, n)), np.zeros((B, T, m)), np.zeros((B, n0)), np.zeros((B, T - 1, nx)),
+                              z, np.zeros((B, T, m)), np.full((B,), 0.1))
+
+
+def _adjoint_qp_np(qp, st, nx):
+    """The adjoint QP of the loss sum |x_N|^2 at an ADMM solution, for the CPU
+    baseline: q = -dL/dz, homogeneous constraints, the active rows of G signed
+    by the dual sign (turbompc_solver.py:544-618, :1387-1439)."""
+    from types import SimpleNamespace as NS
+
+    import numpy as np
+
+    f = lambda t: np.asarray(t, dtype=np.float64)  # noqa: E731
+    x = st.x_blocks
+    dl = np.zeros_like(x)
+    dl[:, -1, :nx] = 2 * x[:, -1, :nx]
+    sign = (st.y_g < -1e-9).astype(np.float64) - (st.y_g > 1e-9).astype(np.float64)
+    return NS(cost=NS(D=f(qp.cost.D), E=f(qp.cost.E), q=-dl),
+              eq=NS(A0=f(qp.eq.A0), A_minus=f(qp.eq.A_minus), A_plus=f(qp.eq.A_plus),
+                    c0=np.zeros_like(f(qp.eq.c0)), c=np.zeros_like(f(qp.eq.c))),
+              ineq=NS(G=f(qp.ineq.G) * sign[..., None], l=np.zeros_like(st.y_g), u=np.zeros_like(st.y_g),
+                      slack_penalization_weight=0.0, use_slack_variables=False))
+
+
+# ----------------------------------------------------------------- helpers ----
 TRAFFIC_FILE = ROOT / "profiles" / "admm_stream_kernel_config3_pmc.txt"
 
 
@@ -127,17 +227,285 @@ def measured_traffic():
     return None
 
 
+class SolveTimer:
+    """Times every ADMMSolver.solve / sqp_step call twice with HIP events on the
+    solve stream: the whole QP solve, and (through the library's hook) the
+    iteration phase alone."""
+
+    def __init__(self, dev):
+        import torch
+
+        from turbompc_amd import _lib
+        from turbompc_amd.solvers.admm import admm as admm_mod
+
+        self.mod, self.dev, self.torch = admm_mod, dev, torch
+        self.solves = []
+        self.iters = _lib.IterationTimer()
+        self.orig = (admm_mod.ADMMSolver.solve, admm_mod.ADMMSolver.sqp_step)
+
+    def __enter__(self):
+        torch = self.torch
+
+        def timed(fn):
+            def wrapper(solver, *a, **kw):
+                s = torch.cuda.current_stream(self.dev)
+                e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+                e0.record(s)
+                with self.iters:
+                    out = fn(solver, *a, **kw)
+                e1.record(s)
+                self.solves.append((e0, e1))
+                return out
+            return wrapper
+
+        self.mod.ADMMSolver.solve = timed(self.orig[0])
+        self.mod.ADMMSolver.sqp_step = timed(self.orig[1])
+        return self
+
+    def __exit__(self, *exc):
+        self.mod.ADMMSolver.solve, self.mod.ADMMSolver.sqp_step = self.orig
+        return False
+
+    def clear(self):
+        self.solves.clear()
+        self.iters.clear()
+
+    def averages_s(self):
+        solve_ms = [a.elapsed_time(b) for a, b in self.solves]
+        iter_ms = self.iters.results()
+        return sum(solve_ms) / len(solve_ms) / 1e3, sum(iter_ms) / len(iter_ms) / 1e3
+
+
+def timed_steps(step, steps, warmup, timer):
+    import torch
+
+    for _ in range(warmup):
+        step()
+    torch.cuda.synchronize()
+    timer.clear()
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        out = step()
+    torch.cuda.synchronize()
+    return time.perf_counter() - t0, out
+
+
+def base_line(metric, value, args, elapsed, dtype, data, config):
+    return {
+        "metric": metric, "value": value, "unit": "MPC solves/s", "n_gpus": 1, "steps": args.steps,
+        "warmup": args.warmup, "ms_per_step": elapsed / args.steps * 1e3, "higher_is_better": True,
+        "scaling": "weak", "vs_baseline": None, "dtype": dtype, "data": data, "config": config,
+    }
+
+
+def roofline(achieved, traffic, kernel, bytes_per_launch, avg_ms, **extra):
+    r = {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": achieved / HBM_PEAK_GBS,
+         "traffic": traffic, "kernel": kernel, "algorithmic_bytes_per_launch": bytes_per_launch,
+         "avg_launch_ms": avg_ms}
+    r.update(extra)
+    return r
+
+
+# --------------------------------------------------------------- workloads ----
+def run_sqp_workload(args, dev):
+    """config3 (the metric) and config4: the SQP solve from the same guess."""
+    import torch
+
+    from turbompc_amd.problems import configs
+    from turbompc_amd.problems.quadrotor import make_quadrotor_config
+
+    c4 = args.workload == "config4"
+    B = args.batch
+    if c4:
+        prob = configs.config4(B=B, seed=args.seed).to(dev, torch.float32)
+    else:
+        prob = make_quadrotor_config(B=B, seed=args.seed, dtype=torch.float32, device=dev)
+    solver = make_solver(prob, args.sqp, args.admm_iters)
+    guess = solver.initial_guess()
+    with SolveTimer(dev) as timer:
+        elapsed, sol = timed_steps(lambda: solver.solve(guess), args.steps, args.warmup, timer)
+    solve_avg_s, iter_avg_s = timer.averages_s()
+    copy_calibration(args, dev)
+
+    T = prob.horizon + 1
+    if c4:  # n = 9, nx = n0 = 6, 3 box rows and 8 obstacle rows (data-carrying)
+        per_qp, F, It = bytes_per_qp(T, 9, 6, 6, 11, args.admm_iters, 4, m_g=8)
+        workload = (f"config 4: obstacle avoidance, double integrator nx=6 nu=3 N={prob.horizon}, 8 spheres "
+                    f"(linearized rows), |u| <= 3, {args.sqp} SQP x {args.admm_iters} ADMM, ADMM state carried "
+                    f"across SQP iterations, direct block-tridiagonal KKT backend")
+        data = "synthetic (seeded obstacle fields: 8 spheres, start and goal on opposite faces of [-4,4]^3)"
+    else:  # n = 17, nx = n0 = 13, 4 box rows
+        per_qp, F, It = bytes_per_qp(T, 17, 13, 13, 4, args.admm_iters, 4)
+        workload = ("config 3: quadrotor nonlinear SQP, nx=13 nu=4 N=40, RK4 dt=0.02, 5 SQP x 20 ADMM, "
+                    "direct block-tridiagonal KKT backend")
+        data = "synthetic (seeded quadrotor fleet: random goals, perturbed hover starts)"
+    iter_bytes = B * args.admm_iters * It  # algorithmic bytes of one iteration-kernel launch
+    achieved = iter_bytes / iter_avg_s / 1e9
+    qp_achieved = per_qp * B / solve_avg_s / 1e9
+    finite = bool(torch.isfinite(sol.states).all() and torch.isfinite(sol.controls).all())
+    line = base_line(f"MPC solves/sec at B={B}{', config 4' if c4 else ''} (1 MI355X)", B * args.steps / elapsed,
+                     args, elapsed, "f32", data, {
+                         "workload": workload, "batch": B, "horizon": prob.horizon, "sqp_iterations": args.sqp,
+                         "admm_iterations": args.admm_iters, "parallelism": "single GPU, batch-parallel",
+                         "solution_finite": finite, "kernel_only_solves_per_s": B / (args.sqp * solve_avg_s)})
+    line["roofline"] = roofline(
+        achieved, None if c4 else measured_traffic(),
+        f"admm_stream_kernel (one launch = {args.admm_iters} ADMM iterations of the batch)", iter_bytes,
+        iter_avg_s * 1e3,
+        qp_solve={"kernels": "stage_pack + factor_std + admm_stream + stage_unpack", "algorithmic_bytes": per_qp * B,
+                  "avg_ms": solve_avg_s * 1e3, "achieved": qp_achieved, "frac": qp_achieved / HBM_PEAK_GBS})
+    return line
+
+
+def run_config5(args, dev):
+    """Forward ADMM (K iterations) and the backward pass of sum |x_N|^2."""
+    import torch
+
+    from turbompc_amd.problems import configs
+    from turbompc_amd.solvers.turbompc_solver import TurboMPCSolver
+
+    B, K = args.batch, args.admm_iters
+    prob = configs.config5(B=B, seed=args.seed).to(dev, torch.float64)
+    solver = TurboMPCSolver(prob, sqp_params(1, K), forward_backend="admm_hip_direct",
+                            backward_backend="direct_hip_kkt")
+    fsolve = solver.get_differentiable_solve_function()
+    guess = solver.initial_guess()
+    keys = ("weights_penalization_reference_state_trajectory", "weights_penalization_control_squared")
+    x0 = prob.x0.clone().requires_grad_(True)
+    w = {k: v.clone().requires_grad_(True) for k, v in prob.weights_dict().items()}
+    bwd_events = []
+    orig_vjp = TurboMPCSolver.solve_vjp
+
+    def timed_vjp(self, *a, **kw):
+        s = torch.cuda.current_stream(dev)
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record(s)
+        out = orig_vjp(self, *a, **kw)
+        e1.record(s)
+        bwd_events.append((e0, e1))
+        return out
+
+    def step():
+        sol = fsolve(guess, {"initial_state": x0}, w)
+        L = (sol.states[:, -1] ** 2).sum()
+        return sol, torch.autograd.grad(L, [x0] + [w[k] for k in keys])
+
+    TurboMPCSolver.solve_vjp = timed_vjp
+    try:
+        with SolveTimer(dev) as timer:
+            bwd_events.clear()
+            elapsed, (sol, grads) = timed_steps(step, args.steps, args.warmup, timer)
+    finally:
+        TurboMPCSolver.solve_vjp = orig_vjp
+    solve_avg_s, iter_avg_s = timer.averages_s()
+    bwd = [a.elapsed_time(b) for a, b in bwd_events[-args.steps:]]
+    bwd_avg_ms = sum(bwd) / len(bwd)
+    copy_calibration(args, dev)
+    T = prob.horizon + 1
+    per_qp, F, It = bytes_per_qp(T, 9, 6, 6, 3, K, 8)
+    iter_bytes = B * K * It
+    achieved = iter_bytes / iter_avg_s / 1e9
+    finite = bool(all(torch.isfinite(g).all() for g in grads) and torch.isfinite(sol.states).all())
+    line = base_line(f"MPC solves/sec at B={B}, config 5 forward + gradient (1 MI355X)", B * args.steps / elapsed,
+                     args, elapsed, "f64",
+                     "synthetic (seeded Clohessy-Wiltshire rendezvous: x0 ~ N(0, diag(100^2 I3, 0.1^2 I3)), "
+                     "Q, R ~ U as learnable weights)", {
+                         "workload": f"config 5: spacecraft rendezvous, Clohessy-Wiltshire nx=6 nu=3 N=100 dt=10 s "
+                                     f"(exact ZOH), |u| <= 0.01, {K} ADMM iterations (direct block-tridiagonal "
+                                     f"KKT), then the adjoint KKT solve and gradients of sum |x_N|^2 w.r.t. x0, Q "
+                                     f"and R (direct_hip_kkt)",
+                         "batch": B, "horizon": prob.horizon, "admm_iterations": K,
+                         "parallelism": "single GPU, batch-parallel", "solution_finite": finite,
+                         "forward_qp_solve_ms": solve_avg_s * 1e3, "backward_ms": bwd_avg_ms})
+    line["roofline"] = roofline(
+        achieved, None, f"admm_stream_kernel, fp64 (one launch = {K} ADMM iterations of the batch)", iter_bytes,
+        iter_avg_s * 1e3,
+        qp_solve={"kernels": "stage_pack + factor_std + admm_stream + stage_unpack", "algorithmic_bytes": per_qp * B,
+                  "avg_ms": solve_avg_s * 1e3, "achieved": per_qp * B / solve_avg_s / 1e9,
+                  "frac": per_qp * B / solve_avg_s / 1e9 / HBM_PEAK_GBS})
+    return line
+
+
+def run_config2(args, dev):
+    """One QP solve of K ADMM iterations on the PCG Schur solve."""
+    import torch
+
+    from turbompc_amd.problems import configs
+    from turbompc_amd.solvers.admm.admm import ADMMSolver
+    from turbompc_amd.solvers.linear_systems_solvers.backends import AdmmBackend
+    from turbompc_amd.solvers.qp_utils import ZShape
+
+    B, K = args.batch, args.admm_iters
+    dt = torch.float64 if args.dtype == "f64" else torch.float32
+    prob = configs.config2(B=B, seed=args.seed).to(dev, dt)
+    qp = prob.build_qp(*prob.initial_guess())
+    _, T, n, nx, n0, m = qp.dims
+    solver = ADMMSolver(ZShape(T - 1, nx, n - nx), {"max_iter": 50, "tol_epsilon": 1e-6}, sigma=1e-6, max_iter=K,
+                        eps_abs=1e-30, eps_rel=1e-30, check_termination_every=K + 1, adapt_rho_every=0,
+                        rho_f_factor=1000.0, admm_backend=AdmmBackend.HIP_PCG, std_dynamics=True)
+    st0 = solver.initial_state(qp, rho_bar=0.1)
+    with SolveTimer(dev) as timer:
+        elapsed, (_, stats, st) = timed_steps(lambda: solver.solve(qp, st0, alpha=1.0), args.steps, args.warmup,
+                                              timer)
+    solve_avg_s, iter_avg_s = timer.averages_s()
+    copy_calibration(args, dev)
+    w = 8 if dt == torch.float64 else 4
+    pcg_total = int(stats.num_pcg_iters.sum())  # PCG iterations of the batch in one solve
+    per_solve, phase = bytes_pcg(T, n, nx, n0, m, K, 0, w)
+    _, pcg_bytes = bytes_pcg(T, n, nx, n0, m, 0, 1, w)
+    phase_bytes = B * phase + pcg_total * pcg_bytes
+    achieved = phase_bytes / iter_avg_s / 1e9
+    finite = bool(torch.isfinite(st.x_blocks).all())
+    line = base_line(f"MPC solves/sec at B={B}, config 2 PCG {args.dtype} (1 MI355X)", B * args.steps / elapsed,
+                     args, elapsed, args.dtype,
+                     "synthetic (seeded random stable LTI systems, spectral radius <= 1.05)", {
+                         "workload": f"config 2: random stable LTI nx=12 nu=4 N=50, |x| <= 5, |u| <= 1, {K} ADMM "
+                                     f"iterations on the block-tridiagonal Schur PCG (block-Jacobi preconditioner, "
+                                     f"tol 1e-6, at most 50 iterations), one QP",
+                         "batch": B, "horizon": T - 1, "admm_iterations": K,
+                         "mean_pcg_iterations": pcg_total / (B * K),
+                         "parallelism": "single GPU, batch-parallel", "solution_finite": finite})
+    line["roofline"] = roofline(
+        achieved, None, f"admm_pcg_chunk_kernel (one launch = {K} ADMM iterations with their PCG solves)",
+        phase_bytes, iter_avg_s * 1e3,
+        qp_solve={"kernels": "schur_build + admm_pcg_chunk", "algorithmic_bytes": B * (per_solve - phase) + phase_bytes,
+                  "avg_ms": solve_avg_s * 1e3})
+    return line
+
+
+def copy_calibration(args, dev):
+    """A device-to-device copy of known size after the timed steps, for
+    calibrating rocprofv3's FETCH_SIZE / WRITE_SIZE against known bytes."""
+    if not args.copy_calibration:
+        return
+    import torch
+
+    x = torch.ones(args.copy_calibration * (1 << 18), dtype=torch.float32, device=dev)
+    y = torch.empty_like(x)
+    y.copy_(x)
+    torch.cuda.synchronize()
+
+
+DEFAULTS = {  # batch, SQP iterations, ADMM iterations
+    "config3": (4096, 5, 20),
+    "config4": (16384, 8, 30),
+    "config5": (2048, 1, 200),
+    "config2": (1024, 1, 100),
+}
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
-    ap.add_argument("--workload", choices=("config3", "config4"), default="config3",
-                    help="config3 (the metric's workload) or the obstacle workload config4 (a secondary line)")
-    ap.add_argument("--batch", type=int, default=None, help="default 4096 (config3), 16384 (config4)")
+    ap.add_argument("--workload", choices=tuple(DEFAULTS), default="config3",
+                    help="config3 (the metric's workload) or a secondary line: config4, config5, config2")
+    ap.add_argument("--batch", type=int, default=None)
     ap.add_argument("--seed", type=int, default=0)
-    ap.add_argument("--sqp", type=int, default=None, help="default 5 (config3), 8 (config4)")
-    ap.add_argument("--admm-iters", type=int, default=None, help="default 20 (config3), 30 (config4)")
+    ap.add_argument("--sqp", type=int, default=None, help="SQP iterations (config3 / config4)")
+    ap.add_argument("--admm-iters", type=int, default=None)
+    ap.add_argument("--dtype", choices=("f32", "f64"), default="f32", help="config2 only")
     ap.add_argument("--cpu-baseline", type=int, default=1)
     ap.add_argument("--cpu-budget", type=float, default=15.0, help="seconds of CPU work for the baseline sample")
     ap.add_argument("--copy-calibration", type=int, default=0,
@@ -148,138 +516,23 @@ def main():
         print("bench.py: this build measures one GPU only (the batch of independent MPC problems would shard "
               "across GPUs with no communication in the forward solve); run with --gpus 1", file=sys.stderr)
         sys.exit(2)
+    B, n_sqp, K = DEFAULTS[args.workload]
+    args.batch = args.batch or B
+    args.sqp = args.sqp or n_sqp
+    args.admm_iters = args.admm_iters or K
 
     import torch
 
-    from turbompc_amd import _lib
-    from turbompc_amd.problems import configs
-    from turbompc_amd.problems.quadrotor import make_quadrotor_config
-    from turbompc_amd.solvers.admm import admm as admm_mod
-
-    c4 = args.workload == "config4"
-    args.batch = args.batch or (16384 if c4 else 4096)
-    args.sqp = args.sqp or (8 if c4 else 5)
-    args.admm_iters = args.admm_iters or (30 if c4 else 20)
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
-    B = args.batch
-    if c4:
-        prob = configs.config4(B=B, seed=args.seed).to(dev, torch.float32)
+    if args.workload in ("config3", "config4"):
+        line = run_sqp_workload(args, dev)
+    elif args.workload == "config5":
+        line = run_config5(args, dev)
     else:
-        prob = make_quadrotor_config(B=B, seed=args.seed, dtype=torch.float32, device=dev)
-    solver = make_solver(prob, args.sqp, args.admm_iters)
-    guess = solver.initial_guess()
-
-    # every ADMM solve (the first SQP iteration's solve and every later SQP
-    # step) is timed twice with HIP events on the stream the library launches
-    # on: the whole QP solve (pack or record rewrite + factorization +
-    # iterations + unpack) and, through the library's hook, the iteration phase
-    # alone (the single admm_stream_kernel launch of a fixed-iteration solve)
-    solve_events = []
-    iter_timer = _lib.IterationTimer()
-    orig, orig_step = admm_mod.ADMMSolver.solve, admm_mod.ADMMSolver.sqp_step
-
-    def timed(fn):
-        def wrapper(self, *a, **kw):
-            s = torch.cuda.current_stream(dev)
-            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-            e0.record(s)
-            with iter_timer:
-                out = fn(self, *a, **kw)
-            e1.record(s)
-            solve_events.append((e0, e1))
-            return out
-        return wrapper
-
-    admm_mod.ADMMSolver.solve = timed(orig)
-    admm_mod.ADMMSolver.sqp_step = timed(orig_step)
-    for _ in range(args.warmup):
-        solver.solve(guess)
-    torch.cuda.synchronize()
-    solve_events.clear()
-    iter_timer.clear()
-    t0 = time.perf_counter()
-    for _ in range(args.steps):
-        sol = solver.solve(guess)
-    torch.cuda.synchronize()
-    elapsed = time.perf_counter() - t0
-    admm_mod.ADMMSolver.solve, admm_mod.ADMMSolver.sqp_step = orig, orig_step
-    solve_ms = [a.elapsed_time(b) for a, b in solve_events]
-    iter_ms = iter_timer.results()
-    solve_avg_s = sum(solve_ms) / len(solve_ms) / 1e3
-    iter_avg_s = sum(iter_ms) / len(iter_ms) / 1e3
-    if args.copy_calibration:
-        x = torch.ones(args.copy_calibration * (1 << 18), dtype=torch.float32, device=dev)
-        y = torch.empty_like(x)
-        y.copy_(x)
-        torch.cuda.synchronize()
-
-    T = prob.horizon + 1
-    if c4:  # n = 9, nx = n0 = 6, 3 box rows and 8 obstacle rows (data-carrying)
-        per_qp, F, It = bytes_per_qp(T, 9, 6, 6, 11, args.admm_iters, 4, m_g=8)
-    else:  # n = 17, nx = n0 = 13, 4 box rows
-        per_qp, F, It = bytes_per_qp(T, 17, 13, 13, 4, args.admm_iters, 4)
-    iter_bytes = B * args.admm_iters * It  # algorithmic bytes of one iteration-kernel launch
-    achieved = iter_bytes / iter_avg_s / 1e9
-    qp_achieved = per_qp * B / solve_avg_s / 1e9
-    finite = bool(torch.isfinite(sol.states).all() and torch.isfinite(sol.controls).all())
-    traffic = None if c4 else measured_traffic()
-
-    value = B * args.steps / elapsed
-    if c4:
-        workload = (f"config 4: obstacle avoidance, double integrator nx=6 nu=3 N={prob.horizon}, 8 spheres "
-                    f"(linearized rows), |u| <= 3, {args.sqp} SQP x {args.admm_iters} ADMM, ADMM state carried "
-                    f"across SQP iterations, direct block-tridiagonal KKT backend")
-        data = "synthetic (seeded obstacle fields: 8 spheres, start and goal on opposite faces of [-4,4]^3)"
-    else:
-        workload = ("config 3: quadrotor nonlinear SQP, nx=13 nu=4 N=40, RK4 dt=0.02, 5 SQP x 20 ADMM, "
-                    "direct block-tridiagonal KKT backend")
-        data = "synthetic (seeded quadrotor fleet: random goals, perturbed hover starts)"
-    line = {
-        "metric": f"MPC solves/sec at B={B}{', config 4' if c4 else ''} (1 MI355X)",
-        "value": value,
-        "unit": "MPC solves/s",
-        "n_gpus": 1,
-        "steps": args.steps,
-        "warmup": args.warmup,
-        "ms_per_step": elapsed / args.steps * 1e3,
-        "higher_is_better": True,
-        "scaling": "weak",
-        "vs_baseline": None,
-        "dtype": "f32",
-        "data": data,
-        "config": {
-            "workload": workload,
-            "batch": B,
-            "horizon": prob.horizon,
-            "sqp_iterations": args.sqp,
-            "admm_iterations": args.admm_iters,
-            "parallelism": "single GPU, batch-parallel",
-            "solution_finite": finite,
-            "kernel_only_solves_per_s": B / (args.sqp * solve_avg_s),
-        },
-        "roofline": {
-            "bound": "hbm",
-            "achieved": achieved,
-            "peak": HBM_PEAK_GBS,
-            "unit": "GB/s",
-            "frac": achieved / HBM_PEAK_GBS,
-            "traffic": traffic,
-            "kernel": f"admm_stream_kernel (one launch = {args.admm_iters} ADMM iterations of the batch)",
-            "algorithmic_bytes_per_launch": iter_bytes,
-            "avg_launch_ms": iter_avg_s * 1e3,
-            "qp_solve": {
-                "kernels": "stage_pack + factor_std + admm_stream + stage_unpack",
-                "algorithmic_bytes": per_qp * B,
-                "avg_ms": solve_avg_s * 1e3,
-                "achieved": qp_achieved,
-                "frac": qp_achieved / HBM_PEAK_GBS,
-            },
-        },
-    }
+        line = run_config2(args, dev)
     if args.cpu_baseline:
-        line["cpu_baseline"] = cpu_baseline(B, args.sqp, args.admm_iters, args.seed, args.cpu_budget,
-                                            args.workload)
+        line["cpu_baseline"] = cpu_baseline(args.workload, args.batch, args)
     print(json.dumps(line), flush=True)
 
 

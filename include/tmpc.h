@@ -103,10 +103,11 @@ const char* tmpc_status_string(int status);
 int tmpc_version(void);
 
 /* Measurement hook (no counterpart in the reference): while set, every
- * tmpc_admm_direct_* call records `before` on its stream right before its
- * ADMM-iteration phase (the iteration kernels and any refactorizations
- * between chunks) and `after` right after it, so the caller can time that
- * phase alone with hipEventElapsedTime.  NULL, NULL switches it off.  The
+ * tmpc_admm_direct_* / tmpc_sqp_admm_step_* / tmpc_admm_pcg_* call records
+ * `before` on its stream right before its ADMM-iteration phase (the iteration
+ * kernels and any refactorizations or Schur rebuilds between chunks) and
+ * `after` right after it, so the caller can time that phase alone with
+ * hipEventElapsedTime.  NULL, NULL switches it off.  The
  * setting is process-wide and not synchronised: set it from the thread that
  * launches the solves. */
 void tmpc_set_timing_events(hipEvent_t before, hipEvent_t after);

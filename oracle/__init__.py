@@ -26,4 +26,5 @@ from .oracle import (  # noqa: F401
     pcg,
     quadrotor_rk4_jac,
     schur_build,
+    use_native_build,
 )

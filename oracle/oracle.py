@@ -98,14 +98,16 @@ class OracleCfg:
         )
 
 
-def load():
-    """Load liboracle.so, building it with make when it is missing."""
+def load(so=None):
+    """Load liboracle.so (or the library at `so`), building the default one
+    with make when it is missing."""
     global _LIB
-    if _LIB is not None:
+    if _LIB is not None and so is None:
         return _LIB
-    so = _HERE / "liboracle.so"
-    if not so.exists():
-        subprocess.run(["make", "-C", str(_HERE)], check=True, capture_output=True)
+    if so is None:
+        so = _HERE / "liboracle.so"
+        if not so.exists():
+            subprocess.run(["make", "-C", str(_HERE)], check=True, capture_output=True)
     lib = ctypes.CDLL(str(so))
     for name in (
         "ora_admm_solve",
@@ -118,6 +120,17 @@ def load():
         getattr(lib, name).restype = ctypes.c_int
     _LIB = lib
     return lib
+
+
+def use_native_build(build_dir):
+    """Build the oracle with -march=native into `build_dir` (make native) and
+    make it the library every oracle call uses from now on.  For the CPU
+    baseline, on the host that times it.  Returns the library path."""
+    subprocess.run(["make", "-C", str(_HERE), "native", f"NATIVE_DIR={build_dir}"], check=True,
+                   capture_output=True)
+    so = Path(build_dir) / "liboracle.so"
+    load(so)
+    return so
 
 
 def _threads(nthreads):

@@ -763,6 +763,7 @@ int admm_pcg_impl(hipStream_t s, const tmpc_dims* dims, const tmpc_qp* qp, const
   st = launch_schur_build<R>(s, d, a.qp, a.st.rho, a.sigma, a.rho_f_factor, nullptr, S, Phi);
   if (st) return st;
   const std::vector<int> bounds = chunk_bounds(cfg->max_iter, cfg->check_every, cfg->adapt_rho_every);
+  if (g_iter_events[0] && hipEventRecord(g_iter_events[0], s) != hipSuccess) return TMPC_ELAUNCH;
   for (size_t k = 0; k + 1 < bounds.size(); ++k) {
     if (k > 0) {
       st = launch_schur_build<R>(s, d, a.qp, a.st.rho, a.sigma, a.rho_f_factor, a.ctl, S, Phi);
@@ -781,6 +782,7 @@ int admm_pcg_impl(hipStream_t s, const tmpc_dims* dims, const tmpc_qp* qp, const
     st = launch_status();
     if (st) return st;
   }
+  if (g_iter_events[1] && hipEventRecord(g_iter_events[1], s) != hipSuccess) return TMPC_ELAUNCH;
   return launch_nonfinite_flags<R>(s, d, a.st, iters);
 }
 
