@@ -12,6 +12,7 @@
 #include "common.hpp"
 #include "factor.hpp"
 #include "pcg.hpp"
+#include "pcg_lds.hpp"
 #include "obstacle.hpp"
 #include "quadrotor.hpp"
 #include "adjoint.hpp"
@@ -705,6 +706,33 @@ void launch_admm_pcg_nc(hipStream_t s, const AdmmPcgArgs<R>& pa) {
   hipLaunchKernelGGL((admm_pcg_chunk_kernel<R, NC>), dim3(grid), dim3(kWave), 0, s, pa);
 }
 
+// LDS-resident PCG ADMM (explicit-integrator QPs): one problem per workgroup,
+// theta_t rows in LDS when they fit (mode 2), else in the workspace (mode 1).
+template <typename R, int NC, bool THL>
+int launch_pcg_lds_th(hipStream_t s, const AdmmPcgArgs<R>& pa) {
+  const size_t smem = pcg_lds_layout<R>(pa.a.d, THL).bytes;
+  if (smem > kMaxLds) return TMPC_EBADSHAPE;
+  lds_optin(admm_pcg_lds_kernel<R, NC, THL>, smem);
+  hipLaunchKernelGGL((admm_pcg_lds_kernel<R, NC, THL>), dim3(pa.a.d.B), dim3(kPcgThreads), smem, s, pa);
+  return launch_status();
+}
+
+template <typename R, int NC>
+int launch_pcg_lds_nc(hipStream_t s, const AdmmPcgArgs<R>& pa, int mode) {
+  return mode == 2 ? launch_pcg_lds_th<R, NC, true>(s, pa) : launch_pcg_lds_th<R, NC, false>(s, pa);
+}
+
+template <typename R>
+int launch_pcg_lds(hipStream_t s, const AdmmPcgArgs<R>& pa, int mode) {
+  switch (pa.a.d.n) {
+    case 6: return launch_pcg_lds_nc<R, 6>(s, pa, mode);
+    case 9: return launch_pcg_lds_nc<R, 9>(s, pa, mode);
+    case 16: return launch_pcg_lds_nc<R, 16>(s, pa, mode);
+    case 17: return launch_pcg_lds_nc<R, 17>(s, pa, mode);
+    default: return TMPC_EBADSHAPE;
+  }
+}
+
 template <typename R>
 int admm_pcg_impl(hipStream_t s, const tmpc_dims* dims, const tmpc_qp* qp, const tmpc_state* in,
                   tmpc_state* out, uint32_t* iters, uint32_t* pcg_iters, const tmpc_admm_cfg* cfg, void* ws,
@@ -760,6 +788,17 @@ int admm_pcg_impl(hipStream_t s, const tmpc_dims* dims, const tmpc_qp* qp, const
   pa.pcg_iters = pcg_iters;
   pa.pcg_eps = (R)cfg->pcg_eps;
   pa.pcg_max_iter = cfg->pcg_max_iter;
+  const bool std_dyn = (cfg->flags & TMPC_FLAG_STD_DYNAMICS) != 0;
+  const int lds_mode = pcg_lds_mode<R>(d);
+  if (std_dyn && (cfg->flags & TMPC_FLAG_GENERIC_KERNEL) == 0 && lds_mode) {
+    // the whole solve in one launch, one problem per workgroup, rho changes
+    // rebuilt in the kernel (pcg_lds.hpp)
+    if (g_iter_events[0] && hipEventRecord(g_iter_events[0], s) != hipSuccess) return TMPC_ELAUNCH;
+    st = launch_pcg_lds<R>(s, pa, lds_mode);
+    if (st) return st;
+    if (g_iter_events[1] && hipEventRecord(g_iter_events[1], s) != hipSuccess) return TMPC_ELAUNCH;
+    return launch_nonfinite_flags<R>(s, d, a.st, iters);
+  }
   st = launch_schur_build<R>(s, d, a.qp, a.st.rho, a.sigma, a.rho_f_factor, nullptr, S, Phi);
   if (st) return st;
   const std::vector<int> bounds = chunk_bounds(cfg->max_iter, cfg->check_every, cfg->adapt_rho_every);

@@ -62,6 +62,22 @@ __device__ __forceinline__ R rinf() {
   return __builtin_huge_val();
 }
 
+// Wavefront-wide sum / max by butterfly shuffles: every lane ends with the
+// same value, combined in the same fixed order on every run.
+template <typename R>
+__device__ __forceinline__ R wave_sum(R v) {
+#pragma unroll
+  for (int off = kWave / 2; off > 0; off >>= 1) v += __shfl_xor(v, off);
+  return v;
+}
+
+template <typename R>
+__device__ __forceinline__ R wave_max(R v) {
+#pragma unroll
+  for (int off = kWave / 2; off > 0; off >>= 1) v = rmax(v, __shfl_xor(v, off));
+  return v;
+}
+
 // Fills n words with v.  Used instead of hipMemsetAsync so that a solve
 // captured in a HIP graph holds kernel nodes only.
 template <typename W>

@@ -39,13 +39,6 @@ __device__ __forceinline__ void atomic_max_abs(R* p, R v) {
 }
 
 template <typename R>
-__device__ __forceinline__ R wave_max(R v) {
-#pragma unroll
-  for (int off = kWave / 2; off > 0; off >>= 1) v = rmax(v, __shfl_xor(v, off));
-  return v;
-}
-
-template <typename R>
 __global__ void sqp_check_init_kernel(int B, R* __restrict__ conv, R* __restrict__ eq, R* __restrict__ iq) {
   const int b = blockIdx.x * blockDim.x + threadIdx.x;
   if (b >= B) return;
