@@ -441,11 +441,13 @@ def run_config2(args, dev):
     prob = configs.config2(B=B, seed=args.seed).to(dev, dt)
     qp = prob.build_qp(*prob.initial_guess())
     _, T, n, nx, n0, m = qp.dims
-    lds = args.pcg_kernel == "lds"
+    kflags = {"dpp": _lib.flag_pcg_kernel(_lib.PCG_KERNEL_DPP), "lds": _lib.flag_pcg_kernel(_lib.PCG_KERNEL_LDS),
+              "chunk": _lib.FLAG_GENERIC_KERNEL}[args.pcg_kernel]
+    one_launch = args.pcg_kernel != "chunk"
     solver = ADMMSolver(ZShape(T - 1, nx, n - nx), {"max_iter": 50, "tol_epsilon": 1e-6}, sigma=1e-6, max_iter=K,
                         eps_abs=1e-30, eps_rel=1e-30, check_termination_every=K + 1, adapt_rho_every=0,
                         rho_f_factor=1000.0, admm_backend=AdmmBackend.HIP_PCG, std_dynamics=True,
-                        kernel_flags=0 if lds else _lib.FLAG_GENERIC_KERNEL)
+                        kernel_flags=kflags)
     st0 = solver.initial_state(qp, rho_bar=0.1)
     with SolveTimer(dev) as timer:
         elapsed, (_, stats, st) = timed_steps(lambda: solver.solve(qp, st0, alpha=1.0), args.steps, args.warmup,
@@ -460,7 +462,7 @@ def run_config2(args, dev):
     solve_bytes = B * (per_solve - phase) + phase_bytes
     # the one-launch kernel also builds S and Phiinv: its launch carries the
     # whole solve's algorithmic bytes; the chunk kernels carry the iteration phase
-    kernel_bytes = solve_bytes if lds else phase_bytes
+    kernel_bytes = solve_bytes if one_launch else phase_bytes
     achieved = kernel_bytes / iter_avg_s / 1e9
     finite = bool(torch.isfinite(st.x_blocks).all())
     line = base_line(f"MPC solves/sec at B={B}, config 2 PCG {args.dtype} (1 MI355X)", B * args.steps / elapsed,
@@ -472,11 +474,11 @@ def run_config2(args, dev):
                          "batch": B, "horizon": T - 1, "admm_iterations": K,
                          "mean_pcg_iterations": pcg_total / (B * K),
                          "parallelism": "single GPU, batch-parallel", "solution_finite": finite})
-    if lds:
-        kname = (f"admm_pcg_lds_kernel (one launch = the whole solve: S and Phiinv blocks built on chip, "
+    if one_launch:
+        kernels = f"admm_pcg_{args.pcg_kernel}"
+        kname = (f"{kernels}_kernel (one launch = the whole solve: S and Phiinv blocks built on chip, "
                  f"{K} ADMM iterations with their PCG solves; algorithmic bytes are the streaming model's, "
                  f"which this kernel does not move: S, Phiinv and the PCG vectors stay in LDS and registers)")
-        kernels = "admm_pcg_lds"
     else:
         kname = f"admm_pcg_chunk_kernel (one launch = {K} ADMM iterations with their PCG solves)"
         kernels = "schur_build + admm_pcg_chunk"
@@ -520,8 +522,9 @@ def main():
     ap.add_argument("--sqp", type=int, default=None, help="SQP iterations (config3 / config4)")
     ap.add_argument("--admm-iters", type=int, default=None)
     ap.add_argument("--dtype", choices=("f32", "f64"), default="f32", help="config2 only")
-    ap.add_argument("--pcg-kernel", choices=("lds", "chunk"), default="lds",
-                    help="config2 only: the one-launch LDS-resident kernel or the S/Phiinv streaming chunk kernel")
+    ap.add_argument("--pcg-kernel", choices=("dpp", "lds", "chunk"), default="dpp",
+                    help="config2 only: the one-launch kernels (dpp: a stage per 16-lane row, lds: LDS-resident) "
+                         "or the chunk kernel that streams S and Phiinv")
     ap.add_argument("--cpu-baseline", type=int, default=1)
     ap.add_argument("--cpu-budget", type=float, default=15.0, help="seconds of CPU work for the baseline sample")
     ap.add_argument("--copy-calibration", type=int, default=0,

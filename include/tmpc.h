@@ -72,6 +72,15 @@ typedef struct tmpc_state {
  * from B). */
 #define TMPC_FLAG_GENERIC_KERNEL 2u
 #define TMPC_FLAG_STREAM_P(p) (((uint32_t)(p) & 3u) << 8)
+/* tmpc_admm_pcg_* with TMPC_FLAG_STD_DYNAMICS runs the whole solve in one
+ * launch, one problem per workgroup, when the shape allows it: the
+ * row-broadcast kernel (n in {6, 9, 16}, 16 T <= 1024, T m <= 1024), else the
+ * LDS-resident kernel (n in {6, 9, 16, 17}, T n <= 1024, T m <= 1024), else
+ * (or with TMPC_FLAG_GENERIC_KERNEL) the chunked kernel that streams S and
+ * Phiinv.  Bits 10-11 force one of them (1 = row-broadcast, 2 = LDS-resident,
+ * 3 = chunked; TMPC_EBADSHAPE if it does not cover the shape), for
+ * cross-checks. */
+#define TMPC_FLAG_PCG_KERNEL(k) (((uint32_t)(k) & 3u) << 10)
 /* Every D_t is diagonal (quadratic costs with per-variable weights), vouched
  * for by the caller.  The streaming kernel then keeps diag(D_t) in its stage
  * records and forms the D_t x terms from it, and the first-order check reads

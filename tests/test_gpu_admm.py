@@ -164,10 +164,12 @@ def test_admm_direct_warm_start_and_in_place_state():
     _assert_state_close(s2, ref, 1e-9)
 
 
-# PCG Schur solve on explicit-integrator QPs: "lds" is the one-launch kernel
-# with the problem resident in LDS (admm_pcg_lds_kernel), "chunk" the kernel
-# that streams S and Phiinv (admm_pcg_chunk_kernel, FLAG_GENERIC_KERNEL).
-PCG_KERNELS = {"lds": 0, "chunk": _lib.FLAG_GENERIC_KERNEL}
+# PCG Schur solve on explicit-integrator QPs: "dpp" is the one-launch kernel
+# with a stage per 16-lane row (admm_pcg_dpp_kernel), "lds" the one-launch
+# kernel with the problem resident in LDS (admm_pcg_lds_kernel), "chunk" the
+# kernel that streams S and Phiinv (admm_pcg_chunk_kernel).
+PCG_KERNELS = {"dpp": _lib.flag_pcg_kernel(_lib.PCG_KERNEL_DPP), "lds": _lib.flag_pcg_kernel(_lib.PCG_KERNEL_LDS),
+               "chunk": _lib.FLAG_GENERIC_KERNEL}
 
 
 @pytest.mark.parametrize("kernel", list(PCG_KERNELS))
@@ -231,18 +233,23 @@ def test_admm_pcg_fixed_pcg_iterations_fp32(kernel):
         assert e < TOL[torch.float32], (k, e)
 
 
-# every n the one-launch kernel is built for, with m = 0, n0 < nx, a single
-# stage pair and 1024 = T n (a full workgroup); fixed PCG counts (pcg_eps = 0)
-# so that the iteration is fully determined, residual checks every 4 iterations
+# every n the one-launch kernels are built for, with m = 0, n0 < nx, a single
+# stage pair and 1024 = 16 T (a full workgroup for the row-broadcast kernel);
+# fixed PCG counts (pcg_eps = 0) so that the iteration is fully determined,
+# residual checks every 4 iterations
 @pytest.mark.parametrize("shape", [(5, 21, 6, 4, 2, 4), (4, 13, 9, 6, 11, 6), (3, 9, 16, 12, 16, 12),
                                    (3, 7, 17, 13, 4, 13), (2, 64, 16, 12, 0, 12), (4, 2, 6, 4, 3, 2)])
 @pytest.mark.parametrize("dtype", [torch.float64, torch.float32])
-def test_admm_pcg_lds_kernel_shapes(shape, dtype):
+@pytest.mark.parametrize("kernel", ["dpp", "lds"])
+def test_admm_pcg_one_launch_kernel_shapes(kernel, shape, dtype):
     B, T, n, nx, m, n0 = shape
+    if kernel == "dpp" and n > 16:
+        pytest.skip("the row-broadcast kernel covers n <= 16")
     qp = random_qp(B, T, n, nx, m, seed=71, std=True, n0=n0)
     cfg = oracle.OracleCfg(max_iter=9, check_every=4, adapt_rho_every=0, sigma=1e-6, eps_abs=1e-12, eps_rel=1e-12,
                            rho_f_factor=100.0, alpha=1.6, pcg_eps=0.0, pcg_max_iter=5)
-    ref, it_ref, pcg_ref, out, stats = _run_pair(qp, cfg, dtype, backend=AdmmBackend.HIP_PCG, schur="pcg")
+    ref, it_ref, pcg_ref, out, stats = _run_pair(qp, cfg, dtype, backend=AdmmBackend.HIP_PCG, schur="pcg",
+                                                 kernel_flags=PCG_KERNELS[kernel])
     np.testing.assert_array_equal(stats.num_iter.cpu().numpy(), it_ref)
     np.testing.assert_array_equal(stats.num_pcg_iters.sum(1).cpu().numpy(), pcg_ref)
     _assert_state_close(out, ref, 1e-9 if dtype == torch.float64 else TOL[torch.float32])

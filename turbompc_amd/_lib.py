@@ -35,6 +35,15 @@ def flag_stream_p(p: int) -> int:
     """Forces the problems per wavefront of the streaming kernel (1-3)."""
     return (int(p) & 3) << 8
 
+
+PCG_KERNEL_DPP, PCG_KERNEL_LDS, PCG_KERNEL_CHUNK = 1, 2, 3
+
+
+def flag_pcg_kernel(k: int) -> int:
+    """TMPC_FLAG_PCG_KERNEL: forces the PCG ADMM kernel (1 row-broadcast,
+    2 LDS-resident, 3 chunked)."""
+    return (int(k) & 3) << 10
+
 _STATUS = {
     0: "ok",
     1: "unsupported dimensions",

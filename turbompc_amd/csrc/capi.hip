@@ -722,6 +722,32 @@ int launch_pcg_lds_nc(hipStream_t s, const AdmmPcgArgs<R>& pa, int mode) {
   return mode == 2 ? launch_pcg_lds_th<R, NC, true>(s, pa) : launch_pcg_lds_th<R, NC, false>(s, pa);
 }
 
+template <typename R, int NC>
+int launch_pcg_dpp_nc(hipStream_t s, const AdmmPcgArgs<R>& pa) {
+  // A_minus in registers for fp32; in LDS for fp64 (the theta rows take the registers)
+  constexpr bool amr = sizeof(R) == 4;
+  const size_t smem = pcg_dpp_layout<R>(pa.a.d, amr).bytes;
+  if (smem > kMaxLds) return TMPC_EBADSHAPE;
+  lds_optin(admm_pcg_dpp_kernel<R, NC, amr>, smem);
+  hipLaunchKernelGGL((admm_pcg_dpp_kernel<R, NC, amr>), dim3(pa.a.d.B), dim3(kPcgThreads), smem, s, pa);
+  return launch_status();
+}
+
+template <typename R>
+int launch_pcg_dpp(hipStream_t s, const AdmmPcgArgs<R>& pa) {
+  switch (pa.a.d.n) {
+    case 6: return launch_pcg_dpp_nc<R, 6>(s, pa);
+    case 9: return launch_pcg_dpp_nc<R, 9>(s, pa);
+    case 16: return launch_pcg_dpp_nc<R, 16>(s, pa);
+    default: return TMPC_EBADSHAPE;
+  }
+}
+
+template <typename R>
+bool pcg_dpp_covers(const Dims& d) {
+  return pcg_dpp_fits(d) && pcg_dpp_layout<R>(d, sizeof(R) == 4).bytes <= kMaxLds;
+}
+
 template <typename R>
 int launch_pcg_lds(hipStream_t s, const AdmmPcgArgs<R>& pa, int mode) {
   switch (pa.a.d.n) {
@@ -790,11 +816,19 @@ int admm_pcg_impl(hipStream_t s, const tmpc_dims* dims, const tmpc_qp* qp, const
   pa.pcg_max_iter = cfg->pcg_max_iter;
   const bool std_dyn = (cfg->flags & TMPC_FLAG_STD_DYNAMICS) != 0;
   const int lds_mode = pcg_lds_mode<R>(d);
-  if (std_dyn && (cfg->flags & TMPC_FLAG_GENERIC_KERNEL) == 0 && lds_mode) {
+  // kernel choice: 1 row-broadcast, 2 LDS-resident, 3 chunked (pcg_lds.hpp, pcg.hpp)
+  int kern = (int)((cfg->flags >> 10) & 3u);
+  if (kern == 0) {
+    if (!std_dyn || (cfg->flags & TMPC_FLAG_GENERIC_KERNEL)) kern = 3;
+    else kern = pcg_dpp_covers<R>(d) ? 1 : lds_mode ? 2 : 3;
+  } else if ((kern == 1 && (!std_dyn || !pcg_dpp_covers<R>(d))) || (kern == 2 && (!std_dyn || !lds_mode))) {
+    return TMPC_EBADSHAPE;
+  }
+  if (kern != 3) {
     // the whole solve in one launch, one problem per workgroup, rho changes
-    // rebuilt in the kernel (pcg_lds.hpp)
+    // rebuilt in the kernel
     if (g_iter_events[0] && hipEventRecord(g_iter_events[0], s) != hipSuccess) return TMPC_ELAUNCH;
-    st = launch_pcg_lds<R>(s, pa, lds_mode);
+    st = kern == 1 ? launch_pcg_dpp<R>(s, pa) : launch_pcg_lds<R>(s, pa, lds_mode);
     if (st) return st;
     if (g_iter_events[1] && hipEventRecord(g_iter_events[1], s) != hipSuccess) return TMPC_ELAUNCH;
     return launch_nonfinite_flags<R>(s, d, a.st, iters);
