@@ -88,16 +88,25 @@ __device__ __forceinline__ double read_lane(double v, int l) {
   return __builtin_bit_cast(double, ((unsigned long long)hi << 32) | lo);
 }
 
+// Sum over each 16-lane row, the same value in every lane of the row: pairs,
+// quads, half rows, rows (every step adds two equal-shaped partials, so all
+// lanes of a row end with the same bits).  Every lane must be active.
+template <typename R>
+__device__ __forceinline__ R row_sum(R v) {
+  v += dpp_move<0xB1>(v);   // quad_perm [1, 0, 3, 2]
+  v += dpp_move<0x4E>(v);   // quad_perm [2, 3, 0, 1]
+  v += dpp_move<0x141>(v);  // row_half_mirror
+  v += dpp_move<0x140>(v);  // row_mirror
+  return v;
+}
+
 // Sum over the 64 lanes, the same value in every lane, in a fixed order:
 // within each 16-lane row by DPP moves (pairs, quads, half rows, rows; every
 // step adds two equal-shaped partials, so all lanes of a row end with the same
 // bits), then the four row sums.  Every lane must be active.
 template <typename R>
 __device__ __forceinline__ R wave_sum(R v) {
-  v += dpp_move<0xB1>(v);   // quad_perm [1, 0, 3, 2]
-  v += dpp_move<0x4E>(v);   // quad_perm [2, 3, 0, 1]
-  v += dpp_move<0x141>(v);  // row_half_mirror
-  v += dpp_move<0x140>(v);  // row_mirror
+  v = row_sum(v);
   return (read_lane(v, 0) + read_lane(v, 16)) + (read_lane(v, 32) + read_lane(v, 48));
 }
 
@@ -160,34 +169,36 @@ __device__ __forceinline__ R row_dot(const R (&w)[NC], R s) {
   return row_dot_seq<R, NC>(w, s, std::make_integer_sequence<int, NC>{});
 }
 
-// The same sums with the broadcast folded into the FMA (v_fmac_*_dpp
-// row_newbcast, one instruction per term instead of a move and an FMA).  The
-// compiler does not form these, so they are written out; the s_nop before the
-// block gives the DPP source the wait states a DPP read needs after a VALU write
-// of its operand (and the one after, any DPP read of the sums that follows).
+// The same sums with the broadcast folded into the arithmetic (v_*_dpp
+// row_newbcast: one instruction per term instead of a move and an FMA; in
+// fp32 the first term of each chain initialises it with a multiply, which has
+// no DPP form in fp64).  The compiler does not form these, so they are written
+// out; the s_nop before the block gives the DPP source the wait states a DPP
+// read needs after a VALU write of its operand, and the one after covers a
+// DPP read of the sums that follows.
 
 __device__ __forceinline__ float row_dot_dpp(const float (&w)[6], float s) {
-  float a0 = float(0), a1 = float(0);
+  float a0, a1;
   asm volatile(
       "s_nop 4\n"
-      "v_fmac_f32_dpp %0, %2, %3 row_newbcast:0 row_mask:0xf bank_mask:0xf\n"
-      "v_fmac_f32_dpp %1, %2, %4 row_newbcast:1 row_mask:0xf bank_mask:0xf\n"
+      "v_mul_f32_dpp %0, %2, %3 row_newbcast:0 row_mask:0xf bank_mask:0xf\n"
+      "v_mul_f32_dpp %1, %2, %4 row_newbcast:1 row_mask:0xf bank_mask:0xf\n"
       "v_fmac_f32_dpp %0, %2, %5 row_newbcast:2 row_mask:0xf bank_mask:0xf\n"
       "v_fmac_f32_dpp %1, %2, %6 row_newbcast:3 row_mask:0xf bank_mask:0xf\n"
       "v_fmac_f32_dpp %0, %2, %7 row_newbcast:4 row_mask:0xf bank_mask:0xf\n"
       "v_fmac_f32_dpp %1, %2, %8 row_newbcast:5 row_mask:0xf bank_mask:0xf\n"
       "s_nop 1"
-      : "+v"(a0), "+v"(a1)
+      : "=&v"(a0), "=&v"(a1)
       : "v"(s), "v"(w[0]), "v"(w[1]), "v"(w[2]), "v"(w[3]), "v"(w[4]), "v"(w[5]));
   return a0 + a1;
 }
 
 __device__ __forceinline__ float row_dot_dpp(const float (&w)[9], float s) {
-  float a0 = float(0), a1 = float(0);
+  float a0, a1;
   asm volatile(
       "s_nop 4\n"
-      "v_fmac_f32_dpp %0, %2, %3 row_newbcast:0 row_mask:0xf bank_mask:0xf\n"
-      "v_fmac_f32_dpp %1, %2, %4 row_newbcast:1 row_mask:0xf bank_mask:0xf\n"
+      "v_mul_f32_dpp %0, %2, %3 row_newbcast:0 row_mask:0xf bank_mask:0xf\n"
+      "v_mul_f32_dpp %1, %2, %4 row_newbcast:1 row_mask:0xf bank_mask:0xf\n"
       "v_fmac_f32_dpp %0, %2, %5 row_newbcast:2 row_mask:0xf bank_mask:0xf\n"
       "v_fmac_f32_dpp %1, %2, %6 row_newbcast:3 row_mask:0xf bank_mask:0xf\n"
       "v_fmac_f32_dpp %0, %2, %7 row_newbcast:4 row_mask:0xf bank_mask:0xf\n"
@@ -196,17 +207,17 @@ __device__ __forceinline__ float row_dot_dpp(const float (&w)[9], float s) {
       "v_fmac_f32_dpp %1, %2, %10 row_newbcast:7 row_mask:0xf bank_mask:0xf\n"
       "v_fmac_f32_dpp %0, %2, %11 row_newbcast:8 row_mask:0xf bank_mask:0xf\n"
       "s_nop 1"
-      : "+v"(a0), "+v"(a1)
+      : "=&v"(a0), "=&v"(a1)
       : "v"(s), "v"(w[0]), "v"(w[1]), "v"(w[2]), "v"(w[3]), "v"(w[4]), "v"(w[5]), "v"(w[6]), "v"(w[7]), "v"(w[8]));
   return a0 + a1;
 }
 
 __device__ __forceinline__ float row_dot_dpp(const float (&w)[16], float s) {
-  float a0 = float(0), a1 = float(0);
+  float a0, a1;
   asm volatile(
       "s_nop 4\n"
-      "v_fmac_f32_dpp %0, %2, %3 row_newbcast:0 row_mask:0xf bank_mask:0xf\n"
-      "v_fmac_f32_dpp %1, %2, %4 row_newbcast:1 row_mask:0xf bank_mask:0xf\n"
+      "v_mul_f32_dpp %0, %2, %3 row_newbcast:0 row_mask:0xf bank_mask:0xf\n"
+      "v_mul_f32_dpp %1, %2, %4 row_newbcast:1 row_mask:0xf bank_mask:0xf\n"
       "v_fmac_f32_dpp %0, %2, %5 row_newbcast:2 row_mask:0xf bank_mask:0xf\n"
       "v_fmac_f32_dpp %1, %2, %6 row_newbcast:3 row_mask:0xf bank_mask:0xf\n"
       "v_fmac_f32_dpp %0, %2, %7 row_newbcast:4 row_mask:0xf bank_mask:0xf\n"
@@ -222,7 +233,7 @@ __device__ __forceinline__ float row_dot_dpp(const float (&w)[16], float s) {
       "v_fmac_f32_dpp %0, %2, %17 row_newbcast:14 row_mask:0xf bank_mask:0xf\n"
       "v_fmac_f32_dpp %1, %2, %18 row_newbcast:15 row_mask:0xf bank_mask:0xf\n"
       "s_nop 1"
-      : "+v"(a0), "+v"(a1)
+      : "=&v"(a0), "=&v"(a1)
       : "v"(s), "v"(w[0]), "v"(w[1]), "v"(w[2]), "v"(w[3]), "v"(w[4]), "v"(w[5]), "v"(w[6]), "v"(w[7]), "v"(w[8]), "v"(w[9]), "v"(w[10]), "v"(w[11]), "v"(w[12]), "v"(w[13]), "v"(w[14]), "v"(w[15]));
   return a0 + a1;
 }

@@ -90,6 +90,7 @@ __global__ __launch_bounds__(kPcgThreads) void admm_pcg_lds_kernel(AdmmPcgArgs<R
   const Dims d = a.d;
   constexpr int n = NC;
   constexpr int NW = kPcgThreads / kWave;
+  static_assert(NW == 16, "block sums read one wavefront sum per lane of a 16-lane row");
   const int T = d.T, N = d.N, nx = d.nx, n0 = d.n0, m = d.m;
   const int b = blockIdx.x, tid = threadIdx.x, lane = tid & (kWave - 1), wid = tid / kWave;
   const int P = pcg_pitch(n);
@@ -270,10 +271,7 @@ __global__ __launch_bounds__(kPcgThreads) void admm_pcg_lds_kernel(AdmmPcgArgs<R
     rslot ^= 1;
     if (lane == 0) rr[wid] = v;
     __syncthreads();
-    R s = R(0);
-#pragma unroll
-    for (int w = 0; w < NW; ++w) s += rr[w];
-    return s;
+    return row_sum(rr[lane & (NW - 1)]);  // the 16 wavefront sums, one per lane of each row
   };
   // rt = Phiinv r for r in vr (complete in LDS); returns this element's rt
   auto apply_phiinv = [&](R rho_f) __attribute__((always_inline)) -> R {
@@ -598,6 +596,7 @@ __global__ __launch_bounds__(kPcgThreads) void admm_pcg_dpp_kernel(AdmmPcgArgs<R
   const Dims d = a.d;
   constexpr int n = NC, W = kPcgRow;
   constexpr int NW = kPcgThreads / kWave;
+  static_assert(NW == 16, "block sums read one wavefront sum per lane of a 16-lane row");
   const int T = d.T, N = d.N, nx = d.nx, n0 = d.n0, m = d.m;
   const int b = blockIdx.x, tid = threadIdx.x, lane = tid & (kWave - 1), wid = tid / kWave;
   const int P = pcg_pitch(n);
@@ -761,10 +760,7 @@ __global__ __launch_bounds__(kPcgThreads) void admm_pcg_dpp_kernel(AdmmPcgArgs<R
     rslot ^= 1;
     if (lane == 0) rr[wid] = v;
     __syncthreads();
-    R s_ = R(0);
-#pragma unroll
-    for (int w = 0; w < NW; ++w) s_ += rr[w];
-    return s_;
+    return row_sum(rr[lane & (NW - 1)]);  // the 16 wavefront sums, one per lane of each row
   };
   // rt = Phiinv r for this lane's r; returns rt (zero off the elements)
   auto apply_phiinv = [&](R r, R rho_f) __attribute__((always_inline)) -> R {
