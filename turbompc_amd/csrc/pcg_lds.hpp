@@ -740,14 +740,21 @@ __global__ __launch_bounds__(kPcgThreads) void admm_pcg_dpp_kernel(AdmmPcgArgs<R
   auto offdiag = [&](const R* buf, R rho_f) __attribute__((always_inline)) -> R {
     const R sp = (st && t >= 1) ? buf[tid - W] : R(0);  // s_{t-1}[i]
     const R sn = (t < N) ? buf[tid + W] : R(0);          // s_{t+1}[i]
-    R ar_[NC], ac_[NC];
+    R rw, cl;
+    if (AMR) {
+      rw = row_dot_dpp(amr, sp);
+      cl = row_dot_dpp(amc, sn);
+    } else {
+      // one block's operands in registers at a time
+      R w_[NC];
 #pragma unroll
-    for (int k = 0; k < NC; ++k) {
-      ar_[k] = AMR ? amr[k] : arow[k];
-      ac_[k] = AMR ? amc[k] : (k < nx ? acol[k * P] : R(0));
+      for (int k = 0; k < NC; ++k) w_[k] = arow[k];
+      rw = row_dot_dpp(w_, sp);
+      __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+      for (int k = 0; k < NC; ++k) w_[k] = k < nx ? acol[k * P] : R(0);
+      cl = row_dot_dpp(w_, sn);
     }
-    const R rw = row_dot_dpp(ar_, sp);
-    const R cl = row_dot_dpp(ac_, sn);
     R acc = R(0);
     acc -= rho_f * rw;
     acc -= rho_f * cl;
