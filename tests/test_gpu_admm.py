@@ -59,6 +59,20 @@ def _run_pair(qp, cfg, dtype, backend=AdmmBackend.HIP_DIRECT, rho0=0.1, schur="d
     return ref, it_ref, pcg_ref, out, stats
 
 
+def _oracle_full_batch(qp, cfg, rho0=0.1):
+    """The fp64 oracle on a whole device batch (the same fp32-valued inputs)."""
+    qc = qp.to("cpu", torch.float64)
+    ref, it_ref, _ = oracle.admm_solve(qc, zero_state(qc, rho0), cfg, dtype=np.float64)
+    return ref, it_ref
+
+
+def _assert_batch_matches_oracle(name, out, ref, tol):
+    for k in ("x_blocks", "y_f_dyn", "y_g", "z_g", "y_f_0"):
+        e = rel_err(getattr(out, k), getattr(ref, k))
+        print(f"{name} {k}: rel err vs fp64 oracle {e:.2e}")
+        assert e < tol, (name, k, e)
+
+
 def _assert_state_close(out, ref, tol):
     for k in FIELDS:
         a, b = getattr(out, k), getattr(ref, k)
@@ -375,6 +389,11 @@ def test_admm_stream_kernel_matches_generic_on_bench_batch():
     assert torch.equal(s_a.num_iter, s_b.num_iter)
     for k in ("x_blocks", "y_f_dyn", "y_g", "z_g", "y_f_0"):
         assert rel_err(getattr(o_a, k), getattr(o_b, k)) < TOL[torch.float32], k
+    # and both against the fp64 oracle on the whole batch
+    ref, it_ref = _oracle_full_batch(qp, cfg)
+    np.testing.assert_array_equal(s_a.num_iter.cpu().numpy(), it_ref)
+    _assert_batch_matches_oracle("config 3 B=4099 stream", o_a, ref, TOL[torch.float32])
+    _assert_batch_matches_oracle("config 3 B=4099 generic", o_b, ref, TOL[torch.float32])
 
 
 @pytest.mark.parametrize("P", [1, 2, 3])
@@ -445,6 +464,10 @@ def test_admm_stream_kernel_wide_rows_match_generic_on_config4_batch():
     for k in ("x_blocks", "y_f_dyn", "y_g", "z_g", "y_f_0"):
         assert rel_err(getattr(o_a, k), getattr(o_b, k)) < TOL[torch.float32], k
     assert not torch.equal(o_a.x_blocks, o_b.x_blocks)  # two different kernels ran
+    ref, it_ref = _oracle_full_batch(qp, cfg)
+    np.testing.assert_array_equal(s_a.num_iter.cpu().numpy(), it_ref)
+    _assert_batch_matches_oracle("config 4 B=4099 wide stream", o_a, ref, TOL[torch.float32])
+    _assert_batch_matches_oracle("config 4 B=4099 generic", o_b, ref, TOL[torch.float32])
 
 
 @pytest.mark.parametrize("kernel", ["stream", "generic"])
@@ -520,3 +543,6 @@ def test_admm_stream_kernel_structured_records_match_dense_on_bench_batch():
     assert torch.equal(s_a.num_iter, s_b.num_iter)
     for k in ("x_blocks", "y_f_dyn", "y_g", "z_g", "y_f_0"):
         assert rel_err(getattr(o_a, k), getattr(o_b, k)) < 1e-5, k
+    ref, it_ref = _oracle_full_batch(qp, cfg)
+    np.testing.assert_array_equal(s_b.num_iter.cpu().numpy(), it_ref)
+    _assert_batch_matches_oracle("config 3 B=4099 diagonal records", o_b, ref, TOL[torch.float32])
