@@ -81,6 +81,11 @@ typedef struct tmpc_state {
  * 3 = chunked; TMPC_EBADSHAPE if it does not cover the shape), for
  * cross-checks. */
 #define TMPC_FLAG_PCG_KERNEL(k) (((uint32_t)(k) & 3u) << 10)
+/* The direct solve's factorization of the explicit-integrator Schur blocks
+ * runs one problem per 16-lane row (four per wavefront); this flag selects
+ * the factorization with P problems per wavefront in lane groups and LDS
+ * pivot rows instead (same blocks; for cross-checks). */
+#define TMPC_FLAG_FACTOR_GROUPS (1u << 12)
 /* Every D_t is diagonal (quadratic costs with per-variable weights), vouched
  * for by the caller.  The streaming kernel then keeps diag(D_t) in its stage
  * records and forms the D_t x terms from it, and the first-order check reads

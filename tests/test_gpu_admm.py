@@ -343,16 +343,20 @@ def test_quadrotor_linearization_matches_complex_step(dtype):
 # ---- streaming kernel (explicit-integrator structure, stage records) ---------
 # B is chosen so that the last wavefront is partially filled for P = 2 and 3.
 
+# "rows": the factorization with a problem per 16-lane row (the default);
+# "groups": the lane-group factorization (TMPC_FLAG_FACTOR_GROUPS)
+@pytest.mark.parametrize("factor", ["rows", "groups"])
 @pytest.mark.parametrize("P", [1, 2, 3])
 @pytest.mark.parametrize("shape", [(13, 21, 6, 4, 2), (8, 11, 17, 13, 4), (7, 13, 9, 6, 5), (5, 9, 16, 12, 0)])
-def test_admm_stream_kernel_fp64_matches_oracle(P, shape):
+def test_admm_stream_kernel_fp64_matches_oracle(P, shape, factor):
     B, T, n, nx, m = shape
     qp = random_qp(B, T, n, nx, m, seed=51, std=True)
     # residual pass every 3 iterations (no adaptation): exercises the
     # residual sweep without changing the fixed-iteration trajectory
     cfg = oracle.OracleCfg(max_iter=20, check_every=3, adapt_rho_every=0, sigma=1e-6, eps_abs=1e-12,
                            eps_rel=1e-12, rho_f_factor=1000.0, alpha=1.6)
-    ref, it_ref, _, out, stats = _run_pair(qp, cfg, torch.float64, kernel_flags=_lib.flag_stream_p(P))
+    flags = _lib.flag_stream_p(P) | (_lib.FLAG_FACTOR_GROUPS if factor == "groups" else 0)
+    ref, it_ref, _, out, stats = _run_pair(qp, cfg, torch.float64, kernel_flags=flags)
     np.testing.assert_array_equal(stats.num_iter.cpu().numpy(), it_ref)
     _assert_state_close(out, ref, 1e-9)
 

@@ -37,6 +37,7 @@ def flag_stream_p(p: int) -> int:
 
 
 PCG_KERNEL_DPP, PCG_KERNEL_LDS, PCG_KERNEL_CHUNK = 1, 2, 3
+FLAG_FACTOR_GROUPS = 1 << 12  # the lane-group factorization (cross-checks)
 
 
 def flag_pcg_kernel(k: int) -> int:

@@ -12,6 +12,7 @@
 #include "common.hpp"
 #include "factor.hpp"
 #include "pcg.hpp"
+#include "factor_rows.hpp"
 #include "pcg_lds.hpp"
 #include "obstacle.hpp"
 #include "quadrotor.hpp"
@@ -278,10 +279,35 @@ void launch_factor_std_nc(hipStream_t s, const Dims& d, const DirectWs<R>& w, co
   }
 }
 
-// fp64 factorization from the stage records (explicit-integrator structure)
+template <typename R, int NC, int NR>
+void launch_factor_row_nc(hipStream_t s, const Dims& d, const DirectWs<R>& w, const QPDev<R>& q, const R* rho,
+                          R sigma, R rho_f_factor, int32_t* ctl, bool diag) {
+  constexpr int per_wave = kWave / kFacRow;
+  const int grid = (d.B + per_wave - 1) / per_wave;
+  hipLaunchKernelGGL((factor_row_kernel<R, NC, NR>), dim3(grid), dim3(kWave), 0, s, d, (const R*)w.am,
+                     (const R*)w.dm, q.A0, rho, sigma, rho_f_factor, ctl, w.thinv, diag ? 1 : 0);
+}
+
+// fp64 factorization from the stage records (explicit-integrator structure):
+// one problem per 16-lane row (factor_rows.hpp), or with `groups` the
+// lane-group kernel with P problems per wavefront
 template <typename R>
 int launch_factor_std(hipStream_t s, const Dims& d, const DirectWs<R>& w, const QPDev<R>& q, const R* rho,
-                      R sigma, R rho_f_factor, int32_t* ctl, int P, bool diag) {
+                      R sigma, R rho_f_factor, int32_t* ctl, int P, bool diag, bool groups = false) {
+  if (!groups) {
+    switch (d.n) {
+      case 6: launch_factor_row_nc<R, 6, 6>(s, d, w, q, rho, sigma, rho_f_factor, ctl, diag); break;
+      case 9:
+        if (stream_wide(d))
+          launch_factor_row_nc<R, 9, kWideRows>(s, d, w, q, rho, sigma, rho_f_factor, ctl, diag);
+        else
+          launch_factor_row_nc<R, 9, 9>(s, d, w, q, rho, sigma, rho_f_factor, ctl, diag);
+        break;
+      case 16: launch_factor_row_nc<R, 16, 16>(s, d, w, q, rho, sigma, rho_f_factor, ctl, diag); break;
+      default: launch_factor_row_nc<R, 17, 17>(s, d, w, q, rho, sigma, rho_f_factor, ctl, diag); break;
+    }
+    return launch_status();
+  }
   switch (d.n) {
     case 6: launch_factor_std_nc<R, 6>(s, d, w, q, rho, sigma, rho_f_factor, ctl, P, diag); break;
     case 9:
@@ -401,6 +427,7 @@ int admm_direct_impl(hipStream_t s, const tmpc_dims* dims, const tmpc_qp* qp,
   const bool std_dyn = (cfg->flags & TMPC_FLAG_STD_DYNAMICS) != 0;
   const int sp = stream_problems_per_wave(d.B, cfg->flags);
   const int fp = factor_problems_per_wave(d.B, cfg->flags);
+  const bool fgroups = (cfg->flags & TMPC_FLAG_FACTOR_GROUPS) != 0;
   const bool diag = (cfg->flags & TMPC_FLAG_DIAG_COST) != 0;
   const bool stream = std_dyn && (cfg->flags & TMPC_FLAG_GENERIC_KERNEL) == 0 && stream_ok<R>(d, sp, diag);
   if (sq && !stream) {
@@ -428,13 +455,13 @@ int admm_direct_impl(hipStream_t s, const tmpc_dims* dims, const tmpc_qp* qp,
                          a.qp.Am, a.qp.c, a.qp.G, a.qp.l, a.qp.u, w.am, w.rv, diag ? 1 : 0);
     st = launch_status();
     if (st) return st;
-    st = launch_factor_std<R>(s, d, w, a.qp, a.st.rho, a.sigma, a.rho_f_factor, nullptr, fp, diag);
+    st = launch_factor_std<R>(s, d, w, a.qp, a.st.rho, a.sigma, a.rho_f_factor, nullptr, fp, diag, fgroups);
   } else if (stream) {
     hipLaunchKernelGGL((stage_pack_kernel<R>), dim3(d.B, d.T), dim3(kWave), 0, s, d, a.qp, a.st, w.am, w.rv, w.dm,
                        diag ? 1 : 0);
     st = launch_status();
     if (st) return st;
-    st = launch_factor_std<R>(s, d, w, a.qp, a.st.rho, a.sigma, a.rho_f_factor, nullptr, fp, diag);
+    st = launch_factor_std<R>(s, d, w, a.qp, a.st.rho, a.sigma, a.rho_f_factor, nullptr, fp, diag, fgroups);
   } else {
     st = launch_factor_qp<R>(s, d, a.qp, a.st.rho, a.sigma, a.rho_f_factor, nullptr, w.thinv);
   }
@@ -443,7 +470,7 @@ int admm_direct_impl(hipStream_t s, const tmpc_dims* dims, const tmpc_qp* qp,
   if (g_iter_events[0] && hipEventRecord(g_iter_events[0], s) != hipSuccess) return TMPC_ELAUNCH;
   for (size_t c = 0; c + 1 < bounds.size(); ++c) {
     if (c > 0) {
-      st = stream ? launch_factor_std<R>(s, d, w, a.qp, a.st.rho, a.sigma, a.rho_f_factor, w.ctl, fp, diag)
+      st = stream ? launch_factor_std<R>(s, d, w, a.qp, a.st.rho, a.sigma, a.rho_f_factor, w.ctl, fp, diag, fgroups)
                   : launch_factor_qp<R>(s, d, a.qp, a.st.rho, a.sigma, a.rho_f_factor, w.ctl, w.thinv);
       if (st) return st;
     }
