@@ -222,6 +222,17 @@ __device__ __forceinline__ double fac_dot(const double (&w)[N], double s) {
   return row_dot_dpp(v, s);
 }
 
+// 1/d by the hardware reciprocal estimate refined with two Newton-Raphson
+// steps r <- r + r (1 - d r) (each roughly squares the relative error; d is
+// a pivot of an SPD block, far from the denormal and overflow ranges)
+__device__ __forceinline__ double recip(double d) {
+  double r = __builtin_amdgcn_rcp(d);
+  double e = __builtin_fma(-d, r, 1.0);
+  r = __builtin_fma(r, e, r);
+  e = __builtin_fma(-d, r, 1.0);
+  return __builtin_fma(r, e, r);
+}
+
 template <int KP, int NL, typename F>
 __device__ __forceinline__ void static_for_pivots(F&& f) {
   if constexpr (KP < NL) {
@@ -248,10 +259,12 @@ __global__ __launch_bounds__(kWave, 1) void factor_row_kernel(Dims d, const R* _
   const int braw = blockIdx.x * (kWave / W) + q;
   const bool real = braw < B;
   const int b = real ? braw : B - 1;
-  const bool lrow = i < NL;          // the lane holds a row
-  const int ic = lrow ? i : 0;       // clamped row index for loads
+  const bool lrow = NL == W || i < NL;  // the lane holds a row
+  const int ic = lrow ? i : 0;          // clamped row index for loads
+  const int arow = min(ic, nr - 1);     // the M row read as the lane's A row (used for i < nx only)
   if (ctl != nullptr && __ballot(real && ctl[b * 4 + 2] != 0) == 0) return;  // nothing flagged here
-  __shared__ C sym[kWave / W][W][W + 1];
+  __shared__ C sym[kWave / W][W][W + 1];  // the lane rows (and column 16) of each problem
+  __shared__ C d16s[kWave / W];            // Theta^{-1}[16][16] (n = 17)
   const C rho_i = (C)rho[b], rho_f = rho_i * (C)rho_f_factor, sig = (C)sigma;
 
   // ---- stage records of the next stage, prefetched into registers ------------------
@@ -259,13 +272,21 @@ __global__ __launch_bounds__(kWave, 1) void factor_row_kernel(Dims d, const R* _
   auto load = [&](int t) __attribute__((always_inline)) {
     const R* M = am + ((size_t)t * B + b) * rg.amp;
     const R* Dr = dm + ((size_t)t * B + b) * rg.dmp;
+    // idle lanes read column 0 (their rows are zeroed where theta_t is built);
+    // lanes i >= nx read a G row as their A row, which only their own unused
+    // Schur values see
 #pragma unroll
     for (int r = 0; r < NR; ++r) {
-      pMc[r] = (r < nr && lrow) ? M[r * n + ic] : R(0);
-      if (IMP) pM16[r] = r < nr ? M[r * n + (n - 1)] : R(0);
+      if (r < nr) {
+        pMc[r] = M[r * n + ic];
+        if (IMP) pM16[r] = M[r * n + (n - 1)];
+      } else {
+        pMc[r] = R(0);
+        if (IMP) pM16[r] = R(0);
+      }
     }
 #pragma unroll
-    for (int k = 0; k < NC; ++k) pAr[k] = (lrow && i < nx) ? M[ic * n + k] : R(0);
+    for (int k = 0; k < NC; ++k) pAr[k] = M[arow * n + k];
     if (diag) {
 #pragma unroll
       for (int k = 0; k < NC; ++k) pD[k] = R(0);
@@ -295,20 +316,28 @@ __global__ __launch_bounds__(kWave, 1) void factor_row_kernel(Dims d, const R* _
     C sv[NC];
 #pragma unroll
     for (int s = 0; s < NC; ++s) sv[s] = C(0);
-    if (t > 0) {
+    if (t > 0 && !IMP) {
 #pragma unroll
       for (int s = 0; s < NC; ++s) {
         if (s < nx) {
-          C y = fac_dot<NC>(a, Mc[s]);  // Y[i][s]
-          if (IMP) y += a[NC - 1] * M16[s];
-          C sc = fac_dot<NC>(Ar, y);    // sum over the lane rows j of A[i][j] Y[j][s]
-          if (IMP) {
-            const C y16 = row_sum(a[NC - 1] * Mc[s]) + a16 * M16[s];  // Y[16][s]
-            sc += Ar[NC - 1] * y16;
-          }
-          sv[s] = sc;
+          const C y = fac_dot<NC>(a, Mc[s]);  // Y[i][s] = (Theta^{-1} A^T)[i][s]
+          sv[s] = fac_dot<NC>(Ar, y);         // sum_j A[i][j] Y[j][s]
         }
       }
+    }
+    if (t > 0 && IMP) {
+      // n = 17: U = A Theta^{-1} from lane i's A row (row 16 of Theta^{-1} is
+      // the lanes' column 16), then S[i][s] = sum_k U[i][k] A[s][k]
+      C u[NC];
+#pragma unroll
+      for (int k = 0; k < NC - 1; ++k) {
+        u[k] = fac_dot<NC>(Ar, a[k]);
+        u[k] += Ar[NC - 1] * row_bcast_at(a[NC - 1], k);  // A[i][16] Theta^{-1}[16][k]
+      }
+      u[NC - 1] = fac_dot<NC>(Ar, a[NC - 1]) + Ar[NC - 1] * a16;
+#pragma unroll
+      for (int s = 0; s < NC; ++s)
+        if (s < nx) sv[s] = fac_dot<NC>(u, Mc[s]) + u[NC - 1] * M16[s];
     }
 
     // this stage's records
@@ -326,13 +355,15 @@ __global__ __launch_bounds__(kWave, 1) void factor_row_kernel(Dims d, const R* _
     if (IMP) D16 = (C)pD16;
     if (t + 1 < T) load(t + 1);
 
-    // theta_t row i (and Theta[16][16])
+    // theta_t row i (and Theta[16][16]); the diagonal terms D_ii (diagonal
+    // records), sigma and rho_f A_plus^T A_plus = rho_f diag(I_nx, 0) in one
     int ii = i;  // the comparisons with the lane's row index are made here
     __asm__ volatile("" : "+v"(ii));
+    const C dgl = (diag ? Dd[0] : C(0)) + sig + ((t > 0 && ii < nx) ? rho_f : C(0));
 #pragma unroll
     for (int k = 0; k < NC; ++k) {
-      const C dk = diag ? (k == ii ? Dd[0] : C(0)) : Dd[k];
-      a[k] = lrow ? dk + (k == ii ? sig : C(0)) : C(0);
+      const C off = diag ? C(0) : Dd[k];
+      a[k] = lrow ? (k == ii ? off + dgl : off) : C(0);
     }
     if (IMP) a16 = D16 + sig;
     const int r0 = t < N ? 0 : nx;  // the last stage has no dynamics rows
@@ -361,11 +392,11 @@ __global__ __launch_bounds__(kWave, 1) void factor_row_kernel(Dims d, const R* _
         }
       }
     }
-    const C f2 = rho_f * rho_f;
+    if (t > 0) {
+      const C fs = ii < nx ? rho_f * rho_f : C(0);  // the Schur term touches rows and columns < nx
 #pragma unroll
-    for (int k = 0; k < NC; ++k) {
-      if (t > 0 && k == ii && ii < nx) a[k] += rho_f;  // A_plus_{t-1}^T A_plus_{t-1} = diag(I_nx, 0)
-      if (t > 0 && k < nx && ii < nx) a[k] -= f2 * sv[k];
+      for (int k = 0; k < NC; ++k)
+        if (k < nx) a[k] -= fs * sv[k];
     }
 
     // symmetric sweep: minus the inverse, lane rows scaled by their pivots
@@ -373,7 +404,7 @@ __global__ __launch_bounds__(kWave, 1) void factor_row_kernel(Dims d, const R* _
     static_for_pivots<0, NL>([&](auto kc) __attribute__((always_inline)) {
       constexpr int KP = decltype(kc)::value;
       const C dk = row_bcast<KP>(a[KP]);
-      const C ip = C(1) / dk;
+      const C ip = recip(dk);
       const bool me = ii == KP;
       const C f = a[KP];
       const C g = me ? C(0) : -f * ip;
@@ -387,7 +418,7 @@ __global__ __launch_bounds__(kWave, 1) void factor_row_kernel(Dims d, const R* _
     });
     if (IMP) {
       // pivot 16: its row is the lanes' column 16 (true values: scaled back)
-      const C ip = C(1) / a16;
+      const C ip = recip(a16);
       const C f = a[NC - 1];
       const C tr = f * myip;
       fac_axpy<NC>(a, tr, -f * ip);
@@ -401,21 +432,31 @@ __global__ __launch_bounds__(kWave, 1) void factor_row_kernel(Dims d, const R* _
     // symmetric part of the lane block: row i averaged with column i
 #pragma unroll
     for (int k = 0; k < NL; ++k) sym[q][i][k] = a[k];
+    if (IMP) {
+      sym[q][i][NC - 1] = a[NC - 1];
+      if (i == 0) d16s[q] = a16;
+    }
     __syncthreads();
 #pragma unroll
     for (int k = 0; k < NL; ++k) a[k] = lrow ? C(0.5) * (a[k] + sym[q][k][i]) : C(0);
-    __syncthreads();
-
-    if (real && lrow) {
+    // the packed lower triangle, the problem's 16 lanes striding it (element e
+    // is (r, c) with r (r + 1) / 2 <= e, c = e - r (r + 1) / 2; the square
+    // root of 8 e + 1 < 1300 is exact at the row starts and at least 1/70 from
+    // the next odd integer elsewhere)
+    if (real) {
       R* out = thinv + ((size_t)t * B + b) * PITCH;
-#pragma unroll
-      for (int k = 0; k < NL; ++k)
-        if (k <= ii) out[pidx(ii, k)] = (R)a[k];
-      if (IMP) {
-        out[pidx(n - 1, ii)] = (R)a[NC - 1];
-        if (ii == 0) out[pidx(n - 1, n - 1)] = (R)a16;
+      for (int e = i; e < packed_size(NC); e += W) {
+        const int r = (int)((__builtin_sqrtf((float)(8 * e + 1)) - 1.0f) * 0.5f);
+        const int c = e - ((r * (r + 1)) >> 1);
+        C v;
+        if (IMP && r == NC - 1)
+          v = c == NC - 1 ? d16s[q] : sym[q][c][NC - 1];
+        else
+          v = C(0.5) * (sym[q][r][c] + sym[q][c][r]);
+        out[e] = (R)v;
       }
     }
+    __syncthreads();
   }
   if (ctl != nullptr && real && i == 0) ctl[b * 4 + 2] = 0;
 }
