@@ -352,7 +352,7 @@ def run_sqp_workload(args, dev):
         achieved, None if c4 else measured_traffic(),
         f"admm_stream_kernel (one launch = {args.admm_iters} ADMM iterations of the batch)", iter_bytes,
         iter_avg_s * 1e3,
-        qp_solve={"kernels": "stage_pack + factor_std + admm_stream + stage_unpack", "algorithmic_bytes": per_qp * B,
+        qp_solve={"kernels": "stage_pack + factor_row + admm_stream + stage_unpack", "algorithmic_bytes": per_qp * B,
                   "avg_ms": solve_avg_s * 1e3, "achieved": qp_achieved, "frac": qp_achieved / HBM_PEAK_GBS})
     return line
 
@@ -420,7 +420,7 @@ def run_config5(args, dev):
     line["roofline"] = roofline(
         achieved, None, f"admm_stream_kernel, fp64 (one launch = {K} ADMM iterations of the batch)", iter_bytes,
         iter_avg_s * 1e3,
-        qp_solve={"kernels": "stage_pack + factor_std + admm_stream + stage_unpack", "algorithmic_bytes": per_qp * B,
+        qp_solve={"kernels": "stage_pack + factor_row + admm_stream + stage_unpack", "algorithmic_bytes": per_qp * B,
                   "avg_ms": solve_avg_s * 1e3, "achieved": per_qp * B / solve_avg_s / 1e9,
                   "frac": per_qp * B / solve_avg_s / 1e9 / HBM_PEAK_GBS})
     return line
