@@ -35,6 +35,7 @@
 // the written state once.
 #pragma once
 #include "admm_direct.hpp"
+#include "stream_dpp.hpp"
 
 namespace tmpc {
 
@@ -477,6 +478,74 @@ __device__ __forceinline__ R lsym(const R* Th, int i, const R* v) {
   return acc;
 }
 
+// A group vector operand of the products below: with D (one or two problems
+// per wavefront, groups on 16-lane row boundaries) the lanes' values seen
+// through DPP row broadcasts (stream_dpp.hpp), otherwise the LDS slot the
+// lanes wrote it to (read after the next LDS ordering point).
+template <typename R, bool D>
+struct GVec;
+template <typename R>
+struct GVec<R, true> {
+  RowPair<R> v;
+};
+template <typename R>
+struct GVec<R, false> {
+  const R* s;
+};
+
+// Lane i's element v of a vector of at most NL elements.  D: all lanes of
+// the wavefront must be active (a 17-lane group's element 16 crosses rows).
+template <bool D, int NL, typename R>
+__device__ __forceinline__ GVec<R, D> gvec(R v, R* slot, int i) {
+  if constexpr (D) {
+    if constexpr (NL > 16)
+      return {row_pair(v)};
+    else
+      return {RowPair<R>{v, v}};
+  } else {
+    slot[i] = v;
+    return {slot};
+  }
+}
+
+// lrow / lcol / lsym with a group vector operand.  D: the block entries are
+// read from LDS as before, the vector comes by DPP, and every lane of the
+// wavefront must be active.
+template <typename R, int NC, bool D>
+__device__ __forceinline__ R mrow(const R* A, int i, const GVec<R, D>& v) {
+  if constexpr (D) {
+    R ak[NC];
+#pragma unroll
+    for (int k = 0; k < NC; ++k) ak[k] = A[i * NC + k];
+    return dot_pair(ak, v.v);
+  } else {
+    return lrow<R, NC>(A, i, v.s);
+  }
+}
+template <typename R, int NC, int NR, bool D>
+__device__ __forceinline__ R mcol(const R* A, int i, const GVec<R, D>& v) {
+  if constexpr (D) {
+    R ak[NR];
+#pragma unroll
+    for (int r = 0; r < NR; ++r) ak[r] = A[r * NC + i];
+    return dot_pair(ak, v.v);
+  } else {
+    return lcol<R, NC, NR>(A, 0, i, v.s);
+  }
+}
+template <typename R, int NC, bool D>
+__device__ __forceinline__ R msym(const R* Th, int i, const GVec<R, D>& v) {
+  if constexpr (D) {
+    R ak[NC];
+    const int ri = (i * (i + 1)) >> 1;
+#pragma unroll
+    for (int k = 0; k < NC; ++k) ak[k] = Th[k <= i ? ri + k : ((k * (k + 1)) >> 1) + i];
+    return dot_pair(ak, v.v);
+  } else {
+    return lsym<R, NC>(Th, i, v.s);
+  }
+}
+
 // Visits t = 0..T-1 (fwd) or T-1..0 in batches of D: stage batch k from
 // registers into LDS slots, issue the loads of batch k+1, compute batch k.
 template <int D, typename Regs, typename Ld, typename St, typename Cp>
@@ -489,7 +558,7 @@ __device__ __forceinline__ void run_sweep(int T, bool fwd, Ld&& load, St&& stage
 #pragma unroll
     for (int j = 0; j < D; ++j)
       if (k0 + j < T) stage(nxt[j], j);
-    wsync();
+    lds_order();
 #pragma unroll
     for (int j = 0; j < D; ++j)
       if (k0 + D + j < T) load(nxt[j], fwd ? k0 + D + j : T - 1 - (k0 + D + j));
@@ -525,6 +594,9 @@ __global__ __launch_bounds__(kWave, StreamOcc<R>::waves) void admm_stream_kernel
   // first nx + m the stacked constraint rows
   const Group G = make_group_strided(NL, P, B);
   const int b = G.prob, i = G.lane, p = G.gid, base = p * (kWave / P), tid = threadIdx.x;
+  // group vectors by DPP row broadcasts (groups at lane offsets 0 and 32)
+  // or through LDS slots (three groups at offsets 0, 21, 42)
+  constexpr bool DV = P <= 2;
   const int b0 = blockIdx.x * P;
   const int nprob = min(P, B - b0);
   const int nch_th = nprob * PITCH / W, nch_am = nprob * amp / W, nch_rv = nprob * rvp / W;
@@ -585,7 +657,7 @@ __global__ __launch_bounds__(kWave, StreamOcc<R>::waves) void admm_stream_kernel
   // ---- LDS starts zeroed (the column products rely on finite data past the
   // blocks); resident data: A0 in LDS, c0 / y_f0 in registers ---------------
   for (int e = tid; e < L.total / W; e += kWave) reinterpret_cast<V*>(lds)[e] = V{};
-  wsync();
+  lds_order();
   for (int e = tid; e < nprob * n0 * n; e += kWave) lds[L.a0 + e] = a.A0[(size_t)b0 * n0 * n + e];
   const R c0v = (i < n0) ? a.c0[(size_t)b * n0 + i] : R(0);
   R yf0v = (i < n0) ? a.y_f0[(size_t)b * n0 + i] : R(0);
@@ -609,7 +681,7 @@ __global__ __launch_bounds__(kWave, StreamOcc<R>::waves) void admm_stream_kernel
   R rho = a.rho[b];
   const bool slack = a.use_slack && m > 0;
   const R gs = (slack && a.slack_w) ? a.slack_w[b] : R(0);
-  wsync();
+  lds_order();
 
   // ---- gamma_t for the current state and rho (compute_gamma, admm.py:157-174),
   // and, in the first chunk of an SQP step, the first-order check of the input
@@ -627,8 +699,9 @@ __global__ __launch_bounds__(kWave, StreamOcc<R>::waves) void admm_stream_kernel
     R c_st = R(0), c_eq = R(0), c_iq = R(0), c_sl = R(0);  // this lane's maxima
     R pend = R(0);  // (A_minus_{t-1} x_{t-1} - c_{t-1})[i], awaiting -x_t
     R yfp = R(0);   // y_f_{t-1}[i]
-    sc0[i] = rho_f * c0v - yf0v;  // 0 past n0
-    if (fochk) sy0[i] = yf0v;     // 0 past n0
+    const GVec<R, DV> vc0 = gvec<DV, NL>(rho_f * c0v - yf0v, sc0, i);  // 0 past n0
+    GVec<R, DV> vy0{};
+    if (fochk) vy0 = gvec<DV, NL>(yf0v, sy0, i);  // 0 past n0
     run_sweep<1, GRegs>(
         T, true,
         [&](GRegs& r, int t) {
@@ -649,31 +722,39 @@ __global__ __launch_bounds__(kWave, StreamOcc<R>::waves) void admm_stream_kernel
           const R czv = rv[rg.cz + icr], yv = crow ? rv[rg.y + icr] : R(0);
           const R sct = crow ? (dyn ? rho_f : rho) * czv - yv : R(0);
           const R xv = rv[rg.x + icn];
-          sc[i] = sct;  // 0 past nr
+          const auto vc = gvec<DV, NL>(sct, sc, i);  // 0 past nr
+          GVec<R, DV> vx{}, vy{};
           if (fochk) {
-            sx[i] = xv;
-            sy[i] = yv;  // [y_f_t; y_g], 0 past nr
+            vx = gvec<DV, NL>(xv, sx, i);
+            vy = gvec<DV, NL>(yv, sy, i);  // [y_f_t; y_g], 0 past nr
           }
-          wsync();
+          lds_order();
           {
             R gv = sigma * xv - rv[rg.q + icn];
-            gv += lcol<R, NC, NL>(mt, nr, icn, sc);
+            gv += mcol<R, NC, NL, DV>(mt, icn, vc);
             if (t > 0) gv -= (i < nx) ? scp : R(0);  // A_plus_{t-1}^T = [-I; 0]
-            if (t == 0) gv += lcol<R, NC, NC>(a0p, n0, icn, sc0);
+            if (t == 0) gv += mcol<R, NC, NC, DV>(a0p, icn, vc0);
             if (i < n) wgp[t * n + i] = gv;
           }
           if (fochk) {
             const R* dmt = dmS(j) + p * dmp;
-            const R px = diagD ? dmt[icn] * xv : lsym<R, NC>(dmt, icn, sx);
-            R aty = lcol<R, NC, NL>(mt, nr, icn, sy);  // A_minus_t^T y_f_t + G_t^T y_g
-            if (t == 0) aty += lcol<R, NC, NC>(a0p, n0, icn, sy0);
+            R px;
+            if (diagD)
+              px = dmt[icn] * xv;
+            else
+              px = msym<R, NC, DV>(dmt, icn, vx);
+            R aty = mcol<R, NC, NL, DV>(mt, icn, vy);  // A_minus_t^T y_f_t + G_t^T y_g
+            if (t == 0) aty += mcol<R, NC, NC, DV>(a0p, icn, vy0);
             if (t > 0) aty -= dyn ? yfp : R(0);  // A_plus_{t-1}^T y_f_{t-1}
             c_st = rmax(c_st, i < n ? rabs(px + rv[rg.q + icn] + aty) : R(0));
-            const R mxv = lrow<R, NC>(mt, icr, sx);
+            const R mxv = mrow<R, NC, DV>(mt, icr, vx);
             // dynamics row t-1 is complete with -x_t
             if (t > 0) c_eq = rmax(c_eq, dyn ? rabs(pend - xv) : R(0));
             pend = (dyn && t < N) ? mxv - czv : R(0);
-            if (t == 0 && i < n0) c_eq = rmax(c_eq, rabs(lrow<R, NC>(a0p, i, sx) - c0v));
+            if (t == 0) {  // every lane computes (DPP); rows past n0 are discarded
+              const R a0x = mrow<R, NC, DV>(a0p, min(i, n0 - 1), vx);
+              if (i < n0) c_eq = rmax(c_eq, rabs(a0x - c0v));
+            }
             const R xiv = rv[rg.xi + ji];
             const R g = mxv + (slack ? xiv : R(0));
             const R viol = rmax(rmax(rv[rg.l + ji] - g, g - rv[rg.u + ji]), R(0));
@@ -683,7 +764,7 @@ __global__ __launch_bounds__(kWave, StreamOcc<R>::waves) void admm_stream_kernel
             yfp = (dyn && t < N) ? yv : R(0);
           }
           scp = sct;
-          wsync();
+          lds_order();
         });
     if (fochk) {
       // group maxima (every lane of a group reduces its group: the result
@@ -693,13 +774,13 @@ __global__ __launch_bounds__(kWave, StreamOcc<R>::waves) void admm_stream_kernel
       red[1 * kWave + tid] = c_eq;
       red[2 * kWave + tid] = c_iq;
       red[3 * kWave + tid] = c_sl;
-      wsync();
+      lds_order();
       R mxs[4] = {R(0), R(0), R(0), R(0)};
 #pragma unroll
       for (int k = 0; k < 4; ++k)
 #pragma unroll
         for (int l = 0; l < NL; ++l) mxs[k] = rmax(mxs[k], red[k * kWave + base + l]);
-      wsync();
+      lds_order();
       const R conv = rmax(rmax(mxs[0], mxs[1]), rmax(mxs[2], mxs[3]));
       const bool act = (a.act_in ? a.act_in[b] != 0 : true) && conv > a.chk_tol;
       if (G.live && i == 0) {
@@ -755,13 +836,13 @@ __global__ __launch_bounds__(kWave, StreamOcc<R>::waves) void admm_stream_kernel
             // lanes past n compute throwaway values in their own vector slots
             R rr = i < n ? wgp[t * n + i] : R(0);
             if (t > 0) rr += (i < nx) ? rho_f * v : R(0);
-            sr[i] = rr;
-            wsync();
-            const R wv = lsym<R, NC>(thS(j) + p * PITCH, icn, sr);
+            const auto vr = gvec<DV, NL>(rr, sr, i);
+            lds_order();
+            const R wv = msym<R, NC, DV>(thS(j) + p * PITCH, icn, vr);
             if (i < n) wgp[t * n + i] = wv;
-            sx[i] = wv;
-            wsync();
-            if (t < N) v = lrow<R, NC>(amS(j) + p * amp, icr, sx);
+            const auto vw = gvec<DV, NL>(wv, sx, i);
+            lds_order();
+            if (t < N) v = mrow<R, NC, DV>(amS(j) + p * amp, icr, vw);
           });
     }
 
@@ -773,7 +854,7 @@ __global__ __launch_bounds__(kWave, StreamOcc<R>::waves) void admm_stream_kernel
     // (-xt_t), the only dependence between stages) together with the rest of
     // stage t (B: constraint products, relaxation, projection, duals, the next
     // gamma_t, residual terms), which needs xt_t only.  A and B share each of
-    // the three barrier-separated regions of a step, so their LDS round trips
+    // the three regions of a step (separated by LDS ordering points), so their LDS round trips
     // overlap.  LDS slots: Theta^{-1} of stage t-1; M of stages t and t-1 (by
     // stage parity); rv and D of stage t.  Registers prefetch the next step's
     // runs (Theta^{-1}, M of t-2; rv, D of t-1).
@@ -815,9 +896,9 @@ __global__ __launch_bounds__(kWave, StreamOcc<R>::waves) void admm_stream_kernel
         }
         store_run<V, CH_RV>(prv, reinterpret_cast<V*>(rv_slot), nch_rv, spl);
         if (chk) store_run<V, CH_TH>(pdm, reinterpret_cast<V*>(dm_slot), nch_dm, spl);
-        su[i] = dyn ? -xa : R(0);  // A_plus_{t-1} xt_t, 0 past nx
-        sx[i] = xa;
-        wsync();
+        const auto vu = gvec<DV, NL>(dyn ? -xa : R(0), su, i);  // A_plus_{t-1} xt_t, 0 past nx
+        const auto vx = gvec<DV, NL>(xa, sx, i);
+        lds_order();
         if (t >= 2) {
           load_run<V, CH_TH>(pth, th_run(t - 2), nch_th);
           load_run<V, CH_AM>(pam, am_run(t - 2), nch_am);
@@ -834,13 +915,17 @@ __global__ __launch_bounds__(kWave, StreamOcc<R>::waves) void admm_stream_kernel
         // masks go past the range and are dropped
         const __amdgpu_buffer_rsrc_t rsg = __builtin_amdgcn_make_buffer_rsrc(
             rv0 + (unsigned)t * srv, (short)0, (int)(nprob * rvp * sizeof(R)), kBufferFlags);
-        if (hasA) ss[i] = rho_f * lcol<R, NC, NL>(mA, nx, icn, su);
+        GVec<R, DV> vs{};
+        if (hasA) vs = gvec<DV, NL>(rho_f * mcol<R, NC, NL, DV>(mA, icn, vu), ss, i);
         const bool drow = dyn && t < N;  // a live dynamics row of stage t
         const R u = drow ? -xn : R(0);   // (A_plus_t xt_{t+1})[i]
         // stacked C and G products of the pre-relaxation iterate
-        const R mx = lrow<R, NC>(mt, icr, sx);
+        const R mx = mrow<R, NC, DV>(mt, icr, vx);
         R cx0 = R(0);
-        if (t == 0 && i < n0) cx0 = lrow<R, NC>(a0p, i, sx);
+        if (t == 0) {  // every lane computes (DPP); rows past n0 are discarded
+          const R a0x = mrow<R, NC, DV>(a0p, min(i, n0 - 1), vx);
+          cx0 = i < n0 ? a0x : R(0);
+        }
         // over-relaxation
         const R xnew = alpha * xa + one_m_alpha * rv[rg.x + icn];
         buf_store(xnew, rsg, commit && i < n, rv_lane + rg.x + i);
@@ -874,18 +959,19 @@ __global__ __launch_bounds__(kWave, StreamOcc<R>::waves) void admm_stream_kernel
           yf0_r = yf0;
         }
         // next iteration's gamma (valid while rho is unchanged)
-        sc[i] = tgt;    // 0 past nr
-        sc0[i] = ct0;   // 0 past n0
+        const auto vc = gvec<DV, NL>(tgt, sc, i);  // 0 past nr
+        GVec<R, DV> vc0{}, vxn{}, vy{}, vy0{};
+        if (t == 0) vc0 = gvec<DV, NL>(ct0, sc0, i);  // 0 past n0
         if (chk) {
-          sxn[i] = xnew;
-          sy[i] = y_r;     // 0 past nr
-          sy0[i] = yf0_r;  // 0 past n0
+          vxn = gvec<DV, NL>(xnew, sxn, i);
+          vy = gvec<DV, NL>(y_r, sy, i);                  // 0 past nr
+          if (t == 0) vy0 = gvec<DV, NL>(yf0_r, sy0, i);  // 0 past n0
         }
-        wsync();
+        lds_order();
         // ---- region 3
         R xa_next = R(0);
         if (hasA) {
-          const R xv = wgp[(t - 1) * n + icn] - lsym<R, NC>(th_slot + p * PITCH, icn, ss);
+          const R xv = wgp[(t - 1) * n + icn] - msym<R, NC, DV>(th_slot + p * PITCH, icn, vs);
           xa_next = i < n ? xv : R(0);
         }
         if (t < N) {
@@ -894,8 +980,8 @@ __global__ __launch_bounds__(kWave, StreamOcc<R>::waves) void admm_stream_kernel
         }
         {
           R gv = sigma * xnew - rv[rg.q + icn];
-          gv += lcol<R, NC, NL>(mt, nr, icn, sc);
-          if (t == 0) gv += lcol<R, NC, NC>(a0p, n0, icn, sc0);
+          gv += mcol<R, NC, NL, DV>(mt, icn, vc);
+          if (t == 0) gv += mcol<R, NC, NC, DV>(a0p, icn, vc0);
           gp = gv;
         }
         if (chk) {
@@ -907,7 +993,7 @@ __global__ __launch_bounds__(kWave, StreamOcc<R>::waves) void admm_stream_kernel
             nAty = rmax(nAty, drow ? rabs(aty) : R(0));
           }
           // stacked primal rows of the relaxed iterate
-          const R m1 = lrow<R, NC>(mt, icr, sxn);
+          const R m1 = mrow<R, NC, DV>(mt, icr, vxn);
           {
             const R cx1 = m1 - xnn;  // A_minus_t x_t - x_{t+1}, dynamics rows
             rp = rmax(rp, drow ? rabs(cx1 - cv) : (ineq ? rabs(m1 - z_r) : R(0)));
@@ -921,18 +1007,24 @@ __global__ __launch_bounds__(kWave, StreamOcc<R>::waves) void admm_stream_kernel
               nyg = rmax(nyg, ineq ? rabs(y_r) : R(0));
             }
           }
-          if (t == 0 && i < n0) {
-            const R cx1 = lrow<R, NC>(a0p, i, sxn);
-            rp = rmax(rp, rabs(cx1 - c0v));
-            nCx = rmax(nCx, rabs(cx1));
-            nc = rmax(nc, rabs(c0v));
+          if (t == 0) {  // every lane computes (DPP); rows past n0 are discarded
+            const R cx1 = mrow<R, NC, DV>(a0p, min(i, n0 - 1), vxn);
+            if (i < n0) {
+              rp = rmax(rp, rabs(cx1 - c0v));
+              nCx = rmax(nCx, rabs(cx1));
+              nc = rmax(nc, rabs(c0v));
+            }
           }
           {
             const R* dmt = dm_slot + p * dmp;
-            const R px = diagD ? dmt[icn] * xnew : lsym<R, NC>(dmt, icn, sxn);
+            R px;
+            if (diagD)
+              px = dmt[icn] * xnew;
+            else
+              px = msym<R, NC, DV>(dmt, icn, vxn);
             R aty = R(0);
-            if (t == 0) aty += lcol<R, NC, NC>(a0p, n0, icn, sy0);
-            aty += lcol<R, NC, NL>(mt, nr, icn, sy);  // A_minus_t^T y_f_t + G_t^T y_g_t
+            if (t == 0) aty += mcol<R, NC, NC, DV>(a0p, icn, vy0);
+            aty += mcol<R, NC, NL, DV>(mt, icn, vy);  // A_minus_t^T y_f_t + G_t^T y_g_t
             const R qv = rv[rg.q + icn];
             const bool wait = t > 0 && dyn;  // awaits -y_f_{t-1}[i]
             pq_p = px + qv;
@@ -946,10 +1038,10 @@ __global__ __launch_bounds__(kWave, StreamOcc<R>::waves) void admm_stream_kernel
         xn = xa;
         xnn = xnew;
         xa = xa_next;
-        wsync();
+        lds_order();
       }
       if (i < n) wgp[i] = gp;
-      wsync();
+      lds_order();
     }
 
     // ---- residual reductions and adaptive rho (admm.py:392-556) --------------
@@ -959,7 +1051,7 @@ __global__ __launch_bounds__(kWave, StreamOcc<R>::waves) void admm_stream_kernel
       const R vals[11] = {rp, nCx, nc, nGx, nz, rd, nPx, nAty, nq, nxi, nyg};
 #pragma unroll
       for (int k = 0; k < 11; ++k) red[k * kWave + tid] = (i < NL) ? vals[k] : R(0);
-      wsync();
+      lds_order();
       // lane i of each group reduces values k = i, i + NL, ... over the group's
       // NL lanes (lanes past NL that land on k < 11 repeat a value of lane k - NL)
       R mx[(11 + NL - 1) / NL];
@@ -971,15 +1063,15 @@ __global__ __launch_bounds__(kWave, StreamOcc<R>::waves) void admm_stream_kernel
 #pragma unroll
           for (int l = 0; l < NL; ++l) mx[q] = rmax(mx[q], red[k * kWave + base + l]);
       }
-      wsync();
+      lds_order();
 #pragma unroll
       for (int q = 0; q < (11 + NL - 1) / NL; ++q)
         if (i + q * NL < 11) red[(i + q * NL) * kWave + base] = mx[q];
-      wsync();
+      lds_order();
       R r[11];
 #pragma unroll
       for (int k = 0; k < 11; ++k) r[k] = red[k * kWave + base];
-      wsync();
+      lds_order();
       const R np = rmax(rmax(r[1], r[3]), rmax(r[2], r[4]));
       R nd = rmax(rmax(r[6], r[7]), r[8]);
       if (slack) nd = rmax(nd, rmax(gs * r[9], r[10]));

@@ -333,6 +333,13 @@ __global__ __launch_bounds__(64) void nonfinite_flag_kernel(Dims d, StateDev<R> 
 // ordered by this barrier (a single-wave s_barrier is cheap on CDNA).
 __device__ __forceinline__ void wsync() { __syncthreads(); }
 
+// Orders LDS accesses between lanes of one wavefront without waiting: the LDS
+// unit executes one wavefront's instructions in issue order, so a read issued
+// after another lane's write returns the written value; only the compiler has
+// to keep the accesses in program order (the memory clobber), and each use of
+// a read still waits for its own data.  For single-wavefront workgroups only.
+__device__ __forceinline__ void lds_order() { asm volatile("" ::: "memory"); }
+
 // A wavefront is split into P = 64 / g groups of g lanes; group p owns one
 // problem and lane i of the group owns row i of every stage block.
 // Reads always use `prob` (clamped into [0, B) so a partially filled last
