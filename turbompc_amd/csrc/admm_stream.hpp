@@ -854,30 +854,48 @@ __global__ __launch_bounds__(kWave, StreamOcc<R>::waves) void admm_stream_kernel
     // (-xt_t), the only dependence between stages) together with the rest of
     // stage t (B: constraint products, relaxation, projection, duals, the next
     // gamma_t, residual terms), which needs xt_t only.  A and B share each of
-    // the three regions of a step (separated by LDS ordering points), so their LDS round trips
-    // overlap.  LDS slots: Theta^{-1} of stage t-1; M of stages t and t-1 (by
-    // stage parity); rv and D of stage t.  Registers prefetch the next step's
-    // runs (Theta^{-1}, M of t-2; rv, D of t-1).
+    // the three regions of a step (separated by LDS ordering points), so
+    // their LDS round trips overlap.  LDS slots: Theta^{-1} of stage t-1; M of
+    // stages t and t-1 (by stage parity); rv and D of stage t.  Registers
+    // prefetch the runs of step t - PFD (Theta^{-1}, M of t-PFD-1; rv, D of
+    // t-PFD) while step t computes.
     const bool chk = mod_zero(iter, a.check_every);
     R rp = 0, nCx = 0, nc = 0, nGx = 0, nz = 0, rd = 0, nPx = 0, nAty = 0, nq = 0, nxi = 0, nyg = 0;
     // per-iteration constants of the projection: y / rho as y * (1 / rho)
     const R inv_rho = R(1) / rho;
     const R frac = slack ? gs / (gs + rho) : R(0), xi_f = slack ? rho / (gs + rho) : R(0);
     {
-      V pth[CH_TH], pam[CH_AM], prv[CH_RV], pdm[CH_TH];
+      // PFD register sets, used by turns: the runs of step t - PFD are loaded
+      // while step t computes (two sets where the registers allow)
+      constexpr int PFD = P <= 2 ? 2 : 1;
+      struct BRegs {
+        V th[CH_TH], am[CH_AM], rv[CH_RV], dm[CH_TH];
+      };
+      BRegs ra, rb;
       auto amP = [&](int t) { return lds + L.am + (t & 1) * (P * amp); };
       R* th_slot = thS(0);
       R* rv_slot = rvS(0);
       R* dm_slot = dmS(0);
-      // prologue: M_{T-1} into its slot; registers <- Theta^{-1}, M of T-2 and rv, D of T-1
-      load_run<V, CH_AM>(pam, am_run(T - 1), nch_am);
-      store_run<V, CH_AM>(pam, reinterpret_cast<V*>(amP(T - 1)), nch_am, spl);
+      // prologue: M_{T-1} into its slot; ra <- Theta^{-1}, M of T-2 and rv, D
+      // of T-1 (step T-1); with two sets rb <- those of T-3 and T-2 (step T-2)
+      load_run<V, CH_AM>(ra.am, am_run(T - 1), nch_am);
+      store_run<V, CH_AM>(ra.am, reinterpret_cast<V*>(amP(T - 1)), nch_am, spl);
       if (T >= 2) {
-        load_run<V, CH_TH>(pth, th_run(T - 2), nch_th);
-        load_run<V, CH_AM>(pam, am_run(T - 2), nch_am);
+        load_run<V, CH_TH>(ra.th, th_run(T - 2), nch_th);
+        load_run<V, CH_AM>(ra.am, am_run(T - 2), nch_am);
       }
-      load_run<V, CH_RV>(prv, rv_run(T - 1), nch_rv);
-      if (chk) load_run<V, CH_TH>(pdm, dm_run(T - 1), nch_dm);
+      load_run<V, CH_RV>(ra.rv, rv_run(T - 1), nch_rv);
+      if (chk) load_run<V, CH_TH>(ra.dm, dm_run(T - 1), nch_dm);
+      if constexpr (PFD == 2) {
+        if (T >= 2) {
+          load_run<V, CH_RV>(rb.rv, rv_run(T - 2), nch_rv);
+          if (chk) load_run<V, CH_TH>(rb.dm, dm_run(T - 2), nch_dm);
+        }
+        if (T >= 3) {
+          load_run<V, CH_TH>(rb.th, th_run(T - 3), nch_th);
+          load_run<V, CH_AM>(rb.am, am_run(T - 3), nch_am);
+        }
+      }
       R xa = i < n ? wgp[N * n + i] : R(0);  // xt_t for the coming step (xt_N = w_N)
       R xn = R(0);   // xt_{t+1}[i]
       R xnn = R(0);  // relaxed x_{t+1}[i]
@@ -885,27 +903,28 @@ __global__ __launch_bounds__(kWave, StreamOcc<R>::waves) void admm_stream_kernel
       // dual residual row t+1 awaiting its A_plus_t^T y_f_t term (i < nx):
       // P x + q and the rest of C^T y + G^T y_g
       R pq_p = R(0), aty_p = R(0);
-      for (int t = T - 1; t >= 0; --t) {
+      auto step = [&](const int t, BRegs& pr) {
         const bool hasA = t >= 1;  // the recursion part of stage t-1 runs in this step
         // ---- region 1: stage the runs; su for A, sx for B.  Lanes past a
         // vector's length write zeros or throwaway values into their own
         // group's slot (never read as part of the vector).
         if (hasA) {
-          store_run<V, CH_TH>(pth, reinterpret_cast<V*>(th_slot), nch_th, spl);
-          store_run<V, CH_AM>(pam, reinterpret_cast<V*>(amP(t - 1)), nch_am, spl);
+          store_run<V, CH_TH>(pr.th, reinterpret_cast<V*>(th_slot), nch_th, spl);
+          store_run<V, CH_AM>(pr.am, reinterpret_cast<V*>(amP(t - 1)), nch_am, spl);
         }
-        store_run<V, CH_RV>(prv, reinterpret_cast<V*>(rv_slot), nch_rv, spl);
-        if (chk) store_run<V, CH_TH>(pdm, reinterpret_cast<V*>(dm_slot), nch_dm, spl);
+        store_run<V, CH_RV>(pr.rv, reinterpret_cast<V*>(rv_slot), nch_rv, spl);
+        if (chk) store_run<V, CH_TH>(pr.dm, reinterpret_cast<V*>(dm_slot), nch_dm, spl);
         const auto vu = gvec<DV, NL>(dyn ? -xa : R(0), su, i);  // A_plus_{t-1} xt_t, 0 past nx
         const auto vx = gvec<DV, NL>(xa, sx, i);
         lds_order();
-        if (t >= 2) {
-          load_run<V, CH_TH>(pth, th_run(t - 2), nch_th);
-          load_run<V, CH_AM>(pam, am_run(t - 2), nch_am);
+        // this set's next use is step t - PFD
+        if (t >= PFD + 1) {
+          load_run<V, CH_TH>(pr.th, th_run(t - PFD - 1), nch_th);
+          load_run<V, CH_AM>(pr.am, am_run(t - PFD - 1), nch_am);
         }
-        if (t >= 1) {
-          load_run<V, CH_RV>(prv, rv_run(t - 1), nch_rv);
-          if (chk) load_run<V, CH_TH>(pdm, dm_run(t - 1), nch_dm);
+        if (t >= PFD) {
+          load_run<V, CH_RV>(pr.rv, rv_run(t - PFD), nch_rv);
+          if (chk) load_run<V, CH_TH>(pr.dm, dm_run(t - PFD), nch_dm);
         }
         // ---- region 2
         const R* mA = amP(t - 1) + p * amp;  // M_{t-1} (A)
@@ -1039,6 +1058,11 @@ __global__ __launch_bounds__(kWave, StreamOcc<R>::waves) void admm_stream_kernel
         xnn = xnew;
         xa = xa_next;
         lds_order();
+      };
+      for (int t = T - 1; t >= 0; t -= PFD) {
+        step(t, ra);
+        if constexpr (PFD == 2)
+          if (t >= 1) step(t - 1, rb);
       }
       if (i < n) wgp[i] = gp;
       lds_order();
