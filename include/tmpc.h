@@ -65,11 +65,13 @@ typedef struct tmpc_state {
  * reading A_plus and E. */
 #define TMPC_FLAG_STD_DYNAMICS 1u
 /* With TMPC_FLAG_STD_DYNAMICS the direct solve streams stage records through
- * a batched kernel when the shape allows it (n in {6, 9, 16, 17}, nx < n, and
- * nx + m <= n with m <= 8, or n = 9 with nx + m <= 17 and m <= 12).  TMPC_FLAG_GENERIC_KERNEL selects the generic per-stage
- * kernel instead (same iteration; for cross-checks).  Bits 8-9 force the
- * number of problems per wavefront of the streaming kernel (1-3; 0 = chosen
- * from B). */
+ * a batched kernel when the shape allows it: n <= 17 and nx < n, with the
+ * records' block width w the smallest of 6, 9, 16, 17 that is >= n and holds
+ * nx + m <= w with m <= 8 (or w = 9 with nx + m <= 17 and m <= 12); for
+ * n < w the records carry w - n decoupled dummy variables, which never reach
+ * the state.  TMPC_FLAG_GENERIC_KERNEL selects the generic per-stage kernel
+ * instead (same iteration; for cross-checks).  Bits 8-9 force the number of
+ * problems per wavefront of the streaming kernel (1-3; 0 = chosen from B). */
 #define TMPC_FLAG_GENERIC_KERNEL 2u
 #define TMPC_FLAG_STREAM_P(p) (((uint32_t)(p) & 3u) << 8)
 /* tmpc_admm_pcg_* with TMPC_FLAG_STD_DYNAMICS runs the whole solve in one

@@ -13,6 +13,8 @@ implementations summing in different orders move rho by ~1e-9 relative and the
 iterates after the change by up to ~1e-6 (measured: oracle vs GPU rho differ by
 2e-9, states by 4e-7 one iteration later).
 """
+import dataclasses
+
 import numpy as np
 import pytest
 import torch
@@ -472,6 +474,91 @@ def test_admm_stream_kernel_wide_rows_match_generic_on_config4_batch():
     np.testing.assert_array_equal(s_a.num_iter.cpu().numpy(), it_ref)
     _assert_batch_matches_oracle("config 4 B=4099 wide stream", o_a, ref, TOL[torch.float32])
     _assert_batch_matches_oracle("config 4 B=4099 generic", o_b, ref, TOL[torch.float32])
+
+
+# block widths outside {6, 9, 16, 17}: the streaming path rounds n up to the
+# next width it is built for (n = 4 -> 6, 7 -> 9, 8 with 11 stacked rows -> the
+# wide 9, 12 and 14 -> 16); the extra variables are decoupled dummies in the
+# stage records and never reach the state
+PADDED_SHAPES = [(9, 11, 4, 2, 2), (10, 13, 7, 4, 3), (7, 9, 8, 5, 6), (6, 9, 12, 8, 4), (5, 7, 14, 10, 5)]
+
+
+def _gpu_solve(qp, cfg, dtype, **kw):
+    qpd = qp.to(DEV, dtype)
+    (_, _), stats, out = _solver(qp, cfg, **kw).solve(qpd, _state_to_dev(zero_state(qp, 0.1), dtype),
+                                                        alpha=cfg.alpha)
+    torch.cuda.synchronize()
+    return stats, out
+
+
+@pytest.mark.parametrize("P", [1, 2, 3])
+@pytest.mark.parametrize("shape", PADDED_SHAPES)
+@pytest.mark.parametrize("variant", ["dense", "diag", "groups"])
+def test_admm_stream_kernel_padded_width_fp64_matches_oracle(P, shape, variant):
+    B, T, n, nx, m = shape
+    diag = variant == "diag"
+    qp = random_qp(B, T, n, nx, m, seed=81, std=True, diag=diag)
+    cfg = oracle.OracleCfg(max_iter=20, check_every=3, adapt_rho_every=0, sigma=1e-6, eps_abs=1e-12,
+                           eps_rel=1e-12, rho_f_factor=1000.0, alpha=1.6)
+    kw = {"diag_cost": True} if diag else {}
+    flags = _lib.flag_stream_p(P) | (_lib.FLAG_FACTOR_GROUPS if variant == "groups" else 0)
+    ref, it_ref, _, out, stats = _run_pair(qp, cfg, torch.float64, kernel_flags=flags, **kw)
+    np.testing.assert_array_equal(stats.num_iter.cpu().numpy(), it_ref)
+    _assert_state_close(out, ref, 1e-9)
+    # the streaming kernels ran, not the generic one (same iterate, other rounding)
+    _, out_g = _gpu_solve(qp, cfg, torch.float64, kernel_flags=_lib.FLAG_GENERIC_KERNEL, **kw)
+    assert rel_err(out.x_blocks, out_g.x_blocks) < 1e-9
+    assert not torch.equal(out.x_blocks, out_g.x_blocks)
+
+
+@pytest.mark.parametrize("shape", [(10, 13, 7, 4, 3), (6, 9, 12, 8, 4)])
+def test_admm_stream_kernel_padded_width_adaptive_rho_fp32(shape):
+    B, T, n, nx, m = shape
+    qp = random_qp(B, T, n, nx, m, seed=82, std=True)
+    cfg = oracle.OracleCfg(max_iter=200, check_every=2, adapt_rho_every=4, sigma=1e-6, eps_abs=1e-6, eps_rel=1e-6,
+                           rho_f_factor=50.0, alpha=1.6, adaptive_rho_tolerance=1.5)
+    ref, it_ref, _, out, stats = _run_pair(qp, cfg, torch.float64, kernel_flags=_lib.flag_stream_p(2))
+    np.testing.assert_array_equal(stats.num_iter.cpu().numpy(), it_ref)
+    assert rel_err(out.rho_bar, ref.rho_bar) < 1e-7
+    _assert_state_close(out, ref, 1e-5)
+    # fp32 against the fp64 oracle at a fixed iteration count
+    cfg32 = oracle.OracleCfg(max_iter=30, check_every=31, adapt_rho_every=0, sigma=1e-6, eps_abs=1e-9,
+                             eps_rel=1e-9, rho_f_factor=1000.0, alpha=1.0)
+    ref32, _, _, out32, _ = _run_pair(qp, cfg32, torch.float32, kernel_flags=_lib.flag_stream_p(2))
+    _assert_state_close(out32, ref32, TOL[torch.float32])
+
+
+@pytest.mark.parametrize("shape", [(10, 13, 7, 4, 3), (7, 9, 8, 5, 6), (5, 7, 14, 10, 5)])
+@pytest.mark.parametrize("ineq", [False, True])
+def test_admm_stream_kernel_padded_width_warm_records(shape, ineq):
+    """An SQP step whose QP differs from the previous call's in A_minus and c
+    (and with ineq in G, l, u), on padded records: rewriting only those records
+    gives the iterate of a step that repacks everything, bit for bit."""
+    from turbompc_amd.solvers.admm.admm_hip_backend import direct_workspace
+
+    B, T, n, nx, m = shape
+    qp1 = random_qp(B, T, n, nx, m, seed=83, std=True).to(DEV, torch.float64)
+    qp2 = random_qp(B, T, n, nx, m, seed=84, std=True).to(DEV, torch.float64)
+    # qp2 keeps qp1's cost, initial rows and (without ineq) inequality rows
+    eq2 = dataclasses.replace(qp2.eq, A0=qp1.eq.A0, c0=qp1.eq.c0)
+    qp2 = dataclasses.replace(qp2, cost=qp1.cost, eq=eq2, ineq=qp2.ineq if ineq else qp1.ineq)
+    cfg = oracle.OracleCfg(max_iter=15, check_every=16, adapt_rho_every=0, sigma=1e-6, eps_abs=1e-12,
+                           eps_rel=1e-12, rho_f_factor=1000.0, alpha=1.0)
+    solver = _solver(qp1, cfg)
+    st0 = solver.initial_state(qp1, rho_bar=0.1)
+    outs = []
+    for warm in (True, False):
+        ws = direct_workspace(qp1)
+        (_, _), _, st1 = solver.solve(qp1, st0, workspace=ws)
+        active = torch.ones(B, dtype=torch.bool, device=DEV)
+        (_, _), stats, st2, _, _ = solver.sqp_step(qp2, st1, active, 0.0, rho_bar=0.1, workspace=ws,
+                                                   warm_records=warm, warm_ineq=warm and ineq)
+        outs.append((stats, st2))
+    torch.cuda.synchronize()
+    (s_w, o_w), (s_c, o_c) = outs
+    assert torch.equal(s_w.num_iter, s_c.num_iter)
+    for k in ("x_blocks", "z_g", "y_g", "y_f_0", "y_f_dyn", "xi_g"):
+        assert torch.equal(getattr(o_w, k), getattr(o_c, k)), k
 
 
 @pytest.mark.parametrize("kernel", ["stream", "generic"])

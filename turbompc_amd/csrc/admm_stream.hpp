@@ -185,35 +185,51 @@ struct StreamArgs {
 
 // ---- pack / unpack -----------------------------------------------------------
 
-// One 64-lane block per (problem, stage).
+// One 64-lane block per (problem, stage).  The QP and state arrays have rows
+// of d.nq entries, the records d.n >= d.nq: variables nq..n-1 are dummies
+// with D = 1 on their diagonal and zero everywhere else (x, q, and their
+// columns of A_minus, G and A0), so theta keeps them decoupled at 1 + sigma
+// and the iteration keeps them at zero without touching any other value.
+// With A0p, block (b, 0) also writes the problem's A0 with rows of n entries.
 template <typename R>
 __global__ __launch_bounds__(kWave) void stage_pack_kernel(Dims d, QPDev<R> qp, StateDev<R> st, R* __restrict__ am,
-                                                           R* __restrict__ rv, R* __restrict__ dm, int diag) {
+                                                           R* __restrict__ rv, R* __restrict__ dm, int diag,
+                                                           R* __restrict__ A0p) {
   const int b = blockIdx.x, t = blockIdx.y, tid = threadIdx.x;
-  const int B = d.B, T = d.T, N = d.N, n = d.n, nx = d.nx, m = d.m;
+  const int B = d.B, T = d.T, N = d.N, n = d.n, nx = d.nx, m = d.m, nq = d.nq;
   const RecGeom g = rec_geom(d, diag != 0);
   const size_t bt = (size_t)b * T + t;
   {
     R* o = am + ((size_t)t * B + b) * g.amp;
-    const R* sa = qp.Am + ((size_t)b * N + t) * nx * n;
-    const R* sg = qp.G + bt * m * n;
+    const R* sa = qp.Am + ((size_t)b * N + t) * nx * nq;
+    const R* sg = qp.G + bt * m * nq;
     for (int e = tid; e < g.amp; e += kWave) {
+      const int r = e / n, k = e - r * n;
       R v = R(0);
-      if (e < nx * n) {
-        if (t < N) v = sa[e];
-      } else if (e < (nx + m) * n) {
-        v = sg[e - nx * n];
+      if (k < nq) {
+        if (r < nx) {
+          if (t < N) v = sa[r * nq + k];
+        } else if (r < nx + m) {
+          v = sg[(r - nx) * nq + k];
+        }
       }
       o[e] = v;
+    }
+  }
+  if (A0p != nullptr && t == 0) {
+    const R* sa0 = qp.A0 + (size_t)b * d.n0 * nq;
+    for (int e = tid; e < d.n0 * n; e += kWave) {
+      const int r = e / n, k = e - r * n;
+      A0p[(size_t)b * d.n0 * n + e] = k < nq ? sa0[r * nq + k] : R(0);
     }
   }
   R* o = rv + ((size_t)t * B + b) * g.rvp;
   for (int e = tid; e < g.rvp; e += kWave) {
     R v = R(0);
     if (e >= g.x && e < g.x + n) {
-      v = st.x[bt * n + e - g.x];
+      if (e - g.x < nq) v = st.x[bt * nq + e - g.x];
     } else if (e >= g.q && e < g.q + n) {
-      v = qp.q[bt * n + e - g.q];
+      if (e - g.q < nq) v = qp.q[bt * nq + e - g.q];
     } else if (m > 0 && e >= g.z && e < g.z + m) {
       v = st.z[bt * m + e - g.z];
     } else if (m > 0 && e >= g.yg && e < g.yg + m) {
@@ -231,19 +247,25 @@ __global__ __launch_bounds__(kWave) void stage_pack_kernel(Dims d, QPDev<R> qp, 
     }
     o[e] = v;
   }
-  // D_t: the diagonal, or packed lower (D is symmetric)
+  // D_t: the diagonal, or packed lower (D is symmetric); 1 on a dummy's diagonal
   R* od = dm + ((size_t)t * B + b) * g.dmp;
-  const R* Dt = qp.D + bt * n * n;
+  const R* Dt = qp.D + bt * nq * nq;
   for (int e = tid; e < g.dmp; e += kWave) {
     R v = R(0);
     if (diag) {
-      if (e < n) v = Dt[e * n + e];
+      if (e < nq)
+        v = Dt[e * nq + e];
+      else if (e < n)
+        v = R(1);
     } else if (e < packed_size(n)) {
       int i = (int)((sqrtf(8.0f * e + 1.0f) - 1.0f) * 0.5f);
       while ((i + 1) * (i + 2) / 2 <= e) ++i;
       while (i * (i + 1) / 2 > e) --i;
       const int k = e - i * (i + 1) / 2;
-      v = Dt[i * n + k];
+      if (i < nq)
+        v = Dt[i * nq + k];
+      else if (k == i)
+        v = R(1);
     }
     od[e] = v;
   }
@@ -270,11 +292,13 @@ __global__ __launch_bounds__(256) void stage_repack_dynamics_kernel(Dims d, cons
                                                                     R* __restrict__ rv, int diag) {
   const int t = blockIdx.y, b0 = blockIdx.x * kRepackProblems;
   const RecGeom g = rec_geom(d, diag != 0);
-  const int n = d.n, nx = d.nx, m = d.m;
-  // per stage: [A_minus (nx n) | c (nx)] for t < N, then [G (m n) | l (m) | u (m)]
+  const int n = d.n, nx = d.nx, m = d.m, nq = d.nq;
+  // per stage: [A_minus (nx nq) | c (nx)] for t < N, then [G (m nq) | l (m) | u (m)];
+  // a record row has n >= nq entries (the dummies' columns stay zero)
   const bool dyn = !INEQ || t < d.N;
-  const int na = dyn ? nx * n : 0, nd = dyn ? na + nx : 0;
-  const int ng = INEQ ? m * n : 0, per = nd + (INEQ ? ng + 2 * m : 0);
+  const int na = dyn ? nx * nq : 0, nd = dyn ? na + nx : 0;
+  const int ng = INEQ ? m * nq : 0, per = nd + (INEQ ? ng + 2 * m : 0);
+  auto rec_col = [&](int e) { return (e / nq) * n + e % nq; };  // row-major nq -> n
   for (int k = threadIdx.x; k < per; k += blockDim.x) {
     R v[kRepackProblems];
 #pragma unroll
@@ -297,11 +321,11 @@ __global__ __launch_bounds__(256) void stage_repack_dynamics_kernel(Dims d, cons
       if (b0 + j >= d.B) break;
       const size_t rec = (size_t)t * d.B + b0 + j;
       if (k < na)
-        am[rec * g.amp + k] = v[j];
+        am[rec * g.amp + rec_col(k)] = v[j];
       else if (k < nd)
         rv[rec * g.rvp + g.c + (k - na)] = v[j];
       else if (k < nd + ng)
-        am[rec * g.amp + nx * n + (k - nd)] = v[j];  // G rows follow the A_minus rows
+        am[rec * g.amp + nx * n + rec_col(k - nd)] = v[j];  // G rows follow the A_minus rows
       else if (k < nd + ng + m)
         rv[rec * g.rvp + g.l + (k - nd - ng)] = v[j];
       else
@@ -316,7 +340,7 @@ __global__ __launch_bounds__(256) void stage_repack_dynamics_kernel(Dims d, cons
 template <typename R>
 __global__ __launch_bounds__(256) void stage_unpack_kernel(Dims d, const R* __restrict__ rv, StateDev<R> st) {
   const int t = blockIdx.y, b0 = blockIdx.x * kRepackProblems;
-  const int B = d.B, T = d.T, N = d.N, n = d.n, nx = d.nx, m = d.m;
+  const int B = d.B, T = d.T, N = d.N, n = d.nq, nx = d.nx, m = d.m;  // n: the state's row length
   const RecGeom g = rec_geom(d);
   const int per = n + 3 * m + (t < N ? nx : 0);
   for (int k = threadIdx.x; k < per; k += blockDim.x) {

@@ -51,22 +51,59 @@ bool dims_ok(const tmpc_dims* d) {
 }
 
 Dims to_dims(const tmpc_dims* d) {
-  return Dims{d->B, d->T, d->T - 1, d->n, d->nx, d->n0, d->m};
+  return Dims{d->B, d->T, d->T - 1, d->n, d->nx, d->n0, d->m, d->n};
 }
 
-// Stage records of the streaming path (admm_stream.hpp).
+// The stage-record shapes the streaming kernels are built for: n in {6, 9,
+// 16, 17}, nx <= n - 1, and either m <= kMaxStreamM with nx + m <= n (the
+// stacked constraint rows of a stage fit the problem's n lanes) or, for n = 9,
+// the wide form with nx + m <= kWideRows and m <= kWideMaxM; stage-run offsets
+// are 32-bit element offsets.
+inline bool stream_wide(const Dims& d) { return d.nx + d.m > d.n; }
+
+inline bool stream_shape_ok(const Dims& d) {
+  if (!(d.n == 6 || d.n == 9 || d.n == 16 || d.n == 17)) return false;
+  if (d.nx > d.n - 1) return false;
+  if (stream_wide(d)) {
+    if (d.n != 9 || d.nx + d.m > kWideRows || d.m > kWideMaxM) return false;
+  } else if (d.m > kMaxStreamM) {
+    return false;
+  }
+  const RecGeom g = rec_geom(d);
+  const int widest = std::max(std::max(g.amp, g.rvp), th_pitch(d.n));
+  return (long long)d.T * d.B * widest < (1LL << 31);
+}
+
+// Record dims of the streaming path: the block width n rounded up to the
+// smallest width above that fits the shape, the extra variables being
+// decoupled dummies (stage_pack_kernel); the QP and state keep rows of nq = n.
+// d itself when no width fits (the generic kernels then run).
+inline Dims stream_record_dims(const Dims& d) {
+  for (int w : {6, 9, 16, 17}) {
+    if (w < d.n) continue;
+    Dims r = d;
+    r.n = w;
+    if (stream_shape_ok(r)) return r;
+  }
+  return d;
+}
+
+// Stage records of the streaming path (admm_stream.hpp), on the record dims,
+// and the padded A0 [B][n0][n] when the records are wider than the QP.
 template <typename R>
 size_t stream_ws_bytes(const Dims& d) {
-  const RecGeom g = rec_geom(d);
-  const size_t B = d.B, T = d.T, N = d.N;
+  const Dims r = stream_record_dims(d);
+  const RecGeom g = rec_geom(r);
+  const size_t B = d.B, T = d.T;
   return align_up(T * B * g.amp * sizeof(R)) + align_up(T * B * g.rvp * sizeof(R)) +
-         align_up(T * B * th_pitch(d.n) * sizeof(R));
+         align_up(T * B * th_pitch(r.n) * sizeof(R)) + align_up(B * d.n0 * r.n * sizeof(R));
 }
 
 template <typename R>
 size_t direct_ws_bytes(const Dims& d) {
   const size_t B = d.B, T = d.T, n = d.n;
-  return align_up(T * B * th_pitch(d.n) * sizeof(R)) + 2 * align_up(T * B * n * sizeof(R)) +
+  const int nth = stream_record_dims(d).n;  // >= n
+  return align_up(T * B * th_pitch(nth) * sizeof(R)) + 2 * align_up(T * B * n * sizeof(R)) +
          align_up(B * 4 * sizeof(int32_t)) + align_up(B * 8 * sizeof(R)) + stream_ws_bytes<R>(d);
 }
 
@@ -75,22 +112,25 @@ struct DirectWs {
   R *thinv, *w, *gam, *res;
   int32_t* ctl;
   R *am, *rv, *dm;  // stage records of the streaming path
+  R* a0p;           // A0 with rows of the records' width
 };
 
 template <typename R>
 DirectWs<R> carve_direct(void* ws, const Dims& d) {
   Carver c{static_cast<char*>(ws)};
   DirectWs<R> w;
-  const size_t B = d.B, T = d.T, N = d.N, n = d.n;
-  const RecGeom g = rec_geom(d);
-  w.thinv = c.take<R>(T * B * th_pitch(d.n));
+  const Dims r = stream_record_dims(d);
+  const size_t B = d.B, T = d.T, n = d.n;
+  const RecGeom g = rec_geom(r);
+  w.thinv = c.take<R>(T * B * th_pitch(r.n));
   w.w = c.take<R>(T * B * n);
   w.gam = c.take<R>(T * B * n);
   w.ctl = c.take<int32_t>(B * 4);
   w.res = c.take<R>(B * 8);
   w.am = c.take<R>(T * B * g.amp);
   w.rv = c.take<R>(T * B * g.rvp);
-  w.dm = c.take<R>(T * B * th_pitch(d.n));
+  w.dm = c.take<R>(T * B * th_pitch(r.n));
+  w.a0p = c.take<R>(B * d.n0 * r.n);
   return w;
 }
 
@@ -185,10 +225,10 @@ void launch_chunk(hipStream_t s, const AdmmArgs<R>& a) {
   }
 }
 
-// Streaming kernel (explicit-integrator structure, n in {6, 9, 16, 17},
-// nx <= n - 1, and nx + m <= n with m <= 8, or for n = 9 the wide form with
-// nx + m <= 17 and m <= 12).  P problems per wavefront: as many as keep about
-// two wavefronts per SIMD busy on a 256-CU device, at most 3.
+// Streaming kernel (explicit-integrator structure, record shapes as in
+// stream_shape_ok, on the record dims of stream_record_dims).  P problems per
+// wavefront: as many as keep about two wavefronts per SIMD busy on a 256-CU
+// device, at most 3.
 constexpr int kStreamDepth = 1;
 constexpr size_t kMaxLds = 160 * 1024;
 
@@ -205,24 +245,12 @@ inline int factor_problems_per_wave(int B, uint32_t flags) {
   return forced ? forced : std::max(1, std::min(3, B / 1024));
 }
 
-// The stacked constraint rows of a stage exceed n lanes: the wide form of the
-// streaming kernels (n = 9, kWideRows row lanes per problem).
-inline bool stream_wide(const Dims& d) { return d.nx + d.m > d.n; }
-
+// d: the record dims (stream_record_dims)
 template <typename R>
 bool stream_ok(const Dims& d, int P, bool diag) {
-  if (!(d.n == 6 || d.n == 9 || d.n == 16 || d.n == 17)) return false;
-  if (d.nx > d.n - 1) return false;
-  if (stream_wide(d)) {
-    if (d.n != 9 || d.nx + d.m > kWideRows || d.m > kWideMaxM || P > kWave / kWideRows) return false;
-  } else if (d.m > kMaxStreamM) {
-    return false;
-  }
+  if (!stream_shape_ok(d)) return false;
+  if (stream_wide(d) && P > kWave / kWideRows) return false;
   const StreamLayout L = stream_layout(d, P, kStreamDepth, diag);
-  // stage-run offsets are 32-bit element offsets
-  const RecGeom g = rec_geom(d, diag);
-  const int widest = std::max(std::max(g.amp, g.rvp), std::max(th_pitch(d.n), g.dmp));
-  if ((long long)d.T * d.B * widest >= (1LL << 31)) return false;
   return (size_t)L.total * sizeof(R) <= kMaxLds;
 }
 
@@ -322,8 +350,10 @@ int launch_factor_std(hipStream_t s, const Dims& d, const DirectWs<R>& w, const 
   return launch_status();
 }
 
+// dr: the record dims, A0r: A0 with rows of the records' width
 template <typename R>
-StreamArgs<R> stream_args(const AdmmArgs<R>& a, const DirectWs<R>& w, bool diag, const tmpc_sqp_step* sq) {
+StreamArgs<R> stream_args(const AdmmArgs<R>& a, const DirectWs<R>& w, const Dims& dr, const R* A0r, bool diag,
+                          const tmpc_sqp_step* sq) {
   StreamArgs<R> s;
   s.chk_conv = sq ? static_cast<R*>(sq->conv) : nullptr;
   s.chk_eq = sq ? static_cast<R*>(sq->eq_err) : nullptr;
@@ -332,13 +362,13 @@ StreamArgs<R> stream_args(const AdmmArgs<R>& a, const DirectWs<R>& w, bool diag,
   s.act_in = sq ? sq->active_in : nullptr;
   s.act_out = sq ? sq->active_out : nullptr;
   s.chk_tol = sq ? (R)sq->tol : R(0);
-  s.d = a.d;
+  s.d = dr;
   s.diag = diag ? 1 : 0;
   s.th = w.thinv;
   s.dm = w.dm;
   s.am = w.am;
   s.rv = w.rv;
-  s.A0 = a.qp.A0;
+  s.A0 = A0r;
   s.c0 = a.qp.c0;
   s.slack_w = a.qp.slack_w;
   s.y_f0 = a.st.y_f0;
@@ -429,7 +459,12 @@ int admm_direct_impl(hipStream_t s, const tmpc_dims* dims, const tmpc_qp* qp,
   const int fp = factor_problems_per_wave(d.B, cfg->flags);
   const bool fgroups = (cfg->flags & TMPC_FLAG_FACTOR_GROUPS) != 0;
   const bool diag = (cfg->flags & TMPC_FLAG_DIAG_COST) != 0;
-  const bool stream = std_dyn && (cfg->flags & TMPC_FLAG_GENERIC_KERNEL) == 0 && stream_ok<R>(d, sp, diag);
+  // the streaming path works on records of width dr.n >= d.n (dummies past n)
+  const Dims dr = stream_record_dims(d);
+  const bool stream = std_dyn && (cfg->flags & TMPC_FLAG_GENERIC_KERNEL) == 0 && stream_ok<R>(dr, sp, diag);
+  const bool pad = dr.n != d.n;
+  QPDev<R> qr = a.qp;  // the QP as the record kernels read it
+  if (pad) qr.A0 = w.a0p;
   if (sq && !stream) {
     // generic path: the check kernel on the input iterate, then the activity
     // test, which the ADMM kernel reads as its per-problem start state
@@ -448,20 +483,20 @@ int admm_direct_impl(hipStream_t s, const tmpc_dims* dims, const tmpc_qp* qp,
   if (stream && (cfg->flags & TMPC_FLAG_WARM_RECORDS)) {
     const unsigned gx = (unsigned)((d.B + kRepackProblems - 1) / kRepackProblems);
     if ((cfg->flags & TMPC_FLAG_WARM_INEQ) != 0 && d.m > 0)
-      hipLaunchKernelGGL((stage_repack_dynamics_kernel<R, true>), dim3(gx, (unsigned)d.T), dim3(256), 0, s, d,
+      hipLaunchKernelGGL((stage_repack_dynamics_kernel<R, true>), dim3(gx, (unsigned)d.T), dim3(256), 0, s, dr,
                          a.qp.Am, a.qp.c, a.qp.G, a.qp.l, a.qp.u, w.am, w.rv, diag ? 1 : 0);
     else
-      hipLaunchKernelGGL((stage_repack_dynamics_kernel<R, false>), dim3(gx, (unsigned)d.N), dim3(256), 0, s, d,
+      hipLaunchKernelGGL((stage_repack_dynamics_kernel<R, false>), dim3(gx, (unsigned)d.N), dim3(256), 0, s, dr,
                          a.qp.Am, a.qp.c, a.qp.G, a.qp.l, a.qp.u, w.am, w.rv, diag ? 1 : 0);
     st = launch_status();
     if (st) return st;
-    st = launch_factor_std<R>(s, d, w, a.qp, a.st.rho, a.sigma, a.rho_f_factor, nullptr, fp, diag, fgroups);
+    st = launch_factor_std<R>(s, dr, w, qr, a.st.rho, a.sigma, a.rho_f_factor, nullptr, fp, diag, fgroups);
   } else if (stream) {
-    hipLaunchKernelGGL((stage_pack_kernel<R>), dim3(d.B, d.T), dim3(kWave), 0, s, d, a.qp, a.st, w.am, w.rv, w.dm,
-                       diag ? 1 : 0);
+    hipLaunchKernelGGL((stage_pack_kernel<R>), dim3(d.B, d.T), dim3(kWave), 0, s, dr, a.qp, a.st, w.am, w.rv, w.dm,
+                       diag ? 1 : 0, pad ? w.a0p : (R*)nullptr);
     st = launch_status();
     if (st) return st;
-    st = launch_factor_std<R>(s, d, w, a.qp, a.st.rho, a.sigma, a.rho_f_factor, nullptr, fp, diag, fgroups);
+    st = launch_factor_std<R>(s, dr, w, qr, a.st.rho, a.sigma, a.rho_f_factor, nullptr, fp, diag, fgroups);
   } else {
     st = launch_factor_qp<R>(s, d, a.qp, a.st.rho, a.sigma, a.rho_f_factor, nullptr, w.thinv);
   }
@@ -470,7 +505,7 @@ int admm_direct_impl(hipStream_t s, const tmpc_dims* dims, const tmpc_qp* qp,
   if (g_iter_events[0] && hipEventRecord(g_iter_events[0], s) != hipSuccess) return TMPC_ELAUNCH;
   for (size_t c = 0; c + 1 < bounds.size(); ++c) {
     if (c > 0) {
-      st = stream ? launch_factor_std<R>(s, d, w, a.qp, a.st.rho, a.sigma, a.rho_f_factor, w.ctl, fp, diag, fgroups)
+      st = stream ? launch_factor_std<R>(s, dr, w, qr, a.st.rho, a.sigma, a.rho_f_factor, w.ctl, fp, diag, fgroups)
                   : launch_factor_qp<R>(s, d, a.qp, a.st.rho, a.sigma, a.rho_f_factor, w.ctl, w.thinv);
       if (st) return st;
     }
@@ -478,7 +513,7 @@ int admm_direct_impl(hipStream_t s, const tmpc_dims* dims, const tmpc_qp* qp,
     a.it_hi = bounds[c + 1];
     a.first_chunk = c == 0 ? 1 : 0;
     if (stream)
-      launch_stream<R>(s, stream_args<R>(a, w, diag, sq), sp);
+      launch_stream<R>(s, stream_args<R>(a, w, dr, qr.A0, diag, sq), sp);
     else if (std_dyn)
       launch_chunk<R, true>(s, a);
     else
@@ -490,7 +525,7 @@ int admm_direct_impl(hipStream_t s, const tmpc_dims* dims, const tmpc_qp* qp,
   if (stream) {
     hipLaunchKernelGGL((stage_unpack_kernel<R>),
                        dim3((unsigned)((d.B + kRepackProblems - 1) / kRepackProblems), (unsigned)d.T), dim3(256), 0, s,
-                       d, (const R*)w.rv, a.st);
+                       dr, (const R*)w.rv, a.st);
     st = launch_status();
     if (st) return st;
   }

@@ -16,8 +16,11 @@ namespace tmpc {
 
 constexpr int kWave = 64;
 
+// n: the block width of the kernels' records; nq: the row length of the QP
+// and state arrays (nq <= n: the streaming path rounds n up to a width it is
+// built for, the extra variables being decoupled dummies; nq = n elsewhere).
 struct Dims {
-  int B, T, N, n, nx, n0, m;
+  int B, T, N, n, nx, n0, m, nq;
 };
 
 template <typename R>
