@@ -67,7 +67,8 @@ typedef struct tmpc_state {
 /* With TMPC_FLAG_STD_DYNAMICS the direct solve streams stage records through
  * a batched kernel when the shape allows it: n <= 17 and nx < n, with the
  * records' block width w the smallest of 6, 9, 16, 17 that is >= n and holds
- * nx + m <= w with m <= 8 (or w = 9 with nx + m <= 17 and m <= 12); for
+ * nx + m <= w with m <= 8 (or a wide form: w = 9 with nx + m <= 17 and
+ * m <= 12, w = 16 with nx + m <= 32 and m <= 28); for
  * n < w the records carry w - n decoupled dummy variables, which never reach
  * the state.  TMPC_FLAG_GENERIC_KERNEL selects the generic per-stage kernel
  * instead (same iteration; for cross-checks).  Bits 8-9 force the number of

@@ -478,15 +478,23 @@ def test_admm_stream_kernel_wide_rows_match_generic_on_config4_batch():
 
 # block widths outside {6, 9, 16, 17}: the streaming path rounds n up to the
 # next width it is built for (n = 4 -> 6, 7 -> 9, 8 with 11 stacked rows -> the
-# wide 9, 12 and 14 -> 16); the extra variables are decoupled dummies in the
-# stage records and never reach the state
-PADDED_SHAPES = [(9, 11, 4, 2, 2), (10, 13, 7, 4, 3), (7, 9, 8, 5, 6), (6, 9, 12, 8, 4), (5, 7, 14, 10, 5)]
+# wide 9, 12 and 14 -> 16, 14 with 20 stacked rows -> the wide 16); the extra
+# variables are decoupled dummies in the stage records and never reach the
+# state.  (5, 9, 16, 12, 16) is the linear workload's widths (box constraints
+# on all 16 variables): the wide 16 form, a half-wave per problem.
+PADDED_SHAPES = [(9, 11, 4, 2, 2), (10, 13, 7, 4, 3), (7, 9, 8, 5, 6), (6, 9, 12, 8, 4), (5, 7, 14, 10, 5),
+                 (5, 9, 16, 12, 16), (6, 7, 14, 10, 10)]
+
+
+def _wide16(shape):
+    _, _, n, nx, m = shape
+    return nx + m > 16 and n > 9
 
 
 def _gpu_solve(qp, cfg, dtype, **kw):
     qpd = qp.to(DEV, dtype)
-    (_, _), stats, out = _solver(qp, cfg, **kw).solve(qpd, _state_to_dev(zero_state(qp, 0.1), dtype),
-                                                        alpha=cfg.alpha)
+    solver = _solver(qp, cfg, **kw)
+    (_, _), stats, out = solver.solve(qpd, solver.initial_state(qpd, rho_bar=0.1), alpha=cfg.alpha)
     torch.cuda.synchronize()
     return stats, out
 
@@ -495,6 +503,8 @@ def _gpu_solve(qp, cfg, dtype, **kw):
 @pytest.mark.parametrize("shape", PADDED_SHAPES)
 @pytest.mark.parametrize("variant", ["dense", "diag", "groups"])
 def test_admm_stream_kernel_padded_width_fp64_matches_oracle(P, shape, variant):
+    if P == 3 and _wide16(shape):
+        pytest.skip("three 32-lane groups do not fit a wavefront (the wide 16 form runs P = 1, 2)")
     B, T, n, nx, m = shape
     diag = variant == "diag"
     qp = random_qp(B, T, n, nx, m, seed=81, std=True, diag=diag)
@@ -509,6 +519,26 @@ def test_admm_stream_kernel_padded_width_fp64_matches_oracle(P, shape, variant):
     _, out_g = _gpu_solve(qp, cfg, torch.float64, kernel_flags=_lib.FLAG_GENERIC_KERNEL, **kw)
     assert rel_err(out.x_blocks, out_g.x_blocks) < 1e-9
     assert not torch.equal(out.x_blocks, out_g.x_blocks)
+
+
+def test_admm_stream_kernel_wide16_config2_direct_backend():
+    # the linear workload (n = 16, nx = 12, m = 16) on the direct backend at a
+    # batch with a partial last wavefront: the wide 16 streaming kernel and the
+    # generic kernel run the same fp32 iteration, both against the fp64 oracle
+    prob = configs.config2(B=515, seed=4).to(DEV, torch.float32)
+    qp = prob.build_qp(*prob.initial_guess())
+    cfg = oracle.OracleCfg(max_iter=40, check_every=41, adapt_rho_every=0, sigma=1e-6, eps_abs=1e-9, eps_rel=1e-9,
+                           rho_f_factor=1000.0, alpha=1.6)
+    outs = []
+    for flags in (0, _lib.FLAG_GENERIC_KERNEL):
+        outs.append(_gpu_solve(qp, cfg, torch.float32, kernel_flags=flags))
+    (s_a, o_a), (s_b, o_b) = outs
+    assert torch.equal(s_a.num_iter, s_b.num_iter)
+    assert not torch.equal(o_a.x_blocks, o_b.x_blocks)  # two different kernels ran
+    ref, it_ref = _oracle_full_batch(qp, cfg)
+    np.testing.assert_array_equal(s_a.num_iter.cpu().numpy(), it_ref)
+    _assert_batch_matches_oracle("config 2 B=515 wide stream", o_a, ref, TOL[torch.float32])
+    _assert_batch_matches_oracle("config 2 B=515 generic", o_b, ref, TOL[torch.float32])
 
 
 @pytest.mark.parametrize("shape", [(10, 13, 7, 4, 3), (6, 9, 12, 8, 4)])
@@ -528,7 +558,7 @@ def test_admm_stream_kernel_padded_width_adaptive_rho_fp32(shape):
     _assert_state_close(out32, ref32, TOL[torch.float32])
 
 
-@pytest.mark.parametrize("shape", [(10, 13, 7, 4, 3), (7, 9, 8, 5, 6), (5, 7, 14, 10, 5)])
+@pytest.mark.parametrize("shape", [(10, 13, 7, 4, 3), (7, 9, 8, 5, 6), (5, 7, 14, 10, 5), (6, 7, 14, 10, 10)])
 @pytest.mark.parametrize("ineq", [False, True])
 def test_admm_stream_kernel_padded_width_warm_records(shape, ineq):
     """An SQP step whose QP differs from the previous call's in A_minus and c

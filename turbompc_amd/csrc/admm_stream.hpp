@@ -93,12 +93,17 @@ __host__ __device__ inline RecGeom rec_geom(const Dims& d, bool diag = false) {
 
 // Compile-time caps of the streaming kernel (host checks, else the generic
 // kernel runs): nx <= n - 1 and either m <= kMaxStreamM, nx + m <= n (the
-// stacked constraint rows of a stage fit the problem's n lanes), or, for
-// n = 9 (the obstacle workload's 6 states and 3 controls), the wide form:
-// m <= kWideMaxM, nx + m <= kWideRows row lanes per problem (NL > NC).
+// stacked constraint rows of a stage fit the problem's n lanes), or a wide
+// form with NL > NC row lanes per problem: n = 9 (the obstacle workload's 6
+// states and 3 controls) with m <= kWideMaxM, nx + m <= kWideRows, up to three
+// problems per wavefront; n = 16 (box constraints on every variable, as in the
+// linear workload) with m <= kWide16MaxM, nx + m <= kWide16Rows, a half-wave
+// per problem.
 constexpr int kMaxStreamM = 8;
 constexpr int kWideRows = 17;
 constexpr int kWideMaxM = 12;
+constexpr int kWide16Rows = 32;
+constexpr int kWide16MaxM = 28;
 
 // NL: lanes of a problem's group that own a stacked constraint row (NL >= NC);
 // MM: most inequality rows per stage.

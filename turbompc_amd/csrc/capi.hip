@@ -56,16 +56,21 @@ Dims to_dims(const tmpc_dims* d) {
 
 // The stage-record shapes the streaming kernels are built for: n in {6, 9,
 // 16, 17}, nx <= n - 1, and either m <= kMaxStreamM with nx + m <= n (the
-// stacked constraint rows of a stage fit the problem's n lanes) or, for n = 9,
-// the wide form with nx + m <= kWideRows and m <= kWideMaxM; stage-run offsets
-// are 32-bit element offsets.
+// stacked constraint rows of a stage fit the problem's n lanes) or a wide
+// form: n = 9 with nx + m <= kWideRows and m <= kWideMaxM, n = 16 with
+// nx + m <= kWide16Rows and m <= kWide16MaxM; stage-run offsets are 32-bit
+// element offsets.
 inline bool stream_wide(const Dims& d) { return d.nx + d.m > d.n; }
+// row lanes per problem of the wide form
+inline int stream_wide_rows(const Dims& d) { return d.n == 16 ? kWide16Rows : kWideRows; }
 
 inline bool stream_shape_ok(const Dims& d) {
   if (!(d.n == 6 || d.n == 9 || d.n == 16 || d.n == 17)) return false;
   if (d.nx > d.n - 1) return false;
   if (stream_wide(d)) {
-    if (d.n != 9 || d.nx + d.m > kWideRows || d.m > kWideMaxM) return false;
+    const bool w9 = d.n == 9 && d.nx + d.m <= kWideRows && d.m <= kWideMaxM;
+    const bool w16 = d.n == 16 && d.nx + d.m <= kWide16Rows && d.m <= kWide16MaxM;
+    if (!w9 && !w16) return false;
   } else if (d.m > kMaxStreamM) {
     return false;
   }
@@ -249,7 +254,7 @@ inline int factor_problems_per_wave(int B, uint32_t flags) {
 template <typename R>
 bool stream_ok(const Dims& d, int P, bool diag) {
   if (!stream_shape_ok(d)) return false;
-  if (stream_wide(d) && P > kWave / kWideRows) return false;
+  if (stream_wide(d) && P > kWave / stream_wide_rows(d)) return false;
   const StreamLayout L = stream_layout(d, P, kStreamDepth, diag);
   return (size_t)L.total * sizeof(R) <= kMaxLds;
 }
@@ -268,7 +273,9 @@ void launch_stream_nc(hipStream_t s, const StreamArgs<R>& a, int P) {
   switch (P) {
     case 1: launch_stream_p<R, NC, 1, NL, MM>(s, a); break;
     case 2: launch_stream_p<R, NC, 2, NL, MM>(s, a); break;
-    default: launch_stream_p<R, NC, 3, NL, MM>(s, a); break;
+    default:
+      if constexpr (3 * NL <= kWave) launch_stream_p<R, NC, 3, NL, MM>(s, a);  // stream_ok rules out the rest
+      break;
   }
 }
 
@@ -282,7 +289,12 @@ void launch_stream(hipStream_t s, const StreamArgs<R>& a, int P) {
       else
         launch_stream_nc<R, 9>(s, a, P);
       break;
-    case 16: launch_stream_nc<R, 16>(s, a, P); break;
+    case 16:
+      if (stream_wide(a.d))
+        launch_stream_nc<R, 16, kWide16Rows, kWide16MaxM>(s, a, P);
+      else
+        launch_stream_nc<R, 16>(s, a, P);
+      break;
     default: launch_stream_nc<R, 17>(s, a, P); break;
   }
 }
@@ -331,7 +343,12 @@ int launch_factor_std(hipStream_t s, const Dims& d, const DirectWs<R>& w, const 
         else
           launch_factor_row_nc<R, 9, 9>(s, d, w, q, rho, sigma, rho_f_factor, ctl, diag);
         break;
-      case 16: launch_factor_row_nc<R, 16, 16>(s, d, w, q, rho, sigma, rho_f_factor, ctl, diag); break;
+      case 16:
+        if (stream_wide(d))
+          launch_factor_row_nc<R, 16, kWide16Rows>(s, d, w, q, rho, sigma, rho_f_factor, ctl, diag);
+        else
+          launch_factor_row_nc<R, 16, 16>(s, d, w, q, rho, sigma, rho_f_factor, ctl, diag);
+        break;
       default: launch_factor_row_nc<R, 17, 17>(s, d, w, q, rho, sigma, rho_f_factor, ctl, diag); break;
     }
     return launch_status();
@@ -344,7 +361,12 @@ int launch_factor_std(hipStream_t s, const Dims& d, const DirectWs<R>& w, const 
       else
         launch_factor_std_nc<R, 9>(s, d, w, q, rho, sigma, rho_f_factor, ctl, P, diag);
       break;
-    case 16: launch_factor_std_nc<R, 16>(s, d, w, q, rho, sigma, rho_f_factor, ctl, P, diag); break;
+    case 16:
+      if (stream_wide(d))
+        launch_factor_std_nc<R, 16, kWide16Rows, kWide16MaxM>(s, d, w, q, rho, sigma, rho_f_factor, ctl, P, diag);
+      else
+        launch_factor_std_nc<R, 16>(s, d, w, q, rho, sigma, rho_f_factor, ctl, P, diag);
+      break;
     default: launch_factor_std_nc<R, 17>(s, d, w, q, rho, sigma, rho_f_factor, ctl, P, diag); break;
   }
   return launch_status();
@@ -455,12 +477,14 @@ int admm_direct_impl(hipStream_t s, const tmpc_dims* dims, const tmpc_qp* qp,
   a.P = kWave / a.g;
   a.act = nullptr;
   const bool std_dyn = (cfg->flags & TMPC_FLAG_STD_DYNAMICS) != 0;
-  const int sp = stream_problems_per_wave(d.B, cfg->flags);
+  int sp = stream_problems_per_wave(d.B, cfg->flags);
   const int fp = factor_problems_per_wave(d.B, cfg->flags);
   const bool fgroups = (cfg->flags & TMPC_FLAG_FACTOR_GROUPS) != 0;
   const bool diag = (cfg->flags & TMPC_FLAG_DIAG_COST) != 0;
   // the streaming path works on records of width dr.n >= d.n (dummies past n)
   const Dims dr = stream_record_dims(d);
+  if (stream_wide(dr) && (cfg->flags & TMPC_FLAG_STREAM_P(3)) == 0)
+    sp = std::min(sp, kWave / stream_wide_rows(dr));  // the wide forms' groups are larger
   const bool stream = std_dyn && (cfg->flags & TMPC_FLAG_GENERIC_KERNEL) == 0 && stream_ok<R>(dr, sp, diag);
   const bool pad = dr.n != d.n;
   QPDev<R> qr = a.qp;  // the QP as the record kernels read it
