@@ -695,7 +695,7 @@ int adjoint_impl(hipStream_t s, const tmpc_dims* dims, const tmpc_qp* qp, R* dz,
   int st = launch_status();
   if (st) return st;
   // block-tridiagonal factorization of the stage-block KKT (factor.hpp, SRC_S)
-  Dims kd{d.B, d.T, d.N, k.nb, 1, 1, 0};
+  Dims kd{d.B, d.T, d.N, k.nb, 1, 1, 0, k.nb};
   const size_t smem = factor_smem_bytes(kd);
   lds_optin(factor_kernel<R, SRC_S>, smem);
   hipLaunchKernelGGL((factor_kernel<R, SRC_S>), dim3(d.B), dim3(kWave), smem, s, kd, QPDev<R>{}, (const R*)K,
