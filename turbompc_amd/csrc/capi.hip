@@ -13,6 +13,7 @@
 #include "factor.hpp"
 #include "pcg.hpp"
 #include "factor_rows.hpp"
+#include "kkt_factor.hpp"
 #include "pcg_lds.hpp"
 #include "obstacle.hpp"
 #include "quadrotor.hpp"
@@ -664,10 +665,64 @@ size_t adjoint_ws_bytes(const Dims& d) {
          5 * align_up(B * T * nb * sizeof(R)) + align_up(B * sizeof(R));
 }
 
+// The rows-in-lanes KKT factorization (kkt_factor.hpp) for n <= 16 and
+// nb <= 32: block capacities NC (Z) and NBC (rows per problem), P problems per
+// wavefront (about two wavefronts per SIMD); false when the shape is not
+// covered (factor_kernel runs).
+template <typename R, int NC, int NBC>
+void launch_kkt_rows_nc(hipStream_t s, const KktDims& k, int P, const R* K, R* th) {
+  if (P >= 2) {
+    hipLaunchKernelGGL((factor_kkt_rows_kernel<R, NC, NBC, 2>), dim3((k.B + 1) / 2), dim3(kWave), 0, s, k, K, th);
+  } else {
+    hipLaunchKernelGGL((factor_kkt_rows_kernel<R, NC, NBC, 1>), dim3(k.B), dim3(kWave), 0, s, k, K, th);
+  }
+}
+
+template <typename R, int NC, int NBC>
+void launch_kkt_solve_nc(hipStream_t s, const KktDims& k, int P, const R* K, const R* th, const R* rhs, R* x) {
+  if (P >= 2) {
+    hipLaunchKernelGGL((kkt_solve_rows_kernel<R, NC, NBC, 2>), dim3((k.B + 1) / 2), dim3(kWave), 0, s, k, K, th,
+                       rhs, x);
+  } else {
+    hipLaunchKernelGGL((kkt_solve_rows_kernel<R, NC, NBC, 1>), dim3(k.B), dim3(kWave), 0, s, k, K, th, rhs, x);
+  }
+}
+
+// 0: not covered; 1, 2, 3: the (NC, NBC) capacities (9, 18), (9, 32), (16, 32)
+inline int kkt_rows_form(const KktDims& k) {
+  if (k.n <= 9 && k.nb <= 18) return 1;
+  if (k.n <= 9 && k.nb <= 32) return 2;
+  if (k.n <= 16 && k.nb <= 32) return 3;
+  return 0;
+}
+inline int kkt_rows_p(const KktDims& k) { return k.B >= 4096 ? 2 : 1; }
+
+template <typename R>
+bool launch_kkt_rows(hipStream_t s, const KktDims& k, const R* K, R* th) {
+  const int P = kkt_rows_p(k);
+  switch (kkt_rows_form(k)) {
+    case 1: launch_kkt_rows_nc<R, 9, 18>(s, k, P, K, th); return true;
+    case 2: launch_kkt_rows_nc<R, 9, 32>(s, k, P, K, th); return true;
+    case 3: launch_kkt_rows_nc<R, 16, 32>(s, k, P, K, th); return true;
+    default: return false;
+  }
+}
+
+template <typename R>
+void launch_kkt_solve(hipStream_t s, const KktDims& k, const Dims& kd, bool rows, const R* K, const R* th,
+                      const R* rhs, R* x) {
+  const int P = kkt_rows_p(k);
+  switch (rows ? kkt_rows_form(k) : 0) {
+    case 1: launch_kkt_solve_nc<R, 9, 18>(s, k, P, K, th, rhs, x); break;
+    case 2: launch_kkt_solve_nc<R, 9, 32>(s, k, P, K, th, rhs, x); break;
+    case 3: launch_kkt_solve_nc<R, 16, 32>(s, k, P, K, th, rhs, x); break;
+    default: launch_blktri_solve_nc<R, 0>(s, kd, k.nb, kWave / k.nb, K, th, rhs, x); break;
+  }
+}
+
 template <typename R>
 int adjoint_impl(hipStream_t s, const tmpc_dims* dims, const tmpc_qp* qp, R* dz, R* mult, double reg,
                  int32_t refine, uint32_t flags, void* ws, size_t wsb) {
-  (void)flags;
   if (!dims_ok(dims)) return TMPC_EBADSHAPE;
   if (!qp || !qp->D || !qp->E || !qp->q || !qp->A0 || !qp->A_minus || !qp->A_plus || !dz || !mult)
     return TMPC_EBADARG;
@@ -694,20 +749,25 @@ int adjoint_impl(hipStream_t s, const tmpc_dims* dims, const tmpc_qp* qp, R* dz,
   hipLaunchKernelGGL((kkt_assemble_kernel<R>), dim3(d.B * d.T), dim3(256), 0, s, k, q, shift, K, dreg, rhs);
   int st = launch_status();
   if (st) return st;
-  // block-tridiagonal factorization of the stage-block KKT (factor.hpp, SRC_S)
+  // block-tridiagonal factorization of the stage-block KKT: rows in lanes
+  // (kkt_factor.hpp) where the shape allows it, else factor_kernel (factor.hpp,
+  // SRC_S); TMPC_FLAG_GENERIC_KERNEL selects the latter (cross-checks)
   Dims kd{d.B, d.T, d.N, k.nb, 1, 1, 0, k.nb};
-  const size_t smem = factor_smem_bytes(kd);
-  lds_optin(factor_kernel<R, SRC_S>, smem);
-  hipLaunchKernelGGL((factor_kernel<R, SRC_S>), dim3(d.B), dim3(kWave), smem, s, kd, QPDev<R>{}, (const R*)K,
-                     (const R*)nullptr, R(0), R(0), (int32_t*)nullptr, th);
+  const bool rows = (flags & TMPC_FLAG_GENERIC_KERNEL) == 0 && launch_kkt_rows<R>(s, k, K, th);
+  if (!rows) {
+    const size_t smem = factor_smem_bytes(kd);
+    lds_optin(factor_kernel<R, SRC_S>, smem);
+    hipLaunchKernelGGL((factor_kernel<R, SRC_S>), dim3(d.B), dim3(kWave), smem, s, kd, QPDev<R>{}, (const R*)K,
+                       (const R*)nullptr, R(0), R(0), (int32_t*)nullptr, th);
+  }
   st = launch_status();
   if (st) return st;
   const int P = kWave / k.nb;
-  launch_blktri_solve_nc<R, 0>(s, kd, k.nb, P, K, th, rhs, x);
+  launch_kkt_solve<R>(s, k, kd, rows, K, th, rhs, x);
   for (int it = 0; it < steps; ++it) {
     hipLaunchKernelGGL((kkt_residual_kernel<R>), dim3((d.B + P - 1) / P), dim3(kWave), 0, s, k, P, (const R*)K,
                        (const R*)dreg, (const R*)rhs, (const R*)x, r);
-    launch_blktri_solve_nc<R, 0>(s, kd, k.nb, P, K, th, r, dx);
+    launch_kkt_solve<R>(s, k, kd, rows, K, th, r, dx);
     hipLaunchKernelGGL((axpy_kernel<R>), dim3((unsigned)((L + 255) / 256)), dim3(256), 0, s, L, (const R*)dx, x);
   }
   hipLaunchKernelGGL((kkt_unpack_kernel<R>), dim3(d.B), dim3(256), 0, s, k, (const R*)x, dz, mult);
