@@ -270,10 +270,11 @@ int tmpc_blktri_solve_f64(hipStream_t stream, int32_t B, int32_t T, int32_t n, c
  * recursion after a quasi-definite shift reg * max|D| (reg <= 0: 1e-12), and
  * refine_steps rounds of iterative refinement against the unshifted matrix
  * remove the shift (< 0: 2 in fp64, 3 in fp32).  Inactive rows get zero
- * multipliers, as in the reference.  The factorization holds a stage block's
- * rows in lanes for n <= 16 and nb <= 32, else runs the ADMM Schur matrix's
- * generic kernel; flags: TMPC_FLAG_GENERIC_KERNEL selects the latter (for
- * cross-checks). */
+ * multipliers, as in the reference.  For n <= 16 and nb <= 32 the
+ * factorization, solves and residuals hold a stage block's rows in lanes and
+ * read the QP blocks directly; other shapes assemble the stage blocks in the
+ * workspace and run the ADMM Schur matrix's generic kernels; flags:
+ * TMPC_FLAG_GENERIC_KERNEL selects the latter (for cross-checks). */
 size_t tmpc_adjoint_kkt_workspace_bytes(int elem_bytes, const tmpc_dims* dims);
 int tmpc_adjoint_kkt_f32(hipStream_t stream, const tmpc_dims* dims, const tmpc_qp* qp, float* dz,
                          float* mult, double reg, int32_t refine_steps, uint32_t flags, void* workspace,

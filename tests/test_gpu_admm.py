@@ -326,6 +326,77 @@ def test_adjoint_kkt_matches_dense_oracle_fp64():
     assert rel_err(mult, mult_ref) < 1e-9
 
 
+# the rows-in-lanes KKT factorization and solve (n <= 16, nb <= 32) against the
+# dense oracle and the generic kernels: config 5 (nb = 18), config 4 (nb = 26),
+# and random QPs with n = 12 (nb = 24) and with E != 0 (the coupling block's E part)
+@pytest.mark.parametrize("case", ["config5", "config4", "random12", "random-E"])
+def test_adjoint_kkt_rows_kernels_match_generic_and_oracle(case):
+    rng = np.random.default_rng(7)
+    if case == "config5":
+        prob = configs.config5(B=5, seed=1)
+        qp = prob.build_qp(*prob.initial_guess())
+    elif case == "config4":
+        prob = configs.config4(B=5, seed=1).to(DEV, torch.float64)  # its linearization runs on the device
+        qp = prob.build_qp(*prob.initial_guess()).to("cpu", torch.float64)
+    elif case == "random12":
+        # n0 + m <= n: the initial-state rows and the active rows of stage 0
+        # both sit on z_0 alone, and more of them than n makes the multipliers
+        # non-unique (dz stays unique)
+        qp = random_qp(5, 9, 12, 8, 4, seed=91, std=True)
+    else:
+        qp = random_qp(5, 9, 9, 6, 3, seed=92, std=False)
+    sign = rng.choice([-1.0, 0.0, 1.0], size=tuple(qp.ineq.l.shape), p=[0.3, 0.4, 0.3])
+    if case == "config4":
+        # box rows only: the obstacle rows act on the position, which the
+        # initial-state rows already pin at stage 0 (a rank-deficient KKT)
+        sign[..., prob.num_box_constraints:] = 0.0
+    G = qp.ineq.G * torch.tensor(sign).unsqueeze(-1)
+    qb = qp.replace_ineq(G=G).replace_cost(q=torch.tensor(rng.standard_normal(tuple(qp.cost.q.shape))))
+    dz_ref, mult_ref = oracle.adjoint_kkt(qb)
+    qd = qb.to(DEV, torch.float64)
+    # four refinement rounds: with this many active rows two rounds against
+    # the shifted factor leave about 2e-9 in the multipliers (either kernel)
+    dz, mult = solve_backward_kkt_hip(qd, refine_steps=4)
+    dz_g, mult_g = solve_backward_kkt_hip(qd, refine_steps=4, kernel_flags=_lib.FLAG_GENERIC_KERNEL)
+    errs = {k: rel_err(a, b) for k, (a, b) in {"dz": (dz, dz_ref), "mult": (mult, mult_ref), "dz generic": (dz_g, dz_ref),
+                                             "mult generic": (mult_g, mult_ref)}.items()}
+    print(case, {k: f"{v:.2e}" for k, v in errs.items()})
+    assert all(v < 1e-10 for v in errs.values()), errs
+    assert not torch.equal(dz, dz_g)  # two different factorizations ran
+
+
+# the rows-in-lanes kernels with two and three problems per wavefront (the
+# batch sets how many: ceil(B / 1024)), last wavefront partly filled, in the
+# three (NC, NBC) forms; T = 6 keeps the dense oracle cheap at B = 2049
+@pytest.mark.parametrize("shape", [(2049, 9, 6, 3), (1100, 9, 6, 3), (1100, 9, 6, 14), (2049, 12, 8, 4)])
+@pytest.mark.parametrize("dtype", [torch.float64, torch.float32])
+def test_adjoint_kkt_rows_kernels_packed_wavefronts(shape, dtype):
+    B, n, nx, m = shape
+    rng = np.random.default_rng(11)
+    qp = random_qp(B, 6, n, nx, m, seed=94, std=False)
+    # at most n - nx - 1 active rows per stage: each stage's controls leave
+    # n - nx directions free, so the multipliers stay unique and the batch's
+    # KKT condition numbers stay below about 1e6 (n - nx active rows reach
+    # 1e9 in a batch this size)
+    k = rng.integers(0, n - nx, size=(B, 6))
+    order = np.argsort(rng.random((B, 6, m)), axis=-1)
+    sign = np.where(order < k[..., None], rng.choice([-1.0, 1.0], size=(B, 6, m)), 0.0)
+    G = qp.ineq.G * torch.tensor(sign).unsqueeze(-1)
+    qb = qp.replace_ineq(G=G).replace_cost(q=torch.tensor(rng.standard_normal(tuple(qp.cost.q.shape))))
+    dz_ref, mult_ref = oracle.adjoint_kkt(qb)
+    qd = qb.to(DEV, dtype)
+    dz, mult = solve_backward_kkt_hip(qd, refine_steps=4)
+    dz_g, mult_g = solve_backward_kkt_hip(qd, refine_steps=4, kernel_flags=_lib.FLAG_GENERIC_KERNEL)
+    tol = 1e-9 if dtype == torch.float64 else 1e-4
+    errs = {"dz": rel_err(dz, dz_ref), "mult": rel_err(mult, mult_ref), "dz generic": rel_err(dz_g, dz_ref),
+            "mult generic": rel_err(mult_g, mult_ref)}
+    errs["rows vs generic"] = rel_err(dz, dz_g)
+    print(shape, dtype, {k: f"{v:.2e}" for k, v in errs.items()})
+    # max-abs errors over the whole batch: every problem counts, the last
+    # (partly filled) wavefront's included
+    assert all(v < tol for v in errs.values()), errs
+
+
 @pytest.mark.parametrize("dtype", [torch.float64, torch.float32])
 def test_quadrotor_linearization_matches_complex_step(dtype):
     prob = make_quadrotor_config(B=16, seed=1, dtype=dtype, device=DEV)

@@ -665,29 +665,10 @@ size_t adjoint_ws_bytes(const Dims& d) {
          5 * align_up(B * T * nb * sizeof(R)) + align_up(B * sizeof(R));
 }
 
-// The rows-in-lanes KKT factorization (kkt_factor.hpp) for n <= 16 and
-// nb <= 32: block capacities NC (Z) and NBC (rows per problem), P problems per
-// wavefront (about two wavefronts per SIMD); false when the shape is not
-// covered (factor_kernel runs).
-template <typename R, int NC, int NBC>
-void launch_kkt_rows_nc(hipStream_t s, const KktDims& k, int P, const R* K, R* th) {
-  if (P >= 2) {
-    hipLaunchKernelGGL((factor_kkt_rows_kernel<R, NC, NBC, 2>), dim3((k.B + 1) / 2), dim3(kWave), 0, s, k, K, th);
-  } else {
-    hipLaunchKernelGGL((factor_kkt_rows_kernel<R, NC, NBC, 1>), dim3(k.B), dim3(kWave), 0, s, k, K, th);
-  }
-}
-
-template <typename R, int NC, int NBC>
-void launch_kkt_solve_nc(hipStream_t s, const KktDims& k, int P, const R* K, const R* th, const R* rhs, R* x) {
-  if (P >= 2) {
-    hipLaunchKernelGGL((kkt_solve_rows_kernel<R, NC, NBC, 2>), dim3((k.B + 1) / 2), dim3(kWave), 0, s, k, K, th,
-                       rhs, x);
-  } else {
-    hipLaunchKernelGGL((kkt_solve_rows_kernel<R, NC, NBC, 1>), dim3(k.B), dim3(kWave), 0, s, k, K, th, rhs, x);
-  }
-}
-
+// The rows-in-lanes KKT factorization and solves (kkt_factor.hpp) for n <= 16
+// and nb <= 32, reading the QP blocks directly: block capacities NC (Z) and
+// NBC (rows per problem), P problems per wavefront.  Shapes they do not cover take the assembled-matrix path
+// (kkt_assemble_kernel, factor_kernel, blktri_solve_kernel).
 // 0: not covered; 1, 2, 3: the (NC, NBC) capacities (9, 18), (9, 32), (16, 32)
 inline int kkt_rows_form(const KktDims& k) {
   if (k.n <= 9 && k.nb <= 18) return 1;
@@ -695,28 +676,65 @@ inline int kkt_rows_form(const KktDims& k) {
   if (k.n <= 16 && k.nb <= 32) return 3;
   return 0;
 }
-inline int kkt_rows_p(const KktDims& k) { return k.B >= 4096 ? 2 : 1; }
+// Problems per wavefront: enough that the launch holds about one wavefront per
+// SIMD (1024 on the chip; the factorization's registers allow one per SIMD,
+// and packing beats a second resident wavefront for the sweeps as well: 374 vs
+// 489 us per solve at B = 2048), up to the groups a wavefront holds.
+inline int kkt_rows_p(const KktDims& k) {
+  const int pmax = kkt_rows_form(k) == 1 ? 3 : 2;  // 64 / NBC groups
+  return std::max(1, std::min(pmax, (k.B + 1023) / 1024));
+}
+inline unsigned kkt_rows_grid(const KktDims& k, int P) { return (unsigned)((k.B + P - 1) / P); }
 
-template <typename R>
-bool launch_kkt_rows(hipStream_t s, const KktDims& k, const R* K, R* th) {
-  const int P = kkt_rows_p(k);
-  switch (kkt_rows_form(k)) {
-    case 1: launch_kkt_rows_nc<R, 9, 18>(s, k, P, K, th); return true;
-    case 2: launch_kkt_rows_nc<R, 9, 32>(s, k, P, K, th); return true;
-    case 3: launch_kkt_rows_nc<R, 16, 32>(s, k, P, K, th); return true;
-    default: return false;
-  }
+// P in {1, 2, 3} (3 where three groups of NBC lanes fit a wavefront)
+#define TMPC_KKT_ROWS_LAUNCH(KERNEL, ...)                                                                      \
+  do {                                                                                                        \
+    if constexpr (3 * NBC <= kWave) {                                                                         \
+      if (P >= 3) {                                                                                           \
+        hipLaunchKernelGGL((KERNEL<R, NC, NBC, 3>), dim3(kkt_rows_grid(k, 3)), dim3(kWave), 0, s, k, __VA_ARGS__); \
+        break;                                                                                                \
+      }                                                                                                       \
+    }                                                                                                         \
+    if (P >= 2)                                                                                               \
+      hipLaunchKernelGGL((KERNEL<R, NC, NBC, 2>), dim3(kkt_rows_grid(k, 2)), dim3(kWave), 0, s, k, __VA_ARGS__);   \
+    else                                                                                                      \
+      hipLaunchKernelGGL((KERNEL<R, NC, NBC, 1>), dim3(k.B), dim3(kWave), 0, s, k, __VA_ARGS__);                   \
+  } while (0)
+
+template <typename R, int NC, int NBC>
+void launch_kkt_rows_nc(hipStream_t s, const KktDims& k, int P, const QPDev<R>& q, const R* shift, R* th) {
+  TMPC_KKT_ROWS_LAUNCH(factor_kkt_rows_kernel, q, shift, th);
 }
 
+template <typename R, int NC, int NBC>
+void launch_kkt_solve_nc(hipStream_t s, const KktDims& k, int P, const QPDev<R>& q, const R* th, const R* rhs,
+                         R* x) {
+  TMPC_KKT_ROWS_LAUNCH(kkt_solve_rows_kernel, q, th, rhs, x);
+}
+
+template <typename R, int NC, int NBC>
+void launch_kkt_residual_nc(hipStream_t s, const KktDims& k, int P, const QPDev<R>& q, const R* x, R* r) {
+  TMPC_KKT_ROWS_LAUNCH(kkt_residual_rows_kernel, q, x, r);
+}
+#undef TMPC_KKT_ROWS_LAUNCH
+
+// which: 0 factor (writes th), 1 solve (in: right-hand side, null for the
+// system's own; out: x), 2 residual (in: x; out: r)
 template <typename R>
-void launch_kkt_solve(hipStream_t s, const KktDims& k, const Dims& kd, bool rows, const R* K, const R* th,
-                      const R* rhs, R* x) {
+void launch_kkt_rows(hipStream_t s, const KktDims& k, int which, const QPDev<R>& q, const R* shift, R* th,
+                     const R* in, R* out) {
   const int P = kkt_rows_p(k);
-  switch (rows ? kkt_rows_form(k) : 0) {
-    case 1: launch_kkt_solve_nc<R, 9, 18>(s, k, P, K, th, rhs, x); break;
-    case 2: launch_kkt_solve_nc<R, 9, 32>(s, k, P, K, th, rhs, x); break;
-    case 3: launch_kkt_solve_nc<R, 16, 32>(s, k, P, K, th, rhs, x); break;
-    default: launch_blktri_solve_nc<R, 0>(s, kd, k.nb, kWave / k.nb, K, th, rhs, x); break;
+  switch (kkt_rows_form(k) * 4 + which) {
+    case 4: launch_kkt_rows_nc<R, 9, 18>(s, k, P, q, shift, th); break;
+    case 5: launch_kkt_solve_nc<R, 9, 18>(s, k, P, q, th, in, out); break;
+    case 6: launch_kkt_residual_nc<R, 9, 18>(s, k, P, q, in, out); break;
+    case 8: launch_kkt_rows_nc<R, 9, 32>(s, k, P, q, shift, th); break;
+    case 9: launch_kkt_solve_nc<R, 9, 32>(s, k, P, q, th, in, out); break;
+    case 10: launch_kkt_residual_nc<R, 9, 32>(s, k, P, q, in, out); break;
+    case 12: launch_kkt_rows_nc<R, 16, 32>(s, k, P, q, shift, th); break;
+    case 13: launch_kkt_solve_nc<R, 16, 32>(s, k, P, q, th, in, out); break;
+    case 14: launch_kkt_residual_nc<R, 16, 32>(s, k, P, q, in, out); break;
+    default: break;
   }
 }
 
@@ -746,28 +764,35 @@ int adjoint_impl(hipStream_t s, const tmpc_dims* dims, const tmpc_qp* qp, R* dz,
   R* shift = c.take<R>(B);
   const QPDev<R> q = to_qp<R>(qp);
   hipLaunchKernelGGL((kkt_scale_kernel<R>), dim3(d.B), dim3(256), 0, s, k, q.D, eps, shift);
-  hipLaunchKernelGGL((kkt_assemble_kernel<R>), dim3(d.B * d.T), dim3(256), 0, s, k, q, shift, K, dreg, rhs);
-  int st = launch_status();
-  if (st) return st;
-  // block-tridiagonal factorization of the stage-block KKT: rows in lanes
-  // (kkt_factor.hpp) where the shape allows it, else factor_kernel (factor.hpp,
-  // SRC_S); TMPC_FLAG_GENERIC_KERNEL selects the latter (cross-checks)
+  // rows in lanes from the QP blocks (kkt_factor.hpp) where the shape allows
+  // it; else the assembled stage-block matrix, factor_kernel (factor.hpp,
+  // SRC_S) and blktri_solve_kernel.  TMPC_FLAG_GENERIC_KERNEL selects the
+  // latter (cross-checks).
+  const bool rows = (flags & TMPC_FLAG_GENERIC_KERNEL) == 0 && kkt_rows_form(k) != 0;
   Dims kd{d.B, d.T, d.N, k.nb, 1, 1, 0, k.nb};
-  const bool rows = (flags & TMPC_FLAG_GENERIC_KERNEL) == 0 && launch_kkt_rows<R>(s, k, K, th);
-  if (!rows) {
+  if (rows) {
+    launch_kkt_rows<R>(s, k, 0, q, shift, th, nullptr, nullptr);
+    launch_kkt_rows<R>(s, k, 1, q, nullptr, th, nullptr, x);
+  } else {
+    hipLaunchKernelGGL((kkt_assemble_kernel<R>), dim3(d.B * d.T), dim3(256), 0, s, k, q, shift, K, dreg, rhs);
     const size_t smem = factor_smem_bytes(kd);
     lds_optin(factor_kernel<R, SRC_S>, smem);
     hipLaunchKernelGGL((factor_kernel<R, SRC_S>), dim3(d.B), dim3(kWave), smem, s, kd, QPDev<R>{}, (const R*)K,
                        (const R*)nullptr, R(0), R(0), (int32_t*)nullptr, th);
+    launch_blktri_solve_nc<R, 0>(s, kd, k.nb, kWave / k.nb, K, th, rhs, x);
   }
-  st = launch_status();
+  int st = launch_status();
   if (st) return st;
-  const int P = kWave / k.nb;
-  launch_kkt_solve<R>(s, k, kd, rows, K, th, rhs, x);
   for (int it = 0; it < steps; ++it) {
-    hipLaunchKernelGGL((kkt_residual_kernel<R>), dim3((d.B + P - 1) / P), dim3(kWave), 0, s, k, P, (const R*)K,
-                       (const R*)dreg, (const R*)rhs, (const R*)x, r);
-    launch_kkt_solve<R>(s, k, kd, rows, K, th, r, dx);
+    if (rows) {
+      launch_kkt_rows<R>(s, k, 2, q, nullptr, th, x, r);
+      launch_kkt_rows<R>(s, k, 1, q, nullptr, th, r, dx);
+    } else {
+      const int Pg = kWave / k.nb;
+      hipLaunchKernelGGL((kkt_residual_kernel<R>), dim3((k.B + Pg - 1) / Pg), dim3(kWave), 0, s, k, Pg, K, dreg,
+                         rhs, x, r);
+      launch_blktri_solve_nc<R, 0>(s, kd, k.nb, kWave / k.nb, K, th, r, dx);
+    }
     hipLaunchKernelGGL((axpy_kernel<R>), dim3((unsigned)((L + 255) / 256)), dim3(256), 0, s, L, (const R*)dx, x);
   }
   hipLaunchKernelGGL((kkt_unpack_kernel<R>), dim3(d.B), dim3(256), 0, s, k, (const R*)x, dz, mult);

@@ -23,11 +23,13 @@ from ..qp_utils import ZShape, unpack_x
 
 
 def solve_backward_kkt_hip(qp_data: QPData, zshape: Optional[ZShape] = None, *, reg: float = 0.0,
-                           refine_steps: int = -1, std_dynamics: Optional[bool] = None):
+                           refine_steps: int = -1, std_dynamics: Optional[bool] = None, kernel_flags: int = 0):
     """Returns (dz, mult); with a ZShape, ((dx_states, dx_controls), mult) as the reference.
 
     reg: relative quasi-definite shift (<= 0: library default 1e-12);
-    refine_steps: iterative-refinement rounds (< 0: library default)."""
+    refine_steps: iterative-refinement rounds (< 0: library default);
+    kernel_flags: _lib.FLAG_GENERIC_KERNEL runs the generic factorization and
+    solve instead of the rows-in-lanes kernels (cross-checks)."""
     lib = _lib.load()
     if not qp_data.cost.D.is_cuda:
         raise ValueError("solve_backward_kkt_hip needs device tensors")
@@ -46,7 +48,8 @@ def solve_backward_kkt_hip(qp_data: QPData, zshape: Optional[ZShape] = None, *, 
     sfx = _lib.suffix(qp_data.dtype)
     st = getattr(lib, f"tmpc_adjoint_kkt_{sfx}")(
         _lib.stream_handle(qp_data.device), ctypes.byref(dims), ctypes.byref(cq), _lib.ptr(dz), _lib.ptr(mult),
-        float(reg), int(refine_steps), _lib.FLAG_STD_DYNAMICS if std else 0, _lib.ptr(ws), nbytes,
+        float(reg), int(refine_steps), (_lib.FLAG_STD_DYNAMICS if std else 0) | int(kernel_flags), _lib.ptr(ws),
+        nbytes,
     )
     _lib.check(f"tmpc_adjoint_kkt_{sfx}", st)
     del keep
