@@ -712,9 +712,12 @@ void launch_kkt_solve_nc(hipStream_t s, const KktDims& k, int P, const QPDev<R>&
   TMPC_KKT_ROWS_LAUNCH(kkt_solve_rows_kernel, q, th, rhs, x);
 }
 
+// the residual's units are (problem, stage) pairs: as many per wavefront as fit
 template <typename R, int NC, int NBC>
-void launch_kkt_residual_nc(hipStream_t s, const KktDims& k, int P, const QPDev<R>& q, const R* x, R* r) {
-  TMPC_KKT_ROWS_LAUNCH(kkt_residual_rows_kernel, q, x, r);
+void launch_kkt_residual_nc(hipStream_t s, const KktDims& k, const QPDev<R>& q, const R* x, R* r) {
+  constexpr int PU = kWave / NBC;
+  const unsigned grid = (unsigned)(((size_t)k.B * k.T + PU - 1) / PU);
+  hipLaunchKernelGGL((kkt_residual_rows_kernel<R, NC, NBC, PU>), dim3(grid), dim3(kWave), 0, s, k, q, x, r);
 }
 #undef TMPC_KKT_ROWS_LAUNCH
 
@@ -727,13 +730,13 @@ void launch_kkt_rows(hipStream_t s, const KktDims& k, int which, const QPDev<R>&
   switch (kkt_rows_form(k) * 4 + which) {
     case 4: launch_kkt_rows_nc<R, 9, 18>(s, k, P, q, shift, th); break;
     case 5: launch_kkt_solve_nc<R, 9, 18>(s, k, P, q, th, in, out); break;
-    case 6: launch_kkt_residual_nc<R, 9, 18>(s, k, P, q, in, out); break;
+    case 6: launch_kkt_residual_nc<R, 9, 18>(s, k, q, in, out); break;
     case 8: launch_kkt_rows_nc<R, 9, 32>(s, k, P, q, shift, th); break;
     case 9: launch_kkt_solve_nc<R, 9, 32>(s, k, P, q, th, in, out); break;
-    case 10: launch_kkt_residual_nc<R, 9, 32>(s, k, P, q, in, out); break;
+    case 10: launch_kkt_residual_nc<R, 9, 32>(s, k, q, in, out); break;
     case 12: launch_kkt_rows_nc<R, 16, 32>(s, k, P, q, shift, th); break;
     case 13: launch_kkt_solve_nc<R, 16, 32>(s, k, P, q, th, in, out); break;
-    case 14: launch_kkt_residual_nc<R, 16, 32>(s, k, P, q, in, out); break;
+    case 14: launch_kkt_residual_nc<R, 16, 32>(s, k, q, in, out); break;
     default: break;
   }
 }
@@ -748,6 +751,7 @@ int adjoint_impl(hipStream_t s, const tmpc_dims* dims, const tmpc_qp* qp, R* dz,
   const Dims d = to_dims(dims);
   const KktDims k = kkt_dims(d);
   if (k.nb > kWave) return TMPC_EBADSHAPE;
+  if ((size_t)d.B * d.T > (size_t)INT32_MAX) return TMPC_EBADSHAPE;  // residual units are counted in int
   if (!ws || wsb < adjoint_ws_bytes<R>(d)) return TMPC_EWORKSPACE;
   const bool f64 = sizeof(R) == 8;
   const R eps = reg > 0 ? (R)reg : R(1e-12);

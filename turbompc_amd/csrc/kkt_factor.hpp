@@ -348,69 +348,44 @@ __global__ __launch_bounds__(kWave) void kkt_solve_rows_kernel(KktDims k, QPDev<
 
 // r = rhs - K x with the unshifted matrix (-1 on padding rows, as in the
 // shifted one) and the KKT system's own right-hand side [-q_t | 0 | 0], as
-// kkt_residual_kernel computes it, with the lane layout above: block row t's
-// sub-diagonal block has its nonzeros in columns < n and its super-diagonal
-// block (phi_t^T) in rows < n.  Stage t + 1's loads are in flight while stage
-// t is formed.
+// kkt_residual_kernel computes it.  A stage's residual needs only x_{t-1},
+// x_t and x_{t+1}, so every (problem, stage) is an independent unit: P units
+// per wavefront, row i of a unit's block row in lane i of its group (the
+// sub-diagonal block's nonzeros in columns < n, the super-diagonal block
+// phi_t^T's in rows < n), the three x blocks through LDS.
 template <typename R, int NC, int NBC, int P>
 __global__ __launch_bounds__(kWave) void kkt_residual_rows_kernel(KktDims k, QPDev<R> qp,
                                                                   const R* __restrict__ x, R* __restrict__ r) {
-  static_assert(NBC * P <= kWave, "a problem's rows must fit its group");
-  const int nb = k.nb, n = k.n, T = k.T, B = k.B;
-  const Group G = make_group_strided(NBC, P, B);
-  const int b = G.prob, i = G.lane, p = G.gid;
+  static_assert(NBC * P <= kWave, "a unit's rows must fit its group");
+  const int nb = k.nb, n = k.n, T = k.T;
+  const Group G = make_group_strided(NBC, P, k.B * T);  // groups over (problem, stage) units
+  const int b = G.prob / T, t = G.prob - b * T, i = G.lane, p = G.gid;
   const int ir = min(i, NBC - 1);
   const bool row = ir < nb;
   const int ic = row ? ir : 0;
   const int icn = min(ir, NC - 1);
-  const bool wr = i < NBC;
-  __shared__ R win[P][3][NBC];  // x_{t-1}, x_t, x_{t+1}
-  const R* X = x + (size_t)b * T * nb;
-  if (wr) {
-    win[p][0][i] = R(0);
-    win[p][1][i] = row ? X[ic] : R(0);
-    win[p][2][i] = (row && T > 1) ? X[nb + ic] : R(0);
+  __shared__ R xw[P][3][NBC];  // x_{t-1}, x_t, x_{t+1}
+  const size_t o = ((size_t)b * T + t) * nb;
+  R sub[NC], dia[NBC], sup[NBC];
+  kkt_phi_row(k, qp, b, t, ir, sub);
+  kkt_theta_row(k, qp, b, t, ir, dia);
+  kkt_phi_col(k, qp, b, t, icn, ir < n && t + 1 < T, sup);  // row ir of phi_t^T
+  const R qn = ir < n ? qp.q[((size_t)b * T + t) * n + ir] : R(0);
+  if (i < NBC) {
+    xw[p][0][i] = (row && t > 0) ? x[o - nb + ic] : R(0);
+    xw[p][1][i] = row ? x[o + ic] : R(0);
+    xw[p][2][i] = (row && t + 1 < T) ? x[o + nb + ic] : R(0);
   }
-  R sub[NC], dia[NBC], sup[NBC], qn, xnn;
-  auto load = [&](int t) {
-    kkt_phi_row(k, qp, b, t, ir, sub);
-    kkt_theta_row(k, qp, b, t, ir, dia);
-    kkt_phi_col(k, qp, b, t, icn, ir < n && t + 1 < T, sup);  // row ir of phi_t^T
-    qn = ir < n ? qp.q[((size_t)b * T + t) * n + ir] : R(0);
-    xnn = (row && t + 2 < T) ? X[(size_t)(t + 2) * nb + ic] : R(0);
-  };
-  // the next stage's loads in flight where the registers allow (fp64 with
-  // NBC = 32 would spill)
-  constexpr bool PF = NBC <= 18 || sizeof(R) == 4;
-  if constexpr (PF) load(0);
-  for (int t = 0; t < T; ++t) {
-    if constexpr (!PF) load(t);
-    R sc[NC], dc[NBC], uc[NBC];
+  kkt_theta_diag(k, t, ir, R(0), dia);
+  lds_order();
+  R s = R(0);
 #pragma unroll
-    for (int c = 0; c < NC; ++c) sc[c] = sub[c];
+  for (int c = 0; c < NC; ++c) s += sub[c] * xw[p][0][c];
 #pragma unroll
-    for (int c = 0; c < NBC; ++c) dc[c] = dia[c];
+  for (int c = 0; c < NBC; ++c) s += dia[c] * xw[p][1][c];
 #pragma unroll
-    for (int c = 0; c < NBC; ++c) uc[c] = sup[c];
-    const R rh = -qn, xn = xnn;
-    if (PF && t + 1 < T) load(t + 1);
-    kkt_theta_diag(k, t, ir, R(0), dc);
-    lds_order();
-    R s = R(0);
-#pragma unroll
-    for (int c = 0; c < NC; ++c) s += sc[c] * win[p][0][c];
-#pragma unroll
-    for (int c = 0; c < NBC; ++c) s += dc[c] * win[p][1][c];
-#pragma unroll
-    for (int c = 0; c < NBC; ++c) s += uc[c] * win[p][2][c];
-    if (G.live && row) r[((size_t)b * T + t) * nb + ic] = rh - s;
-    lds_order();
-    if (wr) {
-      win[p][0][i] = win[p][1][i];
-      win[p][1][i] = win[p][2][i];
-      win[p][2][i] = xn;
-    }
-  }
+  for (int c = 0; c < NBC; ++c) s += sup[c] * xw[p][2][c];
+  if (G.live && row) r[o + ic] = -qn - s;
 }
 
 }  // namespace tmpc
