@@ -233,14 +233,18 @@ void launch_chunk(hipStream_t s, const AdmmArgs<R>& a) {
 
 // Streaming kernel (explicit-integrator structure, record shapes as in
 // stream_shape_ok, on the record dims of stream_record_dims).  P problems per
-// wavefront: as many as keep about two wavefronts per SIMD busy on a 256-CU
-// device, at most 3.
+// wavefront: two from B = 2048 (one wavefront per SIMD carrying two problems
+// beats two wavefronts of one: config 5, fp64 B = 2048, 28.7 vs 30.3 ms per
+// solve), three from B = 6144, where two would need more than two wavefronts
+// per SIMD (three go through LDS slots rather than DPP, so they pay only
+// there: config 3 at B = 4096 runs two).
 constexpr int kStreamDepth = 1;
 constexpr size_t kMaxLds = 160 * 1024;
 
 inline int stream_problems_per_wave(int B, uint32_t flags) {
   const int forced = (int)((flags >> 8) & 3u);
-  return forced ? forced : std::max(1, std::min(3, B / 2048));
+  if (forced) return forced;
+  return B >= 6144 ? 3 : (B >= 2048 ? 2 : 1);
 }
 
 // The factorization is bound by instruction issue rather than latency, so it
