@@ -238,8 +238,14 @@ void launch_chunk(hipStream_t s, const AdmmArgs<R>& a) {
 // solve), three from B = 6144, where two would need more than two wavefronts
 // per SIMD (three go through LDS slots rather than DPP, so they pay only
 // there: config 3 at B = 4096 runs two).
-constexpr int kStreamDepth = 1;
 constexpr size_t kMaxLds = 160 * 1024;
+
+// Stages per sweep batch (DPF).  The n <= 9 records are short enough that a
+// two-stage batch keeps more loads in flight per wavefront without leaving
+// LDS for a second wavefront (config 5, fp64 B = 2048: 28.0 -> 24.8 ms per
+// 200-iteration launch); at n = 16/17 the larger slots cost occupancy (config
+// 3: 1.94 -> 2.02 ms per launch), so they sweep one stage at a time.
+constexpr int stream_depth(int nc) { return nc <= 9 ? 2 : 1; }
 
 inline int stream_problems_per_wave(int B, uint32_t flags) {
   const int forced = (int)((flags >> 8) & 3u);
@@ -260,17 +266,18 @@ template <typename R>
 bool stream_ok(const Dims& d, int P, bool diag) {
   if (!stream_shape_ok(d)) return false;
   if (stream_wide(d) && P > kWave / stream_wide_rows(d)) return false;
-  const StreamLayout L = stream_layout(d, P, kStreamDepth, diag);
+  const StreamLayout L = stream_layout(d, P, stream_depth(d.n), diag);
   return (size_t)L.total * sizeof(R) <= kMaxLds;
 }
 
 template <typename R, int NC, int P, int NL = NC, int MM = kMaxStreamM>
 void launch_stream_p(hipStream_t s, const StreamArgs<R>& a) {
-  const StreamLayout L = stream_layout(a.d, P, kStreamDepth, a.diag != 0);
+  constexpr int DPF = stream_depth(NC);
+  const StreamLayout L = stream_layout(a.d, P, DPF, a.diag != 0);
   const size_t smem = (size_t)L.total * sizeof(R);
-  lds_optin(admm_stream_kernel<R, NC, P, kStreamDepth, NL, MM>, smem);
+  lds_optin(admm_stream_kernel<R, NC, P, DPF, NL, MM>, smem);
   const int grid = (a.d.B + P - 1) / P;
-  hipLaunchKernelGGL((admm_stream_kernel<R, NC, P, kStreamDepth, NL, MM>), dim3(grid), dim3(kWave), smem, s, a);
+  hipLaunchKernelGGL((admm_stream_kernel<R, NC, P, DPF, NL, MM>), dim3(grid), dim3(kWave), smem, s, a);
 }
 
 template <typename R, int NC, int NL = NC, int MM = kMaxStreamM>
