@@ -233,11 +233,14 @@ void launch_chunk(hipStream_t s, const AdmmArgs<R>& a) {
 
 // Streaming kernel (explicit-integrator structure, record shapes as in
 // stream_shape_ok, on the record dims of stream_record_dims).  P problems per
-// wavefront: two from B = 2048 (one wavefront per SIMD carrying two problems
-// beats two wavefronts of one: config 5, fp64 B = 2048, 28.7 vs 30.3 ms per
-// solve), three from B = 6144, where two would need more than two wavefronts
-// per SIMD (three go through LDS slots rather than DPP, so they pay only
-// there: config 3 at B = 4096 runs two).
+// wavefront: two from B = 2048.  One wavefront per SIMD carrying two problems
+// beats two wavefronts of one (config 5, fp64 B = 2048: 28.7 vs 30.3 ms per
+// solve), and two per wavefront beat three at every larger batch measured
+// (config 3: 1.94 vs 2.10 ms at B = 4096, 5.74 vs 6.46 at 12288, 7.77 vs 8.47
+// at 16384; config 5 at 4096 and 8192), since three groups straddle DPP rows
+// and move their vectors through LDS slots.  The wide n = 9 form is the
+// exception from B = 12288 (config 4: 7.95 vs 8.51 ms at 12288, even at
+// 16384, 6.30 vs 5.69 at 8192).
 constexpr size_t kMaxLds = 160 * 1024;
 
 // Stages per sweep batch (DPF).  The n <= 9 records are short enough that a
@@ -247,10 +250,11 @@ constexpr size_t kMaxLds = 160 * 1024;
 // 3: 1.94 -> 2.02 ms per launch), so they sweep one stage at a time.
 constexpr int stream_depth(int nc) { return nc <= 9 ? 2 : 1; }
 
-inline int stream_problems_per_wave(int B, uint32_t flags) {
+inline int stream_problems_per_wave(int B, uint32_t flags, bool wide9) {
   const int forced = (int)((flags >> 8) & 3u);
   if (forced) return forced;
-  return B >= 6144 ? 3 : (B >= 2048 ? 2 : 1);
+  if (wide9 && B >= 12288) return 3;
+  return B >= 2048 ? 2 : 1;
 }
 
 // The factorization is bound by instruction issue rather than latency, so it
@@ -489,12 +493,12 @@ int admm_direct_impl(hipStream_t s, const tmpc_dims* dims, const tmpc_qp* qp,
   a.P = kWave / a.g;
   a.act = nullptr;
   const bool std_dyn = (cfg->flags & TMPC_FLAG_STD_DYNAMICS) != 0;
-  int sp = stream_problems_per_wave(d.B, cfg->flags);
   const int fp = factor_problems_per_wave(d.B, cfg->flags);
   const bool fgroups = (cfg->flags & TMPC_FLAG_FACTOR_GROUPS) != 0;
   const bool diag = (cfg->flags & TMPC_FLAG_DIAG_COST) != 0;
   // the streaming path works on records of width dr.n >= d.n (dummies past n)
   const Dims dr = stream_record_dims(d);
+  int sp = stream_problems_per_wave(d.B, cfg->flags, stream_wide(dr) && dr.n == 9);
   if (stream_wide(dr) && (cfg->flags & TMPC_FLAG_STREAM_P(3)) == 0)
     sp = std::min(sp, kWave / stream_wide_rows(dr));  // the wide forms' groups are larger
   const bool stream = std_dyn && (cfg->flags & TMPC_FLAG_GENERIC_KERNEL) == 0 && stream_ok<R>(dr, sp, diag);
