@@ -19,6 +19,8 @@ from .ocp import LinearOCP, as_tensor
 
 
 class ObstacleOCP(LinearOCP):
+    PER_PROBLEM = LinearOCP.PER_PROBLEM + ("centers", "radii")
+
     def __init__(self, *, obstacles_centers: torch.Tensor, obstacles_radii: torch.Tensor,
                  obstacles_dimension: int = 3, **kw):
         """obstacles_centers (B, K, dim) or (K, dim); obstacles_radii (B, K) or (K,)."""

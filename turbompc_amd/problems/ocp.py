@@ -91,6 +91,27 @@ class QuadraticTrackingOCP:
         self.std_dynamics = True  # explicit integrators: A_plus = [-I 0], E = 0
         self.diag_cost = True  # D_t = diag(2 w): per-variable tracking weights (cost_blocks)
         self._static = None
+        # values derived from the problem's tensors, built on first use (copies
+        # made by with_weights, with_params, to and tile start empty)
+        self._memo: Dict[str, object] = {}
+
+    def _memoized(self, key, make):
+        v = self._memo.get(key)
+        if v is None:
+            v = self._memo[key] = make()
+        return v
+
+    def _box_rows(self):
+        """(rows, lo, hi): the z coordinates with a finite bound (state rows,
+        then control rows) as an index tensor, and their bounds (m,)."""
+        def make():
+            nx = self.num_state_variables
+            rows = [i for i in range(nx) if bool(self.state_mask[i])] + \
+                [nx + j for j in range(self.num_control_variables) if bool(self.control_mask[j])]
+            lo = torch.cat([self.x_bounds[0][self.state_mask], self.u_bounds[0][self.control_mask]])
+            hi = torch.cat([self.x_bounds[1][self.state_mask], self.u_bounds[1][self.control_mask]])
+            return rows, torch.tensor(rows, dtype=torch.long, device=self.device), lo, hi
+        return self._memoized("box_rows", make)
 
     # ------------------------------------------------------------ blocks ----
     def cost_blocks(self):
@@ -121,13 +142,11 @@ class QuadraticTrackingOCP:
 
     def inequality_blocks(self):
         nx, nu = self.num_state_variables, self.num_control_variables
-        rows = [i for i in range(nx) if bool(self.state_mask[i])] + [nx + j for j in range(nu) if bool(self.control_mask[j])]
+        rows, _, lo, hi = self._box_rows()
         T, n, m = self.horizon + 1, nx + nu, len(rows)
         G1 = torch.zeros((m, n), dtype=self.dtype, device=self.device)
         for r, col in enumerate(rows):
             G1[r, col] = 1.0
-        lo = torch.cat([self.x_bounds[0][self.state_mask], self.u_bounds[0][self.control_mask]])
-        hi = torch.cat([self.x_bounds[1][self.state_mask], self.u_bounds[1][self.control_mask]])
         G = G1.expand(self.B, T, m, n).contiguous()
         return G, lo.expand(self.B, T, m).contiguous(), hi.expand(self.B, T, m).contiguous()
 
@@ -152,12 +171,14 @@ class QuadraticTrackingOCP:
         """(w, zref), each (B, T, n): the per-stage weights of the tracking
         cost (w_x + w_f on the final state) and the reference (the control
         reference only with penalize_control_reference)."""
-        B, N = self.B, self.horizon
-        T, n = N + 1, self.num_state_variables + self.num_control_variables
-        w = torch.cat([self.wx, self.wu], dim=-1).unsqueeze(1).expand(B, T, n).clone()
-        w[:, N, : self.num_state_variables] += self.wf
-        uref = self.u_ref if self.penalize_control_reference else torch.zeros_like(self.u_ref)
-        return w, torch.cat([self.x_ref, uref], dim=-1)
+        def make():
+            B, N = self.B, self.horizon
+            T, n = N + 1, self.num_state_variables + self.num_control_variables
+            w = torch.cat([self.wx, self.wu], dim=-1).unsqueeze(1).expand(B, T, n).clone()
+            w[:, N, : self.num_state_variables] += self.wf
+            uref = self.u_ref if self.penalize_control_reference else torch.zeros_like(self.u_ref)
+            return w, torch.cat([self.x_ref, uref], dim=-1)
+        return self._memoized("tracking_weights", make)
 
     def cost(self, states, controls, slacks=None):
         """(B,) cost of each problem (cost, optimal_control_problem.py:982-1066:
@@ -192,13 +213,8 @@ class QuadraticTrackingOCP:
     def inequality_values(self, states, controls):
         """(g, l, u), each (B, T, m): the inequality rows g(x, u) and their
         bounds (step_inequality_constraints, :413-471)."""
-        nx = self.num_state_variables
-        rows = [i for i in range(nx) if bool(self.state_mask[i])] + \
-            [nx + j for j in range(self.num_control_variables) if bool(self.control_mask[j])]
-        z = torch.cat([states, controls], dim=-1)
-        g = z[..., rows]
-        lo = torch.cat([self.x_bounds[0][self.state_mask], self.u_bounds[0][self.control_mask]])
-        hi = torch.cat([self.x_bounds[1][self.state_mask], self.u_bounds[1][self.control_mask]])
+        _, idx, lo, hi = self._box_rows()
+        g = torch.cat([states, controls], dim=-1).index_select(-1, idx)
         return g, lo.expand_as(g), hi.expand_as(g)
 
     # -------------------------------------------------------- parameters ----
@@ -233,7 +249,7 @@ class QuadraticTrackingOCP:
             other.wu = cv(weights[k[1]], self.wu)
         if k[2] in weights:
             other.wf = cv(weights[k[2]], self.wf)
-        other._static = None
+        other._static, other._memo = None, {}
         return other
 
     def with_params(self, problem_params: Optional[Dict[str, torch.Tensor]]) -> "QuadraticTrackingOCP":
@@ -245,7 +261,7 @@ class QuadraticTrackingOCP:
             return self
         other = copy.copy(self)
         other.x0 = as_tensor(problem_params["initial_state"], self.dtype, self.device).expand_as(self.x0).contiguous()
-        other._static = None
+        other._static, other._memo = None, {}
         return other
 
     def weight_gradient(self, states, controls, dx_states, dx_controls) -> Dict[str, torch.Tensor]:
@@ -302,7 +318,27 @@ class QuadraticTrackingOCP:
                 setattr(other, k, v.to(device=device, dtype=dtype if v.is_floating_point() else v.dtype))
             elif isinstance(v, tuple) and v and torch.is_tensor(v[0]):
                 setattr(other, k, tuple(t.to(device=device, dtype=dtype) for t in v))
-        other.dtype, other.device, other._static = dtype, device, None
+        other.dtype, other.device, other._static, other._memo = dtype, device, None, {}
+        return other
+
+    # per-problem tensors (leading axis B); subclasses add theirs
+    PER_PROBLEM = ("x0", "wx", "wu", "wf", "x_ref", "u_ref", "x_final_guess")
+
+    def tile(self, k: int) -> "QuadraticTrackingOCP":
+        """Copy holding k copies of the batch, problem b of copy j at index
+        j B + b: the merit line search evaluates every step candidate of every
+        problem in one pass over the k B problems."""
+        import copy
+
+        tiles = self._memoized("tiles", dict)
+        if k in tiles:
+            return tiles[k]
+        other = copy.copy(self)
+        for name in self.PER_PROBLEM:
+            v = getattr(self, name)
+            setattr(other, name, v.repeat(k, *([1] * (v.dim() - 1))))
+        other.B, other._static, other._memo = self.B * k, None, {}
+        tiles[k] = other
         return other
 
     def weights_dict(self) -> Dict[str, torch.Tensor]:
@@ -315,6 +351,8 @@ class QuadraticTrackingOCP:
 
 class LinearOCP(QuadraticTrackingOCP):
     """x_{t+1} = A x_t + B u_t (+ b): constant dynamics blocks, c_t = -b."""
+
+    PER_PROBLEM = QuadraticTrackingOCP.PER_PROBLEM + ("A", "Bm", "b")
 
     def __init__(self, *, A: torch.Tensor, Bm: torch.Tensor, b: Optional[torch.Tensor] = None, **kw):
         super().__init__(**kw)

@@ -38,6 +38,27 @@ def evaluate_constraints_with_bounds(program, states, controls, slacks, problem_
     return eq, viol.flatten(1).sum(dim=1), g, lo, hi
 
 
+def _candidate_merits(program, alphas, a_t, states, controls, slacks, ds, dc, dsl, mu):
+    """(B, n_alpha): merit(z + alpha dz) for every candidate.  A program that
+    can tile its batch (QuadraticTrackingOCP.tile) evaluates all candidates in
+    one pass over n_alpha B problems, candidate j at rows j B .. j B + B - 1;
+    others are evaluated one candidate at a time."""
+    A, B = len(alphas), states.shape[0]
+    if hasattr(program, "tile"):
+        stack = lambda z, dz: (z[None] + a_t.view(A, *([1] * z.dim())) * dz[None]).flatten(0, 1)  # noqa: E731
+        s_a, c_a, sl_a = stack(states, ds), stack(controls, dc), stack(slacks, dsl)
+        tiled = program.tile(A)
+        e_a, i_a, *_ = evaluate_constraints_with_bounds(tiled, s_a, c_a, sl_a)
+        m = tiled.cost(s_a, c_a, sl_a) + mu.repeat(A) * (e_a + i_a)
+        return m.view(A, B).t()
+    cand = []
+    for a in alphas:
+        s_a, c_a, sl_a = states + a * ds, controls + a * dc, slacks + a * dsl
+        e_a, i_a, *_ = evaluate_constraints_with_bounds(program, s_a, c_a, sl_a)
+        cand.append(program.cost(s_a, c_a, sl_a) + mu * (e_a + i_a))
+    return torch.stack(cand, dim=1)
+
+
 def backtracking_linesearch(program, problem_params, solver_params: Dict[str, Any], states, controls, slacks,
                             states_new, controls_new, slacks_new
                             ) -> Tuple[Tuple[torch.Tensor, torch.Tensor, torch.Tensor], torch.Tensor]:
@@ -59,15 +80,11 @@ def backtracking_linesearch(program, problem_params, solver_params: Dict[str, An
     merit = cost + mu * cl1
     merit_deriv = dcost - mu * cl1
 
-    cand, dec = [], []
-    for a in alphas:
-        s_a, c_a, sl_a = states + a * ds, controls + a * dc, slacks + a * dsl
-        e_a, i_a, *_ = evaluate_constraints_with_bounds(program, s_a, c_a, sl_a)
-        m_a = program.cost(s_a, c_a, sl_a) + mu * (e_a + i_a)
-        cand.append(m_a)
-        dec.append(m_a - (merit + eta * a * merit_deriv))
-    cand, dec = torch.stack(cand, dim=1), torch.stack(dec, dim=1)  # (B, n_alpha)
-    a_t = torch.tensor(alphas, dtype=cand.dtype, device=cand.device)
+    a_t = torch.tensor(alphas, dtype=states.dtype).to(states.device, non_blocking=True)
+    cand = _candidate_merits(program, alphas, a_t, states, controls, slacks, ds, dc, dsl, mu)  # (B, n_alpha)
+    # eta alpha rounded from its double product, as a Python scalar would be
+    ea_t = torch.tensor([eta * a for a in alphas], dtype=states.dtype).to(states.device, non_blocking=True)
+    dec = cand - (merit[:, None] + ea_t[None] * merit_deriv[:, None])
     finite = torch.isfinite(a_t)[None] & torch.isfinite(cand) & torch.isfinite(dec)
     valid = finite & (dec <= 0)
     idx = torch.arange(len(alphas), device=cand.device).expand_as(cand)

@@ -220,6 +220,9 @@ class TurboMPCSolver:
                 f"backward backend {self._backward_backend.name} needs the reference's JAX/CUDA stack; "
                 "use 'direct_hip_kkt'")
         self._forward_admm_backend, self._forward_schur_backend = _FORWARD_BACKEND_COMPONENTS[self._forward_backend]
+        # "device": the SQP loops on the device SQP step where they apply;
+        # "masked": the host-masked loop everywhere (kept for cross-checks)
+        self._sqp_loop = "device"
         self._zshape = ZShape(program.horizon, program.num_state_variables, program.num_control_variables)
         ap = self._params["admm"]
         self._admm_solver_fwd = ADMMSolver(
@@ -432,7 +435,9 @@ class TurboMPCSolver:
     def _solve_impl(self, program, states, controls, admm_state0: Optional[ADMMState] = None) -> TurboMPCSolution:
         """The SQP loop of turbompc_solver.py:1519-1760, batched with per-problem termination."""
         if (self._convergence_criterion == "first_order" and int(self._params["num_sqp_iteration_max"]) > 1
-                and self._forward_admm_backend == AdmmBackend.HIP_DIRECT and not self._params.get("linesearch")):
+                and self._forward_admm_backend == AdmmBackend.HIP_DIRECT and self._sqp_loop != "masked"):
+            if self._params.get("linesearch"):
+                return self._solve_impl_device_ls(program, states, controls, admm_state0)
             return self._solve_impl_device(program, states, controls, admm_state0)
         return self._solve_impl_masked(program, states, controls, admm_state0)
 
@@ -515,6 +520,86 @@ class TurboMPCSolver:
             solver_stats=SolverStats(admm_iters, hist[0].t(), hist[1].t(), hist[2].t()), kkt_state=kkt,
             # the last step scanned every problem's state (stopped ones keep theirs)
             nonfinite=stats.nonfinite,
+        )
+
+    def _solve_impl_device_ls(self, program, states, controls, admm_state0: Optional[ADMMState] = None
+                              ) -> TurboMPCSolution:
+        """The SQP loop with the merit line search on the device SQP step.
+        The iterate is the blend z + alpha (z_QP - z) of the previous iterate
+        and the QP solution, while the ADMM state, its own x included, is
+        carried unblended (turbompc_solver.py:1591-1604), so the step's fused
+        check (of the ADMM state's x) does not apply: the step takes the
+        activity as given (tol -1: conv >= 0 passes) and the first-order check
+        runs on the committed iterate (tmpc_sqp_first_order_*).  Stopped
+        problems are skipped by the step (their ADMM state stays as it was) and
+        keep their iterate by masked selects; relinearizing at the committed
+        iterate rebuilds a stopped problem's QP unchanged.  Same records as
+        _solve_impl_masked, without its host synchronisations."""
+        P, ap = self._params, self._params["admm"]
+        max_iter, tol = int(P["num_sqp_iteration_max"]), float(P["tol_convergence"])
+        alpha = float(ap.get("relaxation_parameter", 1.0))
+        admm = self._admm_solver_fwd
+        B, dev, dt = states.shape[0], states.device, states.dtype
+        qp = program.build_qp(states, controls)
+        own_state = admm_state0 is None
+        if admm_state0 is None:
+            admm_state0 = admm.initial_state(qp, rho_bar=ap["rho"])  # x = 0 (turbompc_solver.py:1545-1551)
+        admm_state = admm_state0
+        slacks = admm_state0.xi_g.clone()  # the iterate's slack (the state's own is updated in place)
+        conv = torch.full((B,), float("inf"), dtype=dt, device=dev)
+        admm_iters = torch.zeros((B, max_iter), dtype=torch.int32, device=dev)
+        eq_v = torch.zeros((B, max_iter), dtype=dt, device=dev)
+        in_v, conv_h = torch.zeros_like(eq_v), torch.zeros_like(eq_v)
+        ls_alphas = torch.zeros((B, max_iter), dtype=dt, device=dev)
+        num_iter = torch.zeros(B, dtype=torch.int32, device=dev)
+        active = torch.ones(B, dtype=torch.bool, device=dev)
+        g_c = None
+        ws = admm_direct_workspace(qp)
+        prev = None
+        for it in range(max_iter):
+            sw = qp.ineq.slack_penalization_weight
+            if it == 0:
+                (s_new, c_new), stats, adm_new = admm.solve(qp, admm_state, rho_bar=ap["rho"], alpha=alpha,
+                                                            slack_weight=sw, workspace=ws, donate_state=own_state)
+            else:
+                active = active & (conv > tol)
+                if tol > 0 and not bool(active.any()):
+                    break
+                warm = _warm_level(qp, prev)
+                (s_new, c_new), stats, adm_new, _, _ = admm.sqp_step(
+                    qp, admm_state, active, -1.0, rho_bar=ap["rho"], alpha=alpha, slack_weight=sw, workspace=ws,
+                    warm_records=warm is not None, warm_ineq=warm == "constraints", donate_state=True)
+            # the step (s_new, c_new, xi) - (states, controls, slacks) is scaled
+            # per problem; the ADMM state is not
+            (s_new, c_new, sl_new), ls_a = backtracking_linesearch(program, None, P, states, controls, slacks,
+                                                                 s_new, c_new, adm_new.xi_g)
+            sel = lambda a, b: torch.where(active.view(-1, *([1] * (a.dim() - 1))), a, b)  # noqa: E731
+            if it + 1 < max_iter:
+                states, controls, slacks = sel(s_new, states), sel(c_new, controls), sel(sl_new, slacks)
+                prev = qp
+                qp = program.build_qp(states, controls)
+                c_err, e_err, i_err, g = self._first_order_check(qp, states, controls, slacks, adm_new)
+            else:
+                # the last iterate is not checked: its record keeps the previous
+                # error, and G x at the QP it was solved on
+                c_err, e_err, i_err = conv, torch.zeros_like(conv), torch.zeros_like(conv)
+                g = apply_G(qp, pack_x(s_new, c_new))
+                states, controls, slacks = sel(s_new, states), sel(c_new, controls), sel(sl_new, slacks)
+            admm_state = adm_new
+            ls_alphas[:, it] = sel(ls_a, ls_alphas[:, it])
+            g_c = g if g_c is None else sel(g, g_c)
+            conv = sel(c_err, conv)
+            admm_iters[:, it] = sel(stats.num_iter, admm_iters[:, it])
+            eq_v[:, it] = sel(e_err, eq_v[:, it])
+            in_v[:, it] = sel(i_err, in_v[:, it])
+            conv_h[:, it] = sel(c_err, conv_h[:, it])
+            num_iter = num_iter + active.to(torch.int32)
+        kkt = self._build_kkt_state(states, controls, admm_state, g_c, qp.ineq.l, qp.ineq.u)
+        return TurboMPCSolution(
+            states=states, controls=controls, slack=admm_state.xi_g, status=self.STATUS_SUCCESS, num_iter=num_iter,
+            convergence_error=conv, admm_iters=admm_iters, linesearch_alphas=ls_alphas, admm_state=admm_state,
+            solver_stats=SolverStats(admm_iters, eq_v, in_v, conv_h), kkt_state=kkt,
+            nonfinite=_nonfinite(states, controls, *admm_state),
         )
 
     def _solve_impl_masked(self, program, states, controls, admm_state0: Optional[ADMMState] = None) -> TurboMPCSolution:
