@@ -434,11 +434,11 @@ class TurboMPCSolver:
 
     def _solve_impl(self, program, states, controls, admm_state0: Optional[ADMMState] = None) -> TurboMPCSolution:
         """The SQP loop of turbompc_solver.py:1519-1760, batched with per-problem termination."""
-        if (self._convergence_criterion == "first_order" and int(self._params["num_sqp_iteration_max"]) > 1
-                and self._forward_admm_backend == AdmmBackend.HIP_DIRECT and self._sqp_loop != "masked"):
-            if self._params.get("linesearch"):
-                return self._solve_impl_device_ls(program, states, controls, admm_state0)
-            return self._solve_impl_device(program, states, controls, admm_state0)
+        if (int(self._params["num_sqp_iteration_max"]) > 1 and self._forward_admm_backend == AdmmBackend.HIP_DIRECT
+                and self._sqp_loop != "masked"):
+            if self._convergence_criterion == "first_order" and not self._params.get("linesearch"):
+                return self._solve_impl_device(program, states, controls, admm_state0)
+            return self._solve_impl_device_ls(program, states, controls, admm_state0)
         return self._solve_impl_masked(program, states, controls, admm_state0)
 
     def _solve_impl_device(self, program, states, controls, admm_state0: Optional[ADMMState] = None) -> TurboMPCSolution:
@@ -524,18 +524,21 @@ class TurboMPCSolver:
 
     def _solve_impl_device_ls(self, program, states, controls, admm_state0: Optional[ADMMState] = None
                               ) -> TurboMPCSolution:
-        """The SQP loop with the merit line search on the device SQP step.
-        The iterate is the blend z + alpha (z_QP - z) of the previous iterate
-        and the QP solution, while the ADMM state, its own x included, is
-        carried unblended (turbompc_solver.py:1591-1604), so the step's fused
-        check (of the ADMM state's x) does not apply: the step takes the
-        activity as given (tol -1: conv >= 0 passes) and the first-order check
-        runs on the committed iterate (tmpc_sqp_first_order_*).  Stopped
-        problems are skipped by the step (their ADMM state stays as it was) and
-        keep their iterate by masked selects; relinearizing at the committed
-        iterate rebuilds a stopped problem's QP unchanged.  Same records as
+        """The SQP loop on the device SQP step for the merit line search and
+        the `step` criterion, where the step's fused check (of the ADMM
+        state's x) is not the convergence error.  With the line search the
+        iterate is the blend z + alpha (z_QP - z) of the previous iterate and
+        the QP solution, while the ADMM state, its own x included, is carried
+        unblended (turbompc_solver.py:1591-1604); the first-order check then
+        runs on the committed iterate (tmpc_sqp_first_order_*).  The `step`
+        criterion takes max |z_new - z| (+ the slack step) instead.  The step
+        takes the activity as given (tol -1: every conv >= 0 passes): stopped
+        problems are skipped (their ADMM state stays as it was) and keep their
+        iterate by masked selects, and relinearizing at the committed iterate
+        rebuilds a stopped problem's QP unchanged.  Same records as
         _solve_impl_masked, without its host synchronisations."""
         P, ap = self._params, self._params["admm"]
+        use_ls, by_step = bool(P.get("linesearch", False)), self._convergence_criterion == "step"
         max_iter, tol = int(P["num_sqp_iteration_max"]), float(P["tol_convergence"])
         alpha = float(ap.get("relaxation_parameter", 1.0))
         admm = self._admm_solver_fwd
@@ -550,10 +553,11 @@ class TurboMPCSolver:
         admm_iters = torch.zeros((B, max_iter), dtype=torch.int32, device=dev)
         eq_v = torch.zeros((B, max_iter), dtype=dt, device=dev)
         in_v, conv_h = torch.zeros_like(eq_v), torch.zeros_like(eq_v)
-        ls_alphas = torch.zeros((B, max_iter), dtype=dt, device=dev)
+        ls_alphas = torch.zeros((B, max_iter), dtype=dt, device=dev) if use_ls else None
         num_iter = torch.zeros(B, dtype=torch.int32, device=dev)
         active = torch.ones(B, dtype=torch.bool, device=dev)
         g_c = None
+        z_prev = pack_z(states, controls) if by_step else None
         ws = admm_direct_workspace(qp)
         prev = None
         for it in range(max_iter):
@@ -569,16 +573,31 @@ class TurboMPCSolver:
                 (s_new, c_new), stats, adm_new, _, _ = admm.sqp_step(
                     qp, admm_state, active, -1.0, rho_bar=ap["rho"], alpha=alpha, slack_weight=sw, workspace=ws,
                     warm_records=warm is not None, warm_ineq=warm == "constraints", donate_state=True)
-            # the step (s_new, c_new, xi) - (states, controls, slacks) is scaled
-            # per problem; the ADMM state is not
-            (s_new, c_new, sl_new), ls_a = backtracking_linesearch(program, None, P, states, controls, slacks,
-                                                                 s_new, c_new, adm_new.xi_g)
+            sl_new = adm_new.xi_g
+            if use_ls:
+                # the step (s_new, c_new, xi) - (states, controls, slacks) is
+                # scaled per problem; the ADMM state is not
+                (s_new, c_new, sl_new), ls_a = backtracking_linesearch(program, None, P, states, controls, slacks,
+                                                                     s_new, c_new, sl_new)
             sel = lambda a, b: torch.where(active.view(-1, *([1] * (a.dim() - 1))), a, b)  # noqa: E731
+            if by_step:
+                z_new = pack_z(s_new, c_new)
+                c_err = (z_new - z_prev).abs().amax(dim=1)
+                if sl_new.shape[-1] > 0:
+                    c_err = c_err + (sl_new - slacks).abs().flatten(1).amax(dim=1)
+                e_err = i_err = torch.zeros_like(c_err)
+                z_prev = sel(z_new, z_prev)
             if it + 1 < max_iter:
                 states, controls, slacks = sel(s_new, states), sel(c_new, controls), sel(sl_new, slacks)
                 prev = qp
                 qp = program.build_qp(states, controls)
-                c_err, e_err, i_err, g = self._first_order_check(qp, states, controls, slacks, adm_new)
+                if by_step:
+                    g = apply_G(qp, pack_x(states, controls))
+                else:
+                    c_err, e_err, i_err, g = self._first_order_check(qp, states, controls, slacks, adm_new)
+            elif by_step:
+                g = apply_G(qp, pack_x(s_new, c_new))
+                states, controls, slacks = sel(s_new, states), sel(c_new, controls), sel(sl_new, slacks)
             else:
                 # the last iterate is not checked: its record keeps the previous
                 # error, and G x at the QP it was solved on
@@ -586,7 +605,8 @@ class TurboMPCSolver:
                 g = apply_G(qp, pack_x(s_new, c_new))
                 states, controls, slacks = sel(s_new, states), sel(c_new, controls), sel(sl_new, slacks)
             admm_state = adm_new
-            ls_alphas[:, it] = sel(ls_a, ls_alphas[:, it])
+            if use_ls:
+                ls_alphas[:, it] = sel(ls_a, ls_alphas[:, it])
             g_c = g if g_c is None else sel(g, g_c)
             conv = sel(c_err, conv)
             admm_iters[:, it] = sel(stats.num_iter, admm_iters[:, it])
