@@ -249,6 +249,10 @@ class TurboMPCSolver:
     name = property(lambda self: self._name)
     forward_backend = property(lambda self: self._forward_backend)
     backward_backend = property(lambda self: self._backward_backend)
+    # the direct adjoint solve runs no ADMM; direct backward backends report
+    # these values in the reference too (turbompc_solver.py:329-334)
+    backward_admm_backend = property(lambda self: AdmmBackend.JAX_LOOP)
+    backward_schur_backend = property(lambda self: SchurSolverBackend.IGNORED)
     forward_admm_backend = property(lambda self: self._forward_admm_backend)
     forward_schur_backend = property(lambda self: self._forward_schur_backend)
 
@@ -279,6 +283,7 @@ class TurboMPCSolver:
         get_differentiable_solve_function, turbompc_solver.py:1052-1084): returns
         (problem_params cotangent {"initial_state": dL/dx0 (B, nx)}, dL/dweights
         {key: (B, ...)}) for the cotangents of the solution's states and controls."""
+        problem_params, weights = self._split_params(problem_params, weights)
         program = self._program_for(problem_params, weights)
         if solution.kkt_state is None:
             raise ValueError("the solution carries no KKT state (no SQP iteration ran)")
@@ -300,7 +305,41 @@ class TurboMPCSolver:
         of turbompc_solver.py:1020-1090)."""
         return DifferentiableSolve(self)
 
+    def make_params_with_weights(self, weights, problem_params=None) -> Dict[str, Any]:
+        """problem_params (or {}) with the entries of `weights` merged in
+        (make_params_with_weights, turbompc_solver.py:511-526); solve and
+        solve_vjp take the weight keys from problem_params as from `weights`."""
+        def merge(dst, src):
+            for k, v in src.items():
+                if isinstance(v, dict) and isinstance(dst.get(k), dict):
+                    merge(dst[k], v)
+                else:
+                    dst[k] = v
+
+        out = dict(problem_params) if problem_params else {}
+        merge(out, dict(weights) if weights else {})
+        return out
+
+    def linesearch(self, states, controls, slacks, states_new, controls_new, slacks_new, problem_params=None):
+        """The merit line search along the SQP step (turbompc_solver.py:1480-1501):
+        ((states, controls, slacks) at the accepted step, alpha (B,))."""
+        program = self._program_for(problem_params, None)
+        return backtracking_linesearch(program, None, self._params, states, controls, slacks, states_new,
+                                       controls_new, slacks_new)
+
+    def _split_params(self, problem_params, weights):
+        """(problem_params, weights) with weight keys merged into problem_params
+        (make_params_with_weights) moved to the weights."""
+        if problem_params:
+            wkeys = set(getattr(self._program, "WEIGHT_KEYS", ())) | {"slack_penalization_weight"}
+            inline = {k: v for k, v in problem_params.items() if k in wkeys}
+            if inline:
+                weights = {**inline, **(weights or {})}
+                problem_params = {k: v for k, v in problem_params.items() if k not in wkeys}
+        return problem_params, weights
+
     def _program_for(self, problem_params, weights):
+        problem_params, weights = self._split_params(problem_params, weights)
         program = self._program
         if weights:
             program = program.with_weights(weights)
