@@ -69,6 +69,13 @@ def test_shape_and_argument_errors_return_before_any_launch(lib):
     assert st == 2  # TMPC_EBADARG: null QP / state pointers
     assert lib.tmpc_blktri_factor_f32(None, 4, 1, 17, None, None, 0) == 1
     assert lib.tmpc_blktri_factor_f32(None, 4, 10, 17, None, None, 0) == 2
+    # obstacle rows: dim <= nx, row0 + K <= m, n = nx + nu <= 64, then pointers
+    obst = lambda nx, nu, dim, K, m, row0: lib.tmpc_obstacle_linearize_f32(  # noqa: E731
+        None, 4, 10, nx, nu, dim, K, None, None, None, m, row0, None, None, None)
+    assert obst(6, 3, 7, 8, 11, 3) == 1
+    assert obst(6, 3, 3, 8, 10, 3) == 1
+    assert obst(40, 25, 3, 8, 11, 3) == 1
+    assert obst(6, 3, 3, 8, 11, 3) == 2
 
 
 def test_noalloc_entry_rejects_on_the_host(lib):

@@ -1099,7 +1099,8 @@ int quad_hess_impl(hipStream_t s, int B, int N, const R* states, const R* contro
 
 // ------------------------------------------------------------- obstacles ----
 inline int obstacle_check(int B, int N, int nx, int nu, int dim, int K, int m, int row0) {
-  if (B < 1 || N < 1 || nx < 1 || nu < 0 || dim < 1 || dim > nx || K < 0 || row0 < 0 || row0 + K > m)
+  if (B < 1 || N < 1 || nx < 1 || nu < 0 || nx + nu > 64 || dim < 1 || dim > nx || K < 0 || row0 < 0 ||
+      row0 + K > m)
     return TMPC_EBADSHAPE;
   return TMPC_OK;
 }
@@ -1112,11 +1113,12 @@ int obstacle_lin_impl(hipStream_t s, int B, int N, int nx, int nu, int dim, int 
   if (K == 0) return TMPC_OK;
   if (!states || !centers || !radii || !G || !l || !u) return TMPC_EBADARG;
   const int T = N + 1, n = nx + nu;
-  const long long total = (long long)B * T * K * n;
-  const int blk = 256;
-  const long long grid = (total + blk - 1) / blk;
-  if (grid > INT32_MAX) return TMPC_EBADSHAPE;
-  hipLaunchKernelGGL((obstacle_linearize_kernel<R>), dim3((unsigned)grid), dim3(blk), 0, s, B, T, nx, n, dim, K,
+  const long long rows = (long long)B * T * K;  // one thread per obstacle row
+  if (rows >= INT32_MAX) return TMPC_EBADSHAPE;
+  const int blk = kObstacleBlock;
+  const long long grid = (rows + blk - 1) / blk;
+  const size_t smem = (size_t)blk * n * sizeof(R);  // n <= 64: at most 64 KB
+  hipLaunchKernelGGL((obstacle_linearize_kernel<R>), dim3((unsigned)grid), dim3(blk), smem, s, B, T, nx, n, dim, K,
                      states, centers, radii, m, row0, G, l, u);
   return launch_status();
 }
@@ -1128,10 +1130,10 @@ int obstacle_hess_impl(hipStream_t s, int B, int N, int nx, int nu, int dim, int
   if (st) return st;
   if (!states || !H || !mus || (K > 0 && (!centers || !radii))) return TMPC_EBADARG;
   const int T = N + 1, n = nx + nu;
-  const long long total = (long long)B * T * n * n;
+  const long long stages = (long long)B * T;  // one thread per stage
+  if (stages >= INT32_MAX) return TMPC_EBADSHAPE;
   const int blk = 256;
-  const long long grid = (total + blk - 1) / blk;
-  if (grid > INT32_MAX) return TMPC_EBADSHAPE;
+  const long long grid = (stages + blk - 1) / blk;
   hipLaunchKernelGGL((obstacle_hessian_kernel<R>), dim3((unsigned)grid), dim3(blk), 0, s, B, T, nx, n, dim, K,
                      states, centers, radii, m, row0, mus, H);
   return launch_status();

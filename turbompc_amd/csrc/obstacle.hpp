@@ -28,72 +28,95 @@ namespace tmpc {
 constexpr double kObstacleMargin = 0.001;
 constexpr double kObstacleLower = -1.0e9;
 
-// One thread per G entry (b, t, k, j): the G rows are written with adjacent
-// threads on adjacent columns; thread j = 0 also writes l and u.  Each thread
-// recomputes the distance (dim <= nx terms), which is cheaper than staging it.
+// One thread per obstacle row (b, t, k), k fastest: the distance once, the
+// row's n G entries into LDS, l and u directly; then the block writes its
+// rows' G entries with adjacent threads on adjacent entries (a stage's K rows
+// are contiguous in G).  Row indices are 32-bit (the host checks
+// B T K < 2^31); G addresses are formed in 64 bits.
+constexpr int kObstacleBlock = 128;
+
 template <typename R>
-__global__ void obstacle_linearize_kernel(int B, int T, int nx, int n, int dim, int K, const R* __restrict__ states,
-                                          const R* __restrict__ centers, const R* __restrict__ radii, int m,
-                                          int row0, R* __restrict__ G, R* __restrict__ l, R* __restrict__ u) {
-  const long long e = (long long)blockIdx.x * blockDim.x + threadIdx.x;
-  const long long total = (long long)B * T * K * n;
-  if (e >= total) return;
-  const int j = (int)(e % n);
-  const long long r = e / n;  // (b, t, k)
-  const int k = (int)(r % K);
-  const long long bt = r / K;
-  const int b = (int)(bt / T);
-  const R* x = states + bt * nx;
-  const R* c = centers + ((long long)b * K + k) * dim;
-  R ss = R(0);
-  for (int i = 0; i < dim; ++i) {
-    const R d = x[i] - c[i];
-    ss += d * d;
-  }
-  const R nrm = sqrt(ss);
-  const R den = radii[(long long)b * K + k] + R(kObstacleMargin);
-  const long long row = bt * m + row0 + k;
-  G[row * n + j] = j < dim ? -((x[j] - c[j]) / nrm) / den : R(0);
-  if (j == 0) {
+__global__ __launch_bounds__(kObstacleBlock) void obstacle_linearize_kernel(int B, int T, int nx, int n, int dim,
+                                                                            int K, const R* __restrict__ states,
+                                                                            const R* __restrict__ centers,
+                                                                            const R* __restrict__ radii, int m,
+                                                                            int row0, R* __restrict__ G,
+                                                                            R* __restrict__ l, R* __restrict__ u) {
+  extern __shared__ __align__(16) unsigned char smem_raw[];
+  R* rowv = reinterpret_cast<R*>(smem_raw);  // [kObstacleBlock][n]
+  const unsigned rows = (unsigned)B * (unsigned)T * (unsigned)K;
+  const unsigned r0 = blockIdx.x * kObstacleBlock;
+  const unsigned r = r0 + threadIdx.x;
+  if (r < rows) {
+    const unsigned bt = r / (unsigned)K, k = r - bt * (unsigned)K;
+    const unsigned b = bt / (unsigned)T;
+    const R* x = states + (size_t)bt * nx;
+    const R* c = centers + ((size_t)b * K + k) * dim;
+    R ss = R(0);
+    for (int i = 0; i < dim; ++i) {
+      const R d = x[i] - c[i];
+      ss += d * d;
+    }
+    const R nrm = sqrt(ss);
+    const R den = radii[(size_t)b * K + k] + R(kObstacleMargin);
+    R* g = rowv + threadIdx.x * n;
     R gx = R(0);  // dg/dx . xbar over the position block (zero elsewhere)
-    for (int i = 0; i < dim; ++i) gx += (-((x[i] - c[i]) / nrm) / den) * x[i];
+    for (int j = 0; j < dim; ++j) {
+      const R gj = -((x[j] - c[j]) / nrm) / den;
+      g[j] = gj;
+      gx += gj * x[j];
+    }
+    for (int j = dim; j < n; ++j) g[j] = R(0);
     const R off = (R(1) - nrm / den) - gx;
+    const size_t row = (size_t)bt * m + row0 + k;
     l[row] = R(kObstacleLower) - off;
     u[row] = R(0) - off;
   }
+  __syncthreads();
+  const unsigned nb = rows - r0 < (unsigned)kObstacleBlock ? rows - r0 : (unsigned)kObstacleBlock;
+  for (unsigned e = threadIdx.x; e < nb * (unsigned)n; e += kObstacleBlock) {
+    const unsigned lr = e / (unsigned)n, j = e - lr * (unsigned)n;
+    const unsigned rr = r0 + lr, bt = rr / (unsigned)K, k = rr - bt * (unsigned)K;
+    G[((size_t)bt * m + row0 + k) * n + j] = rowv[e];
+  }
 }
 
-// One thread per H entry (b, t, i, j).
+// One thread per stage (b, t): the position block of
+// sum_k mu_k d^2 g_k / dx^2, written with the zeros of the rest of the n x n
+// block.  Stage indices are 32-bit (the host checks B T < 2^31).
 template <typename R>
-__global__ void obstacle_hessian_kernel(int B, int T, int nx, int n, int dim, int K, const R* __restrict__ states,
-                                        const R* __restrict__ centers, const R* __restrict__ radii, int m, int row0,
-                                        const R* __restrict__ mus, R* __restrict__ H) {
-  const long long e = (long long)blockIdx.x * blockDim.x + threadIdx.x;
-  const long long total = (long long)B * T * n * n;
-  if (e >= total) return;
-  const int j = (int)(e % n);
-  const int i = (int)((e / n) % n);
-  const long long bt = e / ((long long)n * n);
-  const int b = (int)(bt / T);
-  R h = R(0);
-  if (i < dim && j < dim) {
-    const R* x = states + bt * nx;
-    const R* mu = mus + bt * m + row0;
-    for (int k = 0; k < K; ++k) {
-      const R* c = centers + ((long long)b * K + k) * dim;
-      R ss = R(0);
-      for (int q = 0; q < dim; ++q) {
-        const R d = x[q] - c[q];
-        ss += d * d;
+__global__ __launch_bounds__(256) void obstacle_hessian_kernel(int B, int T, int nx, int n, int dim, int K,
+                                                               const R* __restrict__ states,
+                                                               const R* __restrict__ centers,
+                                                               const R* __restrict__ radii, int m, int row0,
+                                                               const R* __restrict__ mus, R* __restrict__ H) {
+  const unsigned bt = blockIdx.x * blockDim.x + threadIdx.x;
+  if (bt >= (unsigned)B * (unsigned)T) return;
+  const unsigned b = bt / (unsigned)T;
+  const R* x = states + (size_t)bt * nx;
+  const R* mu = mus + (size_t)bt * m + row0;
+  R* h = H + (size_t)bt * n * n;
+  for (int i = 0; i < n; ++i) {
+    for (int j = 0; j < n; ++j) {
+      R v = R(0);
+      if (i < dim && j < dim) {
+        for (int k = 0; k < K; ++k) {
+          const R* c = centers + ((size_t)b * K + k) * dim;
+          R ss = R(0);
+          for (int q = 0; q < dim; ++q) {
+            const R d = x[q] - c[q];
+            ss += d * d;
+          }
+          const R nrm = sqrt(ss);
+          const R den = radii[(size_t)b * K + k] + R(kObstacleMargin);
+          const R di = x[i] - c[i], dj = x[j] - c[j];
+          const R hn = (i == j ? R(1) / nrm : R(0)) - di * dj / (nrm * nrm * nrm);
+          v += mu[k] * (-hn / den);
+        }
       }
-      const R nrm = sqrt(ss);
-      const R den = radii[(long long)b * K + k] + R(kObstacleMargin);
-      const R di = x[i] - c[i], dj = x[j] - c[j];
-      const R hn = (i == j ? R(1) / nrm : R(0)) - di * dj / (nrm * nrm * nrm);
-      h += mu[k] * (-hn / den);
+      h[i * n + j] = v;
     }
   }
-  H[e] = h;
 }
 
 }  // namespace tmpc
