@@ -339,16 +339,31 @@ __global__ __launch_bounds__(256) void stage_repack_dynamics_kernel(Dims d, cons
   }
 }
 
-// The state back from the rv records: a block handles stage t of
-// kRepackProblems consecutive problems, one thread per state value of a stage
-// (x, z, y_g, xi, then y_f for t < N) across those problems.
+// The state back from the rv records, and each problem's non-finite flag
+// (bit 31 of iters[b], TMPC_ITERS_NONFINITE; on this path in place of
+// nonfinite_flag_kernel).  A block handles stage t of kUnpackProblems
+// consecutive problems; work item (j, k) is state value k (x, z, y_g, xi, then
+// y_f for t < N) of problem b0 + j, k fastest, so that the reads of one record
+// and the writes of one row are contiguous runs.  Blocks of stage 0 also scan
+// y_f0 and rho, which the iteration kernel writes directly.  A problem's flag
+// is set by atomicOr from each block that meets one of its non-finite values
+// (the result does not depend on their order).
+constexpr int kUnpackProblems = 32;
+
 template <typename R>
-__global__ __launch_bounds__(256) void stage_unpack_kernel(Dims d, const R* __restrict__ rv, StateDev<R> st) {
-  const int t = blockIdx.y, b0 = blockIdx.x * kRepackProblems;
+__global__ __launch_bounds__(256) void stage_unpack_kernel(Dims d, const R* __restrict__ rv, StateDev<R> st,
+                                                           uint32_t* __restrict__ iters) {
+  __shared__ uint32_t bad[kUnpackProblems];
+  const int t = blockIdx.y, b0 = blockIdx.x * kUnpackProblems;
   const int B = d.B, T = d.T, N = d.N, n = d.nq, nx = d.nx, m = d.m;  // n: the state's row length
   const RecGeom g = rec_geom(d);
   const int per = n + 3 * m + (t < N ? nx : 0);
-  for (int k = threadIdx.x; k < per; k += blockDim.x) {
+  const int nb = min(kUnpackProblems, B - b0);
+  if (threadIdx.x < kUnpackProblems) bad[threadIdx.x] = 0u;
+  __syncthreads();
+  const unsigned total = (unsigned)(nb * per);
+  for (unsigned idx = threadIdx.x; idx < total; idx += blockDim.x) {
+    const int j = (int)(idx / (unsigned)per), k = (int)idx - j * per;
     // source offset in the record, destination array and its per-problem pitch
     int src, e, pitch;
     R* dst;
@@ -364,20 +379,23 @@ __global__ __launch_bounds__(256) void stage_unpack_kernel(Dims d, const R* __re
       src = g.yf + (k - n - 3 * m); dst = st.y_f; e = k - n - 3 * m; pitch = nx;
     }
     const bool dyn = k >= n + 3 * m;  // y_f: (B, N, nx); the others (B, T, .)
-    R v[kRepackProblems];
-#pragma unroll
-    for (int j = 0; j < kRepackProblems; ++j) {
-      const int b = min(b0 + j, B - 1);
-      v[j] = rv[((size_t)t * B + b) * g.rvp + src];
-    }
-#pragma unroll
-    for (int j = 0; j < kRepackProblems; ++j) {
+    const int b = b0 + j;
+    const R v = rv[((size_t)t * B + b) * g.rvp + src];
+    const size_t row = dyn ? (size_t)b * N + t : (size_t)b * T + t;
+    dst[row * pitch + e] = v;
+    if (!__builtin_isfinite(v)) bad[j] = 1u;
+  }
+  if (t == 0) {
+    const int n0 = d.n0, pe = n0 + 1;
+    for (unsigned idx = threadIdx.x; idx < (unsigned)(nb * pe); idx += blockDim.x) {
+      const int j = (int)(idx / (unsigned)pe), k = (int)idx - j * pe;
       const int b = b0 + j;
-      if (b >= B) break;
-      const size_t row = dyn ? (size_t)b * N + t : (size_t)b * T + t;
-      dst[row * pitch + e] = v[j];
+      const R* p = k < n0 ? (st.y_f0 ? st.y_f0 + (size_t)b * n0 + k : nullptr) : (st.rho ? st.rho + b : nullptr);
+      if (p && !__builtin_isfinite(*p)) bad[j] = 1u;
     }
   }
+  __syncthreads();
+  if (iters && threadIdx.x < nb && bad[threadIdx.x]) atomicOr(iters + b0 + threadIdx.x, 0x80000000u);
 }
 
 // ---- wavefront helpers ---------------------------------------------------------

@@ -562,12 +562,11 @@ int admm_direct_impl(hipStream_t s, const tmpc_dims* dims, const tmpc_qp* qp,
     if (st) return st;
   }
   if (g_iter_events[1] && hipEventRecord(g_iter_events[1], s) != hipSuccess) return TMPC_ELAUNCH;
-  if (stream) {
+  if (stream) {  // the unpack also sets the non-finite flags
     hipLaunchKernelGGL((stage_unpack_kernel<R>),
-                       dim3((unsigned)((d.B + kRepackProblems - 1) / kRepackProblems), (unsigned)d.T), dim3(256), 0, s,
-                       dr, (const R*)w.rv, a.st);
-    st = launch_status();
-    if (st) return st;
+                       dim3((unsigned)((d.B + kUnpackProblems - 1) / kUnpackProblems), (unsigned)d.T), dim3(256), 0,
+                       s, dr, (const R*)w.rv, a.st, iters);
+    return launch_status();
   }
   return launch_nonfinite_flags<R>(s, d, a.st, iters);
 }
