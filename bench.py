@@ -82,11 +82,12 @@ def sqp_params(n_sqp, admm_iters):
     return params
 
 
-def make_solver(prob, n_sqp, admm_iters):
+def make_solver(prob, n_sqp, admm_iters, linesearch=False):
     from turbompc_amd.solvers.turbompc_solver import TurboMPCSolver
 
-    return TurboMPCSolver(prob, sqp_params(n_sqp, admm_iters), forward_backend="admm_hip_direct",
-                          backward_backend="direct_hip_kkt")
+    params = sqp_params(n_sqp, admm_iters)
+    params["linesearch"] = bool(linesearch)
+    return TurboMPCSolver(prob, params, forward_backend="admm_hip_direct", backward_backend="direct_hip_kkt")
 
 
 # ------------------------------------------------------------ CPU baseline ----
@@ -320,7 +321,7 @@ def run_sqp_workload(args, dev):
         prob = configs.config4(B=B, seed=args.seed).to(dev, torch.float32)
     else:
         prob = make_quadrotor_config(B=B, seed=args.seed, dtype=torch.float32, device=dev)
-    solver = make_solver(prob, args.sqp, args.admm_iters)
+    solver = make_solver(prob, args.sqp, args.admm_iters, args.linesearch)
     guess = solver.initial_guess()
     with SolveTimer(dev) as timer:
         elapsed, sol = timed_steps(lambda: solver.solve(guess), args.steps, args.warmup, timer)
@@ -338,12 +339,15 @@ def run_sqp_workload(args, dev):
         per_qp, F, It = bytes_per_qp(T, 17, 13, 13, 4, args.admm_iters, 4)
         workload = ("config 3: quadrotor nonlinear SQP, nx=13 nu=4 N=40, RK4 dt=0.02, 5 SQP x 20 ADMM, "
                     "direct block-tridiagonal KKT backend")
+    if args.linesearch:
+        workload += ", merit line search (alphas 0.1 0.3 0.7 1.0) after every QP solve"
         data = "synthetic (seeded quadrotor fleet: random goals, perturbed hover starts)"
     iter_bytes = B * args.admm_iters * It  # algorithmic bytes of one iteration-kernel launch
     achieved = iter_bytes / iter_avg_s / 1e9
     qp_achieved = per_qp * B / solve_avg_s / 1e9
     finite = bool(torch.isfinite(sol.states).all() and torch.isfinite(sol.controls).all())
-    line = base_line(f"MPC solves/sec at B={B}{', config 4' if c4 else ''} (1 MI355X)", B * args.steps / elapsed,
+    label = (", config 4" if c4 else "") + (", merit line search" if args.linesearch else "")
+    line = base_line(f"MPC solves/sec at B={B}{label} (1 MI355X)", B * args.steps / elapsed,
                      args, elapsed, "f32", data, {
                          "workload": workload, "batch": B, "horizon": prob.horizon, "sqp_iterations": args.sqp,
                          "admm_iterations": args.admm_iters, "parallelism": "single GPU, batch-parallel",
@@ -525,6 +529,8 @@ def main():
     ap.add_argument("--pcg-kernel", choices=("dpp", "lds", "chunk"), default="dpp",
                     help="config2 only: the one-launch kernels (dpp: a stage per 16-lane row, lds: LDS-resident) "
                          "or the chunk kernel that streams S and Phiinv")
+    ap.add_argument("--linesearch", action="store_true",
+                    help="config3 / config4: the merit line search after every QP solve (a secondary line)")
     ap.add_argument("--cpu-baseline", type=int, default=1)
     ap.add_argument("--cpu-budget", type=float, default=15.0, help="seconds of CPU work for the baseline sample")
     ap.add_argument("--copy-calibration", type=int, default=0,
@@ -550,7 +556,7 @@ def main():
         line = run_config5(args, dev)
     else:
         line = run_config2(args, dev)
-    if args.cpu_baseline:
+    if args.cpu_baseline and not args.linesearch:  # the CPU port times the workload without the line search
         line["cpu_baseline"] = cpu_baseline(args.workload, args.batch, args)
     print(json.dumps(line), flush=True)
 

@@ -305,6 +305,17 @@ int tmpc_quadrotor_dynamics_f32(hipStream_t stream, int32_t B, int32_t N, const 
 int tmpc_quadrotor_dynamics_f64(hipStream_t stream, int32_t B, int32_t N, const double* states,
                                 const double* controls, double dt, const double* params, double* next);
 
+/* Linear dynamics: next (B,N,nx) = A x_t + Bm u_t + b for t < N, the dynamics
+ * part of equality_constraints (turbompc/problems/optimal_control_problem.py:841-912)
+ * for LinearDynamics (turbompc/dynamics/linear_dynamics.py:28-70), which the
+ * merit line search evaluates at trial points (turbompc/solvers/linesearch.py:14-52).
+ * states (B,N+1,nx), controls (B,N+1,nu), A (B,nx,nx), Bm (B,nx,nu), b (B,nx). */
+int tmpc_linear_dynamics_f32(hipStream_t stream, int32_t B, int32_t N, int32_t nx, int32_t nu, const float* states,
+                             const float* controls, const float* A, const float* Bm, const float* b, float* next);
+int tmpc_linear_dynamics_f64(hipStream_t stream, int32_t B, int32_t N, int32_t nx, int32_t nu, const double* states,
+                             const double* controls, const double* A, const double* Bm, const double* b,
+                             double* next);
+
 /* Lagrangian Hessian of the same dynamics rows for the exact-Hessian backward
  * pass: replaces get_dynamics_lagrangian_hessian for explicit schemes
  * (turbompc/problems/optimal_control_problem.py:1334-1441), called from

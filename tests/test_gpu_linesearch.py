@@ -53,6 +53,21 @@ def test_quadrotor_dynamics_kernel_matches_cpu(dtype):
     assert rel_err(got, f.reshape(B, T - 1, 13)) < (1e-13 if dtype == torch.float64 else 2e-6)
 
 
+@pytest.mark.parametrize("dtype", [torch.float64, torch.float32])
+def test_linear_dynamics_kernel_matches_cpu(dtype):
+    prob = configs.config4(B=7, seed=3)  # double integrator, nx = 6, nu = 3, per-problem A, B, b
+    g = torch.Generator().manual_seed(5)
+    s = torch.randn((7, prob.horizon + 1, 6), generator=g, dtype=torch.float64)
+    u = torch.randn((7, prob.horizon + 1, 3), generator=g, dtype=torch.float64)
+    prob.b = torch.randn(prob.b.shape, generator=g, dtype=torch.float64)
+    ref = prob.next_states(s, u)  # the CPU path (einsum in fp64)
+    dev = prob.to("cuda", dtype)
+    got = dev.next_states(s.to("cuda", dtype), u.to("cuda", dtype))
+    torch.cuda.synchronize()
+    assert got.shape == ref.shape
+    assert rel_err(got, ref.numpy()) < (1e-14 if dtype == torch.float64 else 1e-6)
+
+
 def test_quadrotor_sqp_linesearch_fp64_matches_cpu():
     B, n_sqp, admm_iters = 8, 6, 20
     cpu = make_quadrotor_config(B=B, seed=0, dtype=torch.float64, device="cpu")

@@ -147,6 +147,8 @@ SIGNATURES = {
     "tmpc_sqp_first_order_f64": [_VP, _PD, _PQ, _VP, _VP, _VP, _VP, _VP, _F64, _U32, _VP, _VP, _VP, _VP],
     "tmpc_quadrotor_linearize_f32": [_VP, _I32, _I32, _VP, _VP, _F64, _VP, _VP, _VP],
     "tmpc_quadrotor_linearize_f64": [_VP, _I32, _I32, _VP, _VP, _F64, _VP, _VP, _VP],
+    "tmpc_linear_dynamics_f32": [_VP, _I32, _I32, _I32, _I32, _VP, _VP, _VP, _VP, _VP, _VP],
+    "tmpc_linear_dynamics_f64": [_VP, _I32, _I32, _I32, _I32, _VP, _VP, _VP, _VP, _VP, _VP],
     "tmpc_quadrotor_dynamics_f32": [_VP, _I32, _I32, _VP, _VP, _F64, _VP, _VP],
     "tmpc_quadrotor_dynamics_f64": [_VP, _I32, _I32, _VP, _VP, _F64, _VP, _VP],
     "tmpc_quadrotor_lagrangian_hessian_f32": [_VP, _I32, _I32, _VP, _VP, _F64, _VP, _VP, _VP],

@@ -16,6 +16,7 @@
 #include "kkt_factor.hpp"
 #include "pcg_lds.hpp"
 #include "obstacle.hpp"
+#include "linear.hpp"
 #include "quadrotor.hpp"
 #include "adjoint.hpp"
 #include "sqp.hpp"
@@ -1096,6 +1097,18 @@ int quad_hess_impl(hipStream_t s, int B, int N, const R* states, const R* contro
 }
 
 
+template <typename R>
+int linear_step_impl(hipStream_t s, int B, int N, int nx, int nu, const R* states, const R* controls, const R* A,
+                     const R* Bm, const R* b, R* next) {
+  if (B < 1 || N < 1 || nx < 1 || nu < 0) return TMPC_EBADSHAPE;
+  const long long total = (long long)B * N * nx;  // one thread per (problem, stage, row)
+  if (total >= INT32_MAX) return TMPC_EBADSHAPE;
+  if (!states || !controls || !A || (nu > 0 && !Bm) || !b || !next) return TMPC_EBADARG;
+  hipLaunchKernelGGL((linear_step_kernel<R>), dim3((unsigned)((total + 255) / 256)), dim3(256), 0, s, B, N, nx, nu,
+                     states, controls, A, Bm, b, next);
+  return launch_status();
+}
+
 // ------------------------------------------------------------- obstacles ----
 inline int obstacle_check(int B, int N, int nx, int nu, int dim, int K, int m, int row0) {
   if (B < 1 || N < 1 || nx < 1 || nu < 0 || nx + nu > 64 || dim < 1 || dim > nx || K < 0 || row0 < 0 ||
@@ -1332,6 +1345,15 @@ int tmpc_quadrotor_linearize_f64(hipStream_t s, int32_t B, int32_t N, const doub
   return quad_impl<double>(s, B, N, states, controls, dt, params, A_minus, c);
 }
 
+int tmpc_linear_dynamics_f32(hipStream_t s, int32_t B, int32_t N, int32_t nx, int32_t nu, const float* states,
+                             const float* controls, const float* A, const float* Bm, const float* b, float* next) {
+  return linear_step_impl<float>(s, B, N, nx, nu, states, controls, A, Bm, b, next);
+}
+int tmpc_linear_dynamics_f64(hipStream_t s, int32_t B, int32_t N, int32_t nx, int32_t nu, const double* states,
+                             const double* controls, const double* A, const double* Bm, const double* b,
+                             double* next) {
+  return linear_step_impl<double>(s, B, N, nx, nu, states, controls, A, Bm, b, next);
+}
 int tmpc_quadrotor_dynamics_f32(hipStream_t s, int32_t B, int32_t N, const float* states, const float* controls,
                                 double dt, const double* params, float* next) {
   return quad_step_impl<float>(s, B, N, states, controls, dt, params, next);

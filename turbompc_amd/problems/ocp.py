@@ -365,9 +365,25 @@ class LinearOCP(QuadraticTrackingOCP):
         return None  # linear dynamics
 
     def next_states(self, states, controls):
-        xn = torch.einsum("bij,btj->bti", self.A, states[:, :-1]) + torch.einsum("bij,btj->bti", self.Bm,
-                                                                                controls[:, :-1])
-        return xn + self.b.unsqueeze(1)
+        """(B, N, nx): A x_t + B u_t + b (tmpc_linear_dynamics_* on the device: a
+        batched GEMM of these tiny blocks takes milliseconds)."""
+        if not states.is_cuda:
+            xn = torch.einsum("bij,btj->bti", self.A, states[:, :-1]) + torch.einsum("bij,btj->bti", self.Bm,
+                                                                                    controls[:, :-1])
+            return xn + self.b.unsqueeze(1)
+        from .. import _lib
+
+        lib = _lib.load()
+        B, N, nx, nu = states.shape[0], self.horizon, self.num_state_variables, self.num_control_variables
+        c = lambda t: t.to(self.dtype).contiguous()  # noqa: E731
+        states, controls, A, Bm, b = c(states), c(controls), c(self.A), c(self.Bm), c(self.b)
+        if A.shape[0] != B:
+            raise ValueError(f"states of {B} problems for a problem of {A.shape[0]}")
+        nxt = torch.empty((B, N, nx), dtype=self.dtype, device=states.device)
+        fn = f"tmpc_linear_dynamics_{_lib.suffix(self.dtype)}"
+        _lib.check(fn, getattr(lib, fn)(_lib.stream_handle(states.device), B, N, nx, nu, _lib.ptr(states),
+                                        _lib.ptr(controls), _lib.ptr(A), _lib.ptr(Bm), _lib.ptr(b), _lib.ptr(nxt)))
+        return nxt
 
     def dynamics_blocks(self, states, controls):
         N = self.horizon
