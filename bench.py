@@ -339,9 +339,9 @@ def run_sqp_workload(args, dev):
         per_qp, F, It = bytes_per_qp(T, 17, 13, 13, 4, args.admm_iters, 4)
         workload = ("config 3: quadrotor nonlinear SQP, nx=13 nu=4 N=40, RK4 dt=0.02, 5 SQP x 20 ADMM, "
                     "direct block-tridiagonal KKT backend")
+        data = "synthetic (seeded quadrotor fleet: random goals, perturbed hover starts)"
     if args.linesearch:
         workload += ", merit line search (alphas 0.1 0.3 0.7 1.0) after every QP solve"
-        data = "synthetic (seeded quadrotor fleet: random goals, perturbed hover starts)"
     iter_bytes = B * args.admm_iters * It  # algorithmic bytes of one iteration-kernel launch
     achieved = iter_bytes / iter_avg_s / 1e9
     qp_achieved = per_qp * B / solve_avg_s / 1e9
