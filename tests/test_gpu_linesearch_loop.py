@@ -103,3 +103,23 @@ def test_config4_device_loop_equals_masked(use_slack, stop, mode):
     _assert_same(dev, msk)
     if stop:
         assert len(set(dev.num_iter.tolist())) >= 2
+
+
+@pytest.mark.parametrize("mode", ["linesearch", "step"])
+def test_warm_started_device_loop_equals_masked(mode):
+    """A second solve from the first one's solution (its ADMM state carried):
+    the caller's state is read, not updated, by the device loop."""
+    prob = make_quadrotor_config(B=16, seed=6, dtype=torch.float64, device="cuda")
+    params = _params(4, 20, 0.0, linesearch=mode == "linesearch",
+                     criterion="step" if mode == "step" else "first_order")
+    first = TurboMPCSolver(prob, params).solve(TurboMPCSolver(prob, params).initial_guess())
+    keep = [t.clone() for t in first.admm_state]
+    out = []
+    for loop in ("device", "masked"):
+        solver = TurboMPCSolver(prob, params)
+        solver._sqp_loop = loop
+        out.append(solver.solve(first))
+    torch.cuda.synchronize()
+    _assert_same(*out)
+    for a, b in zip(first.admm_state, keep):
+        assert torch.equal(a, b)
