@@ -92,7 +92,8 @@ class QuadraticTrackingOCP:
         self.diag_cost = True  # D_t = diag(2 w): per-variable tracking weights (cost_blocks)
         self._static = None
         # values derived from the problem's tensors, built on first use (copies
-        # made by with_weights, with_params, to and tile start empty)
+        # made by with_weights, with_params, to and tile start empty); like the
+        # static QP blocks they assume the tensors are not changed in place
         self._memo: Dict[str, object] = {}
 
     def _memoized(self, key, make):
@@ -102,8 +103,9 @@ class QuadraticTrackingOCP:
         return v
 
     def _box_rows(self):
-        """(rows, lo, hi): the z coordinates with a finite bound (state rows,
-        then control rows) as an index tensor, and their bounds (m,)."""
+        """(rows, idx, lo, hi): the z coordinates with a finite bound (state
+        rows, then control rows) as a list and as an index tensor, and their
+        bounds (m,)."""
         def make():
             nx = self.num_state_variables
             rows = [i for i in range(nx) if bool(self.state_mask[i])] + \
