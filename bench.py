@@ -13,7 +13,10 @@ baseline (the oracle's restatement of the reference CPU path, compiled with
 -march=native on this host, on a bounded sample of the same workload, on all
 cores and on one).
 
-Secondary workloads (one line each; the default is the metric's config 3):
+The default run (config 3, no --batch/--sqp/--admm-iters/--linesearch) also
+reports configs 4, 5 and 2 (fp32 and fp64) under "secondary" (short runs:
+--secondary-steps timed steps and a --secondary-cpu-budget CPU sample each;
+--secondary 0 skips them).  Each can also run alone as the line's workload:
   --workload config4  obstacle avoidance, B=16384, 8 SQP x 30 ADMM, fp32
   --workload config5  spacecraft rendezvous, B=2048, fp64: 200 ADMM iterations
                       and the implicit-differentiation backward pass (gradients
@@ -39,6 +42,10 @@ ROOT = Path(__file__).resolve().parent
 sys.path.insert(0, str(ROOT))
 
 HBM_PEAK_GBS = 8000.0  # MI355X HBM3E
+# MI355X vector (VALU) FMA rate, fp64 and fp32 without packed math (the
+# library is built with packed-fp32 instructions disabled): 256 CUs x 4 SIMDs
+# x 16 lanes x 2 flop x 2.4 GHz
+VALU_PEAK_TFLOPS = 78.6
 
 
 def bytes_per_qp(T, n, nx, n0, m, K, w, m_g=0):
@@ -68,6 +75,14 @@ def bytes_pcg(T, n, nx, n0, m, K, pcg_iters, w, m_g=0):
     per_pcg = sp + 9 * T * n
     phase = K * It + pcg_iters * per_pcg
     return w * (F + phase), w * phase
+
+
+def flops_pcg_iteration(T, n):
+    """Algorithmic flops of one PCG iteration of one problem on the
+    block-tridiagonal Schur system (pcg_primal.py:70-175): the products with S
+    and with the block preconditioner Phiinv, (3T - 2) n x n blocks each at 2
+    flop per entry, two dot products and three vector updates of length T n."""
+    return 4 * (3 * T - 2) * n * n + 10 * T * n
 
 
 def sqp_params(n_sqp, admm_iters):
@@ -216,16 +231,24 @@ def _adjoint_qp_np(qp, st, nx):
 TRAFFIC_FILE = ROOT / "profiles" / "admm_stream_kernel_config3_pmc.txt"
 
 
-def measured_traffic():
+def measured_traffic(batch, admm_iters):
     """HBM bytes per launch of the iteration kernel from the committed
-    rocprofv3 --pmc summary (FETCH_SIZE + WRITE_SIZE, copy-calibrated), or None."""
+    rocprofv3 --pmc summary (FETCH_SIZE + WRITE_SIZE, copy-calibrated), when
+    the run has the shape that summary profiled (its `profiled_shape` line),
+    else None."""
+    traffic, shape = None, None
     try:
         for line in TRAFFIC_FILE.read_text().splitlines():
             if line.startswith("traffic_bytes_per_launch"):
-                return float(line.split("=")[1])
+                traffic = float(line.split("=")[1])
+            elif line.startswith("profiled_shape"):
+                f = line.split("=")[1].split()
+                shape = dict(zip(f[0::2], f[1::2]))
     except (OSError, ValueError, IndexError):
-        pass
-    return None
+        return None
+    if not shape or int(shape.get("batch", -1)) != batch or int(shape.get("admm_iters", -1)) != admm_iters:
+        return None
+    return traffic
 
 
 class SolveTimer:
@@ -353,7 +376,7 @@ def run_sqp_workload(args, dev):
                          "admm_iterations": args.admm_iters, "parallelism": "single GPU, batch-parallel",
                          "solution_finite": finite, "kernel_only_solves_per_s": B / (args.sqp * solve_avg_s)})
     line["roofline"] = roofline(
-        achieved, None if c4 else measured_traffic(),
+        achieved, None if c4 else measured_traffic(B, args.admm_iters),
         f"admm_stream_kernel (one launch = {args.admm_iters} ADMM iterations of the batch)", iter_bytes,
         iter_avg_s * 1e3,
         qp_solve={"kernels": "stage_pack + factor_row + admm_stream + stage_unpack", "algorithmic_bytes": per_qp * B,
@@ -468,6 +491,11 @@ def run_config2(args, dev):
     # whole solve's algorithmic bytes; the chunk kernels carry the iteration phase
     kernel_bytes = solve_bytes if one_launch else phase_bytes
     achieved = kernel_bytes / iter_avg_s / 1e9
+    # the one-launch kernels keep S, Phiinv and the PCG vectors on chip, so
+    # they are bound by instruction issue, not by HBM: their roofline is the
+    # algorithmic PCG flop rate against the VALU peak
+    pcg_flops = pcg_total * flops_pcg_iteration(T, n)
+    tflops = pcg_flops / iter_avg_s / 1e12
     finite = bool(torch.isfinite(st.x_blocks).all())
     line = base_line(f"MPC solves/sec at B={B}, config 2 PCG {args.dtype} (1 MI355X)", B * args.steps / elapsed,
                      args, elapsed, args.dtype,
@@ -487,9 +515,23 @@ def run_config2(args, dev):
         kname = f"admm_pcg_chunk_kernel (one launch = {K} ADMM iterations with their PCG solves)"
         kernels = "schur_build + admm_pcg_chunk"
     line["config"]["pcg_kernel"] = args.pcg_kernel
-    line["roofline"] = roofline(
-        achieved, None, kname, kernel_bytes, iter_avg_s * 1e3,
-        qp_solve={"kernels": kernels, "algorithmic_bytes": solve_bytes, "avg_ms": solve_avg_s * 1e3})
+    hbm = roofline(achieved, None, kname, kernel_bytes, iter_avg_s * 1e3,
+                   qp_solve={"kernels": kernels, "algorithmic_bytes": solve_bytes, "avg_ms": solve_avg_s * 1e3})
+    if one_launch:
+        line["roofline"] = {
+            "bound": "valu", "achieved": tflops, "peak": VALU_PEAK_TFLOPS, "unit": "TFLOP/s",
+            "frac": tflops / VALU_PEAK_TFLOPS, "traffic": None, "kernel": kname,
+            "algorithmic_flops_per_launch": pcg_flops, "avg_launch_ms": iter_avg_s * 1e3,
+            "flops_model": "per PCG iteration and problem 4 (3T-2) n^2 + 10 T n (S and Phiinv block products, "
+                           "2 dots, 3 updates) x the PCG iterations the launch ran",
+            "issue_counters": "VALU busy per SIMD 0.56, any instruction issuing 0.19 of wave cycles, 0.56 of wave "
+                              "cycles waiting (barriers): profiles/admm_pcg_dpp_kernel_config2.txt (fp32)",
+            "hbm_streaming_model": {"achieved": achieved, "frac": achieved / HBM_PEAK_GBS,
+                                    "note": "S and Phiinv are not streamed by this kernel; a fraction above 1 "
+                                            "is the on-chip reuse"},
+        }
+    else:
+        line["roofline"] = hbm
     return line
 
 
@@ -535,12 +577,19 @@ def main():
     ap.add_argument("--cpu-budget", type=float, default=15.0, help="seconds of CPU work for the baseline sample")
     ap.add_argument("--copy-calibration", type=int, default=0,
                     help="after timing, copy this many MiB device-to-device (counter calibration under rocprofv3)")
+    ap.add_argument("--secondary", type=int, default=1,
+                    help="with the default workload: also run configs 4, 5 and 2 (fp32, fp64) and report them "
+                         "under `secondary` (short runs, a few seconds of CPU baseline each)")
+    ap.add_argument("--secondary-steps", type=int, default=5)
+    ap.add_argument("--secondary-cpu-budget", type=float, default=3.0)
     args = ap.parse_args()
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
         print("bench.py: this build measures one GPU only (the batch of independent MPC problems would shard "
               "across GPUs with no communication in the forward solve); run with --gpus 1", file=sys.stderr)
         sys.exit(2)
+    default_run = args.workload == "config3" and not args.linesearch and args.batch is None and \
+        args.sqp is None and args.admm_iters is None
     B, n_sqp, K = DEFAULTS[args.workload]
     args.batch = args.batch or B
     args.sqp = args.sqp or n_sqp
@@ -550,6 +599,26 @@ def main():
 
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
+    line = run_workload(args, dev)
+    if default_run and args.secondary:
+        # the other configurations at their own sizes, one entry each (the
+        # metric above stays config 3's)
+        line["secondary"] = {}
+        for name, workload, dtype in (("config4", "config4", "f32"), ("config5", "config5", "f64"),
+                                      ("config2_f32", "config2", "f32"), ("config2_f64", "config2", "f64")):
+            b, s_, k = DEFAULTS[workload]
+            sub = argparse.Namespace(**{**vars(args), "workload": workload, "batch": b, "sqp": s_, "admm_iters": k,
+                                        "dtype": dtype, "steps": args.secondary_steps, "warmup": 2,
+                                        "cpu_budget": args.secondary_cpu_budget, "copy_calibration": 0})
+            print(f"bench.py: secondary {name} ({b} problems, {args.secondary_steps} steps)", file=sys.stderr,
+                  flush=True)
+            line["secondary"][name] = run_workload(sub, dev)
+    print(json.dumps(line), flush=True)
+
+
+def run_workload(args, dev):
+    """One bench line (with its CPU baseline) for args.workload."""
+    print(f"bench.py: {args.workload} ({args.batch} problems, {args.steps} steps)", file=sys.stderr, flush=True)
     if args.workload in ("config3", "config4"):
         line = run_sqp_workload(args, dev)
     elif args.workload == "config5":
@@ -558,7 +627,7 @@ def main():
         line = run_config2(args, dev)
     if args.cpu_baseline and not args.linesearch:  # the CPU port times the workload without the line search
         line["cpu_baseline"] = cpu_baseline(args.workload, args.batch, args)
-    print(json.dumps(line), flush=True)
+    return line
 
 
 if __name__ == "__main__":

@@ -175,12 +175,16 @@ int tmpc_admm_direct_noalloc(hipStream_t stream, int elem_bytes, const tmpc_dims
  * integrator path), the activity test, and the ADMM solve of the problems
  * that pass it.  A problem that fails it runs no iteration: `out` keeps `in`
  * and iters_out is 0, so the caller needs no masked commit.  The workspace is
- * the one of tmpc_admm_direct_*. */
+ * the one of tmpc_admm_direct_*.
+ * With conv NULL the activity is given: no check is evaluated (eq_err,
+ * ineq_err and g_out must be NULL too), active_out = active_in, and the
+ * problems with active_in = 0 run no iteration (for callers whose iterate is
+ * not the ADMM state's x, such as the merit line search's blend). */
 typedef struct {
   const uint8_t* active_in; /* (B,) 1 = still iterating, or NULL = all */
   uint8_t* active_out;      /* (B,) active_in && conv > tol (may alias active_in) */
   double tol;               /* tol_convergence */
-  void* conv;               /* (B,) first-order error of `in` */
+  void* conv;               /* (B,) first-order error of `in`, or NULL: activity given */
   void* eq_err;             /* (B,) equality violation, or NULL */
   void* ineq_err;           /* (B,) inequality violation, or NULL */
   void* g_out;              /* (B,T,m) G x (+ slack) of `in`, or NULL */

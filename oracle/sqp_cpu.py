@@ -160,10 +160,13 @@ def merit_linesearch(merit: Merit, states, controls, slacks, s_new, c_new, sl_ne
 
 
 def sqp_fixed(qp_at, x_guess, u_guess, *, n, m, n0, cfg: "ora.OracleCfg", rho0, n_sqp, dtype=np.float64,
-              nthreads=None, merit: "Merit | None" = None, linesearch=None):
+              nthreads=None, merit: "Merit | None" = None, linesearch=None, state0=None):
     """Fixed-count SQP: qp_at(states, controls) -> QP; the ADMM state (including
     rho and the slack) carries across iterations; x starts at 0
-    (turbompc_solver.py:1545-1551).  With `merit`, each QP solution is a step
+    (turbompc_solver.py:1545-1551), or the solve is warm-started from the
+    ADMM state `state0` (an OracleState, the admm_state of a previous solve,
+    turbompc_solver.py:1032-1037; then rho0 is not used, and the iterate's
+    slack starts at state0's).  With `merit`, each QP solution is a step
     direction scaled by merit_linesearch (options `linesearch`, defaults
     LINESEARCH_DEFAULTS) and the next linearization is at the blended iterate;
     the ADMM state is carried unblended (turbompc_solver.py:1591-1604).
@@ -172,10 +175,13 @@ def sqp_fixed(qp_at, x_guess, u_guess, *, n, m, n0, cfg: "ora.OracleCfg", rho0, 
     states, controls = x_guess.astype(np.float64), u_guess.astype(np.float64)
     B, T, nx = states.shape
     qp = qp_at(states, controls)
-    z0 = np.clip(np.zeros((B, T, m)), qp.ineq.l, qp.ineq.u)
-    st = ora.OracleState(np.zeros((B, T, n)), np.zeros((B, T, m)), np.zeros((B, n0)),
-                         np.zeros((B, T - 1, nx)), z0, np.zeros((B, T, m)), np.full((B,), float(rho0)))
-    slacks = np.zeros((B, T, m))
+    if state0 is None:
+        z0 = np.clip(np.zeros((B, T, m)), qp.ineq.l, qp.ineq.u)
+        st = ora.OracleState(np.zeros((B, T, n)), np.zeros((B, T, m)), np.zeros((B, n0)),
+                             np.zeros((B, T - 1, nx)), z0, np.zeros((B, T, m)), np.full((B,), float(rho0)))
+    else:
+        st = ora.OracleState(*[np.array(a, dtype=np.float64) for a in state0])
+    slacks = st.xi_g.copy()
     alphas = np.zeros((B, n_sqp))
     ls = dict(LINESEARCH_DEFAULTS, **(linesearch or {}))
     for it in range(n_sqp):
@@ -224,11 +230,12 @@ def _no_cross_terms(static):
 
 
 def obstacle_sqp(static, x_guess, u_guess, *, A_minus, c, centers, radii, dim, cfg: "ora.OracleCfg", rho0, n_sqp,
-                 slack_weight=0.0, use_slack=False, dtype=np.float64, nthreads=None, linesearch=None):
+                 slack_weight=0.0, use_slack=False, dtype=np.float64, nthreads=None, linesearch=None, state0=None):
     """static: numpy QP blocks that do not change (D, E, q, A0, c0, A_plus) and
     the box rows (G, l, u) (B,T,mb,n); the obstacle rows follow the box rows.
     linesearch: None, or a dict of line-search options (possibly empty) to run
-    the merit line search (then also returns slacks and alphas)."""
+    the merit line search (then also returns slacks and alphas).  state0: a
+    starting ADMM state (sqp_fixed)."""
     Gb, lb, ub = static["G"], static["l"], static["u"]
     B, T, mb, n = Gb.shape
     K = centers.shape[1]
@@ -259,7 +266,7 @@ def obstacle_sqp(static, x_guess, u_guess, *, A_minus, c, centers, radii, dim, c
         )
 
     return sqp_fixed(qp_at, x_guess, u_guess, n=n, m=mb + K, n0=static["A0"].shape[-2], cfg=cfg, rho0=rho0,
-                     n_sqp=n_sqp, dtype=dtype, nthreads=nthreads, merit=merit, linesearch=linesearch)
+                     n_sqp=n_sqp, dtype=dtype, nthreads=nthreads, merit=merit, linesearch=linesearch, state0=state0)
 
 
 def quadrotor_dynamics_residual(static, dt, params, nthreads=None):
@@ -275,11 +282,11 @@ def quadrotor_dynamics_residual(static, dt, params, nthreads=None):
 
 
 def quadrotor_sqp(static, x_guess, u_guess, *, dt, params, cfg: "ora.OracleCfg", rho0, n_sqp, dtype=np.float64,
-                  nthreads=None, linesearch=None):
+                  nthreads=None, linesearch=None, state0=None):
     """static: dict of numpy QP blocks that do not change (D, E, q, A0, c0, A_plus, G, l, u).
     Returns (states, controls, admm_state); with `linesearch` (a dict of
     options, possibly empty) runs the merit line search and also returns
-    slacks and alphas."""
+    slacks and alphas.  state0: a starting ADMM state (sqp_fixed)."""
     n = static["D"].shape[-1]
     m = static["G"].shape[-2]
     merit = None
@@ -298,4 +305,4 @@ def quadrotor_sqp(static, x_guess, u_guess, *, dt, params, cfg: "ora.OracleCfg",
         )
 
     return sqp_fixed(qp_at, x_guess, u_guess, n=n, m=m, n0=static["A0"].shape[-2], cfg=cfg, rho0=rho0,
-                     n_sqp=n_sqp, dtype=dtype, nthreads=nthreads, merit=merit, linesearch=linesearch)
+                     n_sqp=n_sqp, dtype=dtype, nthreads=nthreads, merit=merit, linesearch=linesearch, state0=state0)

@@ -31,3 +31,17 @@ def test_multi_gpu_request_exits_with_message():
                        timeout=120)
     assert r.returncode == 2
     assert "one GPU" in r.stderr
+
+
+def test_traffic_is_reported_only_for_the_profiled_shape():
+    # the committed --pmc summary profiled B = 4096, 20 ADMM iterations
+    assert bench.measured_traffic(4096, 20) == pytest.approx(13.687e9)
+    assert bench.measured_traffic(2048, 20) is None
+    assert bench.measured_traffic(4096, 10) is None
+
+
+def test_pcg_flop_model():
+    # one block row of S (or Phiinv) has 3 n x n blocks, the end rows 2:
+    # (3T - 2) n^2 entries, 2 flop each, for both products; 2 dots + 3 updates
+    T, n = 51, 16
+    assert bench.flops_pcg_iteration(T, n) == 2 * 2 * (3 * T - 2) * n * n + (2 * 2 + 3 * 2) * T * n

@@ -1,0 +1,204 @@
+"""Initial-control rows (constrain_initial_control: A0 = [I 0; 0 I], c0 =
+[x0; u0], n0 = n) on every GPU path against the oracle: the streaming ADMM
+kernels (one to three problems per wavefront, padded record widths), the
+generic kernel, the three PCG kernels, the adjoint KKT (rows-in-lanes and
+generic kernels), and the solver: the forward solve, dL/du0 from the u_0
+rows' multipliers (turbompc/solvers/turbompc_solver.py:692-705, :765-770)
+and the device SQP loop.
+
+Reference: optimal_control_problem.py:958-978 (the rows), :897-910 (the
+equality residual); the oracle is pinned for n0 = n by its dense ADMM and
+adjoint tests (test_oracle_admm, test_oracle_adjoint_quadrotor).  With A0
+fixing all of z_0, active inequality rows at t = 0 would be linearly
+dependent on it, so the adjoint cases keep them inactive.
+"""
+import copy
+
+import numpy as np
+import pytest
+import torch
+
+import oracle
+from helpers import TOL, rel_err, random_qp, zero_state
+from oracle.sqp_cpu import quadrotor_sqp
+from test_gpu_admm import PCG_KERNELS, _assert_state_close, _run_pair
+from turbompc_amd import _lib
+from turbompc_amd.problems import configs
+from turbompc_amd.problems.quadrotor import hover_thrust, make_quadrotor_config
+from turbompc_amd.solvers.backward.backward_kkt_hip import solve_backward_kkt_hip
+from turbompc_amd.solvers.linear_systems_solvers.backends import AdmmBackend
+from turbompc_amd.solvers.turbompc_solver import DEFAULT_SOLVER_PARAMS, TurboMPCSolver
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda"
+
+KERNELS = {"stream-1": _lib.flag_stream_p(1), "stream-2": _lib.flag_stream_p(2), "stream-3": _lib.flag_stream_p(3),
+           "generic": _lib.FLAG_GENERIC_KERNEL}
+
+
+# (B, T, n, nx, m): n = 7 and 12 run on padded records (widths 9 and 16)
+@pytest.mark.parametrize("shape", [(13, 21, 6, 4, 2), (8, 11, 17, 13, 4), (7, 13, 9, 6, 5), (6, 9, 7, 4, 3),
+                                   (5, 9, 12, 8, 4)])
+@pytest.mark.parametrize("kernel", list(KERNELS))
+def test_admm_direct_with_initial_control_rows_fp64(kernel, shape):
+    B, T, n, nx, m = shape
+    qp = random_qp(B, T, n, nx, m, seed=61, std=True, n0=n)
+    cfg = oracle.OracleCfg(max_iter=20, check_every=3, adapt_rho_every=0, sigma=1e-6, eps_abs=1e-12,
+                           eps_rel=1e-12, rho_f_factor=1000.0, alpha=1.6)
+    print(f"n0 = n = {n}: ADMM direct ({kernel}), shape {shape}", flush=True)
+    ref, it_ref, _, out, stats = _run_pair(qp, cfg, torch.float64, kernel_flags=KERNELS[kernel])
+    np.testing.assert_array_equal(stats.num_iter.cpu().numpy(), it_ref)
+    _assert_state_close(out, ref, 1e-9)
+
+
+def test_admm_direct_with_initial_control_rows_adaptive_rho_and_termination():
+    qp = random_qp(11, 9, 6, 4, 3, seed=62, std=True, n0=6)
+    cfg = oracle.OracleCfg(max_iter=200, check_every=2, adapt_rho_every=4, sigma=1e-6, eps_abs=1e-6, eps_rel=1e-6,
+                           rho_f_factor=50.0, alpha=1.6, adaptive_rho_tolerance=1.5)
+    ref, it_ref, _, out, stats = _run_pair(qp, cfg, torch.float64, kernel_flags=_lib.flag_stream_p(2))
+    np.testing.assert_array_equal(stats.num_iter.cpu().numpy(), it_ref)
+    assert len(set(it_ref.tolist())) > 1 and np.any(ref.rho_bar != 0.1)
+    assert rel_err(out.rho_bar, ref.rho_bar) < 1e-7
+    _assert_state_close(out, ref, 1e-5)
+
+
+def test_admm_direct_with_initial_control_rows_quadrotor_fp32():
+    hov = hover_thrust()
+    u0 = torch.full((64, 4), hov) + 0.1 * torch.randn((64, 4), generator=torch.Generator().manual_seed(1),
+                                                      dtype=torch.float64)
+    prob = make_quadrotor_config(B=64, seed=3, dtype=torch.float64, device=DEV, constrain_initial_control=True,
+                                 initial_control=u0)
+    qp = prob.build_qp(*prob.initial_guess()).to("cpu", torch.float64)  # the RK4 linearization runs on the device
+    assert qp.dims[4] == 17
+    cfg = oracle.OracleCfg(max_iter=20, check_every=25, adapt_rho_every=0, sigma=1e-6, eps_abs=1e-9, eps_rel=1e-9,
+                           rho_f_factor=1000.0, alpha=1.0)
+    ref, it_ref, _, out, stats = _run_pair(qp, cfg, torch.float32)
+    np.testing.assert_array_equal(stats.num_iter.cpu().numpy(), it_ref)
+    for k in ("x_blocks", "y_f_0", "y_f_dyn", "y_g", "z_g"):
+        e = rel_err(getattr(out, k), getattr(ref, k))
+        print(f"quadrotor n0 = 17 fp32 {k}: rel err vs fp64 oracle {e:.2e}")
+        assert e < TOL[torch.float32], (k, e)
+
+
+@pytest.mark.parametrize("dtype", [torch.float64, torch.float32])
+@pytest.mark.parametrize("shape", [(5, 21, 6, 4, 2), (4, 13, 9, 6, 11), (3, 9, 16, 12, 16)])
+@pytest.mark.parametrize("kernel", list(PCG_KERNELS))
+def test_admm_pcg_with_initial_control_rows(kernel, shape, dtype):
+    B, T, n, nx, m = shape
+    qp = random_qp(B, T, n, nx, m, seed=63, std=True, n0=n)
+    cfg = oracle.OracleCfg(max_iter=9, check_every=4, adapt_rho_every=0, sigma=1e-6, eps_abs=1e-12, eps_rel=1e-12,
+                           rho_f_factor=100.0, alpha=1.6, pcg_eps=0.0, pcg_max_iter=5)
+    print(f"n0 = n = {n}: ADMM PCG ({kernel}, {dtype}), shape {shape}", flush=True)
+    ref, it_ref, pcg_ref, out, stats = _run_pair(qp, cfg, dtype, backend=AdmmBackend.HIP_PCG, schur="pcg",
+                                                 kernel_flags=PCG_KERNELS[kernel])
+    np.testing.assert_array_equal(stats.num_iter.cpu().numpy(), it_ref)
+    np.testing.assert_array_equal(stats.num_pcg_iters.sum(1).cpu().numpy(), pcg_ref)
+    _assert_state_close(out, ref, 1e-9 if dtype == torch.float64 else TOL[torch.float32])
+
+
+def _config5_u0(B, seed):
+    rng = np.random.default_rng(seed + 100)
+    return torch.tensor(rng.uniform(-0.005, 0.005, size=(B, 3)))  # inside |u| <= 0.01
+
+
+@pytest.mark.parametrize("kernel", ["rows", "generic"])
+def test_adjoint_kkt_with_initial_control_rows(kernel):
+    B = 5
+    prob = configs.config5(B=B, seed=1, constrain_initial_control=True, initial_control=_config5_u0(B, 1))
+    qp = prob.build_qp(*prob.initial_guess())
+    assert qp.dims[4] == 9
+    rng = np.random.default_rng(8)
+    sign = rng.choice([-1.0, 0.0, 1.0], size=tuple(qp.ineq.l.shape), p=[0.3, 0.4, 0.3])
+    sign[:, 0] = 0.0  # z_0 is fixed by A0
+    G = qp.ineq.G * torch.tensor(sign).unsqueeze(-1)
+    qb = qp.replace_ineq(G=G).replace_cost(q=torch.tensor(rng.standard_normal(tuple(qp.cost.q.shape))))
+    dz_ref, mult_ref = oracle.adjoint_kkt(qb)
+    flags = _lib.FLAG_GENERIC_KERNEL if kernel == "generic" else 0
+    dz, mult = solve_backward_kkt_hip(qb.to(DEV, torch.float64), refine_steps=4, kernel_flags=flags)
+    e_dz, e_mult = rel_err(dz, dz_ref), rel_err(mult, mult_ref)
+    print(f"adjoint n0 = 9 ({kernel}): dz {e_dz:.2e}, multipliers {e_mult:.2e}")
+    assert e_dz < 1e-10 and e_mult < 1e-10
+
+
+def _params(K, n_sqp=1):
+    p = copy.deepcopy(DEFAULT_SOLVER_PARAMS)
+    p["num_sqp_iteration_max"] = n_sqp
+    p["tol_convergence"] = 0.0
+    p["admm"]["max_iter"] = K
+    p["admm"]["adapt_rho_every"] = 0
+    p["admm"]["relaxation_parameter"] = 1.0
+    return p
+
+
+def test_solver_with_initial_control_forward_and_gradient():
+    """Config 1 with the initial control constrained (u0 inside the bounds):
+    the forward solve against the oracle (per-problem termination), the
+    cotangent of initial_control (the u_0 rows' multipliers of the adjoint
+    KKT) against the dense oracle's, and the autograd path returns it.  The
+    ADMM iterate must be near the QP's solution here: where it is not (config
+    5 after 200 iterations still has u_0 far from u0 and the t = 0 bound rows
+    marked active by their duals), those rows are linearly dependent on the
+    u_0 rows and the adjoint KKT is singular -- in the reference too."""
+    B, K = 8, 200
+    rng = np.random.default_rng(100)
+    u0 = torch.tensor(rng.uniform(-0.5, 0.5, size=(B, 2)))  # |u| <= 1
+    prob = configs.config1(B=B, seed=0, constrain_initial_control=True, initial_control=u0)
+    qp = prob.build_qp(*prob.initial_guess())
+    cfg = oracle.OracleCfg(max_iter=K, check_every=25, adapt_rho_every=0, sigma=1e-6, eps_abs=1e-4, eps_rel=1e-3,
+                           rho_f_factor=1000.0, alpha=1.0)
+    ref, it_ref, _ = oracle.admm_solve(qp, zero_state(qp, 0.1), cfg)
+    params = _params(K)
+    params["admm"].update(eps_abs=1e-4, eps_rel=1e-3, check_termination_every=25)
+    solver = TurboMPCSolver(prob.to(DEV), params)
+    x0 = solver.program.x0.clone().requires_grad_(True)
+    u0d = solver.program.u0.clone().requires_grad_(True)
+    sol = solver.get_differentiable_solve_function()(solver.initial_guess(),
+                                                     {"initial_state": x0, "initial_control": u0d}, None)
+    torch.cuda.synchronize()
+    assert torch.equal(sol.admm_iters[:, 0].cpu(), torch.as_tensor(it_ref, dtype=torch.int32))
+    assert rel_err(sol.admm_state.x_blocks, ref.x_blocks) < 1e-9
+    assert rel_err(sol.admm_state.y_f_0, ref.y_f_0) < 1e-9
+    # backward: L = sum ||x_N||^2 + a random functional of the controls
+    gu = torch.randn(sol.controls.shape, generator=torch.Generator().manual_seed(2), dtype=torch.float64).to(DEV)
+    L = (sol.states[:, -1] ** 2).sum() + (gu * sol.controls).sum()
+    L.backward()
+    kkt = sol.kkt_state
+    dl_s = torch.zeros_like(sol.states)
+    dl_s[:, -1] = 2 * sol.states[:, -1].detach()
+    ctx = solver._build_backward_qp(solver.program, sol, dl_s, gu, torch.zeros_like(kkt.slack))
+    _, mult_ref = oracle.adjoint_kkt(ctx.solve_qp.to("cpu"))
+    nx = prob.num_state_variables
+    assert not bool((kkt.ineq_active_lower_idx | kkt.ineq_active_upper_idx)[:, 0].any())
+    e_u0 = rel_err(u0d.grad, mult_ref[:, nx:nx + 2])
+    e_x0 = rel_err(x0.grad, mult_ref[:, :nx])
+    print(f"dL/du0 rel err vs the dense adjoint {e_u0:.2e}, dL/dx0 {e_x0:.2e}")
+    assert e_u0 < 1e-9 and e_x0 < 1e-9
+    cot, _ = solver.solve_vjp(sol, dl_s, gu)
+    assert torch.equal(cot["initial_control"], u0d.grad) and set(cot) == {"initial_state", "initial_control"}
+
+
+@pytest.mark.parametrize("loop", ["device", "masked"])
+def test_quadrotor_sqp_with_initial_control_matches_cpu(loop):
+    B, n_sqp, K = 6, 3, 10
+    hov = hover_thrust()
+    u0 = torch.full((B, 4), hov) + 0.1 * torch.randn((B, 4), generator=torch.Generator().manual_seed(4),
+                                                     dtype=torch.float64)
+    cpu = make_quadrotor_config(B=B, seed=2, dtype=torch.float64, device="cpu", constrain_initial_control=True,
+                                initial_control=u0)
+    D, E, q = (t.numpy() for t in cpu.cost_blocks())
+    A0, c0 = (t.numpy() for t in cpu.initial_equality())
+    assert A0.shape[1] == 17
+    G, l, u = (t.numpy() for t in cpu.inequality_blocks())
+    static = dict(D=D, E=E, q=q, A0=A0, c0=c0, A_plus=cpu.a_plus().numpy(), G=G, l=l, u=u)
+    xg, ug = (t.numpy() for t in cpu.initial_guess())
+    cfg = oracle.OracleCfg(max_iter=K, check_every=25, adapt_rho_every=0, sigma=1e-6, eps_abs=1e-9, eps_rel=1e-9,
+                           rho_f_factor=1000.0, alpha=1.0)
+    xs, us, st = quadrotor_sqp(static, xg, ug, dt=cpu.dt, params=cpu.params, cfg=cfg, rho0=0.1, n_sqp=n_sqp)
+    solver = TurboMPCSolver(cpu.to(DEV), _params(K, n_sqp))
+    solver._sqp_loop = loop
+    sol = solver.solve(solver.initial_guess())
+    torch.cuda.synchronize()
+    print(f"quadrotor SQP n0 = 17 ({loop}): states {rel_err(sol.states, xs):.2e}, y_f0 "
+          f"{rel_err(sol.admm_state.y_f_0, st.y_f_0):.2e}")
+    assert rel_err(sol.states, xs) < 1e-9 and rel_err(sol.controls, us) < 1e-9
+    assert rel_err(sol.admm_state.y_f_0, st.y_f_0) < 1e-8

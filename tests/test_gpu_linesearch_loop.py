@@ -59,18 +59,26 @@ def _both(prob, params):
     return out
 
 
+def _equal(x, y):
+    """Bitwise equality, NaN where the other has NaN counting as equal."""
+    if x is None or y is None:
+        return x is None and y is None
+    if not x.is_floating_point():
+        return torch.equal(x, y)
+    nx, ny = torch.isnan(x), torch.isnan(y)
+    return torch.equal(nx, ny) and torch.equal(x[~nx], y[~ny])
+
+
 def _assert_same(a, b):
     for k in ("states", "controls", "slack", "num_iter", "convergence_error", "admm_iters", "linesearch_alphas",
               "nonfinite"):
-        x, y = getattr(a, k), getattr(b, k)
-        assert (x is None and y is None) or torch.equal(x, y), k
+        assert _equal(getattr(a, k), getattr(b, k)), k
     for k in a.admm_state._fields:
-        assert torch.equal(getattr(a.admm_state, k), getattr(b.admm_state, k)), k
+        assert _equal(getattr(a.admm_state, k), getattr(b.admm_state, k)), k
     for k in a.solver_stats._fields:
-        assert torch.equal(getattr(a.solver_stats, k), getattr(b.solver_stats, k)), k
+        assert _equal(getattr(a.solver_stats, k), getattr(b.solver_stats, k)), k
     for k in a.kkt_state._fields:
-        x, y = getattr(a.kkt_state, k), getattr(b.kkt_state, k)
-        assert (x is None and y is None) or torch.equal(x, y), k
+        assert _equal(getattr(a.kkt_state, k), getattr(b.kkt_state, k)), k
 
 
 @pytest.mark.parametrize("dtype", [torch.float64, torch.float32])
@@ -123,3 +131,21 @@ def test_warm_started_device_loop_equals_masked(mode):
     _assert_same(*out)
     for a, b in zip(first.admm_state, keep):
         assert torch.equal(a, b)
+
+
+@pytest.mark.parametrize("mode", ["linesearch", "step"])
+def test_device_loop_equals_masked_with_a_nonfinite_problem(mode):
+    """One problem's control weight is infinite, so its QP solution (and its
+    ADMM state) is non-finite: the device loop takes the activity as given
+    (no fused check decides it), so it runs that problem exactly when the
+    masked loop does, and every other problem is untouched."""
+    prob = configs.config4(B=8, seed=2).to("cuda")
+    wu = prob.wu.clone()
+    wu[3, 1] = float("inf")
+    prob = prob.with_weights({"weights_penalization_control_squared": wu})
+    params = _params(5, 30, 0.0, linesearch=mode == "linesearch",
+                     criterion="step" if mode == "step" else "first_order")
+    dev, msk = _both(prob, params)
+    print(f"  SQP iterations per problem {dev.num_iter.tolist()}, non-finite {dev.nonfinite.tolist()}", flush=True)
+    assert dev.nonfinite.tolist() == [b == 3 for b in range(8)]
+    _assert_same(dev, msk)

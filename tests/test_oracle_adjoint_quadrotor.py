@@ -18,16 +18,21 @@ from helpers import dense_C, dense_G, dense_P, np_qp, random_qp
 from turbompc_amd.problems.quadrotor import QUAD_PARAMS, hover_thrust
 
 
-def _adjoint_qp(seed, active_frac=0.5):
-    qp = random_qp(2, 5, 4, 2, 3, seed=seed, std=False)
+def _adjoint_qp(seed, active_frac=0.5, n0=None):
+    qp = random_qp(2, 5, 4, 2, 3, seed=seed, std=False, n0=n0)
     rng = np.random.default_rng(seed)
     sign = rng.choice([-1.0, 0.0, 1.0], size=(2, 5, 3), p=[active_frac / 2, 1 - active_frac, active_frac / 2])
+    if n0 == 4:
+        # A0 fixes all of z_0: active rows at t = 0 would be linearly dependent
+        # on it (no unique multipliers), so they are left inactive
+        sign[:, 0] = 0.0
     G = qp.ineq.G * torch.tensor(sign).unsqueeze(-1)
     return qp.replace_ineq(G=G), sign
 
 
-def test_adjoint_matches_dense_kkt():
-    qp, sign = _adjoint_qp(21)
+@pytest.mark.parametrize("n0", [2, 4])  # 4 = n: initial-control rows too
+def test_adjoint_matches_dense_kkt(n0):
+    qp, sign = _adjoint_qp(21, n0=n0)
     dz, mult = oracle.adjoint_kkt(qp)
     a = np_qp(qp)
     for b in range(2):
@@ -46,8 +51,9 @@ def test_adjoint_matches_dense_kkt():
         assert np.all(yi[~act] == 0.0)
 
 
-def test_adjoint_initial_state_multiplier_is_gradient():
-    qp, _ = _adjoint_qp(22)
+@pytest.mark.parametrize("n0", [2, 4])  # 4 = n: the u_0 rows' multipliers are dL/du0
+def test_adjoint_initial_state_multiplier_is_gradient(n0):
+    qp, _ = _adjoint_qp(22, n0=n0)
     a = np_qp(qp)
     b = 0
     P = dense_P(a["D"][b], a["E"][b])

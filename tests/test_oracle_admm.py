@@ -73,9 +73,10 @@ def dense_admm(a, b, x, z, yg, y0, yf, xi, rho, cfg, iters):
 
 
 @pytest.mark.parametrize("alpha", [1.0, 1.6])
-@pytest.mark.parametrize("std", [True, False])
-def test_oracle_admm_matches_dense_restatement(alpha, std):
-    qp = random_qp(3, 5, 4, 2, 3, seed=11, std=std)
+@pytest.mark.parametrize("std,n0", [(True, 2), (False, 2), (True, 4)])
+def test_oracle_admm_matches_dense_restatement(alpha, std, n0):
+    # n0 = n: initial-state and initial-control rows (constrain_initial_control)
+    qp = random_qp(3, 5, 4, 2, 3, seed=11, std=std, n0=n0)
     cfg = oracle.OracleCfg(max_iter=40, check_every=2, adapt_rho_every=4, sigma=1e-6, eps_abs=1e-7, eps_rel=1e-7,
                            rho_f_factor=50.0, alpha=alpha, adaptive_rho_tolerance=1.5)
     st0 = zero_state(qp, 0.1)

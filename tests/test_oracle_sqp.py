@@ -96,6 +96,36 @@ def test_linear_sqp_carries_adaptive_rho():
     assert not np.array_equal(chain.x_blocks, fresh_rho.x_blocks)  # and it matters
 
 
+@pytest.mark.parametrize("adapt", [0, 10])
+def test_warm_started_sqp_continues_the_chain(adapt):
+    """sqp_fixed from a starting ADMM state (a warm-started MPC solve,
+    turbompc_solver.py:1032-1037): on a linear problem, n1 iterations from
+    zero followed by n2 iterations started from the first run's state equal
+    n1 + n2 iterations from zero, bit for bit; starting the second run from
+    the zero state, or with its initial rho, does not."""
+    B, K, n1, n2 = 5, 24, 2, 3
+    qp = _config1_static(B, seed=4)
+    _, T, n, _ = qp.cost.D.shape
+    nx, m, n0 = qp.eq.A_minus.shape[-2], qp.ineq.G.shape[-2], qp.eq.A0.shape[-2]
+    cfg = oracle.OracleCfg(max_iter=K, check_every=5, adapt_rho_every=adapt, sigma=1e-6, eps_abs=1e-30,
+                           eps_rel=1e-30, rho_f_factor=1000.0, alpha=1.6, adaptive_rho_tolerance=1.1)
+    guess = (np.zeros((B, T, nx)), np.zeros((B, T, n - nx)))
+    run = lambda k, st0=None: sqp_fixed(lambda s, u: qp, *guess, n=n, m=m, n0=n0, cfg=cfg, rho0=0.1,  # noqa: E731
+                                        n_sqp=k, state0=st0)
+    _, _, first = run(n1)
+    xs, us, st = run(n2, first)
+    xs_all, us_all, st_all = run(n1 + n2)
+    for k in oracle.OracleState._fields:
+        assert np.array_equal(np.asarray(getattr(st, k)), np.asarray(getattr(st_all, k))), k
+    assert np.array_equal(xs, xs_all) and np.array_equal(us, us_all)
+    _, _, cold = run(n2)
+    assert not np.array_equal(cold.x_blocks, st.x_blocks)
+    if adapt:
+        assert np.any(first.rho_bar != 0.1)
+        _, _, reset = run(n2, first._replace(rho_bar=np.full((B,), 0.1)))
+        assert not np.array_equal(reset.x_blocks, st.x_blocks)
+
+
 # ---- quadrotor model in numpy (independent of liboracle's C++ RK4) ---------
 def _quat_rot(q):
     """Rotation matrix of a unit quaternion (w, x, y, z), (..., 3, 3)."""

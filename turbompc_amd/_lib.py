@@ -52,6 +52,7 @@ _STATUS = {
     3: "workspace too small",
     4: "HIP launch failed",
     5: "problem needs more than the allocation-free scratch",
+    6: "non-finite values in the solution",
 }
 
 

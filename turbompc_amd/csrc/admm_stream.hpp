@@ -181,7 +181,9 @@ struct StreamArgs {
   int it_lo, it_hi, first_chunk;
   // SQP step (optional, first chunk): first-order check of the input iterate
   // and the activity test act_out = act_in && conv > chk_tol; a problem that
-  // fails it runs no iteration
+  // fails it runs no iteration.  With chk_conv NULL and act_in set, the
+  // activity is given: no check, the problems with act_in = 0 run no
+  // iteration.
   R *chk_conv, *chk_eq, *chk_iq, *chk_g;
   const uint8_t* act_in;
   uint8_t* act_out;
@@ -715,7 +717,7 @@ __global__ __launch_bounds__(kWave, StreamOcc<R>::waves) void admm_stream_kernel
   R res[6];
   if (a.first_chunk) {
     it = 0;
-    done = false;
+    done = (a.chk_conv == nullptr && a.act_in) ? a.act_in[b] == 0 : false;
     res[0] = res[1] = res[4] = res[5] = rinf<R>();
     res[2] = res[3] = R(1);
     if (G.live && i == 0) a.ctl[b * 4 + 2] = 0;

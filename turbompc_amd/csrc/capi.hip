@@ -461,7 +461,9 @@ int admm_direct_impl(hipStream_t s, const tmpc_dims* dims, const tmpc_qp* qp,
   if (!dims_ok(dims)) return TMPC_EBADSHAPE;
   if (!cfg || !iters || !qp_ok(qp, dims->m) || !state_ok(in, dims->m) || !state_ok(out, dims->m))
     return TMPC_EBADARG;
-  if (sq && (!sq->conv || !sq->active_out)) return TMPC_EBADARG;
+  // conv NULL: the activity is given (active_in), no check is evaluated
+  if (sq && (!sq->active_out || (!sq->conv && (sq->eq_err || sq->ineq_err || sq->g_out)))) return TMPC_EBADARG;
+  const bool given = sq && !sq->conv;
   if (cfg->use_slack && dims->m > 0 && !qp->slack_weight) return TMPC_EBADARG;
   const Dims d = to_dims(dims);
   if (!ws || wsb < direct_ws_bytes<R>(d)) return TMPC_EWORKSPACE;
@@ -506,7 +508,15 @@ int admm_direct_impl(hipStream_t s, const tmpc_dims* dims, const tmpc_qp* qp,
   const bool pad = dr.n != d.n;
   QPDev<R> qr = a.qp;  // the QP as the record kernels read it
   if (pad) qr.A0 = w.a0p;
-  if (sq && !stream) {
+  if (given) {
+    // the activity as given: act_out = act_in, which the kernels read as the
+    // per-problem start state (the streaming kernel reads act_in itself)
+    hipLaunchKernelGGL((sqp_activity_kernel<R>), dim3((d.B + 255) / 256), dim3(256), 0, s, d.B, (const R*)nullptr,
+                       R(0), sq->active_in, sq->active_out);
+    st = launch_status();
+    if (st) return st;
+    if (!stream) a.act = sq->active_out;
+  } else if (sq && !stream) {
     // generic path: the check kernel on the input iterate, then the activity
     // test, which the ADMM kernel reads as its per-problem start state
     const bool slack = cfg->use_slack && d.m > 0;

@@ -244,13 +244,14 @@ __global__ __launch_bounds__(kWave) void sqp_check_stage_kernel(Dims d, QPDev<R>
 }
 
 // The SQP activity test of one step: act_out = act_in && conv > tol (a NaN
-// error stops the problem, as the reference's `conv > tol` does).
+// error stops the problem, as the reference's `conv > tol` does); with conv
+// NULL the activity is given: act_out = act_in.
 template <typename R>
 __global__ void sqp_activity_kernel(int B, const R* __restrict__ conv, R tol, const uint8_t* __restrict__ act_in,
                                     uint8_t* __restrict__ act_out) {
   const int b = blockIdx.x * blockDim.x + threadIdx.x;
   if (b >= B) return;
-  act_out[b] = ((act_in ? act_in[b] != 0 : true) && conv[b] > tol) ? 1 : 0;
+  act_out[b] = ((act_in ? act_in[b] != 0 : true) && (conv == nullptr || conv[b] > tol)) ? 1 : 0;
 }
 
 template <typename R>

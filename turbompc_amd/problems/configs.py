@@ -8,6 +8,8 @@ config4  3D double integrator among 8 spherical obstacles, nx=6, nu=3, N=60,
 config5  Clohessy-Wiltshire rendezvous, nx=6, nu=3, N=100, dt=10 s (exact
          zero-order-hold discretization), |u|<=0.01
 Each returns a LinearOCP with float64 tensors on the CPU; move it with .to().
+Keyword arguments of config1/2/5 go to the problem (for example
+constrain_initial_control=True, initial_control=u0).
 """
 from __future__ import annotations
 
@@ -19,7 +21,7 @@ from .obstacle import ObstacleOCP
 from .ocp import LinearOCP
 
 
-def config1(B: int = 64, seed: int = 0) -> LinearOCP:
+def config1(B: int = 64, seed: int = 0, **kw) -> LinearOCP:
     rng = np.random.default_rng(seed)
     dt, N, nx, nu = 0.1, 20, 4, 2
     I2 = np.eye(2)
@@ -35,10 +37,11 @@ def config1(B: int = 64, seed: int = 0) -> LinearOCP:
         weights_control=torch.full((B, nu), 0.1, dtype=torch.float64),
         weights_final=torch.full((B, nx), 9.0, dtype=torch.float64),  # Qf = 10 I = Q + 9 I
         control_bounds=(torch.full((nu,), -1.0, dtype=torch.float64), torch.full((nu,), 1.0, dtype=torch.float64)),
+        **kw,
     )
 
 
-def config2(B: int = 1024, seed: int = 0) -> LinearOCP:
+def config2(B: int = 1024, seed: int = 0, **kw) -> LinearOCP:
     rng = np.random.default_rng(seed)
     N, nx, nu = 50, 12, 4
     A = np.empty((B, nx, nx))
@@ -59,6 +62,7 @@ def config2(B: int = 1024, seed: int = 0) -> LinearOCP:
         weights_final=torch.zeros((B, nx), dtype=torch.float64),
         state_bounds=(torch.full((nx,), -5.0, dtype=torch.float64), torch.full((nx,), 5.0, dtype=torch.float64)),
         control_bounds=(torch.full((nu,), -1.0, dtype=torch.float64), torch.full((nu,), 1.0, dtype=torch.float64)),
+        **kw,
     )
 
 
@@ -121,7 +125,7 @@ def cw_discrete(mean_motion: float = 0.0011, dt: float = 10.0):
     return E[:6, :6], E[:6, 6:]
 
 
-def config5(B: int = 2048, seed: int = 0) -> LinearOCP:
+def config5(B: int = 2048, seed: int = 0, **kw) -> LinearOCP:
     rng = np.random.default_rng(seed)
     N, nx, nu = 100, 6, 3
     Ad, Bd = cw_discrete()
@@ -135,4 +139,5 @@ def config5(B: int = 2048, seed: int = 0) -> LinearOCP:
         initial_state=torch.tensor(x0), weights_state=torch.tensor(wq), weights_control=torch.tensor(wr),
         weights_final=torch.zeros((B, nx), dtype=torch.float64),
         control_bounds=(torch.full((nu,), -0.01, dtype=torch.float64), torch.full((nu,), 0.01, dtype=torch.float64)),
+        **kw,
     )

@@ -7,7 +7,8 @@ have closed forms:
     cost :1011-1032):  D_t = 2 diag(w_x, w_u) for t < N, D_N = 2 diag(w_x + w_f, w_u),
     E = 0, q_t = -2 diag(w) z_ref_t (control reference only when
     penalize_control_reference, else 0);
-  * initial condition (:914-980): A0 = [I 0], c0 = x0;
+  * initial condition (:914-980): A0 = [I 0], c0 = x0; with
+    constrain_initial_control also the control rows [0 I], u0 (n0 = nx + nu);
   * dynamics (explicit branch, :1217-1272): A_minus_t = [df/dx, df/du],
     A_plus_t = [-I 0], c_t = -f(xbar, ubar) + A xbar + B ubar;
   * box bounds (:413-471): one G row per state/control coordinate with a finite
@@ -57,6 +58,8 @@ class QuadraticTrackingOCP:
         initial_guess_final_state: Optional[torch.Tensor] = None,  # (B, nx)
         use_slack_variables: bool = False,
         slack_penalization_weight: float = 0.0,
+        constrain_initial_control: bool = False,
+        initial_control: Optional[torch.Tensor] = None,  # (B, nu), with constrain_initial_control
         dtype: torch.dtype = torch.float64,
         device="cpu",
     ):
@@ -86,6 +89,12 @@ class QuadraticTrackingOCP:
         self.x_final_guess = cv(initial_guess_final_state) if initial_guess_final_state is not None else self.x0
         self.use_slack_variables = bool(use_slack_variables)
         self.slack_penalization_weight = float(slack_penalization_weight)
+        # u_0 = initial_control as equality rows of A0 (optimal_control_problem.py:958-978)
+        self.constrain_initial_control = bool(constrain_initial_control)
+        if self.constrain_initial_control and initial_control is None:
+            raise ValueError("initial_control must be provided when constrain_initial_control is True.")
+        self.u0 = (self._per_problem_vector("initial_control", initial_control, nu) if initial_control is not None
+                   else torch.zeros((self.B, nu), dtype=dtype, device=self.device))
         if self.use_slack_variables and not self.slack_penalization_weight > 0.0:
             raise ValueError("use_slack_variables needs a positive slack_penalization_weight")
         self.std_dynamics = True  # explicit integrators: A_plus = [-I 0], E = 0
@@ -95,6 +104,13 @@ class QuadraticTrackingOCP:
         # made by with_weights, with_params, to and tile start empty); like the
         # static QP blocks they assume the tensors are not changed in place
         self._memo: Dict[str, object] = {}
+
+    def _per_problem_vector(self, name, t, k):
+        """t as a (B, k) tensor: a (k,) vector is shared by the batch."""
+        t = as_tensor(t, self.dtype, self.device)
+        if t.shape[-1:] != (k,) or t.dim() > 2 or (t.dim() == 2 and t.shape[0] not in (1, self.B)):
+            raise ValueError(f"{name} has shape {tuple(t.shape)}, expected ({k},) or ({self.B}, {k})")
+        return t.expand(self.B, k).contiguous()
 
     def _memoized(self, key, make):
         v = self._memo.get(key)
@@ -131,10 +147,15 @@ class QuadraticTrackingOCP:
         return D.contiguous(), E, q.contiguous()
 
     def initial_equality(self):
+        """(A0 (B, n0, n), c0 (B, n0)): x_0 = x0, and with
+        constrain_initial_control also u_0 = u0 (n0 = nx + nu)
+        (get_initial_equality_linearized_matrices, :914-980)."""
         nx, nu = self.num_state_variables, self.num_control_variables
-        A0 = torch.zeros((self.B, nx, nx + nu), dtype=self.dtype, device=self.device)
-        A0[:, :, :nx] = torch.eye(nx, dtype=self.dtype, device=self.device)
-        return A0, self.x0.clone()
+        n0 = nx + nu if self.constrain_initial_control else nx
+        A0 = torch.zeros((self.B, n0, nx + nu), dtype=self.dtype, device=self.device)
+        A0[:, :, :n0] = torch.eye(n0, dtype=self.dtype, device=self.device)
+        c0 = torch.cat([self.x0, self.u0], dim=1) if self.constrain_initial_control else self.x0.clone()
+        return A0, c0.contiguous()
 
     def a_plus(self):
         nx, nu = self.num_state_variables, self.num_control_variables
@@ -207,10 +228,14 @@ class QuadraticTrackingOCP:
         raise NotImplementedError
 
     def equality_residuals(self, states, controls):
-        """(B, T, nx): x_0 - x0, then f(x_t, u_t) - x_{t+1} (equality_constraints,
-        optimal_control_problem.py:841-912)."""
+        """(B, T nx [+ nu]) flattened as the reference's equality_constraints
+        (optimal_control_problem.py:841-912): x_0 - x0, then f(x_t, u_t) -
+        x_{t+1}, then u_0 - u0 with constrain_initial_control."""
         x0 = (states[:, 0] - self.x0).unsqueeze(1)
-        return torch.cat([x0, self.next_states(states, controls) - states[:, 1:]], dim=1)
+        h = torch.cat([x0, self.next_states(states, controls) - states[:, 1:]], dim=1).flatten(1)
+        if self.constrain_initial_control:
+            h = torch.cat([h, controls[:, 0] - self.u0], dim=1)
+        return h
 
     def inequality_values(self, states, controls):
         """(g, l, u), each (B, T, m): the inequality rows g(x, u) and their
@@ -256,13 +281,19 @@ class QuadraticTrackingOCP:
 
     def with_params(self, problem_params: Optional[Dict[str, torch.Tensor]]) -> "QuadraticTrackingOCP":
         """Copy with the entries of problem_params that this problem carries
-        ("initial_state": (B, nx)); others are ignored."""
+        ("initial_state": (B, nx), "initial_control": (B, nu)); others are
+        ignored."""
         import copy
 
-        if not problem_params or "initial_state" not in problem_params:
+        if not problem_params or not ({"initial_state", "initial_control"} & set(problem_params)):
             return self
         other = copy.copy(self)
-        other.x0 = as_tensor(problem_params["initial_state"], self.dtype, self.device).expand_as(self.x0).contiguous()
+        if "initial_state" in problem_params:
+            other.x0 = self._per_problem_vector("initial_state", problem_params["initial_state"],
+                                                self.num_state_variables)
+        if "initial_control" in problem_params:
+            other.u0 = self._per_problem_vector("initial_control", problem_params["initial_control"],
+                                                self.num_control_variables)
         other._static, other._memo = None, {}
         return other
 
@@ -324,7 +355,7 @@ class QuadraticTrackingOCP:
         return other
 
     # per-problem tensors (leading axis B); subclasses add theirs
-    PER_PROBLEM = ("x0", "wx", "wu", "wf", "x_ref", "u_ref", "x_final_guess")
+    PER_PROBLEM = ("x0", "u0", "wx", "wu", "wf", "x_ref", "u_ref", "x_final_guess")
 
     def tile(self, k: int) -> "QuadraticTrackingOCP":
         """Copy holding k copies of the batch, problem b of copy j at index
@@ -343,6 +374,16 @@ class QuadraticTrackingOCP:
         tiles[k] = other
         return other
 
+    @property
+    def problem_params(self) -> Dict[str, torch.Tensor]:
+        """The problem parameters with_params and with_weights accept, at
+        their current values (the entries of the reference program's `params`
+        that a solve takes, optimal_control_problem.py:123-240)."""
+        out = {"initial_state": self.x0, **self.weights_dict()}
+        if self.constrain_initial_control:
+            out["initial_control"] = self.u0
+        return out
+
     def weights_dict(self) -> Dict[str, torch.Tensor]:
         return {
             "weights_penalization_reference_state_trajectory": self.wx,
@@ -358,17 +399,35 @@ class LinearOCP(QuadraticTrackingOCP):
 
     def __init__(self, *, A: torch.Tensor, Bm: torch.Tensor, b: Optional[torch.Tensor] = None, **kw):
         super().__init__(**kw)
-        self.A = as_tensor(A, self.dtype, self.device)
-        self.Bm = as_tensor(Bm, self.dtype, self.device)
-        self.b = (as_tensor(b, self.dtype, self.device) if b is not None
-                  else torch.zeros((self.B, self.num_state_variables), dtype=self.dtype, device=self.device))
+        B, nx, nu = self.B, self.num_state_variables, self.num_control_variables
+
+        def per_problem(name, t, shape):
+            # blocks shared by the batch ((nx, nx), (1, nx), ...) are expanded to
+            # one copy per problem: the device kernels index them per problem
+            t = as_tensor(t, self.dtype, self.device)
+            try:
+                return t.expand(shape).contiguous()
+            except RuntimeError:
+                raise ValueError(f"{name} of shape {tuple(t.shape)} does not broadcast to {shape}") from None
+
+        self.A = per_problem("A", A, (B, nx, nx))
+        self.Bm = per_problem("Bm", Bm, (B, nx, nu))
+        self.b = per_problem("b", b if b is not None else torch.zeros(nx, dtype=self.dtype), (B, nx))
 
     def dynamics_lagrangian_hessian(self, states, controls, lambdas):
         return None  # linear dynamics
 
     def next_states(self, states, controls):
         """(B, N, nx): A x_t + B u_t + b (tmpc_linear_dynamics_* on the device: a
-        batched GEMM of these tiny blocks takes milliseconds)."""
+        batched GEMM of these tiny blocks takes milliseconds).  Every block is
+        per problem and the trajectories have N + 1 stages (ValueError
+        otherwise): the kernel indexes them so."""
+        B, N, nx, nu = states.shape[0], self.horizon, self.num_state_variables, self.num_control_variables
+        want = {"A": (self.A, (B, nx, nx)), "Bm": (self.Bm, (B, nx, nu)), "b": (self.b, (B, nx)),
+                "states": (states, (B, N + 1, nx)), "controls": (controls, (B, N + 1, nu))}
+        for name, (t, shape) in want.items():
+            if tuple(t.shape) != shape:
+                raise ValueError(f"next_states: {name} has shape {tuple(t.shape)}, expected {shape}")
         if not states.is_cuda:
             xn = torch.einsum("bij,btj->bti", self.A, states[:, :-1]) + torch.einsum("bij,btj->bti", self.Bm,
                                                                                     controls[:, :-1])
@@ -376,11 +435,8 @@ class LinearOCP(QuadraticTrackingOCP):
         from .. import _lib
 
         lib = _lib.load()
-        B, N, nx, nu = states.shape[0], self.horizon, self.num_state_variables, self.num_control_variables
         c = lambda t: t.to(self.dtype).contiguous()  # noqa: E731
         states, controls, A, Bm, b = c(states), c(controls), c(self.A), c(self.Bm), c(self.b)
-        if A.shape[0] != B:
-            raise ValueError(f"states of {B} problems for a problem of {A.shape[0]}")
         nxt = torch.empty((B, N, nx), dtype=self.dtype, device=states.device)
         fn = f"tmpc_linear_dynamics_{_lib.suffix(self.dtype)}"
         _lib.check(fn, getattr(lib, fn)(_lib.stream_handle(states.device), B, N, nx, nu, _lib.ptr(states),

@@ -99,10 +99,11 @@ def quaternion_from_rotvec(r: torch.Tensor) -> torch.Tensor:
 
 
 def make_quadrotor_config(B: int = 4096, seed: int = 0, *, N: int = 40, dt: float = 0.02,
-                          dtype=torch.float32, device="cpu") -> QuadrotorOCP:
+                          dtype=torch.float32, device="cpu", **kw) -> QuadrotorOCP:
     """Config 3 of the benchmark: goal ~ U[-2,2]^3, x0 = hover + N(0, 0.3) on p and v
     plus a small random rotation; Q = diag(10 I3, I4, I3, 0.1 I3), R = 0.01 I4
-    toward hover thrust, thrusts in [0, 2 hover]."""
+    toward hover thrust, thrusts in [0, 2 hover].  Other keyword arguments go
+    to the problem (for example constrain_initial_control, initial_control)."""
     g = torch.Generator().manual_seed(int(seed))
     hov = hover_thrust()
     goal = torch.rand((B, 3), generator=g, dtype=torch.float64) * 4.0 - 2.0
@@ -131,6 +132,7 @@ def make_quadrotor_config(B: int = 4096, seed: int = 0, *, N: int = 40, dt: floa
         initial_guess_final_state=xg,
         dtype=dtype,
         device=device,
+        **kw,
     )
 
 

@@ -198,7 +198,7 @@ class ADMMSolver:
         iters, bad = _split_iters(iters)
         return (states, controls), ADMMStats(num_iter=iters, num_pcg_iters=pcg_iters, nonfinite=bad), state
 
-    def sqp_step(self, qp_data: QPData, admm_state0: ADMMState, active: torch.Tensor, tol: float,
+    def sqp_step(self, qp_data: QPData, admm_state0: ADMMState, active: torch.Tensor, tol: Optional[float],
                  rho_bar: float = 1.0, alpha: float = 1.0, *, slack_weight=0.0,
                  workspace: Optional[torch.Tensor] = None, warm_records: bool = False,
                  warm_ineq: bool = False, donate_state: bool = False):
@@ -210,7 +210,9 @@ class ADMMSolver:
         on it, whose output is admm_state0, and that qp_data differs from that
         call's QP only in A_minus and c (FLAG_WARM_RECORDS); with warm_ineq
         also in G, l and u (FLAG_WARM_INEQ).  donate_state:
-        admm_state0's buffers may be updated in place.  Returns
+        admm_state0's buffers may be updated in place.  tol None: the
+        activity is given (no check; the problems where `active` is False keep
+        their state, and the check outputs are None).  Returns
         ((states, controls), stats, state, (conv, eq_err, ineq_err, g), active_out)."""
         if self._admm_backend != AdmmBackend.HIP_DIRECT:
             raise ValueError("sqp_step needs the direct Schur solve (HIP_DIRECT)")

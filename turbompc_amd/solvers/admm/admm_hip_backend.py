@@ -94,7 +94,9 @@ def admm_hip_solve(qp: QPData, state0, *, schur: str, cfg: _lib.AdmmCfg,
     (tmpc_sqp_admm_step_*, direct Schur solve only): the first-order check of
     state0 against qp, the activity test active & (conv > tol), and the solve of
     the problems that pass it; the call then also returns (conv, eq_err,
-    ineq_err, g, active_out).
+    ineq_err, g, active_out).  With tol None the activity is given: no check
+    runs, the problems where `active` is False keep their state, and conv,
+    eq_err, ineq_err and g are None.
 
     donate: the caller gives up state0: fields that already have the output's
     shape, dtype and layout are updated in place instead of copied (the
@@ -139,12 +141,16 @@ def admm_hip_solve(qp: QPData, state0, *, schur: str, cfg: _lib.AdmmCfg,
             active, tol = sqp
             act_in = active.to(device=dev, dtype=torch.uint8).contiguous()
             act_out = torch.empty(B, dtype=torch.uint8, device=dev)
-            conv = torch.empty(B, dtype=dt, device=dev)
-            eq = torch.empty(B, dtype=dt, device=dev)
-            iq = torch.empty(B, dtype=dt, device=dev)
-            g = torch.empty((B, T, m), dtype=dt, device=dev)
-            sq = _lib.SqpStep(_lib.ptr(act_in), _lib.ptr(act_out), float(tol), _lib.ptr(conv), _lib.ptr(eq),
-                              _lib.ptr(iq), _lib.ptr(g))
+            if tol is None:  # activity given: no check
+                conv = eq = iq = g = None
+                sq = _lib.SqpStep(_lib.ptr(act_in), _lib.ptr(act_out), 0.0, None, None, None, None)
+            else:
+                conv = torch.empty(B, dtype=dt, device=dev)
+                eq = torch.empty(B, dtype=dt, device=dev)
+                iq = torch.empty(B, dtype=dt, device=dev)
+                g = torch.empty((B, T, m), dtype=dt, device=dev)
+                sq = _lib.SqpStep(_lib.ptr(act_in), _lib.ptr(act_out), float(tol), _lib.ptr(conv), _lib.ptr(eq),
+                                  _lib.ptr(iq), _lib.ptr(g))
             st = getattr(lib, f"tmpc_sqp_admm_step_{sfx}")(
                 stream, ctypes.byref(dims), ctypes.byref(cq), ctypes.byref(sv), ctypes.byref(sv),
                 _lib.ptr(iters), ctypes.byref(cfg), ctypes.byref(sq), _lib.ptr(ws), nbytes,

@@ -281,8 +281,10 @@ class TurboMPCSolver:
                   dl_dslack: Optional[torch.Tensor] = None, problem_params=None, weights=None):
         """Backward pass of the differentiable solve (`_solve_bwd` of
         get_differentiable_solve_function, turbompc_solver.py:1052-1084): returns
-        (problem_params cotangent {"initial_state": dL/dx0 (B, nx)}, dL/dweights
-        {key: (B, ...)}) for the cotangents of the solution's states and controls."""
+        (problem_params cotangent {"initial_state": dL/dx0 (B, nx)}, plus
+        "initial_control": dL/du0 (B, nu) with constrain_initial_control
+        (_build_problem_params_cotangent, :990-1018), dL/dweights {key: (B, ...)})
+        for the cotangents of the solution's states and controls."""
         problem_params, weights = self._split_params(problem_params, weights)
         program = self._program_for(problem_params, weights)
         if solution.kkt_state is None:
@@ -296,6 +298,8 @@ class TurboMPCSolver:
         if weights and "slack_penalization_weight" in weights:
             dL_dw["slack_penalization_weight"] = res.dL_dgamma
         cot = {"initial_state": res.dL_dx_init}
+        if res.dL_du_init is not None:
+            cot["initial_control"] = res.dL_du_init
         return cot, dL_dw
 
     def get_differentiable_solve_function(self):
@@ -306,9 +310,11 @@ class TurboMPCSolver:
         return DifferentiableSolve(self)
 
     def make_params_with_weights(self, weights, problem_params=None) -> Dict[str, Any]:
-        """problem_params (or {}) with the entries of `weights` merged in
-        (make_params_with_weights, turbompc_solver.py:511-526); solve and
-        solve_vjp take the weight keys from problem_params as from `weights`."""
+        """A deep copy of problem_params (of the program's own params when
+        None) with the entries of `weights` merged in, nested dictionaries key
+        by key (make_params_with_weights, turbompc_solver.py:511-526); the
+        caller's dictionaries are not changed.  solve and solve_vjp take the
+        weight keys from problem_params as from `weights`."""
         def merge(dst, src):
             for k, v in src.items():
                 if isinstance(v, dict) and isinstance(dst.get(k), dict):
@@ -316,8 +322,9 @@ class TurboMPCSolver:
                 else:
                     dst[k] = v
 
-        out = dict(problem_params) if problem_params else {}
-        merge(out, dict(weights) if weights else {})
+        base = problem_params if problem_params is not None else getattr(self._program, "problem_params", {})
+        out = copy.deepcopy(dict(base))
+        merge(out, copy.deepcopy(dict(weights)) if weights else {})
         return out
 
     def linesearch(self, states, controls, slacks, states_new, controls_new, slacks_new, problem_params=None):
@@ -402,6 +409,10 @@ class TurboMPCSolver:
         m_eq = n0 + (T - 1) * nx
         y_f0 = mult[:, :n0]
         y_eq_lin = mult[:, :m_eq]
+        if n0 > nx:
+            # constrain_initial_control: the u_0 rows' multipliers go last, as
+            # in the reference's equality-constraint vector (:739-744)
+            y_eq_lin = torch.cat([y_f0[:, :nx], mult[:, n0:m_eq], y_f0[:, nx:]], dim=1)
         kkt = solution.kkt_state
         dL_dgamma = torch.zeros((), dtype=mult.dtype, device=mult.device)
         base = ctx.base_qp
@@ -417,7 +428,9 @@ class TurboMPCSolver:
             dL_dgamma = (sign * kkt.slack * active * g_dz).flatten(1).sum(dim=1)
         else:
             y_ineq_lin = mult[:, m_eq:]
-        return _BackwardSolveResult(dxs, dus, y_eq_lin, y_ineq_lin, dL_dgamma, y_f0[:, :nx], None)
+        # dL/dx0 and, with constrain_initial_control, dL/du0 (:765-770)
+        return _BackwardSolveResult(dxs, dus, y_eq_lin, y_ineq_lin, dL_dgamma, y_f0[:, :nx],
+                                    y_f0[:, nx:] if n0 > nx else None)
 
     # ------------------------------------------------------------ internals ----
     def _first_order_check(self, qp: QPData, states, controls, slacks, admm_state: ADMMState):
@@ -571,7 +584,7 @@ class TurboMPCSolver:
         unblended (turbompc_solver.py:1591-1604); the first-order check then
         runs on the committed iterate (tmpc_sqp_first_order_*).  The `step`
         criterion takes max |z_new - z| (+ the slack step) instead.  The step
-        takes the activity as given (tol -1: every conv >= 0 passes): stopped
+        takes the activity as given (tol None: no fused check runs): stopped
         problems are skipped (their ADMM state stays as it was) and keep their
         iterate by masked selects, and relinearizing at the committed iterate
         rebuilds a stopped problem's QP unchanged.  Same records as
@@ -610,7 +623,7 @@ class TurboMPCSolver:
                     break
                 warm = _warm_level(qp, prev)
                 (s_new, c_new), stats, adm_new, _, _ = admm.sqp_step(
-                    qp, admm_state, active, -1.0, rho_bar=ap["rho"], alpha=alpha, slack_weight=sw, workspace=ws,
+                    qp, admm_state, active, None, rho_bar=ap["rho"], alpha=alpha, slack_weight=sw, workspace=ws,
                     warm_records=warm is not None, warm_ineq=warm == "constraints", donate_state=True)
             sl_new = adm_new.xi_g
             if use_ls:
@@ -782,15 +795,15 @@ class _AttachSolution(torch.autograd.Function):
     of (x0, weights...); the backward pass is TurboMPCSolver.solve_vjp."""
 
     @staticmethod
-    def forward(ctx, solver, sol, params, weights, keys, has_x0, *inputs):
-        ctx.solver, ctx.sol, ctx.params, ctx.weights, ctx.keys, ctx.has_x0 = solver, sol, params, weights, keys, has_x0
+    def forward(ctx, solver, sol, params, weights, keys, pkeys, *inputs):
+        ctx.solver, ctx.sol, ctx.params, ctx.weights, ctx.keys, ctx.pkeys = solver, sol, params, weights, keys, pkeys
         ctx.metas = [(t.shape, t.device, t.dtype) for t in inputs]
         return sol.states.clone(), sol.controls.clone()
 
     @staticmethod
     def backward(ctx, g_states, g_controls):
         cot, dw = ctx.solver.solve_vjp(ctx.sol, g_states, g_controls, None, ctx.params, ctx.weights)
-        grads = ([cot["initial_state"]] if ctx.has_x0 else []) + [dw[k] for k in ctx.keys]
+        grads = [cot[k] for k in ctx.pkeys] + [dw[k] for k in ctx.keys]
         # inputs shared across the batch get the batch sum of their per-problem gradients
         grads = [g.sum_to_size(shape).to(device=dev, dtype=dt) for g, (shape, dev, dt) in zip(grads, ctx.metas)]
         return (None, None, None, None, None, None, *grads)
@@ -804,16 +817,19 @@ class DifferentiableSolve:
 
     def __call__(self, initial_guess: TurboMPCSolution, problem_params=None, weights=None) -> TurboMPCSolution:
         keys = tuple(weights.keys()) if weights else ()
-        x0 = problem_params.get("initial_state") if problem_params else None
-        inputs = ([torch.as_tensor(x0)] if x0 is not None else []) + [torch.as_tensor(weights[k]) for k in keys]
+        # differentiable problem parameters: the initial state, and the initial
+        # control where the problem constrains it
+        constrained_u0 = getattr(self._solver.program, "constrain_initial_control", False)
+        pkeys = ("initial_state",) + (("initial_control",) if constrained_u0 else ())
+        pkeys = tuple(k for k in pkeys if problem_params and problem_params.get(k) is not None)
+        inputs = [torch.as_tensor(problem_params[k]) for k in pkeys] + [torch.as_tensor(weights[k]) for k in keys]
         det = lambda d: {k: (v.detach() if torch.is_tensor(v) else v) for k, v in d.items()} if d else d  # noqa: E731
         params_d, weights_d = det(problem_params), det(weights)
         with torch.no_grad():
             sol = self._solver.solve(initial_guess, params_d, weights_d)
         if not any(t.requires_grad for t in inputs):
             return sol
-        states, controls = _AttachSolution.apply(self._solver, sol, params_d, weights_d, keys, x0 is not None,
-                                                 *inputs)
+        states, controls = _AttachSolution.apply(self._solver, sol, params_d, weights_d, keys, pkeys, *inputs)
         return sol._replace(states=states, controls=controls)
 
 
