@@ -129,6 +129,14 @@ int tmpc_version(void);
  * launches the solves. */
 void tmpc_set_timing_events(hipEvent_t before, hipEvent_t after);
 
+/* ---- zero fill by a kernel ---------------------------------------------------
+ * No counterpart in the reference: for bindings that must zero a result the
+ * reference writes as zero (kernel_ns of the fused ADMM targets,
+ * turbompc/solvers/admm/csrc/admm_cudss.cu:1189-1197) without recording a
+ * memset node into a captured HIP graph.  p and bytes must be multiples of 4
+ * (TMPC_EBADARG otherwise); bytes = 0 does nothing. */
+int tmpc_fill_zero(hipStream_t stream, void* p, size_t bytes);
+
 /* ---- ADMM with the exact block-tridiagonal Schur solve ---------------------
  * Replaces the `admm_cudss_cuda[_f64]` FFI target: AdmmCudssCudaImpl
  * (turbompc/solvers/admm/csrc/admm_cudss_ffi.cc:13-140) / launchADMMCudss

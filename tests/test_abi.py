@@ -111,3 +111,10 @@ def test_iteration_words_split_into_counts_and_nonfinite_flags():
     counts, bad = _split_iters(words)
     assert counts.tolist() == [0, 12, 0x7FFFFFFF, 12, 0]
     assert bad.tolist() == [False, False, False, True, True]
+
+
+def test_fill_zero_checks_alignment_before_any_launch(lib):
+    assert lib.tmpc_fill_zero(None, None, 0) == 0  # nothing to fill
+    assert lib.tmpc_fill_zero(None, None, 16) == 2  # null pointer
+    assert lib.tmpc_fill_zero(None, ctypes.c_void_p(0x1002), 16) == 2  # misaligned pointer
+    assert lib.tmpc_fill_zero(None, ctypes.c_void_p(0x1000), 6) == 2  # not whole words

@@ -111,3 +111,13 @@ def test_nonfinite_flag_reaches_the_sqp_solution():
     torch.cuda.synchronize()
     assert sol.nonfinite.tolist() == [False, True, False, False, False, False]
     assert bool(torch.isfinite(sol.states[[0, 2, 3, 4, 5]]).all())
+
+
+def test_fill_zero_entry_point():
+    """tmpc_fill_zero (a kernel, no memset node): zeroes exactly the words asked for."""
+    lib = _lib.load()
+    x = torch.full((1000,), 7.0, dtype=torch.float32, device=DEV)
+    st = lib.tmpc_fill_zero(_lib.stream_handle(x.device), _lib.ptr(x), 999 * 4)
+    assert st == 0
+    torch.cuda.synchronize()
+    assert bool((x[:999] == 0).all()) and float(x[999]) == 7.0

@@ -121,6 +121,7 @@ _PD, _PQ, _PS, _PC, _PSQ = (ctypes.POINTER(t) for t in (Dims, QP, State, AdmmCfg
 SIGNATURES = {
     "tmpc_version": [],
     "tmpc_set_timing_events": [_VP, _VP],
+    "tmpc_fill_zero": [_VP, _VP, _SZ],
     "tmpc_status_string": [ctypes.c_int],
     "tmpc_admm_direct_workspace_bytes": [ctypes.c_int, _PD],
     "tmpc_admm_direct_f32": [_VP, _PD, _PQ, _PS, _PS, _VP, _PC, _VP, _SZ],

@@ -1222,6 +1222,17 @@ const char* tmpc_status_string(int status) {
 
 int tmpc_version(void) { return 100; }
 
+int tmpc_fill_zero(hipStream_t s, void* p, size_t bytes) {
+  if (bytes == 0) return TMPC_OK;
+  if (!p || (reinterpret_cast<uintptr_t>(p) & 3u) != 0 || (bytes & 3u) != 0) return TMPC_EBADARG;
+  const size_t words = bytes / 4;
+  const size_t blocks = (words + 255) / 256;
+  if (blocks > 0x7fffffffu) return TMPC_EBADARG;
+  hipLaunchKernelGGL((fill_kernel<uint32_t>), dim3((unsigned)blocks), dim3(256), 0, s, static_cast<uint32_t*>(p),
+                     words, 0u);
+  return launch_status();
+}
+
 void tmpc_set_timing_events(hipEvent_t before, hipEvent_t after) {
   g_iter_events[0] = before;
   g_iter_events[1] = after;
