@@ -108,6 +108,13 @@ typedef struct tmpc_state {
  * rows are), whose records are rewritten too; D, E, q, A0, c0 and the slack
  * weight are still unchanged. */
 #define TMPC_FLAG_WARM_INEQ 16u
+/* Every G_t is the same for every stage and problem (box rows of a tracking
+ * problem), vouched for by the caller.  The streaming kernel for n = 17
+ * records then keeps the G rows of its stage blocks in LDS and streams only
+ * the A_minus rows of the stage records in its backward sweep, as in its
+ * forward sweep (fewer bytes per iteration; the same products, so the same
+ * iterates bit for bit).  Ignored by the other paths and shapes. */
+#define TMPC_FLAG_CONST_G 32u
 
 typedef struct tmpc_admm_cfg {
   int32_t max_iter, check_every, adapt_rho_every, pcg_max_iter, use_slack;

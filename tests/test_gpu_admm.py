@@ -20,7 +20,7 @@ import pytest
 import torch
 
 import oracle
-from helpers import TOL, random_qp, rel_err, soften, zero_state
+from helpers import TOL, np_qp, random_qp, rel_err, soften, zero_state
 from turbompc_amd import _lib
 from turbompc_amd.problems import configs
 from turbompc_amd.problems.quadrotor import QUAD_PARAMS, make_quadrotor_config
@@ -738,3 +738,77 @@ def test_admm_stream_kernel_structured_records_match_dense_on_bench_batch():
     ref, it_ref = _oracle_full_batch(qp, cfg)
     np.testing.assert_array_equal(s_b.num_iter.cpu().numpy(), it_ref)
     _assert_batch_matches_oracle("config 3 B=4099 diagonal records", o_b, ref, TOL[torch.float32])
+
+
+# ---- G rows resident in LDS (TMPC_FLAG_CONST_G: the same G_t for every stage
+# and problem, as box rows are): the backward sweep streams only the A_minus
+# rows; the products are the same, so the iterates are bit for bit those of
+# the form that streams the whole records, and match the oracle.
+def _shared_g(qp, seed=0):
+    """qp with one G_t (problem 0's stage 0) for every stage and problem, and
+    bounds around G z at a point z that satisfies the equality constraints
+    (least squares on the dense C), so that the QP stays feasible."""
+    from helpers import dense_C
+
+    G = qp.ineq.G[:1, :1].expand_as(qp.ineq.G).contiguous()
+    a = np_qp(qp)
+    B, T, m, n = G.shape
+    rng = np.random.default_rng(seed)
+    l, u = np.empty((B, T, m)), np.empty((B, T, m))
+    for b in range(B):
+        C = dense_C(a["A0"][b], a["Am"][b], a["Ap"][b])
+        z = np.linalg.lstsq(C, np.concatenate([a["c0"][b], a["c"][b].reshape(-1)]), rcond=None)[0].reshape(T, n)
+        gz = np.einsum("tij,tj->ti", G[b].numpy(), z)
+        l[b] = gz - rng.uniform(0.05, 0.5, size=(T, m))
+        u[b] = gz + rng.uniform(0.05, 0.5, size=(T, m))
+    return qp.replace_ineq(G=G, l=torch.tensor(l), u=torch.tensor(u))
+
+
+@pytest.mark.parametrize("dtype", [torch.float64, torch.float32])
+@pytest.mark.parametrize("P", [1, 2])
+# n = 17 records run the resident-G form (nx + m = 17, 17 and 16 below);
+# elsewhere the flag is ignored (n = 6)
+@pytest.mark.parametrize("shape", [(8, 11, 17, 13, 4), (5, 9, 17, 12, 5), (6, 7, 17, 13, 3), (13, 21, 6, 4, 2)])
+def test_admm_stream_kernel_const_g_rows(shape, P, dtype):
+    B, T, n, nx, m = shape
+    qp = _shared_g(random_qp(B, T, n, nx, m, seed=57, std=True, diag=True))
+    cfg = oracle.OracleCfg(max_iter=20, check_every=3, adapt_rho_every=0, sigma=1e-6, eps_abs=1e-12,
+                           eps_rel=1e-12, rho_f_factor=1000.0, alpha=1.6)
+    outs = []
+    for const_g in (False, True):
+        ref, it_ref, _, out, stats = _run_pair(qp, cfg, dtype, kernel_flags=_lib.flag_stream_p(P), diag_cost=True,
+                                               const_g=const_g)
+        np.testing.assert_array_equal(stats.num_iter.cpu().numpy(), it_ref)
+        outs.append(out)
+    for k in FIELDS:
+        assert torch.equal(getattr(outs[0], k), getattr(outs[1], k)), k
+    assert float(np.max(np.abs(ref.y_g))) > 0  # some rows are active
+    # fp32 on these random QPs (cond(Theta) up to ~1e6 at rho_f = 100, the
+    # inverse rounded to fp32 on store): measured up to 1.3e-4 against the fp64
+    # oracle in either form; the workload tests hold fp32 to 1e-4
+    _assert_state_close(outs[1], ref, 1e-9 if dtype == torch.float64 else 5e-4)
+
+
+def test_quadrotor_sqp_const_g_rows_bit_equal():
+    """The benchmark's solve with and without the resident G rows (the
+    solver sets the flag for box rows): the same iterates bit for bit."""
+    prob = make_quadrotor_config(B=300, seed=9, dtype=torch.float32, device=DEV)
+    import copy as _copy
+
+    from turbompc_amd.solvers.turbompc_solver import DEFAULT_SOLVER_PARAMS, TurboMPCSolver
+
+    params = _copy.deepcopy(DEFAULT_SOLVER_PARAMS)
+    params["num_sqp_iteration_max"], params["tol_convergence"] = 3, 0.0
+    params["admm"].update(max_iter=20, adapt_rho_every=0, relaxation_parameter=1.0)
+    sols = []
+    for const_g in (True, False):
+        p2 = _copy.copy(prob)
+        p2.const_g = const_g
+        solver = TurboMPCSolver(p2, params)
+        assert bool(solver._admm_solver_fwd._kernel_flags & _lib.FLAG_CONST_G) == const_g
+        sols.append(solver.solve(solver.initial_guess()))
+    torch.cuda.synchronize()
+    for k in ("states", "controls"):
+        assert torch.equal(getattr(sols[0], k), getattr(sols[1], k)), k
+    for k in sols[0].admm_state._fields:
+        assert torch.equal(getattr(sols[0].admm_state, k), getattr(sols[1].admm_state, k)), k

@@ -624,7 +624,11 @@ struct StreamOcc {
   static constexpr int waves = sizeof(R) == 4 ? 2 : 1;
 };
 
-template <typename R, int NC, int P, int DPF, int NL = NC, int MM = kMaxStreamM>
+// GRES: G_t is the same for every stage and problem (box rows; vouched for by
+// the caller, TMPC_FLAG_CONST_G).  The G rows of every M slot are written into
+// LDS once, from the wavefront's first record, and the backward sweep streams
+// only the A_minus rows of each stage record, as the forward sweep does.
+template <typename R, int NC, int P, int DPF, int NL = NC, int MM = kMaxStreamM, bool GRES = false>
 __global__ __launch_bounds__(kWave, StreamOcc<R>::waves) void admm_stream_kernel(StreamArgs<R> a) {
   static_assert(NL >= NC && NL <= kWave / P, "row lanes must fit a problem's group");
   using V = typename Vec16<R>::T;
@@ -702,12 +706,48 @@ __global__ __launch_bounds__(kWave, StreamOcc<R>::waves) void admm_stream_kernel
       fa_off[c] = pe < nprob ? (pe * amp + (e - pe * ca) * W) * (int)sizeof(R) : -1;
     }
   }
+  // M runs of the backward sweep: the whole records, or (GRES) their A_minus
+  // rows only, through the same chunk map as the forward sweep
+  auto load_m = [&](V (&r)[CH_AM], int t) __attribute__((always_inline)) {
+    if constexpr (GRES) {
+      const __amdgpu_buffer_rsrc_t rs =
+          __builtin_amdgcn_make_buffer_rsrc(const_cast<V*>(am_run(t)), (short)0, nch_am * 16, kBufferFlags);
+#pragma unroll
+      for (int c = 0; c < CH_AM; ++c)
+        r[c] = __builtin_bit_cast(V, __builtin_amdgcn_raw_buffer_load_b128(rs, fa_off[c], 0, 0));
+    } else {
+      load_run<V, CH_AM>(r, am_run(t), nch_am);
+    }
+  };
+  auto store_m = [&](const V (&r)[CH_AM], R* slot) __attribute__((always_inline)) {
+    if constexpr (GRES) {
+      V* dst = reinterpret_cast<V*>(slot);
+#pragma unroll
+      for (int c = 0; c < CH_AM; ++c) *(fa_off[c] >= 0 ? dst + (fa_off[c] >> 4) : spl) = r[c];
+    } else {
+      store_run<V, CH_AM>(r, reinterpret_cast<V*>(slot), nch_am, spl);
+    }
+  };
 
   // ---- LDS starts zeroed (the column products rely on finite data past the
   // blocks); resident data: A0 in LDS, c0 / y_f0 in registers ---------------
   for (int e = tid; e < L.total / W; e += kWave) reinterpret_cast<V*>(lds)[e] = V{};
   lds_order();
   for (int e = tid; e < nprob * n0 * n; e += kWave) lds[L.a0 + e] = a.A0[(size_t)b0 * n0 * n + e];
+  // GRES: the G rows of every M slot (slot s at L.am + s amp), from stage 0
+  // of the wavefront's first problem; written again after each residual
+  // reduction, whose scratch (from L.th) may reach into the slots
+  auto fill_g = [&]() __attribute__((always_inline)) {
+    if constexpr (GRES) {
+      const R* g0 = a.am + (size_t)b0 * amp + nx * n;
+      const int gl = m * n, nslot = (DPF > 2 ? DPF : 2) * P;
+      for (int e = tid; e < nslot * gl; e += kWave) {
+        const int sl = e / gl, k = e - sl * gl;
+        lds[L.am + sl * amp + nx * n + k] = g0[k];
+      }
+    }
+  };
+  fill_g();
   const R c0v = (i < n0) ? a.c0[(size_t)b * n0 + i] : R(0);
   R yf0v = (i < n0) ? a.y_f0[(size_t)b * n0 + i] : R(0);
 
@@ -830,6 +870,7 @@ __global__ __launch_bounds__(kWave, StreamOcc<R>::waves) void admm_stream_kernel
 #pragma unroll
         for (int l = 0; l < NL; ++l) mxs[k] = rmax(mxs[k], red[k * kWave + base + l]);
       lds_order();
+      fill_g();  // the reduction's scratch may have reached the M slots
       const R conv = rmax(rmax(mxs[0], mxs[1]), rmax(mxs[2], mxs[3]));
       const bool act = (a.act_in ? a.act_in[b] != 0 : true) && conv > a.chk_tol;
       if (G.live && i == 0) {
@@ -927,11 +968,11 @@ __global__ __launch_bounds__(kWave, StreamOcc<R>::waves) void admm_stream_kernel
       R* dm_slot = dmS(0);
       // prologue: M_{T-1} into its slot; ra <- Theta^{-1}, M of T-2 and rv, D
       // of T-1 (step T-1); with two sets rb <- those of T-3 and T-2 (step T-2)
-      load_run<V, CH_AM>(ra.am, am_run(T - 1), nch_am);
-      store_run<V, CH_AM>(ra.am, reinterpret_cast<V*>(amP(T - 1)), nch_am, spl);
+      load_m(ra.am, T - 1);
+      store_m(ra.am, amP(T - 1));
       if (T >= 2) {
         load_run<V, CH_TH>(ra.th, th_run(T - 2), nch_th);
-        load_run<V, CH_AM>(ra.am, am_run(T - 2), nch_am);
+        load_m(ra.am, T - 2);
       }
       load_run<V, CH_RV>(ra.rv, rv_run(T - 1), nch_rv);
       if (chk) load_run<V, CH_TH>(ra.dm, dm_run(T - 1), nch_dm);
@@ -942,7 +983,7 @@ __global__ __launch_bounds__(kWave, StreamOcc<R>::waves) void admm_stream_kernel
         }
         if (T >= 3) {
           load_run<V, CH_TH>(rb.th, th_run(T - 3), nch_th);
-          load_run<V, CH_AM>(rb.am, am_run(T - 3), nch_am);
+          load_m(rb.am, T - 3);
         }
       }
       R xa = i < n ? wgp[N * n + i] : R(0);  // xt_t for the coming step (xt_N = w_N)
@@ -959,7 +1000,7 @@ __global__ __launch_bounds__(kWave, StreamOcc<R>::waves) void admm_stream_kernel
         // group's slot (never read as part of the vector).
         if (hasA) {
           store_run<V, CH_TH>(pr.th, reinterpret_cast<V*>(th_slot), nch_th, spl);
-          store_run<V, CH_AM>(pr.am, reinterpret_cast<V*>(amP(t - 1)), nch_am, spl);
+          store_m(pr.am, amP(t - 1));
         }
         store_run<V, CH_RV>(pr.rv, reinterpret_cast<V*>(rv_slot), nch_rv, spl);
         if (chk) store_run<V, CH_TH>(pr.dm, reinterpret_cast<V*>(dm_slot), nch_dm, spl);
@@ -969,7 +1010,7 @@ __global__ __launch_bounds__(kWave, StreamOcc<R>::waves) void admm_stream_kernel
         // this set's next use is step t - PFD
         if (t >= PFD + 1) {
           load_run<V, CH_TH>(pr.th, th_run(t - PFD - 1), nch_th);
-          load_run<V, CH_AM>(pr.am, am_run(t - PFD - 1), nch_am);
+          load_m(pr.am, t - PFD - 1);
         }
         if (t >= PFD) {
           load_run<V, CH_RV>(pr.rv, rv_run(t - PFD), nch_rv);
@@ -1145,6 +1186,7 @@ __global__ __launch_bounds__(kWave, StreamOcc<R>::waves) void admm_stream_kernel
 #pragma unroll
       for (int k = 0; k < 11; ++k) r[k] = red[k * kWave + base];
       lds_order();
+      fill_g();  // the reduction's scratch may have reached the M slots
       const R np = rmax(rmax(r[1], r[3]), rmax(r[2], r[4]));
       R nd = rmax(rmax(r[6], r[7]), r[8]);
       if (slack) nd = rmax(nd, rmax(gs * r[9], r[10]));

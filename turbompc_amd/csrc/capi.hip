@@ -275,21 +275,38 @@ bool stream_ok(const Dims& d, int P, bool diag) {
   return (size_t)L.total * sizeof(R) <= kMaxLds;
 }
 
-template <typename R, int NC, int P, int NL = NC, int MM = kMaxStreamM>
+template <typename R, int NC, int P, int NL = NC, int MM = kMaxStreamM, bool GRES = false>
 void launch_stream_p(hipStream_t s, const StreamArgs<R>& a) {
   constexpr int DPF = stream_depth(NC);
   const StreamLayout L = stream_layout(a.d, P, DPF, a.diag != 0);
   const size_t smem = (size_t)L.total * sizeof(R);
-  lds_optin(admm_stream_kernel<R, NC, P, DPF, NL, MM>, smem);
+  lds_optin(admm_stream_kernel<R, NC, P, DPF, NL, MM, GRES>, smem);
   const int grid = (a.d.B + P - 1) / P;
-  hipLaunchKernelGGL((admm_stream_kernel<R, NC, P, DPF, NL, MM>), dim3(grid), dim3(kWave), smem, s, a);
+  hipLaunchKernelGGL((admm_stream_kernel<R, NC, P, DPF, NL, MM, GRES>), dim3(grid), dim3(kWave), smem, s, a);
 }
 
+// gres: G_t is the same for every stage and problem (TMPC_FLAG_CONST_G).  Its
+// form (the G rows resident in LDS, A_minus rows streamed) is built for the
+// n = 17 records with one or two problems per wavefront, where it pays: config
+// 3, 1.995 -> 1.924 ms per launch (G is 68 of the 292 words of a record); at
+// n = 9 in fp64 (config 5, 27 of 84 words) the scattered A-row stores cost
+// more than the bytes they save (25.05 -> 25.51 ms)
 template <typename R, int NC, int NL = NC, int MM = kMaxStreamM>
-void launch_stream_nc(hipStream_t s, const StreamArgs<R>& a, int P) {
+void launch_stream_nc(hipStream_t s, const StreamArgs<R>& a, int P, bool gres) {
+  constexpr bool kGres = NL == NC && NC == 17;
   switch (P) {
-    case 1: launch_stream_p<R, NC, 1, NL, MM>(s, a); break;
-    case 2: launch_stream_p<R, NC, 2, NL, MM>(s, a); break;
+    case 1:
+      if (kGres && gres)
+        launch_stream_p<R, NC, 1, NL, MM, kGres>(s, a);
+      else
+        launch_stream_p<R, NC, 1, NL, MM>(s, a);
+      break;
+    case 2:
+      if (kGres && gres)
+        launch_stream_p<R, NC, 2, NL, MM, kGres>(s, a);
+      else
+        launch_stream_p<R, NC, 2, NL, MM>(s, a);
+      break;
     default:
       if constexpr (3 * NL <= kWave) launch_stream_p<R, NC, 3, NL, MM>(s, a);  // stream_ok rules out the rest
       break;
@@ -297,22 +314,22 @@ void launch_stream_nc(hipStream_t s, const StreamArgs<R>& a, int P) {
 }
 
 template <typename R>
-void launch_stream(hipStream_t s, const StreamArgs<R>& a, int P) {
+void launch_stream(hipStream_t s, const StreamArgs<R>& a, int P, bool gres) {
   switch (a.d.n) {
-    case 6: launch_stream_nc<R, 6>(s, a, P); break;
+    case 6: launch_stream_nc<R, 6>(s, a, P, gres); break;
     case 9:
       if (stream_wide(a.d))
-        launch_stream_nc<R, 9, kWideRows, kWideMaxM>(s, a, P);
+        launch_stream_nc<R, 9, kWideRows, kWideMaxM>(s, a, P, gres);
       else
-        launch_stream_nc<R, 9>(s, a, P);
+        launch_stream_nc<R, 9>(s, a, P, gres);
       break;
     case 16:
       if (stream_wide(a.d))
-        launch_stream_nc<R, 16, kWide16Rows, kWide16MaxM>(s, a, P);
+        launch_stream_nc<R, 16, kWide16Rows, kWide16MaxM>(s, a, P, gres);
       else
-        launch_stream_nc<R, 16>(s, a, P);
+        launch_stream_nc<R, 16>(s, a, P, gres);
       break;
-    default: launch_stream_nc<R, 17>(s, a, P); break;
+    default: launch_stream_nc<R, 17>(s, a, P, gres); break;
   }
 }
 
@@ -336,13 +353,32 @@ void launch_factor_std_nc(hipStream_t s, const Dims& d, const DirectWs<R>& w, co
   }
 }
 
+template <typename R, int NC, int NR, bool DIAG, bool FULL>
+void launch_factor_row_k(hipStream_t s, const Dims& d, const DirectWs<R>& w, const QPDev<R>& q, const R* rho,
+                         R sigma, R rho_f_factor, int32_t* ctl) {
+  constexpr int per_wave = kWave / kFacRow;
+  const int grid = (d.B + per_wave - 1) / per_wave;
+  hipLaunchKernelGGL((factor_row_kernel<R, NC, NR, DIAG, FULL>), dim3(grid), dim3(kWave), 0, s, d, (const R*)w.am,
+                     (const R*)w.dm, q.A0, rho, sigma, rho_f_factor, ctl, w.thinv);
+}
+
+// DIAG and FULL (nx + m == NR) select the specialised forms; the wide forms
+// (NR > NC) always test their rows
 template <typename R, int NC, int NR>
 void launch_factor_row_nc(hipStream_t s, const Dims& d, const DirectWs<R>& w, const QPDev<R>& q, const R* rho,
                           R sigma, R rho_f_factor, int32_t* ctl, bool diag) {
-  constexpr int per_wave = kWave / kFacRow;
-  const int grid = (d.B + per_wave - 1) / per_wave;
-  hipLaunchKernelGGL((factor_row_kernel<R, NC, NR>), dim3(grid), dim3(kWave), 0, s, d, (const R*)w.am,
-                     (const R*)w.dm, q.A0, rho, sigma, rho_f_factor, ctl, w.thinv, diag ? 1 : 0);
+  const bool full = NR == NC && d.nx + d.m == NR;
+  if (diag) {
+    if (full)
+      launch_factor_row_k<R, NC, NR, true, NR == NC>(s, d, w, q, rho, sigma, rho_f_factor, ctl);
+    else
+      launch_factor_row_k<R, NC, NR, true, false>(s, d, w, q, rho, sigma, rho_f_factor, ctl);
+  } else {
+    if (full)
+      launch_factor_row_k<R, NC, NR, false, NR == NC>(s, d, w, q, rho, sigma, rho_f_factor, ctl);
+    else
+      launch_factor_row_k<R, NC, NR, false, false>(s, d, w, q, rho, sigma, rho_f_factor, ctl);
+  }
 }
 
 // fp64 factorization from the stage records (explicit-integrator structure):
@@ -499,6 +535,7 @@ int admm_direct_impl(hipStream_t s, const tmpc_dims* dims, const tmpc_qp* qp,
   const int fp = factor_problems_per_wave(d.B, cfg->flags);
   const bool fgroups = (cfg->flags & TMPC_FLAG_FACTOR_GROUPS) != 0;
   const bool diag = (cfg->flags & TMPC_FLAG_DIAG_COST) != 0;
+  const bool const_g = (cfg->flags & TMPC_FLAG_CONST_G) != 0 && d.m > 0;
   // the streaming path works on records of width dr.n >= d.n (dummies past n)
   const Dims dr = stream_record_dims(d);
   int sp = stream_problems_per_wave(d.B, cfg->flags, stream_wide(dr) && dr.n == 9);
@@ -564,7 +601,7 @@ int admm_direct_impl(hipStream_t s, const tmpc_dims* dims, const tmpc_qp* qp,
     a.it_hi = bounds[c + 1];
     a.first_chunk = c == 0 ? 1 : 0;
     if (stream)
-      launch_stream<R>(s, stream_args<R>(a, w, dr, qr.A0, diag, sq), sp);
+      launch_stream<R>(s, stream_args<R>(a, w, dr, qr.A0, diag, sq), sp, const_g);
     else if (std_dyn)
       launch_chunk<R, true>(s, a);
     else

@@ -241,20 +241,29 @@ __device__ __forceinline__ void static_for_pivots(F&& f) {
   }
 }
 
-// NC in {6, 9, 16, 17}; NR bounds the stacked rows nx + m of a stage record.
-template <typename R, int NC, int NR>
+// NC in {6, 9, 16, 17}; NR bounds the stacked rows nx + m of a stage record;
+// DIAG: the D_t records hold the diagonal (RecGeom); FULL: nx + m == NR, so
+// every stacked row of a record is live (no per-row tests).
+//
+// Register budget (one wavefront per SIMD, 4 problems): the records stay in
+// the storage type R until a product reads them (fp64 conversions at the
+// use), the next stage's records are prefetched in R, and each lane writes
+// its own row of the packed inverse from registers (no index arithmetic, no
+// LDS re-read).  The arithmetic, and its order, is that of the symmetric
+// sweep described above.
+template <typename R, int NC, int NR, bool DIAG, bool FULL>
 __global__ __launch_bounds__(kWave, 1) void factor_row_kernel(Dims d, const R* __restrict__ am,
                                                               const R* __restrict__ dm, const R* __restrict__ A0,
                                                               const R* __restrict__ rho, R sigma, R rho_f_factor,
-                                                              int32_t* __restrict__ ctl, R* __restrict__ thinv,
-                                                              int diag) {
+                                                              int32_t* __restrict__ ctl, R* __restrict__ thinv) {
   using C = double;
   constexpr int W = kFacRow;
   constexpr int NL = NC < W ? NC : W;  // rows held by lanes
   constexpr bool IMP = NC > W;         // row 16 implied by symmetry
   constexpr int n = NC, PITCH = th_pitch(NC);
-  const int T = d.T, N = d.N, nx = d.nx, n0 = d.n0, m = d.m, B = d.B, nr = nx + m;
-  const RecGeom rg = rec_geom(d, diag != 0);
+  const int T = d.T, N = d.N, nx = d.nx, n0 = d.n0, m = d.m, B = d.B;
+  const int nr = FULL ? NR : nx + m;
+  const RecGeom rg = rec_geom(d, DIAG);
   const int tid = threadIdx.x, q = tid / W, i = tid - q * W;
   const int braw = blockIdx.x * (kWave / W) + q;
   const bool real = braw < B;
@@ -263,12 +272,11 @@ __global__ __launch_bounds__(kWave, 1) void factor_row_kernel(Dims d, const R* _
   const int ic = lrow ? i : 0;          // clamped row index for loads
   const int arow = min(ic, nr - 1);     // the M row read as the lane's A row (used for i < nx only)
   if (ctl != nullptr && __ballot(real && ctl[b * 4 + 2] != 0) == 0) return;  // nothing flagged here
-  __shared__ C sym[kWave / W][W][W + 1];  // the lane rows (and column 16) of each problem
-  __shared__ C d16s[kWave / W];            // Theta^{-1}[16][16] (n = 17)
+  __shared__ C sym[kWave / W][W][W + 1];  // the lane rows of each problem
   const C rho_i = (C)rho[b], rho_f = rho_i * (C)rho_f_factor, sig = (C)sigma;
 
-  // ---- stage records of the next stage, prefetched into registers ------------------
-  R pMc[NR], pM16[NR], pAr[NC], pD[NC], pD16 = R(0);
+  // ---- stage records of the next stage, prefetched into registers (type R) ----
+  R pMc[NR], pM16[NR], pAr[NC], pD[DIAG ? 1 : NC], pD16 = R(0);
   auto load = [&](int t) __attribute__((always_inline)) {
     const R* M = am + ((size_t)t * B + b) * rg.amp;
     const R* Dr = dm + ((size_t)t * B + b) * rg.dmp;
@@ -277,7 +285,7 @@ __global__ __launch_bounds__(kWave, 1) void factor_row_kernel(Dims d, const R* _
     // Schur values see
 #pragma unroll
     for (int r = 0; r < NR; ++r) {
-      if (r < nr) {
+      if (FULL || r < nr) {
         pMc[r] = M[r * n + ic];
         if (IMP) pM16[r] = M[r * n + (n - 1)];
       } else {
@@ -287,9 +295,7 @@ __global__ __launch_bounds__(kWave, 1) void factor_row_kernel(Dims d, const R* _
     }
 #pragma unroll
     for (int k = 0; k < NC; ++k) pAr[k] = M[arow * n + k];
-    if (diag) {
-#pragma unroll
-      for (int k = 0; k < NC; ++k) pD[k] = R(0);
+    if constexpr (DIAG) {
       pD[0] = lrow ? Dr[ic] : R(0);
       if (IMP) pD16 = Dr[n - 1];
     } else {
@@ -300,15 +306,20 @@ __global__ __launch_bounds__(kWave, 1) void factor_row_kernel(Dims d, const R* _
   };
   load(0);
 
-  C a[NC];   // row i of Theta_t, then of Theta_t^{-1}; a[16]: column 16 (n = 17)
-  C a16 = 0; // Theta[16][16] (n = 17)
-  C Mc[NR], M16[NR], Ar[NC];  // the stage's rows [A_t; G_t]: column i, column 16; row i of A_t
+  C a[NC];    // row i of Theta_t, then of Theta_t^{-1}; a[16]: column 16 (n = 17)
+  C a16 = 0;  // Theta[16][16] (n = 17)
+  R Mc[NR], M16[NR];  // the stage's rows [A_t; G_t]: column i, column 16
+  C Ar[NC];           // row i of A_t
 #pragma unroll
   for (int k = 0; k < NC; ++k) a[k] = C(0);
 #pragma unroll
-  for (int r = 0; r < NR; ++r) Mc[r] = M16[r] = C(0);
+  for (int r = 0; r < NR; ++r) Mc[r] = M16[r] = R(0);
 #pragma unroll
   for (int k = 0; k < NC; ++k) Ar[k] = C(0);
+  // this lane's row of the packed lower triangle starts at i (i + 1) / 2; the
+  // wavefront's problems are wb0 .. wb0 + wnp - 1
+  const int prow = (i * (i + 1)) >> 1;
+  const int wb0 = blockIdx.x * (kWave / W), wnp = min(kWave / W, B - wb0);
 
   for (int t = 0; t < T; ++t) {
     // Schur term rho_f^2 (A_{t-1} Theta_{t-1}^{-1} A_{t-1}^T)[i][s], s < nx, from
@@ -320,8 +331,8 @@ __global__ __launch_bounds__(kWave, 1) void factor_row_kernel(Dims d, const R* _
 #pragma unroll
       for (int s = 0; s < NC; ++s) {
         if (s < nx) {
-          const C y = fac_dot<NC>(a, Mc[s]);  // Y[i][s] = (Theta^{-1} A^T)[i][s]
-          sv[s] = fac_dot<NC>(Ar, y);         // sum_j A[i][j] Y[j][s]
+          const C y = fac_dot<NC>(a, (C)Mc[s]);  // Y[i][s] = (Theta^{-1} A^T)[i][s]
+          sv[s] = fac_dot<NC>(Ar, y);            // sum_j A[i][j] Y[j][s]
         }
       }
     }
@@ -337,21 +348,20 @@ __global__ __launch_bounds__(kWave, 1) void factor_row_kernel(Dims d, const R* _
       u[NC - 1] = fac_dot<NC>(Ar, a[NC - 1]) + Ar[NC - 1] * a16;
 #pragma unroll
       for (int s = 0; s < NC; ++s)
-        if (s < nx) sv[s] = fac_dot<NC>(u, Mc[s]) + u[NC - 1] * M16[s];
+        if (s < nx) sv[s] = fac_dot<NC>(u, (C)Mc[s]) + u[NC - 1] * (C)M16[s];
     }
 
     // this stage's records
-    C Dd[NC], D16 = C(0);
+    C Dd[DIAG ? 1 : NC], D16 = C(0);
 #pragma unroll
     for (int r = 0; r < NR; ++r) {
-      Mc[r] = (C)pMc[r];
-      if (IMP) M16[r] = (C)pM16[r];
+      Mc[r] = pMc[r];
+      if (IMP) M16[r] = pM16[r];
     }
 #pragma unroll
-    for (int k = 0; k < NC; ++k) {
-      Ar[k] = (C)pAr[k];
-      Dd[k] = (C)pD[k];
-    }
+    for (int k = 0; k < NC; ++k) Ar[k] = (C)pAr[k];
+#pragma unroll
+    for (int k = 0; k < (DIAG ? 1 : NC); ++k) Dd[k] = (C)pD[k];
     if (IMP) D16 = (C)pD16;
     if (t + 1 < T) load(t + 1);
 
@@ -359,23 +369,25 @@ __global__ __launch_bounds__(kWave, 1) void factor_row_kernel(Dims d, const R* _
     // records), sigma and rho_f A_plus^T A_plus = rho_f diag(I_nx, 0) in one
     int ii = i;  // the comparisons with the lane's row index are made here
     __asm__ volatile("" : "+v"(ii));
-    const C dgl = (diag ? Dd[0] : C(0)) + sig + ((t > 0 && ii < nx) ? rho_f : C(0));
+    const C dgl = (DIAG ? Dd[0] : C(0)) + sig + ((t > 0 && ii < nx) ? rho_f : C(0));
 #pragma unroll
     for (int k = 0; k < NC; ++k) {
-      const C off = diag ? C(0) : Dd[k];
+      const C off = DIAG ? C(0) : Dd[DIAG ? 0 : k];
       a[k] = lrow ? (k == ii ? off + dgl : off) : C(0);
     }
     if (IMP) a16 = D16 + sig;
     const int r0 = t < N ? 0 : nx;  // the last stage has no dynamics rows
 #pragma unroll
     for (int r = 0; r < NR; ++r) {
-      if (r >= r0 && r < nr) {
+      if (r >= r0 && (FULL || r < nr)) {
         const C w = r < nx ? rho_f : rho_i;
-        const C s = w * Mc[r];
-        fac_axpy<NC>(a, Mc[r], s);
+        const C mc = (C)Mc[r];
+        const C s = w * mc;
+        fac_axpy<NC>(a, mc, s);
         if (IMP) {
-          a[NC - 1] += s * M16[r];
-          a16 += (w * M16[r]) * M16[r];
+          const C m16 = (C)M16[r];
+          a[NC - 1] += s * m16;
+          a16 += (w * m16) * m16;
         }
       }
     }
@@ -432,28 +444,25 @@ __global__ __launch_bounds__(kWave, 1) void factor_row_kernel(Dims d, const R* _
     // symmetric part of the lane block: row i averaged with column i
 #pragma unroll
     for (int k = 0; k < NL; ++k) sym[q][i][k] = a[k];
-    if (IMP) {
-      sym[q][i][NC - 1] = a[NC - 1];
-      if (i == 0) d16s[q] = a16;
-    }
     __syncthreads();
 #pragma unroll
     for (int k = 0; k < NL; ++k) a[k] = lrow ? C(0.5) * (a[k] + sym[q][k][i]) : C(0);
-    // the packed lower triangle, the problem's 16 lanes striding it (element e
-    // is (r, c) with r (r + 1) / 2 <= e, c = e - r (r + 1) / 2; the square
-    // root of 8 e + 1 < 1300 is exact at the row starts and at least 1/70 from
-    // the next odd integer elsewhere)
-    if (real) {
-      R* out = thinv + ((size_t)t * B + b) * PITCH;
-      for (int e = i; e < packed_size(NC); e += W) {
-        const int r = (int)((__builtin_sqrtf((float)(8 * e + 1)) - 1.0f) * 0.5f);
-        const int c = e - ((r * (r + 1)) >> 1);
-        C v;
-        if (IMP && r == NC - 1)
-          v = c == NC - 1 ? d16s[q] : sym[q][c][NC - 1];
-        else
-          v = C(0.5) * (sym[q][r][c] + sym[q][c][r]);
-        out[e] = (R)v;
+    // the packed lower triangle: lane i writes its row's entries k <= i (and,
+    // n = 17, entry i of row 16, which is its column-16 value, and lane 0 the
+    // last diagonal entry).  The stores go through a buffer resource whose
+    // range is the problem's block: a store that is off takes an offset past
+    // the range and is dropped (no exec-mask branches).
+    {
+      // one resource per wavefront (uniform): the blocks of its problems
+      const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
+          thinv + ((size_t)t * B + wb0) * PITCH, (short)0, (int)(wnp * PITCH * sizeof(R)), kBufferFlags);
+      const bool on = real && lrow;
+      const unsigned base = (unsigned)(q * PITCH);
+#pragma unroll
+      for (int k = 0; k < NL; ++k) buf_store((R)a[k], rs, on && k <= ii, base + (unsigned)(prow + k));
+      if (IMP) {
+        buf_store((R)a[NC - 1], rs, on, base + (unsigned)(packed_size(NC - 1) + ii));
+        buf_store((R)a16, rs, on && ii == 0, base + (unsigned)(packed_size(NC) - 1));
       }
     }
     __syncthreads();

@@ -25,6 +25,7 @@ class ObstacleOCP(LinearOCP):
                  obstacles_dimension: int = 3, **kw):
         """obstacles_centers (B, K, dim) or (K, dim); obstacles_radii (B, K) or (K,)."""
         super().__init__(**kw)
+        self.const_g = False  # the obstacle rows are relinearized per problem and stage
         c = as_tensor(obstacles_centers, self.dtype, self.device)
         r = as_tensor(obstacles_radii, self.dtype, self.device)
         self.obstacles_dimension = int(obstacles_dimension)

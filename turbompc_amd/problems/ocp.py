@@ -99,6 +99,9 @@ class QuadraticTrackingOCP:
             raise ValueError("use_slack_variables needs a positive slack_penalization_weight")
         self.std_dynamics = True  # explicit integrators: A_plus = [-I 0], E = 0
         self.diag_cost = True  # D_t = diag(2 w): per-variable tracking weights (cost_blocks)
+        # the inequality rows are the box rows: the same G_t for every stage and
+        # problem (inequality_blocks; subclasses with other rows clear it)
+        self.const_g = True
         self._static = None
         # values derived from the problem's tensors, built on first use (copies
         # made by with_weights, with_params, to and tile start empty); like the

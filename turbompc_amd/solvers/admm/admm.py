@@ -102,6 +102,7 @@ class ADMMSolver:
         std_dynamics: Optional[bool] = None,
         kernel_flags: int = 0,
         diag_cost: bool = False,
+        const_g: bool = False,
     ):
         admm_backend = AdmmBackend(admm_backend)
         if admm_backend not in (AdmmBackend.HIP_DIRECT, AdmmBackend.HIP_PCG):
@@ -127,6 +128,8 @@ class ADMMSolver:
         self._kernel_flags = int(kernel_flags)  # _lib.FLAG_GENERIC_KERNEL / flag_stream_p (cross-checks)
         if diag_cost:  # the caller vouches that every D_t is diagonal
             self._kernel_flags |= _lib.FLAG_DIAG_COST
+        if const_g:  # the caller vouches that G_t is the same for every stage and problem
+            self._kernel_flags |= _lib.FLAG_CONST_G
 
     # properties of the reference solver
     schur_solver = property(lambda self: self._schur_solver)

@@ -242,6 +242,7 @@ class TurboMPCSolver:
             use_slack=bool(getattr(program, "use_slack_variables", False)),
             std_dynamics=getattr(program, "std_dynamics", None),
             diag_cost=bool(getattr(program, "diag_cost", False)),
+            const_g=bool(getattr(program, "const_g", False)),
         )
 
     program = property(lambda self: self._program)
