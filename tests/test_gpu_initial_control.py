@@ -101,8 +101,7 @@ def _config5_u0(B, seed):
     return torch.tensor(rng.uniform(-0.005, 0.005, size=(B, 3)))  # inside |u| <= 0.01
 
 
-@pytest.mark.parametrize("kernel", ["rows", "generic"])
-def test_adjoint_kkt_with_initial_control_rows(kernel):
+def test_adjoint_kkt_with_initial_control_rows():
     B = 5
     prob = configs.config5(B=B, seed=1, constrain_initial_control=True, initial_control=_config5_u0(B, 1))
     qp = prob.build_qp(*prob.initial_guess())
@@ -113,11 +112,15 @@ def test_adjoint_kkt_with_initial_control_rows(kernel):
     G = qp.ineq.G * torch.tensor(sign).unsqueeze(-1)
     qb = qp.replace_ineq(G=G).replace_cost(q=torch.tensor(rng.standard_normal(tuple(qp.cost.q.shape))))
     dz_ref, mult_ref = oracle.adjoint_kkt(qb)
-    flags = _lib.FLAG_GENERIC_KERNEL if kernel == "generic" else 0
-    dz, mult = solve_backward_kkt_hip(qb.to(DEV, torch.float64), refine_steps=4, kernel_flags=flags)
-    e_dz, e_mult = rel_err(dz, dz_ref), rel_err(mult, mult_ref)
-    print(f"adjoint n0 = 9 ({kernel}): dz {e_dz:.2e}, multipliers {e_mult:.2e}")
-    assert e_dz < 1e-10 and e_mult < 1e-10
+    dzs = []
+    for kernel, flags in (("rows", 0), ("generic", _lib.FLAG_GENERIC_KERNEL)):
+        dz, mult = solve_backward_kkt_hip(qb.to(DEV, torch.float64), refine_steps=4, kernel_flags=flags)
+        e_dz, e_mult = rel_err(dz, dz_ref), rel_err(mult, mult_ref)
+        print(f"adjoint n0 = 9 ({kernel}): dz {e_dz:.2e}, multipliers {e_mult:.2e}")
+        assert e_dz < 1e-10 and e_mult < 1e-10
+        dzs.append(dz)
+    # stage blocks of 9 + 9 + 3 = 21 rows: the rows-in-lanes kernels ran, not the fallback
+    assert not torch.equal(dzs[0], dzs[1])
 
 
 def _params(K, n_sqp=1):
