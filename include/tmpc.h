@@ -115,6 +115,15 @@ typedef struct tmpc_state {
  * forward sweep (fewer bytes per iteration; the same products, so the same
  * iterates bit for bit).  Ignored by the other paths and shapes. */
 #define TMPC_FLAG_CONST_G 32u
+/* With TMPC_FLAG_CONST_G on the same n = 17 records (nx n <= 224, at most two
+ * problems per wavefront, a workspace of the size
+ * tmpc_admm_direct_workspace_bytes reports): the entries of A_minus_t that are
+ * the same, bit for bit, in every stage t < N of a problem (found on the
+ * device on every call; a rigid body's position and velocity columns, for
+ * example) stay in LDS, and both sweeps stream only the others (the same
+ * products, so the same iterates bit for bit).  Needs no promise from the
+ * caller; ignored by the other paths and shapes. */
+#define TMPC_FLAG_INVARIANT_A 64u
 
 typedef struct tmpc_admm_cfg {
   int32_t max_iter, check_every, adapt_rho_every, pcg_max_iter, use_slack;
@@ -151,7 +160,10 @@ int tmpc_fill_zero(hipStream_t stream, void* p, size_t bytes);
  * the reference's pure-JAX loop (turbompc/solvers/admm/admm.py:795-1049).
  * `in` is the warm start; `out` receives the final state (in == out allowed).
  * iters_out (B,) uint32 receives the ADMM iteration count per problem, with
- * TMPC_ITERS_NONFINITE set for a problem whose final state is not finite. */
+ * TMPC_ITERS_NONFINITE set for a problem whose final state is not finite.
+ * The workspace size reported covers every form; TMPC_FLAG_INVARIANT_A needs
+ * all of it, the rest of the solve runs in less (the stage records and the
+ * factor, without the compressed A_minus runs of that form). */
 size_t tmpc_admm_direct_workspace_bytes(int elem_bytes, const tmpc_dims* dims);
 int tmpc_admm_direct_f32(hipStream_t stream, const tmpc_dims* dims, const tmpc_qp* qp,
                          const tmpc_state* in, tmpc_state* out, uint32_t* iters_out,

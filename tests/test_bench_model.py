@@ -34,8 +34,18 @@ def test_multi_gpu_request_exits_with_message():
 
 
 def test_traffic_is_reported_only_for_the_profiled_shape():
-    # the committed --pmc summary profiled B = 4096, 20 ADMM iterations
-    assert bench.measured_traffic(4096, 20) == pytest.approx(13.687e9)
+    # the committed --pmc summary profiled B = 4096, 20 ADMM iterations: its
+    # figure is the one reported, and it lies within a factor of two of the
+    # algorithmic bytes of that launch (the kernel streams its records once
+    # or twice per iteration, never many times)
+    import re
+
+    text = bench.TRAFFIC_FILE.read_text()
+    want = float(re.search(r"^traffic_bytes_per_launch = (\d+)", text, re.M).group(1))
+    assert bench.measured_traffic(4096, 20) == want
+    _, F, I = bench.bytes_per_qp(41, 17, 13, 13, 4, 20, 4)
+    algorithmic = 20 * I * 4096
+    assert 0.5 * algorithmic < want < 2.0 * algorithmic
     assert bench.measured_traffic(2048, 20) is None
     assert bench.measured_traffic(4096, 10) is None
 

@@ -34,6 +34,8 @@
 // backward sweep), the rv record once (D_t too when the residuals are due),
 // the written state once.
 #pragma once
+#include <type_traits>
+
 #include "admm_direct.hpp"
 #include "stream_dpp.hpp"
 
@@ -188,7 +190,106 @@ struct StreamArgs {
   const uint8_t* act_in;
   uint8_t* act_out;
   R chk_tol;
+  // stage-invariant A_minus entries (AINV form): amask [kAinvWords], bit e set
+  // when entry e of the row-major nx x n block varies over the stages
+  // (ainv_mask_kernel); ac [N][B][nv] the nv varying entries of each
+  // problem's A_minus_t in row-major order, written by the first chunk
+  const uint32_t* amask;
+  R* ac;
 };
+
+// ---- stage-invariant A_minus entries ---------------------------------------------
+
+// Linearized dynamics often have entries that no linearization point changes
+// (a rigid body's Jacobian with respect to position and velocity: [I; 0] and
+// [dt I; I]); for the quadrotor 97 of the 221 entries of A_minus_t.  The AINV
+// form of the streaming kernel keeps those entries resident in LDS and
+// streams the others.  The mask is found on the device, bit for bit, on every
+// call: entry e is invariant when A_minus_t[e] == A_minus_0[e] as bit patterns
+// for every t < N of every problem, so the LDS slots hold exactly the values
+// the whole records would.
+constexpr int kAinvMaxEntries = 224;  // nx n of the AINV form (7 mask words)
+constexpr int kAinvWords = kAinvMaxEntries / 32;
+constexpr int kAinvWaves = 4;  // problems per workgroup of ainv_partial_kernel
+
+// Partial masks, one workgroup per kAinvWaves problems: wavefront w compares
+// problem b's stage records t = 1..N-1 with its stage 0, 16 bytes per lane
+// (bit patterns), and the workgroup's OR of the varying bits lands in
+// part[blockIdx.x][8], so that no global atomics are needed.
+template <typename R>
+__global__ __launch_bounds__(kWave * kAinvWaves) void ainv_partial_kernel(Dims d, const R* __restrict__ am,
+                                                                         uint32_t* __restrict__ part) {
+  using V = typename Vec16<R>::T;
+  constexpr int W = Vec16<R>::W, CQ = (kAinvMaxEntries / W + kWave - 1) / kWave, LPW = 32 / W;
+  typedef int i32x4 __attribute__((ext_vector_type(4)));
+  __shared__ uint32_t acc[8];
+  const int lane = threadIdx.x % kWave, wv = threadIdx.x / kWave;
+  if (threadIdx.x < 8) acc[threadIdx.x] = 0;
+  __syncthreads();
+  const int b = blockIdx.x * kAinvWaves + wv, ne = d.nx * d.n, B = d.B, N = d.N;
+  const int amp = rec_geom(d).amp;
+  uint32_t bits[CQ] = {};
+  if (b < B) {
+    i32x4 a0[CQ];
+#pragma unroll
+    for (int c = 0; c < CQ; ++c) {
+      const int q = c * kWave + lane;
+      a0[c] = q * W < ne ? __builtin_bit_cast(i32x4, *reinterpret_cast<const V*>(am + (size_t)b * amp + q * W))
+                         : i32x4{};
+    }
+#pragma unroll 4
+    for (int t = 1; t < N; ++t) {
+#pragma unroll
+      for (int c = 0; c < CQ; ++c) {
+        const int q = c * kWave + lane;
+        if (q * W < ne) {
+          const i32x4 v =
+              __builtin_bit_cast(i32x4, *reinterpret_cast<const V*>(am + ((size_t)t * B + b) * amp + q * W));
+#pragma unroll
+          for (int k = 0; k < W; ++k) {  // entry k of the chunk: 32-bit word(s) k * 4 / W ..
+            bool ne_k;
+            if constexpr (W == 4)
+              ne_k = v[k] != a0[c][k];
+            else
+              ne_k = v[2 * k] != a0[c][2 * k] || v[2 * k + 1] != a0[c][2 * k + 1];
+            bits[c] |= (uint32_t)ne_k << k;
+          }
+        }
+      }
+    }
+  }
+  // chunk q holds entries q W .. q W + W - 1: mask word q / LPW, bits W (q % LPW) ..
+#pragma unroll
+  for (int c = 0; c < CQ; ++c) {
+    const int q = c * kWave + lane;
+    uint32_t x = bits[c] << (W * (q % LPW));
+#pragma unroll
+    for (int sh = 1; sh < LPW; sh <<= 1) x |= (uint32_t)__shfl_xor((int)x, sh);
+    if (q % LPW == 0 && q / LPW < 8 && x) atomicOr(&acc[q / LPW], x);  // LDS
+  }
+  __syncthreads();
+  if (threadIdx.x < 8) part[blockIdx.x * 8 + threadIdx.x] = acc[threadIdx.x];
+}
+
+// The OR of the nparts partial masks into the mask words (one workgroup).
+__global__ __launch_bounds__(256) void ainv_reduce_kernel(const uint32_t* __restrict__ part, int nparts,
+                                                          uint32_t* __restrict__ mask) {
+  __shared__ uint32_t acc[8];
+  if (threadIdx.x < 8) acc[threadIdx.x] = 0;
+  __syncthreads();
+  const int w = threadIdx.x & 7;
+  uint32_t x = 0;
+  for (int p = threadIdx.x >> 3; p < nparts; p += 32) x |= part[p * 8 + w];
+  if (x) atomicOr(&acc[w], x);  // LDS
+  __syncthreads();
+  if (threadIdx.x < kAinvWords) mask[threadIdx.x] = acc[threadIdx.x];
+}
+
+// Position of the k-th set bit of x (k < popcount(x)).
+__device__ __forceinline__ int kth_set_bit(uint32_t x, int k) {
+  for (int j = 0; j < k; ++j) x &= x - 1;
+  return __builtin_ctz(x);
+}
 
 // ---- pack / unpack -----------------------------------------------------------
 
@@ -628,13 +729,26 @@ struct StreamOcc {
 // the caller, TMPC_FLAG_CONST_G).  The G rows of every M slot are written into
 // LDS once, from the wavefront's first record, and the backward sweep streams
 // only the A_minus rows of each stage record, as the forward sweep does.
-template <typename R, int NC, int P, int DPF, int NL = NC, int MM = kMaxStreamM, bool GRES = false>
+//
+// AINV (with GRES): the stage-invariant entries of A_minus (a.amask) are
+// written into every M slot from each problem's stage-0 record, and both
+// sweeps stream only the varying entries (a.ac), element by element: the
+// first chunk's gamma sweep, which stages the whole records anyway, writes
+// a.ac.  Outside those fills only varying positions of the slots' A_minus
+// rows are written, so the products read the same values as with whole
+// records; at stage N (A_minus_N = 0) the slots hold another stage's finite
+// entries, which meet zero vector entries only.
+template <typename R, int NC, int P, int DPF, int NL = NC, int MM = kMaxStreamM, bool GRES = false,
+          bool AINV = false>
 __global__ __launch_bounds__(kWave, StreamOcc<R>::waves) void admm_stream_kernel(StreamArgs<R> a) {
   static_assert(NL >= NC && NL <= kWave / P, "row lanes must fit a problem's group");
+  static_assert(!AINV || GRES, "the AINV form streams A_minus rows only (G rows resident)");
   using V = typename Vec16<R>::T;
   using K = StreamShape<R, NC, P, NL, MM>;
   constexpr int n = NC, PITCH = K::PITCH, W = K::W;
   constexpr int CH_TH = K::CH_TH, CH_AM = K::CH_AM, CH_RV = K::CH_RV;
+  // AINV: 16-byte chunks of a wavefront's compressed run per lane (P nx n <= P 224)
+  constexpr int CHD = (P * kAinvMaxEntries / W + kWave - 1) / kWave;
   extern __shared__ __align__(16) unsigned char smem_raw[];
   R* lds = reinterpret_cast<R*>(smem_raw);
   const Dims d = a.d;
@@ -706,10 +820,87 @@ __global__ __launch_bounds__(kWave, StreamOcc<R>::waves) void admm_stream_kernel
       fa_off[c] = pe < nprob ? (pe * amp + (e - pe * ca) * W) * (int)sizeof(R) : -1;
     }
   }
+  // AINV: a problem's compressed run holds its nv varying entries in
+  // row-major order, padded to nvp (a multiple of W) with copies of the last
+  // one; with no varying entry it holds entry 0 (invariant, so streaming it
+  // rewrites the value its slot position already holds).  Entry k has the
+  // row-major index of the k-th set bit of the mask.  Lane tid handles 16-byte
+  // chunks c * 64 + tid of the wavefront's run (nq chunks), clamped to the
+  // last chunk (lanes past the run load and store that chunk again: the same
+  // values to the same places); chunk rows past the run are skipped
+  // (wavefront-uniform).  The offsets of a chunk's W entries in an M slot are
+  // packed 16 bits each (< 2 amp < 2^16).
+  constexpr int APW = W / 2;  // registers of packed offsets per chunk
+  uint32_t adp[AINV ? CHD * APW : 1] = {};
+  int nv = 1;
+  if constexpr (AINV) {
+    uint32_t mw[kAinvWords];
+    int cnt_all = 0;
+#pragma unroll
+    for (int w = 0; w < kAinvWords; ++w) {
+      mw[w] = a.amask[w];
+      cnt_all += __popc(mw[w]);
+    }
+    nv = max(cnt_all, 1);
+    const int nvp_ = (nv + W - 1) / W * W, nq_ = nprob * nvp_ / W;
+#pragma unroll
+    for (int c = 0; c < CHD; ++c)
+#pragma unroll
+      for (int k = 0; k < W; ++k) {
+        const int el = min(c * kWave + tid, nq_ - 1) * W + k, pe = el / nvp_;
+        int kk = min(el - pe * nvp_, nv - 1), pos = 0;
+        bool found = false;
+#pragma unroll
+        for (int w = 0; w < kAinvWords; ++w) {
+          const int cnt = __popc(mw[w]);
+          if (!found && kk < cnt) {
+            pos = 32 * w + kth_set_bit(mw[w], kk);
+            found = true;
+          }
+          if (!found) kk -= cnt;
+        }
+        adp[c * APW + k / 2] |= (uint32_t)(pe * amp + pos) << (16 * (k & 1));
+      }
+  }
+  auto ad = [&](int c, int k) __attribute__((always_inline)) {
+    return (int)((adp[c * APW + k / 2] >> (16 * (k & 1))) & 0xFFFFu);
+  };
+  const int nvp = (nv + W - 1) / W * W;
+  const unsigned nq = (unsigned)(nprob * nvp / W);  // chunks in a wavefront's run (>= 1)
+  // one resource over the wavefront's compressed runs, stage t at byte offset
+  // t B nvp sizeof(R) (the host keeps N B nvp sizeof(R) below 2^31)
+  const __amdgpu_buffer_rsrc_t acr = __builtin_amdgcn_make_buffer_rsrc(
+      AINV ? const_cast<R*>(a.ac + (size_t)b0 * nvp) : const_cast<R*>(a.am), (short)0, 0x7FFFFFFF, kBufferFlags);
+  const unsigned sacb = (unsigned)(B * nvp * (int)sizeof(R));
+  // the varying entries of stage t < N into registers, and from registers
+  // into an M slot
+  auto ac_load = [&](V (&r)[AINV ? CHD : 1], int t) __attribute__((always_inline)) {
+    if constexpr (AINV) {
+#pragma unroll
+      for (int c = 0; c < CHD; ++c) {
+        if (c > 0 && nq <= (unsigned)(c * kWave)) break;
+        const int off = (int)(min((unsigned)(c * kWave + tid), nq - 1) * 16u);
+        r[c] = __builtin_bit_cast(V, __builtin_amdgcn_raw_buffer_load_b128(acr, off, (int)((unsigned)t * sacb), 0));
+      }
+    }
+  };
+  auto ac_store = [&](const V (&r)[AINV ? CHD : 1], R* slot) __attribute__((always_inline)) {
+    if constexpr (AINV) {
+#pragma unroll
+      for (int c = 0; c < CHD; ++c) {
+        if (c > 0 && nq <= (unsigned)(c * kWave)) break;
+#pragma unroll
+        for (int k = 0; k < W; ++k) slot[ad(c, k)] = r[c][k];
+      }
+    }
+  };
   // M runs of the backward sweep: the whole records, or (GRES) their A_minus
-  // rows only, through the same chunk map as the forward sweep
-  auto load_m = [&](V (&r)[CH_AM], int t) __attribute__((always_inline)) {
-    if constexpr (GRES) {
+  // rows only, through the same chunk map as the forward sweep, or (AINV) the
+  // varying entries of A_minus (none at stage N, whose slot keeps what it holds)
+  auto load_m = [&](V (&r)[AINV ? 1 : CH_AM], V (&rc)[AINV ? CHD : 1], int t) __attribute__((always_inline)) {
+    if constexpr (AINV) {
+      if (t < N) ac_load(rc, t);
+    } else if constexpr (GRES) {
       const __amdgpu_buffer_rsrc_t rs =
           __builtin_amdgcn_make_buffer_rsrc(const_cast<V*>(am_run(t)), (short)0, nch_am * 16, kBufferFlags);
 #pragma unroll
@@ -719,8 +910,12 @@ __global__ __launch_bounds__(kWave, StreamOcc<R>::waves) void admm_stream_kernel
       load_run<V, CH_AM>(r, am_run(t), nch_am);
     }
   };
-  auto store_m = [&](const V (&r)[CH_AM], R* slot) __attribute__((always_inline)) {
-    if constexpr (GRES) {
+  auto store_m = [&](const V (&r)[AINV ? 1 : CH_AM], const V (&rc)[AINV ? CHD : 1], R* slot, int t)
+                     __attribute__((always_inline)) {
+    (void)t;
+    if constexpr (AINV) {
+      if (t < N) ac_store(rc, slot);
+    } else if constexpr (GRES) {
       V* dst = reinterpret_cast<V*>(slot);
 #pragma unroll
       for (int c = 0; c < CH_AM; ++c) *(fa_off[c] >= 0 ? dst + (fa_off[c] >> 4) : spl) = r[c];
@@ -737,6 +932,9 @@ __global__ __launch_bounds__(kWave, StreamOcc<R>::waves) void admm_stream_kernel
   // GRES: the G rows of every M slot (slot s at L.am + s amp), from stage 0
   // of the wavefront's first problem; written again after each residual
   // reduction, whose scratch (from L.th) may reach into the slots
+  // AINV: also the A_minus rows of every M slot, from each problem's own
+  // stage-0 record (the invariant entries; the varying ones are overwritten
+  // before use)
   auto fill_g = [&]() __attribute__((always_inline)) {
     if constexpr (GRES) {
       const R* g0 = a.am + (size_t)b0 * amp + nx * n;
@@ -744,6 +942,13 @@ __global__ __launch_bounds__(kWave, StreamOcc<R>::waves) void admm_stream_kernel
       for (int e = tid; e < nslot * gl; e += kWave) {
         const int sl = e / gl, k = e - sl * gl;
         lds[L.am + sl * amp + nx * n + k] = g0[k];
+      }
+    }
+    if constexpr (AINV) {
+      const int al = nx * n, nslot = (DPF > 2 ? DPF : 2) * P;
+      for (int e = tid; e < nslot * al; e += kWave) {
+        const int sl = e / al, k = e - sl * al, pp = sl % P;
+        if (pp < nprob) lds[L.am + sl * amp + k] = a.am[(size_t)(b0 + pp) * amp + k];
       }
     }
   };
@@ -804,6 +1009,23 @@ __global__ __launch_bounds__(kWave, StreamOcc<R>::waves) void admm_stream_kernel
           if (fochk) store_run<V, CH_TH>(r.dm, reinterpret_cast<V*>(dmS(j)), nch_dm, spl);
         },
         [&](int j, int t) {
+          if constexpr (AINV) {
+            // the first chunk writes the compressed runs from the staged records
+            if (a.first_chunk && t < N) {
+              const R* sl = amS(j);
+#pragma unroll
+              for (int c = 0; c < CHD; ++c) {
+                V v;
+#pragma unroll
+                for (int k = 0; k < W; ++k) v[k] = sl[ad(c, k)];
+                const unsigned q = c * kWave + tid;
+                typedef int i32x4 __attribute__((ext_vector_type(4)));
+                if (q < nq)
+                  __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(i32x4, v), acr, (int)(q * 16u),
+                                                         (int)((unsigned)t * sacb), 0);
+              }
+            }
+          }
           const R* mt = amS(j) + p * amp;
           const R* rv = rvS(j) + p * rvp;
           const bool crow = (dyn && t < N) || ineq;  // a live stacked constraint row
@@ -855,6 +1077,10 @@ __global__ __launch_bounds__(kWave, StreamOcc<R>::waves) void admm_stream_kernel
           scp = sct;
           lds_order();
         });
+    if constexpr (AINV) {  // the sweep staged whole records (stage N's A_minus rows are zero)
+      fill_g();
+      lds_order();
+    }
     if (fochk) {
       // group maxima (every lane of a group reduces its group: the result
       // decides whether the problem iterates), then the activity of the step
@@ -900,14 +1126,16 @@ __global__ __launch_bounds__(kWave, StreamOcc<R>::waves) void admm_stream_kernel
     // ---- forward sweep: w_t = Theta_t^{-1} (gamma_t + rho_f [A_minus_{t-1} w_{t-1}; 0])
     {
       struct FRegs {
-        V th[CH_TH], am[CH_AM];
+        V th[CH_TH], am[AINV ? 1 : CH_AM], ac[AINV ? CHD : 1];
       };
       R v = R(0);  // (A_minus_{t-1} w_{t-1})[i], i < nx
       run_sweep<DPF, FRegs>(
           T, true,
           [&](FRegs& r, int t) {
             load_run<V, CH_TH>(r.th, th_run(t), nch_th);
-            if (t < N) {  // the A_minus rows of M_t only
+            if constexpr (AINV) {
+              if (t < N) ac_load(r.ac, t);
+            } else if (t < N) {  // the A_minus rows of M_t only
               const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
                   const_cast<V*>(am_run(t)), (short)0, nch_am * 16, kBufferFlags);
 #pragma unroll
@@ -917,10 +1145,14 @@ __global__ __launch_bounds__(kWave, StreamOcc<R>::waves) void admm_stream_kernel
           },
           [&](FRegs& r, int j) {
             store_run<V, CH_TH>(r.th, reinterpret_cast<V*>(thS(j)), nch_th, spl);
-            V* dst = reinterpret_cast<V*>(amS(j));
+            if constexpr (AINV) {
+              ac_store(r.ac, amS(j));  // at stage N: stage N-1's entries, unused
+            } else {
+              V* dst = reinterpret_cast<V*>(amS(j));
 #pragma unroll
-            for (int c = 0; c < CH_AM; ++c)
-              *(fa_off[c] >= 0 ? dst + (fa_off[c] >> 4) : spl) = r.am[c];
+              for (int c = 0; c < CH_AM; ++c)
+                *(fa_off[c] >= 0 ? dst + (fa_off[c] >> 4) : spl) = r.am[c];
+            }
           },
           [&](int j, int t) {
             // lanes past n compute throwaway values in their own vector slots
@@ -959,7 +1191,7 @@ __global__ __launch_bounds__(kWave, StreamOcc<R>::waves) void admm_stream_kernel
       // while step t computes (two sets where the registers allow)
       constexpr int PFD = P <= 2 ? 2 : 1;
       struct BRegs {
-        V th[CH_TH], am[CH_AM], rv[CH_RV], dm[CH_TH];
+        V th[CH_TH], am[AINV ? 1 : CH_AM], rv[CH_RV], dm[CH_TH], ac[AINV ? CHD : 1];
       };
       BRegs ra, rb;
       auto amP = [&](int t) { return lds + L.am + (t & 1) * (P * amp); };
@@ -968,11 +1200,11 @@ __global__ __launch_bounds__(kWave, StreamOcc<R>::waves) void admm_stream_kernel
       R* dm_slot = dmS(0);
       // prologue: M_{T-1} into its slot; ra <- Theta^{-1}, M of T-2 and rv, D
       // of T-1 (step T-1); with two sets rb <- those of T-3 and T-2 (step T-2)
-      load_m(ra.am, T - 1);
-      store_m(ra.am, amP(T - 1));
+      load_m(ra.am, ra.ac, T - 1);
+      store_m(ra.am, ra.ac, amP(T - 1), T - 1);
       if (T >= 2) {
         load_run<V, CH_TH>(ra.th, th_run(T - 2), nch_th);
-        load_m(ra.am, T - 2);
+        load_m(ra.am, ra.ac, T - 2);
       }
       load_run<V, CH_RV>(ra.rv, rv_run(T - 1), nch_rv);
       if (chk) load_run<V, CH_TH>(ra.dm, dm_run(T - 1), nch_dm);
@@ -983,7 +1215,7 @@ __global__ __launch_bounds__(kWave, StreamOcc<R>::waves) void admm_stream_kernel
         }
         if (T >= 3) {
           load_run<V, CH_TH>(rb.th, th_run(T - 3), nch_th);
-          load_m(rb.am, T - 3);
+          load_m(rb.am, rb.ac, T - 3);
         }
       }
       R xa = i < n ? wgp[N * n + i] : R(0);  // xt_t for the coming step (xt_N = w_N)
@@ -1000,7 +1232,7 @@ __global__ __launch_bounds__(kWave, StreamOcc<R>::waves) void admm_stream_kernel
         // group's slot (never read as part of the vector).
         if (hasA) {
           store_run<V, CH_TH>(pr.th, reinterpret_cast<V*>(th_slot), nch_th, spl);
-          store_m(pr.am, amP(t - 1));
+          store_m(pr.am, pr.ac, amP(t - 1), t - 1);
         }
         store_run<V, CH_RV>(pr.rv, reinterpret_cast<V*>(rv_slot), nch_rv, spl);
         if (chk) store_run<V, CH_TH>(pr.dm, reinterpret_cast<V*>(dm_slot), nch_dm, spl);
@@ -1010,7 +1242,7 @@ __global__ __launch_bounds__(kWave, StreamOcc<R>::waves) void admm_stream_kernel
         // this set's next use is step t - PFD
         if (t >= PFD + 1) {
           load_run<V, CH_TH>(pr.th, th_run(t - PFD - 1), nch_th);
-          load_m(pr.am, t - PFD - 1);
+          load_m(pr.am, pr.ac, t - PFD - 1);
         }
         if (t >= PFD) {
           load_run<V, CH_RV>(pr.rv, rv_run(t - PFD), nch_rv);

@@ -114,16 +114,44 @@ size_t direct_ws_bytes(const Dims& d) {
          align_up(B * 4 * sizeof(int32_t)) + align_up(B * 8 * sizeof(R)) + stream_ws_bytes<R>(d);
 }
 
+// Shapes of the AINV form (stage-invariant A_minus entries resident in LDS,
+// admm_stream.hpp): the n = 17 records with G rows, nx n <= kAinvMaxEntries.
+// The compressed runs are addressed with 32-bit byte offsets.
+inline bool ainv_shape_ok(const Dims& dr, size_t elem_bytes) {
+  return dr.n == 17 && dr.m > 0 && !stream_wide(dr) && dr.nx * dr.n <= kAinvMaxEntries && stream_shape_ok(dr) &&
+         (size_t)dr.N * dr.B * up4(dr.nx * dr.n) * elem_bytes < (1ULL << 31);
+}
+
+// The AINV form's part of the workspace, after the rest: the compressed runs
+// [N][B][up4(nx n)] (at most; they hold the partial masks first) and the mask
+// words last.
+template <typename R>
+size_t ainv_ws_bytes(const Dims& d) {
+  const Dims r = stream_record_dims(d);
+  if (!ainv_shape_ok(r, sizeof(R))) return 0;
+  return align_up((size_t)d.N * d.B * up4(r.nx * r.n) * sizeof(R)) + align_up(kAinvWords * sizeof(uint32_t));
+}
+
+// What tmpc_admm_direct_workspace_bytes reports: room for every form.  A
+// workspace of at least direct_ws_bytes runs every problem; the AINV form
+// needs the whole size.
+template <typename R>
+size_t direct_ws_bytes_full(const Dims& d) {
+  return direct_ws_bytes<R>(d) + ainv_ws_bytes<R>(d);
+}
+
 template <typename R>
 struct DirectWs {
   R *thinv, *w, *gam, *res;
   int32_t* ctl;
   R *am, *rv, *dm;  // stage records of the streaming path
   R* a0p;           // A0 with rows of the records' width
+  R* ac;            // AINV: compressed A_minus runs (null without room)
+  uint32_t* amask;  // AINV: mask words
 };
 
 template <typename R>
-DirectWs<R> carve_direct(void* ws, const Dims& d) {
+DirectWs<R> carve_direct(void* ws, size_t wsb, const Dims& d) {
   Carver c{static_cast<char*>(ws)};
   DirectWs<R> w;
   const Dims r = stream_record_dims(d);
@@ -138,6 +166,12 @@ DirectWs<R> carve_direct(void* ws, const Dims& d) {
   w.rv = c.take<R>(T * B * g.rvp);
   w.dm = c.take<R>(T * B * th_pitch(r.n));
   w.a0p = c.take<R>(B * d.n0 * r.n);
+  w.ac = nullptr;
+  w.amask = nullptr;
+  if (ainv_shape_ok(r, sizeof(R)) && wsb >= direct_ws_bytes_full<R>(d)) {
+    w.ac = c.take<R>((size_t)d.N * B * up4(r.nx * r.n));
+    w.amask = c.take<uint32_t>(kAinvWords);
+  }
   return w;
 }
 
@@ -275,14 +309,15 @@ bool stream_ok(const Dims& d, int P, bool diag) {
   return (size_t)L.total * sizeof(R) <= kMaxLds;
 }
 
-template <typename R, int NC, int P, int NL = NC, int MM = kMaxStreamM, bool GRES = false>
+template <typename R, int NC, int P, int NL = NC, int MM = kMaxStreamM, bool GRES = false, bool AINV = false>
 void launch_stream_p(hipStream_t s, const StreamArgs<R>& a) {
   constexpr int DPF = stream_depth(NC);
   const StreamLayout L = stream_layout(a.d, P, DPF, a.diag != 0);
   const size_t smem = (size_t)L.total * sizeof(R);
-  lds_optin(admm_stream_kernel<R, NC, P, DPF, NL, MM, GRES>, smem);
+  lds_optin(admm_stream_kernel<R, NC, P, DPF, NL, MM, GRES, AINV>, smem);
   const int grid = (a.d.B + P - 1) / P;
-  hipLaunchKernelGGL((admm_stream_kernel<R, NC, P, DPF, NL, MM, GRES>), dim3(grid), dim3(kWave), smem, s, a);
+  hipLaunchKernelGGL((admm_stream_kernel<R, NC, P, DPF, NL, MM, GRES, AINV>), dim3(grid), dim3(kWave), smem, s,
+                     a);
 }
 
 // gres: G_t is the same for every stage and problem (TMPC_FLAG_CONST_G).  Its
@@ -290,19 +325,25 @@ void launch_stream_p(hipStream_t s, const StreamArgs<R>& a) {
 // n = 17 records with one or two problems per wavefront, where it pays: config
 // 3, 1.995 -> 1.924 ms per launch (G is 68 of the 292 words of a record); at
 // n = 9 in fp64 (config 5, 27 of 84 words) the scattered A-row stores cost
-// more than the bytes they save (25.05 -> 25.51 ms)
+// more than the bytes they save (25.05 -> 25.51 ms).  ainv (with gres, the
+// same shapes, ainv_shape_ok): the AINV form, the stage-invariant A_minus
+// entries resident as well (a.amask, a.ac set)
 template <typename R, int NC, int NL = NC, int MM = kMaxStreamM>
-void launch_stream_nc(hipStream_t s, const StreamArgs<R>& a, int P, bool gres) {
+void launch_stream_nc(hipStream_t s, const StreamArgs<R>& a, int P, bool gres, bool ainv) {
   constexpr bool kGres = NL == NC && NC == 17;
   switch (P) {
     case 1:
-      if (kGres && gres)
+      if (kGres && gres && ainv)
+        launch_stream_p<R, NC, 1, NL, MM, kGres, kGres>(s, a);
+      else if (kGres && gres)
         launch_stream_p<R, NC, 1, NL, MM, kGres>(s, a);
       else
         launch_stream_p<R, NC, 1, NL, MM>(s, a);
       break;
     case 2:
-      if (kGres && gres)
+      if (kGres && gres && ainv)
+        launch_stream_p<R, NC, 2, NL, MM, kGres, kGres>(s, a);
+      else if (kGres && gres)
         launch_stream_p<R, NC, 2, NL, MM, kGres>(s, a);
       else
         launch_stream_p<R, NC, 2, NL, MM>(s, a);
@@ -314,22 +355,22 @@ void launch_stream_nc(hipStream_t s, const StreamArgs<R>& a, int P, bool gres) {
 }
 
 template <typename R>
-void launch_stream(hipStream_t s, const StreamArgs<R>& a, int P, bool gres) {
+void launch_stream(hipStream_t s, const StreamArgs<R>& a, int P, bool gres, bool ainv) {
   switch (a.d.n) {
-    case 6: launch_stream_nc<R, 6>(s, a, P, gres); break;
+    case 6: launch_stream_nc<R, 6>(s, a, P, gres, false); break;
     case 9:
       if (stream_wide(a.d))
-        launch_stream_nc<R, 9, kWideRows, kWideMaxM>(s, a, P, gres);
+        launch_stream_nc<R, 9, kWideRows, kWideMaxM>(s, a, P, gres, false);
       else
-        launch_stream_nc<R, 9>(s, a, P, gres);
+        launch_stream_nc<R, 9>(s, a, P, gres, false);
       break;
     case 16:
       if (stream_wide(a.d))
-        launch_stream_nc<R, 16, kWide16Rows, kWide16MaxM>(s, a, P, gres);
+        launch_stream_nc<R, 16, kWide16Rows, kWide16MaxM>(s, a, P, gres, false);
       else
-        launch_stream_nc<R, 16>(s, a, P, gres);
+        launch_stream_nc<R, 16>(s, a, P, gres, false);
       break;
-    default: launch_stream_nc<R, 17>(s, a, P, gres); break;
+    default: launch_stream_nc<R, 17>(s, a, P, gres, ainv); break;
   }
 }
 
@@ -466,6 +507,8 @@ StreamArgs<R> stream_args(const AdmmArgs<R>& a, const DirectWs<R>& w, const Dims
   s.it_lo = a.it_lo;
   s.it_hi = a.it_hi;
   s.first_chunk = a.first_chunk;
+  s.amask = w.amask;
+  s.ac = w.ac;
   return s;
 }
 
@@ -505,7 +548,7 @@ int admm_direct_impl(hipStream_t s, const tmpc_dims* dims, const tmpc_qp* qp,
   if (!ws || wsb < direct_ws_bytes<R>(d)) return TMPC_EWORKSPACE;
   int st = copy_state<R>(s, d, in, out);
   if (st) return st;
-  const DirectWs<R> w = carve_direct<R>(ws, d);
+  const DirectWs<R> w = carve_direct<R>(ws, wsb, d);
   AdmmArgs<R> a;
   a.d = d;
   a.qp = to_qp<R>(qp);
@@ -542,6 +585,10 @@ int admm_direct_impl(hipStream_t s, const tmpc_dims* dims, const tmpc_qp* qp,
   if (stream_wide(dr) && (cfg->flags & TMPC_FLAG_STREAM_P(3)) == 0)
     sp = std::min(sp, kWave / stream_wide_rows(dr));  // the wide forms' groups are larger
   const bool stream = std_dyn && (cfg->flags & TMPC_FLAG_GENERIC_KERNEL) == 0 && stream_ok<R>(dr, sp, diag);
+  // the AINV form: asked for, with the resident G rows, at most two problems
+  // per wavefront, and the whole workspace
+  const bool ainv = stream && const_g && (cfg->flags & TMPC_FLAG_INVARIANT_A) != 0 && ainv_shape_ok(dr, sizeof(R)) && sp <= 2 &&
+                    w.ac != nullptr;
   const bool pad = dr.n != d.n;
   QPDev<R> qr = a.qp;  // the QP as the record kernels read it
   if (pad) qr.A0 = w.a0p;
@@ -589,6 +636,22 @@ int admm_direct_impl(hipStream_t s, const tmpc_dims* dims, const tmpc_qp* qp,
     st = launch_factor_qp<R>(s, d, a.qp, a.st.rho, a.sigma, a.rho_f_factor, nullptr, w.thinv);
   }
   if (st) return st;
+  if (ainv) {
+    // the stage-invariant entries of this call's A_minus rows: partial masks
+    // in the compressed-run region (written later by the streaming kernel),
+    // then their OR (kernels only, no memset, so the call can be captured)
+    if (d.N > 1) {
+      const int nparts = (d.B + kAinvWaves - 1) / kAinvWaves;
+      uint32_t* part = reinterpret_cast<uint32_t*>(w.ac);
+      hipLaunchKernelGGL((ainv_partial_kernel<R>), dim3((unsigned)nparts), dim3(kWave * kAinvWaves), 0, s, dr,
+                         (const R*)w.am, part);
+      hipLaunchKernelGGL(ainv_reduce_kernel, dim3(1), dim3(256), 0, s, (const uint32_t*)part, nparts, w.amask);
+    } else {
+      hipLaunchKernelGGL((fill_kernel<uint32_t>), dim3(1), dim3(256), 0, s, w.amask, (size_t)kAinvWords, 0u);
+    }
+    st = launch_status();
+    if (st) return st;
+  }
   const std::vector<int> bounds = chunk_bounds(cfg->max_iter, cfg->check_every, cfg->adapt_rho_every);
   if (g_iter_events[0] && hipEventRecord(g_iter_events[0], s) != hipSuccess) return TMPC_ELAUNCH;
   for (size_t c = 0; c + 1 < bounds.size(); ++c) {
@@ -601,7 +664,7 @@ int admm_direct_impl(hipStream_t s, const tmpc_dims* dims, const tmpc_qp* qp,
     a.it_hi = bounds[c + 1];
     a.first_chunk = c == 0 ? 1 : 0;
     if (stream)
-      launch_stream<R>(s, stream_args<R>(a, w, dr, qr.A0, diag, sq), sp, const_g);
+      launch_stream<R>(s, stream_args<R>(a, w, dr, qr.A0, diag, sq), sp, const_g, ainv);
     else if (std_dyn)
       launch_chunk<R, true>(s, a);
     else
@@ -653,7 +716,7 @@ int admm_direct_noalloc_impl(hipStream_t s, const tmpc_dims* dims, const tmpc_qp
   if (!dims_ok(dims)) return TMPC_EBADSHAPE;
   if (!cfg) return TMPC_EBADARG;
   if (cfg->flags & TMPC_FLAG_WARM_RECORDS) return TMPC_EBADARG;
-  const size_t need = direct_ws_bytes<R>(to_dims(dims));
+  const size_t need = direct_ws_bytes_full<R>(to_dims(dims));
   if (need > TMPC_NOALLOC_SCRATCH_BYTES) return TMPC_ESCRATCH;
   void* ws = nullptr;
   const int st = noalloc_scratch(s, &ws);
@@ -1278,7 +1341,7 @@ void tmpc_set_timing_events(hipEvent_t before, hipEvent_t after) {
 size_t tmpc_admm_direct_workspace_bytes(int elem_bytes, const tmpc_dims* dims) {
   if (!dims_ok(dims)) return 0;
   const Dims d = to_dims(dims);
-  return elem_bytes == 8 ? direct_ws_bytes<double>(d) : direct_ws_bytes<float>(d);
+  return elem_bytes == 8 ? direct_ws_bytes_full<double>(d) : direct_ws_bytes_full<float>(d);
 }
 
 int tmpc_admm_direct_f32(hipStream_t s, const tmpc_dims* dims, const tmpc_qp* qp, const tmpc_state* in,

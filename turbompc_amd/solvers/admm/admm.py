@@ -103,6 +103,7 @@ class ADMMSolver:
         kernel_flags: int = 0,
         diag_cost: bool = False,
         const_g: bool = False,
+        invariant_a: Optional[bool] = None,
     ):
         admm_backend = AdmmBackend(admm_backend)
         if admm_backend not in (AdmmBackend.HIP_DIRECT, AdmmBackend.HIP_PCG):
@@ -130,6 +131,10 @@ class ADMMSolver:
             self._kernel_flags |= _lib.FLAG_DIAG_COST
         if const_g:  # the caller vouches that G_t is the same for every stage and problem
             self._kernel_flags |= _lib.FLAG_CONST_G
+        # the stage-invariant A_minus entries stay resident (found on the
+        # device; exact, so on by default wherever the G rows are resident)
+        if const_g if invariant_a is None else invariant_a:
+            self._kernel_flags |= _lib.FLAG_INVARIANT_A
 
     # properties of the reference solver
     schur_solver = property(lambda self: self._schur_solver)
