@@ -178,7 +178,7 @@ def _c_abi_solve(qp, flags, full_workspace=True):
     sv = state_struct(*outs)
     iters = torch.zeros(B, dtype=torch.int32, device=DEV)
     nbytes = lib.tmpc_admm_direct_workspace_bytes(8, ctypes.byref(dims))
-    extra = -(-(T - 1) * B * (-(-nx * n // 4) * 4) * 8 // 256) * 256 + 256  # the AINV part: compressed runs, mask words
+    extra = -(-(T - 1) * (B + 1) * 256 * 8 // 256) * 256 + 256  # the AINV part: compressed runs, mask words
     size = nbytes if full_workspace else nbytes - extra
     ws = torch.zeros(nbytes, dtype=torch.uint8, device=DEV)
     st = lib.tmpc_admm_direct_f64(_lib.stream_handle(torch.device(DEV)), ctypes.byref(dims), ctypes.byref(cq),

@@ -820,17 +820,19 @@ __global__ __launch_bounds__(kWave, StreamOcc<R>::waves) void admm_stream_kernel
       fa_off[c] = pe < nprob ? (pe * amp + (e - pe * ca) * W) * (int)sizeof(R) : -1;
     }
   }
-  // AINV: a problem's compressed run holds its nv varying entries in
-  // row-major order, padded to nvp (a multiple of W) with copies of the last
-  // one; with no varying entry it holds entry 0 (invariant, so streaming it
-  // rewrites the value its slot position already holds).  Entry k has the
-  // row-major index of the k-th set bit of the mask.  Lane tid handles 16-byte
-  // chunks c * 64 + tid of the wavefront's run (nq chunks), clamped to the
-  // last chunk (lanes past the run load and store that chunk again: the same
-  // values to the same places); chunk rows past the run are skipped
-  // (wavefront-uniform).  The offsets of a chunk's W entries in an M slot are
+  // AINV: the varying entries of a wavefront's problems, problem by problem,
+  // each in row-major order (entry k of a problem has the row-major index of
+  // the k-th set bit of the mask; with no varying entry, entry 0, which is
+  // invariant, so streaming it rewrites the value its slot position already
+  // holds): nent = nprob nv entries.  They are stored in rows of 64 16-byte
+  // chunks (64 W entries): chunk c * 64 + tid holds entries
+  // (c W + k) 64 + tid, k < W, so that the k-th LDS store of a row covers 64
+  // consecutive entries (few bank conflicts).  Entries past nent repeat entry
+  // nent - 1 (the same value to the same place).  A wavefront's rows of a
+  // stage are nrow = ceil(P nv / 64 W) long; rows past them are skipped
+  // (wavefront-uniform).  The slot offsets of a lane's W entries per row are
   // packed 16 bits each (< 2 amp < 2^16).
-  constexpr int APW = W / 2;  // registers of packed offsets per chunk
+  constexpr int APW = W / 2;  // registers of packed offsets per row
   uint32_t adp[AINV ? CHD * APW : 1] = {};
   int nv = 1;
   if constexpr (AINV) {
@@ -842,13 +844,13 @@ __global__ __launch_bounds__(kWave, StreamOcc<R>::waves) void admm_stream_kernel
       cnt_all += __popc(mw[w]);
     }
     nv = max(cnt_all, 1);
-    const int nvp_ = (nv + W - 1) / W * W, nq_ = nprob * nvp_ / W;
+    const int nent = nprob * nv;
 #pragma unroll
     for (int c = 0; c < CHD; ++c)
 #pragma unroll
       for (int k = 0; k < W; ++k) {
-        const int el = min(c * kWave + tid, nq_ - 1) * W + k, pe = el / nvp_;
-        int kk = min(el - pe * nvp_, nv - 1), pos = 0;
+        const int el = min((c * W + k) * kWave + tid, nent - 1), pe = el / nv;
+        int kk = el - pe * nv, pos = 0;
         bool found = false;
 #pragma unroll
         for (int w = 0; w < kAinvWords; ++w) {
@@ -865,22 +867,23 @@ __global__ __launch_bounds__(kWave, StreamOcc<R>::waves) void admm_stream_kernel
   auto ad = [&](int c, int k) __attribute__((always_inline)) {
     return (int)((adp[c * APW + k / 2] >> (16 * (k & 1))) & 0xFFFFu);
   };
-  const int nvp = (nv + W - 1) / W * W;
-  const unsigned nq = (unsigned)(nprob * nvp / W);  // chunks in a wavefront's run (>= 1)
-  // one resource over the wavefront's compressed runs, stage t at byte offset
-  // t B nvp sizeof(R) (the host keeps N B nvp sizeof(R) below 2^31)
+  const int nrow = (P * nv + kWave * W - 1) / (kWave * W);
+  // one resource over the compressed runs [N][grid][nrow][64 chunks]: this
+  // wavefront's rows of stage t at byte offset t grid nrow 1024 (the host
+  // keeps the array below 2^31 bytes)
   const __amdgpu_buffer_rsrc_t acr = __builtin_amdgcn_make_buffer_rsrc(
-      AINV ? const_cast<R*>(a.ac + (size_t)b0 * nvp) : const_cast<R*>(a.am), (short)0, 0x7FFFFFFF, kBufferFlags);
-  const unsigned sacb = (unsigned)(B * nvp * (int)sizeof(R));
+      AINV ? const_cast<R*>(a.ac + (size_t)blockIdx.x * nrow * kWave * W) : const_cast<R*>(a.am), (short)0,
+      0x7FFFFFFF, kBufferFlags);
+  const unsigned sacb = gridDim.x * (unsigned)nrow * kWave * 16u;
   // the varying entries of stage t < N into registers, and from registers
   // into an M slot
   auto ac_load = [&](V (&r)[AINV ? CHD : 1], int t) __attribute__((always_inline)) {
     if constexpr (AINV) {
 #pragma unroll
       for (int c = 0; c < CHD; ++c) {
-        if (c > 0 && nq <= (unsigned)(c * kWave)) break;
-        const int off = (int)(min((unsigned)(c * kWave + tid), nq - 1) * 16u);
-        r[c] = __builtin_bit_cast(V, __builtin_amdgcn_raw_buffer_load_b128(acr, off, (int)((unsigned)t * sacb), 0));
+        if (c > 0 && nrow <= c) break;
+        r[c] = __builtin_bit_cast(
+            V, __builtin_amdgcn_raw_buffer_load_b128(acr, (int)((c * kWave + tid) * 16u), (int)((unsigned)t * sacb), 0));
       }
     }
   };
@@ -888,7 +891,7 @@ __global__ __launch_bounds__(kWave, StreamOcc<R>::waves) void admm_stream_kernel
     if constexpr (AINV) {
 #pragma unroll
       for (int c = 0; c < CHD; ++c) {
-        if (c > 0 && nq <= (unsigned)(c * kWave)) break;
+        if (c > 0 && nrow <= c) break;
 #pragma unroll
         for (int k = 0; k < W; ++k) slot[ad(c, k)] = r[c][k];
       }
@@ -1015,14 +1018,13 @@ __global__ __launch_bounds__(kWave, StreamOcc<R>::waves) void admm_stream_kernel
               const R* sl = amS(j);
 #pragma unroll
               for (int c = 0; c < CHD; ++c) {
+                if (c > 0 && nrow <= c) break;
                 V v;
 #pragma unroll
                 for (int k = 0; k < W; ++k) v[k] = sl[ad(c, k)];
-                const unsigned q = c * kWave + tid;
                 typedef int i32x4 __attribute__((ext_vector_type(4)));
-                if (q < nq)
-                  __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(i32x4, v), acr, (int)(q * 16u),
-                                                         (int)((unsigned)t * sacb), 0);
+                __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(i32x4, v), acr, (int)((c * kWave + tid) * 16u),
+                                                       (int)((unsigned)t * sacb), 0);
               }
             }
           }

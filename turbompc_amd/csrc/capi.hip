@@ -116,20 +116,24 @@ size_t direct_ws_bytes(const Dims& d) {
 
 // Shapes of the AINV form (stage-invariant A_minus entries resident in LDS,
 // admm_stream.hpp): the n = 17 records with G rows, nx n <= kAinvMaxEntries.
-// The compressed runs are addressed with 32-bit byte offsets.
+// Bytes of the compressed runs: [N][waves][rows of 64 16-byte chunks], at
+// most 256 entries per problem with one or two problems per wavefront
+// (admm_stream.hpp), addressed with 32-bit byte offsets.
+inline size_t ainv_runs_bytes(const Dims& d, size_t elem_bytes) {
+  return (size_t)d.N * (d.B + 1) * 256 * elem_bytes;
+}
 inline bool ainv_shape_ok(const Dims& dr, size_t elem_bytes) {
   return dr.n == 17 && dr.m > 0 && !stream_wide(dr) && dr.nx * dr.n <= kAinvMaxEntries && stream_shape_ok(dr) &&
-         (size_t)dr.N * dr.B * up4(dr.nx * dr.n) * elem_bytes < (1ULL << 31);
+         ainv_runs_bytes(dr, elem_bytes) < (1ULL << 31);
 }
 
 // The AINV form's part of the workspace, after the rest: the compressed runs
-// [N][B][up4(nx n)] (at most; they hold the partial masks first) and the mask
-// words last.
+// (which hold the partial masks first) and the mask words last.
 template <typename R>
 size_t ainv_ws_bytes(const Dims& d) {
   const Dims r = stream_record_dims(d);
   if (!ainv_shape_ok(r, sizeof(R))) return 0;
-  return align_up((size_t)d.N * d.B * up4(r.nx * r.n) * sizeof(R)) + align_up(kAinvWords * sizeof(uint32_t));
+  return align_up(ainv_runs_bytes(r, sizeof(R))) + align_up(kAinvWords * sizeof(uint32_t));
 }
 
 // What tmpc_admm_direct_workspace_bytes reports: room for every form.  A
@@ -169,7 +173,7 @@ DirectWs<R> carve_direct(void* ws, size_t wsb, const Dims& d) {
   w.ac = nullptr;
   w.amask = nullptr;
   if (ainv_shape_ok(r, sizeof(R)) && wsb >= direct_ws_bytes_full<R>(d)) {
-    w.ac = c.take<R>((size_t)d.N * B * up4(r.nx * r.n));
+    w.ac = reinterpret_cast<R*>(c.take<char>(ainv_runs_bytes(r, sizeof(R))));
     w.amask = c.take<uint32_t>(kAinvWords);
   }
   return w;
