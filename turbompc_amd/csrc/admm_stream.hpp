@@ -747,8 +747,10 @@ __global__ __launch_bounds__(kWave, StreamOcc<R>::waves) void admm_stream_kernel
   using K = StreamShape<R, NC, P, NL, MM>;
   constexpr int n = NC, PITCH = K::PITCH, W = K::W;
   constexpr int CH_TH = K::CH_TH, CH_AM = K::CH_AM, CH_RV = K::CH_RV;
-  // AINV: 16-byte chunks of a wavefront's compressed run per lane (P nx n <= P 224)
-  constexpr int CHD = (P * kAinvMaxEntries / W + kWave - 1) / kWave;
+  // AINV: rows of 64 16-byte chunks of a wavefront's compressed run
+  // (P nx n entries, nx <= n - 1, nx n <= kAinvMaxEntries)
+  constexpr int AINV_MAX = (NC - 1) * NC < kAinvMaxEntries ? (NC - 1) * NC : kAinvMaxEntries;
+  constexpr int CHD = (P * AINV_MAX / W + kWave - 1) / kWave;
   extern __shared__ __align__(16) unsigned char smem_raw[];
   R* lds = reinterpret_cast<R*>(smem_raw);
   const Dims d = a.d;

@@ -116,6 +116,9 @@ size_t direct_ws_bytes(const Dims& d) {
 
 // Shapes of the AINV form (stage-invariant A_minus entries resident in LDS,
 // admm_stream.hpp): the n = 17 records with G rows, nx n <= kAinvMaxEntries.
+// (Built for n = 9 too, it streamed no A_minus entry of config 5's
+// time-invariant dynamics and took 25.04 against 24.84 ms per 200-iteration
+// launch: that kernel waits on its per-stage dependence chain, not on HBM.)
 // Bytes of the compressed runs: [N][waves][rows of 64 16-byte chunks], at
 // most 256 entries per problem with one or two problems per wavefront
 // (admm_stream.hpp), addressed with 32-bit byte offsets.
@@ -335,18 +338,19 @@ void launch_stream_p(hipStream_t s, const StreamArgs<R>& a) {
 template <typename R, int NC, int NL = NC, int MM = kMaxStreamM>
 void launch_stream_nc(hipStream_t s, const StreamArgs<R>& a, int P, bool gres, bool ainv) {
   constexpr bool kGres = NL == NC && NC == 17;
+  constexpr bool kAinv = kGres;
   switch (P) {
     case 1:
-      if (kGres && gres && ainv)
-        launch_stream_p<R, NC, 1, NL, MM, kGres, kGres>(s, a);
+      if (kAinv && gres && ainv)
+        launch_stream_p<R, NC, 1, NL, MM, kAinv, kAinv>(s, a);
       else if (kGres && gres)
         launch_stream_p<R, NC, 1, NL, MM, kGres>(s, a);
       else
         launch_stream_p<R, NC, 1, NL, MM>(s, a);
       break;
     case 2:
-      if (kGres && gres && ainv)
-        launch_stream_p<R, NC, 2, NL, MM, kGres, kGres>(s, a);
+      if (kAinv && gres && ainv)
+        launch_stream_p<R, NC, 2, NL, MM, kAinv, kAinv>(s, a);
       else if (kGres && gres)
         launch_stream_p<R, NC, 2, NL, MM, kGres>(s, a);
       else
