@@ -18,6 +18,10 @@ torch.func.jacfwd (tests/test_oracle_adjoint_quadrotor.py); the obstacle rows
 against central differences of g, known answers on the sphere and the exactness
 of the linearization at its own point, and their Hessian against differences
 of the gradient and its null direction (tests/test_oracle_obstacle.py).
+The rescaled QP (scale_qp_np) is pinned by the equivalence it must keep
+(tests/test_rescaling.py): solved to convergence, S times its solution is the
+unscaled QP's solution and its multipliers are the unscaled ones divided by
+the row scales.
 """
 from __future__ import annotations
 
@@ -159,8 +163,48 @@ def merit_linesearch(merit: Merit, states, controls, slacks, s_new, c_new, sl_ne
     return (states + a3 * ds, controls + a3 * du, slacks + a3 * dsl), alpha, mu
 
 
+def scale_qp_np(qp, state_diff, control_diff, ineq_row_scale):
+    """The QP in the scaled variables z_hat = z / [state_diff, control_diff]
+    of the reference's variable rescaling: the problem scales its constraint
+    rows (the initial rows by 1 / state_diff, then 1 / control_diff for u_0
+    rows, optimal_control_problem.py:944-956; the dynamics rows by
+    1 / state_diff, :1324-1332; the inequality rows by ineq_row_scale, :460-469,
+    obstacle_avoidance.py:42-47), then scale_qp_data scales the columns by
+    S = diag(state_diff, control_diff) (qp_data.py:178-211)."""
+    sd, cd = np.asarray(state_diff, dtype=np.float64), np.asarray(control_diff, dtype=np.float64)
+    sc = np.concatenate([sd, cd])
+    r0 = 1.0 / sc[: qp.eq.A0.shape[-2]]
+    rd, rg = 1.0 / sd, np.asarray(ineq_row_scale, dtype=np.float64)
+    return QPNS(
+        _ns(D=qp.cost.D * sc[:, None] * sc, E=qp.cost.E * sc[:, None] * sc, q=qp.cost.q * sc),
+        _ns(A0=qp.eq.A0 * r0[:, None] * sc, A_minus=qp.eq.A_minus * rd[:, None] * sc,
+            A_plus=qp.eq.A_plus * rd[:, None] * sc, c0=qp.eq.c0 * r0, c=qp.eq.c * rd),
+        _ns(G=qp.ineq.G * rg[:, None] * sc, l=qp.ineq.l * rg, u=qp.ineq.u * rg,
+            slack_penalization_weight=qp.ineq.slack_penalization_weight,
+            use_slack_variables=qp.ineq.use_slack_variables),
+    )
+
+
+def _scaled_merit_terms(eq, ineq, n0, scaling):
+    """The merit's residuals with the rows scaled as in scale_qp_np (the
+    reference's equality_constraints and inequality values with rescaling,
+    optimal_control_problem.py:892-910, :460-469)."""
+    sd, cd, rg = (np.asarray(a, dtype=np.float64) for a in scaling)
+    r0 = 1.0 / np.concatenate([sd, cd])[:n0]
+
+    def eq_s(s, u):
+        h = eq(s, u)
+        B = h.shape[0]
+        return np.concatenate([h[:, :n0] * r0, (h[:, n0:].reshape(B, -1, sd.size) / sd).reshape(B, -1)], axis=1)
+
+    def ineq_s(s, u):
+        g, lo, hi = ineq(s, u)
+        return g * rg, lo * rg, hi * rg
+    return eq_s, ineq_s
+
+
 def sqp_fixed(qp_at, x_guess, u_guess, *, n, m, n0, cfg: "ora.OracleCfg", rho0, n_sqp, dtype=np.float64,
-              nthreads=None, merit: "Merit | None" = None, linesearch=None, state0=None):
+              nthreads=None, merit: "Merit | None" = None, linesearch=None, state0=None, scaling=None):
     """Fixed-count SQP: qp_at(states, controls) -> QP; the ADMM state (including
     rho and the slack) carries across iterations; x starts at 0
     (turbompc_solver.py:1545-1551), or the solve is warm-started from the
@@ -170,10 +214,16 @@ def sqp_fixed(qp_at, x_guess, u_guess, *, n, m, n0, cfg: "ora.OracleCfg", rho0, 
     direction scaled by merit_linesearch (options `linesearch`, defaults
     LINESEARCH_DEFAULTS) and the next linearization is at the blended iterate;
     the ADMM state is carried unblended (turbompc_solver.py:1591-1604).
+    scaling: (state_diff, control_diff, ineq_row_scale) to solve each QP in
+    the rescaled variables (scale_qp_np) and unscale its solution
+    (turbompc_solver.py:1151-1155, :1582-1585); the ADMM state stays scaled.
     Returns (states, controls, admm_state), plus (slacks, alphas (B, n_sqp))
     with `merit`."""
     states, controls = x_guess.astype(np.float64), u_guess.astype(np.float64)
     B, T, nx = states.shape
+    qp_raw = qp_at
+    if scaling is not None:
+        qp_at = lambda s_, u_: scale_qp_np(qp_raw(s_, u_), *scaling)  # noqa: E731
     qp = qp_at(states, controls)
     if state0 is None:
         z0 = np.clip(np.zeros((B, T, m)), qp.ineq.l, qp.ineq.u)
@@ -188,6 +238,8 @@ def sqp_fixed(qp_at, x_guess, u_guess, *, n, m, n0, cfg: "ora.OracleCfg", rho0, 
         st, _, _ = ora.admm_solve(qp, st, cfg, schur="direct", dtype=dtype, nthreads=nthreads)
         st = ora.OracleState(*[np.asarray(a, dtype=np.float64) for a in st])
         s_new, c_new, sl_new = st.x_blocks[..., :nx], st.x_blocks[..., nx:], st.xi_g
+        if scaling is not None:
+            s_new, c_new = s_new * np.asarray(scaling[0]), c_new * np.asarray(scaling[1])
         if merit is not None:
             (s_new, c_new, sl_new), alphas[:, it], _ = merit_linesearch(merit, states, controls, slacks, s_new,
                                                                         c_new, sl_new, **ls)
@@ -230,7 +282,8 @@ def _no_cross_terms(static):
 
 
 def obstacle_sqp(static, x_guess, u_guess, *, A_minus, c, centers, radii, dim, cfg: "ora.OracleCfg", rho0, n_sqp,
-                 slack_weight=0.0, use_slack=False, dtype=np.float64, nthreads=None, linesearch=None, state0=None):
+                 slack_weight=0.0, use_slack=False, dtype=np.float64, nthreads=None, linesearch=None, state0=None,
+                 scaling=None):
     """static: numpy QP blocks that do not change (D, E, q, A0, c0, A_plus) and
     the box rows (G, l, u) (B,T,mb,n); the obstacle rows follow the box rows.
     linesearch: None, or a dict of line-search options (possibly empty) to run
@@ -250,8 +303,10 @@ def obstacle_sqp(static, x_guess, u_guess, *, A_minus, c, centers, radii, dim, c
             return (np.concatenate([g, go], axis=2), np.concatenate([lo, np.full_like(go, OBSTACLE_LOWER)], axis=2),
                     np.concatenate([hi, np.zeros_like(go)], axis=2))
 
-        merit = Merit(static["D"], static["q"], _linear_dynamics_residual(static, A_minus, c), ineq,
-                      slack_weight=slack_weight, use_slack=use_slack)
+        eq = _linear_dynamics_residual(static, A_minus, c)
+        if scaling is not None:
+            eq, ineq = _scaled_merit_terms(eq, ineq, static["A0"].shape[-2], scaling)
+        merit = Merit(static["D"], static["q"], eq, ineq, slack_weight=slack_weight, use_slack=use_slack)
 
     def qp_at(s, u):
         grad, lo, up = linearize_obstacles(s, centers, radii, dim)
@@ -266,7 +321,8 @@ def obstacle_sqp(static, x_guess, u_guess, *, A_minus, c, centers, radii, dim, c
         )
 
     return sqp_fixed(qp_at, x_guess, u_guess, n=n, m=mb + K, n0=static["A0"].shape[-2], cfg=cfg, rho0=rho0,
-                     n_sqp=n_sqp, dtype=dtype, nthreads=nthreads, merit=merit, linesearch=linesearch, state0=state0)
+                     n_sqp=n_sqp, dtype=dtype, nthreads=nthreads, merit=merit, linesearch=linesearch, state0=state0,
+                     scaling=scaling)
 
 
 def quadrotor_dynamics_residual(static, dt, params, nthreads=None):
@@ -282,7 +338,7 @@ def quadrotor_dynamics_residual(static, dt, params, nthreads=None):
 
 
 def quadrotor_sqp(static, x_guess, u_guess, *, dt, params, cfg: "ora.OracleCfg", rho0, n_sqp, dtype=np.float64,
-                  nthreads=None, linesearch=None, state0=None):
+                  nthreads=None, linesearch=None, state0=None, scaling=None):
     """static: dict of numpy QP blocks that do not change (D, E, q, A0, c0, A_plus, G, l, u).
     Returns (states, controls, admm_state); with `linesearch` (a dict of
     options, possibly empty) runs the merit line search and also returns
@@ -292,8 +348,10 @@ def quadrotor_sqp(static, x_guess, u_guess, *, dt, params, cfg: "ora.OracleCfg",
     merit = None
     if linesearch is not None:
         _no_cross_terms(static)
-        merit = Merit(static["D"], static["q"], quadrotor_dynamics_residual(static, dt, params, nthreads),
-                      _box_values(static))
+        eq, ineq = quadrotor_dynamics_residual(static, dt, params, nthreads), _box_values(static)
+        if scaling is not None:
+            eq, ineq = _scaled_merit_terms(eq, ineq, static["A0"].shape[-2], scaling)
+        merit = Merit(static["D"], static["q"], eq, ineq)
 
     def qp_at(s, u):
         Am, c = linearize_quadrotor(s, u, dt, params)
@@ -305,4 +363,5 @@ def quadrotor_sqp(static, x_guess, u_guess, *, dt, params, cfg: "ora.OracleCfg",
         )
 
     return sqp_fixed(qp_at, x_guess, u_guess, n=n, m=m, n0=static["A0"].shape[-2], cfg=cfg, rho0=rho0,
-                     n_sqp=n_sqp, dtype=dtype, nthreads=nthreads, merit=merit, linesearch=linesearch, state0=state0)
+                     n_sqp=n_sqp, dtype=dtype, nthreads=nthreads, merit=merit, linesearch=linesearch, state0=state0,
+                     scaling=scaling)

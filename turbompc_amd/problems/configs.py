@@ -67,7 +67,7 @@ def config2(B: int = 1024, seed: int = 0, **kw) -> LinearOCP:
 
 
 def config4(B: int = 16384, seed: int = 0, *, use_slack_variables: bool = False,
-            slack_penalization_weight: float = 100.0) -> ObstacleOCP:
+            slack_penalization_weight: float = 100.0, **kw) -> ObstacleOCP:
     """Start and goal on opposite faces of [-4, 4]^3 (random axis and side, the
     other coordinates uniform), at rest; 8 spheres per problem with centers
     U[-3, 3]^3 and radii U[0.3, 0.8], so the start and goal lie outside every
@@ -102,7 +102,7 @@ def config4(B: int = 16384, seed: int = 0, *, use_slack_variables: bool = False,
         control_bounds=(torch.full((nu,), -3.0, dtype=torch.float64), torch.full((nu,), 3.0, dtype=torch.float64)),
         initial_guess_final_state=f64(xg),
         obstacles_centers=f64(centers), obstacles_radii=f64(radii), obstacles_dimension=3,
-        use_slack_variables=use_slack_variables, slack_penalization_weight=slack_penalization_weight,
+        use_slack_variables=use_slack_variables, slack_penalization_weight=slack_penalization_weight, **kw,
     )
 
 

@@ -85,8 +85,11 @@ class ObstacleOCP(LinearOCP):
         g, lo, hi = super().inequality_values(states, controls)
         d = states[..., None, : self.obstacles_dimension] - self.centers[:, None]
         go = 1.0 - torch.linalg.norm(d, dim=-1) / (self.radii[:, None] + 0.001)
-        return (torch.cat([g, go], dim=-1), torch.cat([lo, torch.full_like(go, -1.0e9)], dim=-1),
-                torch.cat([hi, torch.zeros_like(go)], dim=-1))
+        glo, ghi = torch.full_like(go, -1.0e9), torch.zeros_like(go)
+        if self.rescale_optimization_variables:
+            ro = 1.0 / self.state_diff[: self.obstacles_dimension].mean()
+            go, glo, ghi = go * ro, glo * ro, ghi * ro
+        return torch.cat([g, go], dim=-1), torch.cat([lo, glo], dim=-1), torch.cat([hi, ghi], dim=-1)
 
     def inequality_lagrangian_hessian(self, states, controls, mus):
         """(B, T, n, n): sum_k mu_k d^2 g_k/dz^2 of the obstacle rows (box rows are linear)."""
@@ -106,12 +109,19 @@ class ObstacleOCP(LinearOCP):
         D, E, q, A0, c0, Ap, box = self._static
         Am, c = self.dynamics_blocks(states, controls)
         G, l, u = self.inequality_blocks_at(states, controls, box)
-        return QPData(
+        qp = QPData(
             cost=QPCostBlocks(D, E, q),
             eq=QPEqualityBlocks(A0, Am, Ap, c0, c),
             ineq=QPInequalityBlocks(G, l, u, torch.tensor(self.slack_penalization_weight, dtype=self.dtype),
                                     self.use_slack_variables),
         )
+        return self._rescale_qp(qp, self.num_box_constraints) if self.rescale_optimization_variables else qp
+
+    def inequality_row_scale(self):
+        """Box rows as the base class; each obstacle row by 1 / the mean scale of
+        the position coordinates (obstacle_avoidance.py:42-47)."""
+        ro = 1.0 / self.state_diff[: self.obstacles_dimension].mean()
+        return torch.cat([self.box_row_scale(), ro.expand(self.num_obstacles)])
 
 
 __all__ = ["ObstacleOCP"]

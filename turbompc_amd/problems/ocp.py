@@ -24,7 +24,7 @@ from typing import Dict, Optional, Tuple
 
 import torch
 
-from ..solvers.qp_data import QPCostBlocks, QPData, QPEqualityBlocks, QPInequalityBlocks
+from ..solvers.qp_data import QPCostBlocks, QPData, QPEqualityBlocks, QPInequalityBlocks, scale_qp_data
 
 BOUND_INF = 1.0e6
 
@@ -60,6 +60,11 @@ class QuadraticTrackingOCP:
         slack_penalization_weight: float = 0.0,
         constrain_initial_control: bool = False,
         initial_control: Optional[torch.Tensor] = None,  # (B, nu), with constrain_initial_control
+        rescale_optimization_variables: bool = False,
+        state_rescaling_min: Optional[torch.Tensor] = None,  # (nx,), with rescale_optimization_variables
+        state_rescaling_max: Optional[torch.Tensor] = None,
+        control_rescaling_min: Optional[torch.Tensor] = None,  # (nu,)
+        control_rescaling_max: Optional[torch.Tensor] = None,
         dtype: torch.dtype = torch.float64,
         device="cpu",
     ):
@@ -97,6 +102,26 @@ class QuadraticTrackingOCP:
                    else torch.zeros((self.B, nu), dtype=dtype, device=self.device))
         if self.use_slack_variables and not self.slack_penalization_weight > 0.0:
             raise ValueError("use_slack_variables needs a positive slack_penalization_weight")
+        # variable rescaling (optimal_control_problem.py:170-171, :284-349): the
+        # QP is solved in x / state_diff, u / control_diff with its constraint
+        # rows scaled to match; state_diff = (max - min) / 2
+        self.rescale_optimization_variables = bool(rescale_optimization_variables)
+        if self.rescale_optimization_variables:
+            lims = {"state_rescaling_min": (state_rescaling_min, nx), "state_rescaling_max": (state_rescaling_max, nx),
+                    "control_rescaling_min": (control_rescaling_min, nu),
+                    "control_rescaling_max": (control_rescaling_max, nu)}
+            for name, (v, k) in lims.items():
+                if v is None:
+                    raise ValueError(f"{name} must be provided when rescale_optimization_variables is True")
+                if tuple(torch.as_tensor(v).shape) != (k,):
+                    raise ValueError(f"{name} must have shape ({k},), got {tuple(torch.as_tensor(v).shape)}")
+            self.state_diff = (cv(state_rescaling_max) - cv(state_rescaling_min)) / 2.0
+            self.control_diff = (cv(control_rescaling_max) - cv(control_rescaling_min)) / 2.0
+            if not (bool(torch.all(self.state_diff > 0)) and bool(torch.all(self.control_diff > 0))):
+                raise ValueError("the rescaling ranges must satisfy max > min")
+        else:
+            self.state_diff = torch.ones(nx, dtype=dtype, device=self.device)
+            self.control_diff = torch.ones(nu, dtype=dtype, device=self.device)
         self.std_dynamics = True  # explicit integrators: A_plus = [-I 0], E = 0
         self.diag_cost = True  # D_t = diag(2 w): per-variable tracking weights (cost_blocks)
         # the inequality rows are the box rows: the same G_t for every stage and
@@ -233,11 +258,16 @@ class QuadraticTrackingOCP:
     def equality_residuals(self, states, controls):
         """(B, T nx [+ nu]) flattened as the reference's equality_constraints
         (optimal_control_problem.py:841-912): x_0 - x0, then f(x_t, u_t) -
-        x_{t+1}, then u_0 - u0 with constrain_initial_control."""
+        x_{t+1}, then u_0 - u0 with constrain_initial_control; with rescaling
+        the rows are divided by state_diff (control_diff for u_0)."""
         x0 = (states[:, 0] - self.x0).unsqueeze(1)
-        h = torch.cat([x0, self.next_states(states, controls) - states[:, 1:]], dim=1).flatten(1)
+        h = torch.cat([x0, self.next_states(states, controls) - states[:, 1:]], dim=1)
+        if self.rescale_optimization_variables:
+            h = h / self.state_diff
+        h = h.flatten(1)
         if self.constrain_initial_control:
-            h = torch.cat([h, controls[:, 0] - self.u0], dim=1)
+            hu = controls[:, 0] - self.u0
+            h = torch.cat([h, hu / self.control_diff if self.rescale_optimization_variables else hu], dim=1)
         return h
 
     def inequality_values(self, states, controls):
@@ -245,7 +275,11 @@ class QuadraticTrackingOCP:
         bounds (step_inequality_constraints, :413-471)."""
         _, idx, lo, hi = self._box_rows()
         g = torch.cat([states, controls], dim=-1).index_select(-1, idx)
-        return g, lo.expand_as(g), hi.expand_as(g)
+        lo, hi = lo.expand_as(g), hi.expand_as(g)
+        if self.rescale_optimization_variables:  # rows divided by their variable's scale (:460-469)
+            r = self.box_row_scale()
+            g, lo, hi = g * r, lo * r, hi * r
+        return g, lo, hi
 
     # -------------------------------------------------------- parameters ----
     WEIGHT_KEYS = (
@@ -316,8 +350,59 @@ class QuadraticTrackingOCP:
             self.WEIGHT_KEYS[2]: -2.0 * ex[:, -1] * dx_states[:, -1],
         }
 
+    # ------------------------------------------------------------ rescaling ----
+    def scale_states_controls(self, states, controls):
+        """x / state_diff, u / control_diff with rescaling, else unchanged
+        (scale_states_controls, optimal_control_problem.py:327-336)."""
+        if not self.rescale_optimization_variables:
+            return states, controls
+        return states / self.state_diff, controls / self.control_diff
+
+    def unscale_states_controls(self, states, controls):
+        """The inverse of scale_states_controls (:338-349)."""
+        if not self.rescale_optimization_variables:
+            return states, controls
+        return states * self.state_diff, controls * self.control_diff
+
+    def box_row_scale(self):
+        """(m_box,) 1 / the scale of the variable each box row bounds."""
+        _, idx, _, _ = self._box_rows()
+        return 1.0 / torch.cat([self.state_diff, self.control_diff]).index_select(0, idx)
+
+    def inequality_row_scale(self):
+        """(m,) the factors the inequality rows are multiplied by with rescaling."""
+        return self.box_row_scale()
+
+    def _rescale_qp(self, qp: QPData, num_selector_rows: int) -> QPData:
+        """The QP in scaled variables: its rows scaled as the problem scales
+        its constraints (initial rows by 1 / state_diff and 1 / control_diff,
+        dynamics rows by 1 / state_diff, :944-956, :1324-1332; inequality rows
+        by inequality_row_scale), then its columns by scale_qp_data
+        (turbompc_solver.py:1151-1155).  A0 = [I 0], A_plus = [-I 0] and the box
+        selector rows come out of the two scalings as they went in (r_i s_i = 1
+        for the variable they select), so they are kept exact."""
+        sd, cd = self.state_diff, self.control_diff
+        r0 = 1.0 / torch.cat([sd, cd]) if self.constrain_initial_control else 1.0 / sd
+        rd, rg = 1.0 / sd, self.inequality_row_scale()
+        eq = QPEqualityBlocks(qp.eq.A0 * r0[:, None], qp.eq.A_minus * rd[:, None], qp.eq.A_plus * rd[:, None],
+                              qp.eq.c0 * r0, qp.eq.c * rd)
+        ineq = QPInequalityBlocks(qp.ineq.G * rg[:, None], qp.ineq.l * rg, qp.ineq.u * rg,
+                                  qp.ineq.slack_penalization_weight, qp.ineq.use_slack_variables)
+        out = scale_qp_data(QPData(cost=qp.cost, eq=eq, ineq=ineq), sd, cd)
+        G = out.ineq.G
+        if num_selector_rows:
+            G = G.clone()
+            G[..., :num_selector_rows, :] = qp.ineq.G[..., :num_selector_rows, :]
+        return QPData(
+            cost=out.cost,
+            eq=QPEqualityBlocks(qp.eq.A0, out.eq.A_minus, qp.eq.A_plus, out.eq.c0, out.eq.c),
+            ineq=QPInequalityBlocks(G, out.ineq.l, out.ineq.u, out.ineq.slack_penalization_weight,
+                                    out.ineq.use_slack_variables),
+        )
+
     def build_qp(self, states: torch.Tensor, controls: torch.Tensor) -> QPData:
-        """QP of one SQP iteration (TurboMPCSolver._build_qp_data, turbompc_solver.py:1098-1156)."""
+        """QP of one SQP iteration (TurboMPCSolver._build_qp_data, turbompc_solver.py:1098-1156),
+        in the scaled variables with rescaling."""
         if self._static is None:
             D, E, q = self.cost_blocks()
             A0, c0 = self.initial_equality()
@@ -325,12 +410,13 @@ class QuadraticTrackingOCP:
             self._static = (D, E, q, A0, c0, self.a_plus(), G, l, u)
         D, E, q, A0, c0, Ap, G, l, u = self._static
         Am, c = self.dynamics_blocks(states, controls)
-        return QPData(
+        qp = QPData(
             cost=QPCostBlocks(D, E, q),
             eq=QPEqualityBlocks(A0, Am, Ap, c0, c),
             ineq=QPInequalityBlocks(G, l, u, torch.tensor(self.slack_penalization_weight, dtype=self.dtype),
                                     self.use_slack_variables),
         )
+        return self._rescale_qp(qp, G.shape[2]) if self.rescale_optimization_variables else qp
 
     def initial_guess(self) -> Tuple[torch.Tensor, torch.Tensor]:
         """Straight line from x0 to the final guess, +1e-6; controls 1e-6

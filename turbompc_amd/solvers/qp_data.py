@@ -113,6 +113,22 @@ def qpdata_from_ocp_blocks(D, E, q, A0, c0, As_next, Bs_next, As, Bs, c_dyn, ine
     )
 
 
+def scale_qp_data(qp: QPData, state_scale: torch.Tensor, control_scale: torch.Tensor) -> QPData:
+    """The QP in the variables z_hat with z = S z_hat, S = diag(state_scale,
+    control_scale) (scale_qp_data, qp_data.py:178-211): the cost blocks become
+    S D S, S E S and S q, and every constraint block's columns are scaled by S;
+    the right-hand sides and bounds are unchanged."""
+    s = torch.cat([torch.as_tensor(state_scale), torch.as_tensor(control_scale)]).to(qp.cost.D)
+    col = lambda a: a * s  # noqa: E731  (columns: the last axis)
+    sym = lambda a: a * s[:, None] * s  # noqa: E731
+    return QPData(
+        cost=QPCostBlocks(sym(qp.cost.D), sym(qp.cost.E), qp.cost.q * s),
+        eq=QPEqualityBlocks(col(qp.eq.A0), col(qp.eq.A_minus), col(qp.eq.A_plus), qp.eq.c0, qp.eq.c),
+        ineq=QPInequalityBlocks(col(qp.ineq.G), qp.ineq.l, qp.ineq.u, qp.ineq.slack_penalization_weight,
+                                qp.ineq.use_slack_variables),
+    )
+
+
 def is_std_dynamics(qp: QPData) -> bool:
     """True when every A_plus_t == [-I 0] and every E_t == 0 (explicit schemes
     without a control-rate cost, optimal_control_problem.py:1267-1272)."""

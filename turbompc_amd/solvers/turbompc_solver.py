@@ -364,17 +364,30 @@ class TurboMPCSolver:
         kkt = solution.kkt_state
         qp = program.build_qp(kkt.states, kkt.controls)
         D = qp.cost.D
+        # with rescaling the adjoint is solved in the forward QP's scaled
+        # variables: the same KKT system as the reference's (unscaled variables,
+        # scaled rows, turbompc_solver.py:1347-1349) with its columns scaled by
+        # S, so its multipliers are the reference's and its step is S^-1 dz
+        resc = self._rescaled(program)
+        if resc:
+            s = torch.cat([program.state_diff, program.control_diff]).to(D)
+            colsym = lambda H: H * s[:, None] * s  # noqa: E731
         if self._use_full_hessian:
             lambdas = solution.admm_state.y_f_dyn if solution.admm_state is not None else kkt.y_f[:, 1:]
+            if resc:  # multipliers of rows scaled by 1 / state_diff (:1372-1378)
+                lambdas = lambdas / program.state_diff.to(lambdas)
             H = program.dynamics_lagrangian_hessian(kkt.states, kkt.controls, lambdas)
             if H is not None:
-                D = D + H
+                D = D + (colsym(H) if resc else H)
             # mu = active * y_g (:1357-1385); None when every row is linear (bounds)
             y_g = solution.admm_state.y_g if solution.admm_state is not None else kkt.y_ineq
             active = (kkt.ineq_active_lower_idx | kkt.ineq_active_upper_idx).to(y_g.dtype)
-            Hg = program.inequality_lagrangian_hessian(kkt.states, kkt.controls, active * y_g)
+            mus = active * y_g
+            if resc:
+                mus = mus * program.inequality_row_scale().to(mus)
+            Hg = program.inequality_lagrangian_hessian(kkt.states, kkt.controls, mus)
             if Hg is not None:
-                D = D + Hg
+                D = D + (colsym(Hg) if resc else Hg)
         base = QPData(cost=QPCostBlocks(D, qp.cost.E, qp.cost.q), eq=qp.eq, ineq=qp.ineq)
         eq = QPEqualityBlocks(qp.eq.A0, qp.eq.A_minus, qp.eq.A_plus, torch.zeros_like(qp.eq.c0),
                               torch.zeros_like(qp.eq.c))
@@ -385,6 +398,8 @@ class TurboMPCSolver:
             sign = kkt.ineq_active_lower_idx.to(G.dtype) - kkt.ineq_active_upper_idx.to(G.dtype)
             G_active = G * sign.unsqueeze(-1)
         dl = pack_x(dl_dstates.to(D.dtype), dl_dcontrols.to(D.dtype))
+        if resc:  # the cost's linear term in the scaled variables
+            dl = dl * s
         if qp.ineq.use_slack_variables and G.shape[2] > 0:
             gamma = qp.ineq.slack_penalization_weight
             Gt = G_active.transpose(-1, -2)
@@ -429,9 +444,17 @@ class TurboMPCSolver:
             dL_dgamma = (sign * kkt.slack * active * g_dz).flatten(1).sum(dim=1)
         else:
             y_ineq_lin = mult[:, m_eq:]
-        # dL/dx0 and, with constrain_initial_control, dL/du0 (:765-770)
-        return _BackwardSolveResult(dxs, dus, y_eq_lin, y_ineq_lin, dL_dgamma, y_f0[:, :nx],
-                                    y_f0[:, nx:] if n0 > nx else None)
+        # dL/dx0 and, with constrain_initial_control, dL/du0 (:765-770); with
+        # rescaling the initial rows are x_0 / state_diff = x0 / state_diff
+        # (and u_0 / control_diff), so the cotangents are divided by the
+        # scales (:1007-1016), and the step returns to true units
+        dx0, du0 = y_f0[:, :nx], (y_f0[:, nx:] if n0 > nx else None)
+        if self._rescaled(program):
+            dxs, dus = program.unscale_states_controls(dxs, dus)
+            dx0 = dx0 / program.state_diff.to(dx0)
+            if du0 is not None:
+                du0 = du0 / program.control_diff.to(du0)
+        return _BackwardSolveResult(dxs, dus, y_eq_lin, y_ineq_lin, dL_dgamma, dx0, du0)
 
     # ------------------------------------------------------------ internals ----
     def _first_order_check(self, qp: QPData, states, controls, slacks, admm_state: ADMMState):
@@ -485,6 +508,31 @@ class TurboMPCSolver:
             lo, up = dl | (und & lo), du | (und & up)
         return KKTState(states, controls, admm_state.xi_g, y_f, y_ineq, lo, up)
 
+    @staticmethod
+    def _rescaled(program) -> bool:
+        return bool(getattr(program, "rescale_optimization_variables", False))
+
+    @staticmethod
+    def _to_qp(program, states, controls):
+        """An iterate in the QP's variables (scaled with rescaling, as
+        _first_order_check and _inequality_values_from_qp scale it,
+        turbompc_solver.py:1174, :1235)."""
+        if TurboMPCSolver._rescaled(program):
+            return program.scale_states_controls(states, controls)
+        return states, controls
+
+    @staticmethod
+    def _qp_x(program, states, controls):
+        return pack_x(*TurboMPCSolver._to_qp(program, states, controls))
+
+    @staticmethod
+    def _from_qp(program, states, controls):
+        """A QP solution's states and controls in true units (the unscaling
+        after ADMMSolver.solve, turbompc_solver.py:1582-1585)."""
+        if TurboMPCSolver._rescaled(program):
+            return program.unscale_states_controls(states, controls)
+        return states, controls
+
     def _solve_impl(self, program, states, controls, admm_state0: Optional[ADMMState] = None) -> TurboMPCSolution:
         """The SQP loop of turbompc_solver.py:1519-1760, batched with per-problem termination."""
         if (int(self._params["num_sqp_iteration_max"]) > 1 and self._forward_admm_backend == AdmmBackend.HIP_DIRECT
@@ -533,12 +581,14 @@ class TurboMPCSolver:
                 (states, controls), stats, admm_state = admm.solve(qp, admm_state, rho_bar=ap["rho"], alpha=alpha,
                                                                     slack_weight=sw, workspace=ws,
                                                                     donate_state=own_state)
+                states, controls = self._from_qp(program, states, controls)
             else:
                 # the state is the loop's own from here on: updated in place
                 warm = _warm_level(qp, prev)
                 (states, controls), stats, admm_state, (cv, e, i, g), act = admm.sqp_step(
                     qp, admm_state, active, tol, rho_bar=ap["rho"], alpha=alpha, slack_weight=sw, workspace=ws,
                     warm_records=warm is not None, warm_ineq=warm == "constraints", donate_state=True)
+                states, controls = self._from_qp(program, states, controls)
                 # the check belongs to the iterate committed at it - 1 (the
                 # records of a stopped problem stay zero, as in the reference)
                 if it == 1:
@@ -562,7 +612,7 @@ class TurboMPCSolver:
         # check after its final iteration): its record keeps the previous error
         # and G x at the QP it was solved on
         hist[2, last] = torch.where(active, conv, hist[2, last])
-        g_last = apply_G(qp, pack_x(states, controls))
+        g_last = apply_G(qp, self._qp_x(program, states, controls))
         g_c = g_last if g_c is None else torch.where(active[:, None, None], g_last, g_c)
         kkt = self._build_kkt_state(states, controls, admm_state, g_c, qp.ineq.l, qp.ineq.u)
         num_iter = ran.sum(dim=0, dtype=torch.int32)
@@ -618,6 +668,7 @@ class TurboMPCSolver:
             if it == 0:
                 (s_new, c_new), stats, adm_new = admm.solve(qp, admm_state, rho_bar=ap["rho"], alpha=alpha,
                                                             slack_weight=sw, workspace=ws, donate_state=own_state)
+                s_new, c_new = self._from_qp(program, s_new, c_new)
             else:
                 active = active & (conv > tol)
                 if tol > 0 and not bool(active.any()):
@@ -626,6 +677,7 @@ class TurboMPCSolver:
                 (s_new, c_new), stats, adm_new, _, _ = admm.sqp_step(
                     qp, admm_state, active, None, rho_bar=ap["rho"], alpha=alpha, slack_weight=sw, workspace=ws,
                     warm_records=warm is not None, warm_ineq=warm == "constraints", donate_state=True)
+                s_new, c_new = self._from_qp(program, s_new, c_new)
             sl_new = adm_new.xi_g
             if use_ls:
                 # the step (s_new, c_new, xi) - (states, controls, slacks) is
@@ -645,17 +697,18 @@ class TurboMPCSolver:
                 prev = qp
                 qp = program.build_qp(states, controls)
                 if by_step:
-                    g = apply_G(qp, pack_x(states, controls))
+                    g = apply_G(qp, self._qp_x(program, states, controls))
                 else:
-                    c_err, e_err, i_err, g = self._first_order_check(qp, states, controls, slacks, adm_new)
+                    c_err, e_err, i_err, g = self._first_order_check(
+                        qp, *self._to_qp(program, states, controls), slacks, adm_new)
             elif by_step:
-                g = apply_G(qp, pack_x(s_new, c_new))
+                g = apply_G(qp, self._qp_x(program, s_new, c_new))
                 states, controls, slacks = sel(s_new, states), sel(c_new, controls), sel(sl_new, slacks)
             else:
                 # the last iterate is not checked: its record keeps the previous
                 # error, and G x at the QP it was solved on
                 c_err, e_err, i_err = conv, torch.zeros_like(conv), torch.zeros_like(conv)
-                g = apply_G(qp, pack_x(s_new, c_new))
+                g = apply_G(qp, self._qp_x(program, s_new, c_new))
                 states, controls, slacks = sel(s_new, states), sel(c_new, controls), sel(sl_new, slacks)
             admm_state = adm_new
             if use_ls:
@@ -715,6 +768,7 @@ class TurboMPCSolver:
             all_active = it == 0 or bool(active.all())
             (s_new, c_new), stats, adm_new = admm.solve(qp, admm_state, rho_bar=ap["rho"], alpha=alpha,
                                                         slack_weight=qp.ineq.slack_penalization_weight)
+            s_new, c_new = self._from_qp(program, s_new, c_new)
             sl_new = adm_new.xi_g
             if use_ls:
                 # the step (s_new, c_new, sl_new) - (states, controls, slacks) is
@@ -729,14 +783,15 @@ class TurboMPCSolver:
                     step = step + (sl_new - slacks).abs().flatten(1).amax(dim=1)
             if self._convergence_criterion == "first_order" and it + 1 < max_iter:
                 qp_next = program.build_qp(s_new, c_new)
-                c_new_err, e_err, i_err, g = self._first_order_check(qp_next, s_new, c_new, sl_new, adm_new)
+                c_new_err, e_err, i_err, g = self._first_order_check(
+                    qp_next, *self._to_qp(program, s_new, c_new), sl_new, adm_new)
             else:
                 rebuild = self._convergence_criterion == "step" and it + 1 < max_iter
                 qp_next = program.build_qp(s_new, c_new) if rebuild else qp
                 c_new_err = step if (it == 0 or self._convergence_criterion == "step") else conv
                 e_err = torch.zeros_like(c_new_err)
                 i_err = torch.zeros_like(c_new_err)
-                g = apply_G(qp_next, pack_x(s_new, c_new))
+                g = apply_G(qp_next, self._qp_x(program, s_new, c_new))
             # commit where active (vmapped while_loop semantics)
             if all_active:
                 sel = lambda a, b: a  # noqa: E731
