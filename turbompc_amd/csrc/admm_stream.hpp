@@ -293,18 +293,28 @@ __device__ __forceinline__ int kth_set_bit(uint32_t x, int k) {
 
 // ---- pack / unpack -----------------------------------------------------------
 
-// One 64-lane block per (problem, stage).  The QP and state arrays have rows
-// of d.nq entries, the records d.n >= d.nq: variables nq..n-1 are dummies
-// with D = 1 on their diagonal and zero everywhere else (x, q, and their
-// columns of A_minus, G and A0), so theta keeps them decoupled at 1 + sigma
-// and the iteration keeps them at zero without touching any other value.
-// With A0p, block (b, 0) also writes the problem's A0 with rows of n entries.
+// One wavefront per (problem, stage), kPackWaves problems of a stage per
+// workgroup (adjacent records; one-wavefront workgroups: 215 against 192 us
+// at config 3).  Gathering all of a lane's values before its stores, over one
+// index space for the three records, was slower (319 us): every unrolled
+// value then runs the code of all three records.  The QP and state arrays
+// have rows of d.nq entries, the records d.n >= d.nq: variables nq..n-1 are
+// dummies with D = 1 on their diagonal and zero everywhere else (x, q, and
+// their columns of A_minus, G and A0), so theta keeps them decoupled at
+// 1 + sigma and the iteration keeps them at zero without touching any other
+// value.  With A0p, the wavefront of (b, 0) also writes the problem's A0 with
+// rows of n entries.
+constexpr int kPackWaves = 4;
+
 template <typename R>
-__global__ __launch_bounds__(kWave) void stage_pack_kernel(Dims d, QPDev<R> qp, StateDev<R> st, R* __restrict__ am,
-                                                           R* __restrict__ rv, R* __restrict__ dm, int diag,
-                                                           R* __restrict__ A0p) {
-  const int b = blockIdx.x, t = blockIdx.y, tid = threadIdx.x;
+__global__ __launch_bounds__(kWave * kPackWaves) void stage_pack_kernel(Dims d, QPDev<R> qp, StateDev<R> st,
+                                                                        R* __restrict__ am, R* __restrict__ rv,
+                                                                        R* __restrict__ dm, int diag,
+                                                                        R* __restrict__ A0p) {
+  const int b = blockIdx.x * kPackWaves + (int)(threadIdx.x / kWave), t = blockIdx.y;
+  const int tid = (int)(threadIdx.x % kWave);
   const int B = d.B, T = d.T, N = d.N, n = d.n, nx = d.nx, m = d.m, nq = d.nq;
+  if (b >= B) return;  // the last workgroup's spare wavefronts (no barrier follows)
   const RecGeom g = rec_geom(d, diag != 0);
   const size_t bt = (size_t)b * T + t;
   {

@@ -635,8 +635,9 @@ int admm_direct_impl(hipStream_t s, const tmpc_dims* dims, const tmpc_qp* qp,
     if (st) return st;
     st = launch_factor_std<R>(s, dr, w, qr, a.st.rho, a.sigma, a.rho_f_factor, nullptr, fp, diag, fgroups);
   } else if (stream) {
-    hipLaunchKernelGGL((stage_pack_kernel<R>), dim3(d.B, d.T), dim3(kWave), 0, s, dr, a.qp, a.st, w.am, w.rv, w.dm,
-                       diag ? 1 : 0, pad ? w.a0p : (R*)nullptr);
+    hipLaunchKernelGGL((stage_pack_kernel<R>), dim3((unsigned)((d.B + kPackWaves - 1) / kPackWaves), (unsigned)d.T),
+                       dim3(kWave * kPackWaves), 0, s, dr, a.qp, a.st, w.am, w.rv, w.dm, diag ? 1 : 0,
+                       pad ? w.a0p : (R*)nullptr);
     st = launch_status();
     if (st) return st;
     st = launch_factor_std<R>(s, dr, w, qr, a.st.rho, a.sigma, a.rho_f_factor, nullptr, fp, diag, fgroups);

@@ -179,11 +179,15 @@ class ADMMSolver:
         slack_weight=0.0,
         workspace: Optional[torch.Tensor] = None,
         donate_state: bool = False,
+        iters_out: Optional[torch.Tensor] = None,
     ) -> Tuple[Tuple[torch.Tensor, torch.Tensor], ADMMStats, ADMMState]:
         """`workspace` (direct backend): a caller-owned workspace instead of the
         shared cached one (an SQP loop passes its own, see sqp_step).
         donate_state: admm_state0's buffers may be updated in place (the caller
-        does not read admm_state0 again)."""
+        does not read admm_state0 again).  iters_out: a zero-filled (B,) int32
+        device buffer for the raw iteration words (count | TMPC_ITERS_NONFINITE
+        in bit 31); the caller then splits them (the returned stats carry
+        num_iter and nonfinite None)."""
         if not qp_data.cost.D.is_cuda:
             raise ValueError("ADMMSolver (HIP backends) needs device tensors; there is no CPU path")
         state0 = self.initial_state(qp_data, rho_bar=rho_bar) if admm_state0 is None else admm_state0
@@ -199,17 +203,18 @@ class ADMMSolver:
             want_pcg_iters=self._admm_backend == AdmmBackend.HIP_PCG,
             workspace=workspace,
             donate=donate_state and admm_state0 is not None,
+            iters_out=iters_out,
         )
         x, z, yg, y0, yf, xi, rho = outs
         state = ADMMState(x_blocks=x, y_g=yg, y_f_0=y0, y_f_dyn=yf, z_g=z, xi_g=xi, rho_bar=rho)
         states, controls = unpack_x(x, self._zshape)
-        iters, bad = _split_iters(iters)
+        iters, bad = _split_iters(iters) if iters_out is None else (None, None)
         return (states, controls), ADMMStats(num_iter=iters, num_pcg_iters=pcg_iters, nonfinite=bad), state
 
     def sqp_step(self, qp_data: QPData, admm_state0: ADMMState, active: torch.Tensor, tol: Optional[float],
                  rho_bar: float = 1.0, alpha: float = 1.0, *, slack_weight=0.0,
                  workspace: Optional[torch.Tensor] = None, warm_records: bool = False,
-                 warm_ineq: bool = False, donate_state: bool = False):
+                 warm_ineq: bool = False, donate_state: bool = False, iters_out: Optional[torch.Tensor] = None):
         """One device SQP step (tmpc_sqp_admm_step_*): the first-order check of
         admm_state0's iterate against qp_data, the activity test
         active & (conv > tol), and the solve of the problems that pass it (the
@@ -220,7 +225,8 @@ class ADMMSolver:
         also in G, l and u (FLAG_WARM_INEQ).  donate_state:
         admm_state0's buffers may be updated in place.  tol None: the
         activity is given (no check; the problems where `active` is False keep
-        their state, and the check outputs are None).  Returns
+        their state, and the check outputs are None).  iters_out: as in
+        solve (raw iteration words, stats num_iter and nonfinite None).  Returns
         ((states, controls), stats, state, (conv, eq_err, ineq_err, g), active_out)."""
         if self._admm_backend != AdmmBackend.HIP_DIRECT:
             raise ValueError("sqp_step needs the direct Schur solve (HIP_DIRECT)")
@@ -236,11 +242,11 @@ class ADMMSolver:
         sw = slack_weight if self._use_slack else None
         outs, iters, _, (conv, eq, iq, g, act) = hip.admm_hip_solve(
             qp_data, admm_state0, schur="direct", cfg=cfg, slack_weight=sw, sqp=(active, tol), workspace=workspace,
-            donate=donate_state)
+            donate=donate_state, iters_out=iters_out)
         x, z, yg, y0, yf, xi, rho = outs
         state = ADMMState(x_blocks=x, y_g=yg, y_f_0=y0, y_f_dyn=yf, z_g=z, xi_g=xi, rho_bar=rho)
         states, controls = unpack_x(x, self._zshape)
-        iters, bad = _split_iters(iters)
+        iters, bad = _split_iters(iters) if iters_out is None else (None, None)
         return ((states, controls), ADMMStats(num_iter=iters, num_pcg_iters=None, nonfinite=bad), state,
                 (conv, eq, iq, g), act)
 

@@ -86,7 +86,8 @@ def direct_workspace(qp: QPData) -> torch.Tensor:
 
 def admm_hip_solve(qp: QPData, state0, *, schur: str, cfg: _lib.AdmmCfg,
                    slack_weight: Optional[torch.Tensor] = None, want_pcg_iters: bool = False, sqp=None,
-                   workspace: Optional[torch.Tensor] = None, donate: bool = False):
+                   workspace: Optional[torch.Tensor] = None, donate: bool = False,
+                   iters_out: Optional[torch.Tensor] = None):
     """Run the fused ADMM on the device.  `state0` is an ADMMState of batched
     tensors; returns (state fields tuple, iters (B,), pcg_iters or None).
 
@@ -100,7 +101,11 @@ def admm_hip_solve(qp: QPData, state0, *, schur: str, cfg: _lib.AdmmCfg,
 
     donate: the caller gives up state0: fields that already have the output's
     shape, dtype and layout are updated in place instead of copied (the
-    library reads and writes the same buffers)."""
+    library reads and writes the same buffers).
+
+    iters_out: a zero-filled contiguous (B,) int32 device buffer that receives
+    the iteration words (returned as `iters`) instead of a new one, e.g. a
+    row of an SQP loop's per-iteration record."""
     if sqp is not None and schur != "direct":
         raise ValueError("an SQP step (sqp=...) needs the direct Schur solve")
     lib = _lib.load()
@@ -129,7 +134,13 @@ def admm_hip_solve(qp: QPData, state0, *, schur: str, cfg: _lib.AdmmCfg,
         prep(state0.rho_bar, (B,)),
     ]
     sv = state_struct(*outs)
-    iters = torch.zeros(B, dtype=torch.int32, device=dev)
+    if iters_out is None:
+        iters = torch.zeros(B, dtype=torch.int32, device=dev)
+    elif (iters_out.dtype == torch.int32 and iters_out.shape == (B,) and iters_out.device == dev
+          and iters_out.is_contiguous()):
+        iters = iters_out
+    else:
+        raise ValueError("iters_out must be a contiguous (B,) int32 tensor on the QP's device")
     stream = _lib.stream_handle(dev)
     if schur == "direct":
         nbytes = lib.tmpc_admm_direct_workspace_bytes(ctypes.sizeof(ctypes.c_double) if dt == torch.float64 else 4,
@@ -139,7 +150,11 @@ def admm_hip_solve(qp: QPData, state0, *, schur: str, cfg: _lib.AdmmCfg,
             raise ValueError(f"workspace of {ws.numel()} bytes, {nbytes} needed")
         if sqp is not None:
             active, tol = sqp
-            act_in = active.to(device=dev, dtype=torch.uint8).contiguous()
+            if active.dtype == torch.bool and active.device == dev and active.shape == (B,) \
+                    and active.is_contiguous():
+                act_in = active.view(torch.uint8)  # the same bytes (0 / 1), no copy
+            else:
+                act_in = active.to(device=dev, dtype=torch.uint8).contiguous()
             act_out = torch.empty(B, dtype=torch.uint8, device=dev)
             if tol is None:  # activity given: no check
                 conv = eq = iq = g = None
@@ -157,7 +172,7 @@ def admm_hip_solve(qp: QPData, state0, *, schur: str, cfg: _lib.AdmmCfg,
             )
             _lib.check(f"tmpc_sqp_admm_step_{sfx}", st)
             del keep
-            return outs, iters, None, (conv, eq, iq, g, act_out.bool())
+            return outs, iters, None, (conv, eq, iq, g, act_out.view(torch.bool))  # the library writes 0 / 1
         st = getattr(lib, f"tmpc_admm_direct_{sfx}")(
             stream, ctypes.byref(dims), ctypes.byref(cq), ctypes.byref(sv), ctypes.byref(sv),
             _lib.ptr(iters), ctypes.byref(cfg), _lib.ptr(ws), nbytes,

@@ -525,6 +525,20 @@ class TurboMPCSolver:
     def _qp_x(program, states, controls):
         return pack_x(*TurboMPCSolver._to_qp(program, states, controls))
 
+    def _g_of(self, program, qp: QPData, x_qp: Optional[torch.Tensor], states, controls) -> torch.Tensor:
+        """G x (B, T, m) at the iterate (states, controls), in the QP's
+        variables.  x_qp: the ADMM state's x when the iterate is that state's
+        own solution (without rescaling it is the packed iterate bit for bit),
+        else None.  Where G_t is one block for every stage and problem (the
+        OCP box selectors) the product is one GEMM with it: exact for selector
+        rows, like the batched form apply_G (a product per entry and a sum)."""
+        x = x_qp if x_qp is not None and not self._rescaled(program) else self._qp_x(program, states, controls)
+        G = qp.ineq.G
+        if getattr(program, "const_g", False) and G.shape[2] > 0:
+            B, T, n = x.shape
+            return (x.reshape(B * T, n) @ G[0, 0].t()).view(B, T, G.shape[2])
+        return apply_G(qp, x)
+
     @staticmethod
     def _from_qp(program, states, controls):
         """A QP solution's states and controls in true units (the unscaling
@@ -561,15 +575,17 @@ class TurboMPCSolver:
         if admm_state0 is None:
             admm_state0 = admm.initial_state(qp, rho_bar=ap["rho"])  # x = 0 (turbompc_solver.py:1545-1551)
         admm_state = admm_state0
-        conv = torch.full((B,), float("inf"), dtype=dt, device=dev)
         # per-iteration records, iteration-major so that one iteration's entries
         # are contiguous: [0] eq violation, [1] ineq violation, [2] convergence error
         hist = torch.zeros((3, max_iter, B), dtype=dt, device=dev)
-        admm_iters = torch.zeros((max_iter, B), dtype=torch.int32, device=dev)
-        ran = torch.zeros((max_iter, B), dtype=torch.bool, device=dev)
+        # each step's iteration words (count | TMPC_ITERS_NONFINITE), written
+        # by the library into its row; split once after the loop
+        words = torch.zeros((max_iter, B), dtype=torch.int32, device=dev)
+        ran = []  # the activity of each step that ran
         active = torch.ones(B, dtype=torch.bool, device=dev)
-        g_c = None
+        conv = g_c = None
         last = 0
+        step_words = words[0]
         # a workspace of the solve's own: its stage records stay valid between
         # steps, so a step whose QP differs from the previous one only in the
         # relinearized dynamics (A_minus, c) rewrites just those records
@@ -578,51 +594,54 @@ class TurboMPCSolver:
         for it in range(max_iter):
             sw = qp.ineq.slack_penalization_weight
             if it == 0:  # cond_fun runs the first iteration unconditionally
-                (states, controls), stats, admm_state = admm.solve(qp, admm_state, rho_bar=ap["rho"], alpha=alpha,
-                                                                    slack_weight=sw, workspace=ws,
-                                                                    donate_state=own_state)
+                (states, controls), _, admm_state = admm.solve(qp, admm_state, rho_bar=ap["rho"], alpha=alpha,
+                                                                slack_weight=sw, workspace=ws,
+                                                                donate_state=own_state, iters_out=words[0])
                 states, controls = self._from_qp(program, states, controls)
             else:
                 # the state is the loop's own from here on: updated in place
                 warm = _warm_level(qp, prev)
-                (states, controls), stats, admm_state, (cv, e, i, g), act = admm.sqp_step(
+                (states, controls), _, admm_state, (cv, e, i, g), act = admm.sqp_step(
                     qp, admm_state, active, tol, rho_bar=ap["rho"], alpha=alpha, slack_weight=sw, workspace=ws,
-                    warm_records=warm is not None, warm_ineq=warm == "constraints", donate_state=True)
+                    warm_records=warm is not None, warm_ineq=warm == "constraints", donate_state=True,
+                    iters_out=words[it])
                 states, controls = self._from_qp(program, states, controls)
                 # the check belongs to the iterate committed at it - 1 (the
                 # records of a stopped problem stay zero, as in the reference)
                 if it == 1:
-                    conv = cv
                     hist[:, 0] = torch.stack([e, i, cv])
-                    g_c = g
                 else:
-                    conv = torch.where(active, cv, conv)
                     hist[:, it - 1] = torch.where(active, torch.stack([e, i, cv]), hist[:, it - 1])
-                    g_c = torch.where(active[:, None, None], g, g_c)
+                # a stopped problem keeps its iterate, state and QP, so this
+                # check of it repeats, value for value, the one recorded when
+                # it stopped: conv and G x need no masked merge
+                conv, g_c = cv, g
                 active = act
+                step_words = words[it]
                 if tol > 0 and not bool(active.any()):
                     break  # no problem iterated in this step
-            admm_iters[it] = stats.num_iter
-            ran[it] = active
+            ran.append(active)
             last = it
             prev = qp
             if it + 1 < max_iter:
                 qp = program.build_qp(states, controls)
+        if conv is None:
+            conv = torch.full((B,), float("inf"), dtype=dt, device=dev)
         # the last committed iterate is not checked (the reference evaluates no
         # check after its final iteration): its record keeps the previous error
         # and G x at the QP it was solved on
         hist[2, last] = torch.where(active, conv, hist[2, last])
-        g_last = apply_G(qp, self._qp_x(program, states, controls))
+        g_last = self._g_of(program, qp, admm_state.x_blocks, states, controls)
         g_c = g_last if g_c is None else torch.where(active[:, None, None], g_last, g_c)
         kkt = self._build_kkt_state(states, controls, admm_state, g_c, qp.ineq.l, qp.ineq.u)
-        num_iter = ran.sum(dim=0, dtype=torch.int32)
-        admm_iters = admm_iters.t()
+        num_iter = torch.stack(ran).sum(dim=0, dtype=torch.int32)
+        admm_iters = (words & 0x7FFFFFFF).t()
         return TurboMPCSolution(
             states=states, controls=controls, slack=admm_state.xi_g, status=self.STATUS_SUCCESS, num_iter=num_iter,
             convergence_error=conv, admm_iters=admm_iters, linesearch_alphas=None, admm_state=admm_state,
             solver_stats=SolverStats(admm_iters, hist[0].t(), hist[1].t(), hist[2].t()), kkt_state=kkt,
             # the last step scanned every problem's state (stopped ones keep theirs)
-            nonfinite=stats.nonfinite,
+            nonfinite=step_words < 0,
         )
 
     def _solve_impl_device_ls(self, program, states, controls, admm_state0: Optional[ADMMState] = None
@@ -697,18 +716,18 @@ class TurboMPCSolver:
                 prev = qp
                 qp = program.build_qp(states, controls)
                 if by_step:
-                    g = apply_G(qp, self._qp_x(program, states, controls))
+                    g = self._g_of(program, qp, None, states, controls)
                 else:
                     c_err, e_err, i_err, g = self._first_order_check(
                         qp, *self._to_qp(program, states, controls), slacks, adm_new)
             elif by_step:
-                g = apply_G(qp, self._qp_x(program, s_new, c_new))
+                g = self._g_of(program, qp, None, s_new, c_new)
                 states, controls, slacks = sel(s_new, states), sel(c_new, controls), sel(sl_new, slacks)
             else:
                 # the last iterate is not checked: its record keeps the previous
                 # error, and G x at the QP it was solved on
                 c_err, e_err, i_err = conv, torch.zeros_like(conv), torch.zeros_like(conv)
-                g = apply_G(qp, self._qp_x(program, s_new, c_new))
+                g = self._g_of(program, qp, None, s_new, c_new)
                 states, controls, slacks = sel(s_new, states), sel(c_new, controls), sel(sl_new, slacks)
             admm_state = adm_new
             if use_ls:
@@ -791,7 +810,7 @@ class TurboMPCSolver:
                 c_new_err = step if (it == 0 or self._convergence_criterion == "step") else conv
                 e_err = torch.zeros_like(c_new_err)
                 i_err = torch.zeros_like(c_new_err)
-                g = apply_G(qp_next, self._qp_x(program, s_new, c_new))
+                g = self._g_of(program, qp_next, None, s_new, c_new)
             # commit where active (vmapped while_loop semantics)
             if all_active:
                 sel = lambda a, b: a  # noqa: E731
