@@ -408,6 +408,25 @@ int tmpc_sqp_first_order_f64(hipStream_t stream, const tmpc_dims* dims, const tm
                              const double* y_f0, const double* y_f, const double* y_g, const double* slack,
                              double slack_weight, uint32_t flags, double* conv, double* eq_err, double* ineq_err, double* g_out);
 
+/* ---- KKT state: active inequality sets -------------------------------------
+ * Replaces the XLA-evaluated active-set classification of the solution's KKT
+ * state: identify_active_inequalities (turbompc/solvers/turbompc_solver.py:269-292)
+ * and its disambiguation by the dual's sign in _build_kkt_state (:1387-1439).
+ * Over `count` inequality rows (any layout, the same for every array):
+ * a row is active where min(g - l, u - g) <= eps_abs + eps_rel |bound| (the
+ * bound of the nearer side, upper where u - g < g - l), lower / upper by that
+ * side; with y (the rows' duals, or NULL) a row with y < -dual_tol is lower,
+ * y > dual_tol upper, and the proximity decides only in between.  Outputs
+ * lower, upper (count bytes, 0 / 1).  eps_abs, eps_rel and dual_tol are
+ * rounded to the element type first; the classification then equals the
+ * elementwise torch evaluation of the same formula. */
+int tmpc_kkt_active_sets_f32(hipStream_t stream, int64_t count, const float* g, const float* l, const float* u,
+                             const float* y, double eps_abs, double eps_rel, double dual_tol, uint8_t* lower,
+                             uint8_t* upper);
+int tmpc_kkt_active_sets_f64(hipStream_t stream, int64_t count, const double* g, const double* l,
+                             const double* u, const double* y, double eps_abs, double eps_rel, double dual_tol,
+                             uint8_t* lower, uint8_t* upper);
+
 #ifdef __cplusplus
 }
 #endif

@@ -265,3 +265,55 @@ def test_sqp_warm_records_match_repacking(case):
     assert torch.equal(warm.admm_state.y_g, cold.admm_state.y_g)
     assert torch.equal(warm.slack, cold.slack)
     assert torch.equal(warm.convergence_error, cold.convergence_error)
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.float64])
+@pytest.mark.parametrize("with_dual", [True, False])
+def test_kkt_active_sets_kernel_matches_torch(dtype, with_dual):
+    """tmpc_kkt_active_sets_* against the elementwise torch form of
+    identify_active_inequalities + the dual-sign rule (turbompc_solver.py:269-292,
+    :1387-1439), value for value: rows drawn around the tolerance boundary on
+    both sides (a contracted eps_abs + eps_rel |bound| would flip some of
+    them), infinite and NaN bounds and values, duals at and around +-dual_tol."""
+    from turbompc_amd.solvers.sqp_hip import kkt_active_sets
+    from turbompc_amd.solvers.turbompc_solver import active_sets_torch
+
+    gen = torch.Generator().manual_seed(7)
+    B, T, m = 64, 21, 8
+    ea, er, dtol = 1e-3, 1e-3, 1e-3
+    l = -torch.rand((B, T, m), generator=gen, dtype=torch.float64) * 4.0
+    u = torch.rand((B, T, m), generator=gen, dtype=torch.float64) * 4.0
+    l, u = l.to(dtype), u.to(dtype)
+    tol_l = ea + er * l.abs()
+    tol_u = ea + er * u.abs()
+    side = torch.rand((B, T, m), generator=gen) < 0.5
+    spread = 2e-6 if dtype == torch.float32 else 4e-15  # a few dozen ulps of the tolerance
+    jitter = (1.0 + (torch.rand((B, T, m), generator=gen, dtype=torch.float64) - 0.5) * spread).to(dtype)
+    g = torch.where(side, l + tol_l * jitter, u - tol_u * jitter)  # within a few ulps of the boundary
+    far = torch.rand((B, T, m), generator=gen) < 0.3
+    g = torch.where(far, (l + u) / 2, g)
+    # special rows: infinite bounds, NaN values and bounds, exact bounds, signed zeros
+    g[0, 0, :] = torch.tensor([0.0, float("nan"), 1.0, -0.0, 2.0, float("inf"), -1.0, 0.5], dtype=dtype)
+    l[0, 0, :] = torch.tensor([-float("inf"), -1.0, 1.0, 0.0, float("nan"), 0.0, -float("inf"), 0.5], dtype=dtype)
+    u[0, 0, :] = torch.tensor([float("inf"), 1.0, 2.0, 0.0, 3.0, float("inf"), 0.0, float("inf")], dtype=dtype)
+    y = None
+    if with_dual:
+        y = (torch.randn((B, T, m), generator=gen, dtype=torch.float64) * 2e-3).to(dtype)
+        d = torch.tensor(dtol, dtype=dtype)
+        y[1, 0, :] = torch.stack([d, -d, torch.nextafter(d, d * 2), -torch.nextafter(d, d * 2),
+                                  torch.nextafter(d, d * 0), torch.tensor(0.0, dtype=dtype),
+                                  torch.tensor(float("nan"), dtype=dtype), torch.tensor(-0.0, dtype=dtype)])
+    gd, ld, ud = (t.to("cuda") for t in (g, l, u))
+    yd = y.to("cuda") if y is not None else None
+    lo, up = kkt_active_sets(gd, ld, ud, yd, ea, er, dtol)
+    lo_t, up_t = active_sets_torch(gd, ld, ud, yd, ea, er, dtol)
+    torch.cuda.synchronize()
+    assert lo.dtype == torch.bool and lo.shape == g.shape
+    assert torch.equal(lo, lo_t) and torch.equal(up, up_t)
+    # the CPU evaluation of the same torch form agrees too
+    lo_c, up_c = active_sets_torch(g, l, u, y, ea, er, dtol)
+    assert torch.equal(lo.cpu(), lo_c) and torch.equal(up.cpu(), up_c)
+    # the boundary draws exercise both outcomes
+    n_lo, n_up = int(lo.sum()), int(up.sum())
+    print(f"{dtype} dual={with_dual}: {n_lo} lower, {n_up} upper of {g.numel()}")
+    assert 0 < n_lo < g.numel() and 0 < n_up < g.numel()

@@ -149,6 +149,8 @@ SIGNATURES = {
     "tmpc_adjoint_kkt_f64": [_VP, _PD, _PQ, _VP, _VP, _F64, _I32, _U32, _VP, _SZ],
     "tmpc_sqp_first_order_f32": [_VP, _PD, _PQ, _VP, _VP, _VP, _VP, _VP, _F64, _U32, _VP, _VP, _VP, _VP],
     "tmpc_sqp_first_order_f64": [_VP, _PD, _PQ, _VP, _VP, _VP, _VP, _VP, _F64, _U32, _VP, _VP, _VP, _VP],
+    "tmpc_kkt_active_sets_f32": [_VP, ctypes.c_int64, _VP, _VP, _VP, _VP, _F64, _F64, _F64, _VP, _VP],
+    "tmpc_kkt_active_sets_f64": [_VP, ctypes.c_int64, _VP, _VP, _VP, _VP, _F64, _F64, _F64, _VP, _VP],
     "tmpc_quadrotor_linearize_f32": [_VP, _I32, _I32, _VP, _VP, _F64, _VP, _VP, _VP],
     "tmpc_quadrotor_linearize_f64": [_VP, _I32, _I32, _VP, _VP, _F64, _VP, _VP, _VP],
     "tmpc_linear_dynamics_f32": [_VP, _I32, _I32, _I32, _I32, _VP, _VP, _VP, _VP, _VP, _VP],

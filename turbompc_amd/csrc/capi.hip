@@ -1314,6 +1314,21 @@ int sqp_check_impl(hipStream_t s, const tmpc_dims* dims, const tmpc_qp* qp, cons
 
 using namespace tmpc;
 
+// ----------------------------------------------------------- KKT state ----
+template <typename R>
+int kkt_active_sets_impl(hipStream_t s, int64_t count, const R* g, const R* l, const R* u, const R* y,
+                         double eps_abs, double eps_rel, double dual_tol, uint8_t* lower, uint8_t* upper) {
+  if (count < 0) return TMPC_EBADSHAPE;
+  if (count == 0) return TMPC_OK;
+  if (!g || !l || !u || !lower || !upper) return TMPC_EBADARG;
+  const long long grid = (count + 255) / 256;
+  if (grid > 0x7fffffffLL) return TMPC_EBADSHAPE;
+  // the scalars rounded to R, as torch rounds a Python scalar to the tensor's type
+  hipLaunchKernelGGL((kkt_active_sets_kernel<R>), dim3((unsigned)grid), dim3(256), 0, s, (long long)count, g, l, u,
+                     y, (R)eps_abs, (R)eps_rel, (R)dual_tol, lower, upper);
+  return launch_status();
+}
+
 extern "C" {
 
 const char* tmpc_status_string(int status) {
@@ -1524,6 +1539,17 @@ int tmpc_obstacle_lagrangian_hessian_f64(hipStream_t s, int32_t B, int32_t N, in
                                          const double* radii, int32_t m, int32_t row0, const double* mus,
                                          double* H) {
   return obstacle_hess_impl<double>(s, B, N, nx, nu, dim, K, states, centers, radii, m, row0, mus, H);
+}
+
+int tmpc_kkt_active_sets_f32(hipStream_t s, int64_t count, const float* g, const float* l, const float* u,
+                             const float* y, double eps_abs, double eps_rel, double dual_tol, uint8_t* lower,
+                             uint8_t* upper) {
+  return kkt_active_sets_impl<float>(s, count, g, l, u, y, eps_abs, eps_rel, dual_tol, lower, upper);
+}
+int tmpc_kkt_active_sets_f64(hipStream_t s, int64_t count, const double* g, const double* l, const double* u,
+                             const double* y, double eps_abs, double eps_rel, double dual_tol, uint8_t* lower,
+                             uint8_t* upper) {
+  return kkt_active_sets_impl<double>(s, count, g, l, u, y, eps_abs, eps_rel, dual_tol, lower, upper);
 }
 
 int tmpc_sqp_first_order_f32(hipStream_t s, const tmpc_dims* dims, const tmpc_qp* qp, const float* x,

@@ -254,6 +254,48 @@ __global__ void sqp_activity_kernel(int B, const R* __restrict__ conv, R tol, co
   act_out[b] = ((act_in ? act_in[b] != 0 : true) && (conv == nullptr || conv[b] > tol)) ? 1 : 0;
 }
 
+// The active sets of the KKT state (one thread per inequality row): proximity
+// to a bound, min(g - l, u - g) <= eps_abs + eps_rel |bound| on the nearer
+// side (identify_active_inequalities, turbompc/solvers/turbompc_solver.py:269-292),
+// then, with y, the dual's sign where it is decided (|y| > dual_tol,
+// :1387-1439).  The arithmetic is that of the elementwise torch form, value
+// for value: the differences, then eps_rel |bound| and eps_abs + that as two
+// rounded operations, the scalars rounded to R first; a NaN difference or
+// bound makes the row inactive, as torch.minimum's NaN does.  The product and
+// the sum must not contract into an FMA (hipcc contracts by default, and the
+// intrinsics __fmul_rn / __fadd_rn do not stop it): a row one ulp from its
+// tolerance would flip.
+template <typename R>
+__device__ __forceinline__ R active_tolerance(R eps_abs, R eps_rel, R bound_abs) {
+#pragma clang fp contract(off)
+  return eps_abs + eps_rel * bound_abs;
+}
+
+template <typename R>
+__global__ __launch_bounds__(256) void kkt_active_sets_kernel(long long count, const R* __restrict__ g,
+                                                              const R* __restrict__ l, const R* __restrict__ u,
+                                                              const R* __restrict__ y, R eps_abs, R eps_rel,
+                                                              R dual_tol, uint8_t* __restrict__ lower,
+                                                              uint8_t* __restrict__ upper) {
+  const long long i = (long long)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= count) return;
+  const R gv = g[i], lv = l[i], uv = u[i];
+  const R dl = gv - lv, du = uv - gv;
+  const bool use_upper = du < dl;
+  const R tol = active_tolerance(eps_abs, eps_rel, use_upper ? rabs(uv) : rabs(lv));
+  const bool nan = dl != dl || du != du;
+  const bool active = !nan && (dl < du ? dl : du) <= tol;
+  bool lo = active && !use_upper, up = active && use_upper;
+  if (y != nullptr) {
+    const R yv = y[i];
+    const bool ylo = yv < -dual_tol, yup = yv > dual_tol, und = !(ylo || yup);
+    lo = ylo || (und && lo);
+    up = yup || (und && up);
+  }
+  lower[i] = lo ? 1 : 0;
+  upper[i] = up ? 1 : 0;
+}
+
 template <typename R>
 constexpr size_t check_smem_bytes(int n, int nx, int m) {
   return (size_t)(n + nx + m) * check_ld(n) * sizeof(R);

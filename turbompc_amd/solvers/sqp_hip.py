@@ -43,3 +43,25 @@ def first_order_check(qp: QPData, x: torch.Tensor, y_f0: torch.Tensor, y_f: torc
     _lib.check(f"tmpc_sqp_first_order_{sfx}", st)
     del keep
     return conv, eq, iq, g
+
+
+def kkt_active_sets(g: torch.Tensor, l: torch.Tensor, u: torch.Tensor, y: Optional[torch.Tensor], eps_abs: float,
+                    eps_rel: float, dual_tol: float):
+    """(lower, upper) bool tensors of g's shape: the active sets of the KKT
+    state (tmpc_kkt_active_sets_*; identify_active_inequalities and the dual
+    sign test of _build_kkt_state, turbompc_solver.py:269-292, :1387-1439),
+    one kernel instead of the elementwise chain; y None: proximity only."""
+    if not g.is_cuda:
+        raise ValueError("kkt_active_sets runs on the GPU; pass device tensors")
+    lib = _lib.load()
+    dt, dev = g.dtype, g.device
+    g, l, u = (t.to(device=dev, dtype=dt).expand(g.shape).contiguous() for t in (g, l, u))
+    y = y.to(device=dev, dtype=dt).expand(g.shape).contiguous() if y is not None else None
+    lower = torch.empty(g.shape, dtype=torch.uint8, device=dev)
+    upper = torch.empty(g.shape, dtype=torch.uint8, device=dev)
+    sfx = _lib.suffix(dt)
+    st = getattr(lib, f"tmpc_kkt_active_sets_{sfx}")(
+        _lib.stream_handle(dev), g.numel(), _lib.ptr(g), _lib.ptr(l), _lib.ptr(u), _lib.ptr(y), float(eps_abs),
+        float(eps_rel), float(dual_tol), _lib.ptr(lower), _lib.ptr(upper))
+    _lib.check(f"tmpc_kkt_active_sets_{sfx}", st)
+    return lower.view(torch.bool), upper.view(torch.bool)  # the kernel writes 0 / 1

@@ -33,7 +33,7 @@ from .qp_ops import apply_C_parts, apply_Ct, apply_G, apply_Gt, apply_P, inf_nor
 from .qp_utils import ZShape, pack_x, pack_z
 from .backward.backward_kkt_hip import solve_backward_kkt_hip
 from .qp_data import QPCostBlocks, QPEqualityBlocks, QPInequalityBlocks
-from .sqp_hip import first_order_check
+from .sqp_hip import first_order_check, kkt_active_sets
 
 _PARAMS_DIR = Path(__file__).resolve().parent / "params"
 
@@ -175,12 +175,25 @@ def _nonfinite(*tensors) -> torch.Tensor:
 
 
 def identify_active_inequalities(g, l, u, eps_abs: float, eps_rel: float):
-    """min(g - l, u - g) <= eps_abs + eps_rel |bound| (turbompc_solver.py:269-292)."""
+    """min(g - l, u - g) <= eps_abs + eps_rel |bound| (turbompc_solver.py:269-292).
+    The elementwise torch form; the solver runs tmpc_kkt_active_sets_*, whose
+    tests hold it to active_sets_torch value for value."""
     dl, du = g - l, u - g
     use_upper = du < dl
     tol = eps_abs + eps_rel * torch.where(use_upper, u.abs(), l.abs())
     active = torch.minimum(dl, du) <= tol
     return active & ~use_upper, active & use_upper
+
+
+def active_sets_torch(g, l, u, y, eps_abs: float, eps_rel: float, dual_tol: float):
+    """The KKT state's active sets in torch: proximity, then the dual's sign
+    where |y| > dual_tol (turbompc_solver.py:1387-1439)."""
+    lo, up = identify_active_inequalities(g, l, u, eps_abs, eps_rel)
+    if y is not None and y.shape[-1] > 0:
+        dl, du = y < -dual_tol, y > dual_tol
+        und = ~(dl | du)
+        lo, up = dl | (und & lo), du | (und & up)
+    return lo, up
 
 
 def _where(mask: torch.Tensor, a: torch.Tensor, b: torch.Tensor) -> torch.Tensor:
@@ -500,12 +513,9 @@ class TurboMPCSolver:
             # soft constraints: the slack's sign marks the active side (:1413-1415)
             slack = admm_state.xi_g
             return KKTState(states, controls, slack, y_f, y_ineq, slack > 1.0e-12, slack < -1.0e-12)
-        lo, up = identify_active_inequalities(g, l, u, ap["eps_abs"], ap["eps_rel"])
-        if y_ineq.shape[-1] > 0:
-            tol = ap["eps_abs"]
-            dl, du = y_ineq < -tol, y_ineq > tol
-            und = ~(dl | du)
-            lo, up = dl | (und & lo), du | (und & up)
+        # proximity, then the dual's sign beyond eps_abs, in one kernel
+        lo, up = kkt_active_sets(g, l, u, y_ineq if y_ineq.shape[-1] > 0 else None, ap["eps_abs"], ap["eps_rel"],
+                                 ap["eps_abs"])
         return KKTState(states, controls, admm_state.xi_g, y_f, y_ineq, lo, up)
 
     @staticmethod
