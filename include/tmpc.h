@@ -326,6 +326,18 @@ int tmpc_quadrotor_linearize_f32(hipStream_t stream, int32_t B, int32_t N, const
 int tmpc_quadrotor_linearize_f64(hipStream_t stream, int32_t B, int32_t N, const double* states,
                                  const double* controls, double dt, const double* params,
                                  double* A_minus, double* c);
+/* The same with row strides (elements between consecutive (b, t) rows; >= 13
+ * for states, >= 4 for controls, row (b, t) at b (N+1) + t): for an iterate
+ * held packed, as the QP's z_t = [x_t; u_t] rows of an ADMM state (states at
+ * z, stride n; controls at z + 13, stride n), read in place. */
+int tmpc_quadrotor_linearize_strided_f32(hipStream_t stream, int32_t B, int32_t N, const float* states,
+                                         int64_t states_row_stride, const float* controls,
+                                         int64_t controls_row_stride, double dt, const double* params,
+                                         float* A_minus, float* c);
+int tmpc_quadrotor_linearize_strided_f64(hipStream_t stream, int32_t B, int32_t N, const double* states,
+                                         int64_t states_row_stride, const double* controls,
+                                         int64_t controls_row_stride, double dt, const double* params,
+                                         double* A_minus, double* c);
 
 /* The RK4 step of the same dynamics: next (B,N,13) = predict_next_state(x_t, u_t)
  * for t < N, the dynamics part of equality_constraints

@@ -411,6 +411,18 @@ def test_quadrotor_linearization_matches_complex_step(dtype):
     tol = 1e-12 if dtype == torch.float64 else 1e-5
     assert rel_err(Am, Jr) < tol
     assert rel_err(c, cr) < (1e-11 if dtype == torch.float64 else 1e-5)
+    # the same iterate packed as z rows [x; u] (an ADMM state's layout): read in
+    # place through the row strides, the blocks are the same bit for bit
+    z = torch.cat([st, ct], dim=-1).to(DEV, dtype)
+    zs, zc = z[..., :13], z[..., 13:]
+    assert not zs.is_contiguous() and zs.stride(1) == 17
+    Am2, c2 = prob.dynamics_blocks(zs, zc)
+    assert torch.equal(Am2, Am) and torch.equal(c2, c)
+    # rows that are not evenly strided are copied first; wrong shapes are refused
+    Am3, c3 = prob.dynamics_blocks(st.to(DEV, dtype).transpose(0, 1).contiguous().transpose(0, 1), ct.to(DEV, dtype))
+    assert torch.equal(Am3, Am) and torch.equal(c3, c)
+    with pytest.raises(ValueError, match="expected"):
+        prob.dynamics_blocks(zs[:, :-1], zc[:, :-1])
 
 
 # ---- streaming kernel (explicit-integrator structure, stage records) ---------

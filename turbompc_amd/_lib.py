@@ -153,6 +153,10 @@ SIGNATURES = {
     "tmpc_kkt_active_sets_f64": [_VP, ctypes.c_int64, _VP, _VP, _VP, _VP, _F64, _F64, _F64, _VP, _VP],
     "tmpc_quadrotor_linearize_f32": [_VP, _I32, _I32, _VP, _VP, _F64, _VP, _VP, _VP],
     "tmpc_quadrotor_linearize_f64": [_VP, _I32, _I32, _VP, _VP, _F64, _VP, _VP, _VP],
+    "tmpc_quadrotor_linearize_strided_f32": [_VP, _I32, _I32, _VP, ctypes.c_int64, _VP, ctypes.c_int64, _F64, _VP,
+                                             _VP, _VP],
+    "tmpc_quadrotor_linearize_strided_f64": [_VP, _I32, _I32, _VP, ctypes.c_int64, _VP, ctypes.c_int64, _F64, _VP,
+                                             _VP, _VP],
     "tmpc_linear_dynamics_f32": [_VP, _I32, _I32, _I32, _I32, _VP, _VP, _VP, _VP, _VP, _VP],
     "tmpc_linear_dynamics_f64": [_VP, _I32, _I32, _I32, _I32, _VP, _VP, _VP, _VP, _VP, _VP],
     "tmpc_quadrotor_dynamics_f32": [_VP, _I32, _I32, _VP, _VP, _F64, _VP, _VP],

@@ -1170,17 +1170,18 @@ int admm_pcg_impl(hipStream_t s, const tmpc_dims* dims, const tmpc_qp* qp, const
 
 // ------------------------------------------------------------ quadrotor ----
 template <typename R>
-int quad_impl(hipStream_t s, int B, int N, const R* states, const R* controls, double dt,
+int quad_impl(hipStream_t s, int B, int N, const R* states, int64_t ls, const R* controls, int64_t lu, double dt,
               const double* params, R* Am, R* c) {
   if (B < 1 || N < 1) return TMPC_EBADSHAPE;
   if (!states || !controls || !params || !Am || !c) return TMPC_EBADARG;
+  if (ls < 13 || lu < 4 || ls > (1 << 20) || lu > (1 << 20)) return TMPC_EBADARG;
   QuadParams<R> P{(R)params[0], (R)params[1], (R)params[2], (R)params[3],
                   (R)params[4], (R)params[5], (R)params[6]};
   const long long total = (long long)B * N * 18;
   const int blk = 256;
   const long long grid = (total + blk - 1) / blk;
-  hipLaunchKernelGGL((quad_linearize_kernel<R>), dim3((unsigned)grid), dim3(blk), 0, s, B, N, states, controls,
-                     (R)dt, P, Am, c);
+  hipLaunchKernelGGL((quad_linearize_kernel<R>), dim3((unsigned)grid), dim3(blk), 0, s, B, N, states, (int)ls,
+                     controls, (int)lu, (R)dt, P, Am, c);
   return launch_status();
 }
 
@@ -1482,12 +1483,25 @@ int tmpc_schur_pcg_f64(hipStream_t s, int32_t B, int32_t T, int32_t n, const dou
 int tmpc_quadrotor_linearize_f32(hipStream_t s, int32_t B, int32_t N, const float* states,
                                  const float* controls, double dt, const double* params, float* A_minus,
                                  float* c) {
-  return quad_impl<float>(s, B, N, states, controls, dt, params, A_minus, c);
+  return quad_impl<float>(s, B, N, states, 13, controls, 4, dt, params, A_minus, c);
 }
 int tmpc_quadrotor_linearize_f64(hipStream_t s, int32_t B, int32_t N, const double* states,
                                  const double* controls, double dt, const double* params, double* A_minus,
                                  double* c) {
-  return quad_impl<double>(s, B, N, states, controls, dt, params, A_minus, c);
+  return quad_impl<double>(s, B, N, states, 13, controls, 4, dt, params, A_minus, c);
+}
+int tmpc_quadrotor_linearize_strided_f32(hipStream_t s, int32_t B, int32_t N, const float* states,
+                                         int64_t states_row_stride, const float* controls,
+                                         int64_t controls_row_stride, double dt, const double* params,
+                                         float* A_minus, float* c) {
+  return quad_impl<float>(s, B, N, states, states_row_stride, controls, controls_row_stride, dt, params, A_minus, c);
+}
+int tmpc_quadrotor_linearize_strided_f64(hipStream_t s, int32_t B, int32_t N, const double* states,
+                                         int64_t states_row_stride, const double* controls,
+                                         int64_t controls_row_stride, double dt, const double* params,
+                                         double* A_minus, double* c) {
+  return quad_impl<double>(s, B, N, states, states_row_stride, controls, controls_row_stride, dt, params, A_minus,
+                           c);
 }
 
 int tmpc_linear_dynamics_f32(hipStream_t s, int32_t B, int32_t N, int32_t nx, int32_t nu, const float* states,

@@ -91,8 +91,8 @@ __device__ __forceinline__ void quad_xdot(const D* x, const D* f, const QuadPara
 }
 
 template <typename R>
-__global__ __launch_bounds__(256) void quad_linearize_kernel(int B, int N, const R* __restrict__ states,
-                                                             const R* __restrict__ controls, R dt,
+__global__ __launch_bounds__(256) void quad_linearize_kernel(int B, int N, const R* __restrict__ states, int ls,
+                                                             const R* __restrict__ controls, int lu, R dt,
                                                              QuadParams<R> P, R* __restrict__ Am,
                                                              R* __restrict__ c) {
   const long long gidx = (long long)blockIdx.x * blockDim.x + threadIdx.x;
@@ -102,8 +102,8 @@ __global__ __launch_bounds__(256) void quad_linearize_kernel(int B, int N, const
   const int j = (int)(gidx - pr * 18);
   const int b = (int)(pr / N), t = (int)(pr - (long long)b * N);
   const int T = N + 1;
-  const R* xs = states + ((size_t)b * T + t) * 13;
-  const R* us = controls + ((size_t)b * T + t) * 4;
+  const R* xs = states + ((size_t)b * T + t) * ls;  // rows of ls (>= 13) and lu (>= 4) elements
+  const R* us = controls + ((size_t)b * T + t) * lu;
   Dual<R> x[13], u[4];
 #pragma unroll
   for (int k = 0; k < 13; ++k) x[k] = Dual<R>(xs[k], j == 17 ? xs[k] : (j == k ? R(1) : R(0)));

@@ -37,21 +37,34 @@ class QuadrotorOCP(QuadraticTrackingOCP):
         self.params = tuple(float(p) for p in params)
         self._cparams = (ctypes.c_double * 7)(*self.params)
 
+    @staticmethod
+    def _rows(t: torch.Tensor, width: int):
+        """(t, row stride): t itself where its (b, t) rows are evenly strided
+        with unit column stride (column slices of a packed iterate, such as
+        the ADMM state's z rows), else a contiguous copy."""
+        if t.stride(-1) == 1 and t.stride(1) >= width and t.stride(0) == t.shape[1] * t.stride(1):
+            return t, t.stride(1)
+        return t.contiguous(), width
+
     def dynamics_blocks(self, states, controls):
         if not states.is_cuda:
             raise ValueError("QuadrotorOCP linearization runs on the GPU; pass device tensors")
         lib = _lib.load()
         B, N = self.B, self.horizon
-        states = states.to(self.dtype).contiguous()
-        controls = controls.to(self.dtype).contiguous()
+        if tuple(states.shape) != (B, N + 1, 13) or tuple(controls.shape) != (B, N + 1, 4):
+            raise ValueError(f"states {tuple(states.shape)} / controls {tuple(controls.shape)}: expected "
+                             f"({B}, {N + 1}, 13) / ({B}, {N + 1}, 4)")
+        # read in place where the rows are evenly strided (no copy of a packed iterate)
+        states, ls = self._rows(states.to(self.dtype), 13)
+        controls, lu = self._rows(controls.to(self.dtype), 4)
         Am = torch.empty((B, N, 13, 17), dtype=self.dtype, device=states.device)
         c = torch.empty((B, N, 13), dtype=self.dtype, device=states.device)
         sfx = _lib.suffix(self.dtype)
-        st = getattr(lib, f"tmpc_quadrotor_linearize_{sfx}")(
-            _lib.stream_handle(states.device), B, N, _lib.ptr(states), _lib.ptr(controls), self.dt,
+        st = getattr(lib, f"tmpc_quadrotor_linearize_strided_{sfx}")(
+            _lib.stream_handle(states.device), B, N, states.data_ptr(), ls, controls.data_ptr(), lu, self.dt,
             self._cparams, _lib.ptr(Am), _lib.ptr(c),
         )
-        _lib.check(f"tmpc_quadrotor_linearize_{sfx}", st)
+        _lib.check(f"tmpc_quadrotor_linearize_strided_{sfx}", st)
         return Am, c
 
     def next_states(self, states, controls):
