@@ -8,6 +8,7 @@ import copy
 
 import pytest
 import torch
+from helpers import rel_err
 
 from turbompc_amd.problems import configs
 from turbompc_amd.problems.quadrotor import make_quadrotor_config
@@ -95,6 +96,34 @@ def test_quadrotor_device_loop_equals_masked(dtype, stop, mode):
     _assert_same(dev, msk)
     if stop:  # problems stop at different iterations
         assert len(set(dev.num_iter.tolist())) >= 2
+
+
+@pytest.mark.parametrize("dtype", [torch.float64, torch.float32])
+def test_first_order_device_loop_stops_on_the_recorded_errors(dtype):
+    """The first-order device loop (the fused check of each SQP step, no line
+    search) with problems stopping at different iterations: a stopped
+    problem's convergence error is the check that stopped it, value for
+    value (the loop re-evaluates that check at every later step on the same
+    iterate, state and QP, and takes it without a masked merge).  Against
+    the host-masked loop: the same iterates, stopping steps and ADMM counts
+    bit for bit; the errors agree to rounding (the masked loop evaluates
+    them with the separate check kernel, the device loop in the fused sweep)."""
+    prob = make_quadrotor_config(B=24, seed=4, dtype=dtype, device="cuda")
+    params = _params(8, 20, 0.0, linesearch=False, criterion="first_order")
+    params["tol_convergence"] = _tol_splitting(prob, params)
+    dev, msk = _both(prob, params)
+    it = dev.num_iter.cpu()
+    print(f"  tol {params['tol_convergence']:.3g}, SQP iterations per problem {it.tolist()}", flush=True)
+    assert len(set(it.tolist())) >= 2
+    hist = dev.solver_stats.convergence_errors.cpu()
+    conv = dev.convergence_error.cpu()
+    for b in range(it.shape[0]):
+        assert hist[b, it[b] - 1] == conv[b], (b, int(it[b]), hist[b].tolist(), float(conv[b]))
+    for k in ("states", "controls", "slack", "num_iter", "admm_iters", "nonfinite"):
+        assert _equal(getattr(dev, k), getattr(msk, k)), k
+    tol = 1e-12 if dtype == torch.float64 else 1e-5
+    assert rel_err(dev.convergence_error, msk.convergence_error) < tol
+    assert rel_err(dev.solver_stats.convergence_errors, msk.solver_stats.convergence_errors) < tol
 
 
 @pytest.mark.parametrize("use_slack", [False, True])
