@@ -263,11 +263,14 @@ class ADMMSolver:
         dt, dev = qp_data.dtype, qp_data.device
         zs = self._zshape
         x_zero = states0 is None and controls0 is None  # then G x = 0 needs no product
-        if states0 is None:
-            states0 = torch.zeros((B, T, zs.num_states), dtype=dt, device=dev)
-        if controls0 is None:
-            controls0 = torch.zeros((B, T, zs.num_controls), dtype=dt, device=dev)
-        x0 = pack_x(states0.to(dt), controls0.to(dt)).contiguous()
+        if x_zero:
+            x0 = torch.zeros((B, T, n), dtype=dt, device=dev)
+        else:
+            if states0 is None:
+                states0 = torch.zeros((B, T, zs.num_states), dtype=dt, device=dev)
+            if controls0 is None:
+                controls0 = torch.zeros((B, T, zs.num_controls), dtype=dt, device=dev)
+            x0 = pack_x(states0.to(dt), controls0.to(dt)).contiguous()
         if m == 0:
             z0 = torch.zeros((B, T, 0), dtype=dt, device=dev)
         elif x_zero:

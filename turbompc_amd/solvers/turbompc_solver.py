@@ -586,8 +586,9 @@ class TurboMPCSolver:
             admm_state0 = admm.initial_state(qp, rho_bar=ap["rho"])  # x = 0 (turbompc_solver.py:1545-1551)
         admm_state = admm_state0
         # per-iteration records, iteration-major so that one iteration's entries
-        # are contiguous: [0] eq violation, [1] ineq violation, [2] convergence error
-        hist = torch.zeros((3, max_iter, B), dtype=dt, device=dev)
+        # are one contiguous (3, B) block, written in place:
+        # [:, 0] eq violation, [:, 1] ineq violation, [:, 2] convergence error
+        hist = torch.zeros((max_iter, 3, B), dtype=dt, device=dev)
         # each step's iteration words (count | TMPC_ITERS_NONFINITE), written
         # by the library into its row; split once after the loop
         words = torch.zeros((max_iter, B), dtype=torch.int32, device=dev)
@@ -619,9 +620,9 @@ class TurboMPCSolver:
                 # the check belongs to the iterate committed at it - 1 (the
                 # records of a stopped problem stay zero, as in the reference)
                 if it == 1:
-                    hist[:, 0] = torch.stack([e, i, cv])
+                    torch.stack([e, i, cv], out=hist[0])
                 else:
-                    hist[:, it - 1] = torch.where(active, torch.stack([e, i, cv]), hist[:, it - 1])
+                    torch.where(active, torch.stack([e, i, cv]), hist[it - 1], out=hist[it - 1])
                 # a stopped problem keeps its iterate, state and QP, so this
                 # check of it repeats, value for value, the one recorded when
                 # it stopped: conv and G x need no masked merge
@@ -640,7 +641,7 @@ class TurboMPCSolver:
         # the last committed iterate is not checked (the reference evaluates no
         # check after its final iteration): its record keeps the previous error
         # and G x at the QP it was solved on
-        hist[2, last] = torch.where(active, conv, hist[2, last])
+        torch.where(active, conv, hist[last, 2], out=hist[last, 2])
         g_last = self._g_of(program, qp, admm_state.x_blocks, states, controls)
         g_c = g_last if g_c is None else torch.where(active[:, None, None], g_last, g_c)
         kkt = self._build_kkt_state(states, controls, admm_state, g_c, qp.ineq.l, qp.ineq.u)
@@ -649,7 +650,7 @@ class TurboMPCSolver:
         return TurboMPCSolution(
             states=states, controls=controls, slack=admm_state.xi_g, status=self.STATUS_SUCCESS, num_iter=num_iter,
             convergence_error=conv, admm_iters=admm_iters, linesearch_alphas=None, admm_state=admm_state,
-            solver_stats=SolverStats(admm_iters, hist[0].t(), hist[1].t(), hist[2].t()), kkt_state=kkt,
+            solver_stats=SolverStats(admm_iters, hist[:, 0].t(), hist[:, 1].t(), hist[:, 2].t()), kkt_state=kkt,
             # the last step scanned every problem's state (stopped ones keep theirs)
             nonfinite=step_words < 0,
         )
