@@ -19,7 +19,7 @@ from __future__ import annotations
 import copy
 import enum
 from pathlib import Path
-from typing import Any, Dict, NamedTuple, Optional, Tuple, Union
+from typing import Any, Dict, NamedTuple, Optional, Union
 
 import torch
 import yaml
