@@ -439,6 +439,56 @@ int tmpc_kkt_active_sets_f64(hipStream_t stream, int64_t count, const double* g,
                              const double* u, const double* y, double eps_abs, double eps_rel, double dual_tol,
                              uint8_t* lower, uint8_t* upper);
 
+/* ---- SQP line search: merit terms -------------------------------------------
+ * Replaces the XLA evaluation of the l1 merit function's terms in
+ * backtracking_linesearch / evaluate_constraints_with_bounds
+ * (turbompc/solvers/linesearch.py:14-178) for the tracking OCP whose
+ * inequality rows are its box rows (cost, :982-1066 and :1504-1515;
+ * equality_constraints, :841-912; step_inequality_constraints, :413-471 of
+ * turbompc/problems/optimal_control_problem.py).  P = copies * B0 problems
+ * (problem p reads the batch's per-problem arrays at row p % B0): states
+ * (P, T, nx), controls (P, T, nu) and next (P, T-1, nx) = the model's step
+ * f(x_t, u_t) are device arrays, as are x0 (B0, nx), u0 (B0, nu) or NULL,
+ * the tracking weights w and reference zref (B0, T, nx+nu), slacks
+ * (P, T, mbox) or NULL, the direction (dstates, dcontrols[, dslacks]) or
+ * NULL, and the outputs cost, dcost (or NULL), eq, iq (P).  The per-row
+ * constants are host arrays: box_idx (mbox <= 32 variable indices < nx+nu),
+ * box_lo, box_hi, and with scaled != 0 box_scale (mbox), state_scale (nx) and
+ * control_scale (nu) (nx, nu <= 64).  Outputs per problem:
+ *   cost = sum w (z - zref)^2 (+ gamma/2 |s|^2), dcost its derivative along
+ *   the direction, eq = |x_0 - x0|_1 + sum_t |f_t - x_{t+1}|_1 (+ |u_0 - u0|_1),
+ *   rows divided by the variable scales when scaled, iq = the l1 violation of
+ *   the box rows (scaled by box_scale when scaled, + slack) against
+ *   [box_lo, box_hi] (scaled alike); NaN propagates into every term. */
+typedef struct {
+  int32_t P, B0, T, nx, nu, mbox;
+  const void* states;
+  const void* controls;
+  const void* next;
+  const void* x0;
+  const void* u0;
+  const void* w;
+  const void* zref;
+  int32_t scaled;
+  const double* state_scale;   /* host (nx) */
+  const double* control_scale; /* host (nu) */
+  const int32_t* box_idx;      /* host (mbox) */
+  const double* box_lo;        /* host (mbox) */
+  const double* box_hi;        /* host (mbox) */
+  const double* box_scale;     /* host (mbox) */
+  const void* slacks;
+  double gamma;
+  const void* dstates;
+  const void* dcontrols;
+  const void* dslacks;
+  void* cost;
+  void* dcost;
+  void* eq;
+  void* iq;
+} tmpc_merit_terms;
+int tmpc_ocp_merit_terms_f32(hipStream_t stream, const tmpc_merit_terms* args);
+int tmpc_ocp_merit_terms_f64(hipStream_t stream, const tmpc_merit_terms* args);
+
 #ifdef __cplusplus
 }
 #endif

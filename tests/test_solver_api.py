@@ -145,3 +145,13 @@ def test_tiled_candidates_equal_the_candidate_loop(case):
     for name in prob.PER_PROBLEM:
         v, tv = getattr(prob, name), getattr(t4, name)
         assert tv.shape[0] == 4 * B and torch.equal(tv[2 * B:3 * B], v), name
+
+
+def test_fused_merit_terms_are_a_gpu_form():
+    """QuadraticTrackingOCP.merit_terms has no CPU path: off the GPU it
+    returns None and the line search evaluates the torch forms."""
+    from turbompc_amd.problems import configs
+
+    prob = configs.config1(B=2)
+    s, c = prob.initial_guess()
+    assert prob.merit_terms(s, c, None) is None

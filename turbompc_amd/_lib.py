@@ -117,6 +117,25 @@ class SqpStep(ctypes.Structure):
     ]
 
 
+class MeritTerms(ctypes.Structure):
+    """tmpc_merit_terms: device arrays as c_void_p, the per-row constants as
+    host arrays (POINTER(c_double) / POINTER(c_int32))."""
+    _PDBL, _PI32 = ctypes.POINTER(ctypes.c_double), ctypes.POINTER(ctypes.c_int32)
+    _fields_ = [(k, ctypes.c_int32) for k in ("P", "B0", "T", "nx", "nu", "mbox")] + [
+        (k, ctypes.c_void_p) for k in ("states", "controls", "next", "x0", "u0", "w", "zref")
+    ] + [
+        ("scaled", ctypes.c_int32),
+        ("state_scale", _PDBL),
+        ("control_scale", _PDBL),
+        ("box_idx", _PI32),
+        ("box_lo", _PDBL),
+        ("box_hi", _PDBL),
+        ("box_scale", _PDBL),
+        ("slacks", ctypes.c_void_p),
+        ("gamma", ctypes.c_double),
+    ] + [(k, ctypes.c_void_p) for k in ("dstates", "dcontrols", "dslacks", "cost", "dcost", "eq", "iq")]
+
+
 # name -> argtypes (restype is int unless listed in _SIZE_FNS)
 _VP, _I32, _U32, _F64, _SZ = ctypes.c_void_p, ctypes.c_int32, ctypes.c_uint32, ctypes.c_double, ctypes.c_size_t
 _PD, _PQ, _PS, _PC, _PSQ = (ctypes.POINTER(t) for t in (Dims, QP, State, AdmmCfg, SqpStep))
@@ -149,6 +168,8 @@ SIGNATURES = {
     "tmpc_adjoint_kkt_f64": [_VP, _PD, _PQ, _VP, _VP, _F64, _I32, _U32, _VP, _SZ],
     "tmpc_sqp_first_order_f32": [_VP, _PD, _PQ, _VP, _VP, _VP, _VP, _VP, _F64, _U32, _VP, _VP, _VP, _VP],
     "tmpc_sqp_first_order_f64": [_VP, _PD, _PQ, _VP, _VP, _VP, _VP, _VP, _F64, _U32, _VP, _VP, _VP, _VP],
+    "tmpc_ocp_merit_terms_f32": [_VP, ctypes.POINTER(MeritTerms)],
+    "tmpc_ocp_merit_terms_f64": [_VP, ctypes.POINTER(MeritTerms)],
     "tmpc_kkt_active_sets_f32": [_VP, ctypes.c_int64, _VP, _VP, _VP, _VP, _F64, _F64, _F64, _VP, _VP],
     "tmpc_kkt_active_sets_f64": [_VP, ctypes.c_int64, _VP, _VP, _VP, _VP, _F64, _F64, _F64, _VP, _VP],
     "tmpc_quadrotor_linearize_f32": [_VP, _I32, _I32, _VP, _VP, _F64, _VP, _VP, _VP],

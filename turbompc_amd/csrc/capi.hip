@@ -20,6 +20,7 @@
 #include "quadrotor.hpp"
 #include "adjoint.hpp"
 #include "sqp.hpp"
+#include "merit.hpp"
 
 // Workspace of tmpc_admm_direct_noalloc: one copy per GPU, at its own device
 // address, held until the process ends.  Host code never uses this name as an
@@ -1315,6 +1316,57 @@ int sqp_check_impl(hipStream_t s, const tmpc_dims* dims, const tmpc_qp* qp, cons
 
 using namespace tmpc;
 
+// ------------------------------------------------------ merit terms ----
+template <typename R>
+int merit_impl(hipStream_t s, const tmpc_merit_terms* m) {
+  if (!m) return TMPC_EBADARG;
+  if (m->P < 0 || m->B0 < 1 || m->P % m->B0 != 0 || m->T < 2 || m->nx < 1 || m->nx > kMeritMaxVars ||
+      m->nu < 0 || m->nu > kMeritMaxVars || m->mbox < 0 || m->mbox > kMeritMaxRows)
+    return TMPC_EBADSHAPE;
+  if (m->P == 0) return TMPC_OK;
+  if (!m->states || (m->nu > 0 && !m->controls) || !m->next || !m->x0 || !m->w || !m->zref || !m->cost || !m->eq ||
+      !m->iq || (m->dstates && m->nu > 0 && !m->dcontrols) || (m->dslacks && !m->slacks))
+    return TMPC_EBADARG;
+  if (m->mbox > 0 && (!m->box_idx || !m->box_lo || !m->box_hi)) return TMPC_EBADARG;
+  if (m->scaled && (!m->state_scale || (m->nu > 0 && !m->control_scale) || (m->mbox > 0 && !m->box_scale)))
+    return TMPC_EBADARG;
+  MeritArgs<R> a{};
+  a.P = m->P; a.B0 = m->B0; a.T = m->T; a.nx = m->nx; a.nu = m->nu; a.mbox = m->mbox;
+  a.states = static_cast<const R*>(m->states);
+  a.controls = static_cast<const R*>(m->controls);
+  a.next = static_cast<const R*>(m->next);
+  a.x0 = static_cast<const R*>(m->x0);
+  a.u0 = static_cast<const R*>(m->u0);
+  a.w = static_cast<const R*>(m->w);
+  a.zref = static_cast<const R*>(m->zref);
+  a.scaled = m->scaled ? 1 : 0;
+  for (int j = 0; j < m->mbox; ++j) {
+    if (m->box_idx[j] < 0 || m->box_idx[j] >= m->nx + m->nu) return TMPC_EBADARG;
+    a.box_idx[j] = m->box_idx[j];
+    a.box_lo[j] = (R)m->box_lo[j];
+    a.box_hi[j] = (R)m->box_hi[j];
+    a.box_scale[j] = m->scaled ? (R)m->box_scale[j] : R(1);
+  }
+  if (m->scaled) {
+    for (int k = 0; k < m->nx; ++k) a.sscale[k] = (R)m->state_scale[k];
+    for (int k = 0; k < m->nu; ++k) a.cscale[k] = (R)m->control_scale[k];
+  }
+  a.slacks = static_cast<const R*>(m->slacks);
+  a.gamma = (R)m->gamma;
+  a.dstates = static_cast<const R*>(m->dstates);
+  a.dcontrols = static_cast<const R*>(m->dcontrols);
+  a.dslacks = static_cast<const R*>(m->dslacks);
+  a.cost = static_cast<R*>(m->cost);
+  a.dcost = static_cast<R*>(m->dcost);
+  a.eq = static_cast<R*>(m->eq);
+  a.iq = static_cast<R*>(m->iq);
+  constexpr int per_block = 256 / kWave;
+  const long long grid = ((long long)m->P + per_block - 1) / per_block;
+  if (grid > 0x7fffffffLL) return TMPC_EBADSHAPE;
+  hipLaunchKernelGGL((ocp_merit_terms_kernel<R>), dim3((unsigned)grid), dim3(256), 0, s, a);
+  return launch_status();
+}
+
 // ----------------------------------------------------------- KKT state ----
 template <typename R>
 int kkt_active_sets_impl(hipStream_t s, int64_t count, const R* g, const R* l, const R* u, const R* y,
@@ -1554,6 +1606,9 @@ int tmpc_obstacle_lagrangian_hessian_f64(hipStream_t s, int32_t B, int32_t N, in
                                          double* H) {
   return obstacle_hess_impl<double>(s, B, N, nx, nu, dim, K, states, centers, radii, m, row0, mus, H);
 }
+
+int tmpc_ocp_merit_terms_f32(hipStream_t s, const tmpc_merit_terms* args) { return merit_impl<float>(s, args); }
+int tmpc_ocp_merit_terms_f64(hipStream_t s, const tmpc_merit_terms* args) { return merit_impl<double>(s, args); }
 
 int tmpc_kkt_active_sets_f32(hipStream_t s, int64_t count, const float* g, const float* l, const float* u,
                              const float* y, double eps_abs, double eps_rel, double dual_tol, uint8_t* lower,

@@ -1,0 +1,140 @@
+// Terms of the l1 merit function of the SQP line search, one wavefront per
+// problem (turbompc/solvers/linesearch.py:14-178 over the tracking OCP's
+// cost, equality_constraints and step_inequality_constraints,
+// turbompc/problems/optimal_control_problem.py:413-471, :841-912, :982-1066,
+// :1504-1515).
+//
+// For problem p of P (the line search passes its step candidates as
+// k copies of the batch, copy j at p = j B0 + b, so every per-problem input
+// of the batch is read at b = p % B0):
+//   cost  = sum_t,k w (z - zref)^2                       (+ gamma/2 |s|^2)
+//   dcost = sum_t,k 2 w (z - zref) dz                     (+ gamma s . ds)
+//   eq    = |x_0 - x0|_1 + sum_t |f(x_t, u_t) - x_{t+1}|_1 (+ |u_0 - u0|_1),
+//           each row divided by its variable's scale with rescaling
+//   iq    = sum_t,j max(lo_j - g, 0) + max(g - hi_j, 0),  g = r_j z[idx_j] (+ s),
+//           lo and hi scaled by the same r_j
+// with f(x_t, u_t) given (the model's step, evaluated by its own kernel).
+// Every term is formed as the elementwise torch form forms it (the product
+// (w e) e, the scaled bounds); only the order of the sums differs.
+#pragma once
+#include "common.hpp"
+
+namespace tmpc {
+
+constexpr int kMeritMaxRows = 32;  // box rows
+constexpr int kMeritMaxVars = 64;  // nx and nu (the row scales)
+
+// The per-row constants travel by value in the kernel arguments, so that the
+// host validates the box rows' variable indices before the launch.
+template <typename R>
+struct MeritArgs {
+  int P, B0, T, nx, nu, mbox;
+  const R* states;    // (P, T, nx)
+  const R* controls;  // (P, T, nu)
+  const R* next;      // (P, T - 1, nx)
+  const R* x0;        // (B0, nx)
+  const R* u0;        // (B0, nu) or null: no initial-control rows
+  const R* w;         // (B0, T, nx + nu)
+  const R* zref;      // (B0, T, nx + nu)
+  int scaled;         // equality rows divided by sscale (u0 rows by cscale), box rows scaled
+  R sscale[kMeritMaxVars], cscale[kMeritMaxVars];
+  int box_idx[kMeritMaxRows];  // variable of each box row, < nx + nu
+  R box_lo[kMeritMaxRows], box_hi[kMeritMaxRows], box_scale[kMeritMaxRows];
+  const R* slacks;    // (P, T, mbox) or null
+  R gamma;            // slack penalization weight
+  const R* dstates;   // (P, T, nx) or null: no directional derivative
+  const R* dcontrols; // (P, T, nu)
+  const R* dslacks;   // (P, T, mbox) or null
+  R* cost;
+  R* dcost;           // may be null
+  R* eq;
+  R* iq;
+};
+
+// clamp(x, min=0) as torch evaluates it: a NaN stays NaN (a candidate with a
+// NaN row must not look feasible)
+template <typename R>
+__device__ __forceinline__ R clamp0(R x) {
+  return x < R(0) ? R(0) : x;
+}
+
+template <typename R>
+__global__ __launch_bounds__(256) void ocp_merit_terms_kernel(MeritArgs<R> a) {
+  const int p = (int)(blockIdx.x * (blockDim.x / kWave) + threadIdx.x / kWave);
+  const int lane = (int)(threadIdx.x % kWave);
+  if (p >= a.P) return;  // whole wavefronts: the sums below need every lane of one
+  const int b = p % a.B0, T = a.T, nx = a.nx, nu = a.nu, n = nx + nu, N = T - 1;
+  const R* xs = a.states + (size_t)p * T * nx;
+  const R* us = a.controls + (size_t)p * T * nu;
+  const R* wb = a.w + (size_t)b * T * n;
+  const R* rb = a.zref + (size_t)b * T * n;
+  R c = R(0), dc = R(0), e = R(0), q = R(0);
+  // cost and its directional derivative over the T n entries
+  for (int i = lane; i < T * n; i += kWave) {
+    const int t = i / n, k = i - t * n;
+    const R z = k < nx ? xs[t * nx + k] : us[t * nu + (k - nx)];
+    const R d = z - rb[i];
+    const R wd = wb[i] * d;
+    c += wd * d;
+    if (a.dstates != nullptr) {
+      const R dz = k < nx ? a.dstates[(size_t)p * T * nx + t * nx + k]
+                          : a.dcontrols[(size_t)p * T * nu + t * nu + (k - nx)];
+      dc += (R(2) * wb[i]) * d * dz;
+    }
+  }
+  // equality rows: x_0 - x0, then f(x_t, u_t) - x_{t+1}
+  const R* nb = a.next + (size_t)p * N * nx;
+  for (int i = lane; i < T * nx; i += kWave) {
+    const int t = i / nx, k = i - t * nx;
+    R h = t == 0 ? xs[k] - a.x0[(size_t)b * nx + k] : nb[(t - 1) * nx + k] - xs[t * nx + k];
+    if (a.scaled) h = h / a.sscale[k];
+    e += rabs(h);
+  }
+  if (a.u0 != nullptr) {
+    for (int k = lane; k < nu; k += kWave) {
+      R h = us[k] - a.u0[(size_t)b * nu + k];
+      if (a.scaled) h = h / a.cscale[k];
+      e += rabs(h);
+    }
+  }
+  // box rows (+ slack) against their bounds
+  for (int i = lane; i < T * a.mbox; i += kWave) {
+    const int t = i / a.mbox, j = i - t * a.mbox;
+    const int v = a.box_idx[j];
+    R g = v < nx ? xs[t * nx + v] : us[t * nu + (v - nx)];
+    R lo = a.box_lo[j], hi = a.box_hi[j];
+    if (a.scaled) {
+      const R r = a.box_scale[j];
+      g = g * r;
+      lo = lo * r;
+      hi = hi * r;
+    }
+    if (a.slacks != nullptr) g = g + a.slacks[(size_t)p * T * a.mbox + i];
+    q += clamp0(lo - g) + clamp0(g - hi);
+  }
+  if (a.slacks != nullptr) {
+    R ss = R(0), sd = R(0);
+    for (int i = lane; i < T * a.mbox; i += kWave) {
+      const R s = a.slacks[(size_t)p * T * a.mbox + i];
+      ss += s * s;
+      if (a.dslacks != nullptr) sd += s * a.dslacks[(size_t)p * T * a.mbox + i];
+    }
+    ss = wave_sum(ss);
+    sd = wave_sum(sd);
+    c = wave_sum(c) + (R(0.5) * a.gamma) * ss;
+    dc = wave_sum(dc) + a.gamma * sd;
+  } else {
+    c = wave_sum(c);
+    dc = wave_sum(dc);
+  }
+  e = wave_sum(e);
+  q = wave_sum(q);
+  if (lane == 0) {
+    a.cost[p] = c;
+    if (a.dcost != nullptr) a.dcost[p] = dc;
+    a.eq[p] = e;
+    a.iq[p] = q;
+  }
+}
+
+}  // namespace tmpc

@@ -20,6 +20,7 @@ Every tensor has a leading batch axis B.  Subclasses provide the dynamics.
 """
 from __future__ import annotations
 
+import ctypes
 from typing import Dict, Optional, Tuple
 
 import torch
@@ -280,6 +281,72 @@ class QuadraticTrackingOCP:
             r = self.box_row_scale()
             g, lo, hi = g * r, lo * r, hi * r
         return g, lo, hi
+
+    def _merit_host_constants(self):
+        """The per-row constants of tmpc_ocp_merit_terms_* as host ctypes
+        arrays (read back once per problem object)."""
+        def make():
+            rows, _, lo, hi = self._box_rows()
+            m = len(rows)
+            dbl = lambda v: (ctypes.c_double * max(len(v), 1))(*[float(x) for x in v])  # noqa: E731
+            out = {"mbox": m, "box_idx": (ctypes.c_int32 * max(m, 1))(*rows),
+                   "box_lo": dbl(lo.tolist()), "box_hi": dbl(hi.tolist())}
+            if self.rescale_optimization_variables:
+                out.update(box_scale=dbl(self.box_row_scale().tolist()),
+                           state_scale=dbl(self.state_diff.tolist()), control_scale=dbl(self.control_diff.tolist()))
+            return out
+        return self._memoized("merit_host", make)
+
+    def merit_terms(self, states, controls, slacks=None, dstates=None, dcontrols=None, dslacks=None,
+                    copies: int = 1):
+        """(cost, |h|_1, |viol|_1, dcost or None), each (copies B,), for
+        `copies` stacked batches (copy j at rows j B .. j B + B - 1) in one
+        kernel (tmpc_ocp_merit_terms_*): the terms the merit line search
+        takes from cost, cost_directional_derivative and
+        evaluate_constraints_with_bounds (linesearch.py:14-178), the
+        dynamics residuals from next_states.  None where this problem
+        defines those terms otherwise (a subclass with inequality rows
+        beyond the box rows, or its own cost or residuals), where the
+        shapes exceed the kernel's limits, or off the GPU: the caller then
+        evaluates the torch forms."""
+        base = QuadraticTrackingOCP
+        if not (states.is_cuda and type(self).inequality_values is base.inequality_values
+                and type(self).cost is base.cost and type(self).equality_residuals is base.equality_residuals
+                and type(self).cost_directional_derivative is base.cost_directional_derivative):
+            return None
+        nx, nu = self.num_state_variables, self.num_control_variables
+        hc = self._merit_host_constants()
+        if nx > 64 or nu > 64 or hc["mbox"] > 32 or states.shape[0] != copies * self.B:
+            return None
+        from .. import _lib
+
+        dt, dev = self.dtype, states.device
+        P, T = states.shape[0], states.shape[1]
+        c = lambda t: t.to(device=dev, dtype=dt).contiguous() if t is not None else None  # noqa: E731
+        states, controls = c(states), c(controls)
+        nxt = (self.tile(copies) if copies > 1 else self).next_states(states, controls).to(dt).contiguous()
+        w, zref = (c(t) for t in self.tracking_weights())
+        soft = self.use_slack_variables and slacks is not None and slacks.numel() > 0
+        slacks = c(slacks) if soft else None
+        dstates, dcontrols = c(dstates), c(dcontrols)
+        dslacks = c(dslacks) if soft and dslacks is not None else None
+        x0 = c(self.x0)
+        u0 = c(self.u0) if self.constrain_initial_control else None
+        cost, eq, iq = (torch.empty(P, dtype=dt, device=dev) for _ in range(3))
+        dcost = torch.empty(P, dtype=dt, device=dev) if dstates is not None else None
+        args = _lib.MeritTerms(P=P, B0=self.B, T=T, nx=nx, nu=nu, mbox=hc["mbox"], states=_lib.ptr(states),
+                               controls=_lib.ptr(controls), next=_lib.ptr(nxt), x0=_lib.ptr(x0), u0=_lib.ptr(u0),
+                               w=_lib.ptr(w), zref=_lib.ptr(zref),
+                               scaled=1 if self.rescale_optimization_variables else 0,
+                               state_scale=hc.get("state_scale"), control_scale=hc.get("control_scale"),
+                               box_idx=hc["box_idx"], box_lo=hc["box_lo"], box_hi=hc["box_hi"],
+                               box_scale=hc.get("box_scale"), slacks=_lib.ptr(slacks),
+                               gamma=float(self.slack_penalization_weight), dstates=_lib.ptr(dstates),
+                               dcontrols=_lib.ptr(dcontrols), dslacks=_lib.ptr(dslacks), cost=_lib.ptr(cost),
+                               dcost=_lib.ptr(dcost), eq=_lib.ptr(eq), iq=_lib.ptr(iq))
+        fn = f"tmpc_ocp_merit_terms_{_lib.suffix(dt)}"
+        _lib.check(fn, getattr(_lib.load(), fn)(_lib.stream_handle(dev), ctypes.byref(args)))
+        return cost, eq, iq, dcost
 
     # -------------------------------------------------------- parameters ----
     WEIGHT_KEYS = (

@@ -38,15 +38,28 @@ def evaluate_constraints_with_bounds(program, states, controls, slacks, problem_
     return eq, viol.flatten(1).sum(dim=1), g, lo, hi
 
 
+def _merit_terms(program, states, controls, slacks, ds=None, dc=None, dsl=None, copies=1):
+    """(cost, |h|_1, |viol|_1, dcost or None) from the problem's fused
+    evaluation (QuadraticTrackingOCP.merit_terms: one kernel), or None where
+    it has none for this problem."""
+    fn = getattr(program, "merit_terms", None)
+    return fn(states, controls, slacks, ds, dc, dsl, copies=copies) if fn is not None else None
+
+
 def _candidate_merits(program, alphas, a_t, states, controls, slacks, ds, dc, dsl, mu):
     """(B, n_alpha): merit(z + alpha dz) for every candidate.  A program that
     can tile its batch (QuadraticTrackingOCP.tile) evaluates all candidates in
-    one pass over n_alpha B problems, candidate j at rows j B .. j B + B - 1;
-    others are evaluated one candidate at a time."""
+    one pass over n_alpha B problems, candidate j at rows j B .. j B + B - 1
+    (its terms in one kernel where the problem has one); others are evaluated
+    one candidate at a time."""
     A, B = len(alphas), states.shape[0]
     if hasattr(program, "tile"):
         stack = lambda z, dz: (z[None] + a_t.view(A, *([1] * z.dim())) * dz[None]).flatten(0, 1)  # noqa: E731
         s_a, c_a, sl_a = stack(states, ds), stack(controls, dc), stack(slacks, dsl)
+        fused = _merit_terms(program, s_a, c_a, sl_a, copies=A)
+        if fused is not None:
+            cost_a, e_a, i_a, _ = fused
+            return (cost_a + mu.repeat(A) * (e_a + i_a)).view(A, B).t()
         tiled = program.tile(A)
         e_a, i_a, *_ = evaluate_constraints_with_bounds(tiled, s_a, c_a, sl_a)
         m = tiled.cost(s_a, c_a, sl_a) + mu.repeat(A) * (e_a + i_a)
@@ -71,9 +84,13 @@ def backtracking_linesearch(program, problem_params, solver_params: Dict[str, An
     floor = float(solver_params.get("linesearch_constraint_floor", 1.0e-8))
     ds, dc, dsl = states_new - states, controls_new - controls, slacks_new - slacks
 
-    cost = program.cost(states, controls, slacks)
-    dcost = program.cost_directional_derivative(states, controls, slacks, ds, dc, dsl)
-    eq, iq, *_ = evaluate_constraints_with_bounds(program, states, controls, slacks)
+    fused = _merit_terms(program, states, controls, slacks, ds, dc, dsl)
+    if fused is not None:
+        cost, eq, iq, dcost = fused
+    else:
+        cost = program.cost(states, controls, slacks)
+        dcost = program.cost_directional_derivative(states, controls, slacks, ds, dc, dsl)
+        eq, iq, *_ = evaluate_constraints_with_bounds(program, states, controls, slacks)
     cl1 = eq + iq
     mu_raw = dcost / (0.5 * torch.clamp(cl1, min=floor))
     mu = torch.clamp(torch.nan_to_num(mu_raw, nan=mu_min, posinf=mu_max, neginf=mu_min), mu_min, mu_max)
