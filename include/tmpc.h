@@ -459,7 +459,13 @@ int tmpc_kkt_active_sets_f64(hipStream_t stream, int64_t count, const double* g,
  *   the direction, eq = |x_0 - x0|_1 + sum_t |f_t - x_{t+1}|_1 (+ |u_0 - u0|_1),
  *   rows divided by the variable scales when scaled, iq = the l1 violation of
  *   the box rows (scaled by box_scale when scaled, + slack) against
- *   [box_lo, box_hi] (scaled alike); NaN propagates into every term. */
+ *   [box_lo, box_hi] (scaled alike), then with nobs > 0 of the obstacle rows
+ *   of OptimalControlProblemObstacle (obstacle_avoidance.py:16-52):
+ *   g_k = 1 - |p_t - c_k| / (r_k + 0.001) with p_t the first dim (<= nx)
+ *   state coordinates, bounds (-1e9, 0), all scaled by obs_scale when scaled;
+ *   centers (B0, nobs, dim) and radii (B0, nobs) are device arrays (nobs <=
+ *   32), and slacks then cover mbox + nobs rows.  NaN propagates into every
+ *   term. */
 typedef struct {
   int32_t P, B0, T, nx, nu, mbox;
   const void* states;
@@ -485,6 +491,10 @@ typedef struct {
   void* dcost;
   void* eq;
   void* iq;
+  int32_t nobs, dim;
+  const void* centers;
+  const void* radii;
+  double obs_scale;
 } tmpc_merit_terms;
 int tmpc_ocp_merit_terms_f32(hipStream_t stream, const tmpc_merit_terms* args);
 int tmpc_ocp_merit_terms_f64(hipStream_t stream, const tmpc_merit_terms* args);

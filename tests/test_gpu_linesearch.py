@@ -144,6 +144,14 @@ def _merit_cases(dtype):
         initial_control=torch.full((6, 4), hov, dtype=dtype), **lim)
     yield "config 1 soft", configs.config1(B=6, seed=2, use_slack_variables=True,
                                            slack_penalization_weight=30.0).to("cuda", dtype)
+    yield "config 4 (obstacle rows)", configs.config4(B=6, seed=1).to("cuda", dtype)
+    lim4 = dict(rescale_optimization_variables=True,
+                state_rescaling_min=torch.tensor([-4.0] * 3 + [-2.0] * 3, dtype=torch.float64),
+                state_rescaling_max=torch.tensor([4.0, 5.0, 3.0] + [2.0] * 3, dtype=torch.float64),
+                control_rescaling_min=torch.full((3,), -3.0, dtype=torch.float64),
+                control_rescaling_max=torch.full((3,), 3.0, dtype=torch.float64))
+    yield "config 4 soft rescaled", configs.config4(B=6, seed=2, use_slack_variables=True,
+                                                    slack_penalization_weight=50.0, **lim4).to("cuda", dtype)
 
 
 @pytest.mark.parametrize("dtype", [torch.float64, torch.float32])
@@ -153,7 +161,7 @@ def test_fused_merit_terms_match_torch_forms(dtype):
     (linesearch.py:14-52): the same terms up to the order of the sums, for one
     batch and for four stacked copies (the line search's candidates); a NaN in
     an iterate reaches every term it enters; problems with other inequality
-    rows (config 4's obstacles) have no fused form."""
+    rows than the fused form knows have none."""
     tol = 1e-12 if dtype == torch.float64 else 2e-5
     for name, prob in _merit_cases(dtype):
         gen = torch.Generator().manual_seed(5)
@@ -161,7 +169,7 @@ def test_fused_merit_terms_match_torch_forms(dtype):
         B, T = s0.shape[:2]
         rnd = lambda shape, k: (k * torch.randn(shape, generator=gen, dtype=torch.float64)).to("cuda", dtype)  # noqa: E731
         s, c = s0 + rnd(s0.shape, 0.3), c0 + rnd(c0.shape, 0.5)
-        m = len(prob._box_rows()[0])
+        m = prob.num_inequality_constraints
         sl = rnd((B, T, m), 0.2) if prob.use_slack_variables else torch.zeros((B, T, m), dtype=dtype, device="cuda")
         ds, dc, dsl = rnd(s.shape, 0.1), rnd(c.shape, 0.1), rnd((B, T, m), 0.1)
         got = prob.merit_terms(s, c, sl, ds, dc, dsl)
@@ -188,6 +196,11 @@ def test_fused_merit_terms_match_torch_forms(dtype):
     s[2, 5, 1] = float("nan")
     cost, eq, iq, _ = prob.merit_terms(s, c, None)
     assert torch.isnan(cost[2]) and torch.isnan(eq[2]) and torch.isfinite(cost[[0, 1, 3]]).all()
-    # no fused form where the inequality rows are not the box rows alone
-    p4 = configs.config4(B=4, seed=1).to("cuda", dtype)
-    assert p4.merit_terms(*p4.initial_guess(), None) is None
+    # no fused form for a problem that defines its inequality rows otherwise
+    class OtherRows(type(prob)):
+        def inequality_values(self, states, controls):
+            return super().inequality_values(states, controls)
+
+    other = copy.copy(prob)
+    other.__class__ = OtherRows
+    assert other.merit_terms(*other.initial_guess(), None) is None

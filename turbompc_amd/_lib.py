@@ -133,7 +133,13 @@ class MeritTerms(ctypes.Structure):
         ("box_scale", _PDBL),
         ("slacks", ctypes.c_void_p),
         ("gamma", ctypes.c_double),
-    ] + [(k, ctypes.c_void_p) for k in ("dstates", "dcontrols", "dslacks", "cost", "dcost", "eq", "iq")]
+    ] + [(k, ctypes.c_void_p) for k in ("dstates", "dcontrols", "dslacks", "cost", "dcost", "eq", "iq")] + [
+        ("nobs", ctypes.c_int32),
+        ("dim", ctypes.c_int32),
+        ("centers", ctypes.c_void_p),
+        ("radii", ctypes.c_void_p),
+        ("obs_scale", ctypes.c_double),
+    ]
 
 
 # name -> argtypes (restype is int unless listed in _SIZE_FNS)

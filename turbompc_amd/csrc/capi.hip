@@ -1328,6 +1328,9 @@ int merit_impl(hipStream_t s, const tmpc_merit_terms* m) {
       !m->iq || (m->dstates && m->nu > 0 && !m->dcontrols) || (m->dslacks && !m->slacks))
     return TMPC_EBADARG;
   if (m->mbox > 0 && (!m->box_idx || !m->box_lo || !m->box_hi)) return TMPC_EBADARG;
+  if (m->nobs < 0 || m->nobs > kMeritMaxObstacles || (m->nobs > 0 && (m->dim < 1 || m->dim > m->nx)))
+    return TMPC_EBADSHAPE;
+  if (m->nobs > 0 && (!m->centers || !m->radii)) return TMPC_EBADARG;
   if (m->scaled && (!m->state_scale || (m->nu > 0 && !m->control_scale) || (m->mbox > 0 && !m->box_scale)))
     return TMPC_EBADARG;
   MeritArgs<R> a{};
@@ -1351,6 +1354,11 @@ int merit_impl(hipStream_t s, const tmpc_merit_terms* m) {
     for (int k = 0; k < m->nx; ++k) a.sscale[k] = (R)m->state_scale[k];
     for (int k = 0; k < m->nu; ++k) a.cscale[k] = (R)m->control_scale[k];
   }
+  a.nobs = m->nobs;
+  a.dim = m->nobs > 0 ? m->dim : 0;
+  a.centers = static_cast<const R*>(m->centers);
+  a.radii = static_cast<const R*>(m->radii);
+  a.obs_scale = m->scaled && m->nobs > 0 ? (R)m->obs_scale : R(1);
   a.slacks = static_cast<const R*>(m->slacks);
   a.gamma = (R)m->gamma;
   a.dstates = static_cast<const R*>(m->dstates);

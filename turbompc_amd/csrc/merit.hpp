@@ -11,8 +11,12 @@
 //   dcost = sum_t,k 2 w (z - zref) dz                     (+ gamma s . ds)
 //   eq    = |x_0 - x0|_1 + sum_t |f(x_t, u_t) - x_{t+1}|_1 (+ |u_0 - u0|_1),
 //           each row divided by its variable's scale with rescaling
-//   iq    = sum_t,j max(lo_j - g, 0) + max(g - hi_j, 0),  g = r_j z[idx_j] (+ s),
-//           lo and hi scaled by the same r_j
+//   iq    = sum_t,j max(lo_j - g, 0) + max(g - hi_j, 0) over the box rows,
+//           g = r_j z[idx_j] (+ s), lo and hi scaled by the same r_j, then
+//           over the obstacle rows (when given, OptimalControlProblemObstacle,
+//           turbompc/problems/obstacle_avoidance.py:16-52)
+//           g = ro (1 - |p_t - c_k| / (r_k + 0.001)) (+ s), bounds ro (-1e9, 0),
+//           p_t the first `dim` state coordinates
 // with f(x_t, u_t) given (the model's step, evaluated by its own kernel).
 // Every term is formed as the elementwise torch form forms it (the product
 // (w e) e, the scaled bounds); only the order of the sums differs.
@@ -22,6 +26,7 @@
 namespace tmpc {
 
 constexpr int kMeritMaxRows = 32;  // box rows
+constexpr int kMeritMaxObstacles = 32;
 constexpr int kMeritMaxVars = 64;  // nx and nu (the row scales)
 
 // The per-row constants travel by value in the kernel arguments, so that the
@@ -40,7 +45,11 @@ struct MeritArgs {
   R sscale[kMeritMaxVars], cscale[kMeritMaxVars];
   int box_idx[kMeritMaxRows];  // variable of each box row, < nx + nu
   R box_lo[kMeritMaxRows], box_hi[kMeritMaxRows], box_scale[kMeritMaxRows];
-  const R* slacks;    // (P, T, mbox) or null
+  int nobs, dim;      // obstacle rows after the box rows (0: none), position coordinates
+  const R* centers;   // (B0, nobs, dim)
+  const R* radii;     // (B0, nobs)
+  R obs_scale;        // ro (1 without rescaling)
+  const R* slacks;    // (P, T, mbox + nobs) or null
   R gamma;            // slack penalization weight
   const R* dstates;   // (P, T, nx) or null: no directional derivative
   const R* dcontrols; // (P, T, nu)
@@ -97,27 +106,49 @@ __global__ __launch_bounds__(256) void ocp_merit_terms_kernel(MeritArgs<R> a) {
       e += rabs(h);
     }
   }
-  // box rows (+ slack) against their bounds
-  for (int i = lane; i < T * a.mbox; i += kWave) {
-    const int t = i / a.mbox, j = i - t * a.mbox;
-    const int v = a.box_idx[j];
-    R g = v < nx ? xs[t * nx + v] : us[t * nu + (v - nx)];
-    R lo = a.box_lo[j], hi = a.box_hi[j];
-    if (a.scaled) {
-      const R r = a.box_scale[j];
-      g = g * r;
-      lo = lo * r;
-      hi = hi * r;
+  // inequality rows (+ slack) against their bounds: the box rows, then the
+  // obstacle rows of each stage
+  const int mr = a.mbox + a.nobs;
+  for (int i = lane; i < T * mr; i += kWave) {
+    const int t = i / mr, j = i - t * mr;
+    R g, lo, hi;
+    if (j < a.mbox) {
+      const int v = a.box_idx[j];
+      g = v < nx ? xs[t * nx + v] : us[t * nu + (v - nx)];
+      lo = a.box_lo[j];
+      hi = a.box_hi[j];
+      if (a.scaled) {
+        const R r = a.box_scale[j];
+        g = g * r;
+        lo = lo * r;
+        hi = hi * r;
+      }
+    } else {
+      const int k = j - a.mbox;
+      const R* ck = a.centers + ((size_t)b * a.nobs + k) * a.dim;
+      R d2 = R(0);
+      for (int c = 0; c < a.dim; ++c) {
+        const R dc = xs[t * nx + c] - ck[c];
+        d2 += dc * dc;
+      }
+      g = R(1) - rsqrt_(d2) / (a.radii[(size_t)b * a.nobs + k] + R(0.001));
+      lo = R(-1.0e9);
+      hi = R(0);
+      if (a.scaled) {
+        g = g * a.obs_scale;
+        lo = lo * a.obs_scale;
+        hi = hi * a.obs_scale;
+      }
     }
-    if (a.slacks != nullptr) g = g + a.slacks[(size_t)p * T * a.mbox + i];
+    if (a.slacks != nullptr) g = g + a.slacks[(size_t)p * T * mr + i];
     q += clamp0(lo - g) + clamp0(g - hi);
   }
   if (a.slacks != nullptr) {
     R ss = R(0), sd = R(0);
-    for (int i = lane; i < T * a.mbox; i += kWave) {
-      const R s = a.slacks[(size_t)p * T * a.mbox + i];
+    for (int i = lane; i < T * mr; i += kWave) {
+      const R s = a.slacks[(size_t)p * T * mr + i];
       ss += s * s;
-      if (a.dslacks != nullptr) sd += s * a.dslacks[(size_t)p * T * a.mbox + i];
+      if (a.dslacks != nullptr) sd += s * a.dslacks[(size_t)p * T * mr + i];
     }
     ss = wave_sum(ss);
     sd = wave_sum(sd);

@@ -91,6 +91,18 @@ class ObstacleOCP(LinearOCP):
             go, glo, ghi = go * ro, glo * ro, ghi * ro
         return torch.cat([g, go], dim=-1), torch.cat([lo, glo], dim=-1), torch.cat([hi, ghi], dim=-1)
 
+    _merit_rows_form = inequality_values  # the fused merit terms' obstacle rows reproduce it
+
+    def _merit_obstacle_rows(self):
+        """The obstacle rows of inequality_values for the fused merit terms; the
+        row scale 1 / mean(state_diff[:dim]) read back once per problem."""
+        def make():
+            if not self.rescale_optimization_variables:
+                return 1.0
+            return float(1.0 / self.state_diff[: self.obstacles_dimension].mean())
+        return {"nobs": self.num_obstacles, "dim": self.obstacles_dimension, "centers": self.centers,
+                "radii": self.radii, "scale": self._memoized("merit_obs_scale", make)}
+
     def inequality_lagrangian_hessian(self, states, controls, mus):
         """(B, T, n, n): sum_k mu_k d^2 g_k/dz^2 of the obstacle rows (box rows are linear)."""
         states = states.to(self.dtype).contiguous()

@@ -282,6 +282,10 @@ class QuadraticTrackingOCP:
             g, lo, hi = g * r, lo * r, hi * r
         return g, lo, hi
 
+    # the inequality_values form the fused merit terms reproduce (a subclass
+    # that defines its own rows and has no fused form falls back to torch)
+    _merit_rows_form = inequality_values
+
     def _merit_host_constants(self):
         """The per-row constants of tmpc_ocp_merit_terms_* as host ctypes
         arrays (read back once per problem object)."""
@@ -297,6 +301,11 @@ class QuadraticTrackingOCP:
             return out
         return self._memoized("merit_host", make)
 
+    def _merit_obstacle_rows(self):
+        """The obstacle rows that follow the box rows in the fused merit terms
+        (dict nobs, dim, centers, radii, scale), or None: none here."""
+        return None
+
     def merit_terms(self, states, controls, slacks=None, dstates=None, dcontrols=None, dslacks=None,
                     copies: int = 1):
         """(cost, |h|_1, |viol|_1, dcost or None), each (copies B,), for
@@ -309,14 +318,16 @@ class QuadraticTrackingOCP:
         beyond the box rows, or its own cost or residuals), where the
         shapes exceed the kernel's limits, or off the GPU: the caller then
         evaluates the torch forms."""
-        base = QuadraticTrackingOCP
-        if not (states.is_cuda and type(self).inequality_values is base.inequality_values
-                and type(self).cost is base.cost and type(self).equality_residuals is base.equality_residuals
-                and type(self).cost_directional_derivative is base.cost_directional_derivative):
+        base, cls = QuadraticTrackingOCP, type(self)
+        if not (states.is_cuda and cls.inequality_values is cls._merit_rows_form
+                and cls.cost is base.cost and cls.equality_residuals is base.equality_residuals
+                and cls.cost_directional_derivative is base.cost_directional_derivative):
             return None
         nx, nu = self.num_state_variables, self.num_control_variables
         hc = self._merit_host_constants()
-        if nx > 64 or nu > 64 or hc["mbox"] > 32 or states.shape[0] != copies * self.B:
+        obs = self._merit_obstacle_rows()
+        if (nx > 64 or nu > 64 or hc["mbox"] > 32 or states.shape[0] != copies * self.B
+                or (obs is not None and obs["nobs"] > 32)):
             return None
         from .. import _lib
 
@@ -344,6 +355,9 @@ class QuadraticTrackingOCP:
                                gamma=float(self.slack_penalization_weight), dstates=_lib.ptr(dstates),
                                dcontrols=_lib.ptr(dcontrols), dslacks=_lib.ptr(dslacks), cost=_lib.ptr(cost),
                                dcost=_lib.ptr(dcost), eq=_lib.ptr(eq), iq=_lib.ptr(iq))
+        if obs is not None:
+            args.nobs, args.dim, args.obs_scale = obs["nobs"], obs["dim"], obs["scale"]
+            args.centers, args.radii = _lib.ptr(c(obs["centers"])), _lib.ptr(c(obs["radii"]))
         fn = f"tmpc_ocp_merit_terms_{_lib.suffix(dt)}"
         _lib.check(fn, getattr(_lib.load(), fn)(_lib.stream_handle(dev), ctypes.byref(args)))
         return cost, eq, iq, dcost
