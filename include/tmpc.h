@@ -499,6 +499,27 @@ typedef struct {
 int tmpc_ocp_merit_terms_f32(hipStream_t stream, const tmpc_merit_terms* args);
 int tmpc_ocp_merit_terms_f64(hipStream_t stream, const tmpc_merit_terms* args);
 
+/* The step choice of backtracking_linesearch (turbompc/solvers/linesearch.py:54-178)
+ * from merit terms (the outputs of tmpc_ocp_merit_terms_* for the base point,
+ * cost, dcost, eq, iq (B), and for the A <= 8 candidates, cost_a, eq_a, iq_a
+ * (A B, candidate j of problem b at j B + b)), the candidate steps alphas
+ * (host, A) and the parameters eta, mu_min, mu_max and the constraint floor:
+ * mu = clip(nan_to_num(dcost / (0.5 max(eq + iq, floor))), mu_min, mu_max);
+ * alpha_out[b] = the largest alpha_j whose merit decrease
+ * cand_j - (merit + eta alpha_j (dcost - mu (eq + iq))) is finite and <= 0,
+ * else the finite candidate of least merit (the first of equal ones), else
+ * alpha_0; mu_out (B, or NULL) receives mu.  Every value is rounded as the
+ * elementwise form rounds it (one rounding per operation; eta alpha_j is the
+ * double product rounded), so the choice equals that form's. */
+int tmpc_linesearch_choose_f32(hipStream_t stream, int32_t B, int32_t A, const float* cost, const float* dcost,
+                               const float* eq, const float* iq, const float* cost_a, const float* eq_a,
+                               const float* iq_a, const double* alphas, double eta, double mu_min, double mu_max,
+                               double floor_, float* alpha_out, float* mu_out);
+int tmpc_linesearch_choose_f64(hipStream_t stream, int32_t B, int32_t A, const double* cost, const double* dcost,
+                               const double* eq, const double* iq, const double* cost_a, const double* eq_a,
+                               const double* iq_a, const double* alphas, double eta, double mu_min,
+                               double mu_max, double floor_, double* alpha_out, double* mu_out);
+
 #ifdef __cplusplus
 }
 #endif

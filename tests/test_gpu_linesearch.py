@@ -204,3 +204,59 @@ def test_fused_merit_terms_match_torch_forms(dtype):
     other = copy.copy(prob)
     other.__class__ = OtherRows
     assert other.merit_terms(*other.initial_guess(), None) is None
+
+
+@pytest.mark.parametrize("dtype", [torch.float64, torch.float32])
+def test_fused_step_choice_matches_torch_form(dtype):
+    """tmpc_linesearch_choose_* against the elementwise step choice of
+    backtracking_linesearch (linesearch.py:54-178), value for value, on merit
+    terms drawn so that candidates sit on both sides of the Armijo test within
+    a few ulps, with NaN and infinite terms (a candidate that is not finite
+    is never taken; none finite: alpha_0), equal merits (the first is taken)
+    and a NaN or infinite mu (nan_to_num)."""
+    from turbompc_amd.solvers.linesearch import _choose_fused, _choose_torch
+
+    gen = torch.Generator().manual_seed(9)
+    B, alphas = 4096, [0.1, 0.3, 0.7, 1.0]
+    A = len(alphas)
+    eta, mu_min, mu_max, floor = 1e-4, 0.1, 1.0e6, 1.0e-8
+    f = lambda *s: torch.rand(s, generator=gen, dtype=torch.float64)  # noqa: E731
+    cost, eq, iq = 10 * f(B), f(B), f(B)
+    dcost = -(f(B) * 5)
+    eq[:64] = 0.0
+    iq[:64] = 0.0  # cl1 below the floor
+    dcost[64:96] = float("nan")  # mu NaN -> mu_min
+    dcost[96:128] = float("inf")  # mu +inf -> mu_max
+    dcost[128:160] = -float("inf")
+    cl1 = eq + iq
+    mu = torch.clamp(torch.nan_to_num(dcost / (0.5 * cl1.clamp(min=floor)), nan=mu_min, posinf=mu_max,
+                                      neginf=mu_min), mu_min, mu_max)
+    merit, slope = cost + mu * cl1, dcost - mu * cl1
+    # candidates around the Armijo line merit + eta alpha slope (a few ulps either side)
+    tgt = torch.stack([merit + eta * a * slope for a in alphas])  # (A, B)
+    jit = 1.0 + (f(A, B) - 0.5) * (4e-15 if dtype == torch.float64 else 8e-7)
+    far = f(A, B) < 0.3
+    cand = torch.where(far, tgt * (1.0 + 0.1 * (f(A, B) - 0.5)), tgt * jit)
+    # split each candidate merit into cost_a + mu (eq_a + iq_a)
+    eq_a, iq_a = 0.3 * f(A, B), 0.2 * f(A, B)
+    cost_a = cand - mu[None] * (eq_a + iq_a)
+    cost_a[0, 200:210] = float("nan")
+    cost_a[:, 210:220] = float("nan")  # no finite candidate
+    eq_a[2, 220:230] = float("inf")
+    cost_a[:, 230:240] = cost_a[1, 230:240]  # equal merits
+    eq_a[:, 230:240], iq_a[:, 230:240] = eq_a[1, 230:240], iq_a[1, 230:240]
+    cost_a[:, 230:240] += 1e3  # and none passes
+    d = lambda t: t.to("cuda", dtype).contiguous()  # noqa: E731
+    base = (d(cost), d(eq), d(iq), d(dcost))
+    ca, ea, ia = d(cost_a).flatten(), d(eq_a).flatten(), d(iq_a).flatten()
+    got = _choose_fused(base, (ca, ea, ia, None), alphas, eta, mu_min, mu_max, floor)
+    a_t = torch.tensor(alphas, dtype=dtype, device="cuda")
+    want = _choose_torch(base[0], base[3], base[1], base[2],
+                         lambda m: (ca + m.repeat(A) * (ea + ia)).view(A, B).t(), alphas, a_t, eta, mu_min,
+                         mu_max, floor)
+    torch.cuda.synchronize()
+    assert torch.equal(got, want), int((got != want).sum())
+    counts = {a: int((want == a).sum()) for a in alphas}
+    print(f"{dtype}: steps taken {counts}")
+    assert all(v > 0 for v in counts.values())
+    assert torch.all(want[210:220] == alphas[0])

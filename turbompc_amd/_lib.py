@@ -176,6 +176,8 @@ SIGNATURES = {
     "tmpc_sqp_first_order_f64": [_VP, _PD, _PQ, _VP, _VP, _VP, _VP, _VP, _F64, _U32, _VP, _VP, _VP, _VP],
     "tmpc_ocp_merit_terms_f32": [_VP, ctypes.POINTER(MeritTerms)],
     "tmpc_ocp_merit_terms_f64": [_VP, ctypes.POINTER(MeritTerms)],
+    "tmpc_linesearch_choose_f32": [_VP, _I32, _I32] + [_VP] * 7 + [_VP, _F64, _F64, _F64, _F64, _VP, _VP],
+    "tmpc_linesearch_choose_f64": [_VP, _I32, _I32] + [_VP] * 7 + [_VP, _F64, _F64, _F64, _F64, _VP, _VP],
     "tmpc_kkt_active_sets_f32": [_VP, ctypes.c_int64, _VP, _VP, _VP, _VP, _F64, _F64, _F64, _VP, _VP],
     "tmpc_kkt_active_sets_f64": [_VP, ctypes.c_int64, _VP, _VP, _VP, _VP, _F64, _F64, _F64, _VP, _VP],
     "tmpc_quadrotor_linearize_f32": [_VP, _I32, _I32, _VP, _VP, _F64, _VP, _VP, _VP],

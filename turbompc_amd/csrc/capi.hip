@@ -1375,6 +1375,31 @@ int merit_impl(hipStream_t s, const tmpc_merit_terms* m) {
   return launch_status();
 }
 
+template <typename R>
+int choose_impl(hipStream_t s, int32_t B, int32_t A, const R* cost, const R* dcost, const R* eq, const R* iq,
+                const R* cost_a, const R* eq_a, const R* iq_a, const double* alphas, double eta, double mu_min,
+                double mu_max, double floor_, R* alpha_out, R* mu_out) {
+  if (B < 0 || A < 1 || A > kMaxAlphas) return TMPC_EBADSHAPE;
+  if (B == 0) return TMPC_OK;
+  if (!cost || !dcost || !eq || !iq || !cost_a || !eq_a || !iq_a || !alphas || !alpha_out) return TMPC_EBADARG;
+  ChooseArgs<R> a{};
+  a.B = B;
+  a.A = A;
+  a.cost = cost; a.dcost = dcost; a.eq = eq; a.iq = iq;
+  a.cost_a = cost_a; a.eq_a = eq_a; a.iq_a = iq_a;
+  for (int j = 0; j < A; ++j) {
+    a.alpha[j] = (R)alphas[j];
+    a.eta_alpha[j] = (R)(eta * alphas[j]);  // the double product, then rounded, as a Python scalar
+  }
+  a.mu_min = (R)mu_min;
+  a.mu_max = (R)mu_max;
+  a.floor_ = (R)floor_;
+  a.alpha_out = alpha_out;
+  a.mu_out = mu_out;
+  hipLaunchKernelGGL((linesearch_choose_kernel<R>), dim3((unsigned)((B + 255) / 256)), dim3(256), 0, s, a);
+  return launch_status();
+}
+
 // ----------------------------------------------------------- KKT state ----
 template <typename R>
 int kkt_active_sets_impl(hipStream_t s, int64_t count, const R* g, const R* l, const R* u, const R* y,
@@ -1617,6 +1642,21 @@ int tmpc_obstacle_lagrangian_hessian_f64(hipStream_t s, int32_t B, int32_t N, in
 
 int tmpc_ocp_merit_terms_f32(hipStream_t s, const tmpc_merit_terms* args) { return merit_impl<float>(s, args); }
 int tmpc_ocp_merit_terms_f64(hipStream_t s, const tmpc_merit_terms* args) { return merit_impl<double>(s, args); }
+
+int tmpc_linesearch_choose_f32(hipStream_t s, int32_t B, int32_t A, const float* cost, const float* dcost,
+                               const float* eq, const float* iq, const float* cost_a, const float* eq_a,
+                               const float* iq_a, const double* alphas, double eta, double mu_min, double mu_max,
+                               double floor_, float* alpha_out, float* mu_out) {
+  return choose_impl<float>(s, B, A, cost, dcost, eq, iq, cost_a, eq_a, iq_a, alphas, eta, mu_min, mu_max, floor_,
+                            alpha_out, mu_out);
+}
+int tmpc_linesearch_choose_f64(hipStream_t s, int32_t B, int32_t A, const double* cost, const double* dcost,
+                               const double* eq, const double* iq, const double* cost_a, const double* eq_a,
+                               const double* iq_a, const double* alphas, double eta, double mu_min, double mu_max,
+                               double floor_, double* alpha_out, double* mu_out) {
+  return choose_impl<double>(s, B, A, cost, dcost, eq, iq, cost_a, eq_a, iq_a, alphas, eta, mu_min, mu_max, floor_,
+                             alpha_out, mu_out);
+}
 
 int tmpc_kkt_active_sets_f32(hipStream_t s, int64_t count, const float* g, const float* l, const float* u,
                              const float* y, double eps_abs, double eps_rel, double dual_tol, uint8_t* lower,

@@ -169,3 +169,78 @@ __global__ __launch_bounds__(256) void ocp_merit_terms_kernel(MeritArgs<R> a) {
 }
 
 }  // namespace tmpc
+
+namespace tmpc {
+
+// The step choice of the merit line search (backtracking_linesearch,
+// turbompc/solvers/linesearch.py:54-178), one thread per problem, from the
+// merit terms of the base point and of the A candidates (candidate j of
+// problem b at j B + b):
+//   cl1 = eq + iq, mu = clip(nan_to_num(dcost / (0.5 max(cl1, floor))), mu_min, mu_max),
+//   merit = cost + mu cl1, slope = dcost - mu cl1,
+//   cand_j = cost_j + mu (eq_j + iq_j), dec_j = cand_j - (merit + eta alpha_j slope),
+//   the largest j with every value finite and dec_j <= 0, else the finite
+//   candidate of least merit (the first of equal ones), else candidate 0.
+// Each value is formed as the elementwise torch form forms it: one rounding
+// per operation (no contraction), the scalars rounded to R first.
+constexpr int kMaxAlphas = 8;
+
+template <typename R>
+struct ChooseArgs {
+  int B, A;
+  const R* cost;    // (B)
+  const R* dcost;   // (B)
+  const R* eq;      // (B)
+  const R* iq;      // (B)
+  const R* cost_a;  // (A B)
+  const R* eq_a;    // (A B)
+  const R* iq_a;    // (A B)
+  R alpha[kMaxAlphas];
+  R eta_alpha[kMaxAlphas];  // eta alpha_j, rounded from its double product
+  R mu_min, mu_max, floor_;
+  R* alpha_out;  // (B)
+  R* mu_out;     // (B) or null
+};
+
+template <typename R>
+__device__ __forceinline__ bool finite_(R x) {
+  return __builtin_isfinite(x);
+}
+
+template <typename R>
+__global__ __launch_bounds__(256) void linesearch_choose_kernel(ChooseArgs<R> a) {
+#pragma clang fp contract(off)
+  const int b = (int)(blockIdx.x * blockDim.x + threadIdx.x);
+  if (b >= a.B) return;
+  const R cl1 = a.eq[b] + a.iq[b];
+  const R den = R(0.5) * (cl1 < a.floor_ ? a.floor_ : cl1);  // clamp(min=floor): NaN stays NaN
+  R mu = a.dcost[b] / den;
+  if (mu != mu)
+    mu = a.mu_min;
+  else if (mu == R(__builtin_huge_val()))
+    mu = a.mu_max;
+  else if (mu == -R(__builtin_huge_val()))
+    mu = a.mu_min;
+  mu = mu < a.mu_min ? a.mu_min : (mu > a.mu_max ? a.mu_max : mu);
+  const R t = mu * cl1;
+  const R merit = a.cost[b] + t;
+  const R slope = a.dcost[b] - t;
+  int valid = -1, best = -1;
+  R best_v = R(0);
+  for (int j = 0; j < a.A; ++j) {
+    const size_t q = (size_t)j * a.B + b;
+    const R cand = a.cost_a[q] + mu * (a.eq_a[q] + a.iq_a[q]);
+    const R dec = cand - (merit + a.eta_alpha[j] * slope);
+    const bool fin = finite_(a.alpha[j]) && finite_(cand) && finite_(dec);
+    if (fin && dec <= R(0)) valid = j;
+    if (fin && (best < 0 || cand < best_v)) {
+      best = j;
+      best_v = cand;
+    }
+  }
+  const int index = valid >= 0 ? valid : (best >= 0 ? best : 0);
+  a.alpha_out[b] = a.alpha[index];
+  if (a.mu_out != nullptr) a.mu_out[b] = mu;
+}
+
+}  // namespace tmpc

@@ -72,6 +72,25 @@ def _candidate_merits(program, alphas, a_t, states, controls, slacks, ds, dc, ds
     return torch.stack(cand, dim=1)
 
 
+def _choose_fused(base, cand, alphas, eta, mu_min, mu_max, floor):
+    """alpha (B,): the step choice below in one kernel (tmpc_linesearch_choose_*)
+    from the merit terms of the base point and of the stacked candidates."""
+    import ctypes
+
+    from .. import _lib
+
+    cost, eq, iq, dcost = base
+    cost_a, eq_a, iq_a, _ = cand
+    B, dt, dev = cost.shape[0], cost.dtype, cost.device
+    alpha = torch.empty(B, dtype=dt, device=dev)
+    fn = f"tmpc_linesearch_choose_{_lib.suffix(dt)}"
+    p = _lib.ptr
+    _lib.check(fn, getattr(_lib.load(), fn)(
+        _lib.stream_handle(dev), B, len(alphas), p(cost), p(dcost), p(eq), p(iq), p(cost_a), p(eq_a), p(iq_a),
+        (ctypes.c_double * len(alphas))(*alphas), eta, mu_min, mu_max, floor, p(alpha), None))
+    return alpha
+
+
 def backtracking_linesearch(program, problem_params, solver_params: Dict[str, Any], states, controls, slacks,
                             states_new, controls_new, slacks_new
                             ) -> Tuple[Tuple[torch.Tensor, torch.Tensor, torch.Tensor], torch.Tensor]:
@@ -85,22 +104,42 @@ def backtracking_linesearch(program, problem_params, solver_params: Dict[str, An
     ds, dc, dsl = states_new - states, controls_new - controls, slacks_new - slacks
 
     fused = _merit_terms(program, states, controls, slacks, ds, dc, dsl)
+    if fused is not None and hasattr(program, "tile") and 1 <= len(alphas) <= 8:
+        # the candidates' terms and the choice among them in two kernels
+        A = len(alphas)
+        a_t = torch.tensor(alphas, dtype=states.dtype).to(states.device, non_blocking=True)
+        stack = lambda z, dz: (z[None] + a_t.view(A, *([1] * z.dim())) * dz[None]).flatten(0, 1)  # noqa: E731
+        cand = _merit_terms(program, stack(states, ds), stack(controls, dc), stack(slacks, dsl), copies=A)
+        if cand is not None:
+            alpha = _choose_fused(fused, cand, alphas, eta, mu_min, mu_max, floor)
+            al = alpha.view(-1, 1, 1)
+            return (states + al * ds, controls + al * dc, slacks + al * dsl), alpha
     if fused is not None:
         cost, eq, iq, dcost = fused
     else:
         cost = program.cost(states, controls, slacks)
         dcost = program.cost_directional_derivative(states, controls, slacks, ds, dc, dsl)
         eq, iq, *_ = evaluate_constraints_with_bounds(program, states, controls, slacks)
+    a_t = torch.tensor(alphas, dtype=states.dtype).to(states.device, non_blocking=True)
+    alpha = _choose_torch(cost, dcost, eq, iq,
+                          lambda mu: _candidate_merits(program, alphas, a_t, states, controls, slacks, ds, dc, dsl, mu),
+                          alphas, a_t, eta, mu_min, mu_max, floor)
+    al = alpha.view(-1, 1, 1)
+    return (states + al * ds, controls + al * dc, slacks + al * dsl), alpha
+
+
+def _choose_torch(cost, dcost, eq, iq, candidate_merits, alphas, a_t, eta, mu_min, mu_max, floor):
+    """alpha (B,): the step choice of backtracking_linesearch (linesearch.py:54-178)
+    in elementwise torch operations; candidate_merits(mu) gives the (B,
+    n_alpha) merits of the candidates."""
     cl1 = eq + iq
     mu_raw = dcost / (0.5 * torch.clamp(cl1, min=floor))
     mu = torch.clamp(torch.nan_to_num(mu_raw, nan=mu_min, posinf=mu_max, neginf=mu_min), mu_min, mu_max)
     merit = cost + mu * cl1
     merit_deriv = dcost - mu * cl1
-
-    a_t = torch.tensor(alphas, dtype=states.dtype).to(states.device, non_blocking=True)
-    cand = _candidate_merits(program, alphas, a_t, states, controls, slacks, ds, dc, dsl, mu)  # (B, n_alpha)
+    cand = candidate_merits(mu)  # (B, n_alpha)
     # eta alpha rounded from its double product, as a Python scalar would be
-    ea_t = torch.tensor([eta * a for a in alphas], dtype=states.dtype).to(states.device, non_blocking=True)
+    ea_t = torch.tensor([eta * a for a in alphas], dtype=cost.dtype).to(cost.device, non_blocking=True)
     dec = cand - (merit[:, None] + ea_t[None] * merit_deriv[:, None])
     finite = torch.isfinite(a_t)[None] & torch.isfinite(cand) & torch.isfinite(dec)
     valid = finite & (dec <= 0)
@@ -109,6 +148,4 @@ def backtracking_linesearch(program, problem_params, solver_params: Dict[str, An
     best_finite = torch.where(finite, cand, torch.full_like(cand, float("inf"))).argmin(dim=1)
     fallback = torch.where(finite.any(dim=1), best_finite, torch.zeros_like(best_finite))
     index = torch.where(valid_index >= 0, valid_index, fallback)
-    alpha = a_t[index]
-    al = alpha.view(-1, 1, 1)
-    return (states + al * ds, controls + al * dc, slacks + al * dsl), alpha
+    return a_t[index]
