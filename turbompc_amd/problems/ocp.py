@@ -356,8 +356,9 @@ class QuadraticTrackingOCP:
                                dcontrols=_lib.ptr(dcontrols), dslacks=_lib.ptr(dslacks), cost=_lib.ptr(cost),
                                dcost=_lib.ptr(dcost), eq=_lib.ptr(eq), iq=_lib.ptr(iq))
         if obs is not None:
+            centers, radii = c(obs["centers"]), c(obs["radii"])  # held until the launch
             args.nobs, args.dim, args.obs_scale = obs["nobs"], obs["dim"], obs["scale"]
-            args.centers, args.radii = _lib.ptr(c(obs["centers"])), _lib.ptr(c(obs["radii"]))
+            args.centers, args.radii = _lib.ptr(centers), _lib.ptr(radii)
         fn = f"tmpc_ocp_merit_terms_{_lib.suffix(dt)}"
         _lib.check(fn, getattr(_lib.load(), fn)(_lib.stream_handle(dev), ctypes.byref(args)))
         return cost, eq, iq, dcost

@@ -15,6 +15,7 @@ applied with program.with_params as in the solver.
 """
 from __future__ import annotations
 
+import ctypes
 from typing import Any, Dict, Tuple
 
 import torch
@@ -75,8 +76,6 @@ def _candidate_merits(program, alphas, a_t, states, controls, slacks, ds, dc, ds
 def _choose_fused(base, cand, alphas, eta, mu_min, mu_max, floor):
     """alpha (B,): the step choice below in one kernel (tmpc_linesearch_choose_*)
     from the merit terms of the base point and of the stacked candidates."""
-    import ctypes
-
     from .. import _lib
 
     cost, eq, iq, dcost = base
