@@ -225,6 +225,25 @@ int tmpc_sqp_admm_step_f64(hipStream_t stream, const tmpc_dims* dims, const tmpc
                            const tmpc_admm_cfg* cfg, const tmpc_sqp_step* sqp, void* workspace,
                            size_t workspace_bytes);
 
+/* The same SQP step for the rotor-thrust quadrotor (n = 17, nx = 13), which
+ * also builds the QP's dynamics rows: qp->A_minus (B,N,13,17) and qp->c
+ * (B,N,13) are OUTPUTS, written first with the RK4 linearization of
+ * tmpc_quadrotor_linearize_* at the input iterate (the rows [x_t; u_t] of
+ * in->x; dt and the 7 model parameters as there).  With
+ * TMPC_FLAG_WARM_RECORDS (and without TMPC_FLAG_WARM_INEQ) the same values
+ * go straight into the workspace's stage records on the streaming path, so
+ * the step copies nothing from the QP layout.  This fuses the linearization
+ * of the next SQP iteration (turbompc/solvers/turbompc_solver.py:1098-1156,
+ * optimal_control_problem.py:1217-1272) into the step that consumes it. */
+int tmpc_sqp_admm_step_quadrotor_f32(hipStream_t stream, const tmpc_dims* dims, const tmpc_qp* qp,
+                                     const tmpc_state* in, tmpc_state* out, uint32_t* iters_out,
+                                     const tmpc_admm_cfg* cfg, const tmpc_sqp_step* sqp, double dt,
+                                     const double* params, void* workspace, size_t workspace_bytes);
+int tmpc_sqp_admm_step_quadrotor_f64(hipStream_t stream, const tmpc_dims* dims, const tmpc_qp* qp,
+                                     const tmpc_state* in, tmpc_state* out, uint32_t* iters_out,
+                                     const tmpc_admm_cfg* cfg, const tmpc_sqp_step* sqp, double dt,
+                                     const double* params, void* workspace, size_t workspace_bytes);
+
 /* ---- ADMM with the PCG Schur solve -----------------------------------------
  * Replaces the `admm_fused_cuda[_f64]` FFI target: AdmmFusedCudaImpl
  * (turbompc/solvers/admm/csrc/admm_ffi.cc:13-148) / LaunchADMMFusedF32/F64

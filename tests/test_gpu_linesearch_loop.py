@@ -178,3 +178,29 @@ def test_device_loop_equals_masked_with_a_nonfinite_problem(mode):
     print(f"  SQP iterations per problem {dev.num_iter.tolist()}, non-finite {dev.nonfinite.tolist()}", flush=True)
     assert dev.nonfinite.tolist() == [b == 3 for b in range(8)]
     _assert_same(dev, msk)
+
+
+@pytest.mark.parametrize("dtype", [torch.float64, torch.float32])
+@pytest.mark.parametrize("stop", [False, True])
+def test_quadrotor_step_linearization_equals_build_qp(dtype, stop):
+    """The quadrotor's SQP steps build their own dynamics rows
+    (tmpc_sqp_admm_step_quadrotor_*: the linearization at the step's input
+    iterate, written into the QP buffers and straight into the stage
+    records): the solve is bit for bit the one whose loop builds each QP
+    with build_qp and lets the step copy the rows into the records."""
+    prob = make_quadrotor_config(B=24, seed=7, dtype=dtype, device="cuda")
+    params = _params(6, 20, 0.0, linesearch=False, criterion="first_order")
+    if stop:
+        params["tol_convergence"] = _tol_splitting(prob, params)
+    out = []
+    for fused in (True, False):
+        p = copy.copy(prob)
+        if not fused:
+            p.step_linearization = lambda: None  # noqa: E731  the build_qp path
+        assert (p.step_linearization() is not None) == fused
+        solver = TurboMPCSolver(p, params)
+        out.append(solver.solve(solver.initial_guess()))
+    torch.cuda.synchronize()
+    _assert_same(*out)
+    if stop:
+        assert len(set(out[0].num_iter.tolist())) >= 2

@@ -540,12 +540,27 @@ int sqp_check_impl(hipStream_t s, const tmpc_dims* dims, const tmpc_qp* qp, cons
                    const R* yg, const R* slack, double slack_w, uint32_t flags, R* conv, R* eq, R* iq, R* gout,
                    const R* slack_wp = nullptr);
 
+template <typename R>
+int quad_impl(hipStream_t s, int B, int N, const R* states, int64_t ls, const R* controls, int64_t lu, double dt,
+              const double* params, R* Am, R* c, QuadRecOut<R> rec);
+
+// The quadrotor model of an SQP step that linearizes its own dynamics rows.
+struct QuadLin {
+  double dt;
+  const double* params;  // host, 7
+};
+
 // sq != nullptr: one SQP step -- the first-order check of the input iterate,
-// the activity test, and the ADMM solve of the problems that pass it.
+// the activity test, and the ADMM solve of the problems that pass it.  ql
+// != nullptr (with sq): the QP's A_minus and c are outputs, the quadrotor's
+// RK4 linearization at the input iterate (the state's x rows [x_t; u_t]),
+// written before anything reads them and, where warm stage records take
+// them, into the records as well (no repack).
 template <typename R>
 int admm_direct_impl(hipStream_t s, const tmpc_dims* dims, const tmpc_qp* qp,
                      const tmpc_state* in, tmpc_state* out, uint32_t* iters,
-                     const tmpc_admm_cfg* cfg, void* ws, size_t wsb, const tmpc_sqp_step* sq = nullptr) {
+                     const tmpc_admm_cfg* cfg, void* ws, size_t wsb, const tmpc_sqp_step* sq = nullptr,
+                     const QuadLin* ql = nullptr) {
   if (!dims_ok(dims)) return TMPC_EBADSHAPE;
   if (!cfg || !iters || !qp_ok(qp, dims->m) || !state_ok(in, dims->m) || !state_ok(out, dims->m))
     return TMPC_EBADARG;
@@ -601,6 +616,24 @@ int admm_direct_impl(hipStream_t s, const tmpc_dims* dims, const tmpc_qp* qp,
   const bool pad = dr.n != d.n;
   QPDev<R> qr = a.qp;  // the QP as the record kernels read it
   if (pad) qr.A0 = w.a0p;
+  bool dyn_in_records = false;
+  if (ql) {
+    if (d.n != 17 || d.nx != 13) return TMPC_EBADSHAPE;
+    QuadRecOut<R> rec{};
+    dyn_in_records = stream && (cfg->flags & TMPC_FLAG_WARM_RECORDS) != 0 &&
+                     !((cfg->flags & TMPC_FLAG_WARM_INEQ) != 0 && d.m > 0) && !pad;
+    if (dyn_in_records) {
+      const RecGeom g = rec_geom(dr, diag);
+      rec.am = w.am;
+      rec.rv = w.rv;
+      rec.amp = g.amp;
+      rec.rvp = g.rvp;
+      rec.c_off = g.c;
+    }
+    st = quad_impl<R>(s, d.B, d.N, a.st.x, d.n, a.st.x + 13, d.n, ql->dt, ql->params, const_cast<R*>(a.qp.Am),
+                      const_cast<R*>(a.qp.c), rec);
+    if (st) return st;
+  }
   if (given) {
     // the activity as given: act_out = act_in, which the kernels read as the
     // per-problem start state (the streaming kernel reads act_in itself)
@@ -629,7 +662,7 @@ int admm_direct_impl(hipStream_t s, const tmpc_dims* dims, const tmpc_qp* qp,
     if ((cfg->flags & TMPC_FLAG_WARM_INEQ) != 0 && d.m > 0)
       hipLaunchKernelGGL((stage_repack_dynamics_kernel<R, true>), dim3(gx, (unsigned)d.T), dim3(256), 0, s, dr,
                          a.qp.Am, a.qp.c, a.qp.G, a.qp.l, a.qp.u, w.am, w.rv, diag ? 1 : 0);
-    else
+    else if (!dyn_in_records)
       hipLaunchKernelGGL((stage_repack_dynamics_kernel<R, false>), dim3(gx, (unsigned)d.N), dim3(256), 0, s, dr,
                          a.qp.Am, a.qp.c, a.qp.G, a.qp.l, a.qp.u, w.am, w.rv, diag ? 1 : 0);
     st = launch_status();
@@ -1172,7 +1205,7 @@ int admm_pcg_impl(hipStream_t s, const tmpc_dims* dims, const tmpc_qp* qp, const
 // ------------------------------------------------------------ quadrotor ----
 template <typename R>
 int quad_impl(hipStream_t s, int B, int N, const R* states, int64_t ls, const R* controls, int64_t lu, double dt,
-              const double* params, R* Am, R* c) {
+              const double* params, R* Am, R* c, QuadRecOut<R> rec) {
   if (B < 1 || N < 1) return TMPC_EBADSHAPE;
   if (!states || !controls || !params || !Am || !c) return TMPC_EBADARG;
   if (ls < 13 || lu < 4 || ls > (1 << 20) || lu > (1 << 20)) return TMPC_EBADARG;
@@ -1182,7 +1215,7 @@ int quad_impl(hipStream_t s, int B, int N, const R* states, int64_t ls, const R*
   const int blk = 256;
   const long long grid = (total + blk - 1) / blk;
   hipLaunchKernelGGL((quad_linearize_kernel<R>), dim3((unsigned)grid), dim3(blk), 0, s, B, N, states, (int)ls,
-                     controls, (int)lu, (R)dt, P, Am, c);
+                     controls, (int)lu, (R)dt, P, Am, c, rec);
   return launch_status();
 }
 
@@ -1568,25 +1601,26 @@ int tmpc_schur_pcg_f64(hipStream_t s, int32_t B, int32_t T, int32_t n, const dou
 int tmpc_quadrotor_linearize_f32(hipStream_t s, int32_t B, int32_t N, const float* states,
                                  const float* controls, double dt, const double* params, float* A_minus,
                                  float* c) {
-  return quad_impl<float>(s, B, N, states, 13, controls, 4, dt, params, A_minus, c);
+  return quad_impl<float>(s, B, N, states, 13, controls, 4, dt, params, A_minus, c, QuadRecOut<float>{});
 }
 int tmpc_quadrotor_linearize_f64(hipStream_t s, int32_t B, int32_t N, const double* states,
                                  const double* controls, double dt, const double* params, double* A_minus,
                                  double* c) {
-  return quad_impl<double>(s, B, N, states, 13, controls, 4, dt, params, A_minus, c);
+  return quad_impl<double>(s, B, N, states, 13, controls, 4, dt, params, A_minus, c, QuadRecOut<double>{});
 }
 int tmpc_quadrotor_linearize_strided_f32(hipStream_t s, int32_t B, int32_t N, const float* states,
                                          int64_t states_row_stride, const float* controls,
                                          int64_t controls_row_stride, double dt, const double* params,
                                          float* A_minus, float* c) {
-  return quad_impl<float>(s, B, N, states, states_row_stride, controls, controls_row_stride, dt, params, A_minus, c);
+  return quad_impl<float>(s, B, N, states, states_row_stride, controls, controls_row_stride, dt, params, A_minus, c,
+                          QuadRecOut<float>{});
 }
 int tmpc_quadrotor_linearize_strided_f64(hipStream_t s, int32_t B, int32_t N, const double* states,
                                          int64_t states_row_stride, const double* controls,
                                          int64_t controls_row_stride, double dt, const double* params,
                                          double* A_minus, double* c) {
   return quad_impl<double>(s, B, N, states, states_row_stride, controls, controls_row_stride, dt, params, A_minus,
-                           c);
+                           c, QuadRecOut<double>{});
 }
 
 int tmpc_linear_dynamics_f32(hipStream_t s, int32_t B, int32_t N, int32_t nx, int32_t nu, const float* states,
@@ -1656,6 +1690,23 @@ int tmpc_linesearch_choose_f64(hipStream_t s, int32_t B, int32_t A, const double
                                double floor_, double* alpha_out, double* mu_out) {
   return choose_impl<double>(s, B, A, cost, dcost, eq, iq, cost_a, eq_a, iq_a, alphas, eta, mu_min, mu_max, floor_,
                              alpha_out, mu_out);
+}
+
+int tmpc_sqp_admm_step_quadrotor_f32(hipStream_t s, const tmpc_dims* dims, const tmpc_qp* qp, const tmpc_state* in,
+                                     tmpc_state* out, uint32_t* iters, const tmpc_admm_cfg* cfg,
+                                     const tmpc_sqp_step* sqp, double dt, const double* params, void* ws,
+                                     size_t wsb) {
+  if (!qp || !qp->A_minus || !qp->c || !params || !sqp) return TMPC_EBADARG;
+  const QuadLin ql{dt, params};
+  return admm_direct_impl<float>(s, dims, qp, in, out, iters, cfg, ws, wsb, sqp, &ql);
+}
+int tmpc_sqp_admm_step_quadrotor_f64(hipStream_t s, const tmpc_dims* dims, const tmpc_qp* qp, const tmpc_state* in,
+                                     tmpc_state* out, uint32_t* iters, const tmpc_admm_cfg* cfg,
+                                     const tmpc_sqp_step* sqp, double dt, const double* params, void* ws,
+                                     size_t wsb) {
+  if (!qp || !qp->A_minus || !qp->c || !params || !sqp) return TMPC_EBADARG;
+  const QuadLin ql{dt, params};
+  return admm_direct_impl<double>(s, dims, qp, in, out, iters, cfg, ws, wsb, sqp, &ql);
 }
 
 int tmpc_kkt_active_sets_f32(hipStream_t s, int64_t count, const float* g, const float* l, const float* u,

@@ -90,11 +90,21 @@ __device__ __forceinline__ void quad_xdot(const D* x, const D* f, const QuadPara
   xd[12] = (R(1) / P.Jz) * (tz - (P.Jy - P.Jx) * (wx * wy));
 }
 
+// Optional second destination of the blocks: the streaming solve's stage
+// records (M record of (t, b) at am + (t B + b) amp with rows of 17, c_t at
+// offset c_off of the rv record), so that an SQP step needs no copy of them.
+template <typename R>
+struct QuadRecOut {
+  R* am = nullptr;  // null: the QP layout only
+  R* rv = nullptr;
+  int amp = 0, rvp = 0, c_off = 0;
+};
+
 template <typename R>
 __global__ __launch_bounds__(256) void quad_linearize_kernel(int B, int N, const R* __restrict__ states, int ls,
                                                              const R* __restrict__ controls, int lu, R dt,
                                                              QuadParams<R> P, R* __restrict__ Am,
-                                                             R* __restrict__ c) {
+                                                             R* __restrict__ c, QuadRecOut<R> rec) {
   const long long gidx = (long long)blockIdx.x * blockDim.x + threadIdx.x;
   const long long pairs = (long long)B * N;
   if (gidx >= pairs * 18) return;
@@ -121,13 +131,18 @@ __global__ __launch_bounds__(256) void quad_linearize_kernel(int B, int N, const
   for (int k = 0; k < 13; ++k) tmp[k] = x[k] + dt * k3[k];
   quad_xdot(tmp, u, P, k4);
   R* A = Am + ((size_t)b * N + t) * 13 * 17;
+  const size_t ri = (size_t)t * B + b;  // the stage record of (t, b)
 #pragma unroll
   for (int k = 0; k < 13; ++k) {
     const Dual<R> xn = x[k] + (R(1) / R(6)) * ((k1[k] + R(2) * k2[k] + R(2) * k3[k] + k4[k]) * Dual<R>(dt));
-    if (j < 17)
+    if (j < 17) {
       A[k * 17 + j] = xn.d;
-    else
-      c[((size_t)b * N + t) * 13 + k] = xn.d - xn.v;
+      if (rec.am != nullptr) rec.am[ri * rec.amp + k * 17 + j] = xn.d;
+    } else {
+      const R ck = xn.d - xn.v;
+      c[((size_t)b * N + t) * 13 + k] = ck;
+      if (rec.rv != nullptr) rec.rv[ri * rec.rvp + rec.c_off + k] = ck;
+    }
   }
 }
 

@@ -485,13 +485,17 @@ class QuadraticTrackingOCP:
     def build_qp(self, states: torch.Tensor, controls: torch.Tensor) -> QPData:
         """QP of one SQP iteration (TurboMPCSolver._build_qp_data, turbompc_solver.py:1098-1156),
         in the scaled variables with rescaling."""
+        return self._qp_with_dynamics(*self.dynamics_blocks(states, controls))
+
+    def _qp_with_dynamics(self, Am: torch.Tensor, c: torch.Tensor) -> QPData:
+        """The QP of this problem's blocks (built once) with the dynamics rows
+        (A_minus, c), rescaled with rescaling."""
         if self._static is None:
             D, E, q = self.cost_blocks()
             A0, c0 = self.initial_equality()
             G, l, u = self.inequality_blocks()
             self._static = (D, E, q, A0, c0, self.a_plus(), G, l, u)
         D, E, q, A0, c0, Ap, G, l, u = self._static
-        Am, c = self.dynamics_blocks(states, controls)
         qp = QPData(
             cost=QPCostBlocks(D, E, q),
             eq=QPEqualityBlocks(A0, Am, Ap, c0, c),

@@ -20,6 +20,7 @@ import math
 import torch
 
 from .. import _lib
+from ..solvers.qp_data import QPData
 from .ocp import QuadraticTrackingOCP
 
 # mass [kg], Jxx, Jyy, Jzz [kg m^2], arm [m], yaw-moment coefficient [m], g [m/s^2]
@@ -66,6 +67,23 @@ class QuadrotorOCP(QuadraticTrackingOCP):
         )
         _lib.check(f"tmpc_quadrotor_linearize_strided_{sfx}", st)
         return Am, c
+
+    def step_linearization(self):
+        """(dt, params) for an SQP step that builds this problem's dynamics
+        rows itself (ADMMSolver.sqp_step(quadrotor=...)), or None with
+        rescaling (the step writes the unscaled rows)."""
+        return None if self.rescale_optimization_variables else (self.dt, self._cparams)
+
+    def qp_for_next_step(self) -> QPData:
+        """The QP of the next SQP iteration with its dynamics rows left to the
+        step that solves it: A_minus and c are empty buffers that
+        tmpc_sqp_admm_step_quadrotor_* fills with the linearization at the
+        step's input iterate, the ADMM state's x (the iterate build_qp would
+        be given).  The other blocks are this problem's, as in build_qp."""
+        B, N = self.B, self.horizon
+        Am = torch.empty((B, N, 13, 17), dtype=self.dtype, device=self.device)
+        c = torch.empty((B, N, 13), dtype=self.dtype, device=self.device)
+        return self._qp_with_dynamics(Am, c)
 
     def next_states(self, states, controls):
         """(B, N, 13): the RK4 step at every stage (tmpc_quadrotor_dynamics_*)."""

@@ -87,7 +87,7 @@ def direct_workspace(qp: QPData) -> torch.Tensor:
 def admm_hip_solve(qp: QPData, state0, *, schur: str, cfg: _lib.AdmmCfg,
                    slack_weight: Optional[torch.Tensor] = None, want_pcg_iters: bool = False, sqp=None,
                    workspace: Optional[torch.Tensor] = None, donate: bool = False,
-                   iters_out: Optional[torch.Tensor] = None):
+                   iters_out: Optional[torch.Tensor] = None, quadrotor=None):
     """Run the fused ADMM on the device.  `state0` is an ADMMState of batched
     tensors; returns (state fields tuple, iters (B,), pcg_iters or None).
 
@@ -105,7 +105,11 @@ def admm_hip_solve(qp: QPData, state0, *, schur: str, cfg: _lib.AdmmCfg,
 
     iters_out: a zero-filled contiguous (B,) int32 device buffer that receives
     the iteration words (returned as `iters`) instead of a new one, e.g. a
-    row of an SQP loop's per-iteration record."""
+    row of an SQP loop's per-iteration record.
+
+    quadrotor = (dt, params as a ctypes double[7]) with sqp: the step builds
+    the QP's dynamics rows itself (tmpc_sqp_admm_step_quadrotor_*):
+    qp.eq.A_minus and qp.eq.c are outputs, the linearization at state0's x."""
     if sqp is not None and schur != "direct":
         raise ValueError("an SQP step (sqp=...) needs the direct Schur solve")
     lib = _lib.load()
@@ -166,11 +170,22 @@ def admm_hip_solve(qp: QPData, state0, *, schur: str, cfg: _lib.AdmmCfg,
                 g = torch.empty((B, T, m), dtype=dt, device=dev)
                 sq = _lib.SqpStep(_lib.ptr(act_in), _lib.ptr(act_out), float(tol), _lib.ptr(conv), _lib.ptr(eq),
                                   _lib.ptr(iq), _lib.ptr(g))
-            st = getattr(lib, f"tmpc_sqp_admm_step_{sfx}")(
-                stream, ctypes.byref(dims), ctypes.byref(cq), ctypes.byref(sv), ctypes.byref(sv),
-                _lib.ptr(iters), ctypes.byref(cfg), ctypes.byref(sq), _lib.ptr(ws), nbytes,
-            )
-            _lib.check(f"tmpc_sqp_admm_step_{sfx}", st)
+            if quadrotor is None:
+                fn = f"tmpc_sqp_admm_step_{sfx}"
+                st = getattr(lib, fn)(
+                    stream, ctypes.byref(dims), ctypes.byref(cq), ctypes.byref(sv), ctypes.byref(sv),
+                    _lib.ptr(iters), ctypes.byref(cfg), ctypes.byref(sq), _lib.ptr(ws), nbytes,
+                )
+            else:
+                if not (qp.eq.A_minus.is_contiguous() and qp.eq.c.is_contiguous()):
+                    raise ValueError("the quadrotor step writes A_minus and c in place: they must be contiguous")
+                dt_q, params_q = quadrotor
+                fn = f"tmpc_sqp_admm_step_quadrotor_{sfx}"
+                st = getattr(lib, fn)(
+                    stream, ctypes.byref(dims), ctypes.byref(cq), ctypes.byref(sv), ctypes.byref(sv),
+                    _lib.ptr(iters), ctypes.byref(cfg), ctypes.byref(sq), float(dt_q), params_q, _lib.ptr(ws), nbytes,
+                )
+            _lib.check(fn, st)
             del keep
             return outs, iters, None, (conv, eq, iq, g, act_out.view(torch.bool))  # the library writes 0 / 1
         st = getattr(lib, f"tmpc_admm_direct_{sfx}")(
