@@ -108,6 +108,10 @@ typedef struct tmpc_state {
  * rows are), whose records are rewritten too; D, E, q, A0, c0 and the slack
  * weight are still unchanged. */
 #define TMPC_FLAG_WARM_INEQ 16u
+/* With TMPC_FLAG_WARM_RECORDS: A_minus and c are the previous call's as well
+ * (linear dynamics), so the records keep them and only what else changed
+ * (G, l, u with TMPC_FLAG_WARM_INEQ) is rewritten. */
+#define TMPC_FLAG_WARM_SAME_DYNAMICS (1u << 13)
 /* Every G_t is the same for every stage and problem (box rows of a tracking
  * problem), vouched for by the caller.  The streaming kernel for n = 17
  * records then keeps the G rows of its stage blocks in LDS and streams only

@@ -643,10 +643,13 @@ def test_admm_stream_kernel_padded_width_adaptive_rho_fp32(shape):
 
 @pytest.mark.parametrize("shape", [(10, 13, 7, 4, 3), (7, 9, 8, 5, 6), (5, 7, 14, 10, 5), (6, 7, 14, 10, 10)])
 @pytest.mark.parametrize("ineq", [False, True])
-def test_admm_stream_kernel_padded_width_warm_records(shape, ineq):
+@pytest.mark.parametrize("same_dyn", [False, True])
+def test_admm_stream_kernel_padded_width_warm_records(shape, ineq, same_dyn):
     """An SQP step whose QP differs from the previous call's in A_minus and c
     (and with ineq in G, l, u), on padded records: rewriting only those records
-    gives the iterate of a step that repacks everything, bit for bit."""
+    gives the iterate of a step that repacks everything, bit for bit.  With
+    same_dyn the QP keeps the previous A_minus and c (FLAG_WARM_SAME_DYNAMICS:
+    their records are kept as well; without ineq no record is rewritten)."""
     from turbompc_amd.solvers.admm.admm_hip_backend import direct_workspace
 
     B, T, n, nx, m = shape
@@ -654,6 +657,8 @@ def test_admm_stream_kernel_padded_width_warm_records(shape, ineq):
     qp2 = random_qp(B, T, n, nx, m, seed=84, std=True).to(DEV, torch.float64)
     # qp2 keeps qp1's cost, initial rows and (without ineq) inequality rows
     eq2 = dataclasses.replace(qp2.eq, A0=qp1.eq.A0, c0=qp1.eq.c0)
+    if same_dyn:
+        eq2 = dataclasses.replace(eq2, A_minus=qp1.eq.A_minus, c=qp1.eq.c)
     qp2 = dataclasses.replace(qp2, cost=qp1.cost, eq=eq2, ineq=qp2.ineq if ineq else qp1.ineq)
     cfg = oracle.OracleCfg(max_iter=15, check_every=16, adapt_rho_every=0, sigma=1e-6, eps_abs=1e-12,
                            eps_rel=1e-12, rho_f_factor=1000.0, alpha=1.0)
@@ -665,7 +670,8 @@ def test_admm_stream_kernel_padded_width_warm_records(shape, ineq):
         (_, _), _, st1 = solver.solve(qp1, st0, workspace=ws)
         active = torch.ones(B, dtype=torch.bool, device=DEV)
         (_, _), stats, st2, _, _ = solver.sqp_step(qp2, st1, active, 0.0, rho_bar=0.1, workspace=ws,
-                                                   warm_records=warm, warm_ineq=warm and ineq)
+                                                   warm_records=warm, warm_ineq=warm and ineq,
+                                                   same_dynamics=same_dyn)
         outs.append((stats, st2))
     torch.cuda.synchronize()
     (s_w, o_w), (s_c, o_c) = outs

@@ -28,6 +28,7 @@ FLAG_GENERIC_KERNEL = 2
 FLAG_DIAG_COST = 4  # every D_t diagonal
 FLAG_WARM_RECORDS = 8  # the workspace's stage records are the previous SQP step's
 FLAG_WARM_INEQ = 16  # with FLAG_WARM_RECORDS: G, l, u changed too
+FLAG_WARM_SAME_DYNAMICS = 1 << 13  # with FLAG_WARM_RECORDS: A_minus and c unchanged
 FLAG_CONST_G = 32  # every G_t the same for every stage and problem (box rows)
 FLAG_INVARIANT_A = 64  # with FLAG_CONST_G (n = 17): stage-invariant A_minus entries resident
 NOALLOC_SCRATCH_BYTES = 64 << 20  # TMPC_NOALLOC_SCRATCH_BYTES (scratch of tmpc_admm_direct_noalloc)

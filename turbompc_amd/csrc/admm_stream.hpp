@@ -407,13 +407,14 @@ __global__ __launch_bounds__(256) void stage_repack_dynamics_kernel(Dims d, cons
                                                                     const R* __restrict__ G,
                                                                     const R* __restrict__ l,
                                                                     const R* __restrict__ u, R* __restrict__ am,
-                                                                    R* __restrict__ rv, int diag) {
+                                                                    R* __restrict__ rv, int diag, int dyn_rows) {
   const int t = blockIdx.y, b0 = blockIdx.x * kRepackProblems;
   const RecGeom g = rec_geom(d, diag != 0);
   const int n = d.n, nx = d.nx, m = d.m, nq = d.nq;
-  // per stage: [A_minus (nx nq) | c (nx)] for t < N, then [G (m nq) | l (m) | u (m)];
-  // a record row has n >= nq entries (the dummies' columns stay zero)
-  const bool dyn = !INEQ || t < d.N;
+  // per stage: [A_minus (nx nq) | c (nx)] for t < N (dyn_rows: they changed),
+  // then [G (m nq) | l (m) | u (m)]; a record row has n >= nq entries (the
+  // dummies' columns stay zero)
+  const bool dyn = dyn_rows != 0 && (!INEQ || t < d.N);
   const int na = dyn ? nx * nq : 0, nd = dyn ? na + nx : 0;
   const int ng = INEQ ? m * nq : 0, per = nd + (INEQ ? ng + 2 * m : 0);
   auto rec_col = [&](int e) { return (e / nq) * n + e % nq; };  // row-major nq -> n

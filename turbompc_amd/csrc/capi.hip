@@ -659,12 +659,15 @@ int admm_direct_impl(hipStream_t s, const tmpc_dims* dims, const tmpc_qp* qp,
   }
   if (stream && (cfg->flags & TMPC_FLAG_WARM_RECORDS)) {
     const unsigned gx = (unsigned)((d.B + kRepackProblems - 1) / kRepackProblems);
+    // the A_minus and c rows are rewritten unless they did not change or the
+    // quadrotor step already wrote them
+    const bool dyn_rows = !dyn_in_records && (cfg->flags & TMPC_FLAG_WARM_SAME_DYNAMICS) == 0;
     if ((cfg->flags & TMPC_FLAG_WARM_INEQ) != 0 && d.m > 0)
       hipLaunchKernelGGL((stage_repack_dynamics_kernel<R, true>), dim3(gx, (unsigned)d.T), dim3(256), 0, s, dr,
-                         a.qp.Am, a.qp.c, a.qp.G, a.qp.l, a.qp.u, w.am, w.rv, diag ? 1 : 0);
-    else if (!dyn_in_records)
+                         a.qp.Am, a.qp.c, a.qp.G, a.qp.l, a.qp.u, w.am, w.rv, diag ? 1 : 0, dyn_rows ? 1 : 0);
+    else if (dyn_rows)
       hipLaunchKernelGGL((stage_repack_dynamics_kernel<R, false>), dim3(gx, (unsigned)d.N), dim3(256), 0, s, dr,
-                         a.qp.Am, a.qp.c, a.qp.G, a.qp.l, a.qp.u, w.am, w.rv, diag ? 1 : 0);
+                         a.qp.Am, a.qp.c, a.qp.G, a.qp.l, a.qp.u, w.am, w.rv, diag ? 1 : 0, 1);
     st = launch_status();
     if (st) return st;
     st = launch_factor_std<R>(s, dr, w, qr, a.st.rho, a.sigma, a.rho_f_factor, nullptr, fp, diag, fgroups);

@@ -619,8 +619,13 @@ class LinearOCP(QuadraticTrackingOCP):
         return nxt
 
     def dynamics_blocks(self, states, controls):
-        N = self.horizon
-        AB = torch.cat([self.A, self.Bm], dim=-1)  # (B, nx, n)
-        Am = AB.unsqueeze(1).expand(self.B, N, *AB.shape[1:]).contiguous()
-        c = (-self.b).unsqueeze(1).expand(self.B, N, self.num_state_variables).contiguous()
-        return Am, c
+        """The constant blocks, built once: every SQP step's QP holds the same
+        A_minus and c tensors, so a warm step keeps their stage records."""
+        def make():
+            N = self.horizon
+            AB = torch.cat([self.A, self.Bm], dim=-1)  # (B, nx, n)
+            Am = AB.unsqueeze(1).expand(self.B, N, *AB.shape[1:]).contiguous()
+            c = (-self.b).unsqueeze(1).expand(self.B, N, self.num_state_variables).contiguous()
+            return Am, c
+
+        return self._memoized("dynamics_blocks", make)

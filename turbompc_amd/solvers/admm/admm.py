@@ -215,7 +215,7 @@ class ADMMSolver:
                  rho_bar: float = 1.0, alpha: float = 1.0, *, slack_weight=0.0,
                  workspace: Optional[torch.Tensor] = None, warm_records: bool = False,
                  warm_ineq: bool = False, donate_state: bool = False, iters_out: Optional[torch.Tensor] = None,
-                 quadrotor=None):
+                 quadrotor=None, same_dynamics: bool = False):
         """One device SQP step (tmpc_sqp_admm_step_*): the first-order check of
         admm_state0's iterate against qp_data, the activity test
         active & (conv > tol), and the solve of the problems that pass it (the
@@ -223,7 +223,9 @@ class ADMMSolver:
         caller vouches that `workspace` holds the records of the previous call
         on it, whose output is admm_state0, and that qp_data differs from that
         call's QP only in A_minus and c (FLAG_WARM_RECORDS); with warm_ineq
-        also in G, l and u (FLAG_WARM_INEQ).  donate_state:
+        also in G, l and u (FLAG_WARM_INEQ); with same_dynamics A_minus and
+        c are that call's too (FLAG_WARM_SAME_DYNAMICS: their rows are kept).
+        donate_state:
         admm_state0's buffers may be updated in place.  tol None: the
         activity is given (no check; the problems where `active` is False keep
         their state, and the check outputs are None).  iters_out: as in
@@ -242,6 +244,8 @@ class ADMMSolver:
             flags |= _lib.FLAG_WARM_RECORDS
             if warm_ineq:
                 flags |= _lib.FLAG_WARM_INEQ
+            if same_dynamics and quadrotor is None:
+                flags |= _lib.FLAG_WARM_SAME_DYNAMICS
         cfg = self._cfg(alpha, flags)
         sw = slack_weight if self._use_slack else None
         outs, iters, _, (conv, eq, iq, g, act) = hip.admm_hip_solve(

@@ -621,7 +621,7 @@ class TurboMPCSolver:
                 (states, controls), _, admm_state, (cv, e, i, g), act = admm.sqp_step(
                     qp, admm_state, active, tol, rho_bar=ap["rho"], alpha=alpha, slack_weight=sw, workspace=ws,
                     warm_records=warm is not None, warm_ineq=warm == "constraints", donate_state=True,
-                    iters_out=words[it], quadrotor=lin)
+                    iters_out=words[it], quadrotor=lin, same_dynamics=_same_dynamics(qp, prev))
                 states, controls = self._from_qp(program, states, controls)
                 # the check belongs to the iterate committed at it - 1 (the
                 # records of a stopped problem stay zero, as in the reference)
@@ -712,7 +712,8 @@ class TurboMPCSolver:
                 warm = _warm_level(qp, prev)
                 (s_new, c_new), stats, adm_new, _, _ = admm.sqp_step(
                     qp, admm_state, active, None, rho_bar=ap["rho"], alpha=alpha, slack_weight=sw, workspace=ws,
-                    warm_records=warm is not None, warm_ineq=warm == "constraints", donate_state=True)
+                    warm_records=warm is not None, warm_ineq=warm == "constraints", donate_state=True,
+                    same_dynamics=_same_dynamics(qp, prev))
                 s_new, c_new = self._from_qp(program, s_new, c_new)
             sl_new = adm_new.xi_g
             if use_ls:
@@ -943,6 +944,12 @@ def _warm_level(qp: QPData, prev: Optional[QPData]) -> Optional[str]:
     if same(qp.ineq.G, prev.ineq.G) and same(qp.ineq.l, prev.ineq.l) and same(qp.ineq.u, prev.ineq.u):
         return "dynamics"
     return "constraints"
+
+
+def _same_dynamics(qp: QPData, prev: Optional[QPData]) -> bool:
+    """Whether qp's dynamics rows (A_minus, c) are prev's tensors: linear
+    dynamics, whose blocks the problem builds once (LinearOCP.dynamics_blocks)."""
+    return prev is not None and qp.eq.A_minus is prev.eq.A_minus and qp.eq.c is prev.eq.c
 
 
 def _same_static_blocks(qp: QPData, prev: Optional[QPData]) -> bool:
