@@ -234,9 +234,9 @@ int tmpc_sqp_admm_step_f64(hipStream_t stream, const tmpc_dims* dims, const tmpc
  * (B,N,13) are OUTPUTS, written first with the RK4 linearization of
  * tmpc_quadrotor_linearize_* at the input iterate (the rows [x_t; u_t] of
  * in->x; dt and the 7 model parameters as there).  With
- * TMPC_FLAG_WARM_RECORDS (and without TMPC_FLAG_WARM_INEQ) the same values
- * go straight into the workspace's stage records on the streaming path, so
- * the step copies nothing from the QP layout.  This fuses the linearization
+ * TMPC_FLAG_WARM_RECORDS the same values go straight into the workspace's
+ * stage records on the streaming path, so the step copies no dynamics rows
+ * from the QP layout.  This fuses the linearization
  * of the next SQP iteration (turbompc/solvers/turbompc_solver.py:1098-1156,
  * optimal_control_problem.py:1217-1272) into the step that consumes it. */
 int tmpc_sqp_admm_step_quadrotor_f32(hipStream_t stream, const tmpc_dims* dims, const tmpc_qp* qp,
@@ -247,6 +247,29 @@ int tmpc_sqp_admm_step_quadrotor_f64(hipStream_t stream, const tmpc_dims* dims, 
                                      const tmpc_state* in, tmpc_state* out, uint32_t* iters_out,
                                      const tmpc_admm_cfg* cfg, const tmpc_sqp_step* sqp, double dt,
                                      const double* params, void* workspace, size_t workspace_bytes);
+
+/* The same SQP step for a QP with K spherical obstacle rows (rows row0 ..
+ * row0 + K - 1 of every stage; centers (B,K,dim), radii (B,K) as in
+ * tmpc_obstacle_linearize_*), which also builds those rows: they are OUTPUTS
+ * of qp->G, qp->l and qp->u, written first with the linearization of
+ * tmpc_obstacle_linearize_* at the input iterate (the first dim entries of
+ * the rows of in->x); the other rows of G, l and u are inputs.  With
+ * TMPC_FLAG_WARM_RECORDS the same values go straight into the workspace's
+ * stage records on the streaming path, and the other rows of G, l and u must
+ * then be the previous call's (the records keep them).  This fuses the
+ * obstacle linearization of the next SQP iteration
+ * (turbompc/solvers/turbompc_solver.py:1098-1156,
+ * optimal_control_problem.py:580-626) into the step that consumes it. */
+int tmpc_sqp_admm_step_obstacle_f32(hipStream_t stream, const tmpc_dims* dims, const tmpc_qp* qp,
+                                    const tmpc_state* in, tmpc_state* out, uint32_t* iters_out,
+                                    const tmpc_admm_cfg* cfg, const tmpc_sqp_step* sqp, int32_t dim, int32_t K,
+                                    const float* centers, const float* radii, int32_t row0, void* workspace,
+                                    size_t workspace_bytes);
+int tmpc_sqp_admm_step_obstacle_f64(hipStream_t stream, const tmpc_dims* dims, const tmpc_qp* qp,
+                                    const tmpc_state* in, tmpc_state* out, uint32_t* iters_out,
+                                    const tmpc_admm_cfg* cfg, const tmpc_sqp_step* sqp, int32_t dim, int32_t K,
+                                    const double* centers, const double* radii, int32_t row0, void* workspace,
+                                    size_t workspace_bytes);
 
 /* ---- ADMM with the PCG Schur solve -----------------------------------------
  * Replaces the `admm_fused_cuda[_f64]` FFI target: AdmmFusedCudaImpl

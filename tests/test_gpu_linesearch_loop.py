@@ -204,3 +204,32 @@ def test_quadrotor_step_linearization_equals_build_qp(dtype, stop):
     _assert_same(*out)
     if stop:
         assert len(set(out[0].num_iter.tolist())) >= 2
+
+
+@pytest.mark.parametrize("dtype", [torch.float64, torch.float32])
+@pytest.mark.parametrize("stop", [False, True])
+@pytest.mark.parametrize("slack", [False, True])
+def test_obstacle_step_linearization_equals_build_qp(dtype, stop, slack):
+    """Config 4's SQP steps build their own obstacle rows
+    (tmpc_sqp_admm_step_obstacle_*: the linearization at the step's input
+    iterate, written into the QP's G, l, u and straight into the stage
+    records, the box rows and the dynamics records kept): the solve is bit
+    for bit the one whose loop builds each QP with build_qp and lets the step
+    copy G, l, u into the records (TMPC_FLAG_WARM_INEQ)."""
+    prob = configs.config4(B=24, seed=8, use_slack_variables=slack, slack_penalization_weight=50.0).to(
+        "cuda", dtype)
+    params = _params(6, 15, 0.0, linesearch=False, criterion="first_order")
+    if stop:
+        params["tol_convergence"] = _tol_splitting(prob, params)
+    out = []
+    for fused in (True, False):
+        p = copy.copy(prob)
+        if not fused:
+            p.step_linearization = lambda: None  # noqa: E731  the build_qp path
+        assert (p.step_linearization() is not None) == fused
+        solver = TurboMPCSolver(p, params)
+        out.append(solver.solve(solver.initial_guess()))
+    torch.cuda.synchronize()
+    _assert_same(*out)
+    if stop:
+        assert len(set(out[0].num_iter.tolist())) >= 2

@@ -231,12 +231,15 @@ def test_sqp_step_check_and_activity(kernel, use_slack, dtype):
         np.testing.assert_array_equal(a[on], p[on])
 
 
-@pytest.mark.parametrize("case", ["quadrotor", "config4", "config4-slack"])
+@pytest.mark.parametrize("case", ["quadrotor", "config4", "config4-slack", "config4-built", "config4-built-slack"])
 def test_sqp_warm_records_match_repacking(case):
     """FLAG_WARM_RECORDS: an SQP solve whose steps rewrite only the records
-    that changed (A_minus and c for the quadrotor; with FLAG_WARM_INEQ also the
-    obstacle rows' G, l, u for config 4) gives the same iterates, bit for bit,
-    as one that repacks every record at every step."""
+    that changed gives the same iterates, bit for bit, as one that repacks
+    every record at every step.  The quadrotor's and config 4's steps write
+    their relinearized rows (A_minus and c; the obstacle rows of G, l, u) into
+    the records themselves and keep the rest (config 4's dynamics records with
+    FLAG_WARM_SAME_DYNAMICS); "built": config 4 with each QP from build_qp,
+    whose obstacle rows the step copies in (FLAG_WARM_INEQ)."""
     import turbompc_amd.solvers.turbompc_solver as ts
     from turbompc_amd.problems import configs
 
@@ -247,7 +250,10 @@ def test_sqp_warm_records_match_repacking(case):
     else:
         prob = configs.config4(B=B, seed=6, use_slack_variables=case.endswith("slack"),
                                slack_penalization_weight=50.0).to("cuda", torch.float32)
-        level, n_sqp, iters = "constraints", 5, 15
+        level, n_sqp, iters = "dynamics", 5, 15
+        if "built" in case:
+            prob.step_linearization = lambda: None  # noqa: E731
+            level = "constraints"
     solver = TurboMPCSolver(prob, _params(n_sqp, iters))
     seen = []
     orig = ts._warm_level

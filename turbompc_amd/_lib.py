@@ -159,6 +159,10 @@ SIGNATURES = {
     "tmpc_sqp_admm_step_f64": [_VP, _PD, _PQ, _PS, _PS, _VP, _PC, _PSQ, _VP, _SZ],
     "tmpc_sqp_admm_step_quadrotor_f32": [_VP, _PD, _PQ, _PS, _PS, _VP, _PC, _PSQ, _F64, _VP, _VP, _SZ],
     "tmpc_sqp_admm_step_quadrotor_f64": [_VP, _PD, _PQ, _PS, _PS, _VP, _PC, _PSQ, _F64, _VP, _VP, _SZ],
+    "tmpc_sqp_admm_step_obstacle_f32": [_VP, _PD, _PQ, _PS, _PS, _VP, _PC, _PSQ, _I32, _I32, _VP, _VP, _I32,
+                                        _VP, _SZ],
+    "tmpc_sqp_admm_step_obstacle_f64": [_VP, _PD, _PQ, _PS, _PS, _VP, _PC, _PSQ, _I32, _I32, _VP, _VP, _I32,
+                                        _VP, _SZ],
     "tmpc_admm_pcg_workspace_bytes": [ctypes.c_int, _PD],
     "tmpc_admm_pcg_f32": [_VP, _PD, _PQ, _PS, _PS, _VP, _VP, _PC, _VP, _SZ],
     "tmpc_admm_pcg_f64": [_VP, _PD, _PQ, _PS, _PS, _VP, _VP, _PC, _VP, _SZ],

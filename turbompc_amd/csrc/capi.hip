@@ -550,17 +550,30 @@ struct QuadLin {
   const double* params;  // host, 7
 };
 
+template <typename R>
+int obstacle_lin_impl(hipStream_t s, int B, int N, int nx, int nu, int dim, int K, const R* states, int ls,
+                      const R* centers, const R* radii, int m, int row0, R* G, R* l, R* u, ObsRecOut<R> rec);
+
+// The obstacle rows of an SQP step that linearizes them itself: K spheres in
+// the first dim state coordinates, rows row0 .. row0 + K - 1 of each stage.
+struct ObsLin {
+  int dim, K, row0;
+  const void* centers;  // (B, K, dim) of the QP's type
+  const void* radii;    // (B, K)
+};
+
 // sq != nullptr: one SQP step -- the first-order check of the input iterate,
 // the activity test, and the ADMM solve of the problems that pass it.  ql
 // != nullptr (with sq): the QP's A_minus and c are outputs, the quadrotor's
 // RK4 linearization at the input iterate (the state's x rows [x_t; u_t]),
 // written before anything reads them and, where warm stage records take
-// them, into the records as well (no repack).
+// them, into the records as well (no repack).  ol != nullptr (with sq): the
+// same for the obstacle rows of G, l and u (the other rows are inputs).
 template <typename R>
 int admm_direct_impl(hipStream_t s, const tmpc_dims* dims, const tmpc_qp* qp,
                      const tmpc_state* in, tmpc_state* out, uint32_t* iters,
                      const tmpc_admm_cfg* cfg, void* ws, size_t wsb, const tmpc_sqp_step* sq = nullptr,
-                     const QuadLin* ql = nullptr) {
+                     const QuadLin* ql = nullptr, const ObsLin* ol = nullptr) {
   if (!dims_ok(dims)) return TMPC_EBADSHAPE;
   if (!cfg || !iters || !qp_ok(qp, dims->m) || !state_ok(in, dims->m) || !state_ok(out, dims->m))
     return TMPC_EBADARG;
@@ -616,12 +629,13 @@ int admm_direct_impl(hipStream_t s, const tmpc_dims* dims, const tmpc_qp* qp,
   const bool pad = dr.n != d.n;
   QPDev<R> qr = a.qp;  // the QP as the record kernels read it
   if (pad) qr.A0 = w.a0p;
-  bool dyn_in_records = false;
+  // warm stage records that a model's own linearization writes directly
+  const bool rows_in_records = stream && (cfg->flags & TMPC_FLAG_WARM_RECORDS) != 0 && !pad;
+  bool dyn_in_records = false, ineq_in_records = false;
   if (ql) {
     if (d.n != 17 || d.nx != 13) return TMPC_EBADSHAPE;
     QuadRecOut<R> rec{};
-    dyn_in_records = stream && (cfg->flags & TMPC_FLAG_WARM_RECORDS) != 0 &&
-                     !((cfg->flags & TMPC_FLAG_WARM_INEQ) != 0 && d.m > 0) && !pad;
+    dyn_in_records = rows_in_records;
     if (dyn_in_records) {
       const RecGeom g = rec_geom(dr, diag);
       rec.am = w.am;
@@ -632,6 +646,24 @@ int admm_direct_impl(hipStream_t s, const tmpc_dims* dims, const tmpc_qp* qp,
     }
     st = quad_impl<R>(s, d.B, d.N, a.st.x, d.n, a.st.x + 13, d.n, ql->dt, ql->params, const_cast<R*>(a.qp.Am),
                       const_cast<R*>(a.qp.c), rec);
+    if (st) return st;
+  }
+  if (ol && ol->K > 0) {
+    ObsRecOut<R> rec{};
+    ineq_in_records = rows_in_records;
+    if (ineq_in_records) {
+      const RecGeom g = rec_geom(dr, diag);
+      rec.am = w.am;
+      rec.rv = w.rv;
+      rec.amp = g.amp;
+      rec.rvp = g.rvp;
+      rec.g_off = (d.nx + ol->row0) * dr.n;  // the G rows follow the A_minus rows
+      rec.l_off = g.l + ol->row0;
+      rec.u_off = g.u + ol->row0;
+    }
+    st = obstacle_lin_impl<R>(s, d.B, d.N, d.nx, d.n - d.nx, ol->dim, ol->K, a.st.x, d.n,
+                              static_cast<const R*>(ol->centers), static_cast<const R*>(ol->radii), d.m, ol->row0,
+                              const_cast<R*>(a.qp.G), const_cast<R*>(a.qp.l), const_cast<R*>(a.qp.u), rec);
     if (st) return st;
   }
   if (given) {
@@ -660,9 +692,11 @@ int admm_direct_impl(hipStream_t s, const tmpc_dims* dims, const tmpc_qp* qp,
   if (stream && (cfg->flags & TMPC_FLAG_WARM_RECORDS)) {
     const unsigned gx = (unsigned)((d.B + kRepackProblems - 1) / kRepackProblems);
     // the A_minus and c rows are rewritten unless they did not change or the
-    // quadrotor step already wrote them
+    // quadrotor step already wrote them; G, l and u when they changed, unless
+    // the obstacle step wrote them (its other rows are the previous call's)
     const bool dyn_rows = !dyn_in_records && (cfg->flags & TMPC_FLAG_WARM_SAME_DYNAMICS) == 0;
-    if ((cfg->flags & TMPC_FLAG_WARM_INEQ) != 0 && d.m > 0)
+    const bool ineq_rows = d.m > 0 && !ineq_in_records && ((cfg->flags & TMPC_FLAG_WARM_INEQ) != 0 || ol);
+    if (ineq_rows)
       hipLaunchKernelGGL((stage_repack_dynamics_kernel<R, true>), dim3(gx, (unsigned)d.T), dim3(256), 0, s, dr,
                          a.qp.Am, a.qp.c, a.qp.G, a.qp.l, a.qp.u, w.am, w.rv, diag ? 1 : 0, dyn_rows ? 1 : 0);
     else if (dyn_rows)
@@ -1275,20 +1309,21 @@ inline int obstacle_check(int B, int N, int nx, int nu, int dim, int K, int m, i
 }
 
 template <typename R>
-int obstacle_lin_impl(hipStream_t s, int B, int N, int nx, int nu, int dim, int K, const R* states,
-                      const R* centers, const R* radii, int m, int row0, R* G, R* l, R* u) {
+int obstacle_lin_impl(hipStream_t s, int B, int N, int nx, int nu, int dim, int K, const R* states, int ls,
+                      const R* centers, const R* radii, int m, int row0, R* G, R* l, R* u, ObsRecOut<R> rec) {
   int st = obstacle_check(B, N, nx, nu, dim, K, m, row0);
   if (st) return st;
   if (K == 0) return TMPC_OK;
   if (!states || !centers || !radii || !G || !l || !u) return TMPC_EBADARG;
+  if (ls < nx) return TMPC_EBADSHAPE;
   const int T = N + 1, n = nx + nu;
   const long long rows = (long long)B * T * K;  // one thread per obstacle row
   if (rows >= INT32_MAX) return TMPC_EBADSHAPE;
   const int blk = kObstacleBlock;
   const long long grid = (rows + blk - 1) / blk;
   const size_t smem = (size_t)blk * n * sizeof(R);  // n <= 64: at most 64 KB
-  hipLaunchKernelGGL((obstacle_linearize_kernel<R>), dim3((unsigned)grid), dim3(blk), smem, s, B, T, nx, n, dim, K,
-                     states, centers, radii, m, row0, G, l, u);
+  hipLaunchKernelGGL((obstacle_linearize_kernel<R>), dim3((unsigned)grid), dim3(blk), smem, s, B, T, ls, n, dim, K,
+                     states, centers, radii, m, row0, G, l, u, rec);
   return launch_status();
 }
 
@@ -1658,12 +1693,14 @@ int tmpc_quadrotor_lagrangian_hessian_f64(hipStream_t s, int32_t B, int32_t N, c
 int tmpc_obstacle_linearize_f32(hipStream_t s, int32_t B, int32_t N, int32_t nx, int32_t nu, int32_t dim,
                                 int32_t K, const float* states, const float* centers, const float* radii, int32_t m,
                                 int32_t row0, float* G, float* l, float* u) {
-  return obstacle_lin_impl<float>(s, B, N, nx, nu, dim, K, states, centers, radii, m, row0, G, l, u);
+  return obstacle_lin_impl<float>(s, B, N, nx, nu, dim, K, states, nx, centers, radii, m, row0, G, l, u,
+                                 ObsRecOut<float>{});
 }
 int tmpc_obstacle_linearize_f64(hipStream_t s, int32_t B, int32_t N, int32_t nx, int32_t nu, int32_t dim,
                                 int32_t K, const double* states, const double* centers, const double* radii,
                                 int32_t m, int32_t row0, double* G, double* l, double* u) {
-  return obstacle_lin_impl<double>(s, B, N, nx, nu, dim, K, states, centers, radii, m, row0, G, l, u);
+  return obstacle_lin_impl<double>(s, B, N, nx, nu, dim, K, states, nx, centers, radii, m, row0, G, l, u,
+                                 ObsRecOut<double>{});
 }
 int tmpc_obstacle_lagrangian_hessian_f32(hipStream_t s, int32_t B, int32_t N, int32_t nx, int32_t nu, int32_t dim,
                                          int32_t K, const float* states, const float* centers, const float* radii,
@@ -1710,6 +1747,23 @@ int tmpc_sqp_admm_step_quadrotor_f64(hipStream_t s, const tmpc_dims* dims, const
   if (!qp || !qp->A_minus || !qp->c || !params || !sqp) return TMPC_EBADARG;
   const QuadLin ql{dt, params};
   return admm_direct_impl<double>(s, dims, qp, in, out, iters, cfg, ws, wsb, sqp, &ql);
+}
+
+int tmpc_sqp_admm_step_obstacle_f32(hipStream_t s, const tmpc_dims* dims, const tmpc_qp* qp, const tmpc_state* in,
+                                    tmpc_state* out, uint32_t* iters, const tmpc_admm_cfg* cfg,
+                                    const tmpc_sqp_step* sqp, int32_t dim, int32_t K, const float* centers,
+                                    const float* radii, int32_t row0, void* ws, size_t wsb) {
+  if (!qp || !qp->G || !qp->l || !qp->u || !sqp || (K > 0 && (!centers || !radii))) return TMPC_EBADARG;
+  const ObsLin ol{dim, K, row0, centers, radii};
+  return admm_direct_impl<float>(s, dims, qp, in, out, iters, cfg, ws, wsb, sqp, nullptr, &ol);
+}
+int tmpc_sqp_admm_step_obstacle_f64(hipStream_t s, const tmpc_dims* dims, const tmpc_qp* qp, const tmpc_state* in,
+                                    tmpc_state* out, uint32_t* iters, const tmpc_admm_cfg* cfg,
+                                    const tmpc_sqp_step* sqp, int32_t dim, int32_t K, const double* centers,
+                                    const double* radii, int32_t row0, void* ws, size_t wsb) {
+  if (!qp || !qp->G || !qp->l || !qp->u || !sqp || (K > 0 && (!centers || !radii))) return TMPC_EBADARG;
+  const ObsLin ol{dim, K, row0, centers, radii};
+  return admm_direct_impl<double>(s, dims, qp, in, out, iters, cfg, ws, wsb, sqp, nullptr, &ol);
 }
 
 int tmpc_kkt_active_sets_f32(hipStream_t s, int64_t count, const float* g, const float* l, const float* u,

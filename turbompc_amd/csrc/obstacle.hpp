@@ -35,13 +35,26 @@ constexpr double kObstacleLower = -1.0e9;
 // B T K < 2^31); G addresses are formed in 64 bits.
 constexpr int kObstacleBlock = 128;
 
+// Optional second destination of the rows: the streaming solve's stage
+// records (the M record of (t, b) at am + (t B + b) amp, its rows of n
+// entries, the obstacle rows from g_off; l and u at l_off and u_off of the rv
+// record), so that an SQP step needs no copy of them.
 template <typename R>
-__global__ __launch_bounds__(kObstacleBlock) void obstacle_linearize_kernel(int B, int T, int nx, int n, int dim,
+struct ObsRecOut {
+  R* am = nullptr;  // null: the QP layout only
+  R* rv = nullptr;
+  int amp = 0, rvp = 0, g_off = 0, l_off = 0, u_off = 0;
+};
+
+// states: rows of ls >= dim elements per (b, t) (the positions first)
+template <typename R>
+__global__ __launch_bounds__(kObstacleBlock) void obstacle_linearize_kernel(int B, int T, int ls, int n, int dim,
                                                                             int K, const R* __restrict__ states,
                                                                             const R* __restrict__ centers,
                                                                             const R* __restrict__ radii, int m,
                                                                             int row0, R* __restrict__ G,
-                                                                            R* __restrict__ l, R* __restrict__ u) {
+                                                                            R* __restrict__ l, R* __restrict__ u,
+                                                                            ObsRecOut<R> rec) {
   extern __shared__ __align__(16) unsigned char smem_raw[];
   R* rowv = reinterpret_cast<R*>(smem_raw);  // [kObstacleBlock][n]
   const unsigned rows = (unsigned)B * (unsigned)T * (unsigned)K;
@@ -50,7 +63,7 @@ __global__ __launch_bounds__(kObstacleBlock) void obstacle_linearize_kernel(int 
   if (r < rows) {
     const unsigned bt = r / (unsigned)K, k = r - bt * (unsigned)K;
     const unsigned b = bt / (unsigned)T;
-    const R* x = states + (size_t)bt * nx;
+    const R* x = states + (size_t)bt * ls;
     const R* c = centers + ((size_t)b * K + k) * dim;
     R ss = R(0);
     for (int i = 0; i < dim; ++i) {
@@ -69,8 +82,14 @@ __global__ __launch_bounds__(kObstacleBlock) void obstacle_linearize_kernel(int 
     for (int j = dim; j < n; ++j) g[j] = R(0);
     const R off = (R(1) - nrm / den) - gx;
     const size_t row = (size_t)bt * m + row0 + k;
-    l[row] = R(kObstacleLower) - off;
-    u[row] = R(0) - off;
+    const R lo = R(kObstacleLower) - off, hi = R(0) - off;
+    l[row] = lo;
+    u[row] = hi;
+    if (rec.rv != nullptr) {
+      const size_t ri = (size_t)(bt - b * (unsigned)T) * B + b;  // the record of (t, b)
+      rec.rv[ri * rec.rvp + rec.l_off + k] = lo;
+      rec.rv[ri * rec.rvp + rec.u_off + k] = hi;
+    }
   }
   __syncthreads();
   const unsigned nb = rows - r0 < (unsigned)kObstacleBlock ? rows - r0 : (unsigned)kObstacleBlock;
@@ -78,6 +97,11 @@ __global__ __launch_bounds__(kObstacleBlock) void obstacle_linearize_kernel(int 
     const unsigned lr = e / (unsigned)n, j = e - lr * (unsigned)n;
     const unsigned rr = r0 + lr, bt = rr / (unsigned)K, k = rr - bt * (unsigned)K;
     G[((size_t)bt * m + row0 + k) * n + j] = rowv[e];
+    if (rec.am != nullptr) {
+      const unsigned b = bt / (unsigned)T;
+      const size_t ri = (size_t)(bt - b * (unsigned)T) * B + b;
+      rec.am[ri * rec.amp + rec.g_off + k * n + j] = rowv[e];
+    }
   }
 }
 

@@ -79,6 +79,28 @@ class ObstacleOCP(LinearOCP):
     def inequality_blocks(self):
         raise NotImplementedError("obstacle rows depend on the iterate; use inequality_blocks_at(states, controls)")
 
+    def step_linearization(self):
+        """The keywords of an SQP step that builds the obstacle rows itself
+        (ADMMSolver.sqp_step(obstacles=...), tmpc_sqp_admm_step_obstacle_*), or
+        None with rescaling (the step writes the unscaled rows) or without
+        obstacles."""
+        if self.rescale_optimization_variables or self.num_obstacles == 0:
+            return None
+        from ..solvers.admm.admm_hip_backend import ObstacleRows
+
+        return {"obstacles": ObstacleRows(self.obstacles_dimension, self.num_obstacles, self.centers, self.radii,
+                                          self.num_box_constraints)}
+
+    def qp_for_next_step(self, prev: QPData) -> QPData:
+        """The QP of the next SQP iteration with its obstacle rows left to the
+        step that solves it: prev itself, the previous step's QP (from
+        build_qp or from here).  Its other blocks do not depend on the
+        iterate (the dynamics blocks are built once), and the step overwrites
+        the obstacle rows of its G, l and u with the linearization at the
+        step's input iterate, the ADMM state's x (the iterate build_qp would
+        be given); their box rows stay."""
+        return prev
+
     def inequality_values(self, states, controls):
         """(g, l, u): the box rows, then g_k = 1 - |p - c_k| / (r_k + 0.001) with
         bounds (-1e9, 0) (obstacle_avoidance.py:16-52)."""

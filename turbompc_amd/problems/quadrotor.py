@@ -16,6 +16,7 @@ from __future__ import annotations
 
 import ctypes
 import math
+from typing import Optional
 
 import torch
 
@@ -69,17 +70,18 @@ class QuadrotorOCP(QuadraticTrackingOCP):
         return Am, c
 
     def step_linearization(self):
-        """(dt, params) for an SQP step that builds this problem's dynamics
-        rows itself (ADMMSolver.sqp_step(quadrotor=...)), or None with
-        rescaling (the step writes the unscaled rows)."""
-        return None if self.rescale_optimization_variables else (self.dt, self._cparams)
+        """The keywords of an SQP step that builds this problem's dynamics
+        rows itself (ADMMSolver.sqp_step(quadrotor=(dt, params))), or None
+        with rescaling (the step writes the unscaled rows)."""
+        return None if self.rescale_optimization_variables else {"quadrotor": (self.dt, self._cparams)}
 
-    def qp_for_next_step(self) -> QPData:
+    def qp_for_next_step(self, prev: Optional[QPData] = None) -> QPData:
         """The QP of the next SQP iteration with its dynamics rows left to the
         step that solves it: A_minus and c are empty buffers that
         tmpc_sqp_admm_step_quadrotor_* fills with the linearization at the
         step's input iterate, the ADMM state's x (the iterate build_qp would
-        be given).  The other blocks are this problem's, as in build_qp."""
+        be given).  The other blocks are this problem's, as in build_qp
+        (prev, the previous step's QP, is not needed)."""
         B, N = self.B, self.horizon
         Am = torch.empty((B, N, 13, 17), dtype=self.dtype, device=self.device)
         c = torch.empty((B, N, 13), dtype=self.dtype, device=self.device)

@@ -215,7 +215,7 @@ class ADMMSolver:
                  rho_bar: float = 1.0, alpha: float = 1.0, *, slack_weight=0.0,
                  workspace: Optional[torch.Tensor] = None, warm_records: bool = False,
                  warm_ineq: bool = False, donate_state: bool = False, iters_out: Optional[torch.Tensor] = None,
-                 quadrotor=None, same_dynamics: bool = False):
+                 quadrotor=None, obstacles=None, same_dynamics: bool = False):
         """One device SQP step (tmpc_sqp_admm_step_*): the first-order check of
         admm_state0's iterate against qp_data, the activity test
         active & (conv > tol), and the solve of the problems that pass it (the
@@ -232,7 +232,10 @@ class ADMMSolver:
         solve (raw iteration words, stats num_iter and nonfinite None).
         quadrotor = (dt, params): qp_data's A_minus and c are outputs, built
         by the step as the quadrotor's linearization at admm_state0's x
-        (QuadrotorOCP.qp_for_next_step; tmpc_sqp_admm_step_quadrotor_*).  Returns
+        (QuadrotorOCP.qp_for_next_step; tmpc_sqp_admm_step_quadrotor_*).
+        obstacles (admm_hip_backend.ObstacleRows): the obstacle rows of
+        qp_data's G, l and u are outputs in the same way
+        (ObstacleOCP.qp_for_next_step; tmpc_sqp_admm_step_obstacle_*).  Returns
         ((states, controls), stats, state, (conv, eq_err, ineq_err, g), active_out)."""
         if self._admm_backend != AdmmBackend.HIP_DIRECT:
             raise ValueError("sqp_step needs the direct Schur solve (HIP_DIRECT)")
@@ -250,7 +253,7 @@ class ADMMSolver:
         sw = slack_weight if self._use_slack else None
         outs, iters, _, (conv, eq, iq, g, act) = hip.admm_hip_solve(
             qp_data, admm_state0, schur="direct", cfg=cfg, slack_weight=sw, sqp=(active, tol), workspace=workspace,
-            donate=donate_state, iters_out=iters_out, quadrotor=quadrotor)
+            donate=donate_state, iters_out=iters_out, quadrotor=quadrotor, obstacles=obstacles)
         x, z, yg, y0, yf, xi, rho = outs
         state = ADMMState(x_blocks=x, y_g=yg, y_f_0=y0, y_f_dyn=yf, z_g=z, xi_g=xi, rho_bar=rho)
         states, controls = unpack_x(x, self._zshape)

@@ -11,7 +11,7 @@ needed.
 from __future__ import annotations
 
 import ctypes
-from typing import Optional, Tuple
+from typing import NamedTuple, Optional, Tuple
 
 import torch
 
@@ -84,10 +84,23 @@ def direct_workspace(qp: QPData) -> torch.Tensor:
     return _lib.workspace(nbytes, qp.device)
 
 
+class ObstacleRows(NamedTuple):
+    """Obstacle rows that an SQP step linearizes itself
+    (tmpc_sqp_admm_step_obstacle_*): K spheres (centers (B, K, dim), radii
+    (B, K)) in the first dim state coordinates, rows row0 .. row0 + K - 1 of
+    every stage."""
+    dim: int
+    K: int
+    centers: torch.Tensor
+    radii: torch.Tensor
+    row0: int
+
+
 def admm_hip_solve(qp: QPData, state0, *, schur: str, cfg: _lib.AdmmCfg,
                    slack_weight: Optional[torch.Tensor] = None, want_pcg_iters: bool = False, sqp=None,
                    workspace: Optional[torch.Tensor] = None, donate: bool = False,
-                   iters_out: Optional[torch.Tensor] = None, quadrotor=None):
+                   iters_out: Optional[torch.Tensor] = None, quadrotor=None,
+                   obstacles: Optional["ObstacleRows"] = None):
     """Run the fused ADMM on the device.  `state0` is an ADMMState of batched
     tensors; returns (state fields tuple, iters (B,), pcg_iters or None).
 
@@ -109,7 +122,12 @@ def admm_hip_solve(qp: QPData, state0, *, schur: str, cfg: _lib.AdmmCfg,
 
     quadrotor = (dt, params as a ctypes double[7]) with sqp: the step builds
     the QP's dynamics rows itself (tmpc_sqp_admm_step_quadrotor_*):
-    qp.eq.A_minus and qp.eq.c are outputs, the linearization at state0's x."""
+    qp.eq.A_minus and qp.eq.c are outputs, the linearization at state0's x.
+    obstacles (ObstacleRows) with sqp: the same for the obstacle rows of
+    qp.ineq.G, l and u (tmpc_sqp_admm_step_obstacle_*; their other rows are
+    inputs)."""
+    if quadrotor is not None and obstacles is not None:
+        raise ValueError("a step builds either the quadrotor's or the obstacle rows")
     if sqp is not None and schur != "direct":
         raise ValueError("an SQP step (sqp=...) needs the direct Schur solve")
     lib = _lib.load()
@@ -170,7 +188,18 @@ def admm_hip_solve(qp: QPData, state0, *, schur: str, cfg: _lib.AdmmCfg,
                 g = torch.empty((B, T, m), dtype=dt, device=dev)
                 sq = _lib.SqpStep(_lib.ptr(act_in), _lib.ptr(act_out), float(tol), _lib.ptr(conv), _lib.ptr(eq),
                                   _lib.ptr(iq), _lib.ptr(g))
-            if quadrotor is None:
+            if obstacles is not None:
+                if not all(t.is_contiguous() for t in (qp.ineq.G, qp.ineq.l, qp.ineq.u)):
+                    raise ValueError("the obstacle step writes G, l and u in place: they must be contiguous")
+                centers = obstacles.centers.to(device=dev, dtype=dt).contiguous()
+                radii = obstacles.radii.to(device=dev, dtype=dt).contiguous()
+                fn = f"tmpc_sqp_admm_step_obstacle_{sfx}"
+                st = getattr(lib, fn)(
+                    stream, ctypes.byref(dims), ctypes.byref(cq), ctypes.byref(sv), ctypes.byref(sv),
+                    _lib.ptr(iters), ctypes.byref(cfg), ctypes.byref(sq), int(obstacles.dim), int(obstacles.K),
+                    _lib.ptr(centers), _lib.ptr(radii), int(obstacles.row0), _lib.ptr(ws), nbytes,
+                )
+            elif quadrotor is None:
                 fn = f"tmpc_sqp_admm_step_{sfx}"
                 st = getattr(lib, fn)(
                     stream, ctypes.byref(dims), ctypes.byref(cq), ctypes.byref(sv), ctypes.byref(sv),

@@ -601,10 +601,11 @@ class TurboMPCSolver:
         # steps, so a step whose QP differs from the previous one only in the
         # relinearized dynamics (A_minus, c) rewrites just those records
         ws = admm_direct_workspace(qp)
-        # a problem whose SQP step can build its own dynamics rows (the
-        # quadrotor): each later QP leaves A_minus and c to the step, which
-        # linearizes at its input iterate -- the iterate build_qp would get --
-        # straight into the stage records as well
+        # a problem whose SQP step can build its own relinearized rows (the
+        # quadrotor's dynamics rows, the obstacle rows): each later QP leaves
+        # them to the step, which linearizes at its input iterate -- the
+        # iterate build_qp would get -- straight into the stage records as
+        # well; lin holds the step's keywords
         lin = getattr(program, "step_linearization", None)
         lin = lin() if lin is not None else None
         prev = None
@@ -621,7 +622,7 @@ class TurboMPCSolver:
                 (states, controls), _, admm_state, (cv, e, i, g), act = admm.sqp_step(
                     qp, admm_state, active, tol, rho_bar=ap["rho"], alpha=alpha, slack_weight=sw, workspace=ws,
                     warm_records=warm is not None, warm_ineq=warm == "constraints", donate_state=True,
-                    iters_out=words[it], quadrotor=lin, same_dynamics=_same_dynamics(qp, prev))
+                    iters_out=words[it], same_dynamics=_same_dynamics(qp, prev), **(lin or {}))
                 states, controls = self._from_qp(program, states, controls)
                 # the check belongs to the iterate committed at it - 1 (the
                 # records of a stopped problem stay zero, as in the reference)
@@ -641,7 +642,7 @@ class TurboMPCSolver:
             last = it
             prev = qp
             if it + 1 < max_iter:
-                qp = program.qp_for_next_step() if lin is not None else program.build_qp(states, controls)
+                qp = program.qp_for_next_step(qp) if lin is not None else program.build_qp(states, controls)
         if conv is None:
             conv = torch.full((B,), float("inf"), dtype=dt, device=dev)
         # the last committed iterate is not checked (the reference evaluates no
