@@ -1321,7 +1321,8 @@ int obstacle_lin_impl(hipStream_t s, int B, int N, int nx, int nu, int dim, int 
   if (rows >= INT32_MAX) return TMPC_EBADSHAPE;
   const int blk = kObstacleBlock;
   const long long grid = (rows + blk - 1) / blk;
-  const size_t smem = (size_t)blk * n * sizeof(R);  // n <= 64: at most 64 KB
+  const size_t smem = (size_t)blk * (2 * sizeof(size_t) + n * sizeof(R));  // n <= 64: at most 66 KB
+  lds_optin(obstacle_linearize_kernel<R>, smem);
   hipLaunchKernelGGL((obstacle_linearize_kernel<R>), dim3((unsigned)grid), dim3(blk), smem, s, B, T, ls, n, dim, K,
                      states, centers, radii, m, row0, G, l, u, rec);
   return launch_status();

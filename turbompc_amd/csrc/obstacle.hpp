@@ -56,7 +56,11 @@ __global__ __launch_bounds__(kObstacleBlock) void obstacle_linearize_kernel(int 
                                                                             R* __restrict__ l, R* __restrict__ u,
                                                                             ObsRecOut<R> rec) {
   extern __shared__ __align__(16) unsigned char smem_raw[];
-  R* rowv = reinterpret_cast<R*>(smem_raw);  // [kObstacleBlock][n]
+  // each row's destinations (element offsets of its first entry in G and in
+  // the records), then its n entries
+  size_t* qrow = reinterpret_cast<size_t*>(smem_raw);  // [kObstacleBlock]
+  size_t* rrow = qrow + kObstacleBlock;                 // [kObstacleBlock]
+  R* rowv = reinterpret_cast<R*>(rrow + kObstacleBlock);  // [kObstacleBlock][n]
   const unsigned rows = (unsigned)B * (unsigned)T * (unsigned)K;
   const unsigned r0 = blockIdx.x * kObstacleBlock;
   const unsigned r = r0 + threadIdx.x;
@@ -85,22 +89,25 @@ __global__ __launch_bounds__(kObstacleBlock) void obstacle_linearize_kernel(int 
     const R lo = R(kObstacleLower) - off, hi = R(0) - off;
     l[row] = lo;
     u[row] = hi;
+    qrow[threadIdx.x] = row * n;
     if (rec.rv != nullptr) {
       const size_t ri = (size_t)(bt - b * (unsigned)T) * B + b;  // the record of (t, b)
       rec.rv[ri * rec.rvp + rec.l_off + k] = lo;
       rec.rv[ri * rec.rvp + rec.u_off + k] = hi;
+      rrow[threadIdx.x] = ri * rec.amp + rec.g_off + (size_t)k * n;
     }
   }
   __syncthreads();
+  // the block's rows in passes of kObstacleBlock / n rows, a thread per entry
+  // (n <= 64: at least two rows per pass)
   const unsigned nb = rows - r0 < (unsigned)kObstacleBlock ? rows - r0 : (unsigned)kObstacleBlock;
-  for (unsigned e = threadIdx.x; e < nb * (unsigned)n; e += kObstacleBlock) {
-    const unsigned lr = e / (unsigned)n, j = e - lr * (unsigned)n;
-    const unsigned rr = r0 + lr, bt = rr / (unsigned)K, k = rr - bt * (unsigned)K;
-    G[((size_t)bt * m + row0 + k) * n + j] = rowv[e];
-    if (rec.am != nullptr) {
-      const unsigned b = bt / (unsigned)T;
-      const size_t ri = (size_t)(bt - b * (unsigned)T) * B + b;
-      rec.am[ri * rec.amp + rec.g_off + k * n + j] = rowv[e];
+  const unsigned per = (unsigned)kObstacleBlock / (unsigned)n;
+  const unsigned lr0 = threadIdx.x / (unsigned)n, j = threadIdx.x - lr0 * (unsigned)n;
+  if (lr0 < per) {
+    for (unsigned lr = lr0; lr < nb; lr += per) {
+      const R v = rowv[lr * n + j];
+      G[qrow[lr] + j] = v;
+      if (rec.am != nullptr) rec.am[rrow[lr] + j] = v;
     }
   }
 }
