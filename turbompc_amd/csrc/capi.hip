@@ -37,6 +37,43 @@ constexpr size_t kAlign = 256;
 hipEvent_t g_iter_events[2] = {nullptr, nullptr};
 inline size_t align_up(size_t x) { return (x + kAlign - 1) / kAlign * kAlign; }
 
+constexpr int kMaxDevices = 64;
+
+// A second stream for work that overlaps the factorization (default
+// priority, one per host thread and device, created on first use), with the
+// events that fork it from and join it back to the caller's stream.  The
+// factorization runs at one wavefront per SIMD and waits on its pivot chain
+// for much of the time, so a short memory-bound kernel beside it costs
+// little.  nullptr where it cannot be had (the work then runs in order on
+// the caller's stream).
+struct SideStream {
+  hipStream_t q = nullptr;
+  hipEvent_t fork = nullptr, join = nullptr;
+};
+thread_local SideStream t_side[kMaxDevices];
+
+SideStream* side_stream(hipStream_t s) {
+  int dev = -1;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) return nullptr;
+  if (s != nullptr) {
+    hipDevice_t sdev = -1;
+    if (hipStreamGetDevice(s, &sdev) != hipSuccess || (int)sdev != dev) return nullptr;
+  }
+  SideStream& x = t_side[dev];
+  if (x.q == nullptr) {
+    SideStream y;
+    if (hipStreamCreateWithFlags(&y.q, hipStreamNonBlocking) != hipSuccess) return nullptr;
+    if (hipEventCreateWithFlags(&y.fork, hipEventDisableTiming) != hipSuccess ||
+        hipEventCreateWithFlags(&y.join, hipEventDisableTiming) != hipSuccess) {
+      if (y.fork) (void)hipEventDestroy(y.fork);
+      (void)hipStreamDestroy(y.q);
+      return nullptr;
+    }
+    x = y;
+  }
+  return &x;
+}
+
 struct Carver {
   char* base;
   size_t off = 0;
@@ -573,7 +610,7 @@ template <typename R>
 int admm_direct_impl(hipStream_t s, const tmpc_dims* dims, const tmpc_qp* qp,
                      const tmpc_state* in, tmpc_state* out, uint32_t* iters,
                      const tmpc_admm_cfg* cfg, void* ws, size_t wsb, const tmpc_sqp_step* sq = nullptr,
-                     const QuadLin* ql = nullptr, const ObsLin* ol = nullptr) {
+                     const QuadLin* ql = nullptr, const ObsLin* ol = nullptr, bool overlap = true) {
   if (!dims_ok(dims)) return TMPC_EBADSHAPE;
   if (!cfg || !iters || !qp_ok(qp, dims->m) || !state_ok(in, dims->m) || !state_ok(out, dims->m))
     return TMPC_EBADARG;
@@ -704,32 +741,45 @@ int admm_direct_impl(hipStream_t s, const tmpc_dims* dims, const tmpc_qp* qp,
                          a.qp.Am, a.qp.c, a.qp.G, a.qp.l, a.qp.u, w.am, w.rv, diag ? 1 : 0, 1);
     st = launch_status();
     if (st) return st;
-    st = launch_factor_std<R>(s, dr, w, qr, a.st.rho, a.sigma, a.rho_f_factor, nullptr, fp, diag, fgroups);
   } else if (stream) {
     hipLaunchKernelGGL((stage_pack_kernel<R>), dim3((unsigned)((d.B + kPackWaves - 1) / kPackWaves), (unsigned)d.T),
                        dim3(kWave * kPackWaves), 0, s, dr, a.qp, a.st, w.am, w.rv, w.dm, diag ? 1 : 0,
                        pad ? w.a0p : (R*)nullptr);
     st = launch_status();
     if (st) return st;
-    st = launch_factor_std<R>(s, dr, w, qr, a.st.rho, a.sigma, a.rho_f_factor, nullptr, fp, diag, fgroups);
-  } else {
-    st = launch_factor_qp<R>(s, d, a.qp, a.st.rho, a.sigma, a.rho_f_factor, nullptr, w.thinv);
   }
-  if (st) return st;
-  if (ainv) {
-    // the stage-invariant entries of this call's A_minus rows: partial masks
-    // in the compressed-run region (written later by the streaming kernel),
-    // then their OR (kernels only, no memset, so the call can be captured)
+  // the stage-invariant entries of this call's A_minus rows: partial masks
+  // in the compressed-run region (written later by the streaming kernel),
+  // then their OR (kernels only, no memset, so the call can be captured).
+  // They read the stage records the factorization reads (and write nothing
+  // it touches), so they run beside it on the side stream where there is
+  // one: forked after the records are written, joined before the iterations.
+  auto launch_ainv = [&](hipStream_t q) {
     if (d.N > 1) {
       const int nparts = (d.B + kAinvWaves - 1) / kAinvWaves;
       uint32_t* part = reinterpret_cast<uint32_t*>(w.ac);
-      hipLaunchKernelGGL((ainv_partial_kernel<R>), dim3((unsigned)nparts), dim3(kWave * kAinvWaves), 0, s, dr,
+      hipLaunchKernelGGL((ainv_partial_kernel<R>), dim3((unsigned)nparts), dim3(kWave * kAinvWaves), 0, q, dr,
                          (const R*)w.am, part);
-      hipLaunchKernelGGL(ainv_reduce_kernel, dim3(1), dim3(256), 0, s, (const uint32_t*)part, nparts, w.amask);
+      hipLaunchKernelGGL(ainv_reduce_kernel, dim3(1), dim3(256), 0, q, (const uint32_t*)part, nparts, w.amask);
     } else {
-      hipLaunchKernelGGL((fill_kernel<uint32_t>), dim3(1), dim3(256), 0, s, w.amask, (size_t)kAinvWords, 0u);
+      hipLaunchKernelGGL((fill_kernel<uint32_t>), dim3(1), dim3(256), 0, q, w.amask, (size_t)kAinvWords, 0u);
     }
-    st = launch_status();
+    return launch_status();
+  };
+  SideStream* side = ainv && overlap ? side_stream(s) : nullptr;
+  if (side) {
+    if (hipEventRecord(side->fork, s) != hipSuccess || hipStreamWaitEvent(side->q, side->fork, 0) != hipSuccess)
+      return TMPC_ELAUNCH;
+    st = launch_ainv(side->q);
+    if (st) return st;
+    if (hipEventRecord(side->join, side->q) != hipSuccess) return TMPC_ELAUNCH;
+  }
+  st = stream ? launch_factor_std<R>(s, dr, w, qr, a.st.rho, a.sigma, a.rho_f_factor, nullptr, fp, diag, fgroups)
+              : launch_factor_qp<R>(s, d, a.qp, a.st.rho, a.sigma, a.rho_f_factor, nullptr, w.thinv);
+  if (side && hipStreamWaitEvent(s, side->join, 0) != hipSuccess) return TMPC_ELAUNCH;
+  if (st) return st;
+  if (ainv && !side) {
+    st = launch_ainv(s);
     if (st) return st;
   }
   const std::vector<int> bounds = chunk_bounds(cfg->max_iter, cfg->check_every, cfg->adapt_rho_every);
@@ -765,7 +815,6 @@ int admm_direct_impl(hipStream_t s, const tmpc_dims* dims, const tmpc_qp* qp,
 // ------------------------------------------------------- allocation-free ----
 // Device address of `scratch` on each device, looked up once per device with
 // that device current (each GPU holds its own copy at its own address).
-constexpr int kMaxDevices = 64;
 std::mutex g_scratch_mu;
 void* g_scratch_ptr[kMaxDevices] = {};
 
@@ -801,7 +850,9 @@ int admm_direct_noalloc_impl(hipStream_t s, const tmpc_dims* dims, const tmpc_qp
   void* ws = nullptr;
   const int st = noalloc_scratch(s, &ws);
   if (st) return st;
-  return admm_direct_impl<R>(s, dims, qp, in, out, iters, cfg, ws, TMPC_NOALLOC_SCRATCH_BYTES);
+  // everything on the caller's stream: no side stream is created here
+  return admm_direct_impl<R>(s, dims, qp, in, out, iters, cfg, ws, TMPC_NOALLOC_SCRATCH_BYTES, nullptr, nullptr,
+                             nullptr, false);
 }
 
 // ---------------------------------------------------------------- blktri ----
