@@ -160,6 +160,52 @@ def test_first_order_check_kernel_matches_dense_assembly(std, dtype, use_slack, 
         assert rel_err(g[b].reshape(-1), gv) < tol * 10
 
 
+@pytest.mark.parametrize("std", [False, True])
+@pytest.mark.parametrize("use_slack", [False, True])
+def test_first_order_check_large_batch_equals_small_batches(std, use_slack):
+    """A batch large enough that each wavefront of the check kernel walks
+    several stages (B T >= 2 * 16384; here B = 1536, T = 23: two stages per
+    wave, the last wave of each problem one) gives, problem for problem
+    and bit for bit, the values of small batches (one stage per wave).  Each
+    problem gets its own NaN or infinite entry in some rows, so the per-wave
+    folding of the stage maxima must keep what the per-stage atomics kept."""
+    from helpers import random_qp
+    from turbompc_amd.solvers.qp_data import QPCostBlocks, QPData, QPEqualityBlocks, QPInequalityBlocks
+    from turbompc_amd.solvers.sqp_hip import first_order_check
+
+    B, T, n, nx, m = 1536, 23, 9, 6, 5
+    dtype = torch.float32
+    qp = random_qp(B, T, n, nx, m, seed=23, std=std, diag=True).to("cuda", dtype)
+    gen = torch.Generator(device="cpu").manual_seed(5)
+    rnd = lambda *s: torch.randn(s, generator=gen, dtype=dtype).to("cuda")  # noqa: E731
+    x, yg, y0, yf = rnd(B, T, n), rnd(B, T, m), rnd(B, nx), rnd(B, T - 1, nx)
+    sl = rnd(B, T, m) * 0.3 if use_slack else None
+    x[7, 3, 2] = float("nan")
+    x[100, 20, 0] = float("inf")
+    yg[901, 0, 1] = float("nan")
+    big = first_order_check(qp, x, y0, yf, yg, sl, 2.5, std_dynamics=std, diag_cost=True)
+
+    def part(t, lo, hi):
+        return t[lo:hi].contiguous()
+
+    def sub(lo, hi):
+        c, e, i = qp.cost, qp.eq, qp.ineq
+        q = QPData(cost=QPCostBlocks(part(c.D, lo, hi), part(c.E, lo, hi), part(c.q, lo, hi)),
+                   eq=QPEqualityBlocks(part(e.A0, lo, hi), part(e.A_minus, lo, hi), part(e.A_plus, lo, hi),
+                                       part(e.c0, lo, hi), part(e.c, lo, hi)),
+                   ineq=QPInequalityBlocks(part(i.G, lo, hi), part(i.l, lo, hi), part(i.u, lo, hi),
+                                           i.slack_penalization_weight, i.use_slack_variables))
+        return first_order_check(q, part(x, lo, hi), part(y0, lo, hi), part(yf, lo, hi), part(yg, lo, hi),
+                                 part(sl, lo, hi) if use_slack else None, 2.5, std_dynamics=std, diag_cost=True)
+
+    for lo in range(0, B, 256):
+        small = sub(lo, lo + 256)
+        for a, b in zip(big, small):
+            a, b = a[lo:lo + 256], b
+            nan_a, nan_b = torch.isnan(a), torch.isnan(b)
+            assert torch.equal(nan_a, nan_b) and torch.equal(a[~nan_a], b[~nan_b]), lo
+
+
 def _random_state(qp, rng, dtype, use_slack):
     from turbompc_amd.solvers.admm.admm import ADMMState
 

@@ -1400,16 +1400,17 @@ template <typename R, int NC>
 void launch_sqp_nc(hipStream_t s, const Dims& d, bool std_dyn, int diag, const QPDev<R>& q, const R* x,
                    const R* y0, const R* yf, const R* yg, const R* sl, R sw, R* conv, R* eq, R* iq, R* gout,
                    const R* swp) {
-  const dim3 grid(d.B * d.T);
+  const int spw = check_stages_per_wave(d.B, d.T);
+  const dim3 grid(d.B * ((d.T + spw - 1) / spw));
   const size_t smem = check_smem_bytes<R>(d.n, d.nx, d.m);
   lds_optin(sqp_check_stage_kernel<R, NC, true>, smem);
   lds_optin(sqp_check_stage_kernel<R, NC, false>, smem);
   if (std_dyn)
     hipLaunchKernelGGL((sqp_check_stage_kernel<R, NC, true>), grid, dim3(kWave), smem, s, d, q, x, y0, yf, yg, sl, sw,
-                       swp, conv, eq, iq, gout, diag);
+                       swp, conv, eq, iq, gout, diag, spw);
   else
     hipLaunchKernelGGL((sqp_check_stage_kernel<R, NC, false>), grid, dim3(kWave), smem, s, d, q, x, y0, yf, yg, sl, sw,
-                       swp, conv, eq, iq, gout, diag);
+                       swp, conv, eq, iq, gout, diag, spw);
 }
 
 template <typename R>

@@ -33,12 +33,6 @@ struct Bits<double> {
 };
 
 template <typename R>
-__device__ __forceinline__ void atomic_max_abs(R* p, R v) {
-  using U = typename Bits<R>::U;
-  atomicMax(reinterpret_cast<U*>(p), Bits<R>::of(v));
-}
-
-template <typename R>
 __global__ void sqp_check_init_kernel(int B, R* __restrict__ conv, R* __restrict__ eq, R* __restrict__ iq) {
   const int b = blockIdx.x * blockDim.x + threadIdx.x;
   if (b >= B) return;
@@ -131,11 +125,22 @@ __device__ __forceinline__ R col_bdot(const R* A, int i, int ld, int rows, R v) 
   return acc;
 }
 
-// One wave per (problem, stage).  D_t, A_minus_t and G_t are staged through
-// LDS; the vectors stay in registers (lane k holds element k) and reach the
-// other lanes by broadcast.  STD: A_plus_t = [-I 0] and E_t = 0 (neither is
-// read); otherwise E and A_plus are read from global memory directly.  The
-// slack weight is slack_wp[b] when slack_wp is given, else slack_w.
+// One wave per spw consecutive stages of a problem, one stage after the other
+// (check_stages_per_wave: more stages per wave where the batch leaves plenty
+// of waves, one where it does not).  D_t, A_minus_t and G_t are staged through LDS; the vectors stay
+// in registers (lane k holds element k) and reach the other lanes by
+// broadcast.  STD: A_plus_t = [-I 0] and E_t = 0 (neither is read); otherwise
+// E and A_plus are read from global memory directly.  The slack weight is
+// slack_wp[b] when slack_wp is given, else slack_w.  Each stage's maxima are
+// folded over the wave as before; the wave keeps the largest of its stages'
+// (as bit patterns of the magnitudes, which is what the per-problem atomicMax
+// compares) and issues one atomic per output.
+constexpr int kCheckMaxStages = 16;
+inline int check_stages_per_wave(long long B, int T) {
+  const long long s = B * T / 16384;  // about 16 waves per SIMD at one stage per wave
+  return s < 1 ? 1 : (s > kCheckMaxStages ? kCheckMaxStages : (int)s);
+}
+
 template <typename R, int NC, bool STD>
 __global__ __launch_bounds__(kWave) void sqp_check_stage_kernel(Dims d, QPDev<R> qp, const R* __restrict__ x,
                                                               const R* __restrict__ y0, const R* __restrict__ yf,
@@ -143,103 +148,113 @@ __global__ __launch_bounds__(kWave) void sqp_check_stage_kernel(Dims d, QPDev<R>
                                                               R slack_w, const R* __restrict__ slack_wp,
                                                               R* __restrict__ conv, R* __restrict__ eq_err,
                                                               R* __restrict__ ineq_err, R* __restrict__ gout,
-                                                              int diag) {
+                                                              int diag, int spw) {
   extern __shared__ __align__(16) unsigned char check_smem[];
   R* sD = reinterpret_cast<R*>(check_smem);
-  const int T = d.T, b = blockIdx.x / T, t = blockIdx.x - b * T, i = threadIdx.x;
+  using U = typename Bits<R>::U;
+  const int T = d.T, nsb = (T + spw - 1) / spw, i = threadIdx.x;
+  const int b = blockIdx.x / nsb, t_lo = (blockIdx.x - b * nsb) * spw;
+  const int t_hi = t_lo + spw < T ? t_lo + spw : T;
   const int N = d.N, n = NC > 0 ? NC : d.n, nx = d.nx, n0 = d.n0, m = d.m;
-  const int ld = check_ld(n);
-  R* sAm = sD + n * ld;
-  R* sG = sAm + nx * ld;
-  const size_t bt = (size_t)b * T + t, bn = (size_t)b * N;
-  const bool has_next = t < N, has_prev = t > 0;
-  constexpr int KB = NC > 0 ? (NC * NC + kWave - 1) / kWave : 0;
-  constexpr int KG = NC > 0 ? NC : 0;  // m <= 64 rows of NC
+  U all_b = 0, eq_b = 0, iq_b = 0;
+  for (int t = t_lo; t < t_hi; ++t) {
+    if (t > t_lo) wsync();  // the previous stage's reads of the LDS blocks are done
+    const int ld = check_ld(n);
+    R* sAm = sD + n * ld;
+    R* sG = sAm + nx * ld;
+    const size_t bt = (size_t)b * T + t, bn = (size_t)b * N;
+    const bool has_next = t < N, has_prev = t > 0;
+    constexpr int KB = NC > 0 ? (NC * NC + kWave - 1) / kWave : 0;
+    constexpr int KG = NC > 0 ? NC : 0;  // m <= 64 rows of NC
 
-  // Every load of the stage is issued before the first use.
-  const R xt = i < n ? x[bt * n + i] : R(0);
-  const R xn = has_next && i < n ? x[(bt + 1) * n + i] : R(0);
-  const R xp = !STD && has_prev && i < n ? x[(bt - 1) * n + i] : R(0);
-  const R yc = has_next && i < nx ? yf[(bn + t) * nx + i] : R(0);
-  const R yp = has_prev && i < nx ? yf[(bn + t - 1) * nx + i] : R(0);
-  const R y0v = t == 0 && i < n0 ? y0[(size_t)b * n0 + i] : R(0);
-  const R ygv = i < m ? yg[bt * m + i] : R(0);
-  const R qv = i < n ? qp.q[bt * n + i] : R(0);
-  const R cv = has_next && i < nx ? qp.c[(bn + t) * nx + i] : R(0);
-  const R c0v = t == 0 && i < n0 ? qp.c0[(size_t)b * n0 + i] : R(0);
-  const R lv = i < m ? qp.l[bt * m + i] : R(0);
-  const R uv = i < m ? qp.u[bt * m + i] : R(0);
-  const R slv = slack && i < m ? slack[bt * m + i] : R(0);
-  const R dii = diag && i < n ? qp.D[bt * n * n + (size_t)i * (n + 1)] : R(0);  // diagonal D_t
-  StageBlock<R, KB> bD, bA;
-  StageBlock<R, KG> bG;
-  bD.get(qp.D + bt * n * n, diag ? 0 : n * n);
-  bA.get(qp.Am + (bn + (has_next ? t : 0)) * nx * n, has_next ? nx * n : 0);
-  bG.get(qp.G + bt * m * n, m * n);
-  __builtin_amdgcn_sched_barrier(0);
-  bD.put(sD, n, ld);
-  bA.put(sAm, n, ld);
-  bG.put(sG, n, ld);
-  wsync();
+    // Every load of the stage is issued before the first use.
+    const R xt = i < n ? x[bt * n + i] : R(0);
+    const R xn = has_next && i < n ? x[(bt + 1) * n + i] : R(0);
+    const R xp = !STD && has_prev && i < n ? x[(bt - 1) * n + i] : R(0);
+    const R yc = has_next && i < nx ? yf[(bn + t) * nx + i] : R(0);
+    const R yp = has_prev && i < nx ? yf[(bn + t - 1) * nx + i] : R(0);
+    const R y0v = t == 0 && i < n0 ? y0[(size_t)b * n0 + i] : R(0);
+    const R ygv = i < m ? yg[bt * m + i] : R(0);
+    const R qv = i < n ? qp.q[bt * n + i] : R(0);
+    const R cv = has_next && i < nx ? qp.c[(bn + t) * nx + i] : R(0);
+    const R c0v = t == 0 && i < n0 ? qp.c0[(size_t)b * n0 + i] : R(0);
+    const R lv = i < m ? qp.l[bt * m + i] : R(0);
+    const R uv = i < m ? qp.u[bt * m + i] : R(0);
+    const R slv = slack && i < m ? slack[bt * m + i] : R(0);
+    const R dii = diag && i < n ? qp.D[bt * n * n + (size_t)i * (n + 1)] : R(0);  // diagonal D_t
+    StageBlock<R, KB> bD, bA;
+    StageBlock<R, KG> bG;
+    bD.get(qp.D + bt * n * n, diag ? 0 : n * n);
+    bA.get(qp.Am + (bn + (has_next ? t : 0)) * nx * n, has_next ? nx * n : 0);
+    bG.get(qp.G + bt * m * n, m * n);
+    __builtin_amdgcn_sched_barrier(0);
+    bD.put(sD, n, ld);
+    bA.put(sAm, n, ld);
+    bG.put(sG, n, ld);
+    wsync();
 
-  // Branches below depend on the stage only (uniform); rows past the block's
-  // height are computed on row 0 and dropped, so every lane reaches every
-  // broadcast.
-  const int in = i < n ? i : 0, ix = i < nx ? i : 0, im = i < m ? i : 0, i0 = i < n0 ? i : 0;
-  R px = diag ? dii * xt : row_bdot<R, NC>(sD, in, ld, n, xt);
-  R aty = m ? col_bdot(sG, in, ld, m, ygv) : R(0);
-  if (has_next) aty += col_bdot(sAm, in, ld, nx, yc);
-  if (STD) {
-    if (has_prev && i < nx) aty -= yp;
-  } else {
-    if (has_prev) {
-      const R* Ep = qp.E + (bn + t - 1) * n * n + (size_t)in * n;
-      const R* Ap = qp.Ap + (bn + t - 1) * nx * n;
-      for (int k = 0; k < n; ++k) px += Ep[k] * lane_bcast(xp, k);
-      for (int r = 0; r < nx; ++r) aty += Ap[(size_t)r * n + in] * lane_bcast(yp, r);
-    }
-    if (has_next) {
-      const R* En = qp.E + (bn + t) * n * n;
-      for (int k = 0; k < n; ++k) px += En[(size_t)k * n + in] * lane_bcast(xn, k);
-    }
-  }
-  if (t == 0) {
-    const R* A0 = qp.A0 + (size_t)b * n0 * n;
-    for (int r = 0; r < n0; ++r) aty += A0[(size_t)r * n + in] * lane_bcast(y0v, r);
-  }
-  R st = i < n ? rabs(px + qv + aty) : R(0);
-  R eq = 0, iq = 0, sl = 0;
-  if (has_next) {
-    R cx = row_bdot<R, NC>(sAm, ix, ld, n, xt);
+    // Branches below depend on the stage only (uniform); rows past the block's
+    // height are computed on row 0 and dropped, so every lane reaches every
+    // broadcast.
+    const int in = i < n ? i : 0, ix = i < nx ? i : 0, im = i < m ? i : 0, i0 = i < n0 ? i : 0;
+    R px = diag ? dii * xt : row_bdot<R, NC>(sD, in, ld, n, xt);
+    R aty = m ? col_bdot(sG, in, ld, m, ygv) : R(0);
+    if (has_next) aty += col_bdot(sAm, in, ld, nx, yc);
     if (STD) {
-      cx -= xn;
+      if (has_prev && i < nx) aty -= yp;
     } else {
-      const R* Ap = qp.Ap + (bn + t) * nx * n + (size_t)ix * n;
-      for (int k = 0; k < n; ++k) cx += Ap[k] * lane_bcast(xn, k);
+      if (has_prev) {
+        const R* Ep = qp.E + (bn + t - 1) * n * n + (size_t)in * n;
+        const R* Ap = qp.Ap + (bn + t - 1) * nx * n;
+        for (int k = 0; k < n; ++k) px += Ep[k] * lane_bcast(xp, k);
+        for (int r = 0; r < nx; ++r) aty += Ap[(size_t)r * n + in] * lane_bcast(yp, r);
+      }
+      if (has_next) {
+        const R* En = qp.E + (bn + t) * n * n;
+        for (int k = 0; k < n; ++k) px += En[(size_t)k * n + in] * lane_bcast(xn, k);
+      }
     }
-    if (i < nx) eq = rabs(cx - cv);
-  }
-  if (t == 0) {
-    const R* A0 = qp.A0 + ((size_t)b * n0 + i0) * n;
-    R cx = 0;
-    for (int k = 0; k < n; ++k) cx += A0[k] * lane_bcast(xt, k);
-    if (i < n0) eq = rmax(eq, rabs(cx - c0v));
-  }
-  if (m) {
-    const R gv = row_bdot<R, NC>(sG, im, ld, n, xt) + slv;
-    if (i < m) {
-      if (slack) sl = rabs((slack_wp ? slack_wp[b] : slack_w) * slv + ygv);
-      iq = rmax(rmax(lv - gv, R(0)), rmax(gv - uv, R(0)));
-      if (gout) gout[bt * m + i] = gv;
+    if (t == 0) {
+      const R* A0 = qp.A0 + (size_t)b * n0 * n;
+      for (int r = 0; r < n0; ++r) aty += A0[(size_t)r * n + in] * lane_bcast(y0v, r);
     }
+    R st = i < n ? rabs(px + qv + aty) : R(0);
+    R eq = 0, iq = 0, sl = 0;
+    if (has_next) {
+      R cx = row_bdot<R, NC>(sAm, ix, ld, n, xt);
+      if (STD) {
+        cx -= xn;
+      } else {
+        const R* Ap = qp.Ap + (bn + t) * nx * n + (size_t)ix * n;
+        for (int k = 0; k < n; ++k) cx += Ap[k] * lane_bcast(xn, k);
+      }
+      if (i < nx) eq = rabs(cx - cv);
+    }
+    if (t == 0) {
+      const R* A0 = qp.A0 + ((size_t)b * n0 + i0) * n;
+      R cx = 0;
+      for (int k = 0; k < n; ++k) cx += A0[k] * lane_bcast(xt, k);
+      if (i < n0) eq = rmax(eq, rabs(cx - c0v));
+    }
+    if (m) {
+      const R gv = row_bdot<R, NC>(sG, im, ld, n, xt) + slv;
+      if (i < m) {
+        if (slack) sl = rabs((slack_wp ? slack_wp[b] : slack_w) * slv + ygv);
+        iq = rmax(rmax(lv - gv, R(0)), rmax(gv - uv, R(0)));
+        if (gout) gout[bt * m + i] = gv;
+      }
+    }
+    const R all = wave_max(rmax(rmax(st, eq), rmax(iq, sl)));
+    if (eq_err) eq = wave_max(eq);
+    if (ineq_err) iq = wave_max(iq);
+    all_b = all_b > Bits<R>::of(all) ? all_b : Bits<R>::of(all);
+    eq_b = eq_b > Bits<R>::of(eq) ? eq_b : Bits<R>::of(eq);
+    iq_b = iq_b > Bits<R>::of(iq) ? iq_b : Bits<R>::of(iq);
   }
-  const R all = wave_max(rmax(rmax(st, eq), rmax(iq, sl)));
-  if (eq_err) eq = wave_max(eq);
-  if (ineq_err) iq = wave_max(iq);
   if (i == 0) {
-    atomic_max_abs(conv + b, all);
-    if (eq_err) atomic_max_abs(eq_err + b, eq);
-    if (ineq_err) atomic_max_abs(ineq_err + b, iq);
+    atomicMax(reinterpret_cast<U*>(conv + b), all_b);
+    if (eq_err) atomicMax(reinterpret_cast<U*>(eq_err + b), eq_b);
+    if (ineq_err) atomicMax(reinterpret_cast<U*>(ineq_err + b), iq_b);
   }
 }
 
