@@ -1441,7 +1441,7 @@ __global__ __launch_bounds__(kWave, StreamOcc<R>::waves) void admm_stream_kernel
       if (active) {
 #pragma unroll
         for (int k = 0; k < 6; ++k) res[k] = rv6[k];
-        const R cand = rmin(rmax(rho * rsqrt_(rv6[4] / rv6[5]), a.rho_min), a.rho_max);
+        const R cand = rmin(rmax(rho * r_sqrt(rv6[4] / rv6[5]), a.rho_min), a.rho_max);
         const R ratio = rmax(cand / rho, rho / cand);
         const bool conv = !((rv6[0] > a.eps_abs + a.eps_rel * rv6[2]) || (rv6[1] > a.eps_abs + a.eps_rel * rv6[3]));
         bool keep = iter < 2 || !mod_zero(iter, a.adapt_every);

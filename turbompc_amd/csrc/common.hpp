@@ -59,8 +59,9 @@ __device__ __forceinline__ float rmin(float a, float b) { return __builtin_fminf
 __device__ __forceinline__ double rmin(double a, double b) { return __builtin_fmin(a, b); }
 __device__ __forceinline__ float rabs(float a) { return __builtin_fabsf(a); }
 __device__ __forceinline__ double rabs(double a) { return __builtin_fabs(a); }
-__device__ __forceinline__ float rsqrt_(float a) { return sqrtf(a); }
-__device__ __forceinline__ double rsqrt_(double a) { return sqrt(a); }
+// the square root in the value's own precision (not its reciprocal)
+__device__ __forceinline__ float r_sqrt(float a) { return sqrtf(a); }
+__device__ __forceinline__ double r_sqrt(double a) { return sqrt(a); }
 
 template <typename R>
 __device__ __forceinline__ R rinf() {

@@ -131,7 +131,7 @@ __global__ __launch_bounds__(256) void ocp_merit_terms_kernel(MeritArgs<R> a) {
         const R dc = xs[t * nx + c] - ck[c];
         d2 += dc * dc;
       }
-      g = R(1) - rsqrt_(d2) / (a.radii[(size_t)b * a.nobs + k] + R(0.001));
+      g = R(1) - r_sqrt(d2) / (a.radii[(size_t)b * a.nobs + k] + R(0.001));
       lo = R(-1.0e9);
       hi = R(0);
       if (a.scaled) {

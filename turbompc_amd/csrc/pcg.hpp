@@ -432,7 +432,7 @@ __global__ __launch_bounds__(kWave) void admm_pcg_chunk_kernel(AdmmPcgArgs<R> pa
       if (active) {
 #pragma unroll
         for (int k = 0; k < 6; ++k) res[k] = rv[k];
-        const R cand = rmin(rmax(rho * rsqrt_(rv[4] / rv[5]), a.rho_min), a.rho_max);
+        const R cand = rmin(rmax(rho * r_sqrt(rv[4] / rv[5]), a.rho_min), a.rho_max);
         const R ratio = rmax(cand / rho, rho / cand);
         const bool conv = !((rv[0] > a.eps_abs + a.eps_rel * rv[2]) || (rv[1] > a.eps_abs + a.eps_rel * rv[3]));
         bool keep = iter < 2 || !mod_zero(iter, a.adapt_every);

@@ -515,7 +515,7 @@ __global__ __launch_bounds__(kPcgThreads) void admm_pcg_lds_kernel(AdmmPcgArgs<R
       R nd = rmax(rmax(r_[6], r_[7]), r_[8]);
       if (slack) nd = rmax(nd, rmax(gs * r_[9], r_[10]));
       const R pn = r_[0] / (R(1e-10) + np), dn = r_[5] / (R(1e-10) + nd);
-      const R cand = rmin(rmax(rho * rsqrt_(pn / dn), a.rho_min), a.rho_max);
+      const R cand = rmin(rmax(rho * r_sqrt(pn / dn), a.rho_min), a.rho_max);
       const R ratio = rmax(cand / rho, rho / cand);
       tl = (r_[0] > a.eps_abs + a.eps_rel * np) || (r_[5] > a.eps_abs + a.eps_rel * nd);
       const bool conv = !tl;
@@ -1010,7 +1010,7 @@ __global__ __launch_bounds__(kPcgThreads) void admm_pcg_dpp_kernel(AdmmPcgArgs<R
       R nd = rmax(rmax(r_[6], r_[7]), r_[8]);
       if (slack) nd = rmax(nd, rmax(gs * r_[9], r_[10]));
       const R pn = r_[0] / (R(1e-10) + np), dn = r_[5] / (R(1e-10) + nd);
-      const R cand = rmin(rmax(rho * rsqrt_(pn / dn), a.rho_min), a.rho_max);
+      const R cand = rmin(rmax(rho * r_sqrt(pn / dn), a.rho_min), a.rho_max);
       const R ratio = rmax(cand / rho, rho / cand);
       tl = (r_[0] > a.eps_abs + a.eps_rel * np) || (r_[5] > a.eps_abs + a.eps_rel * nd);
       const bool conv = !tl;
