@@ -252,9 +252,11 @@ def measured_traffic(batch, admm_iters):
 
 
 class SolveTimer:
-    """Times every ADMMSolver.solve / sqp_step call twice with HIP events on the
-    solve stream: the whole QP solve, and (through the library's hook) the
-    iteration phase alone."""
+    """Times ADMMSolver.solve / sqp_step calls with HIP events on the solve
+    stream: the iteration phase alone (through the library's hook: two event
+    records per call, the only ones in the timed region, their events made
+    beforehand) and, while `whole` is set (the last warm-up step), the whole
+    QP solve."""
 
     def __init__(self, dev):
         import torch
@@ -264,6 +266,8 @@ class SolveTimer:
 
         self.mod, self.dev, self.torch = admm_mod, dev, torch
         self.solves = []
+        self.whole = True
+        self.calls = 0  # QP solves since the last clear()
         self.iters = _lib.IterationTimer()
         self.orig = (admm_mod.ADMMSolver.solve, admm_mod.ADMMSolver.sqp_step)
 
@@ -272,6 +276,10 @@ class SolveTimer:
 
         def timed(fn):
             def wrapper(solver, *a, **kw):
+                self.calls += 1
+                if not self.whole:
+                    with self.iters:
+                        return fn(solver, *a, **kw)
                 s = torch.cuda.current_stream(self.dev)
                 e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
                 e0.record(s)
@@ -293,6 +301,7 @@ class SolveTimer:
     def clear(self):
         self.solves.clear()
         self.iters.clear()
+        self.calls = 0
 
     def averages_s(self):
         solve_ms = [a.elapsed_time(b) for a, b in self.solves]
@@ -301,17 +310,33 @@ class SolveTimer:
 
 
 def timed_steps(step, steps, warmup, timer):
+    """Times `steps` calls of step() after `warmup` untimed ones.  The whole
+    QP solves are timed in the last warm-up step (with no warm-up, in the
+    timed steps); the timed region records only the library's iteration
+    events, whose HIP events are made before it."""
     import torch
 
-    for _ in range(warmup):
+    for i in range(warmup):
+        if i == warmup - 1:
+            timer.clear()
         step()
     torch.cuda.synchronize()
+    whole = list(timer.solves)
+    per_step = timer.calls if warmup else 0
     timer.clear()
+    if warmup:
+        timer.whole = False
+        timer.iters.reserve(per_step * steps)
+        torch.cuda.synchronize()
     t0 = time.perf_counter()
     for _ in range(steps):
         out = step()
     torch.cuda.synchronize()
-    return time.perf_counter() - t0, out
+    elapsed = time.perf_counter() - t0
+    if warmup:
+        timer.solves[:0] = whole
+        timer.whole = True
+    return elapsed, out
 
 
 def base_line(metric, value, args, elapsed, dtype, data, config):

@@ -284,14 +284,25 @@ class IterationTimer:
 
     def __init__(self):
         self._pairs = []
+        self._pool = []
         self._lib = load()
 
-    def __enter__(self):
+    @staticmethod
+    def _new_pair():
         import torch
 
         e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
         e0.record()  # materialise the underlying HIP events
         e1.record()
+        return e0, e1
+
+    def reserve(self, n: int):
+        """Materialise n event pairs now (their first records are queued here,
+        e.g. before a timed region), for the next n solves to use."""
+        self._pool.extend(self._new_pair() for _ in range(n))
+
+    def __enter__(self):
+        e0, e1 = self._pool.pop() if self._pool else self._new_pair()
         self._lib.tmpc_set_timing_events(ctypes.c_void_p(e0.cuda_event), ctypes.c_void_p(e1.cuda_event))
         self._pairs.append((e0, e1))
         return self
