@@ -511,7 +511,10 @@ int tmpc_kkt_active_sets_f64(hipStream_t stream, int64_t count, const double* g,
  *   state coordinates, bounds (-1e9, 0), all scaled by obs_scale when scaled;
  *   centers (B0, nobs, dim) and radii (B0, nobs) are device arrays (nobs <=
  *   32), and slacks then cover mbox + nobs rows.  NaN propagates into every
- *   term. */
+ *   term.  With lin_A set the dynamics are linear and next may be NULL:
+ *   f_t = A x_t + Bm u_t + b is formed in the kernel as tmpc_linear_dynamics_*
+ *   forms it, from lin_A (B0, nx, nx), lin_B (B0, nx, nu) and lin_b (B0, nx),
+ *   device arrays. */
 typedef struct {
   int32_t P, B0, T, nx, nu, mbox;
   const void* states;
@@ -541,6 +544,9 @@ typedef struct {
   const void* centers;
   const void* radii;
   double obs_scale;
+  const void* lin_A; /* NULL: f_t from next */
+  const void* lin_B;
+  const void* lin_b;
 } tmpc_merit_terms;
 int tmpc_ocp_merit_terms_f32(hipStream_t stream, const tmpc_merit_terms* args);
 int tmpc_ocp_merit_terms_f64(hipStream_t stream, const tmpc_merit_terms* args);

@@ -189,6 +189,13 @@ def test_fused_merit_terms_match_torch_forms(dtype):
         for k, g, w in zip(("cost", "eq", "iq"), got4[:3], want4[:3]):
             assert g.shape == (A * B,) and rel_err(g, w) < tol, (name, "copies", k)
         assert got4[3] is None
+        if prob._merit_linear_dynamics() is not None:
+            # the linear step formed in the kernel equals the one read from
+            # next_states (tmpc_linear_dynamics_*), bit for bit
+            ref = copy.copy(prob)
+            ref._merit_linear_dynamics = lambda: None  # noqa: E731
+            for g, r in zip(got4, ref.merit_terms(s4, c4, sl4, copies=A)):
+                assert (g is None and r is None) or torch.equal(g, r), (name, "linear step")
     # NaN propagation: one problem's state
     prob = make_quadrotor_config(B=4, seed=1, dtype=dtype, device="cuda")
     s, c = prob.initial_guess()

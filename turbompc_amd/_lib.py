@@ -140,6 +140,9 @@ class MeritTerms(ctypes.Structure):
         ("centers", ctypes.c_void_p),
         ("radii", ctypes.c_void_p),
         ("obs_scale", ctypes.c_double),
+        ("lin_A", ctypes.c_void_p),
+        ("lin_B", ctypes.c_void_p),
+        ("lin_b", ctypes.c_void_p),
     ]
 
 

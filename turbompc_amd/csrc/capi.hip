@@ -1448,7 +1448,9 @@ int merit_impl(hipStream_t s, const tmpc_merit_terms* m) {
       m->nu < 0 || m->nu > kMeritMaxVars || m->mbox < 0 || m->mbox > kMeritMaxRows)
     return TMPC_EBADSHAPE;
   if (m->P == 0) return TMPC_OK;
-  if (!m->states || (m->nu > 0 && !m->controls) || !m->next || !m->x0 || !m->w || !m->zref || !m->cost || !m->eq ||
+  if (m->lin_A && (!m->lin_b || (m->nu > 0 && !m->lin_B))) return TMPC_EBADARG;
+  if (!m->states || (m->nu > 0 && !m->controls) || (!m->next && !m->lin_A) || !m->x0 || !m->w || !m->zref ||
+      !m->cost || !m->eq ||
       !m->iq || (m->dstates && m->nu > 0 && !m->dcontrols) || (m->dslacks && !m->slacks))
     return TMPC_EBADARG;
   if (m->mbox > 0 && (!m->box_idx || !m->box_lo || !m->box_hi)) return TMPC_EBADARG;
@@ -1462,6 +1464,9 @@ int merit_impl(hipStream_t s, const tmpc_merit_terms* m) {
   a.states = static_cast<const R*>(m->states);
   a.controls = static_cast<const R*>(m->controls);
   a.next = static_cast<const R*>(m->next);
+  a.lin_A = static_cast<const R*>(m->lin_A);
+  a.lin_B = static_cast<const R*>(m->lin_B);
+  a.lin_b = static_cast<const R*>(m->lin_b);
   a.x0 = static_cast<const R*>(m->x0);
   a.u0 = static_cast<const R*>(m->u0);
   a.w = static_cast<const R*>(m->w);

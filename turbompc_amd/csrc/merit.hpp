@@ -49,6 +49,9 @@ struct MeritArgs {
   const R* centers;   // (B0, nobs, dim)
   const R* radii;     // (B0, nobs)
   R obs_scale;        // ro (1 without rescaling)
+  const R* lin_A;     // (B0, nx, nx) or null: f_t = A x_t + Bm u_t + b formed here, next unused
+  const R* lin_B;     // (B0, nx, nu)
+  const R* lin_b;     // (B0, nx)
   const R* slacks;    // (P, T, mbox + nobs) or null
   R gamma;            // slack penalization weight
   const R* dstates;   // (P, T, nx) or null: no directional derivative
@@ -91,11 +94,28 @@ __global__ __launch_bounds__(256) void ocp_merit_terms_kernel(MeritArgs<R> a) {
       dc += (R(2) * wb[i]) * d * dz;
     }
   }
-  // equality rows: x_0 - x0, then f(x_t, u_t) - x_{t+1}
+  // equality rows: x_0 - x0, then f(x_t, u_t) - x_{t+1}; f_t is the model's
+  // step from next, or for linear dynamics formed here as the linear step
+  // kernel forms it: (sum_j A_kj x_j + sum_j Bm_kj u_j) + b_k, each sum in j order
   const R* nb = a.next + (size_t)p * N * nx;
   for (int i = lane; i < T * nx; i += kWave) {
     const int t = i / nx, k = i - t * nx;
-    R h = t == 0 ? xs[k] - a.x0[(size_t)b * nx + k] : nb[(t - 1) * nx + k] - xs[t * nx + k];
+    R f = R(0);
+    if (t > 0) {
+      if (a.lin_A != nullptr) {
+        const R* ar = a.lin_A + ((size_t)b * nx + k) * nx;
+        const R* br = a.lin_B + ((size_t)b * nx + k) * nu;
+        const R* xp = xs + (t - 1) * nx;
+        const R* up = us + (t - 1) * nu;
+        R ax = R(0), bu = R(0);
+        for (int j = 0; j < nx; ++j) ax += ar[j] * xp[j];
+        for (int j = 0; j < nu; ++j) bu += br[j] * up[j];
+        f = (ax + bu) + a.lin_b[(size_t)b * nx + k];
+      } else {
+        f = nb[(t - 1) * nx + k];
+      }
+    }
+    R h = t == 0 ? xs[k] - a.x0[(size_t)b * nx + k] : f - xs[t * nx + k];
     if (a.scaled) h = h / a.sscale[k];
     e += rabs(h);
   }

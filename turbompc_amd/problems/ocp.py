@@ -301,6 +301,11 @@ class QuadraticTrackingOCP:
             return out
         return self._memoized("merit_host", make)
 
+    def _merit_linear_dynamics(self):
+        """(A, Bm, b), per problem, when the merit kernel may form the
+        dynamics step itself (linear dynamics); None: it reads next_states."""
+        return None
+
     def _merit_obstacle_rows(self):
         """The obstacle rows that follow the box rows in the fused merit terms
         (dict nobs, dim, centers, radii, scale), or None: none here."""
@@ -335,7 +340,12 @@ class QuadraticTrackingOCP:
         P, T = states.shape[0], states.shape[1]
         c = lambda t: t.to(device=dev, dtype=dt).contiguous() if t is not None else None  # noqa: E731
         states, controls = c(states), c(controls)
-        nxt = (self.tile(copies) if copies > 1 else self).next_states(states, controls).to(dt).contiguous()
+        lin = self._merit_linear_dynamics()
+        if lin is None:
+            nxt = (self.tile(copies) if copies > 1 else self).next_states(states, controls).to(dt).contiguous()
+        else:  # the kernel forms the linear step itself
+            nxt = None
+            lin = tuple(c(t) for t in lin)
         w, zref = (c(t) for t in self.tracking_weights())
         soft = self.use_slack_variables and slacks is not None and slacks.numel() > 0
         slacks = c(slacks) if soft else None
@@ -355,6 +365,8 @@ class QuadraticTrackingOCP:
                                gamma=float(self.slack_penalization_weight), dstates=_lib.ptr(dstates),
                                dcontrols=_lib.ptr(dcontrols), dslacks=_lib.ptr(dslacks), cost=_lib.ptr(cost),
                                dcost=_lib.ptr(dcost), eq=_lib.ptr(eq), iq=_lib.ptr(iq))
+        if lin is not None:
+            args.lin_A, args.lin_B, args.lin_b = (_lib.ptr(t) for t in lin)
         if obs is not None:
             centers, radii = c(obs["centers"]), c(obs["radii"])  # held until the launch
             args.nobs, args.dim, args.obs_scale = obs["nobs"], obs["dim"], obs["scale"]
@@ -591,6 +603,10 @@ class LinearOCP(QuadraticTrackingOCP):
 
     def dynamics_lagrangian_hessian(self, states, controls, lambdas):
         return None  # linear dynamics
+
+    def _merit_linear_dynamics(self):
+        # the step of next_states, unless a subclass defines its own
+        return (self.A, self.Bm, self.b) if type(self).next_states is LinearOCP.next_states else None
 
     def next_states(self, states, controls):
         """(B, N, nx): A x_t + B u_t + b (tmpc_linear_dynamics_* on the device: a
