@@ -90,12 +90,12 @@ __global__ __launch_bounds__(kObstacleBlock) void obstacle_linearize_kernel(int 
     l[row] = lo;
     u[row] = hi;
     qrow[threadIdx.x] = row * n;
+    const size_t ri = (size_t)(bt - b * (unsigned)T) * B + b;  // the record of (t, b)
     if (rec.rv != nullptr) {
-      const size_t ri = (size_t)(bt - b * (unsigned)T) * B + b;  // the record of (t, b)
       rec.rv[ri * rec.rvp + rec.l_off + k] = lo;
       rec.rv[ri * rec.rvp + rec.u_off + k] = hi;
-      rrow[threadIdx.x] = ri * rec.amp + rec.g_off + (size_t)k * n;
     }
+    if (rec.am != nullptr) rrow[threadIdx.x] = ri * rec.amp + rec.g_off + (size_t)k * n;
   }
   __syncthreads();
   // the block's rows in passes of kObstacleBlock / n rows, a thread per entry
