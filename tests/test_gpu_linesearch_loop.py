@@ -206,6 +206,51 @@ def test_quadrotor_step_linearization_equals_build_qp(dtype, stop):
         assert len(set(out[0].num_iter.tolist())) >= 2
 
 
+def _planar_obstacles(B, seed):
+    """A planar double integrator (nx = 4, nu = 2) among three discs: n = 6
+    with 4 + 2 + 3 stacked rows, so the streaming records are 9 wide (padded)."""
+    from turbompc_amd.problems.obstacle import ObstacleOCP
+
+    g = torch.Generator().manual_seed(seed)
+    u = lambda lo, hi, *s: lo + (hi - lo) * torch.rand(s, generator=g, dtype=torch.float64)  # noqa: E731
+    dt, N, nx, nu, K = 0.1, 20, 4, 2, 3
+    A = torch.tensor([[1.0, 0, dt, 0], [0, 1.0, 0, dt], [0, 0, 1.0, 0], [0, 0, 0, 1.0]], dtype=torch.float64)
+    Bm = torch.tensor([[0.5 * dt * dt, 0], [0, 0.5 * dt * dt], [dt, 0], [0, dt]], dtype=torch.float64)
+    x0 = torch.cat([torch.stack([torch.full((B,), -3.0, dtype=torch.float64), u(-1, 1, B)], 1),
+                    torch.zeros(B, 2, dtype=torch.float64)], 1)
+    xg = torch.cat([torch.stack([torch.full((B,), 3.0, dtype=torch.float64), u(-1, 1, B)], 1),
+                    torch.zeros(B, 2, dtype=torch.float64)], 1)
+    return ObstacleOCP(
+        A=A, Bm=Bm, horizon=N, num_states=nx, num_controls=nu, initial_state=x0,
+        weights_state=torch.tensor([1.0, 1.0, 0.1, 0.1], dtype=torch.float64).expand(B, nx),
+        weights_control=torch.full((B, nu), 0.01, dtype=torch.float64),
+        weights_final=torch.tensor([10.0, 10.0, 1.0, 1.0], dtype=torch.float64).expand(B, nx),
+        reference_state=xg[:, None].expand(B, N + 1, nx),
+        control_bounds=(torch.full((nu,), -2.0, dtype=torch.float64), torch.full((nu,), 2.0, dtype=torch.float64)),
+        initial_guess_final_state=xg, obstacles_centers=u(-1.5, 1.5, B, K, 2), obstacles_radii=u(0.2, 0.5, B, K),
+        obstacles_dimension=2)
+
+
+@pytest.mark.parametrize("dtype", [torch.float64, torch.float32])
+def test_obstacle_step_on_padded_records_equals_build_qp(dtype):
+    """The obstacle SQP step where the stage records are wider than the QP
+    (n = 6 padded to 9): the step writes the obstacle rows into the QP only
+    and the library copies G, l, u into the records; the solve equals the
+    build_qp loop's bit for bit."""
+    prob = _planar_obstacles(16, 3).to("cuda", dtype)
+    params = _params(5, 15, 0.0, linesearch=False, criterion="first_order")
+    out = []
+    for fused in (True, False):
+        p = copy.copy(prob)
+        if not fused:
+            p.step_linearization = lambda: None  # noqa: E731  the build_qp path
+        solver = TurboMPCSolver(p, params)
+        out.append(solver.solve(solver.initial_guess()))
+    torch.cuda.synchronize()
+    assert bool(torch.isfinite(out[0].states).all())
+    _assert_same(*out)
+
+
 @pytest.mark.parametrize("dtype", [torch.float64, torch.float32])
 @pytest.mark.parametrize("stop", [False, True])
 @pytest.mark.parametrize("slack", [False, True])
